@@ -1,0 +1,150 @@
+/*
+ * C ABI of the MI355X (gfx950) Linear hot path: W8A16 group-64 dequant
+ * GEMV/GEMM, BF16 W16A16 GEMV/GEMM, and the fused tied-embedding LM head
+ * with argmax.
+ *
+ * Each entry point replaces one free function of the reference's operator
+ * boundary, include/infer/cuda_ops.hpp (Greedy-cy/qwen2.5-jetson-inference),
+ * with the same argument order and meaning:
+ *   - pointers are caller-owned device memory (no allocation inside an op);
+ *   - BF16 tensors are passed as their 16-bit words (uint16_t);
+ *   - weights are row-major [out_features, in_features]; W8A16 scales are
+ *     BF16 [out_features, ceil(in_features / 64)], group g covering columns
+ *     [64 g, 64 g + 64) (tools/export_model.py:228-242);
+ *   - activations are [tokens, in_features], outputs [tokens, out_features],
+ *     FP32 accumulation, BF16 round-to-nearest-even output;
+ *   - bias may be NULL;
+ *   - work is enqueued on `stream` and never synchronised (the caller syncs
+ *     before reading results, as src/qwen2.cpp:668-673 does).
+ * Where the reference throws infer::Error (INFER_CHECK / INFER_CUDA_CHECK,
+ * include/infer/common.hpp:66-82) these return a nonzero status and leave a
+ * message for infer_hip_last_error(); they never throw.
+ *
+ * Fast paths need 16-byte aligned weight and activation pointers and
+ * in_features % 64 == 0 (W8A16) or % 8 == 0 (BF16); anything else runs an
+ * exact-semantics fallback kernel, as the reference's scalar kernels do.
+ */
+#ifndef INFER_LINEAR_H
+#define INFER_LINEAR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define INFER_HIP_ABI_VERSION 1
+
+enum infer_hip_status {
+  INFER_HIP_OK = 0,
+  INFER_HIP_INVALID_ARGUMENT = 1, /* reference: INFER_CHECK throws */
+  INFER_HIP_LAUNCH_FAILED = 2,    /* reference: INFER_CUDA_CHECK throws */
+  INFER_HIP_RUNTIME_ERROR = 3     /* a HIP runtime call other than a launch */
+};
+
+/* Message for the last nonzero status returned on this thread ("" if the
+ * last call succeeded). */
+const char* infer_hip_last_error(void);
+
+/* INFER_HIP_ABI_VERSION of the loaded library. */
+int infer_hip_abi_version(void);
+
+/* y[n] = bf16(sum_k W[n,k] x[k] + bias[n]).
+ * Replaces infer::cuda::gemv_bf16, include/infer/cuda_ops.hpp:24-26
+ * (launcher src/cuda/kernels.cu:1540-1564). */
+int infer_hip_gemv_bf16(const uint16_t* weight, const uint16_t* bias,
+                        const uint16_t* input, uint16_t* output,
+                        int out_features, int in_features, hipStream_t stream);
+
+/* Y[m,n] = bf16(sum_k X[m,k] W[n,k] + bias[n]) for m < tokens.
+ * Replaces infer::cuda::gemm_bf16, include/infer/cuda_ops.hpp:32-35
+ * (launcher src/cuda/kernels.cu:1600-1625). */
+int infer_hip_gemm_bf16(const uint16_t* weight, const uint16_t* bias,
+                        const uint16_t* input, uint16_t* output, int tokens,
+                        int out_features, int in_features, hipStream_t stream);
+
+/* Tied LM head: logits[v] = bf16(E[v,:] h + bias[v]) for v < vocab, and
+ * *argmax = the first index of the maximum of the FP32 sums (ties -> lowest
+ * index, the CPU path's std::max_element, src/cpu_ops.cpp:175-177).
+ * block_max_value / block_max_index are scratch of at least
+ * infer_hip_lm_head_workspace_entries(vocab, in_features) entries each; that
+ * count never exceeds ceil(vocab / 8), the reference's sizing
+ * (src/qwen2.cpp:193-198).
+ * Replaces infer::cuda::lm_head_bf16, include/infer/cuda_ops.hpp:42-45
+ * (launcher src/cuda/kernels.cu:1566-1579).  Difference: the reference
+ * takes the argmax over BF16-rounded logits (kernels.cu:545-547); this one
+ * takes it over the FP32 sums so that it equals the CPU FP32 argmax. */
+int infer_hip_lm_head_bf16(const uint16_t* weight, const uint16_t* bias,
+                           const uint16_t* input, uint16_t* logits,
+                           float* block_max_value, int* block_max_index,
+                           int* argmax, int vocab, int in_features,
+                           hipStream_t stream);
+
+/* Entries of block_max_value / block_max_index infer_hip_lm_head_bf16 uses
+ * for this shape (0 for invalid shapes).  No reference counterpart: the
+ * reference sizes its workspace inline (src/qwen2.cpp:193-198). */
+size_t infer_hip_lm_head_workspace_entries(int vocab, int in_features);
+
+/* y[n] = bf16(sum_k q[n,k] * s[n, k/64] * x[k] + bias[n]), FP32 sums; the
+ * dequantised weight q*s is exact in FP32.  group_size must be 64.
+ * Replaces infer::cuda::gemv_w8a16, include/infer/cuda_ops.hpp:47-50
+ * (launcher src/cuda/kernels.cu:1627-1655). */
+int infer_hip_gemv_w8a16(const int8_t* weight, const uint16_t* scales,
+                         int group_size, const uint16_t* bias,
+                         const uint16_t* input, uint16_t* output,
+                         int out_features, int in_features, hipStream_t stream);
+
+/* Y[m,n] = bf16(sum_k q[n,k] * s[n, k/64] * X[m,k] + bias[n]) for m < tokens.
+ * group_size must be 64.  The group scale is applied to the FP32 partial sum
+ * of each 64-column group, so the product uses the exact dequantised weight
+ * (the reference rounds q*s to BF16 first, kernels.cu:1091).
+ * Replaces infer::cuda::gemm_w8a16, include/infer/cuda_ops.hpp:51-55
+ * (launcher src/cuda/kernels.cu:1657-1684). */
+int infer_hip_gemm_w8a16(const int8_t* weight, const uint16_t* scales,
+                         int group_size, const uint16_t* bias,
+                         const uint16_t* input, uint16_t* output, int tokens,
+                         int out_features, int in_features, hipStream_t stream);
+
+/* ---- Grouped W8A16 GEMV plans ------------------------------------------
+ * No single reference counterpart: a plan is the multi-matrix form of
+ * infer_hip_gemv_w8a16 for GEMVs that are independent of each other, such
+ * as q/k/v on one normed input and gate/up on another (src/qwen2.cpp:
+ * 615-626, 646-651 issue them as separate gemv_w8a16 calls), or a sweep
+ * over many layers' Linears (tools/linear_benchmark.cpp measures them one
+ * by one).  Each descriptor has the meaning of one infer_hip_gemv_w8a16
+ * call and must meet its fast-path preconditions (group_size 64,
+ * in_features % 64 == 0 and <= 8192, 16-byte aligned weight and input);
+ * no output may alias any input of the same plan.  create resolves and
+ * uploads the descriptor table once (it allocates device memory on the
+ * current device); launch enqueues one kernel per K class and allocates
+ * nothing. */
+typedef struct infer_hip_w8a16_gemv_desc {
+  const int8_t* weight;
+  const uint16_t* scales;
+  int group_size;
+  const uint16_t* bias;
+  const uint16_t* input;
+  uint16_t* output;
+  int out_features;
+  int in_features;
+} infer_hip_w8a16_gemv_desc;
+
+typedef struct infer_hip_gemv_plan infer_hip_gemv_plan;
+
+int infer_hip_w8a16_gemv_plan_create(const infer_hip_w8a16_gemv_desc* descs,
+                                     int count, infer_hip_gemv_plan** plan);
+int infer_hip_w8a16_gemv_plan_launch(const infer_hip_gemv_plan* plan,
+                                     hipStream_t stream);
+/* Compulsory bytes one launch moves: weights, scales, inputs, outputs and
+ * biases of every descriptor. */
+double infer_hip_w8a16_gemv_plan_bytes(const infer_hip_gemv_plan* plan);
+int infer_hip_w8a16_gemv_plan_destroy(infer_hip_gemv_plan* plan);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* INFER_LINEAR_H */

@@ -1,0 +1,117 @@
+// Device-side helpers shared by the Linear kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qlin {
+
+constexpr int kWave = 64;
+
+// BF16 word -> FP32: the word is the high half of the float.
+__device__ __forceinline__ float bf16_to_f32(uint32_t word) {
+  return __uint_as_float(word << 16);
+}
+// Low / high BF16 of a packed pair -> FP32 (one VALU op each).
+__device__ __forceinline__ float bf16_lo(uint32_t pair) {
+  return __uint_as_float(pair << 16);
+}
+__device__ __forceinline__ float bf16_hi(uint32_t pair) {
+  return __uint_as_float(pair & 0xFFFF0000u);
+}
+
+// FP32 -> BF16 round-to-nearest-even; a NaN keeps its high half with the
+// quiet bit set.  This is the textbook bit method (the reference states the
+// same rounding at tools/export_model.py:123-131 and uses RNE in its kernels).
+__device__ __forceinline__ uint16_t f32_to_bf16(float value) {
+  uint32_t bits = __float_as_uint(value);
+  if ((bits & 0x7F800000u) == 0x7F800000u && (bits & 0x007FFFFFu) != 0u) {
+    return static_cast<uint16_t>((bits >> 16) | 0x0040u);
+  }
+  bits += 0x7FFFu + ((bits >> 16) & 1u);
+  return static_cast<uint16_t>(bits >> 16);
+}
+
+// Pack two FP32 values, already exactly representable in BF16 (for example
+// small integers), into a BF16 pair by truncation: lo in bits 0-15.
+__device__ __forceinline__ uint32_t pack_bf16_trunc(float lo, float hi) {
+  return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+}
+
+// Sign-extended byte b of a dword, as FP32.  hipcc lowers each of these to a
+// single v_cvt_f32_i32 with an SDWA byte select.
+__device__ __forceinline__ float sbyte0(uint32_t v) {
+  return static_cast<float>(static_cast<int8_t>(v));
+}
+__device__ __forceinline__ float sbyte1(uint32_t v) {
+  return static_cast<float>(static_cast<int8_t>(v >> 8));
+}
+__device__ __forceinline__ float sbyte2(uint32_t v) {
+  return static_cast<float>(static_cast<int8_t>(v >> 16));
+}
+__device__ __forceinline__ float sbyte3(uint32_t v) {
+  return static_cast<float>(static_cast<int>(v) >> 24);
+}
+
+// Sum over the 64 lanes of a wave; every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset);
+  return v;
+}
+
+// Reduce RB per-lane partials (one per row) across the wave with a
+// reduce-scatter butterfly: after log2(RB) halving steps each lane holds one
+// row, then the remaining offsets finish the sum.  On return vals[0] in every
+// lane holds the total of row `reduced_row(lane)`.
+template <int RB>
+__device__ __forceinline__ void wave_reduce_rows(float (&vals)[RB], int lane) {
+  static_assert(RB >= 1 && RB <= 64 && (RB & (RB - 1)) == 0, "RB power of 2");
+  int count = RB;
+  int offset = 32;
+#pragma unroll
+  for (int step = RB; step > 1; step >>= 1) {
+    const int half = count >> 1;
+    const bool upper = (lane & offset) != 0;
+#pragma unroll
+    for (int i = 0; i < step / 2; ++i) {
+      const float send = upper ? vals[i] : vals[i + half];
+      const float keep = upper ? vals[i + half] : vals[i];
+      vals[i] = keep + __shfl_xor(send, offset);
+    }
+    count = half;
+    offset >>= 1;
+  }
+#pragma unroll
+  for (; offset > 0; offset >>= 1) vals[0] += __shfl_xor(vals[0], offset);
+}
+
+// Row index (0..RB-1) whose total wave_reduce_rows leaves in this lane.
+template <int RB>
+__device__ __forceinline__ int reduced_row(int lane) {
+  int row = 0;
+  int offset = 32;
+#pragma unroll
+  for (int step = RB; step > 1; step >>= 1) {
+    if (lane & offset) row += step >> 1;
+    offset >>= 1;
+  }
+  return row;
+}
+
+// The lane that writes row `reduced_row(lane)`: the lowest lane of each
+// group of 64 / RB lanes.
+template <int RB>
+__device__ __forceinline__ bool is_row_writer(int lane) {
+  return (lane & (kWave / RB - 1)) == 0;
+}
+
+// 16-byte global load that bypasses nothing but marks the line as streaming
+// (the weights are read once per call).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_stream16(const void* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+}  // namespace qlin

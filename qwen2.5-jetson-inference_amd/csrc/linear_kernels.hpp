@@ -1,0 +1,62 @@
+// Internal launch interface between the kernel files (not part of the ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace qlin {
+
+struct W8GemvArgs {
+  const int8_t* w;     // [n, k] int8
+  const uint16_t* s;   // [n, k / 64] BF16 scales
+  const uint16_t* bias;  // [n] BF16 or nullptr
+  const uint16_t* x;   // [k] BF16
+  uint16_t* y;         // [n] BF16
+  int n;
+  int k;
+};
+
+// One GEMV of a grouped launch; block_begin is the first block index of the
+// launch that works on it (descriptors sorted by block_begin).
+struct W8GroupDesc {
+  const int8_t* w;
+  const uint16_t* s;
+  const uint16_t* bias;
+  const uint16_t* x;
+  uint16_t* y;
+  int n;
+  int k;
+  int block_begin;
+  int pad;
+};
+
+struct Bf16GemvArgs {
+  const uint16_t* w;     // [n, k] BF16
+  const uint16_t* bias;  // [n] BF16 or nullptr
+  const uint16_t* x;     // [k] BF16
+  uint16_t* y;           // [n] BF16
+  int n;
+  int k;
+};
+
+// gemv.hip
+bool w8a16_gemv_fast_supported(const int8_t* w, const uint16_t* x, int k);
+void launch_w8a16_gemv_fast(const W8GemvArgs& a, hipStream_t stream);
+void launch_w8a16_linear_generic(const int8_t* w, const uint16_t* s, int group_size,
+                                 const uint16_t* bias, const uint16_t* x, uint16_t* y,
+                                 int tokens, int n, int k, hipStream_t stream);
+bool bf16_gemv_fast_supported(const uint16_t* w, const uint16_t* x, int k);
+void launch_bf16_gemv_fast(const Bf16GemvArgs& a, hipStream_t stream);
+void launch_bf16_linear_generic(const uint16_t* w, const uint16_t* bias, const uint16_t* x,
+                                uint16_t* y, int tokens, int n, int k, hipStream_t stream);
+size_t lm_head_blocks(int vocab, int in_features, bool fast);
+
+// Grouped W8A16 GEMV: the slot class S = ceil(K / 1024) of a descriptor,
+// the rows one block of class S covers, and the launch of one class's table.
+int w8a16_slot_class(int k);
+int w8a16_grouped_rows_per_block(int slot_class);
+void launch_w8a16_gemv_grouped(int slot_class, const W8GroupDesc* device_descs, int count,
+                               int total_blocks, hipStream_t stream);
+
+}  // namespace qlin

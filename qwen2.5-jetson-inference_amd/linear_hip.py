@@ -1,0 +1,217 @@
+"""Python binding of the MI355X Linear hot path (``libinfer_linear.so``).
+
+The functions mirror the reference's operator boundary,
+``include/infer/cuda_ops.hpp`` (Greedy-cy/qwen2.5-jetson-inference):
+same names, same argument order and meaning, raw device pointers plus a
+stream.  Each argument may be a device pointer (``int``) or a contiguous
+``torch`` CUDA tensor; ``None`` is a null pointer.  A nonzero status from
+the C ABI raises :class:`InferError` (the reference throws ``infer::Error``,
+``include/infer/common.hpp:66-82``).
+
+There is no fallback: if the library is missing, :func:`load` raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libinfer_linear.so")
+
+OK = 0
+INVALID_ARGUMENT = 1
+LAUNCH_FAILED = 2
+RUNTIME_ERROR = 3
+
+# Every symbol include/infer_linear.h declares.
+EXPORTED_SYMBOLS = (
+    "infer_hip_last_error",
+    "infer_hip_abi_version",
+    "infer_hip_gemv_bf16",
+    "infer_hip_gemm_bf16",
+    "infer_hip_lm_head_bf16",
+    "infer_hip_lm_head_workspace_entries",
+    "infer_hip_gemv_w8a16",
+    "infer_hip_gemm_w8a16",
+    "infer_hip_w8a16_gemv_plan_create",
+    "infer_hip_w8a16_gemv_plan_launch",
+    "infer_hip_w8a16_gemv_plan_bytes",
+    "infer_hip_w8a16_gemv_plan_destroy",
+)
+
+
+class W8A16GemvDesc(ctypes.Structure):
+    """infer_hip_w8a16_gemv_desc: the arguments of one gemv_w8a16 call."""
+    _fields_ = [
+        ("weight", ctypes.c_void_p),
+        ("scales", ctypes.c_void_p),
+        ("group_size", ctypes.c_int),
+        ("bias", ctypes.c_void_p),
+        ("input", ctypes.c_void_p),
+        ("output", ctypes.c_void_p),
+        ("out_features", ctypes.c_int),
+        ("in_features", ctypes.c_int),
+    ]
+
+
+class InferError(RuntimeError):
+    """A nonzero status from the C ABI, with the library's message."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(message)
+        self.status = status
+
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the HIP library (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise InferError(RUNTIME_ERROR,
+                         f"{LIB_PATH} is missing: run __graft_entry__.build()")
+    lib = ctypes.CDLL(LIB_PATH)
+    p, i = ctypes.c_void_p, ctypes.c_int
+    lib.infer_hip_last_error.restype = ctypes.c_char_p
+    lib.infer_hip_abi_version.restype = i
+    sigs = {
+        "infer_hip_gemv_bf16": [p, p, p, p, i, i, p],
+        "infer_hip_gemm_bf16": [p, p, p, p, i, i, i, p],
+        "infer_hip_lm_head_bf16": [p, p, p, p, p, p, p, i, i, p],
+        "infer_hip_gemv_w8a16": [p, p, i, p, p, p, i, i, p],
+        "infer_hip_gemm_w8a16": [p, p, i, p, p, p, i, i, i, p],
+    }
+    for name, args in sigs.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = i
+    lib.infer_hip_lm_head_workspace_entries.argtypes = [i, i]
+    lib.infer_hip_lm_head_workspace_entries.restype = ctypes.c_size_t
+    lib.infer_hip_w8a16_gemv_plan_create.argtypes = [p, i, ctypes.POINTER(p)]
+    lib.infer_hip_w8a16_gemv_plan_create.restype = i
+    lib.infer_hip_w8a16_gemv_plan_launch.argtypes = [p, p]
+    lib.infer_hip_w8a16_gemv_plan_launch.restype = i
+    lib.infer_hip_w8a16_gemv_plan_bytes.argtypes = [p]
+    lib.infer_hip_w8a16_gemv_plan_bytes.restype = ctypes.c_double
+    lib.infer_hip_w8a16_gemv_plan_destroy.argtypes = [p]
+    lib.infer_hip_w8a16_gemv_plan_destroy.restype = i
+    _lib = lib
+    return lib
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    if not t.is_cuda:
+        raise InferError(INVALID_ARGUMENT, "tensor must live on the GPU")
+    if not t.is_contiguous():
+        raise InferError(INVALID_ARGUMENT, "tensor must be contiguous")
+    return t.data_ptr()
+
+
+def _stream(stream):
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def _check(status: int) -> None:
+    if status != OK:
+        msg = load().infer_hip_last_error().decode("utf-8", "replace")
+        raise InferError(status, msg)
+
+
+def gemv_bf16(weight, bias, input, output, out_features, in_features,
+              stream=None):
+    """cuda_ops.hpp:24-26."""
+    _check(load().infer_hip_gemv_bf16(_ptr(weight), _ptr(bias), _ptr(input),
+                                      _ptr(output), out_features, in_features,
+                                      _stream(stream)))
+
+
+def gemm_bf16(weight, bias, input, output, tokens, out_features, in_features,
+              stream=None):
+    """cuda_ops.hpp:32-35."""
+    _check(load().infer_hip_gemm_bf16(_ptr(weight), _ptr(bias), _ptr(input),
+                                      _ptr(output), tokens, out_features,
+                                      in_features, _stream(stream)))
+
+
+def lm_head_workspace_entries(vocab: int, in_features: int) -> int:
+    return int(load().infer_hip_lm_head_workspace_entries(vocab, in_features))
+
+
+def lm_head_bf16(weight, bias, input, logits, block_max_value,
+                 block_max_index, argmax, vocab, in_features, stream=None):
+    """cuda_ops.hpp:42-45 (argmax over FP32 sums, ties to the lowest index)."""
+    _check(load().infer_hip_lm_head_bf16(
+        _ptr(weight), _ptr(bias), _ptr(input), _ptr(logits),
+        _ptr(block_max_value), _ptr(block_max_index), _ptr(argmax), vocab,
+        in_features, _stream(stream)))
+
+
+def gemv_w8a16(weight, scales, group_size, bias, input, output, out_features,
+               in_features, stream=None):
+    """cuda_ops.hpp:47-50."""
+    _check(load().infer_hip_gemv_w8a16(_ptr(weight), _ptr(scales), group_size,
+                                       _ptr(bias), _ptr(input), _ptr(output),
+                                       out_features, in_features,
+                                       _stream(stream)))
+
+
+def gemm_w8a16(weight, scales, group_size, bias, input, output, tokens,
+               out_features, in_features, stream=None):
+    """cuda_ops.hpp:51-55."""
+    _check(load().infer_hip_gemm_w8a16(_ptr(weight), _ptr(scales), group_size,
+                                       _ptr(bias), _ptr(input), _ptr(output),
+                                       tokens, out_features, in_features,
+                                       _stream(stream)))
+
+
+class W8A16GemvPlan:
+    """A grouped W8A16 GEMV plan: ``calls`` is a sequence of
+    ``(weight, scales, group_size, bias, input, output, out_features,
+    in_features)`` tuples, each the arguments of one independent
+    :func:`gemv_w8a16` call.  The tensors must outlive the plan."""
+
+    def __init__(self, calls):
+        calls = list(calls)
+        arr = (W8A16GemvDesc * len(calls))()
+        for d, c in zip(arr, calls):
+            w, s, g, b, x, y, n, k = c
+            d.weight, d.scales, d.group_size = _ptr(w), _ptr(s), g
+            d.bias, d.input, d.output = _ptr(b), _ptr(x), _ptr(y)
+            d.out_features, d.in_features = n, k
+        handle = ctypes.c_void_p()
+        _check(load().infer_hip_w8a16_gemv_plan_create(
+            ctypes.cast(arr, ctypes.c_void_p) if calls else None, len(calls),
+            ctypes.byref(handle)))
+        self._handle = handle
+        self.count = len(calls)
+
+    @property
+    def bytes(self) -> float:
+        """Compulsory bytes one launch moves."""
+        return float(load().infer_hip_w8a16_gemv_plan_bytes(self._handle))
+
+    def launch(self, stream=None) -> None:
+        _check(load().infer_hip_w8a16_gemv_plan_launch(self._handle, _stream(stream)))
+
+    def close(self) -> None:
+        if self._handle:
+            _check(load().infer_hip_w8a16_gemv_plan_destroy(self._handle))
+            self._handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

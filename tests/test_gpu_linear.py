@@ -1,0 +1,242 @@
+"""GPU parity of the Linear hot path through the C ABI, against the CPU
+oracle on the same bytes.
+
+Bar (stated per test): per output |a - e| <= max(1e-2 |e|, 1e-3 rms(e))
+against the oracle's FP32 sums (the BASELINE north star), plus the
+reference's own tolerances where its tests state them: max(1/64, 1 %) for
+W8A16 (test_cuda.cpp:587-594) and max(0.004, 0.8 %) for BF16
+(test_cuda.cpp:611-619).  Argmax must be equal.  Dequantisation (int8
+unpacking and group-scale indexing) must be bit-exact.
+"""
+import numpy as np
+import pytest
+
+import refcases as rc
+from helpers import bf16_out, check_close, to_dev, words
+
+pytestmark = pytest.mark.gpu
+
+W8_REF_CASES = (rc.W8A16_TAIL_CASES + rc.W8A16_QWEN_CASES + rc.W8A16_PREFILL_CASES
+                + rc.W8A16_ALIGNED_K_CASES)
+
+
+def _ref_tol(actual_words, expected, floor, rel):
+    a = rc.bf16_values(actual_words).astype(np.float64).ravel()
+    e = np.asarray(expected, np.float64).ravel()
+    tol = np.maximum(floor, rel * np.abs(e))
+    bad = np.nonzero(np.abs(a - e) > tol)[0]
+    assert bad.size == 0, f"{bad.size} outside max({floor}, {rel}|e|): first {a[bad[0]]} vs {e[bad[0]]}"
+
+
+def _run_w8(hip, dev, q, s, bias, x, m, n, k, gemm=True):
+    dq, ds, dx = to_dev(q, dev), to_dev(s, dev), to_dev(x, dev)
+    db = to_dev(bias, dev) if bias is not None else None
+    y = bf16_out((m, n), dev)
+    if gemm:
+        hip.gemm_w8a16(dq, ds, 64, db, dx, y, m, n, k)
+    else:
+        hip.gemv_w8a16(dq, ds, 64, db, dx, y, n, k)
+    return words(y)
+
+
+@pytest.mark.parametrize("case", W8_REF_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_w8a16_reference_cases(hip, orc, dev, case):
+    # check_w8a16_linear_case, test_cuda.cpp:519-609.
+    m, n, k, bias = case
+    q, s, x, b = rc.w8a16_linear_case(m, n, k)
+    bb = b if bias else None
+    exp32, _ = orc.w8a16_reference(q, s, 64, bb, x)
+    gemm = _run_w8(hip, dev, q, s, bb, x, m, n, k, gemm=True)
+    gemv = _run_w8(hip, dev, q, s, bb, x[:1], 1, n, k, gemm=False)
+    _ref_tol(gemm, exp32, 1.0 / 64, 0.01)
+    check_close(gemm, exp32, what="gemm_w8a16")
+    check_close(gemv, exp32[:1], what="gemv_w8a16")
+    # GEMV equals GEMM row 0 within the reference bound (test_cuda.cpp:604-608)
+    _ref_tol(gemv[0], rc.bf16_values(gemm[0]), 1.0 / 64, 0.01)
+
+
+def _one_hot_positions(k):
+    pos = {0, 1, 15, 16, 63, 64, 65, k // 2, k - 64, k - 17, k - 1}
+    pos.update(range(1023, min(k, 1100), 16))  # second chunk slot of a lane
+    return sorted(p for p in pos if 0 <= p < k)
+
+
+@pytest.mark.parametrize("n,k", [(128, 896), (96, 4864), (64, 1216), (24, 1024)])
+def test_w8a16_gemv_dequant_is_bit_exact(hip, dev, n, k):
+    # With x = e_j the GEMV computes bf16(q[n, j] * s[n, j / 64]) with no
+    # rounding before the final BF16 one: a bitwise check of the kernel's
+    # int8 unpacking and group-scale indexing.
+    rng = rc.philox(20 + k)
+    q, s = rc.w8a16_synthetic(rng, n, k)
+    q[0, :] = 127
+    q[1, :] = -127
+    dq, ds = to_dev(q, dev), to_dev(s, dev)
+    xs = np.zeros((len(_one_hot_positions(k)), k), np.uint16)
+    for i, j in enumerate(_one_hot_positions(k)):
+        xs[i, j] = rc.bf16_words(np.float32(1.0))
+    for i, j in enumerate(_one_hot_positions(k)):
+        y = bf16_out((n,), dev)
+        hip.gemv_w8a16(dq, ds, 64, None, to_dev(xs[i], dev), y, n, k)
+        expect = rc.bf16_words((q[:, j].astype(np.float32)
+                                * rc.bf16_values(s[:, j // 64])).astype(np.float32))
+        np.testing.assert_array_equal(words(y), expect, err_msg=f"column {j}")
+
+
+def test_w8a16_k_zero_gives_bias(hip, dev):
+    n = 9
+    b = rc.bf16_words(np.linspace(-1, 1, n).astype(np.float32))
+    y = bf16_out((n,), dev)
+    dummy = to_dev(np.zeros(16, np.int8), dev)
+    hip.gemv_w8a16(dummy, to_dev(np.zeros(16, np.uint16), dev), 64, to_dev(b, dev),
+                   to_dev(np.zeros(8, np.uint16), dev), y, n, 0)
+    np.testing.assert_array_equal(words(y), b)
+
+
+def test_w8a16_misaligned_pointers_take_exact_fallback(hip, orc, dev):
+    # kernels.cu:1632-1636 sends unaligned input to the scalar kernel; the
+    # result must agree with the aligned fast path.
+    import torch
+    n, k = 200, 896
+    rng = rc.philox(30)
+    q, s = rc.w8a16_synthetic(rng, n, k)
+    x = rc.bf16_normal(rng, (1, k))
+    exp32, _ = orc.w8a16_reference(q, s, 64, None, x)
+    qbuf = torch.zeros(n * k + 16, dtype=torch.int8, device=dev)
+    qbuf[1:1 + n * k] = torch.from_numpy(q.ravel()).to(dev)
+    xbuf = torch.zeros(k + 8, dtype=torch.bfloat16, device=dev)
+    xbuf[1:1 + k] = to_dev(x.ravel(), dev)
+    y = bf16_out((n,), dev)
+    hip.gemv_w8a16(qbuf.data_ptr() + 1, to_dev(s, dev), 64, None, xbuf.data_ptr() + 2, y, n, k)
+    check_close(words(y), exp32[0], what="misaligned gemv_w8a16")
+
+
+@pytest.mark.parametrize("case", rc.BF16_LINEAR_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_bf16_reference_cases(hip, orc, dev, case):
+    # check_bf16_linear_case, test_cuda.cpp:621-694.
+    m, n, k, bias = case
+    w, x, b = rc.bf16_linear_case(m, n, k)
+    bb = b if bias else None
+    exp = orc.bf16_linear_reference(w, bb, x)
+    dw, dx = to_dev(w, dev), to_dev(x, dev)
+    db = to_dev(bb, dev) if bias else None
+    y = bf16_out((m, n), dev)
+    hip.gemm_bf16(dw, db, dx, y, m, n, k)
+    _ref_tol(words(y), exp, 0.004, 0.008)
+    y1 = bf16_out((n,), dev)
+    hip.gemv_bf16(dw, db, to_dev(x[0], dev), y1, n, k)
+    _ref_tol(words(y1), exp[0], 0.004, 0.008)
+
+
+@pytest.mark.parametrize("case", rc.BF16_GEMV_QWEN_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_bf16_gemv_qwen_cases(hip, orc, dev, case):
+    # check_bf16_gemv_qwen_case, test_cuda.cpp:718-786.
+    n, k, bias = case
+    w, x, b = rc.bf16_gemv_qwen_case(n, k)
+    bb = b if bias else None
+    exp = orc.linear_fp32(rc.bf16_values(w), None if bb is None else rc.bf16_values(bb),
+                          rc.bf16_values(x))
+    y = bf16_out((n,), dev)
+    hip.gemv_bf16(to_dev(w, dev), to_dev(bb, dev) if bias else None, to_dev(x, dev), y, n, k)
+    _ref_tol(words(y), exp, 0.004, 0.008)
+    check_close(words(y), exp, what="gemv_bf16")
+
+
+def _lm_head(hip, dev, e, h, vocab, k):
+    import torch
+    entries = hip.lm_head_workspace_entries(vocab, k)
+    bv = torch.empty((vocab + 7) // 8, dtype=torch.float32, device=dev)
+    bi = torch.empty((vocab + 7) // 8, dtype=torch.int32, device=dev)
+    am = torch.full((1,), -7, dtype=torch.int32, device=dev)
+    logits = bf16_out((vocab,), dev)
+    assert entries <= bv.numel()
+    hip.lm_head_bf16(to_dev(e, dev), None, to_dev(h, dev), logits, bv, bi, am, vocab, k)
+    return words(logits), int(am.cpu().item())
+
+
+@pytest.mark.parametrize("case", rc.LM_HEAD_TIE_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_lm_head_tie_cases(hip, orc, dev, case):
+    # check_lm_head_fused_case, test_cuda.cpp:790-880: ties to the lowest index.
+    vocab, k, ta, tb = case
+    e, h = rc.lm_head_fused_case(vocab, k, ta, tb)
+    l32, _, idx = orc.lm_head(e, h)
+    logits, am = _lm_head(hip, dev, e, h, vocab, k)
+    assert am == idx == ta
+    _ref_tol(logits, l32, 0.008, 0.01)
+    lv = rc.bf16_values(logits)
+    assert lv[am] == lv.max()
+
+
+# ---------------------------------------------- BASELINE configs 1 and 2 --
+
+@pytest.mark.parametrize("shape", rc.QWEN_LINEARS, ids=lambda s: s[0])
+def test_config1_w8a16_gemv_synthetic(hip, orc, dev, shape):
+    # Config 1: q ~ U{-127..127}, s = bf16(|N(0,.02)|/127), x = bf16(N(0,1)),
+    # seed 1; CPU FP32 path (cpu_ops.cpp:23-30) on the exactly dequantised
+    # weights is the oracle.
+    name, n, k, _ = shape
+    rng = rc.philox(1 + 1000 * rc.QWEN_LINEARS.index(shape))
+    q, s = rc.w8a16_synthetic(rng, n, k)
+    x = rc.bf16_normal(rng, (k,))
+    exp = orc.linear_fp32(orc.dequant_w8a16(q, s), None, rc.bf16_values(x))
+    y = bf16_out((n,), dev)
+    hip.gemv_w8a16(to_dev(q, dev), to_dev(s, dev), 64, None, to_dev(x, dev), y, n, k)
+    stats = check_close(words(y), exp, what=name)
+    assert stats["bit_identical"] > 0.95, stats
+
+
+def test_config2_lm_head_full_vocab(hip, orc, dev):
+    # Config 2: E = bf16(N(0, 0.02)) [151936, 896], h = bf16(N(0, 1)), seed 2.
+    # The int32 argmax must equal the CPU FP32 argmax exactly.
+    rng = rc.philox(2)
+    e = rc.bf16_normal(rng, (rc.VOCAB, rc.HIDDEN), 0.02)
+    h = rc.bf16_normal(rng, (rc.HIDDEN,))
+    l32, _, idx = orc.lm_head(e, h)
+    logits, am = _lm_head(hip, dev, e, h, rc.VOCAB, rc.HIDDEN)
+    assert am == idx
+    stats = check_close(logits, l32, what="lm_head logits")
+    assert stats["bit_identical"] > 0.95, stats
+
+
+# ------------------------------------------------------ grouped GEMV plan --
+
+def test_w8a16_plan_matches_single_calls(hip, orc, dev):
+    # Mixed K classes and biases in one plan; every output equals the oracle
+    # and (up to the reduction order) the per-call kernel.
+    import torch
+    rng = rc.philox(40)
+    calls, expected, singles = [], [], []
+    for (name, n, k, bias) in rc.QWEN_LINEARS + (("odd", 37, 1216, True), ("wide", 70, 8192, False)):
+        q, s = rc.w8a16_synthetic(rng, n, k)
+        x = rc.bf16_normal(rng, (k,))
+        b = rc.bf16_normal(rng, (n,)) if bias else None
+        exp32, _ = orc.w8a16_reference(q, s, 64, b, x)
+        dq, ds, dx = to_dev(q, dev), to_dev(s, dev), to_dev(x, dev)
+        db = to_dev(b, dev) if bias else None
+        y = bf16_out((n,), dev)
+        calls.append((dq, ds, 64, db, dx, y, n, k))
+        expected.append(exp32[0])
+        y1 = bf16_out((n,), dev)
+        hip.gemv_w8a16(dq, ds, 64, db, dx, y1, n, k)
+        singles.append(y1)
+    plan = hip.W8A16GemvPlan(calls)
+    try:
+        for _ in range(2):  # a second launch rewrites the same outputs
+            plan.launch()
+            torch.cuda.synchronize()
+            for c, e, y1 in zip(calls, expected, singles):
+                check_close(words(c[5]), e, what="plan")
+                from helpers import ulp_distance_bf16
+                assert ulp_distance_bf16(words(c[5]), words(y1)).max() <= 1
+    finally:
+        plan.close()
+
+
+def test_w8a16_plan_rejects_unsupported_descriptors(hip, dev):
+    q = to_dev(np.zeros((4, 70), np.int8), dev)
+    s = to_dev(np.zeros((4, 2), np.uint16), dev)
+    x = to_dev(np.zeros(70, np.uint16), dev)
+    y = bf16_out((4,), dev)
+    with pytest.raises(hip.InferError):
+        hip.W8A16GemvPlan([(q, s, 64, None, x, y, 4, 70)])
+    with pytest.raises(hip.InferError):
+        hip.W8A16GemvPlan([(q, s, 32, None, x, y, 4, 64)])
