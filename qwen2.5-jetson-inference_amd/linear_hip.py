@@ -65,15 +65,37 @@ class InferError(RuntimeError):
 _lib = None
 
 
+def _hip_runtimes_mapped():
+    try:
+        with open("/proc/self/maps") as f:
+            return sorted({line.split()[-1] for line in f
+                           if "libamdhip64" in line and "/" in line})
+    except OSError:
+        return []
+
+
 def load() -> ctypes.CDLL:
-    """Load the HIP library (raises if it has not been built)."""
+    """Load the HIP library (raises if it has not been built).
+
+    torch (when installed) is imported first: its wheel ships its own HIP
+    runtime, whose soname (libamdhip64.so.7) the library's dependency then
+    resolves to, so the process holds one HIP runtime.  Two runtimes in one
+    process cannot share the GPU; that case raises instead of running."""
     global _lib
     if _lib is not None:
         return _lib
     if not os.path.exists(LIB_PATH):
         raise InferError(RUNTIME_ERROR,
                          f"{LIB_PATH} is missing: run __graft_entry__.build()")
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(LIB_PATH)
+    runtimes = _hip_runtimes_mapped()
+    if len(runtimes) > 1:
+        raise InferError(RUNTIME_ERROR,
+                         "two HIP runtimes are loaded in this process: " + ", ".join(runtimes))
     p, i = ctypes.c_void_p, ctypes.c_int
     lib.infer_hip_last_error.restype = ctypes.c_char_p
     lib.infer_hip_abi_version.restype = i

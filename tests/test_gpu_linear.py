@@ -73,7 +73,7 @@ def test_w8a16_gemv_dequant_is_bit_exact(hip, dev, n, k):
     dq, ds = to_dev(q, dev), to_dev(s, dev)
     xs = np.zeros((len(_one_hot_positions(k)), k), np.uint16)
     for i, j in enumerate(_one_hot_positions(k)):
-        xs[i, j] = rc.bf16_words(np.float32(1.0))
+        xs[i, j] = 0x3F80  # BF16 1.0
     for i, j in enumerate(_one_hot_positions(k)):
         y = bf16_out((n,), dev)
         hip.gemv_w8a16(dq, ds, 64, None, to_dev(xs[i], dev), y, n, k)
