@@ -11,7 +11,7 @@ all resident in HBM before timing.
 
 Launch modes (--launch):
   plan   (default) all 168 independent GEMVs through one grouped plan: one
-         kernel per K class (K = 896: 144 GEMVs, K = 4864: 24 GEMVs).
+         kernel launch per step (infer_hip_w8a16_gemv_plan_launch).
   calls  168 separate infer_hip_gemv_w8a16 calls, the reference's per-Linear
          call pattern (src/qwen2.cpp:615-656).
 
@@ -60,6 +60,9 @@ def parse():
                     help="write per-shape and per-mode measurements to this JSON file")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic.json"),
                     help="committed HBM traffic per launch measured with rocprofv3 --pmc")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="after timing, run one device-to-device copy of this many MiB "
+                         "(the known-size reference for rocprofv3 --pmc byte counters)")
     return ap.parse_args()
 
 
@@ -84,33 +87,21 @@ class Layers:
         self.bytes = sum(gemv_bytes(c[6], c[7]) for c in self.calls)
 
 
-def time_steps(step, steps: int, warmup: int, marks=None):
-    """Warm up, then time `steps` calls of step() between synchronisations.
-    Returns (total ms, list of per-mark durations in ms)."""
+def time_steps(step, steps: int, warmup: int):
+    """Warm up, then time `steps` back-to-back calls of step() with events on
+    the current stream, synchronised on both sides.  Returns (total ms, None)."""
     import torch
     for _ in range(warmup):
         step(None)
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    rec = []
-    torch.cuda.synchronize()
     start.record()
     for _ in range(steps):
-        if marks:
-            ev = [torch.cuda.Event(enable_timing=True) for _ in range(marks + 1)]
-            rec.append(ev)
-            step(ev)
-        else:
-            step(None)
+        step(None)
     end.record()
     torch.cuda.synchronize()
-    total = start.elapsed_time(end)
-    per = []
-    if marks:
-        for i in range(marks):
-            per.append(sum(ev[i].elapsed_time(ev[i + 1]) for ev in rec) / len(rec))
-    return total, per
+    return start.elapsed_time(end), None
 
 
 def cpu_baseline(layers, seconds: float):
@@ -168,11 +159,39 @@ def check_outputs(layers, cpu_outs):
     return worst
 
 
+def lm_head_detail(dev, hip):
+    """Config 2: the fused LM head over two distinct 151936 x 896 BF16
+    embedding copies (545 MB, alternated so no call is served from cache)."""
+    import torch
+    vocab, k = 151936, 896
+    g = torch.Generator(device=dev)
+    g.manual_seed(2)
+    emb = [(torch.randn((vocab, k), device=dev, generator=g) * 0.02).to(torch.bfloat16)
+           for _ in range(2)]
+    h = torch.randn((k,), device=dev, generator=g).to(torch.bfloat16)
+    logits = torch.empty((vocab,), dtype=torch.bfloat16, device=dev)
+    bv = torch.empty(((vocab + 7) // 8,), dtype=torch.float32, device=dev)
+    bi = torch.empty(((vocab + 7) // 8,), dtype=torch.int32, device=dev)
+    am = torch.empty((1,), dtype=torch.int32, device=dev)
+    calls = [0]
+
+    def step(ev):
+        e = emb[calls[0] & 1]
+        calls[0] += 1
+        hip.lm_head_bf16(e, None, h, logits, bv, bi, am, vocab, k)
+    t, _ = time_steps(step, 100, 10)
+    nbytes = 2 * vocab * k + 2 * k + 2 * vocab + 4
+    us = t / 100 * 1e3
+    return {"us_per_call": round(us, 2), "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "bytes": nbytes}
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not "
-              "supported (the sharding design is described in DESIGN.md)", file=sys.stderr)
+        print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not "
+              "supported (each GPU would serve its own model replica: value at N GPUs is "
+              "N x the one-GPU figure, and no collective is on the path)", file=sys.stderr)
         return 2
     import torch
     import linear_hip as hip
@@ -190,51 +209,33 @@ def main() -> int:
         for c in layers.calls:
             hip.gemv_w8a16(*c)
 
-    # The plan's two launches (K = 896 class, then K = 4864 class) bracketed
-    # by events so each kernel's duration is measured on its own stream.
-    k896 = [c for c in layers.calls if c[7] == 896]
-    k4864 = [c for c in layers.calls if c[7] == 4864]
-    plan_a = hip.W8A16GemvPlan(k896)
-    plan_b = hip.W8A16GemvPlan(k4864)
-    stream = torch.cuda.current_stream()
-
-    def step_plan_marked(ev):
-        if ev is None:
-            plan_a.launch(); plan_b.launch()
-            return
-        ev[0].record(stream)
-        plan_a.launch()
-        ev[1].record(stream)
-        plan_b.launch()
-        ev[2].record(stream)
-
     step = step_plan if args.launch == "plan" else step_calls
     total_ms, _ = time_steps(step, args.steps, args.warmup)
     ms = total_ms / args.steps
 
-    _, per = time_steps(step_plan_marked, args.steps, args.warmup, marks=2)
-    bytes_a = plan_a.bytes
-    bytes_b = plan_b.bytes
-    # the dominant kernel is the one with the larger share of the step's time
-    dom = ("w8a16_gemv_grouped_kernel<S=1> (144 GEMVs, K=896)", bytes_a, per[0]) \
-        if per[0] >= per[1] else \
-        ("w8a16_gemv_grouped_kernel<S=5> (24 GEMVs, K=4864)", bytes_b, per[1])
-    achieved = dom[1] / (dom[2] * 1e-3) / 1e9
+    # The dominant kernel is the grouped GEMV (in plan mode the only one: one
+    # launch per step, so the back-to-back step time IS its launch duration,
+    # measured by events on the stream it runs on).
+    if args.launch == "plan":
+        launch_ms = ms
+    else:
+        t, _ = time_steps(step_plan, args.steps, args.warmup)
+        launch_ms = t / args.steps
+    achieved = plan.bytes / (launch_ms * 1e-3) / 1e9
     traffic = None
     if os.path.exists(args.traffic):
         with open(args.traffic) as f:
-            t = json.load(f)
-        traffic = t.get("k896_bytes_per_launch")
+            traffic = json.load(f).get("w8a16_gemv_grouped_kernel")
     roofline = {
         "bound": "hbm",
-        "kernel": dom[0],
+        "kernel": "w8a16_gemv_grouped_kernel (168 GEMVs of one decode token)",
         "achieved": round(achieved, 1),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
         "traffic": traffic,
-        "algorithmic_bytes_per_launch": int(dom[1]),
-        "avg_launch_us": round(dom[2] * 1e3, 2),
+        "algorithmic_bytes_per_launch": int(plan.bytes),
+        "avg_launch_us": round(launch_ms * 1e3, 2),
         "step_GBs": round(layers.bytes / (ms * 1e-3) / 1e9, 1),
     }
 
@@ -255,6 +256,16 @@ def main() -> int:
                 "us_per_call": round(per_call * 1e3, 2),
                 "GBs": round(gemv_bytes(n, k) / (per_call * 1e-3) / 1e9, 1),
             }
+
+    if args.detail:
+        detail["lm_head"] = lm_head_detail(dev, hip)
+    if args.copy_calibration > 0:
+        src = torch.empty(args.copy_calibration << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     cpu = None
     if args.cpu_seconds > 0:
@@ -291,7 +302,7 @@ def main() -> int:
         with open(args.detail, "w") as f:
             json.dump({"line": line, "detail": detail}, f, indent=1)
     print(json.dumps(line))
-    plan.close(); plan_a.close(); plan_b.close()
+    plan.close()
     return 0
 
 

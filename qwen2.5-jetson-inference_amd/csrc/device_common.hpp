@@ -106,11 +106,32 @@ __device__ __forceinline__ bool is_row_writer(int lane) {
   return (lane & (kWave / RB - 1)) == 0;
 }
 
-// 16-byte global load that bypasses nothing but marks the line as streaming
-// (the weights are read once per call).
+// Global-address-space access.  Pointers that reach a kernel through memory
+// (a descriptor table) are generic to the compiler, which would then emit
+// FLAT instructions; these casts keep every access a global_* instruction.
+#define QLIN_GLOBAL __attribute__((address_space(1)))
+
+template <typename T>
+__device__ __forceinline__ T gload(const T* p) {
+  return *(const QLIN_GLOBAL T*)(p);
+}
+template <typename T>
+__device__ __forceinline__ void gstore(T* p, T v) {
+  *(QLIN_GLOBAL T*)(p) = v;
+}
+
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte global load.
+__device__ __forceinline__ uint4 load_global16(const void* p) {
+  const u32x4 v = *(const QLIN_GLOBAL u32x4*)(p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// 16-byte global load marked as streaming (the weights are read once per
+// call, so they should not displace reused lines).
 __device__ __forceinline__ uint4 load_stream16(const void* p) {
-  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  const u32x4 v = __builtin_nontemporal_load((const QLIN_GLOBAL u32x4*)(p));
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 

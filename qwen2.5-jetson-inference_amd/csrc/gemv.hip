@@ -33,7 +33,6 @@ namespace {
 
 constexpr int kBlock = 256;            // 4 waves
 constexpr int kWavesPerBlock = kBlock / kWave;
-constexpr int kMaxWaves = 256 * 16;    // persistent cap: 16 waves per CU
 
 // ---------------------------------------------------------------- W8A16 --
 
@@ -60,8 +59,8 @@ __device__ __forceinline__ float dot16_i8(const uint4 w, const float (&x)[16]) {
 
 // Load 16 BF16 activations (32 bytes) as FP32.
 __device__ __forceinline__ void load_x16(const uint16_t* x, float (&out)[16]) {
-  const uint4 a = *reinterpret_cast<const uint4*>(x);
-  const uint4 b = *reinterpret_cast<const uint4*>(x + 8);
+  const uint4 a = load_global16(x);
+  const uint4 b = load_global16(x + 8);
   out[0] = bf16_lo(a.x);  out[1] = bf16_hi(a.x);
   out[2] = bf16_lo(a.y);  out[3] = bf16_hi(a.y);
   out[4] = bf16_lo(a.z);  out[5] = bf16_hi(a.z);
@@ -72,83 +71,204 @@ __device__ __forceinline__ void load_x16(const uint16_t* x, float (&out)[16]) {
   out[14] = bf16_lo(b.w); out[15] = bf16_hi(b.w);
 }
 
-// One wave's share of a W8A16 GEMV: row steps first, first + stride, ...
-// below end, RB rows per step.  S = chunk slots per lane (K <= 1024 S).
+// The weights and scales of one slab (64 chunks of 16 int8) of R rows.
+template <int R>
+__device__ __forceinline__ void w8a16_load_rows(const W8GemvArgs& a, int row0, int row_end,
+                                                int c, bool cv, int groups, uint4 (&w)[R],
+                                                uint32_t (&s)[R]) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = row0 + r;
+    if (cv && row < row_end) {
+      w[r] = load_stream16(a.w + static_cast<size_t>(row) * a.k + 16 * c);
+      s[r] = gload(a.s + static_cast<size_t>(row) * groups + (c >> 2));
+    } else {
+      w[r] = make_uint4(0, 0, 0, 0);
+      s[r] = 0;
+    }
+  }
+}
+
+// Reduce the R row sums of a task across the wave and write them.
+template <int R>
+__device__ __forceinline__ void w8a16_finish_rows(const W8GemvArgs& a, int row0, int row_end,
+                                                  float (&acc)[R], int lane) {
+  wave_reduce_rows<R>(acc, lane);
+  if (is_row_writer<R>(lane)) {
+    const int row = row0 + reduced_row<R>(lane);
+    if (row < row_end) {
+      const float b = a.bias ? bf16_to_f32(gload(a.bias + row)) : 0.0f;
+      gstore(a.y + row, f32_to_bf16(acc[0] + b));
+    }
+  }
+}
+
+// The activations of one slab chunk c (16 BF16 as FP32), zero past K.
+__device__ __forceinline__ void w8a16_load_x(const W8GemvArgs& a, int c, bool cv,
+                                             float (&x)[16]) {
+  if (cv) {
+    load_x16(a.x + 16 * c, x);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) x[e] = 0.0f;
+  }
+}
+
+// One wave's share of a W8A16 GEMV: the R-row tasks starting at rows
+// first, first + stride, ... below row_end.  A row is walked in slabs of
+// 64 chunks (1 KiB of int8); lane l takes chunk l of every slab, so a lane
+// multiplies the same 16 activations into each of the R rows of a slab.
+// Per lane the sum is acc = fma(dot16(q, x), s, acc) slab by slab.
+// PF: the loads of the next (task, slab) unit are issued before the current
+// unit is computed, so each wave keeps two units in flight.
 // Requires K % 64 == 0, 16-byte aligned weight and input.
-template <int S, int RB>
-__device__ __forceinline__ void w8a16_wave_rows(const W8GemvArgs& a, int first, int stride,
-                                                int end) {
+template <int R, bool PF>
+__device__ __forceinline__ void w8a16_wave_span(const W8GemvArgs& a, int first, int stride,
+                                                int row_end) {
+  if (first >= row_end) return;
   const int lane = threadIdx.x & (kWave - 1);
   const int chunks = a.k >> 4;
   const int groups = a.k >> 6;
-
-  float xr[S][16];
+  const int slabs = (chunks + kWave - 1) / kWave;
+  if (slabs == 1) {
+    // K <= 1024: the activations stay in VGPRs for every task.
+    const bool cv = lane < chunks;
+    float x[16];
+    w8a16_load_x(a, lane, cv, x);
+    uint4 w[R];
+    uint32_t s[R];
+    w8a16_load_rows<R>(a, first, row_end, lane, cv, groups, w, s);
+    for (int row0 = first; row0 < row_end; row0 += stride) {
+      uint4 wn[R];
+      uint32_t sn[R];
+      if (PF) w8a16_load_rows<R>(a, row0 + stride, row_end, lane, cv, groups, wn, sn);
+      float acc[R];
 #pragma unroll
-  for (int j = 0; j < S; ++j) {
-    const int c = lane + kWave * j;
-    if (c < chunks) {
-      load_x16(a.x + 16 * c, xr[j]);
-    } else {
+      for (int r = 0; r < R; ++r) acc[r] = fmaf(dot16_i8(w[r], x), bf16_to_f32(s[r]), 0.0f);
+      w8a16_finish_rows<R>(a, row0, row_end, acc, lane);
+      if (PF) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) xr[j][e] = 0.0f;
-    }
-  }
-
-  for (int step = first; step < end; step += stride) {
-    const int r0 = step * RB;
-    uint4 wv[RB][S];
-    uint32_t sv[RB][S];
-#pragma unroll
-    for (int rr = 0; rr < RB; ++rr) {
-      const int row = r0 + rr;
-#pragma unroll
-      for (int j = 0; j < S; ++j) {
-        const int c = lane + kWave * j;
-        if (row < a.n && c < chunks) {
-          wv[rr][j] = load_stream16(a.w + static_cast<size_t>(row) * a.k + 16 * c);
-          sv[rr][j] = a.s[static_cast<size_t>(row) * groups + (c >> 2)];
-        } else {
-          wv[rr][j] = make_uint4(0, 0, 0, 0);
-          sv[rr][j] = 0;
+        for (int r = 0; r < R; ++r) {
+          w[r] = wn[r];
+          s[r] = sn[r];
         }
+      } else {
+        w8a16_load_rows<R>(a, row0 + stride, row_end, lane, cv, groups, w, s);
       }
     }
-    float acc[RB];
+    return;
+  }
+  // K > 1024: walk (task, slab) units in order, activations per slab.
+  int row0 = first;
+  int slab = 0;
+  float x[16];
+  uint4 w[R];
+  uint32_t s[R];
+  w8a16_load_x(a, lane, lane < chunks, x);
+  w8a16_load_rows<R>(a, row0, row_end, lane, lane < chunks, groups, w, s);
+  float acc[R];
 #pragma unroll
-    for (int rr = 0; rr < RB; ++rr) {
-      acc[rr] = 0.0f;
-#pragma unroll
-      for (int j = 0; j < S; ++j) {
-        acc[rr] = fmaf(dot16_i8(wv[rr][j], xr[j]), bf16_to_f32(sv[rr][j]), acc[rr]);
-      }
+  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+  while (row0 < row_end) {
+    const bool last = slab + 1 == slabs;
+    const int nrow0 = last ? row0 + stride : row0;
+    const int nslab = last ? 0 : slab + 1;
+    const int nc = nslab * kWave + lane;
+    const bool ncv = nc < chunks;
+    float xn[16];
+    uint4 wn[R];
+    uint32_t sn[R];
+    if (PF) {
+      w8a16_load_x(a, nc, ncv && nrow0 < row_end, xn);
+      w8a16_load_rows<R>(a, nrow0, row_end, nc, ncv, groups, wn, sn);
     }
-    wave_reduce_rows<RB>(acc, lane);
-    if (is_row_writer<RB>(lane)) {
-      const int row = r0 + reduced_row<RB>(lane);
-      if (row < a.n) {
-        const float b = a.bias ? bf16_to_f32(a.bias[row]) : 0.0f;
-        a.y[row] = f32_to_bf16(acc[0] + b);
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = fmaf(dot16_i8(w[r], x), bf16_to_f32(s[r]), acc[r]);
+    if (last) {
+      w8a16_finish_rows<R>(a, row0, row_end, acc, lane);
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+    }
+    if (PF) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) x[e] = xn[e];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        w[r] = wn[r];
+        s[r] = sn[r];
       }
+    } else {
+      w8a16_load_x(a, nc, ncv && nrow0 < row_end, x);
+      w8a16_load_rows<R>(a, nrow0, row_end, nc, ncv, groups, w, s);
+    }
+    row0 = nrow0;
+    slab = nslab;
+  }
+}
+
+// A single W8A16 GEMV: block b owns rows [b RPB, (b + 1) RPB); its waves take
+// R-row tasks round-robin.
+template <int R, int W, bool PF>
+__global__ __launch_bounds__(kBlock, W) void w8a16_gemv_kernel(W8GemvArgs a,
+                                                               int rows_per_block) {
+  const int begin = blockIdx.x * rows_per_block;
+  const int end = min(a.n, begin + rows_per_block);
+  const int wave = threadIdx.x / kWave;
+  w8a16_wave_span<R, PF>(a, begin + wave * R, kWavesPerBlock * R, end);
+}
+
+// A single W8A16 GEMV with rows longer than one slab, split over K: block b
+// owns rows [b R, b R + R) and wave w takes slabs w, w + 4, ..., so all slabs
+// of a row are in flight at once (a lone GEMV is latency-bound); the four
+// wave partials are summed through LDS in wave order.
+template <int R>
+__global__ __launch_bounds__(kBlock) void w8a16_gemv_splitk_kernel(W8GemvArgs a) {
+  __shared__ float part[kWavesPerBlock][R];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int row0 = blockIdx.x * R;
+  const int chunks = a.k >> 4;
+  const int groups = a.k >> 6;
+  const int slabs = (chunks + kWave - 1) / kWave;
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+  for (int slab = wave; slab < slabs; slab += kWavesPerBlock) {
+    const int c = slab * kWave + lane;
+    const bool cv = c < chunks;
+    float x[16];
+    w8a16_load_x(a, c, cv, x);
+    uint4 w[R];
+    uint32_t s[R];
+    w8a16_load_rows<R>(a, row0, a.n, c, cv, groups, w, s);
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = fmaf(dot16_i8(w[r], x), bf16_to_f32(s[r]), acc[r]);
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) part[wave][r] = acc[r];
+  }
+  __syncthreads();
+  if (threadIdx.x < R) {
+    const int row = row0 + threadIdx.x;
+    if (row < a.n) {
+      float v = part[0][threadIdx.x];
+      for (int w = 1; w < kWavesPerBlock; ++w) v += part[w][threadIdx.x];
+      const float b = a.bias ? bf16_to_f32(gload(a.bias + row)) : 0.0f;
+      gstore(a.y + row, f32_to_bf16(v + b));
     }
   }
 }
 
-// A single W8A16 GEMV; waves walk row steps grid-stride.
-template <int S, int RB>
-__global__ __launch_bounds__(kBlock) void w8a16_gemv_kernel(W8GemvArgs a) {
-  const int wave = (blockIdx.x * kBlock + threadIdx.x) / kWave;
-  const int nwaves = gridDim.x * kWavesPerBlock;
-  w8a16_wave_rows<S, RB>(a, wave, nwaves, (a.n + RB - 1) / RB);
-}
-
-// Many W8A16 GEMVs of one slot class S in one launch.  Block b belongs to
-// the descriptor d with block_begin[d] <= b < block_begin[d + 1] (descriptors
-// sorted by block_begin); within it, block b - block_begin[d] owns rows
-// [RPB (b - begin), RPB (b - begin + 1)), RPB = kWavesPerBlock * RB * kSteps.
-template <int S, int RB, int kSteps>
-__global__ __launch_bounds__(kBlock) void w8a16_gemv_grouped_kernel(
+// Many W8A16 GEMVs in one launch.  Block b belongs to the descriptor d with
+// block_begin[d] <= b < block_begin[d + 1] (descriptors sorted by
+// block_begin) and owns rows [RPB_d (b - block_begin[d]), ...) of it.
+// W = minimum waves per SIMD the register allocation must allow.
+template <int R, int W, bool PF>
+__global__ __launch_bounds__(kBlock, W) void w8a16_gemv_grouped_kernel(
     const W8GroupDesc* __restrict__ descs, int count) {
-  constexpr int kRowsPerBlock = kWavesPerBlock * RB * kSteps;
   const int b = blockIdx.x;
   int lo = 0, hi = count - 1;
   while (lo < hi) {  // last descriptor whose block_begin <= b
@@ -157,12 +277,10 @@ __global__ __launch_bounds__(kBlock) void w8a16_gemv_grouped_kernel(
   }
   const W8GroupDesc& d = descs[lo];
   const W8GemvArgs a{d.w, d.s, d.bias, d.x, d.y, d.n, d.k};
-  const int local = b - d.block_begin;
+  const int begin = (b - d.block_begin) * d.rows_per_block;
+  const int end = min(d.n, begin + d.rows_per_block);
   const int wave = threadIdx.x / kWave;
-  const int step0 = local * (kRowsPerBlock / RB);
-  const int steps_total = (a.n + RB - 1) / RB;
-  const int step_end = min(steps_total, step0 + kRowsPerBlock / RB);
-  w8a16_wave_rows<S, RB>(a, step0 + wave, kWavesPerBlock, step_end);
+  w8a16_wave_span<R, PF>(a, begin + wave * R, kWavesPerBlock * R, end);
 }
 
 // Any K, any alignment, any token count; each wave walks (token, row) items
@@ -200,7 +318,7 @@ __global__ __launch_bounds__(kBlock) void w8a16_linear_generic_kernel(
 // ----------------------------------------------------------------- BF16 --
 
 __device__ __forceinline__ void load_x8(const uint16_t* x, float (&out)[8]) {
-  const uint4 a = *reinterpret_cast<const uint4*>(x);
+  const uint4 a = load_global16(x);
   out[0] = bf16_lo(a.x); out[1] = bf16_hi(a.x);
   out[2] = bf16_lo(a.y); out[3] = bf16_hi(a.y);
   out[4] = bf16_lo(a.z); out[5] = bf16_hi(a.z);
@@ -236,62 +354,78 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
   }
 }
 
-// S = 8-element chunk slots per lane (K <= 512 S), RB = rows per wave step.
-// ARGMAX: also reduce the FP32 (sum + bias) of every row to one
-// (value, index) per block.  Requires K % 8 == 0, 16-byte aligned weight and
-// input.
-template <int S, int RB, bool ARGMAX>
-__global__ __launch_bounds__(kBlock) void bf16_gemv_kernel(
-    Bf16GemvArgs a, float* __restrict__ block_value, int* __restrict__ block_index) {
+// One wave's share of a BF16 GEMV, as w8a16_wave_span: R-row tasks, rows
+// walked in slabs of 64 chunks of 8 BF16 (1 KiB); for K <= 1024 (at most
+// two slabs) the activations stay in VGPRs.  Per lane the sum is a plain
+// FMA chain over the lane's chunks in order.  ARGMAX also folds
+// (sum + bias, row) of every written row into (best_v, best_i).
+// Requires K % 8 == 0, 16-byte aligned weight and input.
+template <int R, bool ARGMAX>
+__device__ __forceinline__ void bf16_wave_span(const Bf16GemvArgs& a, int first, int stride,
+                                               int row_end, float& best_v, int& best_i) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = (blockIdx.x * kBlock + threadIdx.x) / kWave;
-  const int nwaves = gridDim.x * kWavesPerBlock;
   const int chunks = a.k >> 3;
-
-  float xr[S][8];
+  const int slabs = (chunks + kWave - 1) / kWave;
+  const bool hoist = slabs <= 2;
+  float xh[2][8];
 #pragma unroll
-  for (int j = 0; j < S; ++j) {
-    const int c = lane + kWave * j;
-    if (c < chunks) {
-      load_x8(a.x + 8 * c, xr[j]);
+  for (int j = 0; j < 2; ++j) {
+    const int c = j * kWave + lane;
+    if (hoist && c < chunks) {
+      load_x8(a.x + 8 * c, xh[j]);
     } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) xr[j][e] = 0.0f;
+      for (int e = 0; e < 8; ++e) xh[j][e] = 0.0f;
     }
   }
-
-  float best_v = -INFINITY;
-  int best_i = INT_MAX;
-  const int row_steps = (a.n + RB - 1) / RB;
-  for (int step = wave; step < row_steps; step += nwaves) {
-    const int r0 = step * RB;
-    uint4 wv[RB][S];
+  for (int row0 = first; row0 < row_end; row0 += stride) {
+    float acc[R];
 #pragma unroll
-    for (int rr = 0; rr < RB; ++rr) {
-      const int row = r0 + rr;
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+    if (hoist) {
 #pragma unroll
-      for (int j = 0; j < S; ++j) {
-        const int c = lane + kWave * j;
-        if (row < a.n && c < chunks) {
-          wv[rr][j] = load_stream16(a.w + static_cast<size_t>(row) * a.k + 8 * c);
-        } else {
-          wv[rr][j] = make_uint4(0, 0, 0, 0);
+      for (int j = 0; j < 2; ++j) {
+        const int c = j * kWave + lane;
+        uint4 w[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int row = row0 + r;
+          w[r] = (j < slabs && c < chunks && row < row_end)
+                     ? load_stream16(a.w + static_cast<size_t>(row) * a.k + 8 * c)
+                     : make_uint4(0, 0, 0, 0);
         }
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = dot8_bf16(w[r], xh[j], acc[r]);
+      }
+    } else {
+      for (int slab = 0; slab < slabs; ++slab) {
+        const int c = slab * kWave + lane;
+        const bool cv = c < chunks;
+        float x[8];
+        if (cv) {
+          load_x8(a.x + 8 * c, x);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+        }
+        uint4 w[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int row = row0 + r;
+          w[r] = (cv && row < row_end)
+                     ? load_stream16(a.w + static_cast<size_t>(row) * a.k + 8 * c)
+                     : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = dot8_bf16(w[r], x, acc[r]);
       }
     }
-    float acc[RB];
-#pragma unroll
-    for (int rr = 0; rr < RB; ++rr) {
-      acc[rr] = 0.0f;
-#pragma unroll
-      for (int j = 0; j < S; ++j) acc[rr] = dot8_bf16(wv[rr][j], xr[j], acc[rr]);
-    }
-    wave_reduce_rows<RB>(acc, lane);
-    if (is_row_writer<RB>(lane)) {
-      const int row = r0 + reduced_row<RB>(lane);
-      if (row < a.n) {
-        const float v = acc[0] + (a.bias ? bf16_to_f32(a.bias[row]) : 0.0f);
-        a.y[row] = f32_to_bf16(v);
+    wave_reduce_rows<R>(acc, lane);
+    if (is_row_writer<R>(lane)) {
+      const int row = row0 + reduced_row<R>(lane);
+      if (row < row_end) {
+        const float v = acc[0] + (a.bias ? bf16_to_f32(gload(a.bias + row)) : 0.0f);
+        gstore(a.y + row, f32_to_bf16(v));
         if (ARGMAX && better(v, row, best_v, best_i)) {
           best_v = v;
           best_i = row;
@@ -299,60 +433,146 @@ __global__ __launch_bounds__(kBlock) void bf16_gemv_kernel(
       }
     }
   }
+}
 
-  if (ARGMAX) {
-    __shared__ float sv[kWavesPerBlock];
-    __shared__ int si[kWavesPerBlock];
-    wave_argmax(best_v, best_i);
-    const int wave_in_block = threadIdx.x / kWave;
-    if (lane == 0) {
-      sv[wave_in_block] = best_v;
-      si[wave_in_block] = best_i;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      float v = sv[0];
-      int i = si[0];
-      for (int w = 1; w < kWavesPerBlock; ++w) {
-        if (better(sv[w], si[w], v, i)) {
-          v = sv[w];
-          i = si[w];
-        }
+// Fold (best_v, best_i) of every lane of the block into one pair per block.
+__device__ __forceinline__ void block_argmax_store(float best_v, int best_i,
+                                                   float* __restrict__ block_value,
+                                                   int* __restrict__ block_index) {
+  __shared__ float sv[kWavesPerBlock];
+  __shared__ int si[kWavesPerBlock];
+  const int lane = threadIdx.x & (kWave - 1);
+  wave_argmax(best_v, best_i);
+  const int wave_in_block = threadIdx.x / kWave;
+  if (lane == 0) {
+    sv[wave_in_block] = best_v;
+    si[wave_in_block] = best_i;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float v = sv[0];
+    int i = si[0];
+    for (int w = 1; w < kWavesPerBlock; ++w) {
+      if (better(sv[w], si[w], v, i)) {
+        v = sv[w];
+        i = si[w];
       }
-      block_value[blockIdx.x] = v;
-      block_index[blockIdx.x] = i;
+    }
+    block_value[blockIdx.x] = v;
+    block_index[blockIdx.x] = i;
+  }
+}
+
+// A single BF16 GEMV (ARGMAX: the LM head's first stage).  Block b owns rows
+// [b RPB, (b + 1) RPB).
+template <int R, int W, bool ARGMAX>
+__global__ __launch_bounds__(kBlock, W) void bf16_gemv_kernel(
+    Bf16GemvArgs a, int rows_per_block, float* __restrict__ block_value,
+    int* __restrict__ block_index) {
+  const int begin = blockIdx.x * rows_per_block;
+  const int end = min(a.n, begin + rows_per_block);
+  const int wave = threadIdx.x / kWave;
+  float best_v = -INFINITY;
+  int best_i = INT_MAX;
+  bf16_wave_span<R, ARGMAX>(a, begin + wave * R, kWavesPerBlock * R, end, best_v, best_i);
+  if (ARGMAX) block_argmax_store(best_v, best_i, block_value, block_index);
+}
+
+// A single BF16 GEMV with rows of more than two slabs, split over K as
+// w8a16_gemv_splitk_kernel: block b owns rows [b R, b R + R), wave w takes
+// slabs w, w + 4, ..., partials summed through LDS in wave order.
+template <int R>
+__global__ __launch_bounds__(kBlock) void bf16_gemv_splitk_kernel(Bf16GemvArgs a) {
+  __shared__ float part[kWavesPerBlock][R];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int row0 = blockIdx.x * R;
+  const int chunks = a.k >> 3;
+  const int slabs = (chunks + kWave - 1) / kWave;
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+  for (int slab = wave; slab < slabs; slab += kWavesPerBlock) {
+    const int c = slab * kWave + lane;
+    const bool cv = c < chunks;
+    float x[8];
+    if (cv) {
+      load_x8(a.x + 8 * c, x);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+    }
+    uint4 w[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = row0 + r;
+      w[r] = (cv && row < a.n) ? load_stream16(a.w + static_cast<size_t>(row) * a.k + 8 * c)
+                              : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = dot8_bf16(w[r], x, acc[r]);
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) part[wave][r] = acc[r];
+  }
+  __syncthreads();
+  if (threadIdx.x < R) {
+    const int row = row0 + threadIdx.x;
+    if (row < a.n) {
+      float v = part[0][threadIdx.x];
+      for (int w = 1; w < kWavesPerBlock; ++w) v += part[w][threadIdx.x];
+      const float b = a.bias ? bf16_to_f32(gload(a.bias + row)) : 0.0f;
+      gstore(a.y + row, f32_to_bf16(v + b));
     }
   }
 }
 
-// Second argmax stage: one block folds the per-block winners.  A block whose
-// rows were all NaN reports INT_MAX; if every block does, the result is 0,
-// which is what std::max_element returns for an all-NaN range.
-__global__ __launch_bounds__(kBlock) void argmax_reduce_kernel(
+// Second argmax stage: one block of 1024 threads folds the per-block
+// winners, four independent loads in flight per thread.  A block whose rows
+// were all NaN reports INT_MAX; if every block does, the result is 0, which
+// is what std::max_element returns for an all-NaN range.
+constexpr int kReduceThreads = 1024;
+
+__global__ __launch_bounds__(kReduceThreads) void argmax_reduce_kernel(
     const float* __restrict__ block_value, const int* __restrict__ block_index,
     int count, int* __restrict__ argmax) {
   float v = -INFINITY;
   int i = INT_MAX;
-  for (int b = threadIdx.x; b < count; b += kBlock) {
-    if (better(block_value[b], block_index[b], v, i)) {
-      v = block_value[b];
-      i = block_index[b];
+  for (int b = threadIdx.x; b < count; b += 4 * kReduceThreads) {
+    float cv[4];
+    int ci[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int at = b + u * kReduceThreads;
+      cv[u] = at < count ? block_value[at] : -INFINITY;
+      ci[u] = at < count ? block_index[at] : INT_MAX;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (better(cv[u], ci[u], v, i)) {
+        v = cv[u];
+        i = ci[u];
+      }
     }
   }
-  __shared__ float sv[kWavesPerBlock];
-  __shared__ int si[kWavesPerBlock];
+  constexpr int kWaves = kReduceThreads / kWave;
+  __shared__ float sv[kWaves];
+  __shared__ int si[kWaves];
   wave_argmax(v, i);
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave_in_block = threadIdx.x / kWave;
+  const int wave = threadIdx.x / kWave;
   if (lane == 0) {
-    sv[wave_in_block] = v;
-    si[wave_in_block] = i;
+    sv[wave] = v;
+    si[wave] = i;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
     v = sv[0];
     i = si[0];
-    for (int w = 1; w < kWavesPerBlock; ++w) {
+    for (int w = 1; w < kWaves; ++w) {
       if (better(sv[w], si[w], v, i)) {
         v = sv[w];
         i = si[w];
@@ -423,85 +643,78 @@ bool aligned16(const void* p) {
   return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }
 
-int grid_for(int row_steps) {
-  const int waves = row_steps < kMaxWaves ? row_steps : kMaxWaves;
-  return (waves + kWavesPerBlock - 1) / kWavesPerBlock;
-}
-
-template <int S, int RB>
-void launch_w8(const W8GemvArgs& a, hipStream_t stream) {
-  const int steps = (a.n + RB - 1) / RB;
-  hipLaunchKernelGGL((w8a16_gemv_kernel<S, RB>), dim3(grid_for(steps)), dim3(kBlock), 0,
-                     stream, a);
-}
-
-template <int S>
-void launch_w8_rows(const W8GemvArgs& a, hipStream_t stream) {
-  // Few rows: one row per wave step spreads them over the most CUs.
-  if (S <= 2 && a.n >= 2048) {
-    launch_w8<S, 4>(a, stream);
-  } else if (S <= 4 && a.n >= 1024) {
-    launch_w8<S, 2>(a, stream);
-  } else {
-    launch_w8<S, 1>(a, stream);
-  }
-}
-
-// The argmax variant caps its grid at ceil(N / 8) blocks so that its
-// per-block scratch never exceeds the reference's LM-head workspace sizing
-// (src/qwen2.cpp:193-198); the kernels walk rows grid-stride, so any grid
-// size is correct.
+// The argmax variant keeps its grid at or below ceil(N / 8) blocks so that
+// its per-block scratch never exceeds the reference's LM-head workspace
+// sizing (src/qwen2.cpp:193-198).
 int argmax_block_cap(int n) { return (n + 7) / 8; }
 
-template <int S, int RB, bool ARGMAX>
-int launch_bf16(const Bf16GemvArgs& a, float* bv, int* bi, hipStream_t stream) {
-  const int steps = (a.n + RB - 1) / RB;
-  int blocks = grid_for(steps);
-  if (ARGMAX && blocks > argmax_block_cap(a.n)) blocks = argmax_block_cap(a.n);
-  hipLaunchKernelGGL((bf16_gemv_kernel<S, RB, ARGMAX>), dim3(blocks), dim3(kBlock), 0, stream,
-                     a, bv, bi);
-  return blocks;
+// Launch geometry of a single GEMV: R rows per wave task, RPB rows per block.
+// Small N is latency-bound, so it is spread over as many blocks as possible
+// (4 rows per block); large N streams 2-row tasks, two per wave (the LM-head
+// sweep's best: 6.76 TB/s at N = 151936).  The argmax variant needs at least
+// 8 rows per block.
+struct Geometry {
+  int r;
+  int rows_per_block;
+  int blocks;
+};
+
+Geometry single_geometry(int n, bool argmax) {
+  int r = 1, t = 1;
+  if (n >= 65536) {
+    r = 2;
+    t = 2;
+  } else if (n >= 4096 || argmax) {
+    r = 2;
+  }
+  const int rpb = kWavesPerBlock * r * t;
+  return {r, rpb, (n + rpb - 1) / rpb};
 }
 
-template <int S, bool ARGMAX>
-int launch_bf16_rows(const Bf16GemvArgs& a, float* bv, int* bi, hipStream_t stream) {
-  if (S <= 4 && a.n >= 2048) return launch_bf16<S, 4, ARGMAX>(a, bv, bi, stream);
-  if (S <= 8 && a.n >= 1024) return launch_bf16<S, 2, ARGMAX>(a, bv, bi, stream);
-  return launch_bf16<S, 1, ARGMAX>(a, bv, bi, stream);
+template <int R>
+void launch_w8(const W8GemvArgs& a, const Geometry& g, hipStream_t stream) {
+  hipLaunchKernelGGL((w8a16_gemv_kernel<R, 1, true>), dim3(g.blocks), dim3(kBlock), 0, stream,
+                     a, g.rows_per_block);
+}
+
+template <int R, bool ARGMAX>
+void launch_bf16(const Bf16GemvArgs& a, const Geometry& g, float* bv, int* bi,
+                 hipStream_t stream) {
+  hipLaunchKernelGGL((bf16_gemv_kernel<R, 6, ARGMAX>), dim3(g.blocks), dim3(kBlock), 0, stream,
+                     a, g.rows_per_block, bv, bi);
 }
 
 template <bool ARGMAX>
 int dispatch_bf16(const Bf16GemvArgs& a, float* bv, int* bi, hipStream_t stream) {
-  switch ((a.k + 511) / 512) {
-    case 1: return launch_bf16_rows<1, ARGMAX>(a, bv, bi, stream);
-    case 2: return launch_bf16_rows<2, ARGMAX>(a, bv, bi, stream);
-    case 3: return launch_bf16_rows<3, ARGMAX>(a, bv, bi, stream);
-    case 4: return launch_bf16_rows<4, ARGMAX>(a, bv, bi, stream);
-    case 5: return launch_bf16_rows<5, ARGMAX>(a, bv, bi, stream);
-    case 6: return launch_bf16_rows<6, ARGMAX>(a, bv, bi, stream);
-    case 7: return launch_bf16_rows<7, ARGMAX>(a, bv, bi, stream);
-    case 8: return launch_bf16_rows<8, ARGMAX>(a, bv, bi, stream);
-    case 9: return launch_bf16_rows<9, ARGMAX>(a, bv, bi, stream);
-    case 10: return launch_bf16_rows<10, ARGMAX>(a, bv, bi, stream);
-    case 11: return launch_bf16_rows<11, ARGMAX>(a, bv, bi, stream);
-    case 12: return launch_bf16_rows<12, ARGMAX>(a, bv, bi, stream);
-    case 13: return launch_bf16_rows<13, ARGMAX>(a, bv, bi, stream);
-    case 14: return launch_bf16_rows<14, ARGMAX>(a, bv, bi, stream);
-    case 15: return launch_bf16_rows<15, ARGMAX>(a, bv, bi, stream);
-    case 16: return launch_bf16_rows<16, ARGMAX>(a, bv, bi, stream);
-    default: return -1;
+  const int slabs = (a.k / 8 + kWave - 1) / kWave;
+  if (!ARGMAX && slabs > 2 && a.n < 65536) {
+    // Long rows, few of them: split K across the waves of a block.
+    if (a.n >= 2048) {
+      hipLaunchKernelGGL((bf16_gemv_splitk_kernel<2>), dim3((a.n + 1) / 2), dim3(kBlock), 0,
+                         stream, a);
+    } else {
+      hipLaunchKernelGGL((bf16_gemv_splitk_kernel<1>), dim3(a.n), dim3(kBlock), 0, stream, a);
+    }
+    return 0;
   }
+  const Geometry g = single_geometry(a.n, ARGMAX);
+  if (g.r == 1) {
+    launch_bf16<1, ARGMAX>(a, g, bv, bi, stream);
+  } else {
+    launch_bf16<2, ARGMAX>(a, g, bv, bi, stream);
+  }
+  return g.blocks;
 }
 
-constexpr int kMaxFastKBf16 = 512 * 16;
-constexpr int kMaxFastKW8 = 1024 * 8;
+// Slab loops take any K; the bound keeps K in int range arithmetic.
+constexpr int kMaxFastK = 1 << 20;
 
 bool bf16_fast_ok(const uint16_t* w, const uint16_t* x, int k) {
-  return k >= 8 && (k & 7) == 0 && k <= kMaxFastKBf16 && aligned16(w) && aligned16(x);
+  return k >= 8 && (k & 7) == 0 && k <= kMaxFastK && aligned16(w) && aligned16(x);
 }
 
 bool w8_fast_ok(const int8_t* w, const uint16_t* x, int k) {
-  return k >= 64 && (k & 63) == 0 && k <= kMaxFastKW8 && aligned16(w) && aligned16(x);
+  return k >= 64 && (k & 63) == 0 && k <= kMaxFastK && aligned16(w) && aligned16(x);
 }
 
 int generic_blocks(int tokens, int n) {
@@ -510,21 +723,36 @@ int generic_blocks(int tokens, int n) {
   return static_cast<int>(blocks < 65536 ? blocks : 65536);
 }
 
+// Grouped kernel: 4-row wave tasks, registers capped for >= 4 waves per
+// SIMD, no register prefetch — the best of a sweep over R in {2, 4, 8},
+// waves per SIMD in {1, 4, 6, 8}, prefetch on/off and tasks per wave on the
+// 168-GEMV decode set (6.58 TB/s against 6.80 TB/s for a bare streaming
+// read of the same 370 MB).
+constexpr int kGroupedR = 4;
+constexpr int kGroupedWaves = 4;
+constexpr bool kGroupedPrefetch = false;
+
 }  // namespace
 
 // ------------------------------------------------------ internal entries --
 
 void launch_w8a16_gemv_fast(const W8GemvArgs& a, hipStream_t stream) {
-  switch ((a.k + 1023) / 1024) {
-    case 1: launch_w8_rows<1>(a, stream); break;
-    case 2: launch_w8_rows<2>(a, stream); break;
-    case 3: launch_w8_rows<3>(a, stream); break;
-    case 4: launch_w8_rows<4>(a, stream); break;
-    case 5: launch_w8_rows<5>(a, stream); break;
-    case 6: launch_w8_rows<6>(a, stream); break;
-    case 7: launch_w8_rows<7>(a, stream); break;
-    case 8: launch_w8_rows<8>(a, stream); break;
-    default: break;
+  const int slabs = (a.k / 16 + kWave - 1) / kWave;
+  if (slabs > 1 && a.n < 65536) {
+    // Long rows, few of them: split K across the waves of a block.
+    if (a.n >= 2048) {
+      hipLaunchKernelGGL((w8a16_gemv_splitk_kernel<2>), dim3((a.n + 1) / 2), dim3(kBlock), 0,
+                         stream, a);
+    } else {
+      hipLaunchKernelGGL((w8a16_gemv_splitk_kernel<1>), dim3(a.n), dim3(kBlock), 0, stream, a);
+    }
+    return;
+  }
+  const Geometry g = single_geometry(a.n, false);
+  if (g.r == 1) {
+    launch_w8<1>(a, g, stream);
+  } else {
+    launch_w8<2>(a, g, stream);
   }
 }
 
@@ -532,38 +760,17 @@ bool w8a16_gemv_fast_supported(const int8_t* w, const uint16_t* x, int k) {
   return w8_fast_ok(w, x, k);
 }
 
-int w8a16_slot_class(int k) { return (k + 1023) / 1024; }
-
-// Rows per block of the grouped kernel for each slot class: 2 row steps per
-// wave, RB = 4 / 2 / 1 rows per step for S = 1 / 2 / >= 3.
-namespace {
-constexpr int kGroupedSteps = 2;
-constexpr int grouped_rb(int s) { return s == 1 ? 4 : (s == 2 ? 2 : 1); }
-
-template <int S>
-void launch_grouped(const W8GroupDesc* descs, int count, int blocks, hipStream_t stream) {
-  hipLaunchKernelGGL((w8a16_gemv_grouped_kernel<S, grouped_rb(S), kGroupedSteps>), dim3(blocks),
-                     dim3(kBlock), 0, stream, descs, count);
-}
-}  // namespace
-
-int w8a16_grouped_rows_per_block(int slot_class) {
-  return kWavesPerBlock * grouped_rb(slot_class) * kGroupedSteps;
+int w8a16_grouped_rows_per_block(int k) {
+  // Four tasks per wave for K <= 1024 (one slab), two for longer rows.
+  const int slabs = (k / 16 + kWave - 1) / kWave;
+  return kWavesPerBlock * kGroupedR * (slabs == 1 ? 4 : 2);
 }
 
-void launch_w8a16_gemv_grouped(int slot_class, const W8GroupDesc* descs, int count,
-                               int total_blocks, hipStream_t stream) {
-  switch (slot_class) {
-    case 1: launch_grouped<1>(descs, count, total_blocks, stream); break;
-    case 2: launch_grouped<2>(descs, count, total_blocks, stream); break;
-    case 3: launch_grouped<3>(descs, count, total_blocks, stream); break;
-    case 4: launch_grouped<4>(descs, count, total_blocks, stream); break;
-    case 5: launch_grouped<5>(descs, count, total_blocks, stream); break;
-    case 6: launch_grouped<6>(descs, count, total_blocks, stream); break;
-    case 7: launch_grouped<7>(descs, count, total_blocks, stream); break;
-    case 8: launch_grouped<8>(descs, count, total_blocks, stream); break;
-    default: break;
-  }
+void launch_w8a16_gemv_grouped(const W8GroupDesc* descs, int count, int total_blocks,
+                               hipStream_t stream) {
+  hipLaunchKernelGGL((w8a16_gemv_grouped_kernel<kGroupedR, kGroupedWaves, kGroupedPrefetch>),
+                     dim3(total_blocks), dim3(kBlock),
+                     0, stream, descs, count);
 }
 
 void launch_w8a16_linear_generic(const int8_t* w, const uint16_t* s, int group_size,
@@ -589,16 +796,9 @@ void launch_bf16_gemv_fast(const Bf16GemvArgs& a, hipStream_t stream) {
 
 // Blocks the LM head's first stage uses (its workspace entry count).
 size_t lm_head_blocks(int vocab, int in_features, bool fast) {
-  if (vocab <= 0 || in_features <= 0) return 0;
+  if (vocab <= 0 || in_features < 0) return 0;
+  int blocks = fast ? single_geometry(vocab, true).blocks : generic_blocks(1, vocab);
   const int cap = argmax_block_cap(vocab);
-  int blocks;
-  if (!fast) {
-    blocks = generic_blocks(1, vocab);
-  } else {
-    const int s = (in_features + 511) / 512;
-    const int rb = (s <= 4 && vocab >= 2048) ? 4 : ((s <= 8 && vocab >= 1024) ? 2 : 1);
-    blocks = grid_for((vocab + rb - 1) / rb);
-  }
   return static_cast<size_t>(blocks < cap ? blocks : cap);
 }
 
@@ -684,7 +884,7 @@ extern "C" int infer_hip_lm_head_bf16(const uint16_t* weight, const uint16_t* bi
   }
   int rc = check_launch("lm_head_bf16");
   if (rc != INFER_HIP_OK) return rc;
-  hipLaunchKernelGGL(argmax_reduce_kernel, dim3(1), dim3(kBlock), 0, stream, block_max_value,
-                     block_max_index, blocks, argmax);
+  hipLaunchKernelGGL(argmax_reduce_kernel, dim3(1), dim3(kReduceThreads), 0, stream,
+                     block_max_value, block_max_index, blocks, argmax);
   return check_launch("lm_head_bf16 argmax");
 }

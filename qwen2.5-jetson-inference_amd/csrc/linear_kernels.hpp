@@ -18,7 +18,8 @@ struct W8GemvArgs {
 };
 
 // One GEMV of a grouped launch; block_begin is the first block index of the
-// launch that works on it (descriptors sorted by block_begin).
+// launch that works on it (descriptors sorted by block_begin) and each of its
+// blocks covers rows_per_block rows (a multiple of 4 waves x 8-row tasks).
 struct W8GroupDesc {
   const int8_t* w;
   const uint16_t* s;
@@ -28,7 +29,7 @@ struct W8GroupDesc {
   int n;
   int k;
   int block_begin;
-  int pad;
+  int rows_per_block;
 };
 
 struct Bf16GemvArgs {
@@ -52,11 +53,10 @@ void launch_bf16_linear_generic(const uint16_t* w, const uint16_t* bias, const u
                                 uint16_t* y, int tokens, int n, int k, hipStream_t stream);
 size_t lm_head_blocks(int vocab, int in_features, bool fast);
 
-// Grouped W8A16 GEMV: the slot class S = ceil(K / 1024) of a descriptor,
-// the rows one block of class S covers, and the launch of one class's table.
-int w8a16_slot_class(int k);
-int w8a16_grouped_rows_per_block(int slot_class);
-void launch_w8a16_gemv_grouped(int slot_class, const W8GroupDesc* device_descs, int count,
-                               int total_blocks, hipStream_t stream);
+// Grouped W8A16 GEMV: rows per block for a descriptor of in_features k, and
+// the launch of a descriptor table (any mix of K) resident on the device.
+int w8a16_grouped_rows_per_block(int k);
+void launch_w8a16_gemv_grouped(const W8GroupDesc* device_descs, int count, int total_blocks,
+                               hipStream_t stream);
 
 }  // namespace qlin

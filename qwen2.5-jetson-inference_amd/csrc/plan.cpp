@@ -22,23 +22,12 @@
 using namespace qlin;
 
 struct infer_hip_gemv_plan {
-  struct Launch {
-    int slot_class;
-    int count;        // descriptors in this class
-    int blocks;       // total blocks of the launch
-    size_t offset;    // first descriptor of the class in `table`
-  };
   W8GroupDesc* table = nullptr;  // device memory
-  std::vector<Launch> launches;
+  int count = 0;
+  int blocks = 0;
   int device = 0;
   double bytes = 0.0;
 };
-
-namespace {
-
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
-}  // namespace
 
 extern "C" int infer_hip_w8a16_gemv_plan_create(const infer_hip_w8a16_gemv_desc* descs,
                                                 int count, infer_hip_gemv_plan** plan_out) {
@@ -47,7 +36,8 @@ extern "C" int infer_hip_w8a16_gemv_plan_create(const infer_hip_w8a16_gemv_desc*
   if (!descs || count <= 0) {
     return fail(INFER_HIP_INVALID_ARGUMENT, "gemv plan: need at least one descriptor");
   }
-  std::vector<std::vector<W8GroupDesc>> by_class(9);
+  std::vector<W8GroupDesc> table;
+  table.reserve(count);
   double bytes = 0.0;
   for (int i = 0; i < count; ++i) {
     const infer_hip_w8a16_gemv_desc& d = descs[i];
@@ -64,33 +54,30 @@ extern "C" int infer_hip_w8a16_gemv_plan_create(const infer_hip_w8a16_gemv_desc*
     }
     if (!w8a16_gemv_fast_supported(d.weight, d.input, d.in_features)) {
       return fail(INFER_HIP_INVALID_ARGUMENT,
-                  "gemv plan: descriptor %d needs K %% 64 == 0, K <= 8192 and 16-byte aligned "
-                  "weight and input (K=%d)",
+                  "gemv plan: descriptor %d needs K %% 64 == 0 and 16-byte aligned weight and "
+                  "input (K=%d)",
                   i, d.in_features);
     }
-    const int s = w8a16_slot_class(d.in_features);
-    by_class[s].push_back(W8GroupDesc{d.weight, d.scales, d.bias, d.input, d.output,
-                                      d.out_features, d.in_features, 0, 0});
+    table.push_back(W8GroupDesc{d.weight, d.scales, d.bias, d.input, d.output, d.out_features,
+                                d.in_features, 0, w8a16_grouped_rows_per_block(d.in_features)});
     bytes += static_cast<double>(d.out_features) * d.in_features +
              2.0 * d.out_features * (d.in_features / 64) + 2.0 * d.in_features +
              2.0 * d.out_features + (d.bias ? 2.0 * d.out_features : 0.0);
   }
+  // Longest rows first: the blocks that take longest start earliest, which
+  // shortens the launch's tail.
+  std::stable_sort(table.begin(), table.end(),
+                   [](const W8GroupDesc& a, const W8GroupDesc& b) { return a.k > b.k; });
+  long long blocks = 0;
+  for (W8GroupDesc& d : table) {
+    d.block_begin = static_cast<int>(blocks);
+    blocks += (d.n + d.rows_per_block - 1) / d.rows_per_block;
+  }
+  if (blocks > 0x7FFFFFFF) return fail(INFER_HIP_INVALID_ARGUMENT, "gemv plan: too many rows");
   auto* plan = new (std::nothrow) infer_hip_gemv_plan();
   if (!plan) return fail(INFER_HIP_RUNTIME_ERROR, "gemv plan: out of host memory");
-  std::vector<W8GroupDesc> table;
-  table.reserve(count);
-  for (int s = 1; s <= 8; ++s) {
-    if (by_class[s].empty()) continue;
-    const int rpb = w8a16_grouped_rows_per_block(s);
-    int blocks = 0;
-    const size_t offset = table.size();
-    for (W8GroupDesc& d : by_class[s]) {
-      d.block_begin = blocks;
-      blocks += (d.n + rpb - 1) / rpb;
-      table.push_back(d);
-    }
-    plan->launches.push_back({s, static_cast<int>(by_class[s].size()), blocks, offset});
-  }
+  plan->count = count;
+  plan->blocks = static_cast<int>(blocks);
   plan->bytes = bytes;
   hipError_t st = hipGetDevice(&plan->device);
   if (st == hipSuccess) st = hipMalloc(&plan->table, table.size() * sizeof(W8GroupDesc));
@@ -110,12 +97,8 @@ extern "C" int infer_hip_w8a16_gemv_plan_create(const infer_hip_w8a16_gemv_desc*
 extern "C" int infer_hip_w8a16_gemv_plan_launch(const infer_hip_gemv_plan* plan,
                                                 hipStream_t stream) {
   if (!plan) return fail(INFER_HIP_INVALID_ARGUMENT, "gemv plan: null plan");
-  for (const auto& l : plan->launches) {
-    launch_w8a16_gemv_grouped(l.slot_class, plan->table + l.offset, l.count, l.blocks, stream);
-    const int rc = check_launch("w8a16 gemv plan");
-    if (rc != INFER_HIP_OK) return rc;
-  }
-  return ok();
+  launch_w8a16_gemv_grouped(plan->table, plan->count, plan->blocks, stream);
+  return check_launch("w8a16 gemv plan");
 }
 
 extern "C" double infer_hip_w8a16_gemv_plan_bytes(const infer_hip_gemv_plan* plan) {

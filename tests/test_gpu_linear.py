@@ -240,3 +240,29 @@ def test_w8a16_plan_rejects_unsupported_descriptors(hip, dev):
         hip.W8A16GemvPlan([(q, s, 64, None, x, y, 4, 70)])
     with pytest.raises(hip.InferError):
         hip.W8A16GemvPlan([(q, s, 32, None, x, y, 4, 64)])
+
+
+@pytest.mark.parametrize("n,k", [(70000, 896), (3000, 4864), (513, 3072)])
+def test_w8a16_gemv_large_and_split_k_paths(hip, orc, dev, n, k):
+    # N >= 65536 takes 2-row tasks two per wave; K > 1024 with fewer rows
+    # takes the split-K kernel (R = 2 when N >= 2048).
+    rng = rc.philox(50 + n)
+    q, s = rc.w8a16_synthetic(rng, n, k)
+    x = rc.bf16_normal(rng, (k,))
+    b = rc.bf16_normal(rng, (n,))
+    exp32, _ = orc.w8a16_reference(q, s, 64, b, x)
+    y = bf16_out((n,), dev)
+    hip.gemv_w8a16(to_dev(q, dev), to_dev(s, dev), 64, to_dev(b, dev), to_dev(x, dev), y, n, k)
+    check_close(words(y), exp32[0], what=f"gemv_w8a16 {n}x{k}")
+
+
+@pytest.mark.parametrize("n,k", [(70000, 896), (3000, 4864), (513, 3072)])
+def test_bf16_gemv_large_and_split_k_paths(hip, orc, dev, n, k):
+    rng = rc.philox(60 + n)
+    w = rc.bf16_normal(rng, (n, k), 0.02)
+    x = rc.bf16_normal(rng, (k,))
+    b = rc.bf16_normal(rng, (n,))
+    exp = orc.linear_fp32(rc.bf16_values(w), rc.bf16_values(b), rc.bf16_values(x))
+    y = bf16_out((n,), dev)
+    hip.gemv_bf16(to_dev(w, dev), to_dev(b, dev), to_dev(x, dev), y, n, k)
+    check_close(words(y), exp, what=f"gemv_bf16 {n}x{k}")
