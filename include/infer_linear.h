@@ -108,6 +108,27 @@ int infer_hip_gemm_w8a16(const int8_t* weight, const uint16_t* scales,
                          const uint16_t* input, uint16_t* output, int tokens,
                          int out_features, int in_features, hipStream_t stream);
 
+/* ---- Explicit MFMA tile selection --------------------------------------
+ * No reference counterpart (the reference picks its WMMA tile from M and N
+ * divisibility, src/cuda/kernels.cu:1606-1622, 1665-1681).  The same
+ * computation as infer_hip_gemm_w8a16 / infer_hip_gemm_bf16 with the
+ * workgroup tile of the MFMA kernel named by the caller: tile in
+ * [0, infer_hip_gemm_tile_count()) (0 = 128x128, 1 = 128x64, 2 = 64x128,
+ * 3 = 64x64, 4 = 32x128 rows x columns of Y), or -1 for the automatic
+ * choice the plain entry points make.  For tuning sweeps and for tests
+ * that cover every tile.  Shapes outside the MFMA path (tokens == 1,
+ * in_features % 64 != 0, unaligned weight or input) ignore tile. */
+int infer_hip_gemm_tile_count(void);
+int infer_hip_gemm_w8a16_tile(const int8_t* weight, const uint16_t* scales,
+                              int group_size, const uint16_t* bias,
+                              const uint16_t* input, uint16_t* output, int tokens,
+                              int out_features, int in_features, int tile,
+                              hipStream_t stream);
+int infer_hip_gemm_bf16_tile(const uint16_t* weight, const uint16_t* bias,
+                             const uint16_t* input, uint16_t* output, int tokens,
+                             int out_features, int in_features, int tile,
+                             hipStream_t stream);
+
 /* ---- Grouped W8A16 GEMV plans ------------------------------------------
  * No single reference counterpart: a plan is the multi-matrix form of
  * infer_hip_gemv_w8a16 for GEMVs that are independent of each other, such

@@ -1,15 +1,400 @@
-// Prefill (M = tokens > 1) Linear entry points.
+// Prefill (M = tokens > 1) Linear kernels for gfx950: W8A16 group-64 dequant
+// GEMM and BF16 GEMM on CDNA4 MFMA (v_mfma_f32_32x32x16_bf16).
+//
+// Both compute Y[m, n] = bf16(sum_k X[m, k] W[n, k] + bias[n]) with X
+// [M, K] and W [N, K] row-major, K contiguous: the layout MFMA wants for
+// both operands, so no operand is transposed anywhere.
+//
+// Mapping.  A workgroup of 4 waves owns a BM x BN output tile and walks K
+// in stages of 64 columns — one W8A16 quantisation group.  Each stage is
+// staged in LDS as BF16 (X rows and W rows, 128 bytes each), double
+// buffered: the global loads of stage g + 1 are in flight while the MFMAs
+// of stage g run, then written to the other buffer, one barrier per stage.
+// Each wave owns a TM x TN sub-tile = FM x FN MFMA tiles of 32 x 32.
+//
+// W8A16.  The int8 weights are converted to BF16 while filling LDS (exact:
+// |q| <= 127 needs 7 significand bits, BF16 has 8), once per workgroup and
+// shared by every wave that uses those columns.  The MFMAs of a stage sum
+// q * x into a per-stage FP32 partial; the group scale s[n, g] is applied to
+// that partial once (acc = fma(partial, s, acc)).  So the product uses the
+// exact dequantised weight q * s, as the GEMV and the CPU FP32 path do;
+// the reference instead rounds q * s to BF16 before its WMMA
+// (src/cuda/kernels.cu:1091).  In the 32 x 32 accumulator layout every
+// value a lane holds is in one output column, so a lane needs one scale per
+// MFMA tile column per stage.
+//
+// LDS layout.  A staged row is eight 16-byte chunks (8 BF16 each).  Chunk c
+// of row r is stored at slot c ^ (r & 7): the 8 rows a group of lanes reads
+// at one chunk index land in 8 different slots, i.e. all 32 banks.
+//
+// Reference behaviour restated (src/cuda/kernels.cu): gemm_w8a16 launcher
+// 1657-1684 and its WMMA kernels 1096-1322; gemm_bf16 launcher 1600-1625 and
+// kernels 605-951.  Shapes the MFMA path does not take (K % 64 != 0,
+// unaligned pointers) go to the exact generic kernels, as the reference's
+// dispatch sends them to linear_w8a16_kernel (1324-1387).
 #include <stdint.h>
 
+#include "device_common.hpp"
 #include "linear_kernels.hpp"
 #include "status.hpp"
 
+namespace qlin {
+
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr int kThreads = 256;  // 4 waves
+constexpr int kStageK = 64;    // K columns per stage = one quantisation group
+constexpr int kRowChunks = 8;  // 16-byte BF16 chunks per staged row
+#ifndef QLIN_GEMM_PREFETCH
+#define QLIN_GEMM_PREFETCH 2
+#endif
+constexpr int kPrefetch = QLIN_GEMM_PREFETCH;  // stages of loads in flight
+#ifndef QLIN_GEMM_WAVES_ATTR
+#define QLIN_GEMM_WAVES_ATTR
+#endif
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(const uint4 v) {
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+// A raw buffer resource over [base, base + bytes): loads past the end
+// return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes),
+                                           0x00020000);
+}
+
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t voffset,
+                                               uint32_t soffset) {
+  return __builtin_bit_cast(uint4,
+                            __builtin_amdgcn_raw_buffer_load_b128(r, voffset, soffset, 0));
+}
+
+#ifndef QLIN_LDS_SWIZZLE
+#define QLIN_LDS_SWIZZLE 1
+#endif
+__device__ __forceinline__ int lds_slot(int row, int chunk) {
+#if QLIN_LDS_SWIZZLE == 1
+  return row * kRowChunks + (chunk ^ ((row >> 1) & 7));
+#else
+  return row * kRowChunks + (chunk ^ (row & 7));
+#endif
+}
+
+// Two small integers held exactly as FP32 -> a BF16 pair (lo in bits
+// 0-15): the high halves of both words, one byte permute.
+__device__ __forceinline__ uint32_t pack_hi_halves(float lo, float hi) {
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+// 16 int8 -> 16 BF16 (two 16-byte chunks), exact: |q| <= 127 needs 7
+// significand bits, BF16 has 8.
+__device__ __forceinline__ void i8x16_to_bf16(const uint4 q, uint4& lo, uint4& hi) {
+  lo.x = pack_hi_halves(sbyte0(q.x), sbyte1(q.x));
+  lo.y = pack_hi_halves(sbyte2(q.x), sbyte3(q.x));
+  lo.z = pack_hi_halves(sbyte0(q.y), sbyte1(q.y));
+  lo.w = pack_hi_halves(sbyte2(q.y), sbyte3(q.y));
+  hi.x = pack_hi_halves(sbyte0(q.z), sbyte1(q.z));
+  hi.y = pack_hi_halves(sbyte2(q.z), sbyte3(q.z));
+  hi.z = pack_hi_halves(sbyte0(q.w), sbyte1(q.w));
+  hi.w = pack_hi_halves(sbyte2(q.w), sbyte3(q.w));
+}
+
+template <int BM, int BN, int WAVES_M, bool W8>
+struct TileShape {
+  static constexpr int kWavesN = 4 / WAVES_M;
+  static constexpr int TM = BM / WAVES_M;
+  static constexpr int TN = BN / kWavesN;
+  static constexpr int FM = TM / 32;
+  static constexpr int FN = TN / 32;
+  // Global 16-byte loads per thread per stage.
+  static constexpr int A_LOADS = BM * kRowChunks / kThreads;
+  static constexpr int B_LOADS = W8 ? BN * (kStageK / 16) / kThreads : BN * kRowChunks / kThreads;
+  static_assert(WAVES_M == 1 || WAVES_M == 2 || WAVES_M == 4, "4 waves per workgroup");
+  static_assert(FM >= 1 && FN >= 1 && TM % 32 == 0 && TN % 32 == 0, "32 x 32 MFMA tiles");
+  static_assert(A_LOADS >= 1 && B_LOADS >= 1, "every thread loads at least one chunk");
+};
+
+// One workgroup's BM x BN tile of Y at (m0, n0) over all of K (a multiple
+// of 64).  The epilogue adds the bias and writes BF16.
+//
+// Pipeline: the global loads of stage g + D are issued as soon as stage g
+// has been written to LDS, so D stages of loads are in flight while the
+// MFMAs run; a register slot per stage in flight (the loop is unrolled by
+// D so every slot index is a constant).  LDS is double buffered: stage g
+// is written to buffer g & 1, one barrier, then its MFMAs.  A wave that
+// writes stage g + 1 into the other buffer has passed the barrier of stage
+// g, which every wave reaches only after its MFMAs of stage g - 1, the
+// last reader of that buffer.
+template <int BM, int BN, int WAVES_M, bool W8, int D>
+__device__ __forceinline__ void gemm_tile(const GemmArgs& a, int m0, int n0) {
+  using S = TileShape<BM, BN, WAVES_M, W8>;
+  constexpr int FM = S::FM, FN = S::FN;
+  __shared__ uint4 lds_a[2][BM * kRowChunks];
+  __shared__ uint4 lds_b[2][BN * kRowChunks];
+  __shared__ float lds_s[2][W8 ? BN : 1];  // W8: group scales of the stage's rows
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave % WAVES_M;
+  const int wn = wave / WAVES_M;
+  const int r = lane & 31;   // row of an A fragment / column of a B fragment
+  const int h = lane >> 5;   // which half of the 64 staged columns' chunks
+  const int stages = a.k / kStageK;
+  const int groups = a.k / kStageK;  // scale row stride
+
+  // ---- global -> register staging, one slot per stage in flight ----
+  // Buffer loads: a row past M or N is out of the resource's range and
+  // reads as zero, so the loads need no branches (the host checks that
+  // every operand fits a 32-bit byte offset).  Each thread's byte offsets
+  // are fixed; the stage's column offset is a scalar (soffset), clamped to
+  // the last stage so that loads issued past it stay inside the tensor.
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, static_cast<uint32_t>(a.m) * a.k * 2u);
+  const __amdgpu_buffer_rsrc_t wr =
+      make_rsrc(a.w, static_cast<uint32_t>(a.n) * a.k * (W8 ? 1u : 2u));
+  uint32_t xoff[S::A_LOADS], woff[S::B_LOADS];
+#pragma unroll
+  for (int i = 0; i < S::A_LOADS; ++i) {
+    const int c = tid + kThreads * i;
+    xoff[i] = ((static_cast<uint32_t>(m0) + (c >> 3)) * a.k + (c & 7) * 8) * 2u;
+  }
+#pragma unroll
+  for (int i = 0; i < S::B_LOADS; ++i) {
+    const int c = tid + kThreads * i;
+    woff[i] = W8 ? (static_cast<uint32_t>(n0) + (c >> 2)) * a.k + (c & 3) * 16
+                 : ((static_cast<uint32_t>(n0) + (c >> 3)) * a.k + (c & 7) * 8) * 2u;
+  }
+  // W8: the scales of row n0 + tid % BN (clamped into the tensor; rows past
+  // N are never used) for every stage.
+  const uint16_t* srow = W8 ? a.s + static_cast<size_t>(min(n0 + tid % BN, a.n - 1)) * groups
+                            : nullptr;
+  uint4 ra[D][S::A_LOADS];
+  uint4 rb[D][S::B_LOADS];
+  uint32_t rs[D];  // W8: the group scale of row n0 + tid % BN of the stage
+
+  auto load_stage = [&](int g, uint4 (&xa)[S::A_LOADS], uint4 (&xb)[S::B_LOADS],
+                        uint32_t& xs) {
+    const uint32_t gc = static_cast<uint32_t>(min(g, stages - 1));
+    const uint32_t kbyte = gc * kStageK * 2u;
+#pragma unroll
+    for (int i = 0; i < S::A_LOADS; ++i) xa[i] = buffer_load16(xr, xoff[i], kbyte);
+#pragma unroll
+    for (int i = 0; i < S::B_LOADS; ++i)
+      xb[i] = buffer_load16(wr, woff[i], W8 ? gc * kStageK : kbyte);
+    // A 16-bit global load zero-extends in the load itself.
+    if (W8) xs = gload(srow + gc);
+  };
+
+  auto store_stage = [&](int buf, const uint4 (&xa)[S::A_LOADS],
+                         const uint4 (&xb)[S::B_LOADS], uint32_t xs) {
+    if (W8 && tid < BN) lds_s[buf][tid] = bf16_to_f32(xs);
+#pragma unroll
+    for (int i = 0; i < S::A_LOADS; ++i) {
+      const int c = tid + kThreads * i;
+      lds_a[buf][lds_slot(c >> 3, c & 7)] = xa[i];
+    }
+#pragma unroll
+    for (int i = 0; i < S::B_LOADS; ++i) {
+      const int c = tid + kThreads * i;
+      if (W8) {
+        const int row = c >> 2, col = c & 3;
+        uint4 lo, hi;
+        i8x16_to_bf16(xb[i], lo, hi);
+        lds_b[buf][lds_slot(row, 2 * col)] = lo;
+        lds_b[buf][lds_slot(row, 2 * col + 1)] = hi;
+      } else {
+        lds_b[buf][lds_slot(c >> 3, c & 7)] = xb[i];
+      }
+    }
+  };
+
+  f32x16_t acc[FM][FN];
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[fm][fn][e] = 0.0f;
+
+  // Stage g's MFMAs on LDS buffer buf.  Lane (r, h) multiplies k-chunks
+  // 4h .. 4h + 3 of the stage, one per MFMA k-step; A and B fragments use
+  // the same chunk, so their k slots agree.
+  auto compute_stage = [&](int buf) {
+    // All fragments of the stage are read first (distinct registers), so
+    // the LDS latency is paid once per stage instead of once per k-step.
+    bf16x8_t fa[4][FM], fb[4][FN];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int chunk = 4 * h + ks;
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+        fa[ks][fm] = as_bf16x8(lds_a[buf][lds_slot(wm * S::TM + fm * 32 + r, chunk)]);
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+        fb[ks][fn] = as_bf16x8(lds_b[buf][lds_slot(wn * S::TN + fn * 32 + r, chunk)]);
+    }
+    float sc[FN];
+    if (W8) {
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) sc[fn] = lds_s[buf][wn * S::TN + fn * 32 + r];
+    }
+    f32x16_t part[FM][FN];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+          if (W8) {
+            const f32x16_t zero = {};
+            part[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                fa[ks][fm], fb[ks][fn], ks == 0 ? zero : part[fm][fn], 0, 0, 0);
+          } else {
+            acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ks][fm], fb[ks][fn],
+                                                                  acc[fm][fn], 0, 0, 0);
+          }
+        }
+      }
+    }
+    if (W8) {
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            acc[fm][fn][e] = fmaf(part[fm][fn][e], sc[fn], acc[fm][fn][e]);
+      }
+    }
+  };
+
+  // Stage g lives in register slot g % D and LDS buffer g & 1.  Iteration
+  // g runs the MFMAs of stage g and, in the same instruction stream, writes
+  // stage g + 1 into the other LDS buffer and issues the loads of stage
+  // g + 1 + D; one barrier ends the iteration.  The other buffer's last
+  // reader was stage g - 1, finished by every wave before the previous
+  // barrier.  With D even, full rounds of D stages have compile-time
+  // buffer indices, so the compiler sees the writes and the MFMA reads
+  // touch different LDS arrays and can interleave them.  Loads past the
+  // last stage (issued by the last full round) read in-range neighbouring
+  // bytes or zeros and are never stored.
+  static_assert(D % 2 == 0, "full rounds keep the LDS buffer parity");
+#pragma unroll
+  for (int j = 0; j < D; ++j) load_stage(j, ra[j], rb[j], rs[j]);
+  store_stage(0, ra[0], rb[0], rs[0]);
+  load_stage(D, ra[0], rb[0], rs[0]);
+  __syncthreads();
+
+  int g0 = 0;
+  for (; g0 + D < stages; g0 += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      const int g = g0 + j;
+      compute_stage(j & 1);
+      const int jn = (j + 1) % D;
+      store_stage((j + 1) & 1, ra[jn], rb[jn], rs[jn]);
+      load_stage(g + 1 + D, ra[jn], rb[jn], rs[jn]);
+      __syncthreads();
+    }
+  }
+  // The last 1..D stages: stage g0 is in LDS buffer 0, later ones in
+  // register slots 1.. (no further loads).
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    const int g = g0 + j;
+    if (g < stages) {
+      compute_stage(j & 1);
+      if (g + 1 < stages) store_stage((j + 1) & 1, ra[(j + 1) % D], rb[(j + 1) % D], rs[(j + 1) % D]);
+      __syncthreads();
+    }
+  }
+
+  // ---- epilogue: accumulator element e of a 32 x 32 tile is at row
+  // 8 (e / 4) + 4 h + e % 4, column r ----
+#pragma unroll
+  for (int fn = 0; fn < FN; ++fn) {
+    const int n = n0 + wn * S::TN + fn * 32 + r;
+    if (n >= a.n) continue;
+    const float b = a.bias ? bf16_to_f32(gload(a.bias + n)) : 0.0f;
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = m0 + wm * S::TM + fm * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+        if (m < a.m) gstore(a.y + static_cast<size_t>(m) * a.n + n, f32_to_bf16(acc[fm][fn][e] + b));
+      }
+    }
+  }
+}
+
+// Grid: x = N tiles, y = M tiles.
+template <int BM, int BN, int WAVES_M, bool W8>
+__global__ __launch_bounds__(kThreads) QLIN_GEMM_WAVES_ATTR void gemm_mfma_kernel(GemmArgs a) {
+  gemm_tile<BM, BN, WAVES_M, W8, kPrefetch>(a, blockIdx.y * BM, blockIdx.x * BN);
+}
+
+template <int BM, int BN, int WAVES_M, bool W8>
+void launch_tile(const GemmArgs& a, hipStream_t stream) {
+  const dim3 grid((a.n + BN - 1) / BN, (a.m + BM - 1) / BM);
+  hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, WAVES_M, W8>), grid, dim3(kThreads), 0, stream,
+                     a);
+}
+
+template <bool W8>
+void launch_config(int config, const GemmArgs& a, hipStream_t stream) {
+  switch (config) {
+    case kGemmTile128x128: launch_tile<128, 128, 2, W8>(a, stream); break;
+    case kGemmTile128x64: launch_tile<128, 64, 2, W8>(a, stream); break;
+    case kGemmTile64x128: launch_tile<64, 128, 2, W8>(a, stream); break;
+    case kGemmTile64x64: launch_tile<64, 64, 2, W8>(a, stream); break;
+    case kGemmTile32x128: launch_tile<32, 128, 1, W8>(a, stream); break;
+    default: launch_tile<64, 64, 2, W8>(a, stream); break;
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+bool gemm_mfma_supported(const void* w, const uint16_t* x, int m, int n, int k) {
+  // Buffer loads address each operand with a 32-bit byte offset.
+  const long long limit = 0x7FFFFFFFll;
+  return k >= kStageK && k % kStageK == 0 && aligned16(w) && aligned16(x) &&
+         2ll * m * k < limit && 2ll * n * k < limit;
+}
+
+int gemm_pick_tile(int m, int n) {
+  // A stage's time grows with the tile's LDS traffic, and at the Qwen
+  // shapes no grid fills the 256 CUs twice over, so the 64 x 64 tile (the
+  // most workgroups, up to 4 per CU) is fastest for every M <= 512 measured;
+  // grids of over 2048 such tiles switch to 128 x 128.
+  const long long t64 = static_cast<long long>((m + 63) / 64) * ((n + 63) / 64);
+  return t64 > 2048 ? kGemmTile128x128 : kGemmTile64x64;
+}
+
+void launch_gemm_mfma(int tile, bool w8, const GemmArgs& a, hipStream_t stream) {
+  if (w8) {
+    launch_config<true>(tile, a, stream);
+  } else {
+    launch_config<false>(tile, a, stream);
+  }
+}
+
+}  // namespace qlin
+
+// ================================================================ C ABI ==
+
 using namespace qlin;
 
-extern "C" int infer_hip_gemm_w8a16(const int8_t* weight, const uint16_t* scales,
-                                    int group_size, const uint16_t* bias,
-                                    const uint16_t* input, uint16_t* output, int tokens,
-                                    int out_features, int in_features, hipStream_t stream) {
+namespace {
+
+int gemm_w8a16_impl(const int8_t* weight, const uint16_t* scales, int group_size,
+                    const uint16_t* bias, const uint16_t* input, uint16_t* output, int tokens,
+                    int out_features, int in_features, int tile, hipStream_t stream) {
   // kernels.cu:1661 — the only supported group size.
   if (group_size != 64) {
     return fail(INFER_HIP_INVALID_ARGUMENT, "w8a16 group size must be 64 (got %d)", group_size);
@@ -18,12 +403,18 @@ extern "C" int infer_hip_gemm_w8a16(const int8_t* weight, const uint16_t* scales
     return fail(INFER_HIP_INVALID_ARGUMENT, "gemm_w8a16: bad shape M=%d N=%d K=%d", tokens,
                 out_features, in_features);
   }
+  if (tile < -1 || tile >= kGemmTileCount) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "gemm_w8a16: no tile %d", tile);
+  }
   if (!output || (in_features > 0 && (!weight || !scales || !input))) {
     return fail(INFER_HIP_INVALID_ARGUMENT, "gemm_w8a16: null required pointer");
   }
   if (tokens == 1 && w8a16_gemv_fast_supported(weight, input, in_features)) {
     launch_w8a16_gemv_fast({weight, scales, bias, input, output, out_features, in_features},
                            stream);
+  } else if (tokens > 1 && gemm_mfma_supported(weight, input, tokens, out_features, in_features)) {
+    const GemmArgs a{weight, scales, bias, input, output, tokens, out_features, in_features};
+    launch_gemm_mfma(tile < 0 ? gemm_pick_tile(tokens, out_features) : tile, true, a, stream);
   } else {
     launch_w8a16_linear_generic(weight, scales, group_size, bias, input, output, tokens,
                                 out_features, in_features, stream);
@@ -31,21 +422,63 @@ extern "C" int infer_hip_gemm_w8a16(const int8_t* weight, const uint16_t* scales
   return check_launch("gemm_w8a16");
 }
 
-extern "C" int infer_hip_gemm_bf16(const uint16_t* weight, const uint16_t* bias,
-                                   const uint16_t* input, uint16_t* output, int tokens,
-                                   int out_features, int in_features, hipStream_t stream) {
+int gemm_bf16_impl(const uint16_t* weight, const uint16_t* bias, const uint16_t* input,
+                   uint16_t* output, int tokens, int out_features, int in_features, int tile,
+                   hipStream_t stream) {
   if (tokens <= 0 || out_features <= 0 || in_features < 0) {
     return fail(INFER_HIP_INVALID_ARGUMENT, "gemm_bf16: bad shape M=%d N=%d K=%d", tokens,
                 out_features, in_features);
+  }
+  if (tile < -1 || tile >= kGemmTileCount) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "gemm_bf16: no tile %d", tile);
   }
   if (!output || (in_features > 0 && (!weight || !input))) {
     return fail(INFER_HIP_INVALID_ARGUMENT, "gemm_bf16: null required pointer");
   }
   if (tokens == 1 && bf16_gemv_fast_supported(weight, input, in_features)) {
     launch_bf16_gemv_fast({weight, bias, input, output, out_features, in_features}, stream);
+  } else if (tokens > 1 && gemm_mfma_supported(weight, input, tokens, out_features, in_features)) {
+    const GemmArgs a{weight, nullptr, bias, input, output, tokens, out_features, in_features};
+    launch_gemm_mfma(tile < 0 ? gemm_pick_tile(tokens, out_features) : tile, false, a, stream);
   } else {
     launch_bf16_linear_generic(weight, bias, input, output, tokens, out_features, in_features,
                                stream);
   }
   return check_launch("gemm_bf16");
+}
+
+}  // namespace
+
+extern "C" int infer_hip_gemm_w8a16(const int8_t* weight, const uint16_t* scales,
+                                    int group_size, const uint16_t* bias,
+                                    const uint16_t* input, uint16_t* output, int tokens,
+                                    int out_features, int in_features, hipStream_t stream) {
+  return gemm_w8a16_impl(weight, scales, group_size, bias, input, output, tokens, out_features,
+                         in_features, -1, stream);
+}
+
+extern "C" int infer_hip_gemm_bf16(const uint16_t* weight, const uint16_t* bias,
+                                   const uint16_t* input, uint16_t* output, int tokens,
+                                   int out_features, int in_features, hipStream_t stream) {
+  return gemm_bf16_impl(weight, bias, input, output, tokens, out_features, in_features, -1,
+                        stream);
+}
+
+extern "C" int infer_hip_gemm_tile_count(void) { return kGemmTileCount; }
+
+extern "C" int infer_hip_gemm_w8a16_tile(const int8_t* weight, const uint16_t* scales,
+                                         int group_size, const uint16_t* bias,
+                                         const uint16_t* input, uint16_t* output, int tokens,
+                                         int out_features, int in_features, int tile,
+                                         hipStream_t stream) {
+  return gemm_w8a16_impl(weight, scales, group_size, bias, input, output, tokens, out_features,
+                         in_features, tile, stream);
+}
+
+extern "C" int infer_hip_gemm_bf16_tile(const uint16_t* weight, const uint16_t* bias,
+                                        const uint16_t* input, uint16_t* output, int tokens,
+                                        int out_features, int in_features, int tile,
+                                        hipStream_t stream) {
+  return gemm_bf16_impl(weight, bias, input, output, tokens, out_features, in_features, tile,
+                        stream);
 }

@@ -41,6 +41,34 @@ struct Bf16GemvArgs {
   int k;
 };
 
+// One GEMM Y[m, n] = bf16(sum_k X[m, k] W[n, k] + bias[n]); W is int8 with
+// BF16 group-64 scales s (W8A16) or BF16 with s unused.
+struct GemmArgs {
+  const void* w;         // [n, k] int8 or BF16
+  const uint16_t* s;     // [n, k / 64] BF16 scales (W8A16 only)
+  const uint16_t* bias;  // [n] BF16 or nullptr
+  const uint16_t* x;     // [m, k] BF16
+  uint16_t* y;           // [m, n] BF16
+  int m;
+  int n;
+  int k;
+};
+
+// MFMA GEMM workgroup tiles (rows x columns of Y).
+enum GemmTile {
+  kGemmTile128x128 = 0,
+  kGemmTile128x64 = 1,
+  kGemmTile64x128 = 2,
+  kGemmTile64x64 = 3,
+  kGemmTile32x128 = 4,
+  kGemmTileCount = 5,
+};
+
+// gemm.hip
+bool gemm_mfma_supported(const void* w, const uint16_t* x, int m, int n, int k);
+int gemm_pick_tile(int m, int n);
+void launch_gemm_mfma(int tile, bool w8, const GemmArgs& a, hipStream_t stream);
+
 // gemv.hip
 bool w8a16_gemv_fast_supported(const int8_t* w, const uint16_t* x, int k);
 void launch_w8a16_gemv_fast(const W8GemvArgs& a, hipStream_t stream);

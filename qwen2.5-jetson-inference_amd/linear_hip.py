@@ -33,6 +33,9 @@ EXPORTED_SYMBOLS = (
     "infer_hip_lm_head_workspace_entries",
     "infer_hip_gemv_w8a16",
     "infer_hip_gemm_w8a16",
+    "infer_hip_gemm_tile_count",
+    "infer_hip_gemm_w8a16_tile",
+    "infer_hip_gemm_bf16_tile",
     "infer_hip_w8a16_gemv_plan_create",
     "infer_hip_w8a16_gemv_plan_launch",
     "infer_hip_w8a16_gemv_plan_bytes",
@@ -105,11 +108,15 @@ def load() -> ctypes.CDLL:
         "infer_hip_lm_head_bf16": [p, p, p, p, p, p, p, i, i, p],
         "infer_hip_gemv_w8a16": [p, p, i, p, p, p, i, i, p],
         "infer_hip_gemm_w8a16": [p, p, i, p, p, p, i, i, i, p],
+        "infer_hip_gemm_w8a16_tile": [p, p, i, p, p, p, i, i, i, i, p],
+        "infer_hip_gemm_bf16_tile": [p, p, p, p, i, i, i, i, p],
     }
     for name, args in sigs.items():
         fn = getattr(lib, name)
         fn.argtypes = args
         fn.restype = i
+    lib.infer_hip_gemm_tile_count.argtypes = []
+    lib.infer_hip_gemm_tile_count.restype = i
     lib.infer_hip_lm_head_workspace_entries.argtypes = [i, i]
     lib.infer_hip_lm_head_workspace_entries.restype = ctypes.c_size_t
     lib.infer_hip_w8a16_gemv_plan_create.argtypes = [p, i, ctypes.POINTER(p)]
@@ -196,6 +203,31 @@ def gemm_w8a16(weight, scales, group_size, bias, input, output, tokens,
                                        _ptr(bias), _ptr(input), _ptr(output),
                                        tokens, out_features, in_features,
                                        _stream(stream)))
+
+
+# MFMA workgroup tiles (rows x columns of Y) of the explicit-tile entries.
+GEMM_TILES = ("128x128", "128x64", "64x128", "64x64", "32x128")
+
+
+def gemm_tile_count() -> int:
+    return int(load().infer_hip_gemm_tile_count())
+
+
+def gemm_w8a16_tile(weight, scales, group_size, bias, input, output, tokens,
+                    out_features, in_features, tile, stream=None):
+    """gemm_w8a16 with the MFMA workgroup tile named (-1 = automatic)."""
+    _check(load().infer_hip_gemm_w8a16_tile(_ptr(weight), _ptr(scales), group_size,
+                                            _ptr(bias), _ptr(input), _ptr(output),
+                                            tokens, out_features, in_features, tile,
+                                            _stream(stream)))
+
+
+def gemm_bf16_tile(weight, bias, input, output, tokens, out_features,
+                   in_features, tile, stream=None):
+    """gemm_bf16 with the MFMA workgroup tile named (-1 = automatic)."""
+    _check(load().infer_hip_gemm_bf16_tile(_ptr(weight), _ptr(bias), _ptr(input),
+                                           _ptr(output), tokens, out_features,
+                                           in_features, tile, _stream(stream)))
 
 
 class W8A16GemvPlan:
