@@ -54,6 +54,11 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--launch", choices=("plan", "calls"), default="plan")
+    ap.add_argument("--workload", choices=("decode", "prefill"), default="decode",
+                    help="decode: config 1 (the headline); prefill: config 3 GEMMs")
+    ap.add_argument("--tokens", type=int, default=512, help="prefill M (config 3)")
+    ap.add_argument("--dtype", choices=("w8a16", "bf16"), default="w8a16",
+                    help="prefill weight type")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="bounded CPU-baseline sample length (0 disables)")
     ap.add_argument("--detail", default="",
@@ -186,6 +191,106 @@ def lm_head_detail(dev, hip):
             "bytes": nbytes}
 
 
+MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense BF16
+
+
+class PrefillLayers:
+    """Config 3: `layers` layers x the 7 Linears at M tokens, each layer with
+    its own weights (W8A16: q ~ U{-127..127}, s = bf16(|N(0,.02)|/127);
+    BF16: bf16(N(0, .02))), inputs bf16(N(0,1)), seed 3; one grouped plan
+    per layer (its 7 independent GEMMs in one launch)."""
+
+    def __init__(self, dev, hip, m: int, w8: bool, layers: int = 4, seed: int = 3):
+        import torch
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        self.calls = []   # per layer: list of call tuples
+        self.plans = []
+        for _ in range(layers):
+            layer = []
+            for name, n, k in SHAPES:
+                x = torch.randn((m, k), device=dev, generator=g).to(torch.bfloat16)
+                y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+                if w8:
+                    q = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev, generator=g)
+                    sc = ((torch.randn((n, k // 64), device=dev, generator=g) * 0.02).abs_()
+                          / 127.0).to(torch.bfloat16)
+                    layer.append((q, sc, 64, None, x, y, m, n, k))
+                else:
+                    w = (torch.randn((n, k), device=dev, generator=g) * 0.02).to(torch.bfloat16)
+                    layer.append((w, None, x, y, m, n, k))
+            self.calls.append(layer)
+            self.plans.append(hip.GemmPlan(layer))
+        torch.cuda.synchronize()
+        self.flops_per_layer = sum(2.0 * m * n * k for _, n, k in SHAPES)
+
+
+def prefill_main(args, dev, hip) -> int:
+    """Config 3: prefill GEMMs at M = --tokens.  One step = one layer's 7
+    Linears as one grouped launch (value = GEMM TFLOP/s, i.e. the layer's
+    FLOPs / the launch time); per-shape single calls in the roofline block."""
+    import torch
+    w8 = args.dtype == "w8a16"
+    m = args.tokens
+    pl = PrefillLayers(dev, hip, m, w8)
+    nl = len(pl.plans)
+    calls = [0]
+
+    def step(ev):
+        pl.plans[calls[0] % nl].launch()
+        calls[0] += 1
+    t, _ = time_steps(step, args.steps, args.warmup)
+    ms = t / args.steps
+    tflops = pl.flops_per_layer / (ms * 1e-3) / 1e12
+    per_shape = {}
+    for i, (name, n, k) in enumerate(SHAPES):
+        def one(ev, i=i):
+            c = pl.calls[calls[0] % nl][i]
+            calls[0] += 1
+            (hip.gemm_w8a16 if w8 else hip.gemm_bf16)(*c)
+        tt, _ = time_steps(one, max(20, args.steps // 4), 5)
+        us = tt / max(20, args.steps // 4) * 1e3
+        per_shape[name] = {"us_per_call": round(us, 2),
+                           "TFLOPs": round(2.0 * m * n * k / (us * 1e-6) / 1e12, 1)}
+    line = {
+        "metric": f"{'W8A16' if w8 else 'BF16'} prefill GEMM TFLOP/s (% of BF16 MFMA peak), "
+                  f"Qwen2.5-0.5B Linears, M={m}",
+        "value": round(tflops, 1),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 x bf16 -> fp32" if w8 else "bf16 x bf16 -> fp32",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"config 3: one layer's 7 Qwen2.5-0.5B Linear GEMMs at M={m} as one "
+                         f"grouped launch, {nl} layers of distinct weights rotated, seed 3"),
+            "flops_per_step": pl.flops_per_layer,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "gemm_grouped_kernel (7 GEMMs of one layer)",
+            "achieved": round(tflops, 1),
+            "peak": MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "avg_launch_us": round(ms * 1e3, 2),
+            "per_shape_single_calls": per_shape,
+        },
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line))
+    for p in pl.plans:
+        p.close()
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -198,6 +303,8 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.workload == "prefill":
+        return prefill_main(args, dev, hip)
     layers = Layers(dev)
     plan = hip.W8A16GemvPlan(layers.calls)
     assert abs(plan.bytes - layers.bytes) < 1, (plan.bytes, layers.bytes)

@@ -123,5 +123,26 @@ class W8A16GemvPlan {
   infer_hip_gemv_plan* plan_{nullptr};
 };
 
+// A grouped prefill GEMM plan (RAII): many independent gemm_w8a16 (or
+// gemm_bf16) calls in one launch, resolved once; long reductions are split
+// over K.  No single reference counterpart.
+class GemmPlan {
+ public:
+  explicit GemmPlan(const std::vector<infer_hip_gemm_desc>& descs) {
+    check(infer_hip_gemm_plan_create(descs.data(), static_cast<int>(descs.size()), &plan_));
+  }
+  ~GemmPlan() {
+    if (plan_) (void)infer_hip_gemm_plan_destroy(plan_);
+  }
+  GemmPlan(const GemmPlan&) = delete;
+  GemmPlan& operator=(const GemmPlan&) = delete;
+  GemmPlan(GemmPlan&& other) noexcept : plan_(std::exchange(other.plan_, nullptr)) {}
+  void launch(hipStream_t stream) const { check(infer_hip_gemm_plan_launch(plan_, stream)); }
+  double flops() const { return infer_hip_gemm_plan_flops(plan_); }
+
+ private:
+  infer_hip_gemm_plan* plan_{nullptr};
+};
+
 }  // namespace hip
 }  // namespace infer

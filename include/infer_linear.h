@@ -164,6 +164,49 @@ int infer_hip_w8a16_gemv_plan_launch(const infer_hip_gemv_plan* plan,
 double infer_hip_w8a16_gemv_plan_bytes(const infer_hip_gemv_plan* plan);
 int infer_hip_w8a16_gemv_plan_destroy(infer_hip_gemv_plan* plan);
 
+/* ---- Grouped GEMM plans (prefill) --------------------------------------
+ * No single reference counterpart: the multi-matrix form of
+ * infer_hip_gemm_w8a16 / infer_hip_gemm_bf16 for GEMMs independent of
+ * each other, such as q/k/v on one normed input and gate/up on another
+ * (src/qwen2.cpp:526-571 issues them as separate gemm_w8a16 calls), or a
+ * sweep over a layer's Linears (tools/linear_benchmark.cpp measures them
+ * one by one).  Each descriptor has the meaning of one
+ * infer_hip_gemm_w8a16 (w8a16 = 1: weight is int8 with BF16 group-64
+ * scales) or infer_hip_gemm_bf16 (w8a16 = 0: weight is BF16, scales and
+ * group_size ignored) call; all descriptors of a plan have the same
+ * w8a16 value.  Each must meet the MFMA path's preconditions:
+ * tokens >= 2, in_features % 64 == 0, 16-byte aligned weight and input,
+ * every operand under 2 GiB; no output may alias any input of the same
+ * plan.  create resolves and uploads the descriptor table once (it
+ * allocates device memory on the current device: the table and, when some
+ * reduction is split, FP32 partial tiles); launch enqueues one kernel and
+ * allocates nothing.  A descriptor whose K is much longer than the plan's
+ * shortest is split over K into parts of about that length, summed in a
+ * fixed order (results do not depend on scheduling); the longest units
+ * start first.  Launches of one plan must not overlap (they share the
+ * partial tiles): keep them on one stream. */
+typedef struct infer_hip_gemm_desc {
+  int w8a16;
+  const void* weight;
+  const uint16_t* scales;
+  int group_size;
+  const uint16_t* bias;
+  const uint16_t* input;
+  uint16_t* output;
+  int tokens;
+  int out_features;
+  int in_features;
+} infer_hip_gemm_desc;
+
+typedef struct infer_hip_gemm_plan infer_hip_gemm_plan;
+
+int infer_hip_gemm_plan_create(const infer_hip_gemm_desc* descs, int count,
+                               infer_hip_gemm_plan** plan);
+int infer_hip_gemm_plan_launch(const infer_hip_gemm_plan* plan, hipStream_t stream);
+/* 2 * tokens * out_features * in_features summed over the descriptors. */
+double infer_hip_gemm_plan_flops(const infer_hip_gemm_plan* plan);
+int infer_hip_gemm_plan_destroy(infer_hip_gemm_plan* plan);
+
 #ifdef __cplusplus
 }
 #endif

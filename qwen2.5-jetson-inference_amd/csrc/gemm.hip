@@ -44,6 +44,7 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;  // 4 waves
 constexpr int kStageK = 64;    // K columns per stage = one quantisation group
@@ -103,6 +104,128 @@ __device__ __forceinline__ void i8x16_to_bf16(const uint4 q, uint4& lo, uint4& h
   hi.w = pack_hi_halves(sbyte2(q.w), sbyte3(q.w));
 }
 
+// Instruction-group order for one stage (sched_group_barrier masks: 0x008
+// MFMA, 0x100 LDS read, 0x200 LDS write, 0x020 global read, 0x002 VALU).
+// Each MFMA is followed by its share of the stage's remaining fragment
+// reads, of the VALU work (the int8 conversion of the next stage) and of
+// the next stage's LDS writes and global loads, so the matrix core stays
+// busy while the rest issues.  Shares are spread evenly: group i of N gets
+// total * (i + 1) / N - total * i / N.
+template <int I, int N, int READS, int VALU, int WRITES, int LOADS>
+struct StageSchedule {
+  static __device__ __forceinline__ void emit() {
+    constexpr int r = READS * (I + 1) / N - READS * I / N;
+    constexpr int v = VALU * (I + 1) / N - VALU * I / N;
+    constexpr int w = WRITES * (I + 1) / N - WRITES * I / N;
+    constexpr int l = LOADS * (I + 1) / N - LOADS * I / N;
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(0x100, r, 0);
+    if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x002, v, 0);
+    if constexpr (w > 0) __builtin_amdgcn_sched_group_barrier(0x200, w, 0);
+    if constexpr (l > 0) __builtin_amdgcn_sched_group_barrier(0x020, l, 0);
+    StageSchedule<I + 1, N, READS, VALU, WRITES, LOADS>::emit();
+  }
+};
+template <int N, int READS, int VALU, int WRITES, int LOADS>
+struct StageSchedule<N, N, READS, VALU, WRITES, LOADS> {
+  static __device__ __forceinline__ void emit() {}
+};
+
+// A tile reduced over part of K.  The tile's `parts` workgroups each sum
+// `count` stages from `begin` and write their FP32 partial to
+// partial + index * tile_floats (index = this part); the last one to finish
+// (counted on *counter) adds all the parts in index order — so the result
+// does not depend on which finished last — and runs the epilogue.
+struct SplitK {
+  int begin = 0;
+  int count = 0;  // 0: the whole of K, no split
+  int parts = 1;
+  int index = 0;
+  float* partial = nullptr;  // this tile's parts, parts * tile_floats floats
+  int* counter = nullptr;
+};
+
+// Split-K hand-off; returns true in the workgroup that finishes the tile
+// (acc then holds the tile's full sum).  Each thread's FP32 values are
+// stored as 16-byte vectors at [(i * 256 + thread) * 4], i < 4 FM FN, so a
+// wave's stores and loads are contiguous.
+// Coherence across XCDs without cache flushes: the parts are written and
+// read with device-coherent (sc1) buffer accesses, which the AMDGPU memory
+// model uses for agent-scope atomic stores and loads; every thread waits
+// for its stores to complete before the barrier that precedes the arrival
+// count (an agent-scope atomic), and the finishing workgroup reads the parts
+// only after that count.  Nothing waits on another workgroup: the ones that
+// are not last simply exit.
+constexpr int kCoherent = 16;  // buffer cache policy: sc1
+
+template <int FM, int FN>
+__device__ __forceinline__ bool splitk_fixup(f32x16_t (&acc)[FM][FN], const SplitK& sp) {
+  constexpr int kVec = 4 * FM * FN;  // 16-byte vectors per thread
+  constexpr int kTileBytes = kVec * kThreads * 16;
+  __shared__ int last;
+  const int tid = threadIdx.x;
+  const __amdgpu_buffer_rsrc_t pr =
+      make_rsrc(sp.partial, static_cast<uint32_t>(sp.parts) * kTileBytes);
+  const uint32_t mine = static_cast<uint32_t>(sp.index) * kTileBytes;
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int i = (fm * FN + fn) * 4 + q;
+        const f32x4_t v = {acc[fm][fn][4 * q], acc[fm][fn][4 * q + 1], acc[fm][fn][4 * q + 2],
+                           acc[fm][fn][4 * q + 3]};
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), pr,
+                                               mine + (i * kThreads + tid) * 16u, 0, kCoherent);
+      }
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's parts are stored
+  __syncthreads();
+  if (tid == 0) {
+    last = __hip_atomic_fetch_add(sp.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           sp.parts - 1;
+  }
+  __syncthreads();
+  if (!last) return false;
+  f32x16_t sum[FM][FN];
+  for (int p = 0; p < sp.parts; ++p) {
+    const uint32_t base = static_cast<uint32_t>(p) * kTileBytes;
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int i = (fm * FN + fn) * 4 + q;
+          f32x4_t v;
+          if (p == sp.index) {
+            v = f32x4_t{acc[fm][fn][4 * q], acc[fm][fn][4 * q + 1], acc[fm][fn][4 * q + 2],
+                        acc[fm][fn][4 * q + 3]};
+          } else {
+            v = __builtin_bit_cast(
+                f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                             pr, base + (i * kThreads + tid) * 16u, 0, kCoherent));
+          }
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            if (p == 0) {
+              sum[fm][fn][4 * q + c] = v[c];
+            } else {
+              sum[fm][fn][4 * q + c] += v[c];
+            }
+          }
+        }
+  }
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = sum[fm][fn];
+  if (tid == 0) {  // ready for the next launch
+    __hip_atomic_store(sp.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return true;
+}
+
 template <int BM, int BN, int WAVES_M, bool W8>
 struct TileShape {
   static constexpr int kWavesN = 4 / WAVES_M;
@@ -130,7 +253,8 @@ struct TileShape {
 // g, which every wave reaches only after its MFMAs of stage g - 1, the
 // last reader of that buffer.
 template <int BM, int BN, int WAVES_M, bool W8, int D>
-__device__ __forceinline__ void gemm_tile(const GemmArgs& a, int m0, int n0) {
+__device__ __forceinline__ void gemm_tile(const GemmArgs& a, int m0, int n0,
+                                          const SplitK& split = SplitK{}) {
   using S = TileShape<BM, BN, WAVES_M, W8>;
   constexpr int FM = S::FM, FN = S::FN;
   __shared__ uint4 lds_a[2][BM * kRowChunks];
@@ -144,8 +268,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int m0, int n0) {
   const int wn = wave / WAVES_M;
   const int r = lane & 31;   // row of an A fragment / column of a B fragment
   const int h = lane >> 5;   // which half of the 64 staged columns' chunks
-  const int stages = a.k / kStageK;
   const int groups = a.k / kStageK;  // scale row stride
+  // This workgroup's stages: [split.begin, split.begin + stages) of the
+  // K / 64 groups (all of them unless the tile is split over K).
+  const int stages = split.count > 0 ? split.count : groups;
+  const int sbeg = split.count > 0 ? split.begin : 0;
 
   // ---- global -> register staging, one slot per stage in flight ----
   // Buffer loads: a row past M or N is out of the resource's range and
@@ -178,7 +305,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int m0, int n0) {
 
   auto load_stage = [&](int g, uint4 (&xa)[S::A_LOADS], uint4 (&xb)[S::B_LOADS],
                         uint32_t& xs) {
-    const uint32_t gc = static_cast<uint32_t>(min(g, stages - 1));
+    const uint32_t gc = static_cast<uint32_t>(min(g, stages - 1) + sbeg);
     const uint32_t kbyte = gc * kStageK * 2u;
 #pragma unroll
     for (int i = 0; i < S::A_LOADS; ++i) xa[i] = buffer_load16(xr, xoff[i], kbyte);
@@ -191,7 +318,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int m0, int n0) {
 
   auto store_stage = [&](int buf, const uint4 (&xa)[S::A_LOADS],
                          const uint4 (&xb)[S::B_LOADS], uint32_t xs) {
-    if (W8 && tid < BN) lds_s[buf][tid] = bf16_to_f32(xs);
+    // Threads tid and tid + BN hold the same row's scale: both write it,
+    // which keeps the fill free of branches.
+    if (W8) lds_s[buf][tid % BN] = bf16_to_f32(xs);
 #pragma unroll
     for (int i = 0; i < S::A_LOADS; ++i) {
       const int c = tid + kThreads * i;
@@ -272,6 +401,21 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int m0, int n0) {
     }
   };
 
+  // Pipeline order of one main-loop stage (see StageSchedule): the k-step 0
+  // fragments (and the W8 scales) first, the k-step 1..3 fragments spread
+  // over the first three quarters of the MFMAs, the next stage's int8
+  // conversion, LDS writes and global loads over all of them.
+  auto schedule_stage = [&]() {
+    constexpr int kMfma = 4 * FM * FN;
+    constexpr int kFirstReads = FM + FN + (W8 ? FN : 0);
+    constexpr int kLaterReads = 3 * (FM + FN);
+    constexpr int kValu = W8 ? 24 * S::B_LOADS : 0;
+    constexpr int kWrites = S::A_LOADS + (W8 ? 2 : 1) * S::B_LOADS + (W8 ? 1 : 0);
+    constexpr int kLoads = S::A_LOADS + S::B_LOADS + (W8 ? 1 : 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, kFirstReads, 0);
+    StageSchedule<0, kMfma, kLaterReads * 4 / 3, kValu, kWrites, kLoads>::emit();
+  };
+
   // Stage g lives in register slot g % D and LDS buffer g & 1.  Iteration
   // g runs the MFMAs of stage g and, in the same instruction stream, writes
   // stage g + 1 into the other LDS buffer and issues the loads of stage
@@ -298,6 +442,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int m0, int n0) {
       const int jn = (j + 1) % D;
       store_stage((j + 1) & 1, ra[jn], rb[jn], rs[jn]);
       load_stage(g + 1 + D, ra[jn], rb[jn], rs[jn]);
+      schedule_stage();
       __syncthreads();
     }
   }
@@ -312,6 +457,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int m0, int n0) {
       __syncthreads();
     }
   }
+
+  if (split.parts > 1 && !splitk_fixup<FM, FN>(acc, split)) return;
 
   // ---- epilogue: accumulator element e of a 32 x 32 tile is at row
   // 8 (e / 4) + 4 h + e % 4, column r ----
@@ -335,6 +482,38 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int m0, int n0) {
 template <int BM, int BN, int WAVES_M, bool W8>
 __global__ __launch_bounds__(kThreads) QLIN_GEMM_WAVES_ATTR void gemm_mfma_kernel(GemmArgs a) {
   gemm_tile<BM, BN, WAVES_M, W8, kPrefetch>(a, blockIdx.y * BM, blockIdx.x * BN);
+}
+
+// Many GEMMs in one launch.  Block b belongs to the descriptor d with
+// block_begin[d] <= b < block_begin[d + 1] (descriptors sorted by
+// block_begin); its unit u = b - block_begin[d] is part u % splits of
+// output tile u / splits, M tiles fastest (consecutive tiles share one
+// weight tile).
+template <int BM, int BN, int WAVES_M, bool W8>
+__global__ __launch_bounds__(kThreads) QLIN_GEMM_WAVES_ATTR void gemm_grouped_kernel(
+    const GemmGroupDesc* __restrict__ descs, int count) {
+  const int b = blockIdx.x;
+  int lo = 0, hi = count - 1;
+  while (lo < hi) {  // last descriptor whose block_begin <= b
+    const int mid = (lo + hi + 1) >> 1;
+    if (descs[mid].block_begin <= b) lo = mid; else hi = mid - 1;
+  }
+  const GemmGroupDesc& d = descs[lo];
+  const int u = b - d.block_begin;
+  const int tile = u / d.splits;
+  const GemmArgs a{d.w, d.s, d.bias, d.x, d.y, d.m, d.n, d.k};
+  SplitK sp;
+  if (d.splits > 1) {
+    const int groups = d.k / kStageK;
+    sp.parts = d.splits;
+    sp.index = u % d.splits;
+    sp.begin = sp.index * d.split_stages;
+    sp.count = min(d.split_stages, groups - sp.begin);
+    sp.partial = d.partial + static_cast<size_t>(tile) * d.splits * (BM * BN);
+    sp.counter = d.counters + tile;
+  }
+  gemm_tile<BM, BN, WAVES_M, W8, kPrefetch>(a, (tile % d.tiles_m) * BM, (tile / d.tiles_m) * BN,
+                                            sp);
 }
 
 template <int BM, int BN, int WAVES_M, bool W8>
@@ -374,6 +553,36 @@ int gemm_pick_tile(int m, int n) {
   // grids of over 2048 such tiles switch to 128 x 128.
   const long long t64 = static_cast<long long>((m + 63) / 64) * ((n + 63) / 64);
   return t64 > 2048 ? kGemmTile128x128 : kGemmTile64x64;
+}
+
+int gemm_tile_rows(int tile) {
+  static const int rows[kGemmTileCount] = {128, 128, 64, 64, 32};
+  return rows[tile];
+}
+
+int gemm_tile_cols(int tile) {
+  static const int cols[kGemmTileCount] = {128, 64, 128, 64, 128};
+  return cols[tile];
+}
+
+void launch_gemm_grouped(int tile, bool w8, const GemmGroupDesc* device_descs, int count,
+                         int total_blocks, hipStream_t stream) {
+  const dim3 grid(total_blocks), block(kThreads);
+  if (tile == kGemmTile128x128) {
+    if (w8) {
+      hipLaunchKernelGGL((gemm_grouped_kernel<128, 128, 2, true>), grid, block, 0, stream,
+                         device_descs, count);
+    } else {
+      hipLaunchKernelGGL((gemm_grouped_kernel<128, 128, 2, false>), grid, block, 0, stream,
+                         device_descs, count);
+    }
+  } else if (w8) {
+    hipLaunchKernelGGL((gemm_grouped_kernel<64, 64, 2, true>), grid, block, 0, stream,
+                       device_descs, count);
+  } else {
+    hipLaunchKernelGGL((gemm_grouped_kernel<64, 64, 2, false>), grid, block, 0, stream,
+                       device_descs, count);
+  }
 }
 
 void launch_gemm_mfma(int tile, bool w8, const GemmArgs& a, hipStream_t stream) {

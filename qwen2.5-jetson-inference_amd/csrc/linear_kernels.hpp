@@ -64,7 +64,33 @@ enum GemmTile {
   kGemmTileCount = 5,
 };
 
+// One GEMM of a grouped launch: its blocks are block_begin ..
+// block_begin + tiles_m * tiles_n * splits - 1, each one part (of
+// `splits`, split_stages K stages of 64 each) of one output tile of the
+// plan's tile size (gemm_grouped_tile_rows x gemm_grouped_tile_cols).  Split tiles hand off through partial (splits FP32 tiles per
+// output tile) and counters (one per output tile, zero between launches).
+struct GemmGroupDesc {
+  const void* w;
+  const uint16_t* s;
+  const uint16_t* bias;
+  const uint16_t* x;
+  uint16_t* y;
+  int m;
+  int n;
+  int k;
+  int tiles_m;
+  int block_begin;
+  int splits;
+  int split_stages;
+  float* partial;
+  int* counters;
+};
 // gemm.hip
+// Grouped launches use kGemmTile64x64 or kGemmTile128x128.
+int gemm_tile_rows(int tile);
+int gemm_tile_cols(int tile);
+void launch_gemm_grouped(int tile, bool w8, const GemmGroupDesc* device_descs, int count,
+                         int total_blocks, hipStream_t stream);
 bool gemm_mfma_supported(const void* w, const uint16_t* x, int m, int n, int k);
 int gemm_pick_tile(int m, int n);
 void launch_gemm_mfma(int tile, bool w8, const GemmArgs& a, hipStream_t stream);

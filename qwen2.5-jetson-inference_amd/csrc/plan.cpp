@@ -1,5 +1,5 @@
-// Grouped W8A16 GEMV plans: many independent GEMVs streamed by one launch per
-// slot class from a descriptor table resolved once and kept in device memory.
+// Grouped plans: many independent GEMVs (decode) or GEMMs (prefill) run by
+// one launch from a descriptor table resolved once and kept in device memory.
 //
 // This is the multi-matrix form of infer::cuda::gemv_w8a16
 // (include/infer/cuda_ops.hpp:47-50) for callers that issue several GEMVs on
@@ -114,5 +114,164 @@ extern "C" int infer_hip_w8a16_gemv_plan_destroy(infer_hip_gemv_plan* plan) {
   if (prev != plan->device) (void)hipSetDevice(prev);
   delete plan;
   if (st != hipSuccess) return fail(INFER_HIP_RUNTIME_ERROR, "gemv plan: %s", hipGetErrorString(st));
+  return ok();
+}
+
+// ---------------------------------------------------------------------------
+// Grouped GEMM plans (prefill): many independent GEMMs in one launch of the
+// MFMA kernel, one workgroup per output tile (or part of one, split over K).
+
+struct infer_hip_gemm_plan {
+  GemmGroupDesc* table = nullptr;  // device memory
+  float* partial = nullptr;        // split-K partial tiles (device)
+  int* counters = nullptr;         // split-K arrival counters (device, zeroed)
+  int count = 0;
+  int blocks = 0;
+  int device = 0;
+  int tile = kGemmTile64x64;
+  bool w8 = false;
+  double flops = 0.0;
+};
+
+extern "C" int infer_hip_gemm_plan_create(const infer_hip_gemm_desc* descs, int count,
+                                          infer_hip_gemm_plan** plan_out) {
+  if (!plan_out) return fail(INFER_HIP_INVALID_ARGUMENT, "gemm plan: null output pointer");
+  *plan_out = nullptr;
+  if (!descs || count <= 0) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "gemm plan: need at least one descriptor");
+  }
+  const bool w8 = descs[0].w8a16 != 0;
+  // 128 x 128 tiles move half the LDS bytes per FLOP of 64 x 64 ones; for
+  // BF16 they pay off once every GEMM has rows enough to fill them (M=512
+  // layer plan: 43.1 us against 44.6).  The W8A16 128 x 128 kernel needs
+  // more than 256 registers, so one workgroup per CU: slower (56.2 us
+  // against 46.4).
+  int min_tokens = descs[0].tokens;
+  for (int i = 1; i < count; ++i) min_tokens = std::min(min_tokens, descs[i].tokens);
+  const int tile = (!w8 && min_tokens >= 256) ? kGemmTile128x128 : kGemmTile64x64;
+  const int bm = gemm_tile_rows(tile), bn = gemm_tile_cols(tile);
+  std::vector<GemmGroupDesc> table;
+  table.reserve(count);
+  double flops = 0.0;
+  for (int i = 0; i < count; ++i) {
+    const infer_hip_gemm_desc& d = descs[i];
+    if ((d.w8a16 != 0) != w8) {
+      return fail(INFER_HIP_INVALID_ARGUMENT,
+                  "gemm plan: descriptor %d: all descriptors must share one weight type", i);
+    }
+    if (w8 && d.group_size != 64) {
+      return fail(INFER_HIP_INVALID_ARGUMENT, "gemm plan: descriptor %d: group size must be 64",
+                  i);
+    }
+    if (d.tokens < 2 || d.out_features <= 0 || d.in_features <= 0) {
+      return fail(INFER_HIP_INVALID_ARGUMENT, "gemm plan: descriptor %d: bad shape M=%d N=%d K=%d",
+                  i, d.tokens, d.out_features, d.in_features);
+    }
+    if (!d.weight || (w8 && !d.scales) || !d.input || !d.output) {
+      return fail(INFER_HIP_INVALID_ARGUMENT, "gemm plan: descriptor %d: null pointer", i);
+    }
+    if (!gemm_mfma_supported(d.weight, d.input, d.tokens, d.out_features, d.in_features)) {
+      return fail(INFER_HIP_INVALID_ARGUMENT,
+                  "gemm plan: descriptor %d needs K %% 64 == 0, 16-byte aligned weight and "
+                  "input and operands under 2 GiB (K=%d)",
+                  i, d.in_features);
+    }
+    const int tiles_m = (d.tokens + bm - 1) / bm;
+    table.push_back(GemmGroupDesc{d.weight, w8 ? d.scales : nullptr, d.bias, d.input, d.output,
+                                  d.tokens, d.out_features, d.in_features, tiles_m, 0, 1,
+                                  d.in_features / 64, nullptr, nullptr});
+    flops += 2.0 * d.tokens * d.out_features * d.in_features;
+  }
+  // Split K so that no unit is much longer than the plan's shortest
+  // reduction (at least 8 stages of 64): a lone long-K tile would otherwise
+  // be the whole launch's critical path.
+  int min_stages = 1 << 30;
+  for (const GemmGroupDesc& d : table) min_stages = std::min(min_stages, d.k / 64);
+  const int target = std::max(8, min_stages);
+  size_t partial_floats = 0, counter_count = 0;
+  for (GemmGroupDesc& d : table) {
+    const int stages = d.k / 64;
+    const int parts = (stages + target - 1) / target;
+    if (parts > 1) {
+      d.split_stages = (stages + parts - 1) / parts;
+      d.splits = (stages + d.split_stages - 1) / d.split_stages;  // no empty part
+      const size_t tiles =
+          static_cast<size_t>(d.tiles_m) * ((d.n + bn - 1) / bn);
+      partial_floats += tiles * d.splits * bm * bn;
+      counter_count += tiles;
+    }
+  }
+  // Longest units first: they take longest, so starting them earliest
+  // shortens the launch's tail.
+  std::stable_sort(table.begin(), table.end(), [](const GemmGroupDesc& a, const GemmGroupDesc& b) {
+    return a.split_stages > b.split_stages;
+  });
+  long long blocks = 0;
+  for (GemmGroupDesc& d : table) {
+    d.block_begin = static_cast<int>(blocks);
+    blocks += static_cast<long long>(d.tiles_m) * ((d.n + bn - 1) / bn) *
+              d.splits;
+  }
+  if (blocks > 0x7FFFFFFF) return fail(INFER_HIP_INVALID_ARGUMENT, "gemm plan: too many tiles");
+  auto* plan = new (std::nothrow) infer_hip_gemm_plan();
+  if (!plan) return fail(INFER_HIP_RUNTIME_ERROR, "gemm plan: out of host memory");
+  plan->count = count;
+  plan->blocks = static_cast<int>(blocks);
+  plan->w8 = w8;
+  plan->tile = tile;
+  plan->flops = flops;
+  hipError_t st = hipGetDevice(&plan->device);
+  if (st == hipSuccess && partial_floats > 0) {
+    st = hipMalloc(&plan->partial, partial_floats * sizeof(float));
+    if (st == hipSuccess) st = hipMalloc(&plan->counters, counter_count * sizeof(int));
+    if (st == hipSuccess) st = hipMemset(plan->counters, 0, counter_count * sizeof(int));
+    size_t pf = 0, cc = 0;
+    for (GemmGroupDesc& d : table) {
+      if (d.splits <= 1) continue;
+      const size_t tiles =
+          static_cast<size_t>(d.tiles_m) * ((d.n + bn - 1) / bn);
+      d.partial = plan->partial + pf;
+      d.counters = plan->counters + cc;
+      pf += tiles * d.splits * bm * bn;
+      cc += tiles;
+    }
+  }
+  if (st == hipSuccess) st = hipMalloc(&plan->table, table.size() * sizeof(GemmGroupDesc));
+  if (st == hipSuccess) {
+    st = hipMemcpy(plan->table, table.data(), table.size() * sizeof(GemmGroupDesc),
+                   hipMemcpyHostToDevice);
+  }
+  if (st != hipSuccess) {
+    if (plan->table) (void)hipFree(plan->table);
+    if (plan->partial) (void)hipFree(plan->partial);
+    if (plan->counters) (void)hipFree(plan->counters);
+    delete plan;
+    return fail(INFER_HIP_RUNTIME_ERROR, "gemm plan: %s", hipGetErrorString(st));
+  }
+  *plan_out = plan;
+  return ok();
+}
+
+extern "C" int infer_hip_gemm_plan_launch(const infer_hip_gemm_plan* plan, hipStream_t stream) {
+  if (!plan) return fail(INFER_HIP_INVALID_ARGUMENT, "gemm plan: null plan");
+  launch_gemm_grouped(plan->tile, plan->w8, plan->table, plan->count, plan->blocks, stream);
+  return check_launch("gemm plan");
+}
+
+extern "C" double infer_hip_gemm_plan_flops(const infer_hip_gemm_plan* plan) {
+  return plan ? plan->flops : 0.0;
+}
+
+extern "C" int infer_hip_gemm_plan_destroy(infer_hip_gemm_plan* plan) {
+  if (!plan) return ok();
+  int prev = 0;
+  hipError_t st = hipGetDevice(&prev);
+  if (st == hipSuccess && prev != plan->device) st = hipSetDevice(plan->device);
+  if (st == hipSuccess) st = hipFree(plan->table);
+  if (st == hipSuccess && plan->partial) st = hipFree(plan->partial);
+  if (st == hipSuccess && plan->counters) st = hipFree(plan->counters);
+  if (prev != plan->device) (void)hipSetDevice(prev);
+  delete plan;
+  if (st != hipSuccess) return fail(INFER_HIP_RUNTIME_ERROR, "gemm plan: %s", hipGetErrorString(st));
   return ok();
 }

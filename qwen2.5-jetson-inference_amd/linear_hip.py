@@ -40,6 +40,10 @@ EXPORTED_SYMBOLS = (
     "infer_hip_w8a16_gemv_plan_launch",
     "infer_hip_w8a16_gemv_plan_bytes",
     "infer_hip_w8a16_gemv_plan_destroy",
+    "infer_hip_gemm_plan_create",
+    "infer_hip_gemm_plan_launch",
+    "infer_hip_gemm_plan_flops",
+    "infer_hip_gemm_plan_destroy",
 )
 
 
@@ -52,6 +56,22 @@ class W8A16GemvDesc(ctypes.Structure):
         ("bias", ctypes.c_void_p),
         ("input", ctypes.c_void_p),
         ("output", ctypes.c_void_p),
+        ("out_features", ctypes.c_int),
+        ("in_features", ctypes.c_int),
+    ]
+
+
+class GemmDesc(ctypes.Structure):
+    """infer_hip_gemm_desc: the arguments of one gemm_w8a16 / gemm_bf16 call."""
+    _fields_ = [
+        ("w8a16", ctypes.c_int),
+        ("weight", ctypes.c_void_p),
+        ("scales", ctypes.c_void_p),
+        ("group_size", ctypes.c_int),
+        ("bias", ctypes.c_void_p),
+        ("input", ctypes.c_void_p),
+        ("output", ctypes.c_void_p),
+        ("tokens", ctypes.c_int),
         ("out_features", ctypes.c_int),
         ("in_features", ctypes.c_int),
     ]
@@ -127,6 +147,14 @@ def load() -> ctypes.CDLL:
     lib.infer_hip_w8a16_gemv_plan_bytes.restype = ctypes.c_double
     lib.infer_hip_w8a16_gemv_plan_destroy.argtypes = [p]
     lib.infer_hip_w8a16_gemv_plan_destroy.restype = i
+    lib.infer_hip_gemm_plan_create.argtypes = [p, i, ctypes.POINTER(p)]
+    lib.infer_hip_gemm_plan_create.restype = i
+    lib.infer_hip_gemm_plan_launch.argtypes = [p, p]
+    lib.infer_hip_gemm_plan_launch.restype = i
+    lib.infer_hip_gemm_plan_flops.argtypes = [p]
+    lib.infer_hip_gemm_plan_flops.restype = ctypes.c_double
+    lib.infer_hip_gemm_plan_destroy.argtypes = [p]
+    lib.infer_hip_gemm_plan_destroy.restype = i
     _lib = lib
     return lib
 
@@ -263,6 +291,52 @@ class W8A16GemvPlan:
         if self._handle:
             _check(load().infer_hip_w8a16_gemv_plan_destroy(self._handle))
             self._handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class GemmPlan:
+    """A grouped GEMM plan: ``calls`` is a sequence of W8A16 tuples
+    ``(weight, scales, group_size, bias, input, output, tokens,
+    out_features, in_features)`` (the arguments of :func:`gemm_w8a16`) or of
+    BF16 tuples ``(weight, bias, input, output, tokens, out_features,
+    in_features)`` (:func:`gemm_bf16`); all of one kind.  The tensors must
+    outlive the plan."""
+
+    def __init__(self, calls):
+        calls = list(calls)
+        arr = (GemmDesc * len(calls))()
+        for d, c in zip(arr, calls):
+            if len(c) == 9:
+                w, s, g, b, x, y, m, n, k = c
+                d.w8a16, d.scales, d.group_size = 1, _ptr(s), g
+            else:
+                w, b, x, y, m, n, k = c
+                d.w8a16, d.scales, d.group_size = 0, None, 0
+            d.weight, d.bias, d.input, d.output = _ptr(w), _ptr(b), _ptr(x), _ptr(y)
+            d.tokens, d.out_features, d.in_features = m, n, k
+        handle = ctypes.c_void_p()
+        _check(load().infer_hip_gemm_plan_create(
+            ctypes.cast(arr, ctypes.c_void_p) if calls else None, len(calls),
+            ctypes.byref(handle)))
+        self._handle = handle
+        self.count = len(calls)
+
+    @property
+    def flops(self) -> float:
+        return float(load().infer_hip_gemm_plan_flops(self._handle))
+
+    def launch(self, stream=None) -> None:
+        _check(load().infer_hip_gemm_plan_launch(self._handle, _stream(stream)))
+
+    def close(self) -> None:
+        if self._handle:
+            _check(load().infer_hip_gemm_plan_destroy(self._handle))
+            self._handle = None
 
     def __del__(self):
         try:

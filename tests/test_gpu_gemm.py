@@ -116,3 +116,79 @@ def test_gemm_row_matches_gemv(hip, orc, dev):
     hip.gemv_w8a16(dq, ds, 64, None, to_dev(x[0], dev), y1, n, k)
     g, v = rc.bf16_values(words(y)[0]), rc.bf16_values(words(y1))
     assert np.all(np.abs(g - v) <= np.maximum(1.0 / 64, 0.01 * np.abs(v)))
+
+
+# ------------------------------------------------------ grouped GEMM plan --
+
+@pytest.mark.parametrize("m", (130, 300))
+@pytest.mark.parametrize("w8", (True, False), ids=("w8a16", "bf16"))
+def test_gemm_plan_matches_single_calls(hip, orc, dev, w8, m):
+    # The seven Qwen Linears at M = 130 or 300 (ragged last M tiles; BF16
+    # plans with every M >= 256 use 128 x 128 tiles, others 64 x 64) plus a
+    # ragged N and K, in one launch.  The shortest reduction (K = 192, 3 stages)
+    # makes the plan split every K >= 576 into parts of 8 stages, so this
+    # covers split-K hand-offs (up to 10 parts for K = 4864) next to unsplit
+    # tiles.  Each output equals the oracle, agrees with the single call
+    # (same tile; split tiles add their parts in another order)
+    # within the reference's GEMV-vs-GEMM bound max(1/64, 1 %)
+    # (test_cuda.cpp:604-608), and is bit-identical across launches (the
+    # parts are summed in a fixed order whichever finishes last).
+    import torch
+    rng = rc.philox(110 + w8 + m)
+    tile = 0 if (m >= 256 and not w8) else 3  # the plan's tile, for the single calls
+    calls, expected, singles = [], [], []
+    for (name, n, k, bias) in rc.QWEN_LINEARS + (("ragged", 70, 192, True),):
+        x = rc.bf16_normal(rng, (m, k))
+        b = rc.bf16_normal(rng, (n,)) if bias else None
+        dx, db = to_dev(x, dev), (to_dev(b, dev) if bias else None)
+        y, y1 = bf16_out((m, n), dev), bf16_out((m, n), dev)
+        if w8:
+            q, s = rc.w8a16_synthetic(rng, n, k)
+            exp, _ = orc.w8a16_reference(q, s, 64, b, x)
+            dq, ds = to_dev(q, dev), to_dev(s, dev)
+            calls.append((dq, ds, 64, db, dx, y, m, n, k))
+            hip.gemm_w8a16_tile(dq, ds, 64, db, dx, y1, m, n, k, tile)
+        else:
+            w = rc.bf16_normal(rng, (n, k), 0.02)
+            exp = orc.bf16_linear_reference(w, b, x)
+            dw = to_dev(w, dev)
+            calls.append((dw, db, dx, y, m, n, k))
+            hip.gemm_bf16_tile(dw, db, dx, y1, m, n, k, tile)
+        expected.append(exp)
+        singles.append(y1)
+    plan = hip.GemmPlan(calls)
+    try:
+        assert plan.flops == sum(2.0 * c[-3] * c[-2] * c[-1] for c in calls)
+        first = None
+        for _ in range(3):  # later launches rewrite the same outputs
+            plan.launch()
+            torch.cuda.synchronize()
+            got = [words(c[5] if w8 else c[3]) for c in calls]
+            for g, e, y1 in zip(got, expected, singles):
+                check_close(g, e, what="gemm plan")
+                a, b1 = rc.bf16_values(g), rc.bf16_values(words(y1))
+                assert np.all(np.abs(a - b1) <= np.maximum(1.0 / 64, 0.01 * np.abs(b1)))
+            if first is None:
+                first = got
+            for g, f in zip(got, first):
+                np.testing.assert_array_equal(g, f)
+    finally:
+        plan.close()
+
+
+def test_gemm_plan_rejects_unsupported_descriptors(hip, dev):
+    q = to_dev(np.zeros((4, 70), np.int8), dev)
+    s = to_dev(np.zeros((4, 2), np.uint16), dev)
+    x = to_dev(np.zeros((2, 70), np.uint16), dev)
+    y = bf16_out((2, 4), dev)
+    with pytest.raises(hip.InferError):  # K % 64 != 0
+        hip.GemmPlan([(q, s, 64, None, x, y, 2, 4, 70)])
+    q64 = to_dev(np.zeros((4, 64), np.int8), dev)
+    x64 = to_dev(np.zeros((2, 64), np.uint16), dev)
+    w64 = to_dev(np.zeros((4, 64), np.uint16), dev)
+    with pytest.raises(hip.InferError):  # group size
+        hip.GemmPlan([(q64, s, 32, None, x64, y, 2, 4, 64)])
+    with pytest.raises(hip.InferError):  # one token is a GEMV
+        hip.GemmPlan([(q64, s, 64, None, x64, y, 1, 4, 64)])
+    with pytest.raises(hip.InferError):  # mixed weight types
+        hip.GemmPlan([(q64, s, 64, None, x64, y, 2, 4, 64), (w64, None, x64, y, 2, 4, 64)])
