@@ -185,3 +185,121 @@ def lm_head(e_bf16, h_bf16, threads: int = 0):
     if idx < 0:
         raise ValueError("in_features out of range")
     return out32, out16, int(idx)
+
+
+# --------------------------------------------------------- model oracle --
+# model_oracle.c: the non-Linear ops of cpu_ops.cpp and the CPU decode /
+# prefill order of qwen2.cpp (see model_oracle.h for the pinning).
+
+class _ModelConfig(ctypes.Structure):
+    _fields_ = [("layers", ctypes.c_int), ("hidden", ctypes.c_int),
+                ("heads", ctypes.c_int), ("kv_heads", ctypes.c_int),
+                ("inter", ctypes.c_int), ("vocab", ctypes.c_int),
+                ("max_seq", ctypes.c_int), ("eps", ctypes.c_float),
+                ("theta", ctypes.c_float), ("threads", ctypes.c_int)]
+
+
+class _ModelWeights(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_void_p) for name in (
+        "embed", "final_norm", "in_norm", "post_norm", "wq", "bq", "wk", "bk",
+        "wv", "bv", "wo", "wg", "wu", "wd")]
+
+
+def _model_lib():
+    lib = _load()
+    if not getattr(lib, "_model_ready", False):
+        p, i, f = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+        lib.orc_rms_norm.argtypes = [p, p, p, i, f]
+        lib.orc_rope.argtypes = [p, p, i, i, i, i, f]
+        lib.orc_attention_decode.argtypes = [p, p, p, p, i, i, i, i, i, i]
+        lib.orc_silu_mul.argtypes = [p, p, p, i]
+        lib.orc_model_create.argtypes = [p, p]
+        lib.orc_model_create.restype = p
+        lib.orc_model_destroy.argtypes = [p]
+        lib.orc_model_prefill.argtypes = [p, p, i, p]
+        lib.orc_model_prefill.restype = i
+        lib.orc_model_decode.argtypes = [p, i, i, p]
+        lib.orc_model_decode.restype = i
+        lib._model_ready = True
+    return lib
+
+
+def rms_norm(x, weight, eps: float) -> np.ndarray:
+    """cpu_ops.cpp:15-21."""
+    xx, w = _c(x, np.float32), _c(weight, np.float32)
+    out = np.empty_like(xx)
+    _model_lib().orc_rms_norm(_ptr(xx), _ptr(w), _ptr(out), xx.size, eps)
+    return out
+
+
+def rope(q, k, heads: int, kv_heads: int, head_dim: int, position: int,
+         theta: float):
+    """cpu_ops.cpp:33-56 (returns rotated copies)."""
+    qq, kk = _c(q, np.float32).copy(), _c(k, np.float32).copy()
+    _model_lib().orc_rope(_ptr(qq), _ptr(kk), heads, kv_heads, head_dim,
+                          position, theta)
+    return qq, kk
+
+
+def attention_decode(q, key_cache, value_cache, heads: int, kv_heads: int,
+                     head_dim: int, seq_len: int, max_seq: int,
+                     threads: int = 0) -> np.ndarray:
+    """cpu_ops.cpp:58-91; caches [kv_heads, max_seq, head_dim]."""
+    qq = _c(q, np.float32)
+    kc, vc = _c(key_cache, np.float32), _c(value_cache, np.float32)
+    out = np.empty(heads * head_dim, np.float32)
+    _model_lib().orc_attention_decode(_ptr(qq), _ptr(kc), _ptr(vc), _ptr(out),
+                                      heads, kv_heads, head_dim, seq_len,
+                                      max_seq, threads)
+    return out
+
+
+def silu_mul(gate, up) -> np.ndarray:
+    """cpu_ops.cpp:168-173."""
+    g, u = _c(gate, np.float32), _c(up, np.float32)
+    out = np.empty_like(g)
+    _model_lib().orc_silu_mul(_ptr(g), _ptr(u), _ptr(out), g.size)
+    return out
+
+
+class Model:
+    """The reference's CPU FP32 Qwen2 model (qwen2.cpp:376-494) on FP32
+    weights.  ``weights`` maps the names of orc_model_weights (embed,
+    final_norm, in_norm, post_norm, wq, bq, wk, bk, wv, bv, wo, wg, wu, wd)
+    to float32 arrays, the per-layer ones stacked over layers."""
+
+    def __init__(self, weights: dict, layers: int, hidden: int, heads: int,
+                 kv_heads: int, inter: int, vocab: int, max_seq: int,
+                 eps: float = 1e-6, theta: float = 1e6, threads: int = 0):
+        self._keep = {k: _c(v, np.float32) for k, v in weights.items()}
+        w = _ModelWeights(**{k: _ptr(v) for k, v in self._keep.items()})
+        c = _ModelConfig(layers, hidden, heads, kv_heads, inter, vocab, max_seq,
+                         eps, theta, threads)
+        self.vocab = vocab
+        self._handle = _model_lib().orc_model_create(ctypes.byref(c), ctypes.byref(w))
+        if not self._handle:
+            raise ValueError("bad model shape or out of memory")
+
+    def prefill(self, tokens, logits: bool = False):
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.empty(self.vocab, np.float32) if logits else None
+        idx = _model_lib().orc_model_prefill(self._handle, _ptr(t), t.size, _ptr(out))
+        if idx < 0:
+            raise ValueError("bad prefill input")
+        return (idx, out) if logits else idx
+
+    def decode(self, token: int, position: int, logits: bool = False):
+        out = np.empty(self.vocab, np.float32) if logits else None
+        idx = _model_lib().orc_model_decode(self._handle, int(token), int(position),
+                                            _ptr(out))
+        if idx < 0:
+            raise ValueError("bad decode input")
+        return (idx, out) if logits else idx
+
+    def close(self):
+        if self._handle:
+            _model_lib().orc_model_destroy(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        self.close()
