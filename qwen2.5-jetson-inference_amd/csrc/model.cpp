@@ -1,0 +1,730 @@
+// Qwen2 decode runtime on the HIP Linear path: the device-side orchestration
+// of Qwen2Model's BF16 / W8A16 prefill and decode (src/qwen2.cpp:496-743,
+// Greedy-cy/qwen2.5-jetson-inference) behind the C ABI of infer_model.h.
+//
+// Memory: one device arena per model holds the decode state, the
+// activations, the prefill workspace (max_sequence_length rows), the RoPE
+// table, the attention partials, the grouped-GEMV descriptor tables and the
+// KV cache; it is allocated once at creation, and no prefill or decode call
+// allocates.
+//
+// Decode step (one token, position and token read from ModelState):
+//   embedding; per layer: RMSNorm -> q|k|v GEMV -> RoPE + KV store +
+//   attention -> o GEMV (+ residual) -> RMSNorm -> gate|up GEMV -> SiLU-mul
+//   -> down GEMV (+ residual); final RMSNorm -> LM head with argmax into
+//   ModelState.token -> advance (history, position).
+// The residual add rides on the GEMV's bias operand (bias = output = the
+// residual stream): each output element is read as bias and then written
+// by the same lane, so the aliasing is safe.  Under W8A16 the q|k|v and
+// gate|up GEMVs are one grouped launch each.  With use_graph the step is
+// captured once and replayed per token.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "infer_model.h"
+#include "linear_kernels.hpp"
+#include "model_kernels.hpp"
+#include "status.hpp"
+
+using namespace qlin;
+
+namespace {
+
+struct Linear {
+  const void* w = nullptr;
+  const uint16_t* s = nullptr;
+  const uint16_t* b = nullptr;
+  int n = 0;
+  int k = 0;
+};
+
+struct Layer {
+  const uint16_t* in_norm = nullptr;
+  const uint16_t* post_norm = nullptr;
+  Linear q, k, v, o, gate, up, down;
+  uint16_t* key_cache = nullptr;
+  uint16_t* value_cache = nullptr;
+  // W8A16 grouped-GEMV descriptor tables (device) and their block counts.
+  W8GroupDesc* qkv_table = nullptr;
+  W8GroupDesc* gate_up_table = nullptr;
+  int qkv_blocks = 0;
+  int gate_up_blocks = 0;
+};
+
+// Rows per block of the decode step's grouped GEMVs: one 4-row task per
+// wave, the most blocks a grouped launch can have.
+constexpr int kDecodeRowsPerBlock = 16;
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+double now_ms() {
+  return std::chrono::duration<double, std::milli>(
+             std::chrono::steady_clock::now().time_since_epoch())
+      .count();
+}
+
+}  // namespace
+
+struct infer_hip_model {
+  infer_hip_model_config cfg{};
+  bool w8 = false;
+  bool use_graph = false;
+  int max_seq = 0;
+  int head_dim = 0;
+  int kv_dim = 0;
+  int device = 0;
+  hipStream_t stream = nullptr;
+  char* arena = nullptr;
+  size_t arena_bytes = 0;
+  size_t kv_bytes = 0;
+  int* pinned = nullptr;  // host readback slot (hipHostMalloc)
+
+  ModelState* state = nullptr;
+  int* history = nullptr;
+  int* prompt = nullptr;
+  uint16_t *x = nullptr, *norm = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
+  uint16_t *attn = nullptr, *gate = nullptr, *up = nullptr, *mlp = nullptr, *logits = nullptr;
+  float* lm_value = nullptr;
+  int* lm_index = nullptr;
+  float2* rope = nullptr;
+  float* attn_partial = nullptr;
+  int* attn_counters = nullptr;
+  uint16_t *px = nullptr, *pnorm = nullptr, *pq = nullptr, *pk = nullptr, *pv = nullptr;
+  uint16_t *pattn = nullptr, *ptmp = nullptr, *pgate = nullptr, *pup = nullptr, *pmlp = nullptr;
+
+  const uint16_t* embed = nullptr;
+  const uint16_t* final_norm = nullptr;
+  const uint16_t* lm_head = nullptr;
+  std::vector<Layer> layers;
+
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t graph_exec = nullptr;
+
+  int position = 0;
+  bool has_prefilled = false;
+  int last_token = -1;
+};
+
+namespace {
+
+int hip_fail(hipError_t st, const char* what) {
+  return fail(INFER_HIP_RUNTIME_ERROR, "%s: %s", what, hipGetErrorString(st));
+}
+
+// Makes the model's device current for the duration of a call.
+class DeviceGuard {
+ public:
+  explicit DeviceGuard(int device) {
+    if (hipGetDevice(&prev_) == hipSuccess && prev_ != device) {
+      if (hipSetDevice(device) == hipSuccess) restore_ = true;
+    }
+  }
+  ~DeviceGuard() {
+    if (restore_) (void)hipSetDevice(prev_);
+  }
+
+ private:
+  int prev_ = 0;
+  bool restore_ = false;
+};
+
+// One token's GEMV (decode): W8A16 or BF16 fast path.
+void gemv(const infer_hip_model* m, const Linear& l, const uint16_t* bias, const uint16_t* x,
+          uint16_t* y) {
+  if (m->w8) {
+    launch_w8a16_gemv_fast({static_cast<const int8_t*>(l.w), l.s, bias, x, y, l.n, l.k},
+                           m->stream);
+  } else {
+    launch_bf16_gemv_fast({static_cast<const uint16_t*>(l.w), bias, x, y, l.n, l.k}, m->stream);
+  }
+}
+
+// token_count tokens (prefill): MFMA GEMM where it applies, the GEMV for
+// one token, the exact generic kernel otherwise (src/qwen2.cpp:300-330).
+void linear_batch(const infer_hip_model* m, const Linear& l, const uint16_t* x, uint16_t* y,
+                  int tokens) {
+  if (tokens == 1) {
+    gemv(m, l, l.b, x, y);
+  } else if (gemm_mfma_supported(l.w, x, tokens, l.n, l.k)) {
+    launch_gemm_mfma(gemm_pick_tile(tokens, l.n), m->w8,
+                     GemmArgs{l.w, l.s, l.b, x, y, tokens, l.n, l.k}, m->stream);
+  } else if (m->w8) {
+    launch_w8a16_linear_generic(static_cast<const int8_t*>(l.w), l.s, 64, l.b, x, y, tokens, l.n,
+                                l.k, m->stream);
+  } else {
+    launch_bf16_linear_generic(static_cast<const uint16_t*>(l.w), l.b, x, y, tokens, l.n, l.k,
+                               m->stream);
+  }
+}
+
+// Final RMSNorm of `row` and the LM head with its argmax into state->token.
+int lm_head_step(infer_hip_model* m, const uint16_t* row) {
+  const infer_hip_model_config& c = m->cfg;
+  launch_rms_norm(row, m->final_norm, m->norm, 1, c.hidden_size, c.rms_norm_eps, m->stream);
+  return infer_hip_lm_head_bf16(m->lm_head, nullptr, m->norm, m->logits, m->lm_value,
+                                m->lm_index, &m->state->token, c.vocab_size, c.hidden_size,
+                                m->stream);
+}
+
+// Enqueue one decode step (src/qwen2.cpp:597-674) on the model's stream.
+int enqueue_decode_step(infer_hip_model* m) {
+  const infer_hip_model_config& c = m->cfg;
+  const int hidden = c.hidden_size;
+  hipStream_t s = m->stream;
+  launch_embedding(m->embed, &m->state->token, 1, c.vocab_size, hidden, m->x, s);
+  for (const Layer& L : m->layers) {
+    launch_rms_norm(m->x, L.in_norm, m->norm, 1, hidden, c.rms_norm_eps, s);
+    if (m->w8) {
+      launch_w8a16_gemv_grouped(L.qkv_table, 3, L.qkv_blocks, s);
+    } else {
+      gemv(m, L.q, L.q.b, m->norm, m->q);
+      gemv(m, L.k, L.k.b, m->norm, m->k);
+      gemv(m, L.v, L.v.b, m->norm, m->v);
+    }
+    launch_attention_decode(m->q, m->k, m->v, L.key_cache, L.value_cache, m->rope, m->state,
+                            c.num_heads, c.num_kv_heads, m->head_dim, m->max_seq,
+                            m->attn_partial, m->attn_counters, m->attn, s);
+    gemv(m, L.o, m->x, m->attn, m->x);  // x = bf16(Wo attn + x)
+    launch_rms_norm(m->x, L.post_norm, m->norm, 1, hidden, c.rms_norm_eps, s);
+    if (m->w8) {
+      launch_w8a16_gemv_grouped(L.gate_up_table, 2, L.gate_up_blocks, s);
+    } else {
+      gemv(m, L.gate, nullptr, m->norm, m->gate);
+      gemv(m, L.up, nullptr, m->norm, m->up);
+    }
+    launch_silu_mul(m->gate, m->up, m->mlp, c.intermediate_size, s);
+    gemv(m, L.down, m->x, m->mlp, m->x);  // x = bf16(Wd mlp + x)
+  }
+  int rc = check_launch("decode step");
+  if (rc != INFER_HIP_OK) return rc;
+  rc = lm_head_step(m, m->x);
+  if (rc != INFER_HIP_OK) return rc;
+  launch_advance(m->state, m->history, m->max_seq, s);
+  return check_launch("decode step advance");
+}
+
+int ensure_graph(infer_hip_model* m) {
+  if (m->graph_exec) return ok();
+  hipError_t st = hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal);
+  if (st != hipSuccess) return hip_fail(st, "decode graph capture");
+  const int rc = enqueue_decode_step(m);
+  hipGraph_t graph = nullptr;
+  st = hipStreamEndCapture(m->stream, &graph);
+  if (rc != INFER_HIP_OK) {
+    if (graph) (void)hipGraphDestroy(graph);
+    return rc;
+  }
+  if (st != hipSuccess) return hip_fail(st, "decode graph capture");
+  hipGraphExec_t exec = nullptr;
+  st = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  if (st != hipSuccess) {
+    (void)hipGraphDestroy(graph);
+    return hip_fail(st, "decode graph instantiate");
+  }
+  m->graph = graph;
+  m->graph_exec = exec;
+  return ok();
+}
+
+int run_decode_step(infer_hip_model* m) {
+  if (m->use_graph) {
+    const hipError_t st = hipGraphLaunch(m->graph_exec, m->stream);
+    return st == hipSuccess ? ok() : hip_fail(st, "decode graph launch");
+  }
+  return enqueue_decode_step(m);
+}
+
+int read_token(infer_hip_model* m, int* out) {
+  hipError_t st = hipMemcpyAsync(m->pinned, &m->state->token, sizeof(int),
+                                 hipMemcpyDeviceToHost, m->stream);
+  if (st == hipSuccess) st = hipStreamSynchronize(m->stream);
+  if (st != hipSuccess) return hip_fail(st, "token readback");
+  *out = *m->pinned;
+  return ok();
+}
+
+// src/qwen2.cpp:496-595 on the model's stream; returns the argmax.
+int run_prefill(infer_hip_model* m, const int* tokens, int count, int* next) {
+  const infer_hip_model_config& c = m->cfg;
+  const int hidden = c.hidden_size, inter = c.intermediate_size;
+  hipStream_t s = m->stream;
+  hipError_t st = hipMemcpyAsync(m->prompt, tokens, sizeof(int) * count, hipMemcpyHostToDevice, s);
+  if (st != hipSuccess) return hip_fail(st, "prefill token upload");
+  launch_embedding(m->embed, m->prompt, count, c.vocab_size, hidden, m->px, s);
+  const long long rows_h = static_cast<long long>(count) * hidden;
+  for (const Layer& L : m->layers) {
+    launch_rms_norm(m->px, L.in_norm, m->pnorm, count, hidden, c.rms_norm_eps, s);
+    linear_batch(m, L.q, m->pnorm, m->pq, count);
+    linear_batch(m, L.k, m->pnorm, m->pk, count);
+    linear_batch(m, L.v, m->pnorm, m->pv, count);
+    launch_rope_store(m->pq, m->pk, m->pv, L.key_cache, L.value_cache, m->rope, count, 0,
+                      c.num_heads, c.num_kv_heads, m->head_dim, m->max_seq, s);
+    launch_attention_prefill(m->pq, L.key_cache, L.value_cache, m->pattn, count, c.num_heads,
+                             c.num_kv_heads, m->head_dim, m->max_seq, s);
+    linear_batch(m, L.o, m->pattn, m->ptmp, count);
+    launch_add(m->px, m->ptmp, rows_h, s);
+    launch_rms_norm(m->px, L.post_norm, m->pnorm, count, hidden, c.rms_norm_eps, s);
+    linear_batch(m, L.gate, m->pnorm, m->pgate, count);
+    linear_batch(m, L.up, m->pnorm, m->pup, count);
+    launch_silu_mul(m->pgate, m->pup, m->pmlp, static_cast<long long>(count) * inter, s);
+    linear_batch(m, L.down, m->pmlp, m->ptmp, count);
+    launch_add(m->px, m->ptmp, rows_h, s);
+  }
+  int rc = check_launch("prefill");
+  if (rc != INFER_HIP_OK) return rc;
+  rc = lm_head_step(m, m->px + static_cast<size_t>(count - 1) * hidden);
+  if (rc != INFER_HIP_OK) return rc;
+  launch_set_state(m->state, -1, count, 0, s);
+  rc = check_launch("prefill state");
+  if (rc != INFER_HIP_OK) return rc;
+  return read_token(m, next);
+}
+
+int check_linear(const infer_hip_linear& l, bool w8, bool want_bias, int n, int k, int layer,
+                 const char* name) {
+  if (!l.weight || (w8 && !l.scales)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "model: layer %d %s: null weight or scales", layer,
+                name);
+  }
+  if (!want_bias && l.bias) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "model: layer %d %s takes no bias", layer, name);
+  }
+  // The fast GEMV paths: K a multiple of 64 (W8A16) or 8 (BF16), 16-byte
+  // aligned weight (activations are arena buffers, 256-byte aligned).
+  const int k_align = w8 ? 64 : 8;
+  const bool fast = k >= k_align && k % k_align == 0 && aligned16(l.weight);
+  if (!fast || (l.bias && !aligned16(l.bias)) || (l.scales && !aligned16(l.scales))) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "model: layer %d %s [%d, %d]: needs 16-byte aligned tensors and in_features %% "
+                "%d == 0",
+                layer, name, n, k, k_align);
+  }
+  return ok();
+}
+
+void destroy_model(infer_hip_model* m) {
+  if (!m) return;
+  DeviceGuard guard(m->device);
+  if (m->graph_exec) (void)hipGraphExecDestroy(m->graph_exec);
+  if (m->graph) (void)hipGraphDestroy(m->graph);
+  if (m->stream) (void)hipStreamSynchronize(m->stream);
+  if (m->arena) (void)hipFree(m->arena);
+  if (m->pinned) (void)hipHostFree(m->pinned);
+  if (m->stream) (void)hipStreamDestroy(m->stream);
+  delete m;
+}
+
+}  // namespace
+
+extern "C" int infer_hip_model_create(const infer_hip_model_config* config,
+                                      const infer_hip_model_weights* weights,
+                                      const infer_hip_runtime_options* options,
+                                      infer_hip_model** out) {
+  if (!out) return fail(INFER_HIP_INVALID_ARGUMENT, "model: null output pointer");
+  *out = nullptr;
+  if (!config || !weights || !options || !weights->layers) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "model: null config, weights or options");
+  }
+  const infer_hip_model_config& c = *config;
+  // model_config.cpp:42-48 plus what the HIP kernels need.
+  if (c.hidden_size <= 0 || c.intermediate_size <= 0 || c.num_layers <= 0 || c.vocab_size <= 0) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "model: invalid model dimensions");
+  }
+  if (c.num_heads <= 0 || c.num_kv_heads <= 0 || c.num_heads % c.num_kv_heads != 0) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "model: invalid GQA head counts");
+  }
+  if (c.hidden_size % c.num_heads != 0) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "model: invalid attention head dimension");
+  }
+  const int head_dim = c.hidden_size / c.num_heads;
+  if (!attention_head_dim_supported(head_dim) ||
+      c.num_heads / c.num_kv_heads > kAttentionMaxGroup) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "model: head_dim %d / group %d unsupported (head_dim 64 or 128, heads per kv "
+                "head <= %d)",
+                head_dim, c.num_heads / c.num_kv_heads, kAttentionMaxGroup);
+  }
+  if (!(c.rms_norm_eps >= 0.0f) || !(c.rope_theta > 0.0f)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "model: invalid rms_norm_eps or rope_theta");
+  }
+  const int precision = options->precision;
+  if (precision != INFER_HIP_PRECISION_W16A16 && precision != INFER_HIP_PRECISION_W8A16) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "model: precision must be W16A16 or W8A16 (the FP32 path is the CPU's)");
+  }
+  const int max_seq = options->max_sequence_length;
+  if (max_seq <= 0) return fail(INFER_HIP_INVALID_ARGUMENT, "model: max_sequence_length <= 0");
+  const bool w8 = precision == INFER_HIP_PRECISION_W8A16;
+  const int hidden = c.hidden_size, inter = c.intermediate_size;
+  const int kv_dim = c.num_kv_heads * head_dim;
+
+  if (!weights->embed_tokens || !weights->norm) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "model: null embedding or final norm");
+  }
+  const uint16_t* lm_head = weights->lm_head ? weights->lm_head : weights->embed_tokens;
+  if (!aligned16(lm_head) || !aligned16(weights->embed_tokens) || hidden % 8 != 0) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "model: embedding / LM head need 16-byte alignment and hidden %% 8 == 0");
+  }
+  for (int l = 0; l < c.num_layers; ++l) {
+    const infer_hip_layer_weights& L = weights->layers[l];
+    if (!L.input_layernorm || !L.post_attention_layernorm) {
+      return fail(INFER_HIP_INVALID_ARGUMENT, "model: layer %d: null norm weight", l);
+    }
+    int rc = check_linear(L.q_proj, w8, true, hidden, hidden, l, "q_proj");
+    if (rc == INFER_HIP_OK) rc = check_linear(L.k_proj, w8, true, kv_dim, hidden, l, "k_proj");
+    if (rc == INFER_HIP_OK) rc = check_linear(L.v_proj, w8, true, kv_dim, hidden, l, "v_proj");
+    if (rc == INFER_HIP_OK) rc = check_linear(L.o_proj, w8, false, hidden, hidden, l, "o_proj");
+    if (rc == INFER_HIP_OK) {
+      rc = check_linear(L.gate_proj, w8, false, inter, hidden, l, "gate_proj");
+    }
+    if (rc == INFER_HIP_OK) rc = check_linear(L.up_proj, w8, false, inter, hidden, l, "up_proj");
+    if (rc == INFER_HIP_OK) {
+      rc = check_linear(L.down_proj, w8, false, hidden, inter, l, "down_proj");
+    }
+    if (rc != INFER_HIP_OK) return rc;
+  }
+
+  auto* m = new (std::nothrow) infer_hip_model();
+  if (!m) return fail(INFER_HIP_RUNTIME_ERROR, "model: out of host memory");
+  m->cfg = c;
+  m->w8 = w8;
+  m->use_graph = options->use_graph != 0;
+  m->max_seq = max_seq;
+  m->head_dim = head_dim;
+  m->kv_dim = kv_dim;
+  m->embed = weights->embed_tokens;
+  m->final_norm = weights->norm;
+  m->lm_head = lm_head;
+
+  // Arena layout.
+  size_t cursor = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = cursor;
+    cursor = align_up(cursor + bytes);
+    return at;
+  };
+  const size_t lm_entries = infer_hip_lm_head_workspace_entries(c.vocab_size, hidden);
+  const size_t ms = static_cast<size_t>(max_seq);
+  const size_t o_state = take(sizeof(ModelState));
+  const size_t o_history = take(sizeof(int) * ms);
+  const size_t o_prompt = take(sizeof(int) * ms);
+  const size_t o_x = take(2 * hidden), o_norm = take(2 * hidden), o_q = take(2 * hidden);
+  const size_t o_k = take(2 * kv_dim), o_v = take(2 * kv_dim), o_attn = take(2 * hidden);
+  const size_t o_gate = take(2 * inter), o_up = take(2 * inter), o_mlp = take(2 * inter);
+  const size_t o_logits = take(2 * static_cast<size_t>(c.vocab_size));
+  const size_t o_lmv = take(sizeof(float) * lm_entries), o_lmi = take(sizeof(int) * lm_entries);
+  const size_t o_rope = take(sizeof(float2) * ms * (head_dim / 2));
+  const size_t o_partial =
+      take(sizeof(float) * attention_decode_partial_floats(c.num_kv_heads, head_dim, max_seq));
+  const size_t o_counters = take(sizeof(int) * c.num_kv_heads);
+  const size_t o_px = take(2 * ms * hidden), o_pnorm = take(2 * ms * hidden);
+  const size_t o_pq = take(2 * ms * hidden), o_pk = take(2 * ms * kv_dim);
+  const size_t o_pv = take(2 * ms * kv_dim), o_pattn = take(2 * ms * hidden);
+  const size_t o_ptmp = take(2 * ms * hidden), o_pgate = take(2 * ms * inter);
+  const size_t o_pup = take(2 * ms * inter), o_pmlp = take(2 * ms * inter);
+  const size_t o_tables = take(sizeof(W8GroupDesc) * 5 * c.num_layers);
+  // One layer's K and V caches, in BF16 elements: [k|v][kv_head][max_seq][head_dim].
+  const size_t kv_layer = 2 * static_cast<size_t>(c.num_kv_heads) * ms * head_dim;
+  const size_t o_kv = take(2 * kv_layer * c.num_layers);  // bytes
+  m->arena_bytes = cursor;
+  m->kv_bytes = 2 * kv_layer * c.num_layers;
+
+  hipError_t st = hipGetDevice(&m->device);
+  if (st == hipSuccess) st = hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking);
+  if (st == hipSuccess) st = hipMalloc(reinterpret_cast<void**>(&m->arena), m->arena_bytes);
+  if (st == hipSuccess) st = hipMemset(m->arena, 0, m->arena_bytes);
+  if (st == hipSuccess) st = hipHostMalloc(reinterpret_cast<void**>(&m->pinned), sizeof(int));
+  if (st != hipSuccess) {
+    const int rc = hip_fail(st, "model allocation");
+    destroy_model(m);
+    return rc;
+  }
+  char* a = m->arena;
+  m->state = reinterpret_cast<ModelState*>(a + o_state);
+  m->history = reinterpret_cast<int*>(a + o_history);
+  m->prompt = reinterpret_cast<int*>(a + o_prompt);
+  auto bf = [&](size_t o) { return reinterpret_cast<uint16_t*>(a + o); };
+  m->x = bf(o_x); m->norm = bf(o_norm); m->q = bf(o_q); m->k = bf(o_k); m->v = bf(o_v);
+  m->attn = bf(o_attn); m->gate = bf(o_gate); m->up = bf(o_up); m->mlp = bf(o_mlp);
+  m->logits = bf(o_logits);
+  m->lm_value = reinterpret_cast<float*>(a + o_lmv);
+  m->lm_index = reinterpret_cast<int*>(a + o_lmi);
+  m->rope = reinterpret_cast<float2*>(a + o_rope);
+  m->attn_partial = reinterpret_cast<float*>(a + o_partial);
+  m->attn_counters = reinterpret_cast<int*>(a + o_counters);
+  m->px = bf(o_px); m->pnorm = bf(o_pnorm); m->pq = bf(o_pq); m->pk = bf(o_pk); m->pv = bf(o_pv);
+  m->pattn = bf(o_pattn); m->ptmp = bf(o_ptmp); m->pgate = bf(o_pgate); m->pup = bf(o_pup);
+  m->pmlp = bf(o_pmlp);
+  W8GroupDesc* tables = reinterpret_cast<W8GroupDesc*>(a + o_tables);
+  uint16_t* kv = bf(o_kv);
+
+  // RoPE table: (cos, sin) of position * theta^(-2 i / head_dim) in FP32,
+  // the CPU path's arithmetic (src/cpu_ops.cpp:38-41).
+  const int half = head_dim / 2;
+  std::vector<float2> rope(ms * half);
+  for (int p = 0; p < max_seq; ++p) {
+    for (int i = 0; i < half; ++i) {
+      const float frequency = std::pow(c.rope_theta, -2.0f * static_cast<float>(i) / head_dim);
+      const float angle = static_cast<float>(p) * frequency;
+      rope[static_cast<size_t>(p) * half + i] = make_float2(std::cos(angle), std::sin(angle));
+    }
+  }
+  st = hipMemcpy(m->rope, rope.data(), sizeof(float2) * rope.size(), hipMemcpyHostToDevice);
+
+  // Resolve every layer once; build the grouped-GEMV tables.
+  std::vector<W8GroupDesc> host_tables;
+  m->layers.resize(c.num_layers);
+  for (int l = 0; l < c.num_layers && st == hipSuccess; ++l) {
+    const infer_hip_layer_weights& W = weights->layers[l];
+    Layer& L = m->layers[l];
+    L.in_norm = W.input_layernorm;
+    L.post_norm = W.post_attention_layernorm;
+    auto lin = [](const infer_hip_linear& w, int n, int k) {
+      return Linear{w.weight, w.scales, w.bias, n, k};
+    };
+    L.q = lin(W.q_proj, hidden, hidden);
+    L.k = lin(W.k_proj, kv_dim, hidden);
+    L.v = lin(W.v_proj, kv_dim, hidden);
+    L.o = lin(W.o_proj, hidden, hidden);
+    L.gate = lin(W.gate_proj, inter, hidden);
+    L.up = lin(W.up_proj, inter, hidden);
+    L.down = lin(W.down_proj, hidden, inter);
+    L.key_cache = kv + kv_layer * l;
+    L.value_cache = L.key_cache + kv_layer / 2;
+    if (w8) {
+      auto desc = [&](const Linear& li, const uint16_t* x, uint16_t* y, int& blocks) {
+        W8GroupDesc d{static_cast<const int8_t*>(li.w), li.s, li.b, x, y, li.n, li.k, blocks,
+                      kDecodeRowsPerBlock};
+        blocks += (li.n + kDecodeRowsPerBlock - 1) / kDecodeRowsPerBlock;
+        return d;
+      };
+      L.qkv_table = tables + host_tables.size();
+      host_tables.push_back(desc(L.q, m->norm, m->q, L.qkv_blocks));
+      host_tables.push_back(desc(L.k, m->norm, m->k, L.qkv_blocks));
+      host_tables.push_back(desc(L.v, m->norm, m->v, L.qkv_blocks));
+      L.gate_up_table = tables + host_tables.size();
+      host_tables.push_back(desc(L.gate, m->norm, m->gate, L.gate_up_blocks));
+      host_tables.push_back(desc(L.up, m->norm, m->up, L.gate_up_blocks));
+    }
+  }
+  // Every region the kernels write must lie inside the arena.
+  const char* arena_end = m->arena + m->arena_bytes;
+  const bool inside =
+      reinterpret_cast<const char*>(m->layers.back().value_cache + kv_layer / 2) <= arena_end &&
+      reinterpret_cast<const char*>(tables + host_tables.size()) <= a + o_kv &&
+      reinterpret_cast<const char*>(m->pmlp + ms * inter) <= a + o_tables;
+  if (st == hipSuccess && !inside) {
+    destroy_model(m);
+    return fail(INFER_HIP_RUNTIME_ERROR, "model: internal arena layout overflow");
+  }
+  if (st == hipSuccess && !host_tables.empty()) {
+    st = hipMemcpy(tables, host_tables.data(), sizeof(W8GroupDesc) * host_tables.size(),
+                   hipMemcpyHostToDevice);
+  }
+  if (st != hipSuccess) {
+    const int rc = hip_fail(st, "model set-up");
+    destroy_model(m);
+    return rc;
+  }
+  if (m->use_graph) {
+    const int rc = ensure_graph(m);
+    if (rc != INFER_HIP_OK) {
+      destroy_model(m);
+      return rc;
+    }
+  }
+  *out = m;
+  return ok();
+}
+
+extern "C" int infer_hip_model_destroy(infer_hip_model* model) {
+  destroy_model(model);
+  return ok();
+}
+
+extern "C" int infer_hip_model_reset(infer_hip_model* m) {
+  if (!m) return fail(INFER_HIP_INVALID_ARGUMENT, "model: null model");
+  m->position = 0;
+  m->has_prefilled = false;
+  m->last_token = -1;
+  return ok();
+}
+
+extern "C" int infer_hip_model_prefill(infer_hip_model* m, const int* tokens, int count,
+                                       int* next_token) {
+  if (!m || !next_token) return fail(INFER_HIP_INVALID_ARGUMENT, "prefill: null argument");
+  if (!tokens || count <= 0) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "prompt must contain at least one token");
+  }
+  if (m->position != 0 || m->has_prefilled) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "prefill requires a fresh model state; call reset first");
+  }
+  if (count > m->max_seq) return fail(INFER_HIP_INVALID_ARGUMENT, "prompt exceeds KV cache capacity");
+  for (int i = 0; i < count; ++i) {
+    if (tokens[i] < 0 || tokens[i] >= m->cfg.vocab_size) {
+      return fail(INFER_HIP_INVALID_ARGUMENT, "input token out of range");
+    }
+  }
+  DeviceGuard guard(m->device);
+  const int rc = run_prefill(m, tokens, count, next_token);
+  if (rc != INFER_HIP_OK) return rc;
+  m->position = count;
+  m->has_prefilled = true;
+  m->last_token = *next_token;
+  return ok();
+}
+
+extern "C" int infer_hip_model_decode_next(infer_hip_model* m, int token, int* next_token) {
+  if (!m || !next_token) return fail(INFER_HIP_INVALID_ARGUMENT, "decode_next: null argument");
+  if (!m->has_prefilled) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "decode_next requires a successful prefill");
+  }
+  if (token < 0 || token >= m->cfg.vocab_size) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "input token out of range");
+  }
+  if (m->position >= m->max_seq) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "KV cache capacity exceeded");
+  }
+  DeviceGuard guard(m->device);
+  launch_set_state(m->state, token, m->position, 0, m->stream);
+  int rc = check_launch("decode state");
+  if (rc == INFER_HIP_OK) rc = run_decode_step(m);
+  if (rc == INFER_HIP_OK) rc = read_token(m, next_token);
+  if (rc != INFER_HIP_OK) return rc;
+  ++m->position;
+  m->last_token = *next_token;
+  return ok();
+}
+
+extern "C" int infer_hip_model_decode_steps(infer_hip_model* m, int steps, int* tokens_out) {
+  if (!m) return fail(INFER_HIP_INVALID_ARGUMENT, "decode_steps: null model");
+  if (!m->has_prefilled) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "decode_steps requires a successful prefill");
+  }
+  if (steps < 0 || m->position + static_cast<long long>(steps) > m->max_seq) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "KV cache capacity exceeded");
+  }
+  if (steps == 0) return ok();
+  DeviceGuard guard(m->device);
+  launch_set_state(m->state, m->last_token, m->position, 0, m->stream);
+  int rc = check_launch("decode state");
+  for (int i = 0; i < steps && rc == INFER_HIP_OK; ++i) rc = run_decode_step(m);
+  if (rc != INFER_HIP_OK) return rc;
+  hipError_t st = hipSuccess;
+  if (tokens_out) {
+    st = hipMemcpyAsync(tokens_out, m->history, sizeof(int) * steps, hipMemcpyDeviceToHost,
+                        m->stream);
+  }
+  if (st != hipSuccess) return hip_fail(st, "decode history readback");
+  int last = 0;
+  rc = read_token(m, &last);  // synchronizes
+  if (rc != INFER_HIP_OK) return rc;
+  m->position += steps;
+  m->last_token = last;
+  return ok();
+}
+
+extern "C" int infer_hip_model_generate(infer_hip_model* m, const int* prompt, int prompt_count,
+                                        int max_new_tokens, int stop_on_eos, int* tokens_out,
+                                        int* generated, infer_hip_generation_stats* stats) {
+  if (!m || !prompt || !generated || (max_new_tokens > 0 && !tokens_out)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "generate: null argument");
+  }
+  if (prompt_count <= 0) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "prompt must contain at least one token");
+  }
+  if (max_new_tokens < 0) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "max_new_tokens must be non-negative");
+  }
+  if (static_cast<long long>(prompt_count) + std::max(0, max_new_tokens - 1) > m->max_seq) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "prompt and generation exceed KV cache capacity");
+  }
+  *generated = 0;
+  infer_hip_model_reset(m);
+  const double t0 = now_ms();
+  int next = 0;
+  int rc = infer_hip_model_prefill(m, prompt, prompt_count, &next);
+  if (rc != INFER_HIP_OK) return rc;
+  const double t1 = now_ms();
+  int count = 0;
+  if (max_new_tokens > 0) tokens_out[count++] = next;
+  const int eos = m->cfg.eos_token_id;
+  // Without EOS stopping the whole decode is one host-sync-free run; with
+  // it, runs of kEosChunk steps are checked between runs (the steps after
+  // an EOS inside a run are discarded, and the position is set back).
+  constexpr int kEosChunk = 16;
+  bool stopped = stop_on_eos && count > 0 && tokens_out[count - 1] == eos;
+  while (count < max_new_tokens && !stopped) {
+    const int steps = stop_on_eos ? std::min(kEosChunk, max_new_tokens - count)
+                                  : max_new_tokens - count;
+    const int base_position = m->position;
+    rc = infer_hip_model_decode_steps(m, steps, tokens_out + count);
+    if (rc != INFER_HIP_OK) return rc;
+    if (stop_on_eos) {
+      for (int i = 0; i < steps; ++i) {
+        if (tokens_out[count + i] == eos) {
+          m->position = base_position + i + 1;
+          m->last_token = eos;
+          count += i + 1;
+          stopped = true;
+          break;
+        }
+      }
+    }
+    if (!stopped) count += steps;
+  }
+  const double t2 = now_ms();
+  *generated = count;
+  if (stats) {
+    stats->prompt_tokens = prompt_count;
+    stats->generated_tokens = count;
+    stats->ttft_ms = t1 - t0;
+    stats->decode_ms = t2 - t1;
+    stats->total_ms = t2 - t0;
+  }
+  return ok();
+}
+
+extern "C" int infer_hip_model_last_logits(infer_hip_model* m, float* logits) {
+  if (!m || !logits) return fail(INFER_HIP_INVALID_ARGUMENT, "last_logits: null argument");
+  DeviceGuard guard(m->device);
+  std::vector<uint16_t> bits(static_cast<size_t>(m->cfg.vocab_size));
+  hipError_t st = hipMemcpyAsync(bits.data(), m->logits, sizeof(uint16_t) * bits.size(),
+                                 hipMemcpyDeviceToHost, m->stream);
+  if (st == hipSuccess) st = hipStreamSynchronize(m->stream);
+  if (st != hipSuccess) return hip_fail(st, "logits readback");
+  for (size_t i = 0; i < bits.size(); ++i) {
+    const uint32_t word = static_cast<uint32_t>(bits[i]) << 16;
+    std::memcpy(logits + i, &word, sizeof(float));
+  }
+  return ok();
+}
+
+extern "C" int infer_hip_model_position(const infer_hip_model* m) { return m ? m->position : -1; }
+
+extern "C" int infer_hip_model_has_prefilled(const infer_hip_model* m) {
+  return m && m->has_prefilled ? 1 : 0;
+}
+
+extern "C" size_t infer_hip_model_kv_cache_bytes(const infer_hip_model* m) {
+  return m ? m->kv_bytes : 0;
+}
+
+extern "C" size_t infer_hip_model_workspace_bytes(const infer_hip_model* m) {
+  return m ? m->arena_bytes - m->kv_bytes : 0;
+}
+
+extern "C" hipStream_t infer_hip_model_stream(const infer_hip_model* m) {
+  return m ? m->stream : nullptr;
+}

@@ -1,0 +1,50 @@
+// Internal launch interface of the non-Linear decode/prefill kernels
+// (model_kernels.hip) used by the model runtime (model.cpp).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace qlin {
+
+// Decode state kept in device memory so that a decode step needs no host
+// input: `token` is the input of the next step (the LM head's argmax writes
+// it), `pos` that token's position, `step` the index of the next history
+// entry.
+struct ModelState {
+  int token;
+  int pos;
+  int step;
+  int pad;
+};
+
+// Head dimensions the attention kernels are built for.
+bool attention_head_dim_supported(int head_dim);
+// Largest query-head group (heads / kv_heads) the decode attention handles.
+constexpr int kAttentionMaxGroup = 8;
+
+void launch_embedding(const uint16_t* table, const int* tokens, int count, int vocab, int hidden,
+                      uint16_t* out, hipStream_t stream);
+void launch_rms_norm(const uint16_t* x, const uint16_t* w, uint16_t* out, int rows, int hidden,
+                     float eps, hipStream_t stream);
+void launch_rope_store(uint16_t* q, uint16_t* k, const uint16_t* v, uint16_t* key_cache,
+                       uint16_t* value_cache, const float2* rope, int count, int start,
+                       int heads, int kv_heads, int head_dim, int max_seq, hipStream_t stream);
+int attention_decode_chunks(int max_seq);
+size_t attention_decode_partial_floats(int kv_heads, int head_dim, int max_seq);
+void launch_attention_decode(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                             uint16_t* key_cache, uint16_t* value_cache, const float2* rope,
+                             const ModelState* state, int heads, int kv_heads, int head_dim,
+                             int max_seq, float* partial, int* counters, uint16_t* out,
+                             hipStream_t stream);
+void launch_attention_prefill(const uint16_t* q, const uint16_t* key_cache,
+                              const uint16_t* value_cache, uint16_t* out, int count, int heads,
+                              int kv_heads, int head_dim, int max_seq, hipStream_t stream);
+void launch_silu_mul(const uint16_t* gate, const uint16_t* up, uint16_t* out, long long n,
+                     hipStream_t stream);
+void launch_add(uint16_t* x, const uint16_t* y, long long n, hipStream_t stream);
+void launch_set_state(ModelState* state, int token, int pos, int step, hipStream_t stream);
+void launch_advance(ModelState* state, int* history, int history_len, hipStream_t stream);
+
+}  // namespace qlin

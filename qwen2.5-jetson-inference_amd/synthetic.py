@@ -1,0 +1,164 @@
+"""Random-init Qwen2 weights in the archive's tensor layout (numpy, host).
+
+No checkpoint can be fetched here, so models are random-initialised with
+the architecture's shapes and stored as the reference's exporter would
+store them (tools/export_model.py, Greedy-cy/qwen2.5-jetson-inference):
+
+* tensor names as in the QWENBIN1 archive (``model.layers.<i>.self_attn.
+  q_proj.weight`` ...), the W8A16 scales as the sibling ``<name>.scale``
+  (export_model.py:299);
+* BF16 tensors as little-endian uint16 words, FP32 -> BF16 round to nearest
+  even with NaNs quieted (export_model.py:123-131);
+* W8A16 Linear weights (2-D tensors other than the embedding / LM head,
+  export_model.py:220-223) quantized per row in groups of 64 along K:
+  s = max|w| / 127 in FP32 (0 -> 1), q = clip(rint(w / s), -127, 127) with
+  the FP32 s, scale stored as BF16 (export_model.py:226-247, 288-289).
+"""
+from __future__ import annotations
+
+import dataclasses
+
+import numpy as np
+
+
+@dataclasses.dataclass(frozen=True)
+class ModelConfig:
+    """include/infer/model_config.hpp:7-20."""
+    hidden_size: int
+    intermediate_size: int
+    num_layers: int
+    num_heads: int
+    num_kv_heads: int
+    vocab_size: int
+    eos_token_id: int = -1
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 1e6
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden_size // self.num_heads
+
+    @property
+    def kv_dim(self) -> int:
+        return self.num_kv_heads * self.head_dim
+
+
+# Qwen2.5-0.5B(-Instruct): the model every BASELINE configuration uses.
+QWEN25_0_5B = ModelConfig(hidden_size=896, intermediate_size=4864, num_layers=24,
+                          num_heads=14, num_kv_heads=2, vocab_size=151936,
+                          eos_token_id=151645, rms_norm_eps=1e-6, rope_theta=1e6)
+
+LINEARS = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+           "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")
+BIASED = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj")
+
+
+def float32_to_bf16_bits(a: np.ndarray) -> np.ndarray:
+    """FP32 -> BF16 words, round to nearest even, NaN quieted."""
+    v = np.ascontiguousarray(a, dtype=np.float32)
+    bits = v.view(np.uint32)
+    out = ((bits + (np.uint32(0x7FFF) + ((bits >> 16) & np.uint32(1)))) >> 16).astype(np.uint16)
+    nan = np.isnan(v)
+    if np.any(nan):
+        out[nan] = ((bits[nan] >> 16) | np.uint32(0x0040)).astype(np.uint16)
+    return out
+
+
+def bf16_bits_to_float32(a: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(a, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def quantize_groupwise(w: np.ndarray, group_size: int = 64):
+    """Symmetric per-row group quantization; returns (int8 q, FP32 scales
+    [rows, ceil(cols / group_size)]).  The last group may be short."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, cols = w.shape
+    groups = (cols + group_size - 1) // group_size
+    q = np.empty((rows, cols), np.int8)
+    scales = np.empty((rows, groups), np.float32)
+    full = cols // group_size
+    spans = []
+    if full:
+        spans.append((0, full * group_size, full))
+    if cols % group_size:
+        spans.append((full * group_size, cols, 1))
+    g0 = 0
+    for begin, end, count in spans:
+        blocks = w[:, begin:end].reshape(rows, count, -1)
+        s = (np.abs(blocks).max(axis=2) / np.float32(127.0)).astype(np.float32)
+        s = np.where(s == 0.0, np.float32(1.0), s).astype(np.float32)
+        q[:, begin:end] = np.clip(np.rint(blocks / s[:, :, None]), -127, 127).astype(
+            np.int8).reshape(rows, end - begin)
+        scales[:, g0:g0 + count] = s
+        g0 += count
+    return q, scales
+
+
+def linear_shapes(c: ModelConfig):
+    h, i, kv = c.hidden_size, c.intermediate_size, c.kv_dim
+    return {"self_attn.q_proj": (h, h), "self_attn.k_proj": (kv, h),
+            "self_attn.v_proj": (kv, h), "self_attn.o_proj": (h, h),
+            "mlp.gate_proj": (i, h), "mlp.up_proj": (i, h), "mlp.down_proj": (h, i)}
+
+
+def random_model(c: ModelConfig, precision: str = "w8a16", seed: int = 4,
+                 std: float = 0.02) -> dict:
+    """Random-init tensors by archive name: Linear weights, biases and the
+    embedding ~ N(0, std), norm weights 1 + N(0, std); W8A16 quantizes the
+    Linear weights as the exporter does, W16A16 stores them as BF16."""
+    if precision not in ("w8a16", "w16a16"):
+        raise ValueError("precision must be w8a16 or w16a16")
+    rng = np.random.default_rng(seed)
+
+    def normal(*shape):
+        return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std))
+
+    t = {"model.embed_tokens.weight": float32_to_bf16_bits(normal(c.vocab_size, c.hidden_size)),
+         "model.norm.weight": float32_to_bf16_bits(1 + normal(c.hidden_size))}
+    shapes = linear_shapes(c)
+    for layer in range(c.num_layers):
+        p = f"model.layers.{layer}."
+        t[p + "input_layernorm.weight"] = float32_to_bf16_bits(1 + normal(c.hidden_size))
+        t[p + "post_attention_layernorm.weight"] = float32_to_bf16_bits(1 + normal(c.hidden_size))
+        for name in LINEARS:
+            w = normal(*shapes[name])
+            if precision == "w8a16":
+                q, s = quantize_groupwise(w)
+                t[p + name + ".weight"] = q
+                t[p + name + ".weight.scale"] = float32_to_bf16_bits(s)
+            else:
+                t[p + name + ".weight"] = float32_to_bf16_bits(w)
+            if name in BIASED:
+                t[p + name + ".bias"] = float32_to_bf16_bits(normal(shapes[name][0]))
+    return t
+
+
+def dequantized_fp32(t: dict, c: ModelConfig) -> dict:
+    """The FP32 weights the model computes with (q * bf16 scale, exact in
+    FP32; BF16 tensors widened), layer-stacked for a CPU FP32 model."""
+    def f(name):
+        return bf16_bits_to_float32(t[name])
+
+    def linear(name):
+        w = t[name + ".weight"]
+        if w.dtype == np.int8:
+            s = bf16_bits_to_float32(t[name + ".weight.scale"])
+            return (w.reshape(w.shape[0], -1, 64).astype(np.float32) * s[:, :, None]).reshape(
+                w.shape)
+        return bf16_bits_to_float32(w)
+
+    L = c.num_layers
+    out = {"embed": f("model.embed_tokens.weight").reshape(c.vocab_size, c.hidden_size),
+           "final_norm": f("model.norm.weight")}
+    key = {"self_attn.q_proj": "wq", "self_attn.k_proj": "wk", "self_attn.v_proj": "wv",
+           "self_attn.o_proj": "wo", "mlp.gate_proj": "wg", "mlp.up_proj": "wu",
+           "mlp.down_proj": "wd"}
+    out["in_norm"] = np.stack([f(f"model.layers.{i}.input_layernorm.weight") for i in range(L)])
+    out["post_norm"] = np.stack(
+        [f(f"model.layers.{i}.post_attention_layernorm.weight") for i in range(L)])
+    for name, k in key.items():
+        out[k] = np.stack([linear(f"model.layers.{i}.{name}") for i in range(L)])
+    for name, k in (("self_attn.q_proj", "bq"), ("self_attn.k_proj", "bk"),
+                    ("self_attn.v_proj", "bv")):
+        out[k] = np.stack([f(f"model.layers.{i}.{name}.bias") for i in range(L)])
+    return out

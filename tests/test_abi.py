@@ -83,3 +83,73 @@ def test_lm_head_workspace_never_exceeds_reference_sizing(hip, vocab, k):
 
 def test_lm_head_workspace_invalid_shape(hip):
     assert hip.lm_head_workspace_entries(0, 896) == 0
+
+
+# ------------------------------------------------------ model runtime ABI --
+
+def _declared_model_symbols():
+    text = open(os.path.join(ROOT, "include", "infer_model.h")).read()
+    return sorted(set(re.findall(r"\b(infer_hip_model_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_model_symbol(hip):
+    import model_hip
+    lib = model_hip.load()
+    declared = _declared_model_symbols()
+    assert declared
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert sorted(model_hip.EXPORTED_SYMBOLS) == declared
+
+
+def _create(cfg_fields, precision=2, max_seq=16, layers=None):
+    import ctypes
+    import model_hip
+    lib = model_hip.load()
+    cfg = model_hip._Config(*cfg_fields)
+    lay = layers if layers is not None else (model_hip._Layer * max(1, cfg_fields[2]))()
+    w = model_hip._Weights(None, None, None, lay)
+    opts = model_hip._Options(precision, max_seq, 0)
+    h = ctypes.c_void_p()
+    return lib.infer_hip_model_create(ctypes.byref(cfg), ctypes.byref(w), ctypes.byref(opts),
+                                      ctypes.byref(h)), h
+
+
+@pytest.mark.parametrize("fields,why", [
+    ((896, 4864, 0, 14, 2, 151936, -1, 1e-6, 1e6), "invalid model dimensions"),
+    ((896, 4864, 24, 14, 3, 151936, -1, 1e-6, 1e6), "invalid GQA head counts"),
+    ((900, 4864, 24, 14, 2, 151936, -1, 1e-6, 1e6), "invalid attention head dimension"),
+    ((128, 256, 1, 4, 1, 64, -1, 1e-6, 1e6), "head_dim 32"),
+    ((2048, 256, 1, 32, 2, 64, -1, 1e-6, 1e6), "group 16"),
+    ((896, 4864, 24, 14, 2, 151936, -1, 1e-6, 0.0), "rope_theta"),
+])
+def test_model_create_rejects_bad_config_on_host(hip, fields, why):
+    # model_config.cpp:42-48 plus the shapes the HIP kernels support; all
+    # rejected before any HIP call.
+    rc, h = _create(fields)
+    assert rc == hip.INVALID_ARGUMENT and not h.value
+    assert why in hip.load().infer_hip_last_error().decode()
+
+
+def test_model_create_rejects_precision_and_missing_weights(hip):
+    fields = (128, 256, 1, 2, 1, 64, -1, 1e-6, 1e6)
+    rc, _ = _create(fields, precision=0)
+    assert rc == hip.INVALID_ARGUMENT
+    assert "precision" in hip.load().infer_hip_last_error().decode()
+    rc, _ = _create(fields, max_seq=0)
+    assert rc == hip.INVALID_ARGUMENT
+    rc, _ = _create(fields)
+    assert rc == hip.INVALID_ARGUMENT
+    assert "null embedding" in hip.load().infer_hip_last_error().decode()
+
+
+def test_model_null_handles_are_rejected(hip):
+    import ctypes
+    import model_hip
+    lib = model_hip.load()
+    out = ctypes.c_int()
+    assert lib.infer_hip_model_prefill(None, None, 0, ctypes.byref(out)) == hip.INVALID_ARGUMENT
+    assert lib.infer_hip_model_decode_next(None, 0, ctypes.byref(out)) == hip.INVALID_ARGUMENT
+    assert lib.infer_hip_model_decode_steps(None, 1, None) == hip.INVALID_ARGUMENT
+    assert lib.infer_hip_model_position(None) == -1
+    assert lib.infer_hip_model_destroy(None) == hip.OK
