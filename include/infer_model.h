@@ -103,8 +103,8 @@ typedef struct infer_hip_generation_stats {
 typedef struct infer_hip_model infer_hip_model;
 
 /* Qwen2Model::Qwen2Model (src/qwen2.cpp:30-54, workspace 80-199): validates the shapes
- * (head_dim 64 or 128, heads / kv_heads <= 8, K % 64 == 0 and 16-byte
- * aligned weights for the fast Linear paths), allocates the KV cache
+ * (head_dim 64 or 128, at most 32 query heads, hidden <= 4096, K % 64 == 0
+ * and 16-byte aligned weights for the fast Linear paths), allocates the KV cache
  * (BF16 [layer][k|v][kv_head][max_seq][head_dim]) and every workspace on
  * the current device, and creates the model's stream.  The weights are
  * borrowed and must outlive the model. */

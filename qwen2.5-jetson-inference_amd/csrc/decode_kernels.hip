@@ -1,0 +1,534 @@
+// Fused decode-step kernels for gfx950: the W8A16 GEMVs of a decode step with
+// the RMSNorm in front of them (and the SiLU-mul behind gate/up) folded in,
+// and the tied LM head with the final RMSNorm, the argmax and the step's
+// bookkeeping folded in.
+//
+// A decode step is latency-bound: every kernel starts on a cold L2 and each
+// dependent global round trip costs about a microsecond, so these kernels
+// are built to need one round trip: a wave issues its weight loads, then its
+// activation and norm-weight loads (all independent), and only then waits.
+// With K <= 1024 x SLABS, the 64 lanes of one wave hold the whole input
+// vector (lane l owns 16-element chunks l, l + 64, ...), so each wave
+// computes the RMSNorm of x by itself: no workgroup reduction, no extra
+// launch, no normalized copy in memory.
+//
+// Numerics follow the unfused ops exactly in kind (not in summation order):
+// the normalized activations are rounded to BF16 as rms_norm_bf16 stores
+// them (src/cuda/kernels.cu:64-116), gate and up are rounded to BF16 before
+// silu_mul (kernels.cu:302-324), the LM head argmax is over the FP32 sums
+// with ties to the lowest index (kernels.cu:492-603).
+#include <float.h>
+#include <limits.h>
+#include <stdint.h>
+
+#include "decode_kernels.hpp"
+#include "device_common.hpp"
+
+namespace qlin {
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kWaves = kBlock / kWave;
+
+// The 16-element activation chunks (lane l: chunk s * 64 + l of slab s) of
+// x and of the norm weight, and the wave's RMSNorm of x rounded to BF16.
+template <int SLABS>
+__device__ __forceinline__ void wave_rms_norm16(const uint16_t* x, const uint16_t* norm_w, int k,
+                                                float eps, int lane, float (&xn)[SLABS][16]) {
+  const int chunks = k >> 4;
+  float nw[SLABS][16];
+#pragma unroll
+  for (int s = 0; s < SLABS; ++s) {
+    const int c = s * kWave + lane;
+    if (c < chunks) {
+      load_x16(x + 16 * c, xn[s]);
+      load_x16(norm_w + 16 * c, nw[s]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) xn[s][e] = nw[s][e] = 0.0f;
+    }
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int s = 0; s < SLABS; ++s)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) ss = fmaf(xn[s][e], xn[s][e], ss);
+  ss = wave_sum(ss);
+  const float scale = 1.0f / sqrtf(ss / k + eps);
+#pragma unroll
+  for (int s = 0; s < SLABS; ++s)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) xn[s][e] = bf16_to_f32(f32_to_bf16(xn[s][e] * scale * nw[s][e]));
+}
+
+// Same for 8-element chunks (BF16 weights: one 16-byte chunk is 8 values).
+template <int SLABS>
+__device__ __forceinline__ void wave_rms_norm8(const uint16_t* x, const uint16_t* norm_w, int k,
+                                               float eps, int lane, float (&xn)[SLABS][8]) {
+  const int chunks = k >> 3;
+  float nw[SLABS][8];
+#pragma unroll
+  for (int s = 0; s < SLABS; ++s) {
+    const int c = s * kWave + lane;
+    if (c < chunks) {
+      load_x8(x + 8 * c, xn[s]);
+      load_x8(norm_w + 8 * c, nw[s]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xn[s][e] = nw[s][e] = 0.0f;
+    }
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int s = 0; s < SLABS; ++s)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = fmaf(xn[s][e], xn[s][e], ss);
+  ss = wave_sum(ss);
+  const float scale = 1.0f / sqrtf(ss / k + eps);
+#pragma unroll
+  for (int s = 0; s < SLABS; ++s)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xn[s][e] = bf16_to_f32(f32_to_bf16(xn[s][e] * scale * nw[s][e]));
+}
+
+// One row's int8 chunks and group scales (zeros past K or past the rows).
+template <int SLABS>
+__device__ __forceinline__ void load_w8_row(const int8_t* w, const uint16_t* s, int row, bool ok,
+                                            int k, int lane, uint4 (&wq)[SLABS],
+                                            uint32_t (&sc)[SLABS]) {
+  const int chunks = k >> 4, groups = k >> 6;
+#pragma unroll
+  for (int i = 0; i < SLABS; ++i) {
+    const int c = i * kWave + lane;
+    if (ok && c < chunks) {
+      wq[i] = load_stream16(w + static_cast<size_t>(row) * k + 16 * c);
+      sc[i] = gload(s + static_cast<size_t>(row) * groups + (c >> 2));
+    } else {
+      wq[i] = make_uint4(0, 0, 0, 0);
+      sc[i] = 0;
+    }
+  }
+}
+
+template <int SLABS>
+__device__ __forceinline__ float w8_row_dot(const uint4 (&wq)[SLABS], const uint32_t (&sc)[SLABS],
+                                            const float (&xn)[SLABS][16]) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < SLABS; ++i) acc = fmaf(dot16_i8(wq[i], xn[i]), bf16_to_f32(sc[i]), acc);
+  return wave_sum(acc);
+}
+
+// Descriptor of the workgroup: the last one whose block_begin <= b.
+__device__ __forceinline__ NormGemvDesc pick_desc(const NormGemvArgs& a, int b) {
+  NormGemvDesc d = a.d[0];
+  if (a.count > 1 && a.d[1].block_begin <= b) d = a.d[1];
+  if (a.count > 2 && a.d[2].block_begin <= b) d = a.d[2];
+  return d;
+}
+
+}  // namespace
+
+// y = bf16(W8A16(rms_norm(x)) + bias) for up to three GEMVs on the same
+// normalized input (q|k|v), or with PAIR mlp = bf16(silu(bf16(gate)) *
+// bf16(up)) from the gate (w, s) and up (w2, s2) rows of the same index.
+// Each wave computes one output row; four rows per workgroup.
+template <int SLABS, bool PAIR>
+__global__ __launch_bounds__(kBlock) void norm_gemv_w8_kernel(NormGemvArgs a) {
+  const NormGemvDesc d = pick_desc(a, blockIdx.x);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int row = (blockIdx.x - d.block_begin) * kWaves + threadIdx.x / kWave;
+  const bool ok = row < d.n;
+  uint4 w1[SLABS], w2[SLABS];
+  uint32_t s1[SLABS], s2[SLABS];
+  load_w8_row<SLABS>(d.w, d.s, row, ok, a.k, lane, w1, s1);
+  if (PAIR) load_w8_row<SLABS>(d.w2, d.s2, row, ok, a.k, lane, w2, s2);
+  float xn[SLABS][16];
+  wave_rms_norm16<SLABS>(a.x, a.norm_w, a.k, a.eps, lane, xn);
+  const float v1 = w8_row_dot<SLABS>(w1, s1, xn);
+  if (PAIR) {
+    const float v2 = w8_row_dot<SLABS>(w2, s2, xn);
+    if (lane == 0 && ok) {
+      const float g = bf16_to_f32(f32_to_bf16(v1));
+      const float u = bf16_to_f32(f32_to_bf16(v2));
+      gstore(d.y + row, f32_to_bf16(g / (1.0f + expf(-g)) * u));
+    }
+  } else if (lane == 0 && ok) {
+    const float b = d.bias ? bf16_to_f32(gload(d.bias + row)) : 0.0f;
+    gstore(d.y + row, f32_to_bf16(v1 + b));
+  }
+}
+
+// The tied LM head of a decode step: logits = bf16(E rms_norm(x)) with the
+// argmax of the FP32 sums.  A grid of at most lm_head_decode_blocks()
+// workgroups; each wave normalizes x once and walks R-row tasks with a
+// stride of the grid's wave count, keeping the next task's loads in flight.
+// R rows per task (1, 2, 4 or 8).
+// Every workgroup leaves its best (value, index) pair; the last to finish
+// (counted on `counter`) reduces them, writes the token to state->token and,
+// with `advance`, records it in history[state->step] and moves the step and
+// position on by one.  It then resets the counter.
+template <int SLABS, int R>
+__global__ __launch_bounds__(kBlock) void lm_head_decode_kernel(LmHeadDecodeArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int chunks = a.k >> 3;
+  float xn[SLABS][8];
+  const int gw = blockIdx.x * kWaves + wave;
+  const int stride = gridDim.x * kWaves * R;
+  int row0 = gw * R;
+  uint4 w[R][SLABS], wn[R][SLABS];
+  auto load_task = [&](int r0, uint4 (&dst)[R][SLABS]) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = r0 + r;
+#pragma unroll
+      for (int s = 0; s < SLABS; ++s) {
+        const int c = s * kWave + lane;
+        dst[r][s] = row < a.vocab && c < chunks
+                        ? load_stream16(a.w + static_cast<size_t>(row) * a.k + 8 * c)
+                        : make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+  load_task(row0, w);
+  wave_rms_norm8<SLABS>(a.x, a.norm_w, a.k, a.eps, lane, xn);
+  float best_v = -FLT_MAX;
+  int best_i = INT_MAX;
+  for (; row0 < a.vocab; row0 += stride) {
+    load_task(row0 + stride, wn);
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      acc[r] = 0.0f;
+#pragma unroll
+      for (int s = 0; s < SLABS; ++s) acc[r] = dot8_bf16(w[r][s], xn[s], acc[r]);
+    }
+    wave_reduce_rows<R>(acc, lane);
+    if (is_row_writer<R>(lane)) {
+      const int row = row0 + reduced_row<R>(lane);
+      if (row < a.vocab) {
+        gstore(a.logits + row, f32_to_bf16(acc[0]));
+        if (better(acc[0], row, best_v, best_i)) {
+          best_v = acc[0];
+          best_i = row;
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int s = 0; s < SLABS; ++s) w[r][s] = wn[r][s];
+  }
+  wave_argmax(best_v, best_i);
+  __shared__ float wv[kWaves];
+  __shared__ int wi[kWaves];
+  __shared__ int last;
+  if (lane == 0) {
+    wv[wave] = best_v;
+    wi[wave] = best_i;
+  }
+  __syncthreads();
+  const __amdgpu_buffer_rsrc_t cand =
+      coherent_rsrc(a.block_best, static_cast<uint32_t>(gridDim.x) * 8u);
+  if (threadIdx.x == 0) {
+    float v = wv[0];
+    int i = wi[0];
+    for (int k = 1; k < kWaves; ++k) {
+      if (better(wv[k], wi[k], v, i)) {
+        v = wv[k];
+        i = wi[k];
+      }
+    }
+    coherent_store(cand, blockIdx.x * 8u, v);
+    coherent_store(cand, blockIdx.x * 8u + 4u, i);
+    __builtin_amdgcn_s_waitcnt(0);
+    last = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           static_cast<int>(gridDim.x) - 1;
+  }
+  __syncthreads();
+  if (!last) return;
+  // The last workgroup: reduce every workgroup's candidate.
+  float v = -FLT_MAX;
+  int i = INT_MAX;
+  for (int b = threadIdx.x; b < static_cast<int>(gridDim.x); b += kBlock) {
+    const float cv = coherent_load_f32(cand, b * 8u);
+    const int ci = coherent_load_i32(cand, b * 8u + 4u);
+    if (better(cv, ci, v, i)) {
+      v = cv;
+      i = ci;
+    }
+  }
+  wave_argmax(v, i);
+  if (lane == 0) {
+    wv[wave] = v;
+    wi[wave] = i;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int k = 1; k < kWaves; ++k) {
+      if (better(wv[k], wi[k], wv[0], wi[0])) {
+        wv[0] = wv[k];
+        wi[0] = wi[k];
+      }
+    }
+    ModelState* st = a.state;
+    st->token = wi[0];
+    if (a.advance) {
+      const int step = st->step;
+      if (step < a.history_len) a.history[step] = wi[0];
+      st->step = step + 1;
+      st->pos = st->pos + 1;
+    }
+    __hip_atomic_store(a.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+
+// The o-projection of a decode step fused with the merge of the split
+// attention's partials and the residual add:
+//   attn = bf16(merge of the ceil((pos + 1) / span) spans' partials)
+//   x[row] = bf16(Wo[row] . attn + x[row])
+// All 256 threads first request their weight row (one row per wave, four
+// per workgroup) and the partials, then merge into LDS; the GEMV reads attn
+// from LDS.  Partials past a head's last split or past the buffer read as
+// zeros or as other heads' records and are weighted 0.
+template <int SLABS, bool W8, int MAXS>
+__global__ __launch_bounds__(kBlock) void attn_o_gemv_kernel(AttnOArgs a) {
+  constexpr int kChunk = W8 ? 16 : 8;          // values per 16-byte weight chunk
+  constexpr int kMaxK = SLABS * kWave * kChunk;
+  constexpr int kPer = (kMaxK + kBlock - 1) / kBlock;
+  __shared__ float attn[kMaxK];
+  __shared__ float ms[kAttnOMaxHeads][MAXS], ls[kAttnOMaxHeads][MAXS];
+  __shared__ float hw[kAttnOMaxHeads][MAXS];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int row = blockIdx.x * kWaves + tid / kWave;
+  const bool ok = row < a.n;
+  const int chunks = a.k / kChunk;
+  // Weight row.
+  uint4 wq[SLABS];
+  uint32_t sc[SLABS];
+  if (W8) {
+    load_w8_row<SLABS>(static_cast<const int8_t*>(a.w), a.s, row, ok, a.k, lane, wq, sc);
+  } else {
+#pragma unroll
+    for (int i = 0; i < SLABS; ++i) {
+      const int c = i * kWave + lane;
+      wq[i] = ok && c < chunks
+                  ? load_stream16(static_cast<const uint16_t*>(a.w) + static_cast<size_t>(row) * a.k +
+                                  8 * c)
+                  : make_uint4(0, 0, 0, 0);
+    }
+  }
+  // Partials.
+  const int hd = a.head_dim, rec = hd + 2;
+  const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(a.partial), 0, a.heads * a.max_splits * rec * 4, 0x00020000);
+  float acc_s[kPer][MAXS];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int o = tid + kBlock * i;
+    const int h = o / hd, d = o % hd;
+#pragma unroll
+    for (int sp = 0; sp < MAXS; ++sp) {
+      acc_s[i][sp] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+          pr, static_cast<uint32_t>(((h * a.max_splits + sp) * rec + d) * 4), 0, 0));
+    }
+  }
+  float mv = 0.0f, lv = 0.0f;
+  if (tid < a.heads * MAXS) {
+    const int h = tid / MAXS, sp = tid % MAXS;
+    const uint32_t base = static_cast<uint32_t>(((h * a.max_splits + sp) * rec + hd) * 4);
+    mv = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pr, base, 0, 0));
+    lv = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pr, base + 4u, 0, 0));
+  }
+  const int pos = min(a.state->pos, a.max_seq - 1);
+  const int splits = pos / a.span + 1;
+  if (tid < a.heads * MAXS) {
+    ms[tid / MAXS][tid % MAXS] = mv;
+    ls[tid / MAXS][tid % MAXS] = lv;
+  }
+  __syncthreads();
+  if (tid < a.heads) {
+    float mm = ms[tid][0];
+#pragma unroll
+    for (int sp = 1; sp < MAXS; ++sp) {
+      if (sp < splits) mm = fmaxf(mm, ms[tid][sp]);
+    }
+    float e[MAXS], ll = 0.0f;
+#pragma unroll
+    for (int sp = 0; sp < MAXS; ++sp) {
+      e[sp] = sp < splits ? expf(ms[tid][sp] - mm) : 0.0f;
+      ll = fmaf(ls[tid][sp], e[sp], ll);
+    }
+#pragma unroll
+    for (int sp = 0; sp < MAXS; ++sp) hw[tid][sp] = e[sp] / ll;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int o = tid + kBlock * i;
+    if (o < a.k) {
+      const int h = o / hd;
+      float v = 0.0f;
+#pragma unroll
+      for (int sp = 0; sp < MAXS; ++sp) v = fmaf(acc_s[i][sp], hw[h][sp], v);
+      attn[o] = bf16_to_f32(f32_to_bf16(v));  // the attention output is BF16
+    }
+  }
+  __syncthreads();
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < SLABS; ++i) {
+    const int c = i * kWave + lane;
+    float xv[kChunk];
+#pragma unroll
+    for (int e = 0; e < kChunk; ++e) xv[e] = c < chunks ? attn[kChunk * c + e] : 0.0f;
+    if (W8) {
+      acc = fmaf(dot16_i8(wq[i], reinterpret_cast<const float(&)[16]>(xv)), bf16_to_f32(sc[i]),
+                 acc);
+    } else {
+      acc = dot8_bf16(wq[i], reinterpret_cast<const float(&)[8]>(xv), acc);
+    }
+  }
+  acc = wave_sum(acc);
+  if (lane == 0 && ok) gstore(a.x + row, f32_to_bf16(acc + bf16_to_f32(gload(a.x + row))));
+}
+
+// ------------------------------------------------------------ launchers --
+
+int norm_gemv_w8_slabs(int k) { return (k + 1023) / 1024; }
+
+bool norm_gemv_w8_supported(int k) {
+  return k >= 64 && k % 64 == 0 && norm_gemv_w8_slabs(k) <= kNormGemvMaxSlabs;
+}
+
+int norm_gemv_blocks(int n) { return (n + kWaves - 1) / kWaves; }
+
+template <bool PAIR>
+static void launch_norm_gemv(const NormGemvArgs& a, int blocks, hipStream_t stream) {
+  switch (norm_gemv_w8_slabs(a.k)) {
+    case 1:
+      hipLaunchKernelGGL((norm_gemv_w8_kernel<1, PAIR>), dim3(blocks), dim3(kBlock), 0, stream,
+                         a);
+      break;
+    case 2:
+      hipLaunchKernelGGL((norm_gemv_w8_kernel<2, PAIR>), dim3(blocks), dim3(kBlock), 0, stream,
+                         a);
+      break;
+    default:
+      hipLaunchKernelGGL((norm_gemv_w8_kernel<4, PAIR>), dim3(blocks), dim3(kBlock), 0, stream,
+                         a);
+      break;
+  }
+}
+
+void launch_norm_gemv_w8(const NormGemvArgs& a, int blocks, bool pair, hipStream_t stream) {
+  if (pair) {
+    launch_norm_gemv<true>(a, blocks, stream);
+  } else {
+    launch_norm_gemv<false>(a, blocks, stream);
+  }
+}
+
+int attn_o_slabs(int k, bool w8) {
+  const int per_slab = kWave * (w8 ? 16 : 8);
+  const int slabs = (k + per_slab - 1) / per_slab;
+  return slabs <= 1 ? 1 : slabs <= 2 ? 2 : slabs <= 4 ? 4 : 8;
+}
+
+bool attn_o_supported(int k, int heads, bool w8) {
+  const int chunk = w8 ? 16 : 8;
+  return k % (w8 ? 64 : 8) == 0 && k % chunk == 0 && heads <= kAttnOMaxHeads &&
+         attn_o_slabs(k, w8) <= (w8 ? 4 : 8) && heads * kAttnMaxSplits <= kBlock;
+}
+
+template <int SLABS, bool W8>
+static void launch_attn_o_slabs(const AttnOArgs& a, hipStream_t stream) {
+  const dim3 grid((a.n + kWaves - 1) / kWaves), block(kBlock);
+  if (a.max_splits <= 1) {
+    hipLaunchKernelGGL((attn_o_gemv_kernel<SLABS, W8, 1>), grid, block, 0, stream, a);
+  } else if (a.max_splits <= 2) {
+    hipLaunchKernelGGL((attn_o_gemv_kernel<SLABS, W8, 2>), grid, block, 0, stream, a);
+  } else if (a.max_splits <= 4) {
+    hipLaunchKernelGGL((attn_o_gemv_kernel<SLABS, W8, 4>), grid, block, 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((attn_o_gemv_kernel<SLABS, W8, 8>), grid, block, 0, stream, a);
+  }
+}
+
+void launch_attn_o_gemv(const AttnOArgs& a, bool w8, hipStream_t stream) {
+  const int slabs = attn_o_slabs(a.k, w8);
+  if (w8) {
+    if (slabs == 1) {
+      launch_attn_o_slabs<1, true>(a, stream);
+    } else if (slabs == 2) {
+      launch_attn_o_slabs<2, true>(a, stream);
+    } else {
+      launch_attn_o_slabs<4, true>(a, stream);
+    }
+  } else {
+    if (slabs <= 2) {
+      launch_attn_o_slabs<2, false>(a, stream);
+    } else if (slabs == 4) {
+      launch_attn_o_slabs<4, false>(a, stream);
+    } else {
+      launch_attn_o_slabs<8, false>(a, stream);
+    }
+  }
+}
+
+int lm_head_decode_slabs(int k) { return (k + 511) / 512; }
+
+bool lm_head_decode_supported(int k) {
+  return k >= 8 && k % 8 == 0 && lm_head_decode_slabs(k) <= kLmHeadMaxSlabs;
+}
+
+int lm_head_decode_blocks(int vocab) {
+  // Two workgroups per CU on 256 CUs (the best of a sweep over 256-8192
+  // workgroups and 1, 2 or 4 rows per task at V = 151936, K = 896: every
+  // workgroup also takes the finishing counter once, so more of them cost
+  // more); fewer for small vocabularies (at least one task per wave).
+  const int cap = 512;
+  const int need = (vocab + kWaves * kLmHeadRows - 1) / (kWaves * kLmHeadRows);
+  return need < cap ? need : cap;
+}
+
+template <int R>
+static void launch_lm_head_rows(const LmHeadDecodeArgs& a, int grid, hipStream_t stream) {
+  switch (lm_head_decode_slabs(a.k)) {
+    case 1:
+      hipLaunchKernelGGL((lm_head_decode_kernel<1, R>), dim3(grid), dim3(kBlock), 0, stream, a);
+      break;
+    case 2:
+      hipLaunchKernelGGL((lm_head_decode_kernel<2, R>), dim3(grid), dim3(kBlock), 0, stream, a);
+      break;
+    case 3:
+    case 4:
+      hipLaunchKernelGGL((lm_head_decode_kernel<4, R>), dim3(grid), dim3(kBlock), 0, stream, a);
+      break;
+    default:
+      hipLaunchKernelGGL((lm_head_decode_kernel<8, R>), dim3(grid), dim3(kBlock), 0, stream, a);
+      break;
+  }
+}
+
+void launch_lm_head_decode_shape(const LmHeadDecodeArgs& a, int grid, int rows,
+                                 hipStream_t stream) {
+  if (rows == 8) {
+    launch_lm_head_rows<8>(a, grid, stream);
+  } else if (rows == 4) {
+    launch_lm_head_rows<4>(a, grid, stream);
+  } else if (rows == 1) {
+    launch_lm_head_rows<1>(a, grid, stream);
+  } else {
+    launch_lm_head_rows<2>(a, grid, stream);
+  }
+}
+
+void launch_lm_head_decode(const LmHeadDecodeArgs& a, hipStream_t stream) {
+  launch_lm_head_decode_shape(a, lm_head_decode_blocks(a.vocab), kLmHeadRows, stream);
+}
+
+}  // namespace qlin

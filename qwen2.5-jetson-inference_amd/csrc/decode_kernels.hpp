@@ -1,0 +1,94 @@
+// Internal launch interface of the fused decode-step kernels
+// (decode_kernels.hip) used by the model runtime.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "model_kernels.hpp"
+
+namespace qlin {
+
+// One GEMV of a fused RMSNorm + W8A16 GEMV launch.  Rows are 4 per
+// workgroup; block_begin is the launch's first workgroup for this GEMV.
+// With the PAIR form, (w, s) are gate_proj, (w2, s2) up_proj and y the
+// SiLU-mul output; bias is unused.
+struct NormGemvDesc {
+  const int8_t* w;
+  const uint16_t* s;
+  const int8_t* w2;
+  const uint16_t* s2;
+  const uint16_t* bias;
+  uint16_t* y;
+  int n;
+  int block_begin;
+};
+
+constexpr int kNormGemvMaxDescs = 3;
+constexpr int kNormGemvMaxSlabs = 4;  // K <= 4096
+
+struct NormGemvArgs {
+  const uint16_t* x;       // [k] BF16 (the residual stream)
+  const uint16_t* norm_w;  // [k] BF16 RMSNorm weight
+  float eps;
+  int k;
+  int count;
+  NormGemvDesc d[kNormGemvMaxDescs];
+};
+
+int norm_gemv_w8_slabs(int k);
+bool norm_gemv_w8_supported(int k);
+int norm_gemv_blocks(int n);
+void launch_norm_gemv_w8(const NormGemvArgs& a, int blocks, bool pair, hipStream_t stream);
+
+// o-projection fused with the decode attention's split merge and the
+// residual add (x = bf16(Wo attn + x)).
+constexpr int kAttnOMaxHeads = 32;
+
+struct AttnOArgs {
+  const float* partial;     // heads x max_splits x (head_dim + 2) floats
+  const ModelState* state;
+  int heads;
+  int head_dim;
+  int span;                 // attention_span(max_seq)
+  int max_splits;           // attention_splits(max_seq)
+  int max_seq;
+  const void* w;            // [n, k] int8 (W8A16) or BF16
+  const uint16_t* s;        // [n, k / 64] BF16 scales (W8A16)
+  uint16_t* x;              // [n] residual stream, updated in place
+  int n;
+  int k;                    // heads x head_dim
+};
+
+bool attn_o_supported(int k, int heads, bool w8);
+void launch_attn_o_gemv(const AttnOArgs& a, bool w8, hipStream_t stream);
+
+constexpr int kLmHeadMaxSlabs = 8;  // K <= 4096
+
+struct LmHeadDecodeArgs {
+  const uint16_t* x;       // [k] BF16 final hidden state (before the norm)
+  const uint16_t* norm_w;  // [k] BF16 final RMSNorm weight
+  float eps;
+  const uint16_t* w;       // [vocab, k] BF16 (tied embedding)
+  int vocab;
+  int k;
+  uint16_t* logits;        // [vocab] BF16
+  float* block_best;       // lm_head_decode_blocks(vocab) (value, index) pairs
+  int* counter;            // zero between launches
+  ModelState* state;
+  int* history;
+  int history_len;
+  int advance;             // nonzero: record the token and advance step / pos
+};
+
+constexpr int kLmHeadRows = 4;  // rows per wave task
+
+bool lm_head_decode_supported(int k);
+// The grid the model's launches use (block_best holds this many pairs).
+int lm_head_decode_blocks(int vocab);
+void launch_lm_head_decode(const LmHeadDecodeArgs& a, hipStream_t stream);
+// Explicit grid (<= lm_head_decode_blocks(vocab)) and rows per task (1, 2, 4, 8).
+void launch_lm_head_decode_shape(const LmHeadDecodeArgs& a, int grid, int rows,
+                                 hipStream_t stream);
+
+}  // namespace qlin

@@ -135,4 +135,115 @@ __device__ __forceinline__ uint4 load_stream16(const void* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// ------------------------------------------------- GEMV building blocks --
+
+// Dot product of one 16-byte chunk of int8 weights with 16 FP32 activations.
+__device__ __forceinline__ float dot16_i8(const uint4 w, const float (&x)[16]) {
+  float p = sbyte0(w.x) * x[0];
+  p = fmaf(sbyte1(w.x), x[1], p);
+  p = fmaf(sbyte2(w.x), x[2], p);
+  p = fmaf(sbyte3(w.x), x[3], p);
+  p = fmaf(sbyte0(w.y), x[4], p);
+  p = fmaf(sbyte1(w.y), x[5], p);
+  p = fmaf(sbyte2(w.y), x[6], p);
+  p = fmaf(sbyte3(w.y), x[7], p);
+  p = fmaf(sbyte0(w.z), x[8], p);
+  p = fmaf(sbyte1(w.z), x[9], p);
+  p = fmaf(sbyte2(w.z), x[10], p);
+  p = fmaf(sbyte3(w.z), x[11], p);
+  p = fmaf(sbyte0(w.w), x[12], p);
+  p = fmaf(sbyte1(w.w), x[13], p);
+  p = fmaf(sbyte2(w.w), x[14], p);
+  p = fmaf(sbyte3(w.w), x[15], p);
+  return p;
+}
+
+// Load 16 BF16 activations (32 bytes) as FP32.
+__device__ __forceinline__ void load_x16(const uint16_t* x, float (&out)[16]) {
+  const uint4 a = load_global16(x);
+  const uint4 b = load_global16(x + 8);
+  out[0] = bf16_lo(a.x);  out[1] = bf16_hi(a.x);
+  out[2] = bf16_lo(a.y);  out[3] = bf16_hi(a.y);
+  out[4] = bf16_lo(a.z);  out[5] = bf16_hi(a.z);
+  out[6] = bf16_lo(a.w);  out[7] = bf16_hi(a.w);
+  out[8] = bf16_lo(b.x);  out[9] = bf16_hi(b.x);
+  out[10] = bf16_lo(b.y); out[11] = bf16_hi(b.y);
+  out[12] = bf16_lo(b.z); out[13] = bf16_hi(b.z);
+  out[14] = bf16_lo(b.w); out[15] = bf16_hi(b.w);
+}
+
+__device__ __forceinline__ void load_x8(const uint16_t* x, float (&out)[8]) {
+  const uint4 a = load_global16(x);
+  out[0] = bf16_lo(a.x); out[1] = bf16_hi(a.x);
+  out[2] = bf16_lo(a.y); out[3] = bf16_hi(a.y);
+  out[4] = bf16_lo(a.z); out[5] = bf16_hi(a.z);
+  out[6] = bf16_lo(a.w); out[7] = bf16_hi(a.w);
+}
+
+__device__ __forceinline__ float dot8_bf16(const uint4 w, const float (&x)[8], float acc) {
+  acc = fmaf(bf16_lo(w.x), x[0], acc);
+  acc = fmaf(bf16_hi(w.x), x[1], acc);
+  acc = fmaf(bf16_lo(w.y), x[2], acc);
+  acc = fmaf(bf16_hi(w.y), x[3], acc);
+  acc = fmaf(bf16_lo(w.z), x[4], acc);
+  acc = fmaf(bf16_hi(w.z), x[5], acc);
+  acc = fmaf(bf16_lo(w.w), x[6], acc);
+  acc = fmaf(bf16_hi(w.w), x[7], acc);
+  return acc;
+}
+
+// Better (value, index) pair: larger value, ties to the lower index.
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) {
+    const float ov = __shfl_xor(v, offset);
+    const int oi = __shfl_xor(i, offset);
+    if (better(ov, oi, v, i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+}
+
+// ------------------------------------------ device-coherent data exchange --
+//
+// Workgroups that hand data to each other inside one launch (split-K
+// partials, attention partials, argmax candidates) store and load it with
+// the sc1 cache policy: the accesses are coherent across the XCDs' separate
+// L2 caches without the L2 write-back / invalidate a release / acquire
+// fence would cost.  The hand-off itself is an agent-scope atomic counter
+// taken after the stores have completed (s_waitcnt).
+constexpr int kCoherentPolicy = 16;  // buffer cache policy bits: sc1
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const void* base,
+                                                                 uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes),
+                                           0x00020000);
+}
+
+__device__ __forceinline__ void coherent_store(__amdgpu_buffer_rsrc_t r, uint32_t byte_offset,
+                                               float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, byte_offset, 0, kCoherentPolicy);
+}
+
+__device__ __forceinline__ void coherent_store(__amdgpu_buffer_rsrc_t r, uint32_t byte_offset,
+                                               int v) {
+  __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(v), r, byte_offset, 0,
+                                        kCoherentPolicy);
+}
+
+// Out-of-range offsets (beyond the resource's byte count) read 0.
+__device__ __forceinline__ float coherent_load_f32(__amdgpu_buffer_rsrc_t r,
+                                                   uint32_t byte_offset) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, byte_offset, 0, kCoherentPolicy));
+}
+
+__device__ __forceinline__ int coherent_load_i32(__amdgpu_buffer_rsrc_t r, uint32_t byte_offset) {
+  return static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(r, byte_offset, 0, kCoherentPolicy));
+}
+
 }  // namespace qlin

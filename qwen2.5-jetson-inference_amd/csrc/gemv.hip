@@ -36,41 +36,6 @@ constexpr int kWavesPerBlock = kBlock / kWave;
 
 // ---------------------------------------------------------------- W8A16 --
 
-// Dot product of one 16-byte chunk of int8 weights with 16 FP32 activations.
-__device__ __forceinline__ float dot16_i8(const uint4 w, const float (&x)[16]) {
-  float p = sbyte0(w.x) * x[0];
-  p = fmaf(sbyte1(w.x), x[1], p);
-  p = fmaf(sbyte2(w.x), x[2], p);
-  p = fmaf(sbyte3(w.x), x[3], p);
-  p = fmaf(sbyte0(w.y), x[4], p);
-  p = fmaf(sbyte1(w.y), x[5], p);
-  p = fmaf(sbyte2(w.y), x[6], p);
-  p = fmaf(sbyte3(w.y), x[7], p);
-  p = fmaf(sbyte0(w.z), x[8], p);
-  p = fmaf(sbyte1(w.z), x[9], p);
-  p = fmaf(sbyte2(w.z), x[10], p);
-  p = fmaf(sbyte3(w.z), x[11], p);
-  p = fmaf(sbyte0(w.w), x[12], p);
-  p = fmaf(sbyte1(w.w), x[13], p);
-  p = fmaf(sbyte2(w.w), x[14], p);
-  p = fmaf(sbyte3(w.w), x[15], p);
-  return p;
-}
-
-// Load 16 BF16 activations (32 bytes) as FP32.
-__device__ __forceinline__ void load_x16(const uint16_t* x, float (&out)[16]) {
-  const uint4 a = load_global16(x);
-  const uint4 b = load_global16(x + 8);
-  out[0] = bf16_lo(a.x);  out[1] = bf16_hi(a.x);
-  out[2] = bf16_lo(a.y);  out[3] = bf16_hi(a.y);
-  out[4] = bf16_lo(a.z);  out[5] = bf16_hi(a.z);
-  out[6] = bf16_lo(a.w);  out[7] = bf16_hi(a.w);
-  out[8] = bf16_lo(b.x);  out[9] = bf16_hi(b.x);
-  out[10] = bf16_lo(b.y); out[11] = bf16_hi(b.y);
-  out[12] = bf16_lo(b.z); out[13] = bf16_hi(b.z);
-  out[14] = bf16_lo(b.w); out[15] = bf16_hi(b.w);
-}
-
 // The weights and scales of one slab (64 chunks of 16 int8) of R rows.
 template <int R>
 __device__ __forceinline__ void w8a16_load_rows(const W8GemvArgs& a, int row0, int row_end,
@@ -317,42 +282,6 @@ __global__ __launch_bounds__(kBlock) void w8a16_linear_generic_kernel(
 
 // ----------------------------------------------------------------- BF16 --
 
-__device__ __forceinline__ void load_x8(const uint16_t* x, float (&out)[8]) {
-  const uint4 a = load_global16(x);
-  out[0] = bf16_lo(a.x); out[1] = bf16_hi(a.x);
-  out[2] = bf16_lo(a.y); out[3] = bf16_hi(a.y);
-  out[4] = bf16_lo(a.z); out[5] = bf16_hi(a.z);
-  out[6] = bf16_lo(a.w); out[7] = bf16_hi(a.w);
-}
-
-__device__ __forceinline__ float dot8_bf16(const uint4 w, const float (&x)[8], float acc) {
-  acc = fmaf(bf16_lo(w.x), x[0], acc);
-  acc = fmaf(bf16_hi(w.x), x[1], acc);
-  acc = fmaf(bf16_lo(w.y), x[2], acc);
-  acc = fmaf(bf16_hi(w.y), x[3], acc);
-  acc = fmaf(bf16_lo(w.z), x[4], acc);
-  acc = fmaf(bf16_hi(w.z), x[5], acc);
-  acc = fmaf(bf16_lo(w.w), x[6], acc);
-  acc = fmaf(bf16_hi(w.w), x[7], acc);
-  return acc;
-}
-
-// Better (value, index) pair: larger value, ties to the lower index.
-__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
-  return v > bv || (v == bv && i < bi);
-}
-
-__device__ __forceinline__ void wave_argmax(float& v, int& i) {
-#pragma unroll
-  for (int offset = 32; offset > 0; offset >>= 1) {
-    const float ov = __shfl_xor(v, offset);
-    const int oi = __shfl_xor(i, offset);
-    if (better(ov, oi, v, i)) {
-      v = ov;
-      i = oi;
-    }
-  }
-}
 
 // One wave's share of a BF16 GEMV, as w8a16_wave_span: R-row tasks, rows
 // walked in slabs of 64 chunks of 8 BF16 (1 KiB); for K <= 1024 (at most

@@ -8,16 +8,21 @@
 // KV cache; it is allocated once at creation, and no prefill or decode call
 // allocates.
 //
-// Decode step (one token, position and token read from ModelState):
-//   embedding; per layer: RMSNorm -> q|k|v GEMV -> RoPE + KV store +
-//   attention -> o GEMV (+ residual) -> RMSNorm -> gate|up GEMV -> SiLU-mul
-//   -> down GEMV (+ residual); final RMSNorm -> LM head with argmax into
-//   ModelState.token -> advance (history, position).
-// The residual add rides on the GEMV's bias operand (bias = output = the
-// residual stream): each output element is read as bias and then written
-// by the same lane, so the aliasing is safe.  Under W8A16 the q|k|v and
-// gate|up GEMVs are one grouped launch each.  With use_graph the step is
-// captured once and replayed per token.
+// Decode step (one token, position and token read from ModelState), W8A16:
+//   embedding; per layer five launches:
+//     RMSNorm + q|k|v GEMV (norm_gemv_w8),
+//     RoPE + KV store + attention split over the context (partials),
+//     split merge + o GEMV + residual (attn_o_gemv),
+//     RMSNorm + gate|up GEMV + SiLU-mul (norm_gemv_w8, paired rows),
+//     down GEMV + residual;
+//   final RMSNorm + LM head + argmax + step bookkeeping (lm_head_decode).
+// Every launch is built to wait on one round of global loads: a decode
+// step is latency-bound, not bandwidth-bound.  W16A16 runs the unfused
+// norm / GEMV / SiLU-mul launches around the same attention, o and LM head
+// kernels.  The down GEMV's residual add rides on the GEMV's bias operand
+// (bias = output = the residual stream): each output element is read as
+// bias and then written by the same lane, so the aliasing is safe.  With
+// use_graph the step is captured once and replayed per token.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -27,6 +32,7 @@
 #include <new>
 #include <vector>
 
+#include "decode_kernels.hpp"
 #include "infer_model.h"
 #include "linear_kernels.hpp"
 #include "model_kernels.hpp"
@@ -50,11 +56,17 @@ struct Layer {
   Linear q, k, v, o, gate, up, down;
   uint16_t* key_cache = nullptr;
   uint16_t* value_cache = nullptr;
-  // W8A16 grouped-GEMV descriptor tables (device) and their block counts.
+  // W8A16 grouped-GEMV descriptor tables (device) and their block counts
+  // (the unfused path).
   W8GroupDesc* qkv_table = nullptr;
   W8GroupDesc* gate_up_table = nullptr;
   int qkv_blocks = 0;
   int gate_up_blocks = 0;
+  // The fused path: RMSNorm + q|k|v, RMSNorm + gate|up + SiLU-mul.
+  NormGemvArgs qkv_args{};
+  NormGemvArgs gate_up_args{};
+  int qkv_fused_blocks = 0;
+  int gate_up_fused_blocks = 0;
 };
 
 // Rows per block of the decode step's grouped GEMVs: one 4-row task per
@@ -78,6 +90,8 @@ struct infer_hip_model {
   infer_hip_model_config cfg{};
   bool w8 = false;
   bool use_graph = false;
+  bool fused_norm_gemv = false;  // W8A16 with hidden % 64 == 0, hidden <= 4096
+  bool fused_lm_head = false;    // hidden % 8 == 0, hidden <= 4096
   int max_seq = 0;
   int head_dim = 0;
   int kv_dim = 0;
@@ -92,12 +106,13 @@ struct infer_hip_model {
   int* history = nullptr;
   int* prompt = nullptr;
   uint16_t *x = nullptr, *norm = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
-  uint16_t *attn = nullptr, *gate = nullptr, *up = nullptr, *mlp = nullptr, *logits = nullptr;
+  uint16_t *gate = nullptr, *up = nullptr, *mlp = nullptr, *logits = nullptr;
   float* lm_value = nullptr;
   int* lm_index = nullptr;
+  float* lm_best = nullptr;   // fused LM head: per-workgroup (value, index)
+  int* lm_counter = nullptr;
   float2* rope = nullptr;
-  float* attn_partial = nullptr;
-  int* attn_counters = nullptr;
+  float* attn_partial = nullptr;  // decode attention split partials
   uint16_t *px = nullptr, *pnorm = nullptr, *pq = nullptr, *pk = nullptr, *pv = nullptr;
   uint16_t *pattn = nullptr, *ptmp = nullptr, *pgate = nullptr, *pup = nullptr, *pmlp = nullptr;
 
@@ -166,13 +181,24 @@ void linear_batch(const infer_hip_model* m, const Linear& l, const uint16_t* x, 
   }
 }
 
-// Final RMSNorm of `row` and the LM head with its argmax into state->token.
-int lm_head_step(infer_hip_model* m, const uint16_t* row) {
+// Final RMSNorm of `row` and the LM head with its argmax into state->token;
+// with `advance` the step's bookkeeping too (history, step, position).
+int lm_head_step(infer_hip_model* m, const uint16_t* row, bool advance) {
   const infer_hip_model_config& c = m->cfg;
+  if (m->fused_lm_head) {
+    launch_lm_head_decode({row, m->final_norm, c.rms_norm_eps, m->lm_head, c.vocab_size,
+                           c.hidden_size, m->logits, m->lm_best, m->lm_counter, m->state,
+                           m->history, m->max_seq, advance ? 1 : 0},
+                          m->stream);
+    return check_launch("lm head");
+  }
   launch_rms_norm(row, m->final_norm, m->norm, 1, c.hidden_size, c.rms_norm_eps, m->stream);
-  return infer_hip_lm_head_bf16(m->lm_head, nullptr, m->norm, m->logits, m->lm_value,
-                                m->lm_index, &m->state->token, c.vocab_size, c.hidden_size,
-                                m->stream);
+  const int rc = infer_hip_lm_head_bf16(m->lm_head, nullptr, m->norm, m->logits, m->lm_value,
+                                        m->lm_index, &m->state->token, c.vocab_size,
+                                        c.hidden_size, m->stream);
+  if (rc != INFER_HIP_OK || !advance) return rc;
+  launch_advance(m->state, m->history, m->max_seq, m->stream);
+  return check_launch("decode step advance");
 }
 
 // Enqueue one decode step (src/qwen2.cpp:597-674) on the model's stream.
@@ -182,34 +208,42 @@ int enqueue_decode_step(infer_hip_model* m) {
   hipStream_t s = m->stream;
   launch_embedding(m->embed, &m->state->token, 1, c.vocab_size, hidden, m->x, s);
   for (const Layer& L : m->layers) {
-    launch_rms_norm(m->x, L.in_norm, m->norm, 1, hidden, c.rms_norm_eps, s);
-    if (m->w8) {
+    if (m->fused_norm_gemv) {
+      launch_norm_gemv_w8(L.qkv_args, L.qkv_fused_blocks, false, s);
+    } else if (m->w8) {
+      launch_rms_norm(m->x, L.in_norm, m->norm, 1, hidden, c.rms_norm_eps, s);
       launch_w8a16_gemv_grouped(L.qkv_table, 3, L.qkv_blocks, s);
     } else {
+      launch_rms_norm(m->x, L.in_norm, m->norm, 1, hidden, c.rms_norm_eps, s);
       gemv(m, L.q, L.q.b, m->norm, m->q);
       gemv(m, L.k, L.k.b, m->norm, m->k);
       gemv(m, L.v, L.v.b, m->norm, m->v);
     }
     launch_attention_decode(m->q, m->k, m->v, L.key_cache, L.value_cache, m->rope, m->state,
                             c.num_heads, c.num_kv_heads, m->head_dim, m->max_seq,
-                            m->attn_partial, m->attn_counters, m->attn, s);
-    gemv(m, L.o, m->x, m->attn, m->x);  // x = bf16(Wo attn + x)
-    launch_rms_norm(m->x, L.post_norm, m->norm, 1, hidden, c.rms_norm_eps, s);
-    if (m->w8) {
-      launch_w8a16_gemv_grouped(L.gate_up_table, 2, L.gate_up_blocks, s);
+                            m->attn_partial, s);
+    // x = bf16(Wo attn + x), attn merged from the attention's split partials
+    launch_attn_o_gemv({m->attn_partial, m->state, c.num_heads, m->head_dim,
+                        attention_span(m->max_seq), attention_splits(m->max_seq), m->max_seq,
+                        L.o.w, L.o.s, m->x, hidden, hidden},
+                       m->w8, s);
+    if (m->fused_norm_gemv) {
+      launch_norm_gemv_w8(L.gate_up_args, L.gate_up_fused_blocks, true, s);
     } else {
-      gemv(m, L.gate, nullptr, m->norm, m->gate);
-      gemv(m, L.up, nullptr, m->norm, m->up);
+      launch_rms_norm(m->x, L.post_norm, m->norm, 1, hidden, c.rms_norm_eps, s);
+      if (m->w8) {
+        launch_w8a16_gemv_grouped(L.gate_up_table, 2, L.gate_up_blocks, s);
+      } else {
+        gemv(m, L.gate, nullptr, m->norm, m->gate);
+        gemv(m, L.up, nullptr, m->norm, m->up);
+      }
+      launch_silu_mul(m->gate, m->up, m->mlp, c.intermediate_size, s);
     }
-    launch_silu_mul(m->gate, m->up, m->mlp, c.intermediate_size, s);
     gemv(m, L.down, m->x, m->mlp, m->x);  // x = bf16(Wd mlp + x)
   }
   int rc = check_launch("decode step");
   if (rc != INFER_HIP_OK) return rc;
-  rc = lm_head_step(m, m->x);
-  if (rc != INFER_HIP_OK) return rc;
-  launch_advance(m->state, m->history, m->max_seq, s);
-  return check_launch("decode step advance");
+  return lm_head_step(m, m->x, true);
 }
 
 int ensure_graph(infer_hip_model* m) {
@@ -281,7 +315,7 @@ int run_prefill(infer_hip_model* m, const int* tokens, int count, int* next) {
   }
   int rc = check_launch("prefill");
   if (rc != INFER_HIP_OK) return rc;
-  rc = lm_head_step(m, m->px + static_cast<size_t>(count - 1) * hidden);
+  rc = lm_head_step(m, m->px + static_cast<size_t>(count - 1) * hidden, false);
   if (rc != INFER_HIP_OK) return rc;
   launch_set_state(m->state, -1, count, 0, s);
   rc = check_launch("prefill state");
@@ -346,12 +380,16 @@ extern "C" int infer_hip_model_create(const infer_hip_model_config* config,
     return fail(INFER_HIP_INVALID_ARGUMENT, "model: invalid attention head dimension");
   }
   const int head_dim = c.hidden_size / c.num_heads;
-  if (!attention_head_dim_supported(head_dim) ||
-      c.num_heads / c.num_kv_heads > kAttentionMaxGroup) {
+  if (!attention_head_dim_supported(head_dim)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "model: head_dim %d unsupported (64 or 128)",
+                head_dim);
+  }
+  if (!attn_o_supported(c.hidden_size, c.num_heads, options->precision == INFER_HIP_PRECISION_W8A16) ||
+      c.num_heads > kAttnOMaxHeads) {
     return fail(INFER_HIP_INVALID_ARGUMENT,
-                "model: head_dim %d / group %d unsupported (head_dim 64 or 128, heads per kv "
-                "head <= %d)",
-                head_dim, c.num_heads / c.num_kv_heads, kAttentionMaxGroup);
+                "model: %d attention heads / hidden %d unsupported by the decode attention "
+                "(at most %d heads, hidden <= 4096)",
+                c.num_heads, c.hidden_size, kAttnOMaxHeads);
   }
   if (!(c.rms_norm_eps >= 0.0f) || !(c.rope_theta > 0.0f)) {
     return fail(INFER_HIP_INVALID_ARGUMENT, "model: invalid rms_norm_eps or rope_theta");
@@ -405,6 +443,8 @@ extern "C" int infer_hip_model_create(const infer_hip_model_config* config,
   m->embed = weights->embed_tokens;
   m->final_norm = weights->norm;
   m->lm_head = lm_head;
+  m->fused_norm_gemv = w8 && norm_gemv_w8_supported(hidden);
+  m->fused_lm_head = lm_head_decode_supported(hidden);
 
   // Arena layout.
   size_t cursor = 0;
@@ -419,14 +459,15 @@ extern "C" int infer_hip_model_create(const infer_hip_model_config* config,
   const size_t o_history = take(sizeof(int) * ms);
   const size_t o_prompt = take(sizeof(int) * ms);
   const size_t o_x = take(2 * hidden), o_norm = take(2 * hidden), o_q = take(2 * hidden);
-  const size_t o_k = take(2 * kv_dim), o_v = take(2 * kv_dim), o_attn = take(2 * hidden);
+  const size_t o_k = take(2 * kv_dim), o_v = take(2 * kv_dim);
   const size_t o_gate = take(2 * inter), o_up = take(2 * inter), o_mlp = take(2 * inter);
   const size_t o_logits = take(2 * static_cast<size_t>(c.vocab_size));
   const size_t o_lmv = take(sizeof(float) * lm_entries), o_lmi = take(sizeof(int) * lm_entries);
+  const size_t o_lmbest = take(8 * static_cast<size_t>(lm_head_decode_blocks(c.vocab_size)));
+  const size_t o_lmcounter = take(sizeof(int));
   const size_t o_rope = take(sizeof(float2) * ms * (head_dim / 2));
-  const size_t o_partial =
-      take(sizeof(float) * attention_decode_partial_floats(c.num_kv_heads, head_dim, max_seq));
-  const size_t o_counters = take(sizeof(int) * c.num_kv_heads);
+  const size_t o_partial = take(sizeof(float) * c.num_heads * attention_splits(max_seq) *
+                                (head_dim + 2));
   const size_t o_px = take(2 * ms * hidden), o_pnorm = take(2 * ms * hidden);
   const size_t o_pq = take(2 * ms * hidden), o_pk = take(2 * ms * kv_dim);
   const size_t o_pv = take(2 * ms * kv_dim), o_pattn = take(2 * ms * hidden);
@@ -455,13 +496,14 @@ extern "C" int infer_hip_model_create(const infer_hip_model_config* config,
   m->prompt = reinterpret_cast<int*>(a + o_prompt);
   auto bf = [&](size_t o) { return reinterpret_cast<uint16_t*>(a + o); };
   m->x = bf(o_x); m->norm = bf(o_norm); m->q = bf(o_q); m->k = bf(o_k); m->v = bf(o_v);
-  m->attn = bf(o_attn); m->gate = bf(o_gate); m->up = bf(o_up); m->mlp = bf(o_mlp);
+  m->gate = bf(o_gate); m->up = bf(o_up); m->mlp = bf(o_mlp);
   m->logits = bf(o_logits);
   m->lm_value = reinterpret_cast<float*>(a + o_lmv);
   m->lm_index = reinterpret_cast<int*>(a + o_lmi);
+  m->lm_best = reinterpret_cast<float*>(a + o_lmbest);
+  m->lm_counter = reinterpret_cast<int*>(a + o_lmcounter);
   m->rope = reinterpret_cast<float2*>(a + o_rope);
   m->attn_partial = reinterpret_cast<float*>(a + o_partial);
-  m->attn_counters = reinterpret_cast<int*>(a + o_counters);
   m->px = bf(o_px); m->pnorm = bf(o_pnorm); m->pq = bf(o_pq); m->pk = bf(o_pk); m->pv = bf(o_pv);
   m->pattn = bf(o_pattn); m->ptmp = bf(o_ptmp); m->pgate = bf(o_pgate); m->pup = bf(o_pup);
   m->pmlp = bf(o_pmlp);
@@ -515,6 +557,21 @@ extern "C" int infer_hip_model_create(const infer_hip_model_config* config,
       L.gate_up_table = tables + host_tables.size();
       host_tables.push_back(desc(L.gate, m->norm, m->gate, L.gate_up_blocks));
       host_tables.push_back(desc(L.up, m->norm, m->up, L.gate_up_blocks));
+    }
+    if (m->fused_norm_gemv) {
+      auto fdesc = [](const Linear& li, const Linear* pair, uint16_t* y, int& blocks) {
+        NormGemvDesc d{static_cast<const int8_t*>(li.w), li.s,
+                       pair ? static_cast<const int8_t*>(pair->w) : nullptr,
+                       pair ? pair->s : nullptr, li.b, y, li.n, blocks};
+        blocks += norm_gemv_blocks(li.n);
+        return d;
+      };
+      L.qkv_args = NormGemvArgs{m->x, L.in_norm, c.rms_norm_eps, hidden, 3, {}};
+      L.qkv_args.d[0] = fdesc(L.q, nullptr, m->q, L.qkv_fused_blocks);
+      L.qkv_args.d[1] = fdesc(L.k, nullptr, m->k, L.qkv_fused_blocks);
+      L.qkv_args.d[2] = fdesc(L.v, nullptr, m->v, L.qkv_fused_blocks);
+      L.gate_up_args = NormGemvArgs{m->x, L.post_norm, c.rms_norm_eps, hidden, 1, {}};
+      L.gate_up_args.d[0] = fdesc(L.gate, &L.up, m->mlp, L.gate_up_fused_blocks);
     }
   }
   // Every region the kernels write must lie inside the arena.

@@ -131,223 +131,211 @@ __global__ __launch_bounds__(kThreads) void rope_store_kernel(
 
 // ------------------------------------------------------ decode attention --
 
-// One decode step's attention for every head, split over the context.
-// Workgroup (c, g) takes positions [c * kChunk, (c + 1) * kChunk) of the
-// context [0, pos] for the `group` query heads of kv head g.  Every
-// workgroup rotates the group's q in LDS; the chunk holding pos also
-// rotates that token's k and stores its k and v into the caches (no other
-// workgroup reads position pos: the chunk's own reads of that row take the
-// new values from k_new / v_new).  The chunk's value rows are staged in LDS
-// with 16-byte loads; lane p scores position p (its key row as 16-byte
-// loads), lane d accumulates output dimension d (and d + 64 when HD = 128).
-// Each workgroup writes its per-head (acc[HD], max, sum) partial; the last
-// one of kv head g to finish (counted on counters[g] with device-coherent
-// accesses) merges the partials in chunk order, writes the heads' BF16
-// outputs and resets its counter.  A context of one chunk skips the merge.
-constexpr int kChunk = 64;
+// One decode step's attention, split over the context.  Workgroup (c, h)
+// takes the positions [c span, (c + 1) span) of the context [0, pos] for
+// query head h (kv head g = h / group).  Its kAttnWaves waves take 64-
+// position tiles of the span in turn; in a tile lane p holds position p's
+// key and value rows (16-byte buffer loads whose range ends at the context,
+// so rows past it read as zeros without a branch around the loads), scores
+// it against the rotated q (in LDS), and the tile's value rows go through
+// the wave's LDS slice so that lane d can accumulate output dimension d
+// (and d + 64 when HD = 128).  The softmax runs online across a wave's
+// tiles; the waves are merged in LDS and the workgroup stores the head's
+// (acc[HD], max, sum) partial for its span at
+// partial[(h * max_splits + c) * (HD + 2)].  The o-projection kernel merges
+// the partials of the ceil((pos + 1) / span) spans (attn_o_gemv_kernel).
+// The query heads of a kv head read the same rows; they meet in L2.
+//
+// Latency: a wave's first tile is requested at kernel entry, before the q
+// rotation, and (HD = 64) each next tile before the current one is
+// computed.
+//
+// Position pos is the new token: its k (rotated here) and v come from
+// k_new / v_new through LDS, never from the cache, and the workgroup of
+// the first query head of the kv head whose span holds pos writes them into
+// the caches.
+constexpr int kTile = 64;
 
 template <int HD>
-__global__ __launch_bounds__(kThreads) void attention_decode_kernel(
+__device__ __forceinline__ void load_tile_rows(__amdgpu_buffer_rsrc_t kr_rsrc,
+                                               __amdgpu_buffer_rsrc_t vr_rsrc, int p,
+                                               uint4 (&kr)[HD / 8], uint4 (&vr)[HD / 8]) {
+  const uint32_t row = static_cast<uint32_t>(p) * HD * 2u;
+#pragma unroll
+  for (int j = 0; j < HD / 8; ++j) {
+    kr[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kr_rsrc, row + 16u * j,
+                                                                            0, 0));
+  }
+#pragma unroll
+  for (int j = 0; j < HD / 8; ++j) {
+    vr[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr_rsrc, row + 16u * j,
+                                                                            0, 0));
+  }
+}
+
+template <int HD>
+__global__ __launch_bounds__(kAttnWaves * kWave) void attention_decode_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_new,
     const uint16_t* __restrict__ v_new, uint16_t* __restrict__ key_cache,
     uint16_t* __restrict__ value_cache, const float2* __restrict__ rope,
-    const ModelState* __restrict__ state, int heads, int kv_heads, int max_seq,
-    float* __restrict__ partial, int* __restrict__ counters, uint16_t* __restrict__ out) {
+    const ModelState* __restrict__ state, int heads, int kv_heads, int max_seq, int span,
+    int max_splits, float* __restrict__ partial) {
+  constexpr int W = kAttnWaves;
   constexpr int half = HD / 2;
-  constexpr int kDims = HD / kWave;     // output dimensions per lane
-  constexpr int kPieces = HD / 8;       // 16-byte pieces per cache row
-  constexpr int kWaves = kThreads / kWave;
-  constexpr int kRec = HD + 2;          // partial record: acc[HD], max, sum
-  const int g = blockIdx.y;
+  constexpr int kDims = HD / kWave;  // output dimensions per lane
+  constexpr int kPieces = HD / 8;    // 16-byte pieces per row
+  constexpr int kRow = HD + 8;       // LDS row stride (BF16 elements), padded
+  constexpr bool kPrefetch = HD <= 64;  // register budget
   const int c = blockIdx.x;
+  const int h = blockIdx.y;
   const int pos = min(state->pos, max_seq - 1);
   const int seq = pos + 1;
-  const int chunks = (seq + kChunk - 1) / kChunk;
-  if (c >= chunks) return;  // the grid covers max_seq; idle chunks exit
+  const int begin = c * span;
+  if (begin >= seq) return;  // the grid covers max_seq; spans past the context exit
+  const int end = min(seq, begin + span);
   const int group = heads / kv_heads;
+  const int g = h / group;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-  const int p0 = c * kChunk;
-  const int plen = min(kChunk, seq - p0);
   const size_t head_base = static_cast<size_t>(g) * max_seq * HD;
+  const __amdgpu_buffer_rsrc_t kr_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(key_cache + head_base, 0, end * HD * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vr_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(value_cache + head_base, 0, end * HD * 2, 0x00020000);
 
-  __shared__ float qs[kAttentionMaxGroup][HD];
-  __shared__ float knew[HD];
-  __shared__ __align__(16) uint16_t vt[kChunk][HD];
-  __shared__ float sc[kAttentionMaxGroup][kChunk];
-  __shared__ float mx[kAttentionMaxGroup], sm[kAttentionMaxGroup];
-  __shared__ int last;
+  uint4 kr[kPieces], vr[kPieces];
+  load_tile_rows<HD>(kr_rsrc, vr_rsrc, begin + wave * kTile + lane, kr, vr);
 
-  // This lane's key row (raw BF16), issued first to overlap its latency.
-  const int p = p0 + lane;
-  const bool valid = lane < plen;
-  uint4 kraw[kPieces];
-  if (valid && p != pos) {
-    const uint4* kr = reinterpret_cast<const uint4*>(key_cache + head_base +
-                                                     static_cast<size_t>(p) * HD);
-#pragma unroll
-    for (int j = 0; j < kPieces; ++j) kraw[j] = kr[j];
-  }
-  // Stage the chunk's value rows; row pos comes from v_new.
-  for (int i = tid; i < plen * kPieces; i += kThreads) {
-    const int row = i / kPieces, piece = i % kPieces;
-    const uint16_t* src = p0 + row == pos
-                              ? v_new + static_cast<size_t>(g) * HD
-                              : value_cache + head_base + static_cast<size_t>(p0 + row) * HD;
-    reinterpret_cast<uint4*>(vt[row])[piece] = reinterpret_cast<const uint4*>(src)[piece];
-  }
-  // Rotate the group's q (rounded to BF16 as the reference's rope kernel
-  // stores q) and, in the owner chunk, the new k.
+  __shared__ float qs[HD];
+  __shared__ __align__(16) uint16_t knew[HD];
+  __shared__ __align__(16) uint16_t vnew[HD];
+  __shared__ __align__(16) uint16_t vt[W][kTile][kRow];
+  __shared__ float et[W][kTile];
+  __shared__ float wm[W], wl[W];
+  __shared__ float wacc[W][HD];
+
+  // q of head h and this token's k, rotated and rounded to BF16 (as the
+  // reference's rope kernel stores them), and this token's v.
   const float2* cs = rope + static_cast<size_t>(pos) * half;
-  for (int j = tid; j < group * half; j += kThreads) {
-    const int h = j / half, i = j % half;
-    const uint16_t* qh = q + static_cast<size_t>(g * group + h) * HD;
-    float a = load_bf16(qh + i), b = load_bf16(qh + i + half);
-    rope_pair(a, b, cs[i]);
-    qs[h][i] = bf16_to_f32(f32_to_bf16(a));
-    qs[h][i + half] = bf16_to_f32(f32_to_bf16(b));
-  }
-  const bool owner = pos >= p0 && pos < p0 + kChunk;
-  if (owner) {
-    const size_t at = head_base + static_cast<size_t>(pos) * HD;
-    for (int i = tid; i < half; i += kThreads) {
-      const uint16_t* kh = k_new + static_cast<size_t>(g) * HD;
-      float a = load_bf16(kh + i), b = load_bf16(kh + i + half);
-      rope_pair(a, b, cs[i]);
-      const uint16_t ka = f32_to_bf16(a), kb = f32_to_bf16(b);
-      knew[i] = bf16_to_f32(ka);
-      knew[i + half] = bf16_to_f32(kb);
-      key_cache[at + i] = ka;
-      key_cache[at + i + half] = kb;
-    }
-    for (int i = tid; i < HD; i += kThreads) {
-      value_cache[at + i] = v_new[static_cast<size_t>(g) * HD + i];
-    }
+  if (tid < half) {
+    const uint16_t* qh = q + static_cast<size_t>(h) * HD;
+    const uint16_t* kh = k_new + static_cast<size_t>(g) * HD;
+    const float2 r = cs[tid];
+    float q0 = load_bf16(qh + tid), q1 = load_bf16(qh + tid + half);
+    float k0 = load_bf16(kh + tid), k1 = load_bf16(kh + tid + half);
+    rope_pair(q0, q1, r);
+    rope_pair(k0, k1, r);
+    qs[tid] = bf16_to_f32(f32_to_bf16(q0));
+    qs[tid + half] = bf16_to_f32(f32_to_bf16(q1));
+    knew[tid] = f32_to_bf16(k0);
+    knew[tid + half] = f32_to_bf16(k1);
+  } else if (tid < half + kPieces) {
+    const int j = tid - half;
+    reinterpret_cast<uint4*>(vnew)[j] =
+        reinterpret_cast<const uint4*>(v_new + static_cast<size_t>(g) * HD)[j];
   }
   __syncthreads();
-
-  float key[HD];
-  if (valid && p != pos) {
-#pragma unroll
-    for (int j = 0; j < kPieces; ++j) {
-      key[8 * j + 0] = bf16_lo(kraw[j].x); key[8 * j + 1] = bf16_hi(kraw[j].x);
-      key[8 * j + 2] = bf16_lo(kraw[j].y); key[8 * j + 3] = bf16_hi(kraw[j].y);
-      key[8 * j + 4] = bf16_lo(kraw[j].z); key[8 * j + 5] = bf16_hi(kraw[j].z);
-      key[8 * j + 6] = bf16_lo(kraw[j].w); key[8 * j + 7] = bf16_hi(kraw[j].w);
-    }
-  } else {
-#pragma unroll
-    for (int d = 0; d < HD; ++d) key[d] = valid ? knew[d] : 0.0f;
+  if (h % group == 0 && pos >= begin && pos < end && tid < 2 * kPieces) {
+    // The kv head's first query head, in the span holding pos, stores the
+    // new token's k and v.
+    const int j = tid % kPieces;
+    uint16_t* dst = (tid < kPieces ? key_cache : value_cache) + head_base +
+                    static_cast<size_t>(pos) * HD;
+    const uint16_t* src = tid < kPieces ? knew : vnew;
+    reinterpret_cast<uint4*>(dst)[j] = reinterpret_cast<const uint4*>(src)[j];
   }
+
   const float scale = 1.0f / sqrtf(static_cast<float>(HD));
-  for (int h = wave; h < group; h += kWaves) {
+  float m = -INFINITY, l = 0.0f;
+  float acc[kDims];
+#pragma unroll
+  for (int j = 0; j < kDims; ++j) acc[j] = 0.0f;
+  for (int t0 = begin + wave * kTile; t0 < end; t0 += W * kTile) {
+    const int p = t0 + lane;
+    uint4 kn[kPieces], vn[kPieces];
+    if (kPrefetch && t0 + W * kTile < end) {
+      load_tile_rows<HD>(kr_rsrc, vr_rsrc, p + W * kTile, kn, vn);
+    }
+    if (p == pos) {
+#pragma unroll
+      for (int j = 0; j < kPieces; ++j) {
+        kr[j] = reinterpret_cast<const uint4*>(knew)[j];
+        vr[j] = reinterpret_cast<const uint4*>(vnew)[j];
+      }
+    }
+    const bool valid = p < end;
     float dot = 0.0f;
 #pragma unroll
-    for (int d = 0; d < HD; ++d) dot = fmaf(qs[h][d], key[d], dot);
-    const float s = valid ? dot * scale : -INFINITY;
-    float m = s;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    const float e = valid ? expf(s - m) : 0.0f;
-    const float l = wave_sum(e);
-    sc[h][lane] = e;
-    if (lane == 0) {
-      mx[h] = m;
-      sm[h] = l;
+    for (int j = 0; j < kPieces; ++j) {
+      dot = fmaf(qs[8 * j + 0], bf16_lo(kr[j].x), dot);
+      dot = fmaf(qs[8 * j + 1], bf16_hi(kr[j].x), dot);
+      dot = fmaf(qs[8 * j + 2], bf16_lo(kr[j].y), dot);
+      dot = fmaf(qs[8 * j + 3], bf16_hi(kr[j].y), dot);
+      dot = fmaf(qs[8 * j + 4], bf16_lo(kr[j].z), dot);
+      dot = fmaf(qs[8 * j + 5], bf16_hi(kr[j].z), dot);
+      dot = fmaf(qs[8 * j + 6], bf16_lo(kr[j].w), dot);
+      dot = fmaf(qs[8 * j + 7], bf16_hi(kr[j].w), dot);
     }
-  }
-  __syncthreads();
-
-  // acc[r][j]: head wave + 4 r, dimension lane + 64 j.
-  float acc[2][kDims];
+    const float sc = valid ? dot * scale : -INFINITY;
+    float bm = sc;
 #pragma unroll
-  for (int r = 0; r < 2; ++r)
+    for (int off = 32; off > 0; off >>= 1) bm = fmaxf(bm, __shfl_xor(bm, off));
+    const float nm = fmaxf(m, bm);
+    const float e = valid ? expf(sc - nm) : 0.0f;
+    const float f = expf(m - nm);  // m = -inf on a wave's first tile: f = 0
+    l = fmaf(l, f, wave_sum(e));
 #pragma unroll
-    for (int j = 0; j < kDims; ++j) acc[r][j] = 0.0f;
-  const int h0 = wave, h1 = wave + kWaves;
-#pragma unroll 4
-  for (int pp = 0; pp < plen; ++pp) {
+    for (int j = 0; j < kDims; ++j) acc[j] *= f;
+    m = nm;
+    et[wave][lane] = e;
 #pragma unroll
-    for (int j = 0; j < kDims; ++j) {
-      const float vd = bf16_to_f32(vt[pp][lane + kWave * j]);
-      if (h0 < group) acc[0][j] = fmaf(sc[h0][pp], vd, acc[0][j]);
-      if (h1 < group) acc[1][j] = fmaf(sc[h1][pp], vd, acc[1][j]);
-    }
-  }
-
-  if (chunks == 1) {
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int h = wave + r * kWaves;
-      if (h < group) {
-#pragma unroll
-        for (int j = 0; j < kDims; ++j) {
-          out[static_cast<size_t>(g * group + h) * HD + lane + kWave * j] =
-              f32_to_bf16(acc[r][j] / sm[h]);
-        }
-      }
-    }
-    return;
-  }
-
-  // Partial layout: [g][chunk][head][kRec] floats.
-  const int max_chunks = (max_seq + kChunk - 1) / kChunk;
-  float* base = partial + static_cast<size_t>(g) * max_chunks * kAttentionMaxGroup * kRec;
-  float* mine = base + static_cast<size_t>(c) * kAttentionMaxGroup * kRec;
-#pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int h = wave + r * kWaves;
-    if (h < group) {
+    for (int j = 0; j < kPieces; ++j) reinterpret_cast<uint4*>(vt[wave][lane])[j] = vr[j];
+    __builtin_amdgcn_wave_barrier();  // the tile is in this wave's LDS slice
+    const int n = min(kTile, end - t0);
+#pragma unroll 8
+    for (int pp = 0; pp < n; ++pp) {
+      const float w = et[wave][pp];
 #pragma unroll
       for (int j = 0; j < kDims; ++j) {
-        __hip_atomic_store(mine + h * kRec + lane + kWave * j, acc[r][j], __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-      }
-      if (lane == 0) {
-        __hip_atomic_store(mine + h * kRec + HD, mx[h], __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(mine + h * kRec + HD + 1, sm[h], __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+        acc[j] = fmaf(w, bf16_to_f32(vt[wave][pp][lane + kWave * j]), acc[j]);
       }
     }
+    __builtin_amdgcn_wave_barrier();  // reads done before the next tile's writes
+    if (kPrefetch) {
+#pragma unroll
+      for (int j = 0; j < kPieces; ++j) {
+        kr[j] = kn[j];
+        vr[j] = vn[j];
+      }
+    } else if (t0 + W * kTile < end) {
+      load_tile_rows<HD>(kr_rsrc, vr_rsrc, p + W * kTile, kr, vr);
+    }
   }
-  __builtin_amdgcn_s_waitcnt(0);
+  if (lane == 0) {
+    wm[wave] = m;
+    wl[wave] = l;
+  }
+#pragma unroll
+  for (int j = 0; j < kDims; ++j) wacc[wave][lane + kWave * j] = acc[j];
   __syncthreads();
-  if (tid == 0) {
-    last = __hip_atomic_fetch_add(counters + g, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-           chunks - 1;
-  }
-  __syncthreads();
-  if (!last) return;
-
-  // Merge the chunks of every head of the group in chunk order.
-  for (int h = wave; h < group; h += kWaves) {
-    float m = -INFINITY;
-    for (int cc = 0; cc < chunks; ++cc) {
-      m = fmaxf(m, __hip_atomic_load(base + (cc * kAttentionMaxGroup + h) * kRec + HD,
-                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  // Merge the waves (idle waves have l = 0) and store the span's partial.
+  if (tid < HD) {
+    float mm = wm[0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) mm = fmaxf(mm, wm[w]);
+    float ll = 0.0f, aa = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const float f = wl[w] > 0.0f ? expf(wm[w] - mm) : 0.0f;
+      ll = fmaf(wl[w], f, ll);
+      aa = fmaf(wacc[w][tid], f, aa);
     }
-    float l = 0.0f;
-    float o[kDims];
-#pragma unroll
-    for (int j = 0; j < kDims; ++j) o[j] = 0.0f;
-    for (int cc = 0; cc < chunks; ++cc) {
-      const float* rec = base + (cc * kAttentionMaxGroup + h) * kRec;
-      const float f = expf(
-          __hip_atomic_load(rec + HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - m);
-      l = fmaf(__hip_atomic_load(rec + HD + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), f, l);
-#pragma unroll
-      for (int j = 0; j < kDims; ++j) {
-        o[j] = fmaf(__hip_atomic_load(rec + lane + kWave * j, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT),
-                    f, o[j]);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < kDims; ++j) {
-      out[static_cast<size_t>(g * group + h) * HD + lane + kWave * j] = f32_to_bf16(o[j] / l);
+    float* rec = partial + (static_cast<size_t>(h) * max_splits + c) * (HD + 2);
+    rec[tid] = aa;
+    if (tid == 0) {
+      rec[HD] = mm;
+      rec[HD + 1] = ll;
     }
   }
-  if (tid == 0) __hip_atomic_store(counters + g, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ----------------------------------------------------- prefill attention --
@@ -503,27 +491,35 @@ void launch_rope_store(uint16_t* q, uint16_t* k, const uint16_t* v, uint16_t* ke
 
 bool attention_head_dim_supported(int head_dim) { return head_dim == 64 || head_dim == 128; }
 
-int attention_decode_chunks(int max_seq) { return (max_seq + kChunk - 1) / kChunk; }
+int attention_span(int max_seq) {
+  // Spans of kAttnWaves 64-position tiles (one tile per wave), widened so
+  // that a context has at most kAttnMaxSplits spans.
+  const int base = kAttnWaves * kTile;
+  const int need = (max_seq + kAttnMaxSplits - 1) / kAttnMaxSplits;
+  const int tiles = (need + base - 1) / base;
+  return base * (tiles > 1 ? tiles : 1);
+}
 
-size_t attention_decode_partial_floats(int kv_heads, int head_dim, int max_seq) {
-  return static_cast<size_t>(kv_heads) * attention_decode_chunks(max_seq) * kAttentionMaxGroup *
-         (head_dim + 2);
+int attention_splits(int max_seq) {
+  const int span = attention_span(max_seq);
+  return (max_seq + span - 1) / span;
 }
 
 void launch_attention_decode(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
                              uint16_t* key_cache, uint16_t* value_cache, const float2* rope,
                              const ModelState* state, int heads, int kv_heads, int head_dim,
-                             int max_seq, float* partial, int* counters, uint16_t* out,
-                             hipStream_t stream) {
-  const dim3 grid(attention_decode_chunks(max_seq), kv_heads);
+                             int max_seq, float* partial, hipStream_t stream) {
+  const int span = attention_span(max_seq);
+  const int splits = attention_splits(max_seq);
+  const dim3 grid(splits, heads), block(kAttnWaves * kWave);
   if (head_dim == 64) {
-    hipLaunchKernelGGL(attention_decode_kernel<64>, grid, dim3(kThreads), 0, stream, q, k_new,
-                       v_new, key_cache, value_cache, rope, state, heads, kv_heads, max_seq,
-                       partial, counters, out);
+    hipLaunchKernelGGL(attention_decode_kernel<64>, grid, block, 0, stream, q, k_new, v_new,
+                       key_cache, value_cache, rope, state, heads, kv_heads, max_seq, span,
+                       splits, partial);
   } else {
-    hipLaunchKernelGGL(attention_decode_kernel<128>, grid, dim3(kThreads), 0, stream, q, k_new,
-                       v_new, key_cache, value_cache, rope, state, heads, kv_heads, max_seq,
-                       partial, counters, out);
+    hipLaunchKernelGGL(attention_decode_kernel<128>, grid, block, 0, stream, q, k_new, v_new,
+                       key_cache, value_cache, rope, state, heads, kv_heads, max_seq, span,
+                       splits, partial);
   }
 }
 

@@ -21,8 +21,6 @@ struct ModelState {
 
 // Head dimensions the attention kernels are built for.
 bool attention_head_dim_supported(int head_dim);
-// Largest query-head group (heads / kv_heads) the decode attention handles.
-constexpr int kAttentionMaxGroup = 8;
 
 void launch_embedding(const uint16_t* table, const int* tokens, int count, int vocab, int hidden,
                       uint16_t* out, hipStream_t stream);
@@ -31,13 +29,18 @@ void launch_rms_norm(const uint16_t* x, const uint16_t* w, uint16_t* out, int ro
 void launch_rope_store(uint16_t* q, uint16_t* k, const uint16_t* v, uint16_t* key_cache,
                        uint16_t* value_cache, const float2* rope, int count, int start,
                        int heads, int kv_heads, int head_dim, int max_seq, hipStream_t stream);
-int attention_decode_chunks(int max_seq);
-size_t attention_decode_partial_floats(int kv_heads, int head_dim, int max_seq);
+// Decode attention split over the context (see attention_decode_kernel):
+// one workgroup per (span, query head), spans of attention_span(max_seq)
+// positions, at most attention_splits(max_seq) of them; partial holds
+// heads x attention_splits() x (head_dim + 2) floats.
+constexpr int kAttnWaves = 4;
+constexpr int kAttnMaxSplits = 8;
+int attention_span(int max_seq);
+int attention_splits(int max_seq);
 void launch_attention_decode(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
                              uint16_t* key_cache, uint16_t* value_cache, const float2* rope,
                              const ModelState* state, int heads, int kv_heads, int head_dim,
-                             int max_seq, float* partial, int* counters, uint16_t* out,
-                             hipStream_t stream);
+                             int max_seq, float* partial, hipStream_t stream);
 void launch_attention_prefill(const uint16_t* q, const uint16_t* key_cache,
                               const uint16_t* value_cache, uint16_t* out, int count, int heads,
                               int kv_heads, int head_dim, int max_seq, hipStream_t stream);

@@ -120,7 +120,7 @@ def _create(cfg_fields, precision=2, max_seq=16, layers=None):
     ((896, 4864, 24, 14, 3, 151936, -1, 1e-6, 1e6), "invalid GQA head counts"),
     ((900, 4864, 24, 14, 2, 151936, -1, 1e-6, 1e6), "invalid attention head dimension"),
     ((128, 256, 1, 4, 1, 64, -1, 1e-6, 1e6), "head_dim 32"),
-    ((2048, 256, 1, 32, 2, 64, -1, 1e-6, 1e6), "group 16"),
+    ((2560, 256, 1, 40, 8, 64, -1, 1e-6, 1e6), "40 attention heads"),
     ((896, 4864, 24, 14, 2, 151936, -1, 1e-6, 0.0), "rope_theta"),
 ])
 def test_model_create_rejects_bad_config_on_host(hip, fields, why):
