@@ -1,26 +1,35 @@
-"""Benchmark of the MI355X Linear hot path.
+"""Benchmark of the MI355X Linear hot path and the decode step around it.
 
-Workload (one step): the decode-time W8A16 GEMVs of one token of a
-Qwen2.5-0.5B-shaped model — 24 layers x the 7 Linear shapes (q 896x896,
-k/v 128x896, o 896x896, gate/up 4864x896, down 896x4864), M = 1, no bias,
-each layer with its own weights, so 168 GEMVs over 370.1 MB of distinct
-int8 weights + BF16 scales (larger than the 256 MB last-level cache, so no
-step is served from cache).  Weights q ~ U{-127..127}, scales
-bf16(|N(0, 0.02)| / 127) per 64-column group, inputs bf16(N(0, 1)); seed 1;
-all resident in HBM before timing.
+Workloads (--workload):
 
-Launch modes (--launch):
-  plan   (default) all 168 independent GEMVs through one grouped plan: one
-         kernel launch per step (infer_hip_w8a16_gemv_plan_launch).
-  calls  168 separate infer_hip_gemv_w8a16 calls, the reference's per-Linear
-         call pattern (src/qwen2.cpp:615-656).
+  e2e (default).  W8A16 greedy decode of a random-init
+      Qwen2.5-0.5B-shaped model (24 layers, hidden 896, 14/2 heads, inter
+      4864, vocab 151936, tied embedding; weights ~N(0, 0.02) exported to
+      group-64 int8 with BF16 scales, norm weights 1, biases 0; seed 4) on
+      the HIP decode runtime: prompt of 512 uniform-random tokens (prefill,
+      not timed), then --steps decode steps (default 511: the 512 generated
+      tokens of config 4 minus the prefill's), max_seq 1024, BF16 KV cache.
+      One step = one decode token (all 24 layers + LM head + argmax),
+      replayed from a captured HIP graph with no host sync between steps.
+      value = decode tokens/s.  The roofline object is for the decode step's
+      dominant kernel (largest time per token), timed launch by launch with
+      HIP events on the model's stream at the middle of the timed context;
+      `linear_gemv_plan` adds config 1's figure (below).  cpu_baseline is
+      the CPU FP32 oracle model (a C restatement of the reference's
+      cpu_ops.cpp + qwen2.cpp CPU path) on the same dequantised weights,
+      config 0's workload (prompt 32, greedy decode), a bounded sample.
 
-Prints ONE JSON line (value = tokens/s, i.e. steps/s).  The roofline object
-is for the dominant kernel: algorithmic bytes per launch / its average
-duration from HIP events recorded around that launch on its stream inside
-the timed region.  cpu_baseline is the CPU FP32 oracle (a C restatement of
-the reference's cpu_ops.cpp linear_fp32) on the same dequantised weights,
-timed on this host for a bounded sample.
+  gemv.  The decode-time W8A16 GEMVs of one token:
+      24 layers x the 7 Linear shapes, 168 GEMVs over 370.1 MB of distinct
+      int8 weights + BF16 scales (more than the 256 MB last-level cache);
+      q ~ U{-127..127}, scales bf16(|N(0, 0.02)| / 127), x bf16(N(0, 1)),
+      seed 1.  --launch plan: one grouped launch per step; calls: 168
+      separate GEMV calls.  value = tokens/s of the Linear layers alone.
+
+  prefill.  One layer's 7 GEMMs at M = --tokens as one
+      grouped launch; value = TFLOP/s.
+
+Prints ONE JSON line.  All inputs are resident in HBM before timing.
 """
 from __future__ import annotations
 
@@ -51,11 +60,18 @@ def gemv_bytes(n: int, k: int, bias: bool = False) -> int:
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default: e2e 511, gemv 200, prefill 200)")
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed steps (default: e2e 1 full generate, else 20)")
     ap.add_argument("--launch", choices=("plan", "calls"), default="plan")
-    ap.add_argument("--workload", choices=("decode", "prefill"), default="decode",
-                    help="decode: config 1 (the headline); prefill: config 3 GEMMs")
+    ap.add_argument("--workload", choices=("e2e", "gemv", "prefill"), default="e2e",
+                    help="e2e: config 4 decode (the headline); gemv: config 1; "
+                         "prefill: config 3 GEMMs")
+    ap.add_argument("--prompt", type=int, default=512, help="e2e prompt length")
+    ap.add_argument("--graph", choices=("on", "off"), default="on",
+                    help="e2e: replay each decode step from a HIP graph (on) or launch its "
+                         "kernels one by one (off; no per-kernel timing, for counter runs)")
     ap.add_argument("--tokens", type=int, default=512, help="prefill M (config 3)")
     ap.add_argument("--dtype", choices=("w8a16", "bf16"), default="w8a16",
                     help="prefill weight type")
@@ -68,7 +84,12 @@ def parse():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="after timing, run one device-to-device copy of this many MiB "
                          "(the known-size reference for rocprofv3 --pmc byte counters)")
-    return ap.parse_args()
+    args = ap.parse_args()
+    if args.steps is None:
+        args.steps = 511 if args.workload == "e2e" else 200
+    if args.warmup is None:
+        args.warmup = 1 if args.workload == "e2e" else 20
+    return args
 
 
 class Layers:
@@ -291,6 +312,178 @@ def prefill_main(args, dev, hip) -> int:
     return 0
 
 
+def e2e_cpu_baseline(cfg, tensors, gpu_model, seconds: float):
+    """Config 0 on the CPU: the FP32 oracle model on the dequantised weights
+    of the GPU run, prompt of 32 uniform-random tokens (seed 0), greedy
+    decode until `seconds` of decode time or 128 tokens.  Also runs the GPU
+    model on the same prompt and reports where the two greedy sequences
+    first differ (near-ties between FP32 and BF16 activations may split
+    them; the per-step agreement is pinned by tests/test_gpu_model.py)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle  # test infrastructure: the CPU baseline leg only
+    import synthetic as S
+    oracle.build()
+    threads = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit():
+        threads = min(threads, int(env))
+    fp32 = S.dequantized_fp32(tensors, cfg)
+    max_seq = 256
+    cpu = oracle.Model(fp32, cfg.num_layers, cfg.hidden_size, cfg.num_heads, cfg.num_kv_heads,
+                       cfg.intermediate_size, cfg.vocab_size, max_seq, cfg.rms_norm_eps,
+                       cfg.rope_theta, threads)
+    prompt = [int(v) for v in np.random.default_rng(0).integers(0, cfg.vocab_size, 32)]
+    t0 = time.perf_counter()
+    tok = cpu.prefill(prompt)
+    prefill_s = time.perf_counter() - t0
+    cpu_tokens = [tok]
+    t0 = time.perf_counter()
+    while len(cpu_tokens) < 128:
+        cpu_tokens.append(cpu.decode(cpu_tokens[-1], len(prompt) + len(cpu_tokens) - 1))
+        if time.perf_counter() - t0 >= seconds:
+            break
+    decode_s = time.perf_counter() - t0
+    steps = len(cpu_tokens) - 1
+    cpu.close()
+    gpu_tokens, _ = gpu_model.generate(prompt, len(cpu_tokens), stop_on_eos=False)
+    first_diff = next((i for i, (a, b) in enumerate(zip(gpu_tokens, cpu_tokens)) if a != b),
+                      None)
+    return {
+        "value": round(steps / decode_s, 3),
+        "unit": "tok/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"config 0 workload: prompt 32 (prefill {32 / prefill_s:.1f} tok/s), then "
+                   f"{steps} greedy decode steps in {decode_s:.1f} s; FP32 C/OpenMP "
+                   f"restatement of cpu_ops.cpp + the qwen2.cpp CPU op order on the "
+                   f"dequantised weights of the GPU run (max_seq {max_seq})"),
+        "greedy_tokens_compared": len(cpu_tokens),
+        "first_divergence_vs_gpu": first_diff,
+    }
+
+
+def e2e_roofline(model, mid: int, ms: float, traffic_path: str):
+    """The decode step's dominant kernel kind (largest time per token), from
+    the model's per-kind graph replays timed with HIP events on its stream
+    (infer_hip_model_kernel_times, which resets the model)."""
+    kt = model.kernel_times(mid, reps=20)
+    per_token_us = {n: us * launches for n, (us, _, launches) in kt.items()}
+    dominant = max(per_token_us, key=per_token_us.get)
+    us, nbytes, launches = kt[dominant]
+    achieved = nbytes / (us * 1e-6) / 1e9
+    traffic = None
+    if os.path.exists(traffic_path):
+        with open(traffic_path) as f:
+            traffic = json.load(f).get(dominant)
+    step_bytes = sum(nb * ln for (_, nb, ln) in kt.values())
+    breakdown = {n: {"us_per_launch": round(u, 2), "launches_per_token": ln,
+                     "us_per_token": round(u * ln, 1), "GBs": round(nb / (u * 1e-6) / 1e9, 1)}
+                 for n, (u, nb, ln) in kt.items()}
+    return {
+        "bound": "hbm",
+        "kernel": f"{dominant} (decode step, W8A16, context {mid + 1})",
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": traffic,
+        "algorithmic_bytes_per_launch": int(nbytes),
+        "avg_launch_us": round(us, 2),
+        "decode_step": {
+            "compulsory_bytes_per_token": int(step_bytes),
+            "step_GBs": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+            "kernels": breakdown,
+        },
+    }
+
+
+def e2e_main(args, dev):
+    import numpy as np
+    import torch
+    import model_hip
+    import synthetic as S
+    cfg = S.QWEN25_0_5B
+    max_seq = 1024
+    steps, prompt_len = args.steps, args.prompt
+    if prompt_len + steps + 1 > max_seq:
+        print(f"bench.py: prompt {prompt_len} + {steps} steps exceeds max_seq {max_seq}",
+              file=sys.stderr)
+        return 2
+    tensors = S.random_model(cfg, "w8a16", seed=4, plain_init=True)
+    graph = args.graph == "on"
+    model = model_hip.Qwen2Model(cfg, tensors, "w8a16", max_sequence_length=max_seq,
+                                 use_graph=graph)
+    prompt = [int(v) for v in np.random.default_rng(4).integers(0, cfg.vocab_size, prompt_len)]
+    for _ in range(args.warmup):
+        model.generate(prompt, steps + 1, stop_on_eos=False)
+    model.reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    first = model.prefill(prompt)
+    ttft_ms = (time.perf_counter() - t0) * 1e3
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    tokens = model.decode_steps(steps)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed * 1e3 / steps
+    mid = prompt_len + steps // 2
+    roofline = None
+    if graph:
+        roofline = e2e_roofline(model, mid, ms, args.traffic)
+    # Config 1 beside it: the 168 Linear GEMVs of a token as one grouped plan.
+    import linear_hip as hip
+    layers = Layers(dev)
+    plan = hip.W8A16GemvPlan(layers.calls)
+    t_plan, _ = time_steps(lambda ev: plan.launch(), 100, 10)
+    plan_ms = t_plan / 100
+    plan_gbs = plan.bytes / (plan_ms * 1e-3) / 1e9
+    plan_line = {
+        "workload": "config 1: 168 W8A16 GEMVs of one token (24 layers x 7 shapes), one "
+                    "grouped launch",
+        "achieved": round(plan_gbs, 1), "unit": "GB/s",
+        "frac": round(plan_gbs / HBM_PEAK_GBS, 4), "avg_launch_us": round(plan_ms * 1e3, 2),
+    }
+    if roofline is not None:
+        roofline["linear_gemv_plan"] = plan_line
+    plan.close()
+    del layers
+    cpu = None
+    if args.cpu_seconds > 0:
+        cpu = e2e_cpu_baseline(cfg, tensors, model, args.cpu_seconds)
+    line = {
+        "metric": METRIC,
+        "value": round(steps / elapsed, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "w8a16: int8 weights x bf16 activations, fp32 accumulate",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"config 4: W8A16 greedy decode, random-init Qwen2.5-0.5B-shaped "
+                         f"model (seed 4), prompt {prompt_len} (prefill untimed: "
+                         f"{ttft_ms:.2f} ms), {steps} decode steps timed, max_seq {max_seq}, "
+                         f"BF16 KV cache, batch 1, "
+                         + ("one HIP graph replay per token" if graph
+                            else "kernels launched one by one")),
+            "parallelism": "single GPU",
+            "first_token": first,
+            "last_token": tokens[-1] if tokens else first,
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+    model.close()
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -305,6 +498,8 @@ def main() -> int:
     torch.cuda.set_device(dev)
     if args.workload == "prefill":
         return prefill_main(args, dev, hip)
+    if args.workload == "e2e":
+        return e2e_main(args, dev)
     layers = Layers(dev)
     plan = hip.W8A16GemvPlan(layers.calls)
     assert abs(plan.bytes - layers.bytes) < 1, (plan.bytes, layers.bytes)

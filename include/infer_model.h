@@ -155,6 +155,23 @@ size_t infer_hip_model_workspace_bytes(const infer_hip_model* model);
 /* The stream every kernel of the model runs on (infer::cuda::Context). */
 hipStream_t infer_hip_model_stream(const infer_hip_model* model);
 
+/* Per-kernel timing of the decode step (the HIP counterpart of the
+ * reference's NVTX profiling ranges, src/qwen2.cpp:14-24): the launches of
+ * each kind in one decode step (e.g. the 24 layers' gate|up GEMVs) are
+ * captured as a graph and replayed `reps` times between two HIP events on
+ * the model's stream, at the KV-cache context `position` (1 <= position <=
+ * the model's position).  For kind i (0 <= i < INFER_HIP_MODEL_KERNEL_KINDS,
+ * names from infer_hip_model_kernel_name): us[i] = microseconds per launch
+ * (the kernel plus its share of graph dispatch, as in the decode step),
+ * bytes[i] = its compulsory HBM bytes per launch, launches[i] = launches of
+ * that kind per decode step (0: the kind does not occur).  The replays
+ * overwrite the KV-cache row at `position` and the activations, so the call
+ * ends with the model reset (position 0, not prefilled). */
+#define INFER_HIP_MODEL_KERNEL_KINDS 9
+int infer_hip_model_kernel_times(infer_hip_model* model, int position, int reps, double* us,
+                                 double* bytes, int* launches, int count);
+const char* infer_hip_model_kernel_name(int kind);
+
 #ifdef __cplusplus
 }
 #endif

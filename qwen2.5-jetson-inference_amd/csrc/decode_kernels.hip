@@ -133,30 +133,50 @@ __device__ __forceinline__ NormGemvDesc pick_desc(const NormGemvArgs& a, int b) 
 // y = bf16(W8A16(rms_norm(x)) + bias) for up to three GEMVs on the same
 // normalized input (q|k|v), or with PAIR mlp = bf16(silu(bf16(gate)) *
 // bf16(up)) from the gate (w, s) and up (w2, s2) rows of the same index.
-// Each wave computes one output row; four rows per workgroup.
-template <int SLABS, bool PAIR>
+// Each wave computes R consecutive output rows (all their loads in flight
+// together); 4 R rows per workgroup.
+template <int SLABS, bool PAIR, int R>
 __global__ __launch_bounds__(kBlock) void norm_gemv_w8_kernel(NormGemvArgs a) {
   const NormGemvDesc d = pick_desc(a, blockIdx.x);
   const int lane = threadIdx.x & (kWave - 1);
-  const int row = (blockIdx.x - d.block_begin) * kWaves + threadIdx.x / kWave;
-  const bool ok = row < d.n;
-  uint4 w1[SLABS], w2[SLABS];
-  uint32_t s1[SLABS], s2[SLABS];
-  load_w8_row<SLABS>(d.w, d.s, row, ok, a.k, lane, w1, s1);
-  if (PAIR) load_w8_row<SLABS>(d.w2, d.s2, row, ok, a.k, lane, w2, s2);
+  const int row0 = ((blockIdx.x - d.block_begin) * kWaves + threadIdx.x / kWave) * R;
+  uint4 w1[R][SLABS], w2[R][SLABS];
+  uint32_t s1[R][SLABS], s2[R][SLABS];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const bool ok = row0 + r < d.n;
+    load_w8_row<SLABS>(d.w, d.s, row0 + r, ok, a.k, lane, w1[r], s1[r]);
+    if (PAIR) load_w8_row<SLABS>(d.w2, d.s2, row0 + r, ok, a.k, lane, w2[r], s2[r]);
+  }
   float xn[SLABS][16];
   wave_rms_norm16<SLABS>(a.x, a.norm_w, a.k, a.eps, lane, xn);
-  const float v1 = w8_row_dot<SLABS>(w1, s1, xn);
-  if (PAIR) {
-    const float v2 = w8_row_dot<SLABS>(w2, s2, xn);
-    if (lane == 0 && ok) {
-      const float g = bf16_to_f32(f32_to_bf16(v1));
-      const float u = bf16_to_f32(f32_to_bf16(v2));
-      gstore(d.y + row, f32_to_bf16(g / (1.0f + expf(-g)) * u));
+  float v1[R], v2[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    v1[r] = w8_row_dot<SLABS>(w1[r], s1[r], xn);
+    if (PAIR) v2[r] = w8_row_dot<SLABS>(w2[r], s2[r], xn);
+  }
+  if (lane < R) {
+    // Lane r writes row row0 + r (every lane holds every total).
+    float g = v1[0], u = PAIR ? v2[0] : 0.0f;
+#pragma unroll
+    for (int r = 1; r < R; ++r) {
+      if (lane == r) {
+        g = v1[r];
+        if (PAIR) u = v2[r];
+      }
     }
-  } else if (lane == 0 && ok) {
-    const float b = d.bias ? bf16_to_f32(gload(d.bias + row)) : 0.0f;
-    gstore(d.y + row, f32_to_bf16(v1 + b));
+    const int row = row0 + lane;
+    if (row < d.n) {
+      if (PAIR) {
+        const float gb = bf16_to_f32(f32_to_bf16(g));
+        const float ub = bf16_to_f32(f32_to_bf16(u));
+        gstore(d.y + row, f32_to_bf16(gb / (1.0f + expf(-gb)) * ub));
+      } else {
+        const float b = d.bias ? bf16_to_f32(gload(d.bias + row)) : 0.0f;
+        gstore(d.y + row, f32_to_bf16(g + b));
+      }
+    }
   }
 }
 
@@ -404,22 +424,40 @@ bool norm_gemv_w8_supported(int k) {
   return k >= 64 && k % 64 == 0 && norm_gemv_w8_slabs(k) <= kNormGemvMaxSlabs;
 }
 
-int norm_gemv_blocks(int n) { return (n + kWaves - 1) / kWaves; }
+int norm_gemv_blocks(int n, int rows_per_wave) {
+  const int rows = kWaves * rows_per_wave;
+  return (n + rows - 1) / rows;
+}
+
+template <int SLABS, bool PAIR>
+static void launch_norm_gemv_rows(const NormGemvArgs& a, int blocks, hipStream_t stream) {
+  switch (a.rows_per_wave) {
+    case 4:
+      hipLaunchKernelGGL((norm_gemv_w8_kernel<SLABS, PAIR, 4>), dim3(blocks), dim3(kBlock), 0,
+                         stream, a);
+      break;
+    case 2:
+      hipLaunchKernelGGL((norm_gemv_w8_kernel<SLABS, PAIR, 2>), dim3(blocks), dim3(kBlock), 0,
+                         stream, a);
+      break;
+    default:
+      hipLaunchKernelGGL((norm_gemv_w8_kernel<SLABS, PAIR, 1>), dim3(blocks), dim3(kBlock), 0,
+                         stream, a);
+      break;
+  }
+}
 
 template <bool PAIR>
 static void launch_norm_gemv(const NormGemvArgs& a, int blocks, hipStream_t stream) {
   switch (norm_gemv_w8_slabs(a.k)) {
     case 1:
-      hipLaunchKernelGGL((norm_gemv_w8_kernel<1, PAIR>), dim3(blocks), dim3(kBlock), 0, stream,
-                         a);
+      launch_norm_gemv_rows<1, PAIR>(a, blocks, stream);
       break;
     case 2:
-      hipLaunchKernelGGL((norm_gemv_w8_kernel<2, PAIR>), dim3(blocks), dim3(kBlock), 0, stream,
-                         a);
+      launch_norm_gemv_rows<2, PAIR>(a, blocks, stream);
       break;
     default:
-      hipLaunchKernelGGL((norm_gemv_w8_kernel<4, PAIR>), dim3(blocks), dim3(kBlock), 0, stream,
-                         a);
+      launch_norm_gemv_rows<4, PAIR>(a, blocks, stream);
       break;
   }
 }

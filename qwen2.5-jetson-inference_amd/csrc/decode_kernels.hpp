@@ -9,8 +9,9 @@
 
 namespace qlin {
 
-// One GEMV of a fused RMSNorm + W8A16 GEMV launch.  Rows are 4 per
-// workgroup; block_begin is the launch's first workgroup for this GEMV.
+// One GEMV of a fused RMSNorm + W8A16 GEMV launch.  Rows are 4 x
+// rows_per_wave per workgroup; block_begin is the launch's first workgroup
+// for this GEMV.
 // With the PAIR form, (w, s) are gate_proj, (w2, s2) up_proj and y the
 // SiLU-mul output; bias is unused.
 struct NormGemvDesc {
@@ -33,12 +34,13 @@ struct NormGemvArgs {
   float eps;
   int k;
   int count;
+  int rows_per_wave;  // 1, 2 or 4
   NormGemvDesc d[kNormGemvMaxDescs];
 };
 
 int norm_gemv_w8_slabs(int k);
 bool norm_gemv_w8_supported(int k);
-int norm_gemv_blocks(int n);
+int norm_gemv_blocks(int n, int rows_per_wave);
 void launch_norm_gemv_w8(const NormGemvArgs& a, int blocks, bool pair, hipStream_t stream);
 
 // o-projection fused with the decode attention's split merge and the

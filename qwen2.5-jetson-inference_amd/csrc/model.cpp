@@ -72,6 +72,9 @@ struct Layer {
 // Rows per block of the decode step's grouped GEMVs: one 4-row task per
 // wave, the most blocks a grouped launch can have.
 constexpr int kDecodeRowsPerBlock = 16;
+// Rows (gate|up: row pairs) per wave of the fused RMSNorm + GEMV launches.
+constexpr int kQkvRowsPerWave = 1;
+constexpr int kGateUpRowsPerWave = 1;
 
 constexpr size_t kAlign = 256;
 size_t align_up(size_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
@@ -201,49 +204,151 @@ int lm_head_step(infer_hip_model* m, const uint16_t* row, bool advance) {
   return check_launch("decode step advance");
 }
 
+// Launch kinds of a decode step, for infer_hip_model_kernel_times.
+enum StepKind {
+  kKindEmbedding = 0,
+  kKindNorm,       // RMSNorm (unfused paths)
+  kKindQkv,        // q|k|v GEMV(s) (W8A16: with the RMSNorm)
+  kKindAttention,  // RoPE + KV store + split attention
+  kKindAttnO,      // split merge + o GEMV + residual
+  kKindGateUp,     // gate|up GEMV(s) (W8A16: with the RMSNorm and SiLU-mul)
+  kKindSiluMul,    // SiLU-mul (unfused paths)
+  kKindDown,       // down GEMV + residual
+  kKindLmHead,     // final RMSNorm + LM head + argmax + step bookkeeping
+  kKindCount
+};
+
+const char* const kKindNames[kKindCount] = {
+    "embedding", "rms_norm", "qkv_gemv", "attention", "attn_o_gemv",
+    "gate_up_gemv", "silu_mul", "down_gemv", "lm_head"};
+
 // Enqueue one decode step (src/qwen2.cpp:597-674) on the model's stream.
-int enqueue_decode_step(infer_hip_model* m) {
+// only >= 0 enqueues just the launches of that kind; events (only with
+// `only`) gets one record before the first launch and one after each.
+int enqueue_decode_step(infer_hip_model* m, int only = -1, hipEvent_t* events = nullptr) {
   const infer_hip_model_config& c = m->cfg;
   const int hidden = c.hidden_size;
   hipStream_t s = m->stream;
-  launch_embedding(m->embed, &m->state->token, 1, c.vocab_size, hidden, m->x, s);
+  int recorded = 0;
+  if (events) (void)hipEventRecord(events[recorded++], s);
+  auto run = [&](int kind, auto&& launch) {
+    if (only >= 0 && only != kind) return;
+    launch();
+    if (events) (void)hipEventRecord(events[recorded++], s);
+  };
+  run(kKindEmbedding,
+      [&] { launch_embedding(m->embed, &m->state->token, 1, c.vocab_size, hidden, m->x, s); });
   for (const Layer& L : m->layers) {
     if (m->fused_norm_gemv) {
-      launch_norm_gemv_w8(L.qkv_args, L.qkv_fused_blocks, false, s);
-    } else if (m->w8) {
-      launch_rms_norm(m->x, L.in_norm, m->norm, 1, hidden, c.rms_norm_eps, s);
-      launch_w8a16_gemv_grouped(L.qkv_table, 3, L.qkv_blocks, s);
+      run(kKindQkv, [&] { launch_norm_gemv_w8(L.qkv_args, L.qkv_fused_blocks, false, s); });
     } else {
-      launch_rms_norm(m->x, L.in_norm, m->norm, 1, hidden, c.rms_norm_eps, s);
-      gemv(m, L.q, L.q.b, m->norm, m->q);
-      gemv(m, L.k, L.k.b, m->norm, m->k);
-      gemv(m, L.v, L.v.b, m->norm, m->v);
-    }
-    launch_attention_decode(m->q, m->k, m->v, L.key_cache, L.value_cache, m->rope, m->state,
-                            c.num_heads, c.num_kv_heads, m->head_dim, m->max_seq,
-                            m->attn_partial, s);
-    // x = bf16(Wo attn + x), attn merged from the attention's split partials
-    launch_attn_o_gemv({m->attn_partial, m->state, c.num_heads, m->head_dim,
-                        attention_span(m->max_seq), attention_splits(m->max_seq), m->max_seq,
-                        L.o.w, L.o.s, m->x, hidden, hidden},
-                       m->w8, s);
-    if (m->fused_norm_gemv) {
-      launch_norm_gemv_w8(L.gate_up_args, L.gate_up_fused_blocks, true, s);
-    } else {
-      launch_rms_norm(m->x, L.post_norm, m->norm, 1, hidden, c.rms_norm_eps, s);
+      run(kKindNorm,
+          [&] { launch_rms_norm(m->x, L.in_norm, m->norm, 1, hidden, c.rms_norm_eps, s); });
       if (m->w8) {
-        launch_w8a16_gemv_grouped(L.gate_up_table, 2, L.gate_up_blocks, s);
+        run(kKindQkv, [&] { launch_w8a16_gemv_grouped(L.qkv_table, 3, L.qkv_blocks, s); });
       } else {
-        gemv(m, L.gate, nullptr, m->norm, m->gate);
-        gemv(m, L.up, nullptr, m->norm, m->up);
+        run(kKindQkv, [&] { gemv(m, L.q, L.q.b, m->norm, m->q); });
+        run(kKindQkv, [&] { gemv(m, L.k, L.k.b, m->norm, m->k); });
+        run(kKindQkv, [&] { gemv(m, L.v, L.v.b, m->norm, m->v); });
       }
-      launch_silu_mul(m->gate, m->up, m->mlp, c.intermediate_size, s);
     }
-    gemv(m, L.down, m->x, m->mlp, m->x);  // x = bf16(Wd mlp + x)
+    run(kKindAttention, [&] {
+      launch_attention_decode(m->q, m->k, m->v, L.key_cache, L.value_cache, m->rope, m->state,
+                              c.num_heads, c.num_kv_heads, m->head_dim, m->max_seq,
+                              m->attn_partial, s);
+    });
+    // x = bf16(Wo attn + x), attn merged from the attention's split partials
+    run(kKindAttnO, [&] {
+      launch_attn_o_gemv({m->attn_partial, m->state, c.num_heads, m->head_dim,
+                          attention_span(m->max_seq), attention_splits(m->max_seq), m->max_seq,
+                          L.o.w, L.o.s, m->x, hidden, hidden},
+                         m->w8, s);
+    });
+    if (m->fused_norm_gemv) {
+      run(kKindGateUp,
+          [&] { launch_norm_gemv_w8(L.gate_up_args, L.gate_up_fused_blocks, true, s); });
+    } else {
+      run(kKindNorm,
+          [&] { launch_rms_norm(m->x, L.post_norm, m->norm, 1, hidden, c.rms_norm_eps, s); });
+      if (m->w8) {
+        run(kKindGateUp,
+            [&] { launch_w8a16_gemv_grouped(L.gate_up_table, 2, L.gate_up_blocks, s); });
+      } else {
+        run(kKindGateUp, [&] { gemv(m, L.gate, nullptr, m->norm, m->gate); });
+        run(kKindGateUp, [&] { gemv(m, L.up, nullptr, m->norm, m->up); });
+      }
+      run(kKindSiluMul,
+          [&] { launch_silu_mul(m->gate, m->up, m->mlp, c.intermediate_size, s); });
+    }
+    run(kKindDown, [&] { gemv(m, L.down, m->x, m->mlp, m->x); });  // x = bf16(Wd mlp + x)
   }
   int rc = check_launch("decode step");
   if (rc != INFER_HIP_OK) return rc;
-  return lm_head_step(m, m->x, true);
+  run(kKindLmHead, [&] { rc = lm_head_step(m, m->x, only < 0); });
+  return rc;
+}
+
+// Compulsory HBM bytes of one decode step's launches of `kind` at context
+// length ctx (positions [0, ctx)), and how many launches the step has.
+double kind_bytes(const infer_hip_model* m, int kind, int ctx, int* launches) {
+  const infer_hip_model_config& c = m->cfg;
+  const double H = c.hidden_size, I = c.intermediate_size, V = c.vocab_size;
+  const double KV = m->kv_dim, hd = m->head_dim, nl = c.num_layers;
+  const double wb = m->w8 ? 1.0 : 2.0;  // weight bytes per element
+  auto linear = [&](double n, double k) {
+    return n * k * wb + (m->w8 ? 2.0 * n * (k / 64) : 0.0);
+  };
+  const double splits = (ctx + attention_span(m->max_seq) - 1) / attention_span(m->max_seq);
+  const double partials = c.num_heads * splits * (hd + 2) * 4;
+  const bool fused = m->fused_norm_gemv;
+  const bool bf16_split = !m->w8;  // separate q, k, v (and gate, up) launches
+  int n = 0;
+  double b = 0.0;
+  switch (kind) {
+    case kKindEmbedding:
+      n = 1;
+      b = 4 * H;
+      break;
+    case kKindNorm:
+      n = fused ? 0 : 2 * c.num_layers;
+      b = n * 6 * H;
+      break;
+    case kKindQkv:
+      n = c.num_layers * (bf16_split ? 3 : 1);
+      b = nl * (linear(H + 2 * KV, H) + 2 * (H + 2 * KV) /* bias */ +
+                2 * (H + 2 * KV) /* out */ + (fused ? 4 * H : 2 * H * (bf16_split ? 3 : 1)));
+      break;
+    case kKindAttention:
+      n = c.num_layers;
+      b = nl * (2 * c.num_kv_heads * (ctx - 1) * hd * 2 /* cached K, V */ +
+                2 * H /* q */ + 4 * KV /* new k, v */ + 4 * KV /* their store */ + partials);
+      break;
+    case kKindAttnO:
+      n = c.num_layers;
+      b = nl * (linear(H, H) + partials + 4 * H);
+      break;
+    case kKindGateUp:
+      n = c.num_layers * (bf16_split ? 2 : 1);
+      b = nl * (2 * linear(I, H) +
+                (fused ? 4 * H + 2 * I : 2 * H * (bf16_split ? 2 : 1) + 4 * I));
+      break;
+    case kKindSiluMul:
+      n = fused ? 0 : c.num_layers;
+      b = n * 6 * I;
+      break;
+    case kKindDown:
+      n = c.num_layers;
+      b = nl * (linear(H, I) + 2 * I + 4 * H);
+      break;
+    case kKindLmHead:
+      n = 1;
+      b = V * H * 2 + 4 * H + 2 * V;
+      break;
+    default:
+      break;
+  }
+  *launches = n;
+  return b;
 }
 
 int ensure_graph(infer_hip_model* m) {
@@ -559,19 +664,22 @@ extern "C" int infer_hip_model_create(const infer_hip_model_config* config,
       host_tables.push_back(desc(L.up, m->norm, m->up, L.gate_up_blocks));
     }
     if (m->fused_norm_gemv) {
-      auto fdesc = [](const Linear& li, const Linear* pair, uint16_t* y, int& blocks) {
+      auto fdesc = [](const Linear& li, const Linear* pair, uint16_t* y, int rows_per_wave,
+                      int& blocks) {
         NormGemvDesc d{static_cast<const int8_t*>(li.w), li.s,
                        pair ? static_cast<const int8_t*>(pair->w) : nullptr,
                        pair ? pair->s : nullptr, li.b, y, li.n, blocks};
-        blocks += norm_gemv_blocks(li.n);
+        blocks += norm_gemv_blocks(li.n, rows_per_wave);
         return d;
       };
-      L.qkv_args = NormGemvArgs{m->x, L.in_norm, c.rms_norm_eps, hidden, 3, {}};
-      L.qkv_args.d[0] = fdesc(L.q, nullptr, m->q, L.qkv_fused_blocks);
-      L.qkv_args.d[1] = fdesc(L.k, nullptr, m->k, L.qkv_fused_blocks);
-      L.qkv_args.d[2] = fdesc(L.v, nullptr, m->v, L.qkv_fused_blocks);
-      L.gate_up_args = NormGemvArgs{m->x, L.post_norm, c.rms_norm_eps, hidden, 1, {}};
-      L.gate_up_args.d[0] = fdesc(L.gate, &L.up, m->mlp, L.gate_up_fused_blocks);
+      L.qkv_args = NormGemvArgs{m->x, L.in_norm, c.rms_norm_eps, hidden, 3, kQkvRowsPerWave, {}};
+      L.qkv_args.d[0] = fdesc(L.q, nullptr, m->q, kQkvRowsPerWave, L.qkv_fused_blocks);
+      L.qkv_args.d[1] = fdesc(L.k, nullptr, m->k, kQkvRowsPerWave, L.qkv_fused_blocks);
+      L.qkv_args.d[2] = fdesc(L.v, nullptr, m->v, kQkvRowsPerWave, L.qkv_fused_blocks);
+      L.gate_up_args =
+          NormGemvArgs{m->x, L.post_norm, c.rms_norm_eps, hidden, 1, kGateUpRowsPerWave, {}};
+      L.gate_up_args.d[0] =
+          fdesc(L.gate, &L.up, m->mlp, kGateUpRowsPerWave, L.gate_up_fused_blocks);
     }
   }
   // Every region the kernels write must lie inside the arena.
@@ -784,4 +892,71 @@ extern "C" size_t infer_hip_model_workspace_bytes(const infer_hip_model* m) {
 
 extern "C" hipStream_t infer_hip_model_stream(const infer_hip_model* m) {
   return m ? m->stream : nullptr;
+}
+
+extern "C" const char* infer_hip_model_kernel_name(int kind) {
+  return kind >= 0 && kind < kKindCount ? kKindNames[kind] : nullptr;
+}
+
+extern "C" int infer_hip_model_kernel_times(infer_hip_model* m, int position, int reps,
+                                            double* us, double* bytes, int* launches,
+                                            int count) {
+  if (!m || !us || !bytes || !launches || count < kKindCount || reps <= 0) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "kernel_times: bad argument");
+  }
+  if (!m->has_prefilled || position < 1 || position >= m->max_seq || position > m->position) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "kernel_times: position must lie in [1, current position] of a prefilled model");
+  }
+  DeviceGuard guard(m->device);
+  hipEvent_t start = nullptr, stop = nullptr;
+  hipError_t st = hipEventCreate(&start);
+  if (st == hipSuccess) st = hipEventCreate(&stop);
+  int rc = st == hipSuccess ? ok() : hip_fail(st, "kernel_times events");
+  for (int kind = 0; kind < kKindCount && rc == INFER_HIP_OK; ++kind) {
+    bytes[kind] = kind_bytes(m, kind, position + 1, &launches[kind]);
+    us[kind] = 0.0;
+    if (launches[kind] == 0) continue;
+    bytes[kind] /= launches[kind];
+    // The kind's launches of one step, captured as a graph (as the decode
+    // step runs them) and replayed `reps` times between two events.
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    st = hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal);
+    if (st != hipSuccess) {
+      rc = hip_fail(st, "kernel_times capture");
+      break;
+    }
+    rc = enqueue_decode_step(m, kind);
+    st = hipStreamEndCapture(m->stream, &graph);
+    if (rc == INFER_HIP_OK && st != hipSuccess) rc = hip_fail(st, "kernel_times capture");
+    if (rc == INFER_HIP_OK) {
+      st = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+      if (st != hipSuccess) rc = hip_fail(st, "kernel_times instantiate");
+    }
+    if (rc == INFER_HIP_OK) {
+      launch_set_state(m->state, m->last_token, position, 0, m->stream);
+      st = hipGraphLaunch(exec, m->stream);  // warm-up
+      if (st == hipSuccess) st = hipEventRecord(start, m->stream);
+      for (int r = 0; r < reps && st == hipSuccess; ++r) st = hipGraphLaunch(exec, m->stream);
+      if (st == hipSuccess) st = hipEventRecord(stop, m->stream);
+      if (st == hipSuccess) st = hipEventSynchronize(stop);
+      float ms = 0.0f;
+      if (st == hipSuccess) st = hipEventElapsedTime(&ms, start, stop);
+      if (st != hipSuccess) {
+        rc = hip_fail(st, "kernel_times");
+      } else {
+        us[kind] = ms * 1e3 / (static_cast<double>(reps) * launches[kind]);
+      }
+    }
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+  }
+  if (start) (void)hipEventDestroy(start);
+  if (stop) (void)hipEventDestroy(stop);
+  // The replays rewrote the KV-cache row at `position` and the activations:
+  // the model needs a fresh prefill.
+  m->position = 0;
+  m->has_prefilled = false;
+  return rc;
 }

@@ -39,7 +39,10 @@ EXPORTED_SYMBOLS = (
     "infer_hip_model_kv_cache_bytes",
     "infer_hip_model_workspace_bytes",
     "infer_hip_model_stream",
+    "infer_hip_model_kernel_times",
+    "infer_hip_model_kernel_name",
 )
+KERNEL_KINDS = 9
 
 
 class _Config(ctypes.Structure):
@@ -117,6 +120,9 @@ def load():
         "infer_hip_model_kv_cache_bytes": ([p], ctypes.c_size_t),
         "infer_hip_model_workspace_bytes": ([p], ctypes.c_size_t),
         "infer_hip_model_stream": ([p], p),
+        "infer_hip_model_kernel_times": ([p, i, i, ctypes.POINTER(ctypes.c_double),
+                                          ctypes.POINTER(ctypes.c_double), ip, i], i),
+        "infer_hip_model_kernel_name": ([i], ctypes.c_char_p),
     }
     for name, (args, res) in sigs.items():
         fn = getattr(lib, name)
@@ -259,6 +265,22 @@ class Qwen2Model:
     @property
     def stream(self) -> int:
         return self._lib.infer_hip_model_stream(self._h) or 0
+
+    def kernel_times(self, position: int, reps: int = 3) -> dict:
+        """Per launch kind of the decode step: {name: (us per launch, bytes per
+        launch, launches per step)}, timed with HIP events on the model's
+        stream at KV context `position` (infer_hip_model_kernel_times)."""
+        n = KERNEL_KINDS
+        us = (ctypes.c_double * n)()
+        nb = (ctypes.c_double * n)()
+        ln = (ctypes.c_int * n)()
+        _check(self._lib.infer_hip_model_kernel_times(self._h, position, reps, us, nb, ln, n))
+        out = {}
+        for k in range(n):
+            if ln[k]:
+                name = self._lib.infer_hip_model_kernel_name(k).decode()
+                out[name] = (us[k], nb[k], ln[k])
+        return out
 
     def close(self) -> None:
         if getattr(self, "_h", None):

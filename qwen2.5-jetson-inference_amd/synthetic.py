@@ -102,10 +102,12 @@ def linear_shapes(c: ModelConfig):
 
 
 def random_model(c: ModelConfig, precision: str = "w8a16", seed: int = 4,
-                 std: float = 0.02) -> dict:
-    """Random-init tensors by archive name: Linear weights, biases and the
-    embedding ~ N(0, std), norm weights 1 + N(0, std); W8A16 quantizes the
-    Linear weights as the exporter does, W16A16 stores them as BF16."""
+                 std: float = 0.02, plain_init: bool = False) -> dict:
+    """Random-init tensors by archive name: Linear weights and the embedding
+    ~ N(0, std); norm weights 1 + N(0, std) and biases N(0, std), or with
+    plain_init the initial values of a freshly built model (norm weights 1,
+    biases 0); W8A16 quantizes the Linear weights as the
+    exporter does, W16A16 stores them as BF16."""
     if precision not in ("w8a16", "w16a16"):
         raise ValueError("precision must be w8a16 or w16a16")
     rng = np.random.default_rng(seed)
@@ -113,13 +115,17 @@ def random_model(c: ModelConfig, precision: str = "w8a16", seed: int = 4,
     def normal(*shape):
         return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std))
 
+    def norm_weight():
+        return float32_to_bf16_bits(np.ones(c.hidden_size, np.float32) if plain_init
+                                    else 1 + normal(c.hidden_size))
+
     t = {"model.embed_tokens.weight": float32_to_bf16_bits(normal(c.vocab_size, c.hidden_size)),
-         "model.norm.weight": float32_to_bf16_bits(1 + normal(c.hidden_size))}
+         "model.norm.weight": norm_weight()}
     shapes = linear_shapes(c)
     for layer in range(c.num_layers):
         p = f"model.layers.{layer}."
-        t[p + "input_layernorm.weight"] = float32_to_bf16_bits(1 + normal(c.hidden_size))
-        t[p + "post_attention_layernorm.weight"] = float32_to_bf16_bits(1 + normal(c.hidden_size))
+        t[p + "input_layernorm.weight"] = norm_weight()
+        t[p + "post_attention_layernorm.weight"] = norm_weight()
         for name in LINEARS:
             w = normal(*shapes[name])
             if precision == "w8a16":
@@ -129,7 +135,9 @@ def random_model(c: ModelConfig, precision: str = "w8a16", seed: int = 4,
             else:
                 t[p + name + ".weight"] = float32_to_bf16_bits(w)
             if name in BIASED:
-                t[p + name + ".bias"] = float32_to_bf16_bits(normal(shapes[name][0]))
+                n = shapes[name][0]
+                t[p + name + ".bias"] = float32_to_bf16_bits(
+                    np.zeros(n, np.float32) if plain_init else normal(n))
     return t
 
 

@@ -294,3 +294,27 @@ def test_qwen25_full_size_teacher_forced(orc, dev):
     assert agree >= 15
     g.close()
     o.close()
+
+
+def test_kernel_times_reports_every_launch_kind_and_resets(dev):
+    t, _ = weights(TINY, "w8a16")
+    g = model_hip.Qwen2Model(TINY, t, "w8a16", max_sequence_length=64)
+    p = prompt(10, TINY.vocab_size, seed=6)
+    ref, _ = g.generate(p, 6, stop_on_eos=False)
+    kt = g.kernel_times(12, reps=2)
+    assert set(kt) == {"embedding", "qkv_gemv", "attention", "attn_o_gemv", "gate_up_gemv",
+                       "down_gemv", "lm_head"}
+    for name, (us, nbytes, launches) in kt.items():
+        assert us > 0 and nbytes > 0
+        assert launches == (1 if name in ("embedding", "lm_head") else TINY.num_layers)
+    assert g.position == 0 and not g.has_prefilled
+    with pytest.raises(model_hip.InferError):
+        g.decode_next(1)
+    again, _ = g.generate(p, 6, stop_on_eos=False)
+    assert again == ref
+    with pytest.raises(model_hip.InferError):
+        g.kernel_times(g.position + 1)  # past the decoded context
+    g.reset()
+    with pytest.raises(model_hip.InferError):
+        g.kernel_times(5)  # not prefilled
+    g.close()
