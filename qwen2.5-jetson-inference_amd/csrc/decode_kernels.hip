@@ -31,92 +31,105 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
 
-// The 16-element activation chunks (lane l: chunk s * 64 + l of slab s) of
-// x and of the norm weight, and the wave's RMSNorm of x rounded to BF16.
-template <int SLABS>
-__device__ __forceinline__ void wave_rms_norm16(const uint16_t* x, const uint16_t* norm_w, int k,
-                                                float eps, int lane, float (&xn)[SLABS][16]) {
-  const int chunks = k >> 4;
-  float nw[SLABS][16];
-#pragma unroll
-  for (int s = 0; s < SLABS; ++s) {
-    const int c = s * kWave + lane;
-    if (c < chunks) {
-      load_x16(x + 16 * c, xn[s]);
-      load_x16(norm_w + 16 * c, nw[s]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) xn[s][e] = nw[s][e] = 0.0f;
-    }
-  }
-  float ss = 0.0f;
-#pragma unroll
-  for (int s = 0; s < SLABS; ++s)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) ss = fmaf(xn[s][e], xn[s][e], ss);
-  ss = wave_sum(ss);
-  const float scale = 1.0f / sqrtf(ss / k + eps);
-#pragma unroll
-  for (int s = 0; s < SLABS; ++s)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) xn[s][e] = bf16_to_f32(f32_to_bf16(xn[s][e] * scale * nw[s][e]));
-}
+// Branch-free loads.  Every load of these kernels is issued unconditionally
+// from a clamped index (a row past the matrix reads its last row, a chunk
+// past K its last chunk) and the value is masked afterwards, so that no
+// branch separates the loads: the compiler would otherwise wait for each
+// branch's loads before leaving it and serialise the weight and activation
+// round trips.  Kernels issue their weight loads first, then the activation
+// loads, then a scheduling barrier, then compute.
 
-// Same for 8-element chunks (BF16 weights: one 16-byte chunk is 8 values).
+// Raw 16-byte chunks of a BF16 vector of k values: 8 values per chunk,
+// lane l holding chunk s * 64 + l of slab s (clamped).
 template <int SLABS>
-__device__ __forceinline__ void wave_rms_norm8(const uint16_t* x, const uint16_t* norm_w, int k,
-                                               float eps, int lane, float (&xn)[SLABS][8]) {
+__device__ __forceinline__ void load_vec8_raw(const uint16_t* v, int k, int lane,
+                                              uint4 (&raw)[SLABS]) {
   const int chunks = k >> 3;
-  float nw[SLABS][8];
 #pragma unroll
   for (int s = 0; s < SLABS; ++s) {
-    const int c = s * kWave + lane;
-    if (c < chunks) {
-      load_x8(x + 8 * c, xn[s]);
-      load_x8(norm_w + 8 * c, nw[s]);
-    } else {
+    raw[s] = load_global16(v + 8 * min(s * kWave + lane, chunks - 1));
+  }
+}
+
+// 16-value chunks: two 16-byte halves per chunk.
+template <int SLABS>
+__device__ __forceinline__ void load_vec16_raw(const uint16_t* v, int k, int lane,
+                                               uint4 (&lo)[SLABS], uint4 (&hi)[SLABS]) {
+  const int chunks = k >> 4;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) xn[s][e] = nw[s][e] = 0.0f;
+  for (int s = 0; s < SLABS; ++s) {
+    const int c = min(s * kWave + lane, chunks - 1);
+    lo[s] = load_global16(v + 16 * c);
+    hi[s] = load_global16(v + 16 * c + 8);
+  }
+}
+
+__device__ __forceinline__ void unpack8(const uint4 w, bool keep, float* out) {
+  out[0] = keep ? bf16_lo(w.x) : 0.0f; out[1] = keep ? bf16_hi(w.x) : 0.0f;
+  out[2] = keep ? bf16_lo(w.y) : 0.0f; out[3] = keep ? bf16_hi(w.y) : 0.0f;
+  out[4] = keep ? bf16_lo(w.z) : 0.0f; out[5] = keep ? bf16_hi(w.z) : 0.0f;
+  out[6] = keep ? bf16_lo(w.w) : 0.0f; out[7] = keep ? bf16_hi(w.w) : 0.0f;
+}
+
+// The wave's RMSNorm of x (chunks of C values, C = 8 or 16, already loaded
+// raw) rounded to BF16, zero past K.
+template <int SLABS, int C>
+__device__ __forceinline__ void wave_rms_norm(const uint4 (&xr)[SLABS][C / 8],
+                                              const uint4 (&nr)[SLABS][C / 8], int k, float eps,
+                                              int lane, float (&xn)[SLABS][C]) {
+  const int chunks = k / C;
+  float nw[SLABS][C];
+#pragma unroll
+  for (int s = 0; s < SLABS; ++s) {
+    const bool keep = s * kWave + lane < chunks;
+#pragma unroll
+    for (int h = 0; h < C / 8; ++h) {
+      unpack8(xr[s][h], keep, &xn[s][8 * h]);
+      unpack8(nr[s][h], true, &nw[s][8 * h]);
     }
   }
   float ss = 0.0f;
 #pragma unroll
   for (int s = 0; s < SLABS; ++s)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) ss = fmaf(xn[s][e], xn[s][e], ss);
+    for (int e = 0; e < C; ++e) ss = fmaf(xn[s][e], xn[s][e], ss);
   ss = wave_sum(ss);
   const float scale = 1.0f / sqrtf(ss / k + eps);
 #pragma unroll
   for (int s = 0; s < SLABS; ++s)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) xn[s][e] = bf16_to_f32(f32_to_bf16(xn[s][e] * scale * nw[s][e]));
+    for (int e = 0; e < C; ++e) xn[s][e] = bf16_to_f32(f32_to_bf16(xn[s][e] * scale * nw[s][e]));
 }
 
-// One row's int8 chunks and group scales (zeros past K or past the rows).
+// Raw int8 chunks and group scales of one row (clamped row and chunks).
 template <int SLABS>
-__device__ __forceinline__ void load_w8_row(const int8_t* w, const uint16_t* s, int row, bool ok,
+__device__ __forceinline__ void load_w8_row(const int8_t* w, const uint16_t* s, int row, int n,
                                             int k, int lane, uint4 (&wq)[SLABS],
                                             uint32_t (&sc)[SLABS]) {
   const int chunks = k >> 4, groups = k >> 6;
+  const int r = min(row, n - 1);
 #pragma unroll
   for (int i = 0; i < SLABS; ++i) {
-    const int c = i * kWave + lane;
-    if (ok && c < chunks) {
-      wq[i] = load_stream16(w + static_cast<size_t>(row) * k + 16 * c);
-      sc[i] = gload(s + static_cast<size_t>(row) * groups + (c >> 2));
-    } else {
-      wq[i] = make_uint4(0, 0, 0, 0);
-      sc[i] = 0;
-    }
+    const int c = min(i * kWave + lane, chunks - 1);
+    wq[i] = load_stream16(w + static_cast<size_t>(r) * k + 16 * c);
+    sc[i] = gload(s + static_cast<size_t>(r) * groups + (c >> 2));
   }
 }
 
+// The row's dot product with the activations, summed over the wave.  The
+// scales of chunks past K (or of a row past the matrix) are taken as 0;
+// the int8 weights are finite, so those chunks add exactly 0.
 template <int SLABS>
 __device__ __forceinline__ float w8_row_dot(const uint4 (&wq)[SLABS], const uint32_t (&sc)[SLABS],
-                                            const float (&xn)[SLABS][16]) {
+                                            const float (&xn)[SLABS][16], bool row_ok, int k,
+                                            int lane) {
+  const int chunks = k >> 4;
   float acc = 0.0f;
 #pragma unroll
-  for (int i = 0; i < SLABS; ++i) acc = fmaf(dot16_i8(wq[i], xn[i]), bf16_to_f32(sc[i]), acc);
+  for (int i = 0; i < SLABS; ++i) {
+    const float scale = row_ok && i * kWave + lane < chunks ? bf16_to_f32(sc[i]) : 0.0f;
+    acc = fmaf(dot16_i8(wq[i], xn[i]), scale, acc);
+  }
   return wave_sum(acc);
 }
 
@@ -144,17 +157,34 @@ __global__ __launch_bounds__(kBlock) void norm_gemv_w8_kernel(NormGemvArgs a) {
   uint32_t s1[R][SLABS], s2[R][SLABS];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const bool ok = row0 + r < d.n;
-    load_w8_row<SLABS>(d.w, d.s, row0 + r, ok, a.k, lane, w1[r], s1[r]);
-    if (PAIR) load_w8_row<SLABS>(d.w2, d.s2, row0 + r, ok, a.k, lane, w2[r], s2[r]);
+    load_w8_row<SLABS>(d.w, d.s, row0 + r, d.n, a.k, lane, w1[r], s1[r]);
+    if (PAIR) load_w8_row<SLABS>(d.w2, d.s2, row0 + r, d.n, a.k, lane, w2[r], s2[r]);
   }
+  uint4 xr[SLABS][2], nr[SLABS][2];
+  {
+    uint4 lo[SLABS], hi[SLABS];
+    load_vec16_raw<SLABS>(a.x, a.k, lane, lo, hi);
+#pragma unroll
+    for (int s = 0; s < SLABS; ++s) {
+      xr[s][0] = lo[s];
+      xr[s][1] = hi[s];
+    }
+    load_vec16_raw<SLABS>(a.norm_w, a.k, lane, lo, hi);
+#pragma unroll
+    for (int s = 0; s < SLABS; ++s) {
+      nr[s][0] = lo[s];
+      nr[s][1] = hi[s];
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every load is in flight
   float xn[SLABS][16];
-  wave_rms_norm16<SLABS>(a.x, a.norm_w, a.k, a.eps, lane, xn);
+  wave_rms_norm<SLABS, 16>(xr, nr, a.k, a.eps, lane, xn);
   float v1[R], v2[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    v1[r] = w8_row_dot<SLABS>(w1[r], s1[r], xn);
-    if (PAIR) v2[r] = w8_row_dot<SLABS>(w2[r], s2[r], xn);
+    const bool ok = row0 + r < d.n;
+    v1[r] = w8_row_dot<SLABS>(w1[r], s1[r], xn, ok, a.k, lane);
+    if (PAIR) v2[r] = w8_row_dot<SLABS>(w2[r], s2[r], xn, ok, a.k, lane);
   }
   if (lane < R) {
     // Lane r writes row row0 + r (every lane holds every total).
@@ -180,6 +210,35 @@ __global__ __launch_bounds__(kBlock) void norm_gemv_w8_kernel(NormGemvArgs a) {
   }
 }
 
+// One W8A16 GEMV row per wave, all K chunks of the row requested at once
+// (lane l: chunks l, l + 64, ...), with the residual add: y[row] =
+// bf16(W[row] . x + bias[row]); bias may alias y (each element is read and
+// then written by the same lane).
+template <int SLABS>
+__global__ __launch_bounds__(kBlock) void gemv_w8_rows_kernel(GemvRowsArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int row = blockIdx.x * kWaves + threadIdx.x / kWave;
+  uint4 wq[SLABS];
+  uint32_t sc[SLABS];
+  load_w8_row<SLABS>(static_cast<const int8_t*>(a.w), a.s, row, a.n, a.k, lane, wq, sc);
+  uint4 lo[SLABS], hi[SLABS];
+  load_vec16_raw<SLABS>(a.x, a.k, lane, lo, hi);
+  __builtin_amdgcn_sched_barrier(0);  // every load is in flight
+  const int chunks = a.k >> 4;
+  float xv[SLABS][16];
+#pragma unroll
+  for (int s = 0; s < SLABS; ++s) {
+    const bool keep = s * kWave + lane < chunks;
+    unpack8(lo[s], keep, &xv[s][0]);
+    unpack8(hi[s], keep, &xv[s][8]);
+  }
+  const float v = w8_row_dot<SLABS>(wq, sc, xv, row < a.n, a.k, lane);
+  if (lane == 0 && row < a.n) {
+    const float b = a.bias ? bf16_to_f32(gload(a.bias + row)) : 0.0f;
+    gstore(a.y + row, f32_to_bf16(v + b));
+  }
+}
+
 // The tied LM head of a decode step: logits = bf16(E rms_norm(x)) with the
 // argmax of the FP32 sums.  A grid of at most lm_head_decode_blocks()
 // workgroups; each wave normalizes x once and walks R-row tasks with a
@@ -200,20 +259,30 @@ __global__ __launch_bounds__(kBlock) void lm_head_decode_kernel(LmHeadDecodeArgs
   int row0 = gw * R;
   uint4 w[R][SLABS], wn[R][SLABS];
   auto load_task = [&](int r0, uint4 (&dst)[R][SLABS]) {
+    // Clamped rows and chunks: past-the-end rows are not written, and past
+    // K the activations are 0.
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int row = r0 + r;
+      const int row = min(r0 + r, a.vocab - 1);
 #pragma unroll
       for (int s = 0; s < SLABS; ++s) {
-        const int c = s * kWave + lane;
-        dst[r][s] = row < a.vocab && c < chunks
-                        ? load_stream16(a.w + static_cast<size_t>(row) * a.k + 8 * c)
-                        : make_uint4(0, 0, 0, 0);
+        const int c = min(s * kWave + lane, chunks - 1);
+        dst[r][s] = load_stream16(a.w + static_cast<size_t>(row) * a.k + 8 * c);
       }
     }
   };
   load_task(row0, w);
-  wave_rms_norm8<SLABS>(a.x, a.norm_w, a.k, a.eps, lane, xn);
+  {
+    uint4 xr[SLABS][1], nr[SLABS][1], raw[SLABS];
+    load_vec8_raw<SLABS>(a.x, a.k, lane, raw);
+#pragma unroll
+    for (int s = 0; s < SLABS; ++s) xr[s][0] = raw[s];
+    load_vec8_raw<SLABS>(a.norm_w, a.k, lane, raw);
+#pragma unroll
+    for (int s = 0; s < SLABS; ++s) nr[s][0] = raw[s];
+    __builtin_amdgcn_sched_barrier(0);  // every load is in flight
+    wave_rms_norm<SLABS, 8>(xr, nr, a.k, a.eps, lane, xn);
+  }
   float best_v = -FLT_MAX;
   int best_i = INT_MAX;
   for (; row0 < a.vocab; row0 += stride) {
@@ -330,15 +399,14 @@ __global__ __launch_bounds__(kBlock) void attn_o_gemv_kernel(AttnOArgs a) {
   uint4 wq[SLABS];
   uint32_t sc[SLABS];
   if (W8) {
-    load_w8_row<SLABS>(static_cast<const int8_t*>(a.w), a.s, row, ok, a.k, lane, wq, sc);
+    load_w8_row<SLABS>(static_cast<const int8_t*>(a.w), a.s, row, a.n, a.k, lane, wq, sc);
   } else {
+    const int r = min(row, a.n - 1);
 #pragma unroll
     for (int i = 0; i < SLABS; ++i) {
-      const int c = i * kWave + lane;
-      wq[i] = ok && c < chunks
-                  ? load_stream16(static_cast<const uint16_t*>(a.w) + static_cast<size_t>(row) * a.k +
-                                  8 * c)
-                  : make_uint4(0, 0, 0, 0);
+      const int c = min(i * kWave + lane, chunks - 1);
+      wq[i] = load_stream16(static_cast<const uint16_t*>(a.w) + static_cast<size_t>(r) * a.k +
+                            8 * c);
     }
   }
   // Partials.
@@ -356,13 +424,13 @@ __global__ __launch_bounds__(kBlock) void attn_o_gemv_kernel(AttnOArgs a) {
           pr, static_cast<uint32_t>(((h * a.max_splits + sp) * rec + d) * 4), 0, 0));
     }
   }
-  float mv = 0.0f, lv = 0.0f;
-  if (tid < a.heads * MAXS) {
-    const int h = tid / MAXS, sp = tid % MAXS;
-    const uint32_t base = static_cast<uint32_t>(((h * a.max_splits + sp) * rec + hd) * 4);
-    mv = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pr, base, 0, 0));
-    lv = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pr, base + 4u, 0, 0));
-  }
+  // (max, sum) of (head tid / MAXS, split tid % MAXS); past the last head the
+  // offsets leave the buffer and read 0.
+  const uint32_t ml = static_cast<uint32_t>(
+      (((tid / MAXS) * a.max_splits + tid % MAXS) * rec + hd) * 4);
+  const float mv = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pr, ml, 0, 0));
+  const float lv = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pr, ml + 4u, 0, 0));
+  __builtin_amdgcn_sched_barrier(0);  // every load is in flight
   const int pos = min(a.state->pos, a.max_seq - 1);
   const int splits = pos / a.span + 1;
   if (tid < a.heads * MAXS) {
@@ -417,6 +485,29 @@ __global__ __launch_bounds__(kBlock) void attn_o_gemv_kernel(AttnOArgs a) {
 }
 
 // ------------------------------------------------------------ launchers --
+
+bool gemv_w8_rows_supported(int k) { return k >= 64 && k % 64 == 0 && k <= 8192; }
+
+void launch_gemv_w8_rows(const GemvRowsArgs& a, hipStream_t stream) {
+  const dim3 grid((a.n + kWaves - 1) / kWaves), block(kBlock);
+  switch ((a.k + 1023) / 1024) {
+#define QLIN_ROWS(S)                                                                    \
+  case S:                                                                               \
+    hipLaunchKernelGGL(gemv_w8_rows_kernel<S>, grid, block, 0, stream, a);              \
+    break;
+    QLIN_ROWS(1)
+    QLIN_ROWS(2)
+    QLIN_ROWS(3)
+    QLIN_ROWS(4)
+    QLIN_ROWS(5)
+    QLIN_ROWS(6)
+    QLIN_ROWS(7)
+    default:
+      hipLaunchKernelGGL(gemv_w8_rows_kernel<8>, grid, block, 0, stream, a);
+      break;
+#undef QLIN_ROWS
+  }
+}
 
 int norm_gemv_w8_slabs(int k) { return (k + 1023) / 1024; }
 

@@ -43,6 +43,22 @@ bool norm_gemv_w8_supported(int k);
 int norm_gemv_blocks(int n, int rows_per_wave);
 void launch_norm_gemv_w8(const NormGemvArgs& a, int blocks, bool pair, hipStream_t stream);
 
+// One W8A16 GEMV row per wave with the whole row's loads in flight at once:
+// y[row] = bf16(W[row] . x + bias[row]), bias may alias y (the residual add).
+// K % 64 == 0, K <= 8192, 16-byte aligned w and x.
+struct GemvRowsArgs {
+  const void* w;         // [n, k] int8
+  const uint16_t* s;     // [n, k / 64] BF16 scales
+  const uint16_t* bias;  // [n] BF16 or nullptr
+  const uint16_t* x;     // [k] BF16
+  uint16_t* y;           // [n] BF16
+  int n;
+  int k;
+};
+
+bool gemv_w8_rows_supported(int k);
+void launch_gemv_w8_rows(const GemvRowsArgs& a, hipStream_t stream);
+
 // o-projection fused with the decode attention's split merge and the
 // residual add (x = bf16(Wo attn + x)).
 constexpr int kAttnOMaxHeads = 32;

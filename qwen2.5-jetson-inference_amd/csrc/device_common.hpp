@@ -53,11 +53,51 @@ __device__ __forceinline__ float sbyte3(uint32_t v) {
   return static_cast<float>(static_cast<int>(v) >> 24);
 }
 
-// Sum over the 64 lanes of a wave; every lane receives the total.
+// Cross-lane moves without LDS.  dpp_from<CTRL> reads v from the lane the
+// DPP control selects within the lane's row of 16 (quad permutes, row
+// mirrors); rows_swapped16 / rows_swapped32 add the value of the lane 16 / 32
+// rows away through gfx950's v_permlane16_swap / v_permlane32_swap: each swap
+// exchanges half of one operand with half of the other, and with both
+// operands = v the two results together hold the lane's row and its partner
+// row, so their sum is the pair's total in every lane.  All lanes of the wave
+// must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_from(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+constexpr int kDppQuadSwap1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int kDppQuadSwap2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+// Sum over the 64 lanes of a wave; every lane receives the total (the same
+// total, summed in a fixed order).
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset);
-  return v;
+  v += dpp_from<kDppQuadSwap1>(v);
+  v += dpp_from<kDppQuadSwap2>(v);
+  v += dpp_from<kDppRowHalfMirror>(v);
+  v += dpp_from<kDppRowMirror>(v);
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false,
+                                                    false);
+  v = __int_as_float(r16[0]) + __int_as_float(r16[1]);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false,
+                                                    false);
+  return __int_as_float(r32[0]) + __int_as_float(r32[1]);
+}
+
+// Maximum over the 64 lanes of a wave; every lane receives it.
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_from<kDppQuadSwap1>(v));
+  v = fmaxf(v, dpp_from<kDppQuadSwap2>(v));
+  v = fmaxf(v, dpp_from<kDppRowHalfMirror>(v));
+  v = fmaxf(v, dpp_from<kDppRowMirror>(v));
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false,
+                                                    false);
+  v = fmaxf(__int_as_float(r16[0]), __int_as_float(r16[1]));
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false,
+                                                    false);
+  return fmaxf(__int_as_float(r32[0]), __int_as_float(r32[1]));
 }
 
 // Reduce RB per-lane partials (one per row) across the wave with a

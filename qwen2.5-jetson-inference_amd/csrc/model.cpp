@@ -280,7 +280,13 @@ int enqueue_decode_step(infer_hip_model* m, int only = -1, hipEvent_t* events = 
       run(kKindSiluMul,
           [&] { launch_silu_mul(m->gate, m->up, m->mlp, c.intermediate_size, s); });
     }
-    run(kKindDown, [&] { gemv(m, L.down, m->x, m->mlp, m->x); });  // x = bf16(Wd mlp + x)
+    run(kKindDown, [&] {  // x = bf16(Wd mlp + x)
+      if (m->w8 && gemv_w8_rows_supported(L.down.k)) {
+        launch_gemv_w8_rows({L.down.w, L.down.s, m->x, m->mlp, m->x, L.down.n, L.down.k}, s);
+      } else {
+        gemv(m, L.down, m->x, m->mlp, m->x);
+      }
+    });
   }
   int rc = check_launch("decode step");
   if (rc != INFER_HIP_OK) return rc;

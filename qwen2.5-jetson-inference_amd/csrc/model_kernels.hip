@@ -276,9 +276,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void attention_decode_kernel(
       dot = fmaf(qs[8 * j + 7], bf16_hi(kr[j].w), dot);
     }
     const float sc = valid ? dot * scale : -INFINITY;
-    float bm = sc;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) bm = fmaxf(bm, __shfl_xor(bm, off));
+    const float bm = wave_max(sc);
     const float nm = fmaxf(m, bm);
     const float e = valid ? expf(sc - nm) : 0.0f;
     const float f = expf(m - nm);  // m = -inf on a wave's first tile: f = 0
@@ -389,9 +387,7 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(
       }
       s = dot * scale;
     }
-    float bm = s;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) bm = fmaxf(bm, __shfl_xor(bm, off));
+    const float bm = wave_max(s);
     const float nm = fmaxf(m, bm);
     const float e = p <= t ? expf(s - nm) : 0.0f;
     const float f = expf(m - nm);  // m = -inf on the first block: f = 0
