@@ -100,30 +100,72 @@ __device__ __forceinline__ float wave_max(float v) {
   return fmaxf(__int_as_float(r32[0]), __int_as_float(r32[1]));
 }
 
+// Sum within each row of 16 lanes; every lane of the row receives it.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_from<kDppQuadSwap1>(v);
+  v += dpp_from<kDppQuadSwap2>(v);
+  v += dpp_from<kDppRowHalfMirror>(v);
+  return v + dpp_from<kDppRowMirror>(v);
+}
+
+// The lanes 32 (16) apart, exchanged between two values: with a and b the
+// values of rows {0,1} and {2,3} (or of rows {0,2} and {1,3}), the sum
+// returned is a's pair total in the lanes that keep a and b's in the others
+// (gfx950 v_permlane32_swap / v_permlane16_swap).
+__device__ __forceinline__ float swap32_sum(float a, float b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(a), __float_as_int(b), false,
+                                                  false);
+  return __int_as_float(r[0]) + __int_as_float(r[1]);
+}
+__device__ __forceinline__ float swap16_sum(float a, float b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_int(a), __float_as_int(b), false,
+                                                  false);
+  return __int_as_float(r[0]) + __int_as_float(r[1]);
+}
+
 // Reduce RB per-lane partials (one per row) across the wave with a
-// reduce-scatter butterfly: after log2(RB) halving steps each lane holds one
-// row, then the remaining offsets finish the sum.  On return vals[0] in every
-// lane holds the total of row `reduced_row(lane)`.
+// reduce-scatter: each halving step hands half of the rows to the lanes 32,
+// then 16, apart (permlane swaps for RB <= 4, shuffles beyond), and the
+// remaining lanes of a group are summed (DPP within rows of 16).  On return
+// vals[0] in every lane holds the total of row `reduced_row(lane)`.  All
+// lanes must be active.
 template <int RB>
 __device__ __forceinline__ void wave_reduce_rows(float (&vals)[RB], int lane) {
   static_assert(RB >= 1 && RB <= 64 && (RB & (RB - 1)) == 0, "RB power of 2");
-  int count = RB;
-  int offset = 32;
+  if constexpr (RB == 1) {
+    vals[0] = wave_sum(vals[0]);
+    return;
+  } else if constexpr (RB == 2) {
+    // lanes 0-31 keep row 0, 32-63 row 1; then the 32 lanes of each half.
+    const float h = swap32_sum(vals[0], vals[1]);
+    vals[0] = row16_sum(swap16_sum(h, h));
+    return;
+  } else if constexpr (RB == 4) {
+    // lanes 0-31 keep rows 0 and 1, 32-63 rows 2 and 3; then rows of 16
+    // lanes: 0-15 / 32-47 keep the even row, 16-31 / 48-63 the odd one.
+    const float a = swap32_sum(vals[0], vals[2]);
+    const float b = swap32_sum(vals[1], vals[3]);
+    vals[0] = row16_sum(swap16_sum(a, b));
+    return;
+  } else {
+    int count = RB;
+    int offset = 32;
 #pragma unroll
-  for (int step = RB; step > 1; step >>= 1) {
-    const int half = count >> 1;
-    const bool upper = (lane & offset) != 0;
+    for (int step = RB; step > 1; step >>= 1) {
+      const int half = count >> 1;
+      const bool upper = (lane & offset) != 0;
 #pragma unroll
-    for (int i = 0; i < step / 2; ++i) {
-      const float send = upper ? vals[i] : vals[i + half];
-      const float keep = upper ? vals[i + half] : vals[i];
-      vals[i] = keep + __shfl_xor(send, offset);
+      for (int i = 0; i < step / 2; ++i) {
+        const float send = upper ? vals[i] : vals[i + half];
+        const float keep = upper ? vals[i + half] : vals[i];
+        vals[i] = keep + __shfl_xor(send, offset);
+      }
+      count = half;
+      offset >>= 1;
     }
-    count = half;
-    offset >>= 1;
-  }
 #pragma unroll
-  for (; offset > 0; offset >>= 1) vals[0] += __shfl_xor(vals[0], offset);
+    for (; offset > 0; offset >>= 1) vals[0] += __shfl_xor(vals[0], offset);
+  }
 }
 
 // Row index (0..RB-1) whose total wave_reduce_rows leaves in this lane.
