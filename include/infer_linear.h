@@ -114,7 +114,8 @@ int infer_hip_gemm_w8a16(const int8_t* weight, const uint16_t* scales,
  * computation as infer_hip_gemm_w8a16 / infer_hip_gemm_bf16 with the
  * workgroup tile of the MFMA kernel named by the caller: tile in
  * [0, infer_hip_gemm_tile_count()) (0 = 128x128, 1 = 128x64, 2 = 64x128,
- * 3 = 64x64, 4 = 32x128 rows x columns of Y), or -1 for the automatic
+ * 3 = 64x64, 4 = 32x128, 5 = 256x128 with 8 waves, rows x columns of Y),
+ * or -1 for the automatic
  * choice the plain entry points make.  For tuning sweeps and for tests
  * that cover every tile.  Shapes outside the MFMA path (tokens == 1,
  * in_features % 64 != 0, unaligned weight or input) ignore tile. */

@@ -158,10 +158,10 @@ struct SplitK {
 // are not last simply exit.
 constexpr int kCoherent = 16;  // buffer cache policy: sc1
 
-template <int FM, int FN>
+template <int FM, int FN, int THREADS = kThreads>
 __device__ __forceinline__ bool splitk_fixup(f32x16_t (&acc)[FM][FN], const SplitK& sp) {
   constexpr int kVec = 4 * FM * FN;  // 16-byte vectors per thread
-  constexpr int kTileBytes = kVec * kThreads * 16;
+  constexpr int kTileBytes = kVec * THREADS * 16;
   __shared__ int last;
   const int tid = threadIdx.x;
   const __amdgpu_buffer_rsrc_t pr =
@@ -177,7 +177,7 @@ __device__ __forceinline__ bool splitk_fixup(f32x16_t (&acc)[FM][FN], const Spli
         const f32x4_t v = {acc[fm][fn][4 * q], acc[fm][fn][4 * q + 1], acc[fm][fn][4 * q + 2],
                            acc[fm][fn][4 * q + 3]};
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), pr,
-                                               mine + (i * kThreads + tid) * 16u, 0, kCoherent);
+                                               mine + (i * THREADS + tid) * 16u, 0, kCoherent);
       }
   __builtin_amdgcn_s_waitcnt(0);  // this thread's parts are stored
   __syncthreads();
@@ -204,7 +204,7 @@ __device__ __forceinline__ bool splitk_fixup(f32x16_t (&acc)[FM][FN], const Spli
           } else {
             v = __builtin_bit_cast(
                 f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                             pr, base + (i * kThreads + tid) * 16u, 0, kCoherent));
+                             pr, base + (i * THREADS + tid) * 16u, 0, kCoherent));
           }
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
@@ -478,6 +478,329 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int m0, int n0,
   }
 }
 
+// ------------------------------------------------------------------------
+// Wide tile: 256 x 128 of Y per workgroup of 8 waves (512 threads), for M
+// of a few hundred rows and more.
+//
+// Why this shape on gfx950.  The MFMA pipe of a SIMD needs two waves to
+// stay busy while one of them waits on LDS, so 8 waves share the CU; each
+// wave owns a 64 x 64 block (2 x 2 tiles of 32 x 32, waves 4 along M x 2
+// along N).  LDS traffic is what bounds a stage here (the fill of a stage is
+// not overlapped with the fragment reads), and the fill bytes per FLOP fall
+// with the tile size: 256 x 128 moves (256 + 128) x 128 B per 4.2 MFLOP.
+// With 256 rows the W8A16 int8 -> BF16 conversion is done once per weight
+// element per 256 rows.
+//
+// LDS rows are padded to 9 chunks of 16 B: the 8 rows that lanes read at one
+// chunk index land in 8 different bank groups, and the k-step index of a
+// fragment read is an immediate offset.  Two buffers of X (256 rows) and W
+// (128 rows): 108 KB.
+//
+// Per stage each wave computes four 4-MFMA chains (one per 32 x 32 tile,
+// k-steps 0..3); under W8A16 each chain starts from zero and is folded into
+// the accumulator with the group scale while the next chain runs, so the
+// product is the exact dequantised q * s, as in gemm_tile.
+constexpr int kWideThreads = 512;
+constexpr int kWideRows = 256;
+constexpr int kWideCols = 128;
+constexpr int kWideRowStride = 9;  // 16-byte chunks per padded LDS row
+// Epilogue staging row (floats): 128 columns + 8 pad, so the two row groups a
+// wave writes at once (rows r and r + 4) fall in disjoint banks.
+constexpr int kWideEpStride = kWideCols + 8;
+constexpr int kWideLdsChunks =
+    (2 * (kWideRows + kWideCols) * kWideRowStride > kWideRows * kWideEpStride / 4)
+        ? 2 * (kWideRows + kWideCols) * kWideRowStride
+        : kWideRows * kWideEpStride / 4;
+
+// 8 int8 -> 8 BF16 (one 16-byte chunk), exact.
+__device__ __forceinline__ uint4 i8x8_to_bf16(const uint2 q) {
+  uint4 o;
+  o.x = pack_hi_halves(sbyte0(q.x), sbyte1(q.x));
+  o.y = pack_hi_halves(sbyte2(q.x), sbyte3(q.x));
+  o.z = pack_hi_halves(sbyte0(q.y), sbyte1(q.y));
+  o.w = pack_hi_halves(sbyte2(q.y), sbyte3(q.y));
+  return o;
+}
+
+__device__ __forceinline__ uint2 buffer_load8(__amdgpu_buffer_rsrc_t r, uint32_t voffset,
+                                              uint32_t soffset) {
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, voffset, soffset, 0));
+}
+
+template <bool W8>
+__device__ __forceinline__ void gemm_wide_tile(const GemmArgs& a, int m0, int n0,
+                                               const SplitK& split = SplitK{}) {
+  constexpr int BM = kWideRows, BN = kWideCols, NT = kWideThreads, RS = kWideRowStride;
+  constexpr int A_LD = BM * kRowChunks / NT;  // X chunks per thread per stage (4)
+  constexpr int B_LD = BN * kRowChunks / NT;  // W chunks per thread per stage (2)
+  // LDS: the two stage buffers of X and W; after the main loop the same
+  // bytes stage the FP32 tile for the epilogue.
+  __shared__ uint4 lds_raw[kWideLdsChunks];
+  uint4 (*lds_a)[BM * RS] = reinterpret_cast<uint4 (*)[BM * RS]>(lds_raw);
+  uint4 (*lds_b)[BN * RS] = reinterpret_cast<uint4 (*)[BN * RS]>(lds_raw + 2 * BM * RS);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 3, wn = wave >> 2;
+  const int r = lane & 31, h = lane >> 5;
+  const int groups = a.k / kStageK;  // scale row stride
+  const int stages = split.count > 0 ? split.count : groups;
+  const int sbeg = split.count > 0 ? split.begin : 0;
+
+  // Branch-free buffer loads as in gemm_tile: rows past M or N read zero.
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, static_cast<uint32_t>(a.m) * a.k * 2u);
+  const __amdgpu_buffer_rsrc_t wr =
+      make_rsrc(a.w, static_cast<uint32_t>(a.n) * a.k * (W8 ? 1u : 2u));
+  const __amdgpu_buffer_rsrc_t sr =
+      make_rsrc(a.s, W8 ? static_cast<uint32_t>(a.n) * groups * 2u : 0u);
+  uint32_t xoff[A_LD], woff[B_LD];
+#pragma unroll
+  for (int i = 0; i < A_LD; ++i) {
+    const int c = tid + NT * i;
+    xoff[i] = ((static_cast<uint32_t>(m0) + (c >> 3)) * a.k + (c & 7) * 8) * 2u;
+  }
+#pragma unroll
+  for (int i = 0; i < B_LD; ++i) {
+    const int c = tid + NT * i;
+    woff[i] = ((static_cast<uint32_t>(n0) + (c >> 3)) * a.k + (c & 7) * 8) * (W8 ? 1u : 2u);
+  }
+  // W8: scale rows of this lane's two output columns
+  uint32_t soff[2];
+#pragma unroll
+  for (int fn = 0; fn < 2; ++fn)
+    soff[fn] = (static_cast<uint32_t>(n0 + wn * 64 + fn * 32 + r) * groups) * 2u;
+  const int fa_base[2] = {(wm * 64 + r) * RS + 4 * h, (wm * 64 + 32 + r) * RS + 4 * h};
+  const int fb_base[2] = {(wn * 64 + r) * RS + 4 * h, (wn * 64 + 32 + r) * RS + 4 * h};
+
+  // Global -> register staging, one slot per stage in flight (2).
+  struct Slot {
+    uint4 a[A_LD];
+    uint4 b[W8 ? 1 : B_LD];  // BF16 W
+    uint2 q[W8 ? B_LD : 1];  // int8 W
+  };
+  Slot sl[2];
+  auto load = [&](int g, Slot& d) {
+    const uint32_t gc = static_cast<uint32_t>(min(g, stages - 1) + sbeg);
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) d.a[i] = buffer_load16(xr, xoff[i], gc * kStageK * 2u);
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i) {
+      if (W8) {
+        d.q[i] = buffer_load8(wr, woff[i], gc * kStageK);
+      } else {
+        d.b[i] = buffer_load16(wr, woff[i], gc * kStageK * 2u);
+      }
+    }
+  };
+  // W8: the group scales of stage g, loaded one stage ahead
+  auto load_scales = [&](int g, uint32_t (&xs)[2]) {
+    if (W8) {
+      const uint32_t gc = static_cast<uint32_t>(min(g, stages - 1) + sbeg);
+#pragma unroll
+      for (int fn = 0; fn < 2; ++fn) {
+        xs[fn] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff[fn], gc * 2u, 0);
+      }
+    }
+  };
+  auto store = [&](int buf, const Slot& d) {
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      const int c = tid + NT * i;
+      lds_a[buf][(c >> 3) * RS + (c & 7)] = d.a[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i) {
+      const int c = tid + NT * i;
+      lds_b[buf][(c >> 3) * RS + (c & 7)] = W8 ? i8x8_to_bf16(d.q[i]) : d.b[i];
+    }
+  };
+
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  typedef bf16x8_t Frag[4];  // k-steps 0..3 of one 32-row fragment
+  auto chain = [&](const Frag& fa, const Frag& fb, f32x16_t& c, bool fresh) {
+    const f32x16_t zero = {};
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[0], fb[0], fresh ? zero : c, 0, 0, 0);
+#pragma unroll
+    for (int ks = 1; ks < 4; ++ks) {
+      c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ks], fb[ks], c, 0, 0, 0);
+    }
+  };
+  auto fold = [&](f32x16_t& dst, const f32x16_t& p, uint32_t s) {
+    const float sc = bf16_to_f32(s);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dst[e] = fmaf(p[e], sc, dst[e]);
+  };
+  // Stage on LDS buffer buf with scales cs; loads stage sg's scales into ns;
+  // the store of the next stage (slot sd into buffer nbuf) and the loads of
+  // stage lg (into slot sd) ride in the MFMA stream.
+  auto compute = [&](int buf, const uint32_t (&cs)[2], uint32_t (&ns)[2], int sg, bool st,
+                     int nbuf, Slot* sd, bool ld, int lg) {
+    load_scales(sg, ns);
+    Frag A0, A1, B0, B1;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      A0[ks] = as_bf16x8(lds_a[buf][fa_base[0] + ks]);
+      B0[ks] = as_bf16x8(lds_b[buf][fb_base[0] + ks]);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) B1[ks] = as_bf16x8(lds_b[buf][fb_base[1] + ks]);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) A1[ks] = as_bf16x8(lds_a[buf][fa_base[1] + ks]);
+    if (W8) {
+      f32x16_t p0, p1;
+      chain(A0, B0, p0, true);
+      chain(A0, B1, p1, true);
+      if (st) store(nbuf, *sd);
+      fold(acc[0][0], p0, cs[0]);
+      chain(A1, B0, p0, true);
+      fold(acc[0][1], p1, cs[1]);
+      if (ld) load(lg, *sd);
+      chain(A1, B1, p1, true);
+      fold(acc[1][0], p0, cs[0]);
+      fold(acc[1][1], p1, cs[1]);
+    } else {
+      chain(A0, B0, acc[0][0], false);
+      chain(A0, B1, acc[0][1], false);
+      if (st) store(nbuf, *sd);
+      chain(A1, B0, acc[1][0], false);
+      if (ld) load(lg, *sd);
+      chain(A1, B1, acc[1][1], false);
+    }
+  };
+
+  // Stage g: LDS buffer g & 1, register slot g & 1.  Iteration g computes
+  // stage g, stores stage g + 1 (slot (g + 1) & 1, loaded two iterations
+  // ago) into the other buffer — last read in iteration g - 1, before the
+  // barrier that ended it — and reloads slot g & 1 with stage g + 2.  The
+  // main loop is unrolled by two so buffer and slot indices are constants
+  // and the vmcnt waits the compiler derives stay partial.
+  uint32_t csa[2] = {0u, 0u}, csb[2] = {0u, 0u};
+  load_scales(0, csa);
+  load(0, sl[0]);
+  load(1, sl[1]);
+  store(0, sl[0]);
+  load(2, sl[0]);
+  __syncthreads();
+  int g = 0;
+  for (; g + 2 < stages; g += 2) {
+    compute(0, csa, csb, g + 1, true, 1, &sl[1], true, g + 3);
+    __syncthreads();
+    compute(1, csb, csa, g + 2, true, 0, &sl[0], true, g + 4);
+    __syncthreads();
+  }
+  {
+    const bool more = g + 1 < stages;
+    compute(0, csa, csb, g + 1, more, 1, &sl[1], false, 0);
+    if (more) {
+      __syncthreads();
+      compute(1, csb, csa, g + 2, false, 0, &sl[0], false, 0);
+    }
+  }
+
+  if (split.parts > 1 && !splitk_fixup<2, 2, NT>(acc, split)) return;
+
+  // Epilogue through LDS: the FP32 tile is staged row-major (element e of
+  // tile (fm, fn) is row 8 (e / 4) + 4 h + e % 4, column r of that tile),
+  // then each thread adds the bias to 8 consecutive columns of a row and
+  // writes them as one 16-byte BF16 store.  Scattered 2-byte stores of the
+  // accumulator layout cost several microseconds per tile.
+  float* ep = reinterpret_cast<float*>(lds_raw);
+  __syncthreads();  // every wave is done with the stage buffers
+#pragma unroll
+  for (int fm = 0; fm < 2; ++fm)
+#pragma unroll
+    for (int fn = 0; fn < 2; ++fn)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = wm * 64 + fm * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+        ep[row * kWideEpStride + wn * 64 + fn * 32 + r] = acc[fm][fn][e];
+      }
+  __syncthreads();
+  constexpr int kChunksPerRow = BN / 8;
+  constexpr int kChunks = BM * kChunksPerRow / NT;  // 8 per thread
+  const int col = (tid % kChunksPerRow) * 8;  // the same for all of a thread's chunks
+  const int n = n0 + col;
+  // All LDS reads first (16-byte aligned: rows are kWideEpStride / 4 chunks
+  // apart), then the stores, so no store waits behind a read.
+  uint4 v[kChunks][2];
+#pragma unroll
+  for (int i = 0; i < kChunks; ++i) {
+    const int row = (tid + NT * i) / kChunksPerRow;
+    const int idx = row * (kWideEpStride / 4) + col / 4;
+    v[i][0] = lds_raw[idx];
+    v[i][1] = lds_raw[idx + 1];
+  }
+  float bias[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    bias[j] = (a.bias && n + j < a.n) ? bf16_to_f32(gload(a.bias + n + j)) : 0.0f;
+  }
+  const bool vec = (a.n % 8) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15u) == 0;
+#pragma unroll
+  for (int i = 0; i < kChunks; ++i) {
+    const int m = m0 + (tid + NT * i) / kChunksPerRow;
+    if (m >= a.m || n >= a.n) continue;
+    float f[8];
+    f[0] = __uint_as_float(v[i][0].x); f[1] = __uint_as_float(v[i][0].y);
+    f[2] = __uint_as_float(v[i][0].z); f[3] = __uint_as_float(v[i][0].w);
+    f[4] = __uint_as_float(v[i][1].x); f[5] = __uint_as_float(v[i][1].y);
+    f[6] = __uint_as_float(v[i][1].z); f[7] = __uint_as_float(v[i][1].w);
+    uint16_t* dst = a.y + static_cast<size_t>(m) * a.n + n;
+    if (vec) {
+      u32x4 o;
+      o.x = pack2_bf16(f[0] + bias[0], f[1] + bias[1]);
+      o.y = pack2_bf16(f[2] + bias[2], f[3] + bias[3]);
+      o.z = pack2_bf16(f[4] + bias[4], f[5] + bias[5]);
+      o.w = pack2_bf16(f[6] + bias[6], f[7] + bias[7]);
+      *(QLIN_GLOBAL u32x4*)(dst) = o;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (n + j < a.n) gstore(dst + j, f32_to_bf16(f[j] + bias[j]));
+      }
+    }
+  }
+}
+
+template <bool W8>
+__global__ __launch_bounds__(kWideThreads) void gemm_wide_kernel(GemmArgs a) {
+  gemm_wide_tile<W8>(a, blockIdx.y * kWideRows, blockIdx.x * kWideCols);
+}
+
+// Grouped form of gemm_wide_kernel (same block -> unit mapping as
+// gemm_grouped_kernel).
+template <bool W8>
+__global__ __launch_bounds__(kWideThreads) void gemm_wide_grouped_kernel(
+    const GemmGroupDesc* __restrict__ descs, int count) {
+  const int b = blockIdx.x;
+  int lo = 0, hi = count - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (descs[mid].block_begin <= b) lo = mid; else hi = mid - 1;
+  }
+  const GemmGroupDesc& d = descs[lo];
+  const int u = b - d.block_begin;
+  const int tile = u / d.splits;
+  const GemmArgs a{d.w, d.s, d.bias, d.x, d.y, d.m, d.n, d.k};
+  SplitK sp;
+  if (d.splits > 1) {
+    const int groups = d.k / kStageK;
+    sp.parts = d.splits;
+    sp.index = u % d.splits;
+    sp.begin = sp.index * d.split_stages;
+    sp.count = min(d.split_stages, groups - sp.begin);
+    sp.partial = d.partial + static_cast<size_t>(tile) * d.splits * (kWideRows * kWideCols);
+    sp.counter = d.counters + tile;
+  }
+  gemm_wide_tile<W8>(a, (tile % d.tiles_m) * kWideRows, (tile / d.tiles_m) * kWideCols, sp);
+}
+
 // Grid: x = N tiles, y = M tiles.
 template <int BM, int BN, int WAVES_M, bool W8>
 __global__ __launch_bounds__(kThreads) QLIN_GEMM_WAVES_ATTR void gemm_mfma_kernel(GemmArgs a) {
@@ -531,6 +854,11 @@ void launch_config(int config, const GemmArgs& a, hipStream_t stream) {
     case kGemmTile64x128: launch_tile<64, 128, 2, W8>(a, stream); break;
     case kGemmTile64x64: launch_tile<64, 64, 2, W8>(a, stream); break;
     case kGemmTile32x128: launch_tile<32, 128, 1, W8>(a, stream); break;
+    case kGemmTile256x128: {
+      const dim3 grid((a.n + kWideCols - 1) / kWideCols, (a.m + kWideRows - 1) / kWideRows);
+      hipLaunchKernelGGL((gemm_wide_kernel<W8>), grid, dim3(kWideThreads), 0, stream, a);
+      break;
+    }
     default: launch_tile<64, 64, 2, W8>(a, stream); break;
   }
 }
@@ -547,28 +875,38 @@ bool gemm_mfma_supported(const void* w, const uint16_t* x, int m, int n, int k) 
 }
 
 int gemm_pick_tile(int m, int n) {
-  // A stage's time grows with the tile's LDS traffic, and at the Qwen
-  // shapes no grid fills the 256 CUs twice over, so the 64 x 64 tile (the
-  // most workgroups, up to 4 per CU) is fastest for every M <= 512 measured;
-  // grids of over 2048 such tiles switch to 128 x 128.
-  const long long t64 = static_cast<long long>((m + 63) / 64) * ((n + 63) / 64);
-  return t64 > 2048 ? kGemmTile128x128 : kGemmTile64x64;
+  // A single GEMM at the Qwen shapes (M <= 512) gives too few 256 x 128
+  // tiles to fill the 256 CUs, so the 64 x 64 tile (the most workgroups, up
+  // to 4 per CU) is fastest there; once the wide tile alone has a workgroup
+  // for (nearly) every CU, its lower LDS traffic per FLOP wins.
+  const long long wide = static_cast<long long>((m + kWideRows - 1) / kWideRows) *
+                         ((n + kWideCols - 1) / kWideCols);
+  if (m >= kWideRows && wide >= 240) return kGemmTile256x128;
+  return kGemmTile64x64;
 }
 
 int gemm_tile_rows(int tile) {
-  static const int rows[kGemmTileCount] = {128, 128, 64, 64, 32};
+  static const int rows[kGemmTileCount] = {128, 128, 64, 64, 32, kWideRows};
   return rows[tile];
 }
 
 int gemm_tile_cols(int tile) {
-  static const int cols[kGemmTileCount] = {128, 64, 128, 64, 128};
+  static const int cols[kGemmTileCount] = {128, 64, 128, 64, 128, kWideCols};
   return cols[tile];
 }
 
 void launch_gemm_grouped(int tile, bool w8, const GemmGroupDesc* device_descs, int count,
                          int total_blocks, hipStream_t stream) {
   const dim3 grid(total_blocks), block(kThreads);
-  if (tile == kGemmTile128x128) {
+  if (tile == kGemmTile256x128) {
+    if (w8) {
+      hipLaunchKernelGGL((gemm_wide_grouped_kernel<true>), grid, dim3(kWideThreads), 0, stream,
+                         device_descs, count);
+    } else {
+      hipLaunchKernelGGL((gemm_wide_grouped_kernel<false>), grid, dim3(kWideThreads), 0,
+                         stream, device_descs, count);
+    }
+  } else if (tile == kGemmTile128x128) {
     if (w8) {
       hipLaunchKernelGGL((gemm_grouped_kernel<128, 128, 2, true>), grid, block, 0, stream,
                          device_descs, count);

@@ -61,7 +61,8 @@ enum GemmTile {
   kGemmTile64x128 = 2,
   kGemmTile64x64 = 3,
   kGemmTile32x128 = 4,
-  kGemmTileCount = 5,
+  kGemmTile256x128 = 5,  // 8 waves; grouped plans at M >= 256
+  kGemmTileCount = 6,
 };
 
 // One GEMM of a grouped launch: its blocks are block_begin ..
@@ -86,7 +87,7 @@ struct GemmGroupDesc {
   int* counters;
 };
 // gemm.hip
-// Grouped launches use kGemmTile64x64 or kGemmTile128x128.
+// Grouped launches use kGemmTile64x64, kGemmTile128x128 or kGemmTile256x128.
 int gemm_tile_rows(int tile);
 int gemm_tile_cols(int tile);
 void launch_gemm_grouped(int tile, bool w8, const GemmGroupDesc* device_descs, int count,

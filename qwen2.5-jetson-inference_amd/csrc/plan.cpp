@@ -141,14 +141,13 @@ extern "C" int infer_hip_gemm_plan_create(const infer_hip_gemm_desc* descs, int 
     return fail(INFER_HIP_INVALID_ARGUMENT, "gemm plan: need at least one descriptor");
   }
   const bool w8 = descs[0].w8a16 != 0;
-  // 128 x 128 tiles move half the LDS bytes per FLOP of 64 x 64 ones; for
-  // BF16 they pay off once every GEMM has rows enough to fill them (M=512
-  // layer plan: 43.1 us against 44.6).  The W8A16 128 x 128 kernel needs
-  // more than 256 registers, so one workgroup per CU: slower (56.2 us
-  // against 46.4).
+  // Once every GEMM has 256 rows or more, the 8-wave 256 x 128 tile: it
+  // moves the fewest LDS bytes per FLOP and runs two waves per SIMD.  Below
+  // that, 64 x 64 tiles (the most workgroups; up to 4 per CU).
   int min_tokens = descs[0].tokens;
   for (int i = 1; i < count; ++i) min_tokens = std::min(min_tokens, descs[i].tokens);
-  const int tile = (!w8 && min_tokens >= 256) ? kGemmTile128x128 : kGemmTile64x64;
+  const int tile = min_tokens >= gemm_tile_rows(kGemmTile256x128) ? kGemmTile256x128
+                                                                   : kGemmTile64x64;
   const int bm = gemm_tile_rows(tile), bn = gemm_tile_cols(tile);
   std::vector<GemmGroupDesc> table;
   table.reserve(count);
@@ -184,10 +183,35 @@ extern "C" int infer_hip_gemm_plan_create(const infer_hip_gemm_desc* descs, int 
   }
   // Split K so that no unit is much longer than the plan's shortest
   // reduction (at least 8 stages of 64): a lone long-K tile would otherwise
-  // be the whole launch's critical path.
-  int min_stages = 1 << 30;
-  for (const GemmGroupDesc& d : table) min_stages = std::min(min_stages, d.k / 64);
-  const int target = std::max(8, min_stages);
+  // be the whole launch's critical path.  With the wide tile every CU holds
+  // one workgroup, so the unit length is raised, if needed, until all units
+  // fit on the device's CUs at once (M = 512 layer: down's 76 stages in 5
+  // parts of 16 instead of 6 of 13, 254 units on 256 CUs).
+  int min_stages = 1 << 30, max_stages = 0;
+  for (const GemmGroupDesc& d : table) {
+    min_stages = std::min(min_stages, d.k / 64);
+    max_stages = std::max(max_stages, d.k / 64);
+  }
+  int target = std::max(8, min_stages);
+  if (tile == kGemmTile256x128) {
+    int device = 0, cus = 0;
+    if (hipGetDevice(&device) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) !=
+            hipSuccess) {
+      return fail(INFER_HIP_RUNTIME_ERROR, "gemm plan: cannot query the device");
+    }
+    auto units_for = [&](int t) {
+      long long u = 0;
+      for (const GemmGroupDesc& d : table) {
+        const int stages = d.k / 64;
+        const int per = (stages + ((stages + t - 1) / t) - 1) / ((stages + t - 1) / t);
+        const int parts = (stages + per - 1) / per;
+        u += static_cast<long long>(d.tiles_m) * ((d.n + bn - 1) / bn) * parts;
+      }
+      return u;
+    };
+    while (target < max_stages && units_for(target) > cus) ++target;
+  }
   size_t partial_floats = 0, counter_count = 0;
   for (GemmGroupDesc& d : table) {
     const int stages = d.k / 64;

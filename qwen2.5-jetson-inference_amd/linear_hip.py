@@ -234,7 +234,7 @@ def gemm_w8a16(weight, scales, group_size, bias, input, output, tokens,
 
 
 # MFMA workgroup tiles (rows x columns of Y) of the explicit-tile entries.
-GEMM_TILES = ("128x128", "128x64", "64x128", "64x64", "32x128")
+GEMM_TILES = ("128x128", "128x64", "64x128", "64x64", "32x128", "256x128")
 
 
 def gemm_tile_count() -> int:

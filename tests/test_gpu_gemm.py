@@ -16,7 +16,7 @@ from helpers import bf16_out, check_close, to_dev, words
 
 pytestmark = pytest.mark.gpu
 
-TILES = range(5)  # infer_hip_gemm_tile_count()
+TILES = range(6)  # infer_hip_gemm_tile_count()
 RAGGED = ((33, 100, 128), (130, 70, 192), (2, 128, 64), (200, 260, 1024), (65, 33, 4864))
 
 
