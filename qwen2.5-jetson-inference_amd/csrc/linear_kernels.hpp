@@ -86,6 +86,30 @@ struct GemmGroupDesc {
   float* partial;
   int* counters;
 };
+// Split-K in the wide-tile grouped launch.  A GEMM whose wide tiles are
+// split over K in `parts` parts writes each part's FP32 tile, row-major
+// 256 x 128, to partial + (tile * parts + part) * 256 * 128 (tile = m_tile
+// + tiles_m * n_tile); a second, reduction launch sums the parts in index
+// order, adds the bias and writes BF16 Y.  Its blocks block_begin ..
+// block_begin + tiles * 16 - 1 cover the GEMM, 16 rows of a tile each.
+struct SplitReduceDesc {
+  const float* partial;
+  const uint16_t* bias;
+  uint16_t* y;
+  int m;
+  int n;
+  int tiles_m;
+  int parts;
+  int block_begin;
+};
+constexpr int kSplitReduceRows = 16;  // rows of a tile per reduction block
+
+// The wide-tile grouped launch (`units` blocks over descs) and, when some
+// GEMM is split, its reduction launch (`reducers` blocks over rdescs).
+void launch_gemm_wide_grouped(bool w8, const GemmGroupDesc* descs, int count, int units,
+                              const SplitReduceDesc* rdescs, int rcount, int reducers,
+                              hipStream_t stream);
+
 // gemm.hip
 // Grouped launches use kGemmTile64x64, kGemmTile128x128 or kGemmTile256x128.
 int gemm_tile_rows(int tile);

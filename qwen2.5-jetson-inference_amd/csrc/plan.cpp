@@ -125,6 +125,9 @@ struct infer_hip_gemm_plan {
   GemmGroupDesc* table = nullptr;  // device memory
   float* partial = nullptr;        // split-K partial tiles (device)
   int* counters = nullptr;         // split-K arrival counters (device, zeroed)
+  SplitReduceDesc* reduce = nullptr;  // split-K reduction table (device; wide tile)
+  int reduce_count = 0;
+  int reduce_blocks = 0;
   int count = 0;
   int blocks = 0;
   int device = 0;
@@ -244,20 +247,43 @@ extern "C" int infer_hip_gemm_plan_create(const infer_hip_gemm_desc* descs, int 
   plan->w8 = w8;
   plan->tile = tile;
   plan->flops = flops;
+  // Split tiles: with the 64 x 64 tile the last part to arrive (counted on a
+  // per-tile counter) sums the parts inside the launch; the wide tile's
+  // parts are summed by a second, reduction launch spread over many CUs —
+  // one CU reading every part of a 256 x 128 FP32 tile took microseconds.
+  const bool wide = tile == kGemmTile256x128;
+  std::vector<SplitReduceDesc> reduce;
   hipError_t st = hipGetDevice(&plan->device);
   if (st == hipSuccess && partial_floats > 0) {
     st = hipMalloc(&plan->partial, partial_floats * sizeof(float));
-    if (st == hipSuccess) st = hipMalloc(&plan->counters, counter_count * sizeof(int));
-    if (st == hipSuccess) st = hipMemset(plan->counters, 0, counter_count * sizeof(int));
+    if (st == hipSuccess && !wide) {
+      st = hipMalloc(&plan->counters, counter_count * sizeof(int));
+      if (st == hipSuccess) st = hipMemset(plan->counters, 0, counter_count * sizeof(int));
+    }
     size_t pf = 0, cc = 0;
+    int rblocks = 0;
     for (GemmGroupDesc& d : table) {
       if (d.splits <= 1) continue;
       const size_t tiles =
           static_cast<size_t>(d.tiles_m) * ((d.n + bn - 1) / bn);
       d.partial = plan->partial + pf;
-      d.counters = plan->counters + cc;
+      if (!wide) d.counters = plan->counters + cc;
+      if (wide) {
+        reduce.push_back(SplitReduceDesc{d.partial, d.bias, d.y, d.m, d.n, d.tiles_m, d.splits,
+                                         rblocks});
+        rblocks += static_cast<int>(tiles) * (bm / kSplitReduceRows);
+      }
       pf += tiles * d.splits * bm * bn;
       cc += tiles;
+    }
+    plan->reduce_count = static_cast<int>(reduce.size());
+    plan->reduce_blocks = rblocks;
+  }
+  if (st == hipSuccess && !reduce.empty()) {
+    st = hipMalloc(&plan->reduce, reduce.size() * sizeof(SplitReduceDesc));
+    if (st == hipSuccess) {
+      st = hipMemcpy(plan->reduce, reduce.data(), reduce.size() * sizeof(SplitReduceDesc),
+                     hipMemcpyHostToDevice);
     }
   }
   if (st == hipSuccess) st = hipMalloc(&plan->table, table.size() * sizeof(GemmGroupDesc));
@@ -269,6 +295,7 @@ extern "C" int infer_hip_gemm_plan_create(const infer_hip_gemm_desc* descs, int 
     if (plan->table) (void)hipFree(plan->table);
     if (plan->partial) (void)hipFree(plan->partial);
     if (plan->counters) (void)hipFree(plan->counters);
+    if (plan->reduce) (void)hipFree(plan->reduce);
     delete plan;
     return fail(INFER_HIP_RUNTIME_ERROR, "gemm plan: %s", hipGetErrorString(st));
   }
@@ -278,7 +305,12 @@ extern "C" int infer_hip_gemm_plan_create(const infer_hip_gemm_desc* descs, int 
 
 extern "C" int infer_hip_gemm_plan_launch(const infer_hip_gemm_plan* plan, hipStream_t stream) {
   if (!plan) return fail(INFER_HIP_INVALID_ARGUMENT, "gemm plan: null plan");
-  launch_gemm_grouped(plan->tile, plan->w8, plan->table, plan->count, plan->blocks, stream);
+  if (plan->tile == kGemmTile256x128) {
+    launch_gemm_wide_grouped(plan->w8, plan->table, plan->count, plan->blocks, plan->reduce,
+                             plan->reduce_count, plan->reduce_blocks, stream);
+  } else {
+    launch_gemm_grouped(plan->tile, plan->w8, plan->table, plan->count, plan->blocks, stream);
+  }
   return check_launch("gemm plan");
 }
 
@@ -294,6 +326,7 @@ extern "C" int infer_hip_gemm_plan_destroy(infer_hip_gemm_plan* plan) {
   if (st == hipSuccess) st = hipFree(plan->table);
   if (st == hipSuccess && plan->partial) st = hipFree(plan->partial);
   if (st == hipSuccess && plan->counters) st = hipFree(plan->counters);
+  if (st == hipSuccess && plan->reduce) st = hipFree(plan->reduce);
   if (prev != plan->device) (void)hipSetDevice(prev);
   delete plan;
   if (st != hipSuccess) return fail(INFER_HIP_RUNTIME_ERROR, "gemm plan: %s", hipGetErrorString(st));

@@ -123,21 +123,25 @@ def test_gemm_row_matches_gemv(hip, orc, dev):
 @pytest.mark.parametrize("m", (130, 300))
 @pytest.mark.parametrize("w8", (True, False), ids=("w8a16", "bf16"))
 def test_gemm_plan_matches_single_calls(hip, orc, dev, w8, m):
-    # The seven Qwen Linears at M = 130 or 300 (ragged last M tiles; BF16
-    # plans with every M >= 256 use 128 x 128 tiles, others 64 x 64) plus a
-    # ragged N and K, in one launch.  The shortest reduction (K = 192, 3 stages)
-    # makes the plan split every K >= 576 into parts of 8 stages, so this
-    # covers split-K hand-offs (up to 10 parts for K = 4864) next to unsplit
-    # tiles.  Each output equals the oracle, agrees with the single call
-    # (same tile; split tiles add their parts in another order)
+    # The seven Qwen Linears at M = 130 or 300 (ragged last M tiles; plans
+    # with every M >= 256 use the 8-wave 256 x 128 tile, others 64 x 64)
+    # plus ragged-N descriptors with bias, in one launch.  At M = 130 the
+    # shortest reduction (K = 192, 3 stages) makes the plan split every K >=
+    # 576 into parts of 8 stages: split-K hand-offs through arrival counters
+    # (up to 10 parts for K = 4864).  At M = 300 the wide-tile plan raises
+    # the part length until its units fit the CUs, and split tiles (down and
+    # the K = 2048 ragged one, which has a bias) go through the separate
+    # reduction launch.  Each output equals the oracle, agrees with the
+    # single call (same tile; split tiles add their parts in another order)
     # within the reference's GEMV-vs-GEMM bound max(1/64, 1 %)
     # (test_cuda.cpp:604-608), and is bit-identical across launches (the
     # parts are summed in a fixed order whichever finishes last).
     import torch
     rng = rc.philox(110 + w8 + m)
-    tile = 0 if (m >= 256 and not w8) else 3  # the plan's tile, for the single calls
+    tile = 5 if m >= 256 else 3  # the plan's tile, for the single calls
     calls, expected, singles = [], [], []
-    for (name, n, k, bias) in rc.QWEN_LINEARS + (("ragged", 70, 192, True),):
+    extra = (("ragged", 70, 192, True), ("ragged_long", 70, 2048, True))
+    for (name, n, k, bias) in rc.QWEN_LINEARS + extra:
         x = rc.bf16_normal(rng, (m, k))
         b = rc.bf16_normal(rng, (n,)) if bias else None
         dx, db = to_dev(x, dev), (to_dev(b, dev) if bias else None)
