@@ -295,7 +295,9 @@ def prefill_main(args, dev, hip) -> int:
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "gemm_grouped_kernel (7 GEMMs of one layer)",
+            "kernel": ("gemm_wide_grouped_kernel + splitk_reduce_kernel (7 GEMMs of one layer; "
+                       "256 x 128 tiles, down_proj split over K)" if m >= 256 else
+                       "gemm_grouped_kernel (7 GEMMs of one layer; 64 x 64 tiles)"),
             "achieved": round(tflops, 1),
             "peak": MFMA_PEAK_TFLOPS,
             "unit": "TFLOP/s",

@@ -160,7 +160,9 @@ hipStream_t infer_hip_model_stream(const infer_hip_model* model);
  * each kind in one decode step (e.g. the 24 layers' gate|up GEMVs) are
  * captured as a graph and replayed `reps` times between two HIP events on
  * the model's stream, at the KV-cache context `position` (1 <= position <=
- * the model's position).  For kind i (0 <= i < INFER_HIP_MODEL_KERNEL_KINDS,
+ * the model's position); a kind with fewer than 24 launches per step is
+ * captured that many times over, so the graph launch's overhead is shared as
+ * in the decode step.  For kind i (0 <= i < INFER_HIP_MODEL_KERNEL_KINDS,
  * names from infer_hip_model_kernel_name): us[i] = microseconds per launch
  * (the kernel plus its share of graph dispatch, as in the decode step),
  * bytes[i] = its compulsory HBM bytes per launch, launches[i] = launches of
