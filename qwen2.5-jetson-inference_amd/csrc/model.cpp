@@ -29,10 +29,13 @@
 #include <chrono>
 #include <cmath>
 #include <cstring>
+#include <initializer_list>
 #include <new>
+#include <string>
 #include <vector>
 
 #include "decode_kernels.hpp"
+#include "infer_archive.h"
 #include "infer_model.h"
 #include "linear_kernels.hpp"
 #include "model_kernels.hpp"
@@ -104,6 +107,7 @@ struct infer_hip_model {
   size_t arena_bytes = 0;
   size_t kv_bytes = 0;
   int* pinned = nullptr;  // host readback slot (hipHostMalloc)
+  void* owned_weights = nullptr;  // archive upload of infer_hip_model_open, else NULL
 
   ModelState* state = nullptr;
   int* history = nullptr;
@@ -463,6 +467,7 @@ void destroy_model(infer_hip_model* m) {
   if (m->graph) (void)hipGraphDestroy(m->graph);
   if (m->stream) (void)hipStreamSynchronize(m->stream);
   if (m->arena) (void)hipFree(m->arena);
+  if (m->owned_weights) (void)hipFree(m->owned_weights);
   if (m->pinned) (void)hipHostFree(m->pinned);
   if (m->stream) (void)hipStreamDestroy(m->stream);
   delete m;
@@ -720,6 +725,179 @@ extern "C" int infer_hip_model_create(const infer_hip_model_config* config,
 
 extern "C" int infer_hip_model_destroy(infer_hip_model* model) {
   destroy_model(model);
+  return ok();
+}
+
+namespace {
+
+// Closes the archive on every exit of infer_hip_model_open.
+struct ArchiveHandle {
+  infer_hip_archive* a = nullptr;
+  ~ArchiveHandle() { (void)infer_hip_archive_close(a); }
+};
+
+// Record `name` with the given dtype and shape, or an error naming it.
+int expect_record(const infer_hip_archive* a, const std::string& name, int dtype,
+                  std::initializer_list<int64_t> shape, infer_hip_tensor_record* rec) {
+  const int i = infer_hip_archive_find(a, name.c_str());
+  if (i < 0) return fail(INFER_HIP_INVALID_ARGUMENT, "missing tensor: %s", name.c_str());
+  int rc = infer_hip_archive_record(a, i, rec);
+  if (rc != INFER_HIP_OK) return rc;
+  bool same = rec->dtype == dtype && rec->ndim == static_cast<int>(shape.size());
+  int d = 0;
+  for (int64_t v : shape) same = same && rec->shape[d++] == v;
+  if (!same) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "tensor %s: unexpected dtype or shape",
+                name.c_str());
+  }
+  return ok();
+}
+
+}  // namespace
+
+// Qwen2Model::Qwen2Model(model_directory, options) and initialize_weights
+// (src/qwen2.cpp:30-78): every record goes into one device allocation, each
+// at a 256-byte aligned offset in file order; the Linear tensors are then
+// resolved by their archive names (src/qwen2.cpp:606-660) and the scale
+// tensor of a quantised weight through its "quant" record.
+extern "C" int infer_hip_model_open(const char* model_directory,
+                                    const infer_hip_runtime_options* options,
+                                    infer_hip_model** out) {
+  if (!out) return fail(INFER_HIP_INVALID_ARGUMENT, "model: null output pointer");
+  *out = nullptr;
+  if (!model_directory || !options) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "model: null directory or options");
+  }
+  const std::string dir = model_directory;
+  infer_hip_model_config cfg{};
+  int max_positions = 0;
+  int rc = infer_hip_model_config_load((dir + "/config.json").c_str(), &cfg, &max_positions);
+  if (rc != INFER_HIP_OK) return rc;
+  if (options->max_sequence_length <= 0) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "max sequence length must be positive");
+  }
+  if (options->max_sequence_length > max_positions) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "max sequence length exceeds model limit");
+  }
+  const bool w8 = options->precision == INFER_HIP_PRECISION_W8A16;
+  if (!w8 && options->precision != INFER_HIP_PRECISION_W16A16) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "model: precision must be W16A16 or W8A16 (the FP32 path is the CPU's)");
+  }
+  // archive_filename (include/infer/common.hpp:49-55)
+  const std::string file = dir + (w8 ? "/model.w8a16.qbin" : "/model.w16a16.qbin");
+  ArchiveHandle archive;
+  rc = infer_hip_archive_open(file.c_str(), &archive.a);
+  if (rc != INFER_HIP_OK) return rc;
+  const infer_hip_archive* a = archive.a;
+
+  // Device layout: one allocation, each record at a 256-byte aligned offset.
+  const int count = infer_hip_archive_tensor_count(a);
+  std::vector<size_t> offsets(count);
+  size_t total = 0;
+  for (int i = 0; i < count; ++i) {
+    infer_hip_tensor_record r;
+    rc = infer_hip_archive_record(a, i, &r);
+    if (rc != INFER_HIP_OK) return rc;
+    total = align_up(total);
+    offsets[i] = total;
+    total += r.nbytes;
+  }
+
+  const int hidden = cfg.hidden_size, inter = cfg.intermediate_size;
+  const int head_dim = hidden / cfg.num_heads;  // the config loader checked divisibility
+  const int kv_dim = cfg.num_kv_heads * head_dim;
+  infer_hip_model_weights weights{};
+  std::vector<infer_hip_layer_weights> layers(cfg.num_layers);
+  // Resolves every weight the model needs against `base`; run once with
+  // base 0 to validate names, dtypes and shapes before any allocation, then
+  // with the device allocation.
+  auto resolve = [&](uintptr_t base) {
+    infer_hip_tensor_record r;
+    auto at = [&](const infer_hip_tensor_record& rec) {
+      return reinterpret_cast<const void*>(base + offsets[infer_hip_archive_find(a, rec.name)]);
+    };
+    auto bf16_vector = [&](const std::string& name, int64_t n, const uint16_t** p) {
+      const int e = expect_record(a, name, INFER_HIP_DTYPE_BFLOAT16, {n}, &r);
+      if (e == INFER_HIP_OK) *p = static_cast<const uint16_t*>(at(r));
+      return e;
+    };
+    auto linear = [&](const std::string& name, int64_t n, int64_t k, bool bias,
+                      infer_hip_linear* l) {
+      *l = infer_hip_linear{};
+      int e = expect_record(a, name + ".weight",
+                            w8 ? INFER_HIP_DTYPE_INT8 : INFER_HIP_DTYPE_BFLOAT16, {n, k}, &r);
+      if (e != INFER_HIP_OK) return e;
+      l->weight = at(r);
+      if (w8) {
+        if (r.quant_group_size != 64 || r.quant_axis != 1 || !r.scale_tensor) {
+          return fail(INFER_HIP_INVALID_ARGUMENT,
+                      "tensor %s.weight: expected group-64 quantisation", name.c_str());
+        }
+        const std::string scale = r.scale_tensor;
+        e = expect_record(a, scale, INFER_HIP_DTYPE_BFLOAT16, {n, (k + 63) / 64}, &r);
+        if (e != INFER_HIP_OK) return e;
+        l->scales = static_cast<const uint16_t*>(at(r));
+      }
+      return bias ? bf16_vector(name + ".bias", n, &l->bias) : ok();
+    };
+    weights = infer_hip_model_weights{};
+    int e = expect_record(a, "model.embed_tokens.weight", INFER_HIP_DTYPE_BFLOAT16,
+                          {cfg.vocab_size, hidden}, &r);
+    if (e != INFER_HIP_OK) return e;
+    weights.embed_tokens = static_cast<const uint16_t*>(at(r));
+    e = bf16_vector("model.norm.weight", hidden, &weights.norm);
+    if (e == INFER_HIP_OK && infer_hip_archive_find(a, "lm_head.weight") >= 0) {
+      e = expect_record(a, "lm_head.weight", INFER_HIP_DTYPE_BFLOAT16, {cfg.vocab_size, hidden},
+                        &r);
+      if (e == INFER_HIP_OK) weights.lm_head = static_cast<const uint16_t*>(at(r));
+    }
+    for (int l = 0; l < cfg.num_layers && e == INFER_HIP_OK; ++l) {
+      const std::string p = "model.layers." + std::to_string(l) + ".";
+      infer_hip_layer_weights& L = layers[l];
+      e = bf16_vector(p + "input_layernorm.weight", hidden, &L.input_layernorm);
+      if (e == INFER_HIP_OK) {
+        e = bf16_vector(p + "post_attention_layernorm.weight", hidden,
+                        &L.post_attention_layernorm);
+      }
+      if (e == INFER_HIP_OK) e = linear(p + "self_attn.q_proj", hidden, hidden, true, &L.q_proj);
+      if (e == INFER_HIP_OK) e = linear(p + "self_attn.k_proj", kv_dim, hidden, true, &L.k_proj);
+      if (e == INFER_HIP_OK) e = linear(p + "self_attn.v_proj", kv_dim, hidden, true, &L.v_proj);
+      if (e == INFER_HIP_OK) e = linear(p + "self_attn.o_proj", hidden, hidden, false, &L.o_proj);
+      if (e == INFER_HIP_OK) e = linear(p + "mlp.gate_proj", inter, hidden, false, &L.gate_proj);
+      if (e == INFER_HIP_OK) e = linear(p + "mlp.up_proj", inter, hidden, false, &L.up_proj);
+      if (e == INFER_HIP_OK) e = linear(p + "mlp.down_proj", hidden, inter, false, &L.down_proj);
+    }
+    weights.layers = layers.data();
+    return e;
+  };
+  rc = resolve(0);
+  if (rc != INFER_HIP_OK) return rc;
+
+  char* device = nullptr;
+  hipError_t st = hipMalloc(reinterpret_cast<void**>(&device), std::max<size_t>(total, 256));
+  if (st != hipSuccess) return hip_fail(st, "model weight allocation");
+  for (int i = 0; i < count && st == hipSuccess; ++i) {
+    infer_hip_tensor_record r;
+    (void)infer_hip_archive_record(a, i, &r);
+    if (r.nbytes) {
+      st = hipMemcpy(device + offsets[i], infer_hip_archive_data(a, i), r.nbytes,
+                     hipMemcpyHostToDevice);
+    }
+  }
+  if (st != hipSuccess) {
+    (void)hipFree(device);
+    return hip_fail(st, "model weight upload");
+  }
+  rc = resolve(reinterpret_cast<uintptr_t>(device));
+  infer_hip_model* m = nullptr;
+  if (rc == INFER_HIP_OK) rc = infer_hip_model_create(&cfg, &weights, options, &m);
+  if (rc != INFER_HIP_OK) {
+    (void)hipFree(device);
+    return rc;
+  }
+  m->owned_weights = device;
+  *out = m;
   return ok();
 }
 

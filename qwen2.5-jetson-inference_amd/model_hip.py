@@ -123,6 +123,8 @@ def load():
         "infer_hip_model_kernel_times": ([p, i, i, ctypes.POINTER(ctypes.c_double),
                                           ctypes.POINTER(ctypes.c_double), ip, i], i),
         "infer_hip_model_kernel_name": ([i], ctypes.c_char_p),
+        "infer_hip_model_open": ([ctypes.c_char_p, ctypes.POINTER(_Options), ctypes.POINTER(p)],
+                                 i),
     }
     for name, (args, res) in sigs.items():
         fn = getattr(lib, name)
@@ -208,6 +210,30 @@ class Qwen2Model:
         self._lib = lib
         self._h = handle
         self.max_sequence_length = max_sequence_length
+
+    @classmethod
+    def open(cls, model_directory, precision: str = "w8a16", max_sequence_length: int = 2048,
+             use_graph: bool = True) -> "Qwen2Model":
+        """Qwen2Model(model_directory, options) (src/qwen2.cpp:30-78): loads
+        <dir>/config.json and <dir>/model.<precision>.qbin into weights the
+        model owns, on the current device (infer_hip_model_open)."""
+        import os
+        import archive_hip
+        lib = load()
+        if precision not in PRECISIONS:
+            raise InferError(linear_hip.INVALID_ARGUMENT, "precision must be w8a16 or w16a16")
+        self = cls.__new__(cls)
+        self.config, _ = archive_hip.load_config(os.path.join(model_directory, "config.json"))
+        self.precision = precision
+        self._keep = {}
+        opts = _Options(PRECISIONS[precision], max_sequence_length, 1 if use_graph else 0)
+        handle = ctypes.c_void_p()
+        _check(lib.infer_hip_model_open(os.fsencode(os.fspath(model_directory)),
+                                        ctypes.byref(opts), ctypes.byref(handle)))
+        self._lib = lib
+        self._h = handle
+        self.max_sequence_length = max_sequence_length
+        return self
 
     # -- reference surface (include/infer/qwen2.hpp:46-67) --
     def prefill(self, prompt_tokens) -> int:

@@ -141,6 +141,32 @@ def random_model(c: ModelConfig, precision: str = "w8a16", seed: int = 4,
     return t
 
 
+def random_checkpoint(c: ModelConfig, seed: int = 4, std: float = 0.02,
+                      tied: bool = True) -> dict:
+    """Random FP32 checkpoint tensors by archive name, in the order a
+    Hugging Face checkpoint lists them: what the archive exporter reads.
+    With tied=False an lm_head.weight is included."""
+    rng = np.random.default_rng(seed)
+
+    def normal(*shape):
+        return rng.standard_normal(shape, dtype=np.float32) * np.float32(std)
+
+    t = {"model.embed_tokens.weight": normal(c.vocab_size, c.hidden_size)}
+    shapes = linear_shapes(c)
+    for layer in range(c.num_layers):
+        p = f"model.layers.{layer}."
+        t[p + "input_layernorm.weight"] = 1 + normal(c.hidden_size)
+        for name in LINEARS:
+            t[p + name + ".weight"] = normal(*shapes[name])
+            if name in BIASED:
+                t[p + name + ".bias"] = normal(shapes[name][0])
+        t[p + "post_attention_layernorm.weight"] = 1 + normal(c.hidden_size)
+    t["model.norm.weight"] = 1 + normal(c.hidden_size)
+    if not tied:
+        t["lm_head.weight"] = normal(c.vocab_size, c.hidden_size)
+    return t
+
+
 def dequantized_fp32(t: dict, c: ModelConfig) -> dict:
     """The FP32 weights the model computes with (q * bf16 scale, exact in
     FP32; BF16 tensors widened), layer-stacked for a CPU FP32 model."""

@@ -102,6 +102,17 @@ def test_library_exports_every_model_symbol(hip):
     assert sorted(model_hip.EXPORTED_SYMBOLS) == declared
 
 
+def test_library_exports_every_archive_symbol(hip):
+    import archive_hip
+    lib = archive_hip.load()
+    text = open(os.path.join(ROOT, "include", "infer_archive.h")).read()
+    declared = sorted(set(re.findall(r"\b(infer_hip_\w+)\s*\(", text)))
+    assert declared
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert sorted(archive_hip.EXPORTED_SYMBOLS) == declared
+
+
 def _create(cfg_fields, precision=2, max_seq=16, layers=None):
     import ctypes
     import model_hip
