@@ -18,9 +18,10 @@
  *     656-660).  Both are within the model's BF16 tolerance of the FP32
  *     CPU path.
  *
- * Every entry point returns an infer_hip_status (include/infer_linear.h);
- * infer_hip_last_error() has the message.  A model is not thread-safe: one
- * host thread drives it at a time, as the reference's Qwen2Model.
+ * Every entry point that returns int returns a status code of
+ * include/infer_linear.h, with the message in infer_hip_last_error.  A
+ * model is not thread-safe: one host thread drives it at a time, as the
+ * reference's Qwen2Model.
  */
 #ifndef INFER_MODEL_H
 #define INFER_MODEL_H
@@ -151,6 +152,20 @@ int infer_hip_model_has_prefilled(const infer_hip_model* model);
 /* Qwen2Model::kv_cache_bytes / workspace_bytes (include/infer/qwen2.hpp:60-67). */
 size_t infer_hip_model_kv_cache_bytes(const infer_hip_model* model);
 size_t infer_hip_model_workspace_bytes(const infer_hip_model* model);
+
+/* attention_prefill_bf16 (include/infer/cuda_ops.hpp:92-97, src/cuda/
+ * kernels.cu:221-283, 1507-1518): causal attention of token_count queries at
+ * positions 0 .. token_count - 1 over caches [num_kv_heads][max_sequence_length]
+ * [head_dim] already holding those positions; q and output are
+ * [token_count][num_heads][head_dim] BF16, query head h reads kv head
+ * h / (num_heads / num_kv_heads).  The kernel the model's prefill runs: MFMA
+ * tiles of 32 queries x 32 keys when every pointer is 16-byte aligned, an
+ * exact per-query loop otherwise.  head_dim 64 or 128; FP32 softmax and
+ * accumulation, BF16 output.  Stream-ordered, no synchronisation. */
+int infer_hip_attention_prefill_bf16(const uint16_t* q, const uint16_t* key_cache,
+                                     const uint16_t* value_cache, uint16_t* output,
+                                     int token_count, int num_heads, int num_kv_heads,
+                                     int head_dim, int max_sequence_length, hipStream_t stream);
 
 /* The stream every kernel of the model runs on (infer::cuda::Context). */
 hipStream_t infer_hip_model_stream(const infer_hip_model* model);

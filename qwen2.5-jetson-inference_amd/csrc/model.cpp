@@ -1078,6 +1078,29 @@ extern "C" hipStream_t infer_hip_model_stream(const infer_hip_model* m) {
   return m ? m->stream : nullptr;
 }
 
+extern "C" int infer_hip_attention_prefill_bf16(const uint16_t* q, const uint16_t* key_cache,
+                                                const uint16_t* value_cache, uint16_t* output,
+                                                int token_count, int num_heads, int num_kv_heads,
+                                                int head_dim, int max_sequence_length,
+                                                hipStream_t stream) {
+  if (!q || !key_cache || !value_cache || !output) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "attention_prefill: null pointer");
+  }
+  if (token_count <= 0 || token_count > max_sequence_length || num_heads <= 0 ||
+      num_kv_heads <= 0 || num_heads % num_kv_heads != 0) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "attention_prefill: bad shape (tokens %d, heads %d / %d, max_seq %d)",
+                token_count, num_heads, num_kv_heads, max_sequence_length);
+  }
+  if (!attention_head_dim_supported(head_dim)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "attention_prefill: head_dim %d unsupported (64 or 128)",
+                head_dim);
+  }
+  launch_attention_prefill(q, key_cache, value_cache, output, token_count, num_heads,
+                           num_kv_heads, head_dim, max_sequence_length, stream);
+  return check_launch("attention_prefill");
+}
+
 extern "C" const char* infer_hip_model_kernel_name(int kind) {
   return kind >= 0 && kind < kKindCount ? kKindNames[kind] : nullptr;
 }

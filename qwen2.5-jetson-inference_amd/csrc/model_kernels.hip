@@ -339,16 +339,16 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void attention_decode_kernel(
 // ----------------------------------------------------- prefill attention --
 
 // Causal attention of count tokens (positions 0 .. count - 1, already in
-// the caches): one wave per (query token, head), online softmax over the
-// key positions 0 .. t in blocks of 64 (lane p scores key p of the block),
-// then lane d accumulates output dimension d (and d + 64 when HD = 128).
+// the caches), the exact fallback for operands that are not 16-byte
+// aligned: one wave per (query token, head), online softmax over the key
+// positions 0 .. t in blocks of 64 (lane p scores key p of the block), then
+// lane d accumulates output dimension d (and d + 64 when HD = 128).
 template <int HD>
-__global__ __launch_bounds__(kThreads) void attention_prefill_kernel(
+__global__ __launch_bounds__(kThreads) void attention_prefill_scalar_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ key_cache,
     const uint16_t* __restrict__ value_cache, uint16_t* __restrict__ out, int count, int heads,
     int kv_heads, int max_seq) {
   constexpr int kDims = HD / kWave;
-  constexpr int kPieces = HD / 8;
   const int lane = threadIdx.x & (kWave - 1);
   const int item = blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
   if (item >= count * heads) return;
@@ -371,20 +371,11 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(
     const int p = p0 + lane;
     float s = -INFINITY;
     if (p <= t) {
-      const uint4* kr = reinterpret_cast<const uint4*>(kbase + static_cast<size_t>(p) * HD);
+      // 2-byte loads: this kernel serves operands of any (2-byte) alignment
+      const uint16_t* kr = kbase + static_cast<size_t>(p) * HD;
       float dot = 0.0f;
 #pragma unroll
-      for (int j = 0; j < kPieces; ++j) {
-        const uint4 w8 = kr[j];
-        dot = fmaf(qv[8 * j + 0], bf16_lo(w8.x), dot);
-        dot = fmaf(qv[8 * j + 1], bf16_hi(w8.x), dot);
-        dot = fmaf(qv[8 * j + 2], bf16_lo(w8.y), dot);
-        dot = fmaf(qv[8 * j + 3], bf16_hi(w8.y), dot);
-        dot = fmaf(qv[8 * j + 4], bf16_lo(w8.z), dot);
-        dot = fmaf(qv[8 * j + 5], bf16_hi(w8.z), dot);
-        dot = fmaf(qv[8 * j + 6], bf16_lo(w8.w), dot);
-        dot = fmaf(qv[8 * j + 7], bf16_hi(w8.w), dot);
-      }
+      for (int d = 0; d < HD; ++d) dot = fmaf(qv[d], load_bf16(kr + d), dot);
       s = dot * scale;
     }
     const float bm = wave_max(s);
@@ -409,6 +400,232 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(
 #pragma unroll
   for (int j = 0; j < kDims; ++j) {
     out[(static_cast<size_t>(t) * heads + h) * HD + lane + kWave * j] = f32_to_bf16(acc[j] / l);
+  }
+}
+
+// Causal prefill attention on MFMA (v_mfma_f32_32x32x16_bf16).  Workgroup
+// (query block b, head h) takes the 32 queries 32 b .. 32 b + 31; its four
+// waves take the 32-key blocks 0 .. b round robin (block w, w + 4, ...), each
+// with its own online softmax, and are merged in LDS at the end.
+//
+// Per key block a wave computes S^T = K Q^T (keys x queries) rather than
+// S = Q K^T: in the accumulator layout lane (r, h) = (lane % 32, lane / 32)
+// then holds query r and the 16 keys 8 (e / 4) + 4 h + e % 4 (e < 16), so a
+// query's max and sum are 16 in-register values plus one exchange with lane
+// r + 32.  The probabilities are already laid out as the B operand of
+// O^T = V^T P^T (k-step s takes accumulator elements 8 s .. 8 s + 7, i.e. keys
+// 16 s + 4 h + 0..3 and 16 s + 8 + 4 h + 0..3), and O^T's column is the
+// lane's own query, so the online-softmax rescale needs no exchange at all.
+// V^T's A fragments need the same key order per dimension: the block's value
+// rows go through the wave's LDS slice transposed (4 keys packed per
+// 8-byte write), and each fragment is then two 8-byte reads.  P is split
+// into BF16 hi + lo parts (two MFMAs each), so P V keeps about 16 bits of
+// each probability instead of 8: the result stays within a few FP32 ulps of
+// the reference's FP32 loop rather than BF16 rounding of P.
+typedef __bf16 attn_bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 attn_bf16x4_t __attribute__((ext_vector_type(4)));
+typedef float attn_f32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr int kPrefillQueries = 32;     // queries per workgroup
+constexpr int kPrefillWaves = 4;
+constexpr int kPrefillVtStride = 36;    // BF16 words per transposed value row (32 keys + pad)
+
+template <int HD>
+struct alignas(16) PrefillSmem {
+  uint16_t vt[kPrefillWaves][HD * kPrefillVtStride];       // per wave: V^T of one key block
+  float o[kPrefillWaves][HD][kPrefillQueries + 1];         // per wave: O^T at the end
+  float m[kPrefillWaves][kPrefillQueries];
+  float l[kPrefillWaves][kPrefillQueries];
+};
+
+__device__ __forceinline__ float swap32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false,
+                                                  false);
+  return fmaxf(__int_as_float(r[0]), __int_as_float(r[1]));
+}
+
+template <int HD>
+__global__ __launch_bounds__(kThreads) void attention_prefill_mfma_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ key_cache,
+    const uint16_t* __restrict__ value_cache, uint16_t* __restrict__ out, int count, int heads,
+    int kv_heads, int max_seq) {
+  constexpr int KS = HD / 16;          // k-steps of S^T (16 dimensions each)
+  constexpr int DT = HD / 32;          // 32-dimension row tiles of O^T
+  constexpr int kChunks = HD / 8;      // 16-byte chunks per row
+  constexpr int VC = 8 * kChunks / 64; // (key quad, chunk) pairs per lane
+  __shared__ PrefillSmem<HD> sm;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 31, h = lane >> 5;
+  const int qb = blockIdx.x, head = blockIdx.y;
+  const int g = head / (heads / kv_heads);
+  const int q0 = qb * kPrefillQueries;
+  const int query = q0 + r;
+  const float scale = 1.0f / sqrtf(static_cast<float>(HD));
+
+  // Q^T fragments (B of S^T): lane (r, h) holds dimensions 16 ks + 8 h .. + 7
+  // of query r (rows past count are clamped; their results are dropped).
+  attn_bf16x8_t qf[KS];
+  {
+    const uint16_t* qp =
+        q + (static_cast<size_t>(min(query, count - 1)) * heads + head) * HD + 8 * h;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = __builtin_bit_cast(attn_bf16x8_t, load_global16(qp + 16 * ks));
+  }
+  const uint16_t* kbase = key_cache + static_cast<size_t>(g) * max_seq * HD;
+  const uint16_t* vbase = value_cache + static_cast<size_t>(g) * max_seq * HD;
+  uint16_t* vt = sm.vt[wave];
+
+  float m = -INFINITY, l = 0.0f;
+  attn_f32x16_t o[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[dt][e] = 0.0f;
+
+  // Loads of key block kb: K rows (A of S^T, lane (r, h): key r, dimensions
+  // 16 ks + 8 h ..) and the value chunks this lane transposes (pair i:
+  // keys 4 a .. 4 a + 3, dimensions 8 c .. 8 c + 7).  Keys past max_seq are
+  // clamped into the cache; keys past count are masked (K) or zeroed (V).
+  uint4 kr[KS], vr[VC][4];
+  auto load_block = [&](int kb) {
+    const int k0 = kb * 32;
+    const uint16_t* kp = kbase + static_cast<size_t>(min(k0 + r, max_seq - 1)) * HD + 8 * h;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) kr[ks] = load_global16(kp + 16 * ks);
+#pragma unroll
+    for (int i = 0; i < VC; ++i) {
+      const int idx = lane + 64 * i, a = idx / kChunks, c = idx % kChunks;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = k0 + 4 * a + j;
+        vr[i][j] = load_global16(vbase + static_cast<size_t>(min(key, max_seq - 1)) * HD + 8 * c);
+        if (key >= count) vr[i][j] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+
+  int kb = wave;
+  if (kb <= qb) load_block(kb);
+  for (; kb <= qb; kb += kPrefillWaves) {
+    const int k0 = kb * 32;
+    // transpose this block's values into vt[d][key]: 4 keys per 8-byte write
+    __builtin_amdgcn_wave_barrier();  // the previous block's reads are done
+#pragma unroll
+    for (int i = 0; i < VC; ++i) {
+      const int idx = lane + 64 * i, a = idx / kChunks, c = idx % kChunks;
+      const uint32_t w[4][4] = {{vr[i][0].x, vr[i][0].y, vr[i][0].z, vr[i][0].w},
+                                {vr[i][1].x, vr[i][1].y, vr[i][1].z, vr[i][1].w},
+                                {vr[i][2].x, vr[i][2].y, vr[i][2].z, vr[i][2].w},
+                                {vr[i][3].x, vr[i][3].y, vr[i][3].z, vr[i][3].w}};
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {  // dimensions 8 c + 2 p, 8 c + 2 p + 1
+        // selector 0x05040100: low halves of (src1, src0); 0x07060302: high halves
+        const uint32_t lo01 = __builtin_amdgcn_perm(w[1][p], w[0][p], 0x05040100u);
+        const uint32_t lo23 = __builtin_amdgcn_perm(w[3][p], w[2][p], 0x05040100u);
+        const uint32_t hi01 = __builtin_amdgcn_perm(w[1][p], w[0][p], 0x07060302u);
+        const uint32_t hi23 = __builtin_amdgcn_perm(w[3][p], w[2][p], 0x07060302u);
+        *reinterpret_cast<uint2*>(vt + (8 * c + 2 * p) * kPrefillVtStride + 4 * a) =
+            make_uint2(lo01, lo23);
+        *reinterpret_cast<uint2*>(vt + (8 * c + 2 * p + 1) * kPrefillVtStride + 4 * a) =
+            make_uint2(hi01, hi23);
+      }
+    }
+    // S^T = K Q^T
+    attn_f32x16_t st;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) st[e] = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(attn_bf16x8_t, kr[ks]),
+                                                   qf[ks], st, 0, 0, 0);
+    }
+    if (kb + kPrefillWaves <= qb) load_block(kb + kPrefillWaves);  // next block in flight
+    // scale, causal mask, online softmax of query r over this block
+    float bm = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int key = k0 + 8 * (e >> 2) + 4 * h + (e & 3);
+      st[e] = key <= query ? st[e] * scale : -INFINITY;
+      bm = fmaxf(bm, st[e]);
+    }
+    bm = swap32_max(bm);
+    const float mn = fmaxf(m, bm);
+    const float f = expf(m - mn);  // m = -inf on the first block: f = 0
+    float ps = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      st[e] = expf(st[e] - mn);
+      ps += st[e];
+    }
+    ps = swap32_sum(ps, ps);
+    l = fmaf(l, f, ps);
+    m = mn;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[dt][e] *= f;
+    __builtin_amdgcn_wave_barrier();  // vt complete for the whole wave
+    // O^T += V^T (P_hi + P_lo)^T
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      attn_bf16x8_t phi, plo;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float p = st[8 * s + j];
+        const __bf16 hi = static_cast<__bf16>(p);
+        phi[j] = hi;
+        plo[j] = static_cast<__bf16>(p - static_cast<float>(hi));
+      }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const uint16_t* vrow = vt + (32 * dt + r) * kPrefillVtStride + 16 * s + 4 * h;
+        const uint2 v0 = *reinterpret_cast<const uint2*>(vrow);
+        const uint2 v1 = *reinterpret_cast<const uint2*>(vrow + 8);
+        const attn_bf16x8_t va =
+            __builtin_bit_cast(attn_bf16x8_t, make_uint4(v0.x, v0.y, v1.x, v1.y));
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, phi, o[dt], 0, 0, 0);
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, plo, o[dt], 0, 0, 0);
+      }
+    }
+  }
+
+  // merge the waves: O^T element e of tile dt is dimension 32 dt + 8 (e / 4)
+  // + 4 h + e % 4 of query r
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sm.o[wave][32 * dt + 8 * (e >> 2) + 4 * h + (e & 3)][r] = o[dt][e];
+  if (h == 0) {
+    sm.m[wave][r] = m;
+    sm.l[wave][r] = l;
+  }
+  __syncthreads();
+  constexpr int kItems = kPrefillQueries * kChunks;  // (query, 8-dimension chunk)
+#pragma unroll
+  for (int it = threadIdx.x; it < kItems; it += kThreads) {
+    const int qi = it / kChunks, c = it % kChunks;
+    if (q0 + qi >= count) continue;
+    float mm = sm.m[0][qi];
+#pragma unroll
+    for (int w = 1; w < kPrefillWaves; ++w) mm = fmaxf(mm, sm.m[w][qi]);
+    float cw[kPrefillWaves], den = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kPrefillWaves; ++w) {
+      cw[w] = expf(sm.m[w][qi] - mm);  // a wave with no block: m = -inf, weight 0
+      den = fmaf(sm.l[w][qi], cw[w], den);
+    }
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float a = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kPrefillWaves; ++w) a = fmaf(sm.o[w][8 * c + j][qi], cw[w], a);
+      acc[j] = a / den;
+    }
+    uint16_t* dst = out + (static_cast<size_t>(q0 + qi) * heads + head) * HD + 8 * c;
+    *reinterpret_cast<uint4*>(dst) =
+        make_uint4(pack2_bf16(acc[0], acc[1]), pack2_bf16(acc[2], acc[3]),
+                   pack2_bf16(acc[4], acc[5]), pack2_bf16(acc[6], acc[7]));
   }
 }
 
@@ -522,14 +739,28 @@ void launch_attention_decode(const uint16_t* q, const uint16_t* k_new, const uin
 void launch_attention_prefill(const uint16_t* q, const uint16_t* key_cache,
                               const uint16_t* value_cache, uint16_t* out, int count, int heads,
                               int kv_heads, int head_dim, int max_seq, hipStream_t stream) {
+  const bool aligned = ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(key_cache) |
+                         reinterpret_cast<uintptr_t>(value_cache) |
+                         reinterpret_cast<uintptr_t>(out)) & 15u) == 0;
+  if (aligned) {
+    const dim3 grid((count + kPrefillQueries - 1) / kPrefillQueries, heads);
+    if (head_dim == 64) {
+      hipLaunchKernelGGL(attention_prefill_mfma_kernel<64>, grid, dim3(kThreads), 0, stream, q,
+                         key_cache, value_cache, out, count, heads, kv_heads, max_seq);
+    } else {
+      hipLaunchKernelGGL(attention_prefill_mfma_kernel<128>, grid, dim3(kThreads), 0, stream, q,
+                         key_cache, value_cache, out, count, heads, kv_heads, max_seq);
+    }
+    return;
+  }
   const int waves = count * heads;
   const int blocks = (waves + kThreads / kWave - 1) / (kThreads / kWave);
   if (head_dim == 64) {
-    hipLaunchKernelGGL(attention_prefill_kernel<64>, dim3(blocks), dim3(kThreads), 0, stream, q,
-                       key_cache, value_cache, out, count, heads, kv_heads, max_seq);
+    hipLaunchKernelGGL(attention_prefill_scalar_kernel<64>, dim3(blocks), dim3(kThreads), 0,
+                       stream, q, key_cache, value_cache, out, count, heads, kv_heads, max_seq);
   } else {
-    hipLaunchKernelGGL(attention_prefill_kernel<128>, dim3(blocks), dim3(kThreads), 0, stream, q,
-                       key_cache, value_cache, out, count, heads, kv_heads, max_seq);
+    hipLaunchKernelGGL(attention_prefill_scalar_kernel<128>, dim3(blocks), dim3(kThreads), 0,
+                       stream, q, key_cache, value_cache, out, count, heads, kv_heads, max_seq);
   }
 }
 

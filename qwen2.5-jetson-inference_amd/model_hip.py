@@ -41,6 +41,7 @@ EXPORTED_SYMBOLS = (
     "infer_hip_model_stream",
     "infer_hip_model_kernel_times",
     "infer_hip_model_kernel_name",
+    "infer_hip_attention_prefill_bf16",
 )
 KERNEL_KINDS = 9
 
@@ -123,6 +124,7 @@ def load():
         "infer_hip_model_kernel_times": ([p, i, i, ctypes.POINTER(ctypes.c_double),
                                           ctypes.POINTER(ctypes.c_double), ip, i], i),
         "infer_hip_model_kernel_name": ([i], ctypes.c_char_p),
+        "infer_hip_attention_prefill_bf16": ([p, p, p, p, i, i, i, i, i, p], i),
         "infer_hip_model_open": ([ctypes.c_char_p, ctypes.POINTER(_Options), ctypes.POINTER(p)],
                                  i),
     }
@@ -132,6 +134,18 @@ def load():
         fn.restype = res
     _bound = True
     return lib
+
+
+def attention_prefill_bf16(q, key_cache, value_cache, output, token_count: int,
+                           num_heads: int, num_kv_heads: int, head_dim: int,
+                           max_sequence_length: int, stream=None) -> None:
+    """infer::cuda::attention_prefill_bf16 (cuda_ops.hpp:92-97) on device
+    tensors (BF16 as int16/uint16/bfloat16 words)."""
+    lib = load()
+    _check(lib.infer_hip_attention_prefill_bf16(
+        linear_hip._ptr(q), linear_hip._ptr(key_cache), linear_hip._ptr(value_cache),
+        linear_hip._ptr(output), token_count, num_heads, num_kv_heads, head_dim,
+        max_sequence_length, linear_hip._stream(stream)))
 
 
 def _dtype_name(t) -> str:

@@ -89,7 +89,7 @@ def test_lm_head_workspace_invalid_shape(hip):
 
 def _declared_model_symbols():
     text = open(os.path.join(ROOT, "include", "infer_model.h")).read()
-    return sorted(set(re.findall(r"\b(infer_hip_model_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(infer_hip_\w+)\s*\(", text)))
 
 
 def test_library_exports_every_model_symbol(hip):
@@ -164,3 +164,15 @@ def test_model_null_handles_are_rejected(hip):
     assert lib.infer_hip_model_decode_steps(None, 1, None) == hip.INVALID_ARGUMENT
     assert lib.infer_hip_model_position(None) == -1
     assert lib.infer_hip_model_destroy(None) == hip.OK
+
+
+def test_attention_prefill_rejects_bad_arguments_on_host(hip):
+    import model_hip
+    lib = model_hip.load()
+    f = lib.infer_hip_attention_prefill_bf16
+    assert f(None, 16, 16, 16, 4, 2, 1, 64, 8, None) == hip.INVALID_ARGUMENT
+    assert f(16, 16, 16, 16, 4, 2, 1, 32, 8, None) == hip.INVALID_ARGUMENT
+    assert "head_dim 32" in lib.infer_hip_last_error().decode()
+    assert f(16, 16, 16, 16, 9, 2, 1, 64, 8, None) == hip.INVALID_ARGUMENT
+    assert f(16, 16, 16, 16, 4, 3, 2, 64, 8, None) == hip.INVALID_ARGUMENT
+    assert f(16, 16, 16, 16, 0, 2, 1, 64, 8, None) == hip.INVALID_ARGUMENT
