@@ -795,20 +795,9 @@ __global__ __launch_bounds__(kWideThreads) void gemm_wide_kernel(GemmArgs a) {
 }
 
 // Grouped form of gemm_wide_kernel (same block -> unit mapping as
-// gemm_grouped_kernel).
-// Grouped form of gemm_wide_kernel (same block -> unit mapping as
 // gemm_grouped_kernel: part u % splits of tile u / splits, M tiles fastest).
 template <bool W8>
-__global__ __launch_bounds__(kWideThreads) void gemm_wide_grouped_kernel(
-    const GemmGroupDesc* __restrict__ descs, int count) {
-  const int b = blockIdx.x;
-  int lo = 0, hi = count - 1;
-  while (lo < hi) {  // last descriptor whose block_begin <= b
-    const int mid = (lo + hi + 1) >> 1;
-    if (descs[mid].block_begin <= b) lo = mid; else hi = mid - 1;
-  }
-  const GemmGroupDesc& d = descs[lo];
-  const int u = b - d.block_begin;
+__device__ __forceinline__ void gemm_wide_unit(const GemmGroupDesc& d, int u) {
   const int tile = u / d.splits;
   const GemmArgs a{d.w, d.s, d.bias, d.x, d.y, d.m, d.n, d.k};
   SplitK sp;
@@ -823,19 +812,35 @@ __global__ __launch_bounds__(kWideThreads) void gemm_wide_grouped_kernel(
   gemm_wide_tile<W8>(a, (tile % d.tiles_m) * kWideRows, (tile / d.tiles_m) * kWideCols, sp);
 }
 
+template <bool W8>
+__global__ __launch_bounds__(kWideThreads) void gemm_wide_grouped_kernel(
+    const GemmGroupDesc* __restrict__ descs, int count) {
+  const int b = blockIdx.x;
+  int lo = 0, hi = count - 1;
+  while (lo < hi) {  // last descriptor whose block_begin <= b
+    const int mid = (lo + hi + 1) >> 1;
+    if (descs[mid].block_begin <= b) lo = mid; else hi = mid - 1;
+  }
+  gemm_wide_unit<W8>(descs[lo], b - descs[lo].block_begin);
+}
+
+// The same with the descriptors in the kernel arguments.
+template <bool W8>
+__global__ __launch_bounds__(kWideThreads) void gemm_wide_inline_kernel(GemmGroupArgs g) {
+  const int b = blockIdx.x;
+  int lo = 0;
+#pragma unroll
+  for (int i = 1; i < kInlineGroupMax; ++i) {
+    if (i < g.count && g.d[i].block_begin <= b) lo = i;
+  }
+  gemm_wide_unit<W8>(g.d[lo], b - g.d[lo].block_begin);
+}
+
 // Split-K reduction, the second launch of a wide-tile plan: each block sums
 // 16 rows of one split tile over its parts in index order (the result does
 // not depend on which part finished first), adds the bias and writes BF16;
 // each thread 8 consecutive columns of one row.
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(
-    const SplitReduceDesc* __restrict__ descs, int count) {
-  const int b = blockIdx.x;
-  int lo = 0, hi = count - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (descs[mid].block_begin <= b) lo = mid; else hi = mid - 1;
-  }
-  const SplitReduceDesc& d = descs[lo];
+__device__ __forceinline__ void splitk_reduce_block(const SplitReduceDesc& d, int b) {
   constexpr int kBlocksPerTile = kWideRows / kSplitReduceRows;
   const int u = b - d.block_begin;
   const int tile = u / kBlocksPerTile;
@@ -887,6 +892,27 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(
   }
 }
 
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(
+    const SplitReduceDesc* __restrict__ descs, int count) {
+  const int b = blockIdx.x;
+  int lo = 0, hi = count - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (descs[mid].block_begin <= b) lo = mid; else hi = mid - 1;
+  }
+  splitk_reduce_block(descs[lo], b);
+}
+
+__global__ __launch_bounds__(256) void splitk_reduce_inline_kernel(SplitReduceArgs r) {
+  const int b = blockIdx.x;
+  int lo = 0;
+#pragma unroll
+  for (int i = 1; i < kInlineGroupMax; ++i) {
+    if (i < r.count && r.d[i].block_begin <= b) lo = i;
+  }
+  splitk_reduce_block(r.d[lo], b);
+}
+
 // Grid: x = N tiles, y = M tiles.
 template <int BM, int BN, int WAVES_M, bool W8>
 __global__ __launch_bounds__(kThreads) QLIN_GEMM_WAVES_ATTR void gemm_mfma_kernel(GemmArgs a) {
@@ -899,16 +925,7 @@ __global__ __launch_bounds__(kThreads) QLIN_GEMM_WAVES_ATTR void gemm_mfma_kerne
 // output tile u / splits, M tiles fastest (consecutive tiles share one
 // weight tile).
 template <int BM, int BN, int WAVES_M, bool W8>
-__global__ __launch_bounds__(kThreads) QLIN_GEMM_WAVES_ATTR void gemm_grouped_kernel(
-    const GemmGroupDesc* __restrict__ descs, int count) {
-  const int b = blockIdx.x;
-  int lo = 0, hi = count - 1;
-  while (lo < hi) {  // last descriptor whose block_begin <= b
-    const int mid = (lo + hi + 1) >> 1;
-    if (descs[mid].block_begin <= b) lo = mid; else hi = mid - 1;
-  }
-  const GemmGroupDesc& d = descs[lo];
-  const int u = b - d.block_begin;
+__device__ __forceinline__ void gemm_grouped_unit(const GemmGroupDesc& d, int u) {
   const int tile = u / d.splits;
   const GemmArgs a{d.w, d.s, d.bias, d.x, d.y, d.m, d.n, d.k};
   SplitK sp;
@@ -923,6 +940,30 @@ __global__ __launch_bounds__(kThreads) QLIN_GEMM_WAVES_ATTR void gemm_grouped_ke
   }
   gemm_tile<BM, BN, WAVES_M, W8, kPrefetch>(a, (tile % d.tiles_m) * BM, (tile / d.tiles_m) * BN,
                                             sp);
+}
+
+template <int BM, int BN, int WAVES_M, bool W8>
+__global__ __launch_bounds__(kThreads) QLIN_GEMM_WAVES_ATTR void gemm_grouped_kernel(
+    const GemmGroupDesc* __restrict__ descs, int count) {
+  const int b = blockIdx.x;
+  int lo = 0, hi = count - 1;
+  while (lo < hi) {  // last descriptor whose block_begin <= b
+    const int mid = (lo + hi + 1) >> 1;
+    if (descs[mid].block_begin <= b) lo = mid; else hi = mid - 1;
+  }
+  gemm_grouped_unit<BM, BN, WAVES_M, W8>(descs[lo], b - descs[lo].block_begin);
+}
+
+template <int BM, int BN, int WAVES_M, bool W8>
+__global__ __launch_bounds__(kThreads) QLIN_GEMM_WAVES_ATTR void gemm_grouped_inline_kernel(
+    GemmGroupArgs g) {
+  const int b = blockIdx.x;
+  int lo = 0;
+#pragma unroll
+  for (int i = 1; i < kInlineGroupMax; ++i) {
+    if (i < g.count && g.d[i].block_begin <= b) lo = i;
+  }
+  gemm_grouped_unit<BM, BN, WAVES_M, W8>(g.d[lo], b - g.d[lo].block_begin);
 }
 
 template <int BM, int BN, int WAVES_M, bool W8>
@@ -1013,6 +1054,29 @@ void launch_gemm_wide_grouped(bool w8, const GemmGroupDesc* descs, int count, in
   }
   if (rcount > 0) {
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3(reducers), dim3(256), 0, stream, rdescs, rcount);
+  }
+}
+
+void launch_gemm_group_inline(const GemmGroupLaunch& l, hipStream_t stream) {
+  const dim3 grid(l.blocks);
+  if (l.tile == kGemmTile256x128) {
+    if (l.w8) {
+      hipLaunchKernelGGL((gemm_wide_inline_kernel<true>), grid, dim3(kWideThreads), 0, stream,
+                         l.g);
+    } else {
+      hipLaunchKernelGGL((gemm_wide_inline_kernel<false>), grid, dim3(kWideThreads), 0, stream,
+                         l.g);
+    }
+    if (l.r.count > 0) {
+      hipLaunchKernelGGL(splitk_reduce_inline_kernel, dim3(l.reducers), dim3(256), 0, stream,
+                         l.r);
+    }
+  } else if (l.w8) {
+    hipLaunchKernelGGL((gemm_grouped_inline_kernel<64, 64, 2, true>), grid, dim3(kThreads), 0,
+                       stream, l.g);
+  } else {
+    hipLaunchKernelGGL((gemm_grouped_inline_kernel<64, 64, 2, false>), grid, dim3(kThreads), 0,
+                       stream, l.g);
   }
 }
 

@@ -104,6 +104,47 @@ struct SplitReduceDesc {
 };
 constexpr int kSplitReduceRows = 16;  // rows of a tile per reduction block
 
+// A grouped launch laid out on the host and passed by value as kernel
+// arguments, for callers whose shapes change from call to call (the model's
+// prefill at the prompt's length): no descriptor table in device memory.
+constexpr int kInlineGroupMax = 4;
+struct GemmGroupArgs {
+  GemmGroupDesc d[kInlineGroupMax];
+  int count;
+};
+struct SplitReduceArgs {
+  SplitReduceDesc d[kInlineGroupMax];
+  int count;
+};
+struct GemmGroupLaunch {
+  int tile;
+  bool w8;
+  int blocks;    // workgroups of the GEMM launch
+  int reducers;  // workgroups of the split-K reduction launch (wide tile only)
+  GemmGroupArgs g;
+  SplitReduceArgs r;
+};
+
+// plan.cpp: the layout shared by grouped plans and inline launches.  Sets
+// every descriptor's tiles_m, splits, split_stages and block_begin (and
+// sorts them, longest units first) for one launch on a device with `cus`
+// CUs.  The tile is 256 x 128 once every GEMM has 256 rows or more (with
+// `fill`, also only when the group has wide tiles for half the CUs), else
+// 64 x 64.  K is split so that no unit is much longer than the group's
+// shortest reduction (at least 8 stages); with `fill`, for a lone or long-K
+// group of one launch, into at most 4 parts of at least 14 stages instead.
+// Returns the tile; *blocks, *partial_floats and *counters receive the
+// launch size and its split-K scratch needs.
+int layout_gemm_group(GemmGroupDesc* descs, int count, int cus, bool fill, int* blocks,
+                      size_t* partial_floats, size_t* counters);
+// Points the split descriptors at `partial` / `counters` (sizes from
+// layout_gemm_group) and writes the wide tile's reduction descriptors to
+// reduce (at most count); returns the number of reduction descriptors and
+// sets *reducers to the reduction launch's workgroups.
+int bind_gemm_group(GemmGroupDesc* descs, int count, int tile, float* partial, int* counters,
+                    SplitReduceDesc* reduce, int* reducers);
+void launch_gemm_group_inline(const GemmGroupLaunch& l, hipStream_t stream);
+
 // The wide-tile grouped launch (`units` blocks over descs) and, when some
 // GEMM is split, its reduction launch (`reducers` blocks over rdescs).
 void launch_gemm_wide_grouped(bool w8, const GemmGroupDesc* descs, int count, int units,

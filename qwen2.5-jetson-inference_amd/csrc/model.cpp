@@ -120,6 +120,13 @@ struct infer_hip_model {
   int* lm_counter = nullptr;
   float2* rope = nullptr;
   float* attn_partial = nullptr;  // decode attention split partials
+  // split-K scratch of the prefill's grouped GEMM launches (sized at creation
+  // for every prompt length up to max_seq)
+  float* gemm_partial = nullptr;
+  int* gemm_counters = nullptr;
+  size_t gemm_partial_floats = 0;
+  size_t gemm_counter_count = 0;
+  int cus = 0;
   uint16_t *px = nullptr, *pnorm = nullptr, *pq = nullptr, *pk = nullptr, *pv = nullptr;
   uint16_t *pattn = nullptr, *ptmp = nullptr, *pgate = nullptr, *pup = nullptr, *pmlp = nullptr;
 
@@ -185,6 +192,74 @@ void linear_batch(const infer_hip_model* m, const Linear& l, const uint16_t* x, 
   } else {
     launch_bf16_linear_generic(static_cast<const uint16_t*>(l.w), l.b, x, y, tokens, l.n, l.k,
                                m->stream);
+  }
+}
+
+// Several independent Linears of the prefill as one grouped MFMA launch
+// (src/qwen2.cpp:300-330 per Linear), laid out for `tokens` rows with K split
+// until the group covers the CUs; the split-K scratch is the arena's.  Falls
+// back to one launch per Linear where the grouped kernels do not apply.
+struct GemmItem {
+  const Linear* l;
+  const uint16_t* x;
+  uint16_t* y;
+};
+
+void linear_group(const infer_hip_model* m, const GemmItem* items, int count, int tokens) {
+  bool grouped = tokens > 1 && count <= kInlineGroupMax;
+  for (int i = 0; i < count && grouped; ++i) {
+    grouped = gemm_mfma_supported(items[i].l->w, items[i].x, tokens, items[i].l->n,
+                                  items[i].l->k);
+  }
+  GemmGroupLaunch g{};
+  if (grouped) {
+    for (int i = 0; i < count; ++i) {
+      const Linear& l = *items[i].l;
+      g.g.d[i] = GemmGroupDesc{l.w, m->w8 ? l.s : nullptr, l.b, items[i].x, items[i].y, tokens,
+                               l.n, l.k, 0, 0, 1, l.k / 64, nullptr, nullptr};
+    }
+    g.g.count = count;
+    g.w8 = m->w8;
+    size_t pf = 0, cc = 0;
+    g.tile = layout_gemm_group(g.g.d, count, m->cus, true, &g.blocks, &pf, &cc);
+    grouped = g.blocks > 0 && pf <= m->gemm_partial_floats && cc <= m->gemm_counter_count;
+  }
+  if (!grouped) {
+    for (int i = 0; i < count; ++i) linear_batch(m, *items[i].l, items[i].x, items[i].y, tokens);
+    return;
+  }
+  g.r.count = bind_gemm_group(g.g.d, count, g.tile, m->gemm_partial, m->gemm_counters, g.r.d,
+                              &g.reducers);
+  launch_gemm_group_inline(g, m->stream);
+}
+
+// The split-K scratch the prefill's groups (q|k|v, o, gate|up, down) need at
+// any prompt length up to max_seq.
+void prefill_scratch_needs(const infer_hip_model_config& c, int head_dim, int max_seq, int cus,
+                           size_t* partial_floats, size_t* counters) {
+  const int hidden = c.hidden_size, inter = c.intermediate_size;
+  const int kv_dim = c.num_kv_heads * head_dim;
+  const int shapes[4][3][2] = {{{hidden, hidden}, {kv_dim, hidden}, {kv_dim, hidden}},
+                               {{hidden, hidden}, {0, 0}, {0, 0}},
+                               {{inter, hidden}, {inter, hidden}, {0, 0}},
+                               {{hidden, inter}, {0, 0}, {0, 0}}};
+  const int counts[4] = {3, 1, 2, 1};
+  *partial_floats = 0;
+  *counters = 0;
+  for (int tokens = 2; tokens <= max_seq; ++tokens) {
+    for (int g = 0; g < 4; ++g) {
+      GemmGroupDesc d[kInlineGroupMax] = {};
+      for (int i = 0; i < counts[g]; ++i) {
+        d[i].m = tokens;
+        d[i].n = shapes[g][i][0];
+        d[i].k = shapes[g][i][1];
+      }
+      int blocks = 0;
+      size_t pf = 0, cc = 0;
+      (void)layout_gemm_group(d, counts[g], cus, true, &blocks, &pf, &cc);
+      *partial_floats = std::max(*partial_floats, pf);
+      *counters = std::max(*counters, cc);
+    }
   }
 }
 
@@ -412,20 +487,22 @@ int run_prefill(infer_hip_model* m, const int* tokens, int count, int* next) {
   const long long rows_h = static_cast<long long>(count) * hidden;
   for (const Layer& L : m->layers) {
     launch_rms_norm(m->px, L.in_norm, m->pnorm, count, hidden, c.rms_norm_eps, s);
-    linear_batch(m, L.q, m->pnorm, m->pq, count);
-    linear_batch(m, L.k, m->pnorm, m->pk, count);
-    linear_batch(m, L.v, m->pnorm, m->pv, count);
+    const GemmItem qkv[3] = {{&L.q, m->pnorm, m->pq}, {&L.k, m->pnorm, m->pk},
+                             {&L.v, m->pnorm, m->pv}};
+    linear_group(m, qkv, 3, count);
     launch_rope_store(m->pq, m->pk, m->pv, L.key_cache, L.value_cache, m->rope, count, 0,
                       c.num_heads, c.num_kv_heads, m->head_dim, m->max_seq, s);
     launch_attention_prefill(m->pq, L.key_cache, L.value_cache, m->pattn, count, c.num_heads,
                              c.num_kv_heads, m->head_dim, m->max_seq, s);
-    linear_batch(m, L.o, m->pattn, m->ptmp, count);
+    const GemmItem o[1] = {{&L.o, m->pattn, m->ptmp}};
+    linear_group(m, o, 1, count);
     launch_add(m->px, m->ptmp, rows_h, s);
     launch_rms_norm(m->px, L.post_norm, m->pnorm, count, hidden, c.rms_norm_eps, s);
-    linear_batch(m, L.gate, m->pnorm, m->pgate, count);
-    linear_batch(m, L.up, m->pnorm, m->pup, count);
+    const GemmItem gate_up[2] = {{&L.gate, m->pnorm, m->pgate}, {&L.up, m->pnorm, m->pup}};
+    linear_group(m, gate_up, 2, count);
     launch_silu_mul(m->pgate, m->pup, m->pmlp, static_cast<long long>(count) * inter, s);
-    linear_batch(m, L.down, m->pmlp, m->ptmp, count);
+    const GemmItem down[1] = {{&L.down, m->pmlp, m->ptmp}};
+    linear_group(m, down, 1, count);
     launch_add(m->px, m->ptmp, rows_h, s);
   }
   int rc = check_launch("prefill");
@@ -589,6 +666,19 @@ extern "C" int infer_hip_model_create(const infer_hip_model_config* config,
   const size_t o_pv = take(2 * ms * kv_dim), o_pattn = take(2 * ms * hidden);
   const size_t o_ptmp = take(2 * ms * hidden), o_pgate = take(2 * ms * inter);
   const size_t o_pup = take(2 * ms * inter), o_pmlp = take(2 * ms * inter);
+  int cus = 0;
+  {
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) {
+      delete m;
+      return fail(INFER_HIP_RUNTIME_ERROR, "model: cannot query the device");
+    }
+  }
+  size_t gemm_pf = 0, gemm_cc = 0;
+  prefill_scratch_needs(c, head_dim, max_seq, cus, &gemm_pf, &gemm_cc);
+  const size_t o_gemm_partial = take(sizeof(float) * gemm_pf);
+  const size_t o_gemm_counters = take(sizeof(int) * gemm_cc);
   const size_t o_tables = take(sizeof(W8GroupDesc) * 5 * c.num_layers);
   // One layer's K and V caches, in BF16 elements: [k|v][kv_head][max_seq][head_dim].
   const size_t kv_layer = 2 * static_cast<size_t>(c.num_kv_heads) * ms * head_dim;
@@ -623,6 +713,11 @@ extern "C" int infer_hip_model_create(const infer_hip_model_config* config,
   m->px = bf(o_px); m->pnorm = bf(o_pnorm); m->pq = bf(o_pq); m->pk = bf(o_pk); m->pv = bf(o_pv);
   m->pattn = bf(o_pattn); m->ptmp = bf(o_ptmp); m->pgate = bf(o_pgate); m->pup = bf(o_pup);
   m->pmlp = bf(o_pmlp);
+  m->cus = cus;
+  m->gemm_partial = reinterpret_cast<float*>(a + o_gemm_partial);
+  m->gemm_counters = reinterpret_cast<int*>(a + o_gemm_counters);
+  m->gemm_partial_floats = gemm_pf;
+  m->gemm_counter_count = gemm_cc;
   W8GroupDesc* tables = reinterpret_cast<W8GroupDesc*>(a + o_tables);
   uint16_t* kv = bf(o_kv);
 

@@ -121,6 +121,129 @@ extern "C" int infer_hip_w8a16_gemv_plan_destroy(infer_hip_gemv_plan* plan) {
 // Grouped GEMM plans (prefill): many independent GEMMs in one launch of the
 // MFMA kernel, one workgroup per output tile (or part of one, split over K).
 
+namespace qlin {
+
+namespace {
+constexpr int kWideRowsHost = 256;  // gemm_tile_rows(kGemmTile256x128)
+constexpr int kWideColsHost = 128;
+}  // namespace
+
+int layout_gemm_group(GemmGroupDesc* table, int count, int cus, bool fill, int* blocks_out,
+                      size_t* partial_floats, size_t* counters) {
+  int min_tokens = table[0].m;
+  long long wide_tiles = 0;
+  for (int i = 0; i < count; ++i) {
+    min_tokens = std::min(min_tokens, table[i].m);
+    wide_tiles += static_cast<long long>((table[i].m + kWideRowsHost - 1) / kWideRowsHost) *
+                  ((table[i].n + kWideColsHost - 1) / kWideColsHost);
+  }
+  // Once every GEMM has 256 rows or more, the 8-wave 256 x 128 tile: it
+  // moves the fewest LDS bytes per FLOP and runs two waves per SIMD.  Below
+  // that, 64 x 64 tiles (the most workgroups; up to 4 per CU).  A `fill`
+  // group also needs wide tiles for at least half the CUs: measured on
+  // MI355X at M = 512, q|k|v (18 wide tiles) and o (14) take 7.9 us on 64 x 64
+  // tiles against 15-18 us on wide ones, while gate|up (152 wide tiles) takes
+  // 18.3 us wide against 20.9 us.
+  const bool wide = min_tokens >= kWideRowsHost && (!fill || 2 * wide_tiles >= cus);
+  const int tile = wide ? kGemmTile256x128 : kGemmTile64x64;
+  const int bm = gemm_tile_rows(tile), bn = gemm_tile_cols(tile);
+  int min_stages = 1 << 30, max_stages = 0;
+  for (int i = 0; i < count; ++i) {
+    GemmGroupDesc& d = table[i];
+    d.tiles_m = (d.m + bm - 1) / bm;
+    d.splits = 1;
+    d.split_stages = d.k / 64;
+    d.partial = nullptr;
+    d.counters = nullptr;
+    min_stages = std::min(min_stages, d.k / 64);
+    max_stages = std::max(max_stages, d.k / 64);
+  }
+  auto units_for = [&](int t) {
+    long long u = 0;
+    for (int i = 0; i < count; ++i) {
+      const GemmGroupDesc& d = table[i];
+      const int stages = d.k / 64;
+      const int per = (stages + ((stages + t - 1) / t) - 1) / ((stages + t - 1) / t);
+      const int parts = (stages + per - 1) / per;
+      u += static_cast<long long>(d.tiles_m) * ((d.n + bn - 1) / bn) * parts;
+    }
+    return u;
+  };
+  // Split K so that no unit is much longer than the group's shortest
+  // reduction (at least 8 stages of 64): a lone long-K tile would otherwise
+  // be the whole launch's critical path.  With the wide tile every CU holds
+  // one workgroup, so the unit length is raised, if needed, until all units
+  // fit on the CUs at once (M = 512 layer: down's 76 stages in 5 parts of 16
+  // instead of 6 of 13, 254 units on 256 CUs).
+  // A `fill` group is split into at most 4 parts of at least 14 stages, and
+  // into fewer while it has more than two units per CU: measured at
+  // M = 128-512, down (76 stages) is fastest in 4 parts of 19 on 64 x 64
+  // tiles (16.2 us at M = 512, 448 units), and 14-stage GEMMs gain nothing
+  // from a split.
+  int target = std::max(8, min_stages);
+  if (fill) {
+    target = std::min(max_stages, std::max(14, (max_stages + 3) / 4));
+    while (target < max_stages && units_for(target) > 2ll * cus) ++target;
+  } else if (tile == kGemmTile256x128) {
+    while (target < max_stages && units_for(target) > cus) ++target;
+  }
+  size_t pf = 0, cc = 0;
+  for (int i = 0; i < count; ++i) {
+    GemmGroupDesc& d = table[i];
+    const int stages = d.k / 64;
+    const int parts = (stages + target - 1) / target;
+    if (parts > 1) {
+      d.split_stages = (stages + parts - 1) / parts;
+      d.splits = (stages + d.split_stages - 1) / d.split_stages;  // no empty part
+      const size_t tiles = static_cast<size_t>(d.tiles_m) * ((d.n + bn - 1) / bn);
+      pf += tiles * d.splits * bm * bn;
+      if (tile != kGemmTile256x128) cc += tiles;
+    }
+  }
+  // Longest units first: they take longest, so starting them earliest
+  // shortens the launch's tail.
+  std::stable_sort(table, table + count, [](const GemmGroupDesc& a, const GemmGroupDesc& b) {
+    return a.split_stages > b.split_stages;
+  });
+  long long blocks = 0;
+  for (int i = 0; i < count; ++i) {
+    GemmGroupDesc& d = table[i];
+    d.block_begin = static_cast<int>(blocks);
+    blocks += static_cast<long long>(d.tiles_m) * ((d.n + bn - 1) / bn) * d.splits;
+  }
+  *blocks_out = blocks > 0x7FFFFFFF ? -1 : static_cast<int>(blocks);
+  *partial_floats = pf;
+  *counters = cc;
+  return tile;
+}
+
+int bind_gemm_group(GemmGroupDesc* table, int count, int tile, float* partial, int* counters,
+                    SplitReduceDesc* reduce, int* reducers) {
+  const bool wide = tile == kGemmTile256x128;
+  const int bm = gemm_tile_rows(tile), bn = gemm_tile_cols(tile);
+  size_t pf = 0, cc = 0;
+  int rcount = 0, rblocks = 0;
+  for (int i = 0; i < count; ++i) {
+    GemmGroupDesc& d = table[i];
+    if (d.splits <= 1) continue;
+    const size_t tiles = static_cast<size_t>(d.tiles_m) * ((d.n + bn - 1) / bn);
+    d.partial = partial + pf;
+    if (!wide) d.counters = counters + cc;
+    if (wide) {
+      reduce[rcount++] =
+          SplitReduceDesc{d.partial, d.bias, d.y, d.m, d.n, d.tiles_m, d.splits, rblocks};
+      rblocks += static_cast<int>(tiles) * (bm / kSplitReduceRows);
+    } else {
+      cc += tiles;
+    }
+    pf += tiles * d.splits * bm * bn;
+  }
+  *reducers = rblocks;
+  return rcount;
+}
+
+}  // namespace qlin
+
 struct infer_hip_gemm_plan {
   GemmGroupDesc* table = nullptr;  // device memory
   float* partial = nullptr;        // split-K partial tiles (device)
@@ -144,14 +267,6 @@ extern "C" int infer_hip_gemm_plan_create(const infer_hip_gemm_desc* descs, int 
     return fail(INFER_HIP_INVALID_ARGUMENT, "gemm plan: need at least one descriptor");
   }
   const bool w8 = descs[0].w8a16 != 0;
-  // Once every GEMM has 256 rows or more, the 8-wave 256 x 128 tile: it
-  // moves the fewest LDS bytes per FLOP and runs two waves per SIMD.  Below
-  // that, 64 x 64 tiles (the most workgroups; up to 4 per CU).
-  int min_tokens = descs[0].tokens;
-  for (int i = 1; i < count; ++i) min_tokens = std::min(min_tokens, descs[i].tokens);
-  const int tile = min_tokens >= gemm_tile_rows(kGemmTile256x128) ? kGemmTile256x128
-                                                                   : kGemmTile64x64;
-  const int bm = gemm_tile_rows(tile), bn = gemm_tile_cols(tile);
   std::vector<GemmGroupDesc> table;
   table.reserve(count);
   double flops = 0.0;
@@ -178,72 +293,25 @@ extern "C" int infer_hip_gemm_plan_create(const infer_hip_gemm_desc* descs, int 
                   "input and operands under 2 GiB (K=%d)",
                   i, d.in_features);
     }
-    const int tiles_m = (d.tokens + bm - 1) / bm;
     table.push_back(GemmGroupDesc{d.weight, w8 ? d.scales : nullptr, d.bias, d.input, d.output,
-                                  d.tokens, d.out_features, d.in_features, tiles_m, 0, 1,
+                                  d.tokens, d.out_features, d.in_features, 0, 0, 1,
                                   d.in_features / 64, nullptr, nullptr});
     flops += 2.0 * d.tokens * d.out_features * d.in_features;
   }
-  // Split K so that no unit is much longer than the plan's shortest
-  // reduction (at least 8 stages of 64): a lone long-K tile would otherwise
-  // be the whole launch's critical path.  With the wide tile every CU holds
-  // one workgroup, so the unit length is raised, if needed, until all units
-  // fit on the device's CUs at once (M = 512 layer: down's 76 stages in 5
-  // parts of 16 instead of 6 of 13, 254 units on 256 CUs).
-  int min_stages = 1 << 30, max_stages = 0;
-  for (const GemmGroupDesc& d : table) {
-    min_stages = std::min(min_stages, d.k / 64);
-    max_stages = std::max(max_stages, d.k / 64);
+  int device = 0, cus = 0;
+  if (hipGetDevice(&device) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) {
+    return fail(INFER_HIP_RUNTIME_ERROR, "gemm plan: cannot query the device");
   }
-  int target = std::max(8, min_stages);
-  if (tile == kGemmTile256x128) {
-    int device = 0, cus = 0;
-    if (hipGetDevice(&device) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) !=
-            hipSuccess) {
-      return fail(INFER_HIP_RUNTIME_ERROR, "gemm plan: cannot query the device");
-    }
-    auto units_for = [&](int t) {
-      long long u = 0;
-      for (const GemmGroupDesc& d : table) {
-        const int stages = d.k / 64;
-        const int per = (stages + ((stages + t - 1) / t) - 1) / ((stages + t - 1) / t);
-        const int parts = (stages + per - 1) / per;
-        u += static_cast<long long>(d.tiles_m) * ((d.n + bn - 1) / bn) * parts;
-      }
-      return u;
-    };
-    while (target < max_stages && units_for(target) > cus) ++target;
-  }
+  int blocks = 0;
   size_t partial_floats = 0, counter_count = 0;
-  for (GemmGroupDesc& d : table) {
-    const int stages = d.k / 64;
-    const int parts = (stages + target - 1) / target;
-    if (parts > 1) {
-      d.split_stages = (stages + parts - 1) / parts;
-      d.splits = (stages + d.split_stages - 1) / d.split_stages;  // no empty part
-      const size_t tiles =
-          static_cast<size_t>(d.tiles_m) * ((d.n + bn - 1) / bn);
-      partial_floats += tiles * d.splits * bm * bn;
-      counter_count += tiles;
-    }
-  }
-  // Longest units first: they take longest, so starting them earliest
-  // shortens the launch's tail.
-  std::stable_sort(table.begin(), table.end(), [](const GemmGroupDesc& a, const GemmGroupDesc& b) {
-    return a.split_stages > b.split_stages;
-  });
-  long long blocks = 0;
-  for (GemmGroupDesc& d : table) {
-    d.block_begin = static_cast<int>(blocks);
-    blocks += static_cast<long long>(d.tiles_m) * ((d.n + bn - 1) / bn) *
-              d.splits;
-  }
-  if (blocks > 0x7FFFFFFF) return fail(INFER_HIP_INVALID_ARGUMENT, "gemm plan: too many tiles");
+  const int tile = layout_gemm_group(table.data(), count, cus, false, &blocks, &partial_floats,
+                                     &counter_count);
+  if (blocks < 0) return fail(INFER_HIP_INVALID_ARGUMENT, "gemm plan: too many tiles");
   auto* plan = new (std::nothrow) infer_hip_gemm_plan();
   if (!plan) return fail(INFER_HIP_RUNTIME_ERROR, "gemm plan: out of host memory");
   plan->count = count;
-  plan->blocks = static_cast<int>(blocks);
+  plan->blocks = blocks;
   plan->w8 = w8;
   plan->tile = tile;
   plan->flops = flops;
@@ -251,34 +319,22 @@ extern "C" int infer_hip_gemm_plan_create(const infer_hip_gemm_desc* descs, int 
   // per-tile counter) sums the parts inside the launch; the wide tile's
   // parts are summed by a second, reduction launch spread over many CUs —
   // one CU reading every part of a 256 x 128 FP32 tile took microseconds.
-  const bool wide = tile == kGemmTile256x128;
-  std::vector<SplitReduceDesc> reduce;
+  std::vector<SplitReduceDesc> reduce(count);
+  int rcount = 0;
   hipError_t st = hipGetDevice(&plan->device);
   if (st == hipSuccess && partial_floats > 0) {
     st = hipMalloc(&plan->partial, partial_floats * sizeof(float));
-    if (st == hipSuccess && !wide) {
+    if (st == hipSuccess && counter_count > 0) {
       st = hipMalloc(&plan->counters, counter_count * sizeof(int));
       if (st == hipSuccess) st = hipMemset(plan->counters, 0, counter_count * sizeof(int));
     }
-    size_t pf = 0, cc = 0;
-    int rblocks = 0;
-    for (GemmGroupDesc& d : table) {
-      if (d.splits <= 1) continue;
-      const size_t tiles =
-          static_cast<size_t>(d.tiles_m) * ((d.n + bn - 1) / bn);
-      d.partial = plan->partial + pf;
-      if (!wide) d.counters = plan->counters + cc;
-      if (wide) {
-        reduce.push_back(SplitReduceDesc{d.partial, d.bias, d.y, d.m, d.n, d.tiles_m, d.splits,
-                                         rblocks});
-        rblocks += static_cast<int>(tiles) * (bm / kSplitReduceRows);
-      }
-      pf += tiles * d.splits * bm * bn;
-      cc += tiles;
+    if (st == hipSuccess) {
+      rcount = bind_gemm_group(table.data(), count, tile, plan->partial, plan->counters,
+                               reduce.data(), &plan->reduce_blocks);
     }
-    plan->reduce_count = static_cast<int>(reduce.size());
-    plan->reduce_blocks = rblocks;
   }
+  reduce.resize(rcount);
+  plan->reduce_count = rcount;
   if (st == hipSuccess && !reduce.empty()) {
     st = hipMalloc(&plan->reduce, reduce.size() * sizeof(SplitReduceDesc));
     if (st == hipSuccess) {
