@@ -463,3 +463,20 @@ def test_model_open_rejects_before_any_device_call(arc, tmp_path):
     d = _model_dir(tmp_path, emb, "w8a16")
     with pytest.raises(arc.InferError, match="model.norm.weight: unexpected dtype or shape"):
         model_hip.Qwen2Model.open(d, "w8a16", max_sequence_length=16)
+
+
+# ------------------------------------------------------ C++17 boundary --
+
+def test_cpp_archive_boundary(tmp_path):
+    # tests/cpp/test_archive.cpp drives include/infer/archive_hip.hpp
+    # (infer::ModelArchive, infer::ModelConfig, infer::export_archive) as the
+    # reference's gtest suite drives its ModelArchive; host-only.
+    import subprocess
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    binary = os.path.join(root, "tests", "cpp", "test_archive")
+    if not os.path.exists(binary):
+        subprocess.run(["make", "-C", os.path.join(root, "tests", "cpp"), "test_archive"],
+                       check=True, capture_output=True)
+    out = subprocess.run([binary, str(tmp_path)], capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert "PASSED" in out.stdout
