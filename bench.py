@@ -4,10 +4,12 @@ Workloads (--workload):
 
   e2e (default).  W8A16 greedy decode of a random-init
       Qwen2.5-0.5B-shaped model (24 layers, hidden 896, 14/2 heads, inter
-      4864, vocab 151936, tied embedding; weights ~N(0, 0.02) exported to
-      group-64 int8 with BF16 scales, norm weights 1, biases 0; seed 4) on
-      the HIP decode runtime: prompt of 512 uniform-random tokens (prefill,
-      not timed), then --steps decode steps (default 511: the 512 generated
+      4864, vocab 151936, tied embedding; FP32 weights ~N(0, 0.02), norm
+      weights 1, biases 0, seed 4, exported by the library's QWENBIN1
+      exporter to group-64 int8 with BF16 scales and BF16 non-quantised
+      tensors, and opened from that model directory) on the HIP decode
+      runtime: prompt of 512 uniform-random tokens (prefill, not timed),
+      then --steps decode steps (default 511: the 512 generated
       tokens of config 4 minus the prefill's), max_seq 1024, BF16 KV cache.
       One step = one decode token (all 24 layers + LM head + argmax),
       replayed from a captured HIP graph with no host sync between steps.
@@ -412,10 +414,42 @@ def e2e_main(args, dev):
         print(f"bench.py: prompt {prompt_len} + {steps} steps exceeds max_seq {max_seq}",
               file=sys.stderr)
         return 2
-    tensors = S.random_model(cfg, "w8a16", seed=4, plain_init=True)
+    # Config 4's model: the FP32 checkpoint exported to a W8A16 archive and
+    # opened from its model directory (the reference's export_model.py then
+    # Qwen2Model(dir, options)).
+    import shutil
+    import tempfile
+    import archive_hip
     graph = args.graph == "on"
-    model = model_hip.Qwen2Model(cfg, tensors, "w8a16", max_sequence_length=max_seq,
-                                 use_graph=graph)
+    workdir = tempfile.mkdtemp(prefix="qwen-w8a16-")
+    try:
+        t0 = time.perf_counter()
+        checkpoint = S.random_checkpoint(cfg, seed=4, std=0.02, plain_init=True)
+        with open(os.path.join(workdir, "config.json"), "w") as f:
+            json.dump({"model_type": "qwen2", "hidden_size": cfg.hidden_size,
+                       "intermediate_size": cfg.intermediate_size,
+                       "num_hidden_layers": cfg.num_layers,
+                       "num_attention_heads": cfg.num_heads,
+                       "num_key_value_heads": cfg.num_kv_heads, "vocab_size": cfg.vocab_size,
+                       "max_position_embeddings": 32768, "eos_token_id": cfg.eos_token_id,
+                       "rms_norm_eps": cfg.rms_norm_eps, "rope_theta": cfg.rope_theta,
+                       "tie_word_embeddings": True}, f)
+        t1 = time.perf_counter()
+        report = archive_hip.export(checkpoint, os.path.join(workdir, "model.w8a16.qbin"),
+                                    "w8a16", 64, source="random_checkpoint(seed=4)")
+        t2 = time.perf_counter()
+        del checkpoint
+        model = model_hip.Qwen2Model.open(workdir, "w8a16", max_sequence_length=max_seq,
+                                          use_graph=graph)
+        t3 = time.perf_counter()
+        with archive_hip.ModelArchive(os.path.join(workdir, "model.w8a16.qbin")) as archive:
+            tensors = {r.name: archive.data(r.name) for r in archive.records}
+    finally:
+        shutil.rmtree(workdir, ignore_errors=True)
+    archive_info = {"export_s": round(t2 - t1, 2), "open_s": round(t3 - t2, 2),
+                    "archive_bytes": report["bytes"],
+                    "max_groupwise_abs_error": report["max_groupwise_abs_error"],
+                    "init_s": round(t1 - t0, 2)}
     prompt = [int(v) for v in np.random.default_rng(4).integers(0, cfg.vocab_size, prompt_len)]
     for _ in range(args.warmup):
         model.generate(prompt, steps + 1, stop_on_eos=False)
@@ -475,6 +509,7 @@ def e2e_main(args, dev):
                          + ("one HIP graph replay per token" if graph
                             else "kernels launched one by one")),
             "parallelism": "single GPU",
+            "archive": archive_info,
             "first_token": first,
             "last_token": tokens[-1] if tokens else first,
         },

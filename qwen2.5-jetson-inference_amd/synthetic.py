@@ -142,26 +142,32 @@ def random_model(c: ModelConfig, precision: str = "w8a16", seed: int = 4,
 
 
 def random_checkpoint(c: ModelConfig, seed: int = 4, std: float = 0.02,
-                      tied: bool = True) -> dict:
+                      tied: bool = True, plain_init: bool = False) -> dict:
     """Random FP32 checkpoint tensors by archive name, in the order a
     Hugging Face checkpoint lists them: what the archive exporter reads.
-    With tied=False an lm_head.weight is included."""
+    With tied=False an lm_head.weight is included; with plain_init the norm
+    weights are 1 and the biases 0 (a freshly built model),
+    else 1 + N(0, std) and N(0, std)."""
     rng = np.random.default_rng(seed)
 
     def normal(*shape):
         return rng.standard_normal(shape, dtype=np.float32) * np.float32(std)
 
+    def norm_weight():
+        return np.ones(c.hidden_size, np.float32) if plain_init else 1 + normal(c.hidden_size)
+
     t = {"model.embed_tokens.weight": normal(c.vocab_size, c.hidden_size)}
     shapes = linear_shapes(c)
     for layer in range(c.num_layers):
         p = f"model.layers.{layer}."
-        t[p + "input_layernorm.weight"] = 1 + normal(c.hidden_size)
+        t[p + "input_layernorm.weight"] = norm_weight()
         for name in LINEARS:
             t[p + name + ".weight"] = normal(*shapes[name])
             if name in BIASED:
-                t[p + name + ".bias"] = normal(shapes[name][0])
-        t[p + "post_attention_layernorm.weight"] = 1 + normal(c.hidden_size)
-    t["model.norm.weight"] = 1 + normal(c.hidden_size)
+                n = shapes[name][0]
+                t[p + name + ".bias"] = np.zeros(n, np.float32) if plain_init else normal(n)
+        t[p + "post_attention_layernorm.weight"] = norm_weight()
+    t["model.norm.weight"] = norm_weight()
     if not tied:
         t["lm_head.weight"] = normal(c.vocab_size, c.hidden_size)
     return t
