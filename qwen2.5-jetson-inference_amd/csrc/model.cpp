@@ -485,8 +485,11 @@ int run_prefill(infer_hip_model* m, const int* tokens, int count, int* next) {
   if (st != hipSuccess) return hip_fail(st, "prefill token upload");
   launch_embedding(m->embed, m->prompt, count, c.vocab_size, hidden, m->px, s);
   const long long rows_h = static_cast<long long>(count) * hidden;
-  for (const Layer& L : m->layers) {
-    launch_rms_norm(m->px, L.in_norm, m->pnorm, count, hidden, c.rms_norm_eps, s);
+  // The residual adds ride with the RMSNorm behind them (after o: the
+  // post-attention norm; after down: the next layer's input norm).
+  launch_rms_norm(m->px, m->layers[0].in_norm, m->pnorm, count, hidden, c.rms_norm_eps, s);
+  for (size_t l = 0; l < m->layers.size(); ++l) {
+    const Layer& L = m->layers[l];
     const GemmItem qkv[3] = {{&L.q, m->pnorm, m->pq}, {&L.k, m->pnorm, m->pk},
                              {&L.v, m->pnorm, m->pv}};
     linear_group(m, qkv, 3, count);
@@ -496,14 +499,18 @@ int run_prefill(infer_hip_model* m, const int* tokens, int count, int* next) {
                              c.num_kv_heads, m->head_dim, m->max_seq, s);
     const GemmItem o[1] = {{&L.o, m->pattn, m->ptmp}};
     linear_group(m, o, 1, count);
-    launch_add(m->px, m->ptmp, rows_h, s);
-    launch_rms_norm(m->px, L.post_norm, m->pnorm, count, hidden, c.rms_norm_eps, s);
+    launch_add_rms_norm(m->px, m->ptmp, L.post_norm, m->pnorm, count, hidden, c.rms_norm_eps, s);
     const GemmItem gate_up[2] = {{&L.gate, m->pnorm, m->pgate}, {&L.up, m->pnorm, m->pup}};
     linear_group(m, gate_up, 2, count);
     launch_silu_mul(m->pgate, m->pup, m->pmlp, static_cast<long long>(count) * inter, s);
     const GemmItem down[1] = {{&L.down, m->pmlp, m->ptmp}};
     linear_group(m, down, 1, count);
-    launch_add(m->px, m->ptmp, rows_h, s);
+    if (l + 1 < m->layers.size()) {
+      launch_add_rms_norm(m->px, m->ptmp, m->layers[l + 1].in_norm, m->pnorm, count, hidden,
+                          c.rms_norm_eps, s);
+    } else {
+      launch_add(m->px, m->ptmp, rows_h, s);
+    }
   }
   int rc = check_launch("prefill");
   if (rc != INFER_HIP_OK) return rc;

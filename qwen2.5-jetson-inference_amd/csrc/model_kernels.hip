@@ -85,6 +85,48 @@ __global__ __launch_bounds__(kThreads) void rms_norm_kernel(const uint16_t* __re
   }
 }
 
+// Residual add and the RMSNorm behind it, one block per row: x = bf16(x +
+// y) in place, then out = bf16(x * scale * w) of the new x (the two kernels'
+// arithmetic and summation order, in one launch).  hidden <= 16 * kThreads.
+__global__ __launch_bounds__(kThreads) void add_rms_norm_kernel(uint16_t* __restrict__ x,
+                                                                const uint16_t* __restrict__ y,
+                                                                const uint16_t* __restrict__ w,
+                                                                uint16_t* __restrict__ out,
+                                                                int rows, int hidden, float eps) {
+  constexpr int kPer = 16;
+  const int row = blockIdx.x;
+  if (row >= rows) return;
+  uint16_t* xr = x + static_cast<size_t>(row) * hidden;
+  const uint16_t* yr = y + static_cast<size_t>(row) * hidden;
+  uint16_t* orow = out + static_cast<size_t>(row) * hidden;
+  float v[kPer];
+  float sum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int i = threadIdx.x + j * kThreads;
+    v[j] = 0.0f;
+    if (i < hidden) {
+      const uint16_t s = f32_to_bf16(load_bf16(xr + i) + load_bf16(yr + i));
+      xr[i] = s;
+      v[j] = bf16_to_f32(s);
+      sum = fmaf(v[j], v[j], sum);
+    }
+  }
+  __shared__ float part[kThreads / kWave];
+  sum = wave_sum(sum);
+  if ((threadIdx.x & (kWave - 1)) == 0) part[threadIdx.x / kWave] = sum;
+  __syncthreads();
+  float total = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kThreads / kWave; ++i) total += part[i];
+  const float scale = 1.0f / sqrtf(total / hidden + eps);
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int i = threadIdx.x + j * kThreads;
+    if (i < hidden) orow[i] = f32_to_bf16(v[j] * scale * load_bf16(w + i));
+  }
+}
+
 // ------------------------------------------------------- RoPE + KV store --
 
 // Rotate one head (head_dim values, pairs (i, i + half)) by the angles of
@@ -691,6 +733,12 @@ void launch_rms_norm(const uint16_t* x, const uint16_t* w, uint16_t* out, int ro
                      float eps, hipStream_t stream) {
   hipLaunchKernelGGL(rms_norm_kernel, dim3(rows), dim3(kThreads), 0, stream, x, w, out, rows,
                      hidden, eps);
+}
+
+void launch_add_rms_norm(uint16_t* x, const uint16_t* y, const uint16_t* w, uint16_t* out,
+                         int rows, int hidden, float eps, hipStream_t stream) {
+  hipLaunchKernelGGL(add_rms_norm_kernel, dim3(rows), dim3(kThreads), 0, stream, x, y, w, out,
+                     rows, hidden, eps);
 }
 
 void launch_rope_store(uint16_t* q, uint16_t* k, const uint16_t* v, uint16_t* key_cache,

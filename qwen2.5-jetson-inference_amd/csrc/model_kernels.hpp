@@ -47,6 +47,9 @@ void launch_attention_prefill(const uint16_t* q, const uint16_t* key_cache,
 void launch_silu_mul(const uint16_t* gate, const uint16_t* up, uint16_t* out, long long n,
                      hipStream_t stream);
 void launch_add(uint16_t* x, const uint16_t* y, long long n, hipStream_t stream);
+// x += y (BF16, in place) and out = rms_norm(x) * w, rows of hidden <= 4096.
+void launch_add_rms_norm(uint16_t* x, const uint16_t* y, const uint16_t* w, uint16_t* out,
+                         int rows, int hidden, float eps, hipStream_t stream);
 void launch_set_state(ModelState* state, int token, int pos, int step, hipStream_t stream);
 void launch_advance(ModelState* state, int* history, int history_len, hipStream_t stream);
 
