@@ -33,7 +33,7 @@ void launch_rope_store(uint16_t* q, uint16_t* k, const uint16_t* v, uint16_t* ke
 // one workgroup per (span, query head), spans of attention_span(max_seq)
 // positions, at most attention_splits(max_seq) of them; partial holds
 // heads x attention_splits() x (head_dim + 2) floats.
-constexpr int kAttnWaves = 4;
+constexpr int kAttnWaves = 2;
 constexpr int kAttnMaxSplits = 8;
 int attention_span(int max_seq);
 int attention_splits(int max_seq);
