@@ -77,7 +77,7 @@ struct Layer {
 constexpr int kDecodeRowsPerBlock = 16;
 // Rows (gate|up: row pairs) per wave of the fused RMSNorm + GEMV launches.
 constexpr int kQkvRowsPerWave = 1;
-constexpr int kGateUpRowsPerWave = 1;
+constexpr int kGateUpRowsPerWave = 2;
 
 constexpr size_t kAlign = 256;
 size_t align_up(size_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
