@@ -76,7 +76,7 @@ struct Layer {
 // wave, the most blocks a grouped launch can have.
 constexpr int kDecodeRowsPerBlock = 16;
 // Rows (gate|up: row pairs) per wave of the fused RMSNorm + GEMV launches.
-constexpr int kQkvRowsPerWave = 1;
+constexpr int kQkvRowsPerWave = 2;
 constexpr int kGateUpRowsPerWave = 2;
 
 constexpr size_t kAlign = 256;
