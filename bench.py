@@ -8,18 +8,24 @@ Workloads (--workload):
       weights 1, biases 0, seed 4, exported by the library's QWENBIN1
       exporter to group-64 int8 with BF16 scales and BF16 non-quantised
       tensors, and opened from that model directory) on the HIP decode
-      runtime: prompt of 512 uniform-random tokens (prefill, not timed),
-      then --steps decode steps (default 511: the 512 generated
-      tokens of config 4 minus the prefill's), max_seq 1024, BF16 KV cache.
-      One step = one decode token (all 24 layers + LM head + argmax),
-      replayed from a captured HIP graph with no host sync between steps.
-      value = decode tokens/s.  The roofline object is for the decode step's
-      dominant kernel (largest time per token), timed launch by launch with
-      HIP events on the model's stream at the middle of the timed context;
-      `linear_gemv_plan` adds config 1's figure (below).  cpu_baseline is
-      the CPU FP32 oracle model (a C restatement of the reference's
+      runtime: prompt of 512 uniform-random tokens, prefilled once (not
+      timed), max_seq 1024, BF16 KV cache.  One step = config 4's whole
+      decode: the model is rewound to the end of the prompt (its KV cache
+      kept) and runs the 511 greedy decode steps that follow the
+      prefill's token (512 generated tokens, contexts 513-1023), each one
+      graph replay, with no host sync inside the decode.  --steps such
+      decodes are timed.  value = decode tokens/s.  The roofline object is
+      for the decode step's dominant kernel (largest time per token), timed
+      launch by launch with HIP events on the model's stream at the middle
+      of the decoded context; `decode_linear` is the step's Linear launches
+      combined, `linear_gemv_plan` config 1's figure (below).  cpu_baseline
+      is the CPU FP32 oracle model (a C restatement of the reference's
       cpu_ops.cpp + qwen2.cpp CPU path) on the same dequantised weights,
-      config 0's workload (prompt 32, greedy decode), a bounded sample.
+      config 0's workload (prompt 32, greedy decode), a bounded sample,
+      with the first greedy divergence from the GPU checked by the
+      near-tie rule.  --detail FILE adds the reference's sweeps
+      (canonical, prefill, decode context; W8A16 and W16A16), the
+      per-Linear single calls and the LM head.
 
   gemv.  The decode-time W8A16 GEMVs of one token:
       24 layers x the 7 Linear shapes, 168 GEMVs over 370.1 MB of distinct
@@ -63,9 +69,9 @@ def parse():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None,
-                    help="timed steps (default: e2e 511, gemv 200, prefill 200)")
+                    help="timed steps (default: e2e 10 whole decodes, gemv 200, prefill 200)")
     ap.add_argument("--warmup", type=int, default=None,
-                    help="untimed steps (default: e2e 1 full generate, else 20)")
+                    help="untimed steps (default: e2e 2, else 20)")
     ap.add_argument("--launch", choices=("plan", "calls"), default="plan")
     ap.add_argument("--workload", choices=("e2e", "gemv", "prefill"), default="e2e",
                     help="e2e: config 4 decode (the headline); gemv: config 1; "
@@ -88,9 +94,9 @@ def parse():
                          "(the known-size reference for rocprofv3 --pmc byte counters)")
     args = ap.parse_args()
     if args.steps is None:
-        args.steps = 511 if args.workload == "e2e" else 200
+        args.steps = 10 if args.workload == "e2e" else 200
     if args.warmup is None:
-        args.warmup = 1 if args.workload == "e2e" else 20
+        args.warmup = 2 if args.workload == "e2e" else 20
     return args
 
 
@@ -316,13 +322,30 @@ def prefill_main(args, dev, hip) -> int:
     return 0
 
 
+def near_tie_rule(gpu_logits, ref_logits, gpu_tok: int, ref_tok: int) -> dict:
+    """The per-step rule of tests/test_gpu_model.py: a different argmax is a
+    near-tie when the oracle's margin between the two tokens is within
+    twice the step's largest logit error plus the BF16 rounding of the
+    logits."""
+    import numpy as np
+    g = np.asarray(gpu_logits, dtype=np.float64)
+    r = np.asarray(ref_logits, dtype=np.float64)
+    err = float(np.max(np.abs(g - r)))
+    margin = float(r[ref_tok] - r[gpu_tok])
+    bound = 2 * err + 2.0 ** -8 * float(np.max(np.abs(r)))
+    cos = float(g @ r / np.sqrt((g @ g) * (r @ r)))
+    return {"gpu_token": int(gpu_tok), "oracle_token": int(ref_tok), "margin": margin,
+            "bound": bound, "logits_cosine": round(cos, 6), "near_tie": margin <= bound}
+
+
 def e2e_cpu_baseline(cfg, tensors, gpu_model, seconds: float):
     """Config 0 on the CPU: the FP32 oracle model on the dequantised weights
     of the GPU run, prompt of 32 uniform-random tokens (seed 0), greedy
     decode until `seconds` of decode time or 128 tokens.  Also runs the GPU
-    model on the same prompt and reports where the two greedy sequences
-    first differ (near-ties between FP32 and BF16 activations may split
-    them; the per-step agreement is pinned by tests/test_gpu_model.py)."""
+    model on the same prompt, finds where the two greedy sequences first
+    differ and checks that step with the per-step near-tie rule (both
+    models teacher-forced to the common prefix); a difference that is not
+    a near-tie fails the bench."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
     import oracle  # test infrastructure: the CPU baseline leg only
@@ -349,10 +372,21 @@ def e2e_cpu_baseline(cfg, tensors, gpu_model, seconds: float):
             break
     decode_s = time.perf_counter() - t0
     steps = len(cpu_tokens) - 1
-    cpu.close()
     gpu_tokens, _ = gpu_model.generate(prompt, len(cpu_tokens), stop_on_eos=False)
     first_diff = next((i for i, (a, b) in enumerate(zip(gpu_tokens, cpu_tokens)) if a != b),
                       None)
+    divergence = None
+    if first_diff is not None:
+        # Both models on the common prefix, then the step that differs.
+        ref_tok, ref_logits = cpu.prefill(prompt, logits=True)
+        gpu_model.reset()
+        gpu_tok = gpu_model.prefill(prompt)
+        for i in range(first_diff):
+            ref_tok, ref_logits = cpu.decode(cpu_tokens[i], len(prompt) + i, logits=True)
+            gpu_tok = gpu_model.decode_next(cpu_tokens[i])
+        divergence = near_tie_rule(gpu_model.last_logits_host(), ref_logits, gpu_tok, ref_tok)
+        divergence["step"] = first_diff
+    cpu.close()
     return {
         "value": round(steps / decode_s, 3),
         "unit": "tok/s",
@@ -364,13 +398,18 @@ def e2e_cpu_baseline(cfg, tensors, gpu_model, seconds: float):
                    f"dequantised weights of the GPU run (max_seq {max_seq})"),
         "greedy_tokens_compared": len(cpu_tokens),
         "first_divergence_vs_gpu": first_diff,
+        "divergence_check": divergence,
     }
 
 
-def e2e_roofline(model, mid: int, ms: float, traffic_path: str):
+LINEAR_KINDS = ("qkv_gemv", "attn_o_gemv", "gate_up_gemv", "down_gemv")
+
+
+def e2e_roofline(model, mid: int, ms_per_token: float, traffic_path: str):
     """The decode step's dominant kernel kind (largest time per token), from
     the model's per-kind graph replays timed with HIP events on its stream
-    (infer_hip_model_kernel_times, which resets the model)."""
+    (infer_hip_model_kernel_times, which resets the model), and the decode
+    Linear launches' combined rate (decode_linear)."""
     kt = model.kernel_times(mid, reps=20)
     per_token_us = {n: us * launches for n, (us, _, launches) in kt.items()}
     dominant = max(per_token_us, key=per_token_us.get)
@@ -384,6 +423,10 @@ def e2e_roofline(model, mid: int, ms: float, traffic_path: str):
     breakdown = {n: {"us_per_launch": round(u, 2), "launches_per_token": ln,
                      "us_per_token": round(u * ln, 1), "GBs": round(nb / (u * 1e-6) / 1e9, 1)}
                  for n, (u, nb, ln) in kt.items()}
+    lin = [kt[n] for n in LINEAR_KINDS if n in kt]
+    lin_bytes = sum(nb * ln for (_, nb, ln) in lin)
+    lin_us = sum(u * ln for (u, _, ln) in lin)
+    lin_gbs = lin_bytes / (lin_us * 1e-6) / 1e9
     return {
         "bound": "hbm",
         "kernel": f"{dominant} (decode step, W8A16, context {mid + 1})",
@@ -394,12 +437,157 @@ def e2e_roofline(model, mid: int, ms: float, traffic_path: str):
         "traffic": traffic,
         "algorithmic_bytes_per_launch": int(nbytes),
         "avg_launch_us": round(us, 2),
+        "decode_linear": {
+            "what": ("the decode step's Linear launches per token (q|k|v with the RMSNorm, "
+                     "o with the attention merge and residual, gate|up with the RMSNorm and "
+                     "SiLU-mul, down with the residual): their compulsory bytes over their "
+                     "summed launch time"),
+            "bytes_per_token": int(lin_bytes),
+            "us_per_token": round(lin_us, 1),
+            "achieved": round(lin_gbs, 1),
+            "unit": "GB/s",
+            "frac": round(lin_gbs / HBM_PEAK_GBS, 4),
+        },
         "decode_step": {
             "compulsory_bytes_per_token": int(step_bytes),
-            "step_GBs": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+            "step_GBs": round(step_bytes / (ms_per_token * 1e-3) / 1e9, 1),
             "kernels": breakdown,
         },
     }
+
+
+def export_model_dir(cfg, checkpoint, workdir: str, precision: str):
+    """The reference's export_model.py then Qwen2Model(dir): the FP32
+    checkpoint through the library's QWENBIN1 exporter into workdir."""
+    import archive_hip
+    with open(os.path.join(workdir, "config.json"), "w") as f:
+        json.dump({"model_type": "qwen2", "hidden_size": cfg.hidden_size,
+                   "intermediate_size": cfg.intermediate_size,
+                   "num_hidden_layers": cfg.num_layers,
+                   "num_attention_heads": cfg.num_heads,
+                   "num_key_value_heads": cfg.num_kv_heads, "vocab_size": cfg.vocab_size,
+                   "max_position_embeddings": 32768, "eos_token_id": cfg.eos_token_id,
+                   "rms_norm_eps": cfg.rms_norm_eps, "rope_theta": cfg.rope_theta,
+                   "tie_word_embeddings": True}, f)
+    return archive_hip.export(checkpoint, os.path.join(workdir, f"model.{precision}.qbin"),
+                              precision, 64, source="random_checkpoint(seed=4)")
+
+
+def stats_of(values):
+    import numpy as np
+    v = np.asarray(values, dtype=np.float64)
+    return {"mean": round(float(v.mean()), 3), "p50": round(float(np.percentile(v, 50)), 3),
+            "p95": round(float(np.percentile(v, 95)), 3)}
+
+
+def e2e_detail(workdirs: dict, cfg, warmup: int = 5, repeat: int = 20) -> dict:
+    """The reference's protocol (docs/performance.md:44-52) on the HIP path,
+    W8A16 and W16A16, models opened from their exported model directories:
+    canonical (32 prompt + 128 output, max_seq 256), prefill sweep (1/32/128/
+    512 prompt + 1 output, max_seq 640), decode context sweep (32/128/512
+    prompt + 128 output, max_seq 640; and 895 + 128 at max_seq 1024, contexts
+    to 1023).  Each cell: warmup 5, repeat 20, prompt seed 0."""
+    import numpy as np
+    import model_hip
+    out = {}
+    for precision, wd in workdirs.items():
+        res = {}
+
+        def run(max_seq, prompt_len, new_tokens):
+            prompt = [int(v) for v in
+                      np.random.default_rng(0).integers(0, cfg.vocab_size, prompt_len)]
+            m = model_hip.Qwen2Model.open(wd, precision, max_sequence_length=max_seq)
+            for _ in range(warmup):
+                m.generate(prompt, new_tokens, stop_on_eos=False)
+            ttft, dec = [], []
+            for _ in range(repeat):
+                _, st = m.generate(prompt, new_tokens, stop_on_eos=False)
+                ttft.append(st.ttft_ms)
+                if new_tokens > 1:
+                    dec.append(st.decode_tokens_per_second())
+            m.close()
+            cell = {"ttft_ms": stats_of(ttft),
+                    "prefill_tok_s": round(prompt_len / (float(np.median(ttft)) * 1e-3), 1)}
+            if dec:
+                cell["decode_tok_s"] = stats_of(dec)
+                cell["tpot_ms"] = round(1000.0 / float(np.median(dec)), 4)
+            return cell
+
+        res["canonical_32+128_max256"] = run(256, 32, 128)
+        res["prefill_sweep_max640"] = {f"p{p}": run(640, p, 1) for p in (1, 32, 128, 512)}
+        sweep = {f"context_{p}": run(640, p, 128) for p in (32, 128, 512)}
+        sweep["context_895_to_1023_max1024"] = run(1024, 895, 128)
+        res["decode_context_sweep"] = sweep
+        out[precision] = res
+    return out
+
+
+def linear_calls_detail(dev) -> dict:
+    """tools/linear_benchmark.cpp:230-550 on the HIP path: each of the seven
+    Linears of a layer as its own call (the reference's per-Linear call
+    pattern), M = 1 (GEMV) and M = 32 / 128 / 512 (GEMM), W8A16 and BF16,
+    weights rotated over 4 layers' distinct tensors; per shape the mean
+    launch time over 100 calls after 20, and the layer's sum."""
+    import torch
+    import linear_hip as hip
+    out = {}
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    layers = 4
+    for w8 in (True, False):
+        for m in (1, 32, 128, 512):
+            per = {}
+            total_us = 0.0
+            for name, n, k in SHAPES:
+                calls = []
+                for _ in range(layers):
+                    x = torch.randn((m, k), device=dev, generator=g).to(torch.bfloat16)
+                    y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+                    if w8:
+                        q = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev,
+                                          generator=g)
+                        sc = ((torch.randn((n, k // 64), device=dev, generator=g) * 0.02)
+                              .abs_() / 127.0).to(torch.bfloat16)
+                        calls.append((q, sc, 64, None, x, y, m, n, k) if m > 1 else
+                                     (q, sc, 64, None, x, y, n, k))
+                    else:
+                        w = (torch.randn((n, k), device=dev, generator=g) * 0.02).to(
+                            torch.bfloat16)
+                        calls.append((w, None, x, y, m, n, k) if m > 1 else
+                                     (w, None, x, y, n, k))
+                fn = ({(True, True): hip.gemv_w8a16, (True, False): hip.gemm_w8a16,
+                       (False, True): hip.gemv_bf16, (False, False): hip.gemm_bf16}
+                      [(w8, m == 1)])
+                idx = [0]
+
+                def one(ev, calls=calls, fn=fn):
+                    fn(*calls[idx[0] % layers])
+                    idx[0] += 1
+                t, _ = time_steps(one, 100, 20)
+                us = t / 100 * 1e3
+                total_us += us
+                cell = {"us_per_call": round(us, 2)}
+                if m == 1:
+                    nbytes = (gemv_bytes(n, k) if w8 else 2 * n * k + 2 * k + 2 * n)
+                    cell["GBs"] = round(nbytes / (us * 1e-6) / 1e9, 1)
+                else:
+                    cell["TFLOPs"] = round(2.0 * m * n * k / (us * 1e-6) / 1e12, 2)
+                per[name] = cell
+            out[f"{'w8a16' if w8 else 'bf16'}_M{m}"] = {"per_shape": per,
+                                                        "layer_us": round(total_us, 2)}
+    return out
+
+
+def hbm_read_ceiling(dev) -> dict:
+    """A library streaming read (torch sum over 1 GiB of FP32, more than the
+    256 MB last-level cache) as the practical read-bandwidth reference."""
+    import torch
+    x = torch.ones((1 << 28,), dtype=torch.float32, device=dev)
+    t, _ = time_steps(lambda ev: x.sum(), 20, 3)
+    ms = t / 20
+    del x
+    return {"kernel": "torch.sum over 1 GiB FP32", "us": round(ms * 1e3, 1),
+            "GBs": round((1 << 30) / (ms * 1e-3) / 1e9, 1)}
 
 
 def e2e_main(args, dev):
@@ -409,9 +597,10 @@ def e2e_main(args, dev):
     import synthetic as S
     cfg = S.QWEN25_0_5B
     max_seq = 1024
-    steps, prompt_len = args.steps, args.prompt
-    if prompt_len + steps + 1 > max_seq:
-        print(f"bench.py: prompt {prompt_len} + {steps} steps exceeds max_seq {max_seq}",
+    prompt_len = args.prompt
+    decode_len = max_seq - 1 - prompt_len   # config 4: 512 generated = 1 + 511 decode steps
+    if decode_len < 1:
+        print(f"bench.py: prompt {prompt_len} leaves no decode step at max_seq {max_seq}",
               file=sys.stderr)
         return 2
     # Config 4's model: the FP32 checkpoint exported to a W8A16 archive and
@@ -421,81 +610,93 @@ def e2e_main(args, dev):
     import tempfile
     import archive_hip
     graph = args.graph == "on"
-    workdir = tempfile.mkdtemp(prefix="qwen-w8a16-")
+    workdirs = {p: tempfile.mkdtemp(prefix=f"qwen-{p}-") for p in ("w8a16", "w16a16")}
     try:
         t0 = time.perf_counter()
         checkpoint = S.random_checkpoint(cfg, seed=4, std=0.02, plain_init=True)
-        with open(os.path.join(workdir, "config.json"), "w") as f:
-            json.dump({"model_type": "qwen2", "hidden_size": cfg.hidden_size,
-                       "intermediate_size": cfg.intermediate_size,
-                       "num_hidden_layers": cfg.num_layers,
-                       "num_attention_heads": cfg.num_heads,
-                       "num_key_value_heads": cfg.num_kv_heads, "vocab_size": cfg.vocab_size,
-                       "max_position_embeddings": 32768, "eos_token_id": cfg.eos_token_id,
-                       "rms_norm_eps": cfg.rms_norm_eps, "rope_theta": cfg.rope_theta,
-                       "tie_word_embeddings": True}, f)
         t1 = time.perf_counter()
-        report = archive_hip.export(checkpoint, os.path.join(workdir, "model.w8a16.qbin"),
-                                    "w8a16", 64, source="random_checkpoint(seed=4)")
+        report = export_model_dir(cfg, checkpoint, workdirs["w8a16"], "w8a16")
         t2 = time.perf_counter()
+        if args.detail:
+            export_model_dir(cfg, checkpoint, workdirs["w16a16"], "w16a16")
         del checkpoint
-        model = model_hip.Qwen2Model.open(workdir, "w8a16", max_sequence_length=max_seq,
-                                          use_graph=graph)
         t3 = time.perf_counter()
-        with archive_hip.ModelArchive(os.path.join(workdir, "model.w8a16.qbin")) as archive:
+        model = model_hip.Qwen2Model.open(workdirs["w8a16"], "w8a16",
+                                          max_sequence_length=max_seq, use_graph=graph)
+        t4 = time.perf_counter()
+        with archive_hip.ModelArchive(os.path.join(workdirs["w8a16"],
+                                                   "model.w8a16.qbin")) as archive:
             tensors = {r.name: archive.data(r.name) for r in archive.records}
+        archive_info = {"export_s": round(t2 - t1, 2), "open_s": round(t4 - t3, 2),
+                        "archive_bytes": report["bytes"],
+                        "max_groupwise_abs_error": report["max_groupwise_abs_error"],
+                        "init_s": round(t1 - t0, 2)}
+        prompt = [int(v) for v in
+                  np.random.default_rng(4).integers(0, cfg.vocab_size, prompt_len)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        first = model.prefill(prompt)
+        ttft_ms = (time.perf_counter() - t0) * 1e3
+        # One step = config 4's whole decode: back to the end of the prompt
+        # (its KV cache is kept; no prefill inside the timed region), then
+        # decode_len free-running greedy steps, one graph replay each.
+        tokens = []
+
+        def step():
+            model.rewind(prompt_len, first)
+            tokens.append(model.decode_steps(decode_len))
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        if any(t != tokens[0] for t in tokens):
+            raise SystemExit("bench: repeated decodes of one prompt gave different tokens")
+        ms_per_step = elapsed * 1e3 / args.steps
+        ms_per_token = ms_per_step / decode_len
+        mid = prompt_len + decode_len // 2
+        roofline = None
+        if graph:
+            roofline = e2e_roofline(model, mid, ms_per_token, args.traffic)
+        # Config 1 beside it: the 168 Linear GEMVs of a token as one grouped plan.
+        import linear_hip as hip
+        layers = Layers(dev)
+        plan = hip.W8A16GemvPlan(layers.calls)
+        t_plan, _ = time_steps(lambda ev: plan.launch(), 100, 10)
+        plan_ms = t_plan / 100
+        plan_gbs = plan.bytes / (plan_ms * 1e-3) / 1e9
+        plan_line = {
+            "workload": "config 1: 168 W8A16 GEMVs of one token (24 layers x 7 shapes), one "
+                        "grouped launch",
+            "achieved": round(plan_gbs, 1), "unit": "GB/s",
+            "frac": round(plan_gbs / HBM_PEAK_GBS, 4), "avg_launch_us": round(plan_ms * 1e3, 2),
+        }
+        if roofline is not None:
+            roofline["linear_gemv_plan"] = plan_line
+        plan.close()
+        del layers
+        cpu = None
+        if args.cpu_seconds > 0:
+            cpu = e2e_cpu_baseline(cfg, tensors, model, args.cpu_seconds)
+        model.close()
+        detail = None
+        if args.detail:
+            detail = {"e2e": e2e_detail(workdirs, cfg), "linear_calls": linear_calls_detail(dev),
+                      "lm_head": lm_head_detail(dev, hip), "hbm_read_ceiling": hbm_read_ceiling(dev)}
     finally:
-        shutil.rmtree(workdir, ignore_errors=True)
-    archive_info = {"export_s": round(t2 - t1, 2), "open_s": round(t3 - t2, 2),
-                    "archive_bytes": report["bytes"],
-                    "max_groupwise_abs_error": report["max_groupwise_abs_error"],
-                    "init_s": round(t1 - t0, 2)}
-    prompt = [int(v) for v in np.random.default_rng(4).integers(0, cfg.vocab_size, prompt_len)]
-    for _ in range(args.warmup):
-        model.generate(prompt, steps + 1, stop_on_eos=False)
-    model.reset()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    first = model.prefill(prompt)
-    ttft_ms = (time.perf_counter() - t0) * 1e3
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    tokens = model.decode_steps(steps)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    ms = elapsed * 1e3 / steps
-    mid = prompt_len + steps // 2
-    roofline = None
-    if graph:
-        roofline = e2e_roofline(model, mid, ms, args.traffic)
-    # Config 1 beside it: the 168 Linear GEMVs of a token as one grouped plan.
-    import linear_hip as hip
-    layers = Layers(dev)
-    plan = hip.W8A16GemvPlan(layers.calls)
-    t_plan, _ = time_steps(lambda ev: plan.launch(), 100, 10)
-    plan_ms = t_plan / 100
-    plan_gbs = plan.bytes / (plan_ms * 1e-3) / 1e9
-    plan_line = {
-        "workload": "config 1: 168 W8A16 GEMVs of one token (24 layers x 7 shapes), one "
-                    "grouped launch",
-        "achieved": round(plan_gbs, 1), "unit": "GB/s",
-        "frac": round(plan_gbs / HBM_PEAK_GBS, 4), "avg_launch_us": round(plan_ms * 1e3, 2),
-    }
-    if roofline is not None:
-        roofline["linear_gemv_plan"] = plan_line
-    plan.close()
-    del layers
-    cpu = None
-    if args.cpu_seconds > 0:
-        cpu = e2e_cpu_baseline(cfg, tensors, model, args.cpu_seconds)
+        for wd in workdirs.values():
+            shutil.rmtree(wd, ignore_errors=True)
     line = {
         "metric": METRIC,
-        "value": round(steps / elapsed, 1),
+        "value": round(args.steps * decode_len / elapsed, 1),
         "unit": "tok/s",
         "n_gpus": 1,
-        "steps": steps,
+        "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
+        "ms_per_step": round(ms_per_step, 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -503,21 +704,31 @@ def e2e_main(args, dev):
         "data": "synthetic",
         "config": {
             "workload": (f"config 4: W8A16 greedy decode, random-init Qwen2.5-0.5B-shaped "
-                         f"model (seed 4), prompt {prompt_len} (prefill untimed: "
-                         f"{ttft_ms:.2f} ms), {steps} decode steps timed, max_seq {max_seq}, "
-                         f"BF16 KV cache, batch 1, "
+                         f"model (seed 4), prompt {prompt_len} (prefill once, untimed: "
+                         f"{ttft_ms:.2f} ms), one step = the whole {decode_len}-token decode "
+                         f"to context {prompt_len + decode_len} (max_seq {max_seq}), BF16 KV "
+                         f"cache, batch 1, "
                          + ("one HIP graph replay per token" if graph
                             else "kernels launched one by one")),
+            "decode_tokens_per_step": decode_len,
+            "ms_per_token": round(ms_per_token, 5),
             "parallelism": "single GPU",
             "archive": archive_info,
             "first_token": first,
-            "last_token": tokens[-1] if tokens else first,
+            "last_token": tokens[-1][-1],
         },
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
+    if args.detail:
+        with open(args.detail, "w") as f:
+            json.dump({"line": line, "detail": detail}, f, indent=1)
     print(json.dumps(line))
-    model.close()
+    div = (cpu or {}).get("divergence_check")
+    if div is not None and not div["near_tie"]:
+        print(f"bench.py: GPU and CPU greedy tokens differ at step {div['step']} by more "
+              f"than a near-tie: {div}", file=sys.stderr)
+        return 3
     return 0
 
 

@@ -1,0 +1,139 @@
+/*
+ * C ABI of the fused decode-step operators: the kernels the HIP decode
+ * runtime (infer_model.h) runs for one token, exposed one by one on
+ * caller-owned device memory.
+ *
+ * No single reference function corresponds to any of them.  Each replaces a
+ * short sequence of the reference's per-op calls on the decode path of
+ * Qwen2Model::decode_next (src/qwen2.cpp:597-674, Greedy-cy/qwen2.5-jetson-
+ * inference) with one launch:
+ *
+ *   infer_hip_rms_norm_gemv_w8a16      rms_norm_bf16 (include/infer/cuda_ops.hpp:
+ *                                      63-65) + gemv_w8a16 (cuda_ops.hpp:47-50)
+ *                                      for q, k and v (qwen2.cpp:612-626)
+ *   infer_hip_rms_norm_gate_up_silu_w8a16
+ *                                      rms_norm_bf16 + gemv_w8a16 (gate, up) +
+ *                                      silu_mul_bf16 (cuda_ops.hpp:100-101;
+ *                                      qwen2.cpp:643-654)
+ *   infer_hip_gemv_w8a16_rows          gemv_w8a16 + add_inplace_bf16 (cuda_ops.hpp:
+ *                                      98-99) for down_proj and the residual
+ *                                      (qwen2.cpp:655-659)
+ *   infer_hip_attention_merge_o_proj   the merge of a context-split
+ *                                      attention_decode_bf16 (cuda_ops.hpp:86-91)
+ *                                      + gemv (o_proj) + add_inplace_bf16
+ *                                      (qwen2.cpp:633-641)
+ *   infer_hip_rms_norm_lm_head_argmax  rms_norm_bf16 + lm_head_bf16
+ *                                      (cuda_ops.hpp:42-45; qwen2.cpp:660-667)
+ *
+ * Numerics are those of the unfused ops: the normalised activations are
+ * rounded to BF16 as rms_norm_bf16 stores them, gate and up are rounded to
+ * BF16 before SiLU-mul, sums are FP32 and outputs BF16 round-to-nearest-
+ * even.  Differences, on purpose: a residual add is one rounding,
+ * bf16(W x + r), where the reference rounds W x first; the LM-head argmax is
+ * over the FP32 sums (ties to the lowest index), as the CPU path's
+ * std::max_element (src/cpu_ops.cpp:175-177).
+ *
+ * Preconditions, checked on the host (status INFER_HIP_INVALID_ARGUMENT):
+ * in_features % 64 == 0 for the W8A16 operators, 16-byte aligned weight,
+ * input and norm-weight pointers, and the size limits of each entry point.
+ * Every entry point is asynchronous on `stream`, allocates nothing and
+ * returns an infer_linear.h status, with the message in
+ * infer_hip_last_error on failure.
+ */
+#ifndef INFER_DECODE_H
+#define INFER_DECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#include "infer_linear.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* One GEMV of infer_hip_rms_norm_gemv_w8a16 (W8A16, group 64). */
+typedef struct infer_hip_norm_gemv {
+  const int8_t* weight;   /* int8 [out_features, in_features] */
+  const uint16_t* scales; /* BF16 [out_features, in_features / 64] */
+  const uint16_t* bias;   /* BF16 [out_features] or NULL */
+  uint16_t* output;       /* BF16 [out_features] */
+  int out_features;
+} infer_hip_norm_gemv;
+
+/* xn = bf16(rms_norm(input) * norm_weight) (src/cpu_ops.cpp:15-21 with the
+ * BF16 store of rms_norm_bf16), then for each of the `count` (1..3) GEMVs
+ * output = bf16(W xn + bias), one launch.  in_features <= 4096. */
+int infer_hip_rms_norm_gemv_w8a16(const uint16_t* input, const uint16_t* norm_weight,
+                                  float epsilon, int in_features,
+                                  const infer_hip_norm_gemv* gemvs, int count,
+                                  hipStream_t stream);
+
+/* xn as above; output[i] = bf16(silu(g) * u) with g = bf16(gate_i . xn),
+ * u = bf16(up_i . xn) (src/cpu_ops.cpp:168-173 on BF16 operands), one
+ * launch.  in_features <= 4096. */
+int infer_hip_rms_norm_gate_up_silu_w8a16(const uint16_t* input, const uint16_t* norm_weight,
+                                          float epsilon, int in_features,
+                                          const int8_t* gate_weight,
+                                          const uint16_t* gate_scales,
+                                          const int8_t* up_weight, const uint16_t* up_scales,
+                                          uint16_t* output, int intermediate_size,
+                                          hipStream_t stream);
+
+/* output[n] = bf16(sum_k q[n,k] s[n,k/64] input[k] + bias[n]) with one
+ * wave per output row and the whole row in flight at once.  bias may be
+ * NULL or equal to output (the in-place residual add of the decode step:
+ * every element is read and then written by the same lane); it must not
+ * otherwise overlap output.  in_features <= 8192. */
+int infer_hip_gemv_w8a16_rows(const int8_t* weight, const uint16_t* scales,
+                              const uint16_t* bias, const uint16_t* input, uint16_t* output,
+                              int out_features, int in_features, hipStream_t stream);
+
+/* Context span and split count of the decode attention at a KV capacity of
+ * max_sequence_length positions: split i covers positions
+ * [i * span, (i + 1) * span).  0 for max_sequence_length < 1. */
+int infer_hip_attention_decode_span(int max_sequence_length);
+int infer_hip_attention_decode_splits(int max_sequence_length);
+
+/* Merge of a context-split decode attention, then the o-projection with the
+ * residual add:
+ *   p     = min(*position, max_sequence_length - 1) (device memory),
+ *   S     = p / span + 1 splits,
+ *   a[h]  = bf16( sum_{i<S} acc[h,i] e^(m[h,i]-M) / sum_{i<S} l[h,i] e^(m[h,i]-M) ),
+ *           M = max_{i<S} m[h,i]   (FP32, per head h and dimension),
+ *   residual[n] = bf16(W[n] . a + residual[n]).
+ * partials holds num_heads x max_splits records of head_dim + 2 floats:
+ * acc[0..head_dim) (the split's unnormalised sum of e^(score - m) v), m
+ * (its largest score) and l (its sum of e^(score - m)); records of splits
+ * >= S are not read.  weight is [out_features, num_heads * head_dim], int8
+ * with BF16 group-64 scales, or BF16 when scales is NULL.  span and
+ * max_splits must be infer_hip_attention_decode_span / _splits of
+ * max_sequence_length; num_heads <= 32, head_dim 64 or 128. */
+int infer_hip_attention_merge_o_proj(const float* partials, const int* position,
+                                     int num_heads, int head_dim, int span, int max_splits,
+                                     int max_sequence_length, const void* weight,
+                                     const uint16_t* scales, uint16_t* residual,
+                                     int out_features, hipStream_t stream);
+
+/* Workspace of infer_hip_rms_norm_lm_head_argmax for a vocabulary of `vocab`
+ * rows (0 if vocab < 1).  The caller zeroes it once before the first call;
+ * every call leaves it zeroed again. */
+size_t infer_hip_lm_head_decode_workspace_bytes(int vocab);
+
+/* logits[v] = bf16(E[v] . xn) with xn = bf16(rms_norm(input) * norm_weight),
+ * and *argmax = the first index of the largest FP32 sum, one launch; the
+ * last workgroup to finish reduces the per-workgroup winners.  weight is
+ * BF16 [vocab, in_features]; in_features % 8 == 0 and <= 4096; workspace
+ * as above (calls that share a workspace must not overlap). */
+int infer_hip_rms_norm_lm_head_argmax(const uint16_t* input, const uint16_t* norm_weight,
+                                      float epsilon, const uint16_t* weight, int vocab,
+                                      int in_features, uint16_t* logits, void* workspace,
+                                      int* argmax, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* INFER_DECODE_H */

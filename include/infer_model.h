@@ -128,6 +128,16 @@ int infer_hip_model_prefill(infer_hip_model* model, const int* tokens, int count
  * the current position; writes the argmax to *next_token (synchronizes). */
 int infer_hip_model_decode_next(infer_hip_model* model, int token, int* next_token);
 
+/* Truncates the context to its first `position` positions (their KV-cache
+ * rows are kept) and makes `token` the next decode input, at `position`:
+ * the state a prefill of those positions leaves, without recomputing it.
+ * Requires a prefilled model, 1 <= position <= its position and a token
+ * in range; host-side only (no GPU work).  No reference counterpart (the
+ * reference can only reset, src/qwen2.cpp:711-714): for decoding again
+ * from a shared prompt, e.g. a benchmark that repeats one decode, or for
+ * dropping tokens a caller rejects. */
+int infer_hip_model_rewind(infer_hip_model* model, int position, int token);
+
 /* Free-running greedy decode: `steps` steps, each feeding the previous
  * step's argmax, starting from the token the last prefill / decode_next
  * returned.  No host synchronization between steps; tokens_out (host, may

@@ -253,8 +253,8 @@ __global__ __launch_bounds__(kBlock) void gemv_w8_rows_kernel(GemvRowsArgs a) {
 // stride of the grid's wave count, keeping the next task's loads in flight.
 // R rows per task (1, 2, 4 or 8).
 // Every workgroup leaves its best (value, index) pair; the last to finish
-// (counted on `counter`) reduces them, writes the token to state->token and,
-// with `advance`, records it in history[state->step] and moves the step and
+// (counted on `counter`) reduces them, writes the token to *token and, with
+// `advance`, records it in history[state->step] and moves the step and
 // position on by one.  It then resets the counter.
 template <int SLABS, int R>
 __global__ __launch_bounds__(kBlock) void lm_head_decode_kernel(LmHeadDecodeArgs a) {
@@ -370,9 +370,9 @@ __global__ __launch_bounds__(kBlock) void lm_head_decode_kernel(LmHeadDecodeArgs
         wi[0] = wi[k];
       }
     }
-    ModelState* st = a.state;
-    st->token = wi[0];
+    *a.token = wi[0];
     if (a.advance) {
+      ModelState* st = a.state;
       const int step = st->step;
       if (step < a.history_len) a.history[step] = wi[0];
       st->step = step + 1;
@@ -389,8 +389,9 @@ __global__ __launch_bounds__(kBlock) void lm_head_decode_kernel(LmHeadDecodeArgs
 //   x[row] = bf16(Wo[row] . attn + x[row])
 // All 256 threads first request their weight row (one row per wave, four
 // per workgroup) and the partials, then merge into LDS; the GEMV reads attn
-// from LDS.  Partials past a head's last split or past the buffer read as
-// zeros or as other heads' records and are weighted 0.
+// from LDS.  Records past a head's last split (stale, or other heads'
+// records, or zeros past the buffer) are loaded with the rest but never
+// enter a sum, so whatever they hold cannot reach the result.
 template <int SLABS, bool W8, int MAXS, int R>
 __global__ __launch_bounds__(kBlock) void attn_o_gemv_kernel(AttnOArgs a) {
   constexpr int kChunk = W8 ? 16 : 8;          // values per 16-byte weight chunk
@@ -442,7 +443,7 @@ __global__ __launch_bounds__(kBlock) void attn_o_gemv_kernel(AttnOArgs a) {
   const float mv = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pr, ml, 0, 0));
   const float lv = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pr, ml + 4u, 0, 0));
   __builtin_amdgcn_sched_barrier(0);  // every load is in flight
-  const int pos = min(a.state->pos, a.max_seq - 1);
+  const int pos = min(*a.pos, a.max_seq - 1);
   const int splits = pos / a.span + 1;
   if (tid < a.heads * MAXS) {
     ms[tid / MAXS][tid % MAXS] = mv;
@@ -459,7 +460,7 @@ __global__ __launch_bounds__(kBlock) void attn_o_gemv_kernel(AttnOArgs a) {
 #pragma unroll
     for (int sp = 0; sp < MAXS; ++sp) {
       e[sp] = sp < splits ? expf(ms[tid][sp] - mm) : 0.0f;
-      ll = fmaf(ls[tid][sp], e[sp], ll);
+      if (sp < splits) ll = fmaf(ls[tid][sp], e[sp], ll);
     }
 #pragma unroll
     for (int sp = 0; sp < MAXS; ++sp) hw[tid][sp] = e[sp] / ll;
@@ -472,7 +473,9 @@ __global__ __launch_bounds__(kBlock) void attn_o_gemv_kernel(AttnOArgs a) {
       const int h = o / hd;
       float v = 0.0f;
 #pragma unroll
-      for (int sp = 0; sp < MAXS; ++sp) v = fmaf(acc_s[i][sp], hw[h][sp], v);
+      for (int sp = 0; sp < MAXS; ++sp) {
+        if (sp < splits) v = fmaf(acc_s[i][sp], hw[h][sp], v);
+      }
       attn[o] = bf16_to_f32(f32_to_bf16(v));  // the attention output is BF16
     }
   }
@@ -653,21 +656,31 @@ int lm_head_decode_blocks(int vocab) {
   return need < cap ? need : cap;
 }
 
+// A wave keeps two tasks of R rows x SLABS 16-byte chunks in flight (the
+// current one and the next), 8 VGPRs per (row, chunk): R x SLABS is capped at
+// 16 so that they fit without spilling (K > 2048 takes fewer rows per task).
+template <int SLABS, int R>
+static void launch_lm_head_fit(const LmHeadDecodeArgs& a, int grid, hipStream_t stream) {
+  constexpr int kFit = R * SLABS > 16 ? 16 / SLABS : R;
+  hipLaunchKernelGGL((lm_head_decode_kernel<SLABS, kFit>), dim3(grid), dim3(kBlock), 0, stream,
+                     a);
+}
+
 template <int R>
 static void launch_lm_head_rows(const LmHeadDecodeArgs& a, int grid, hipStream_t stream) {
   switch (lm_head_decode_slabs(a.k)) {
     case 1:
-      hipLaunchKernelGGL((lm_head_decode_kernel<1, R>), dim3(grid), dim3(kBlock), 0, stream, a);
+      launch_lm_head_fit<1, R>(a, grid, stream);
       break;
     case 2:
-      hipLaunchKernelGGL((lm_head_decode_kernel<2, R>), dim3(grid), dim3(kBlock), 0, stream, a);
+      launch_lm_head_fit<2, R>(a, grid, stream);
       break;
     case 3:
     case 4:
-      hipLaunchKernelGGL((lm_head_decode_kernel<4, R>), dim3(grid), dim3(kBlock), 0, stream, a);
+      launch_lm_head_fit<4, R>(a, grid, stream);
       break;
     default:
-      hipLaunchKernelGGL((lm_head_decode_kernel<8, R>), dim3(grid), dim3(kBlock), 0, stream, a);
+      launch_lm_head_fit<8, R>(a, grid, stream);
       break;
   }
 }

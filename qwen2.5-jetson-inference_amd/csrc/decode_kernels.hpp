@@ -27,6 +27,11 @@ struct NormGemvDesc {
 
 constexpr int kNormGemvMaxDescs = 3;
 constexpr int kNormGemvMaxSlabs = 4;  // K <= 4096
+// Rows (gate|up: row pairs) per wave of the decode step's fused launches:
+// measured at the Qwen2.5-0.5B shapes, two beat one (q|k|v 3.26 -> 3.07 us,
+// gate|up 5.14 -> 4.95 us per launch).
+constexpr int kQkvRowsPerWave = 2;
+constexpr int kGateUpRowsPerWave = 2;
 
 struct NormGemvArgs {
   const uint16_t* x;       // [k] BF16 (the residual stream)
@@ -65,7 +70,7 @@ constexpr int kAttnOMaxHeads = 32;
 
 struct AttnOArgs {
   const float* partial;     // heads x max_splits x (head_dim + 2) floats
-  const ModelState* state;
+  const int* pos;           // position of the decoded token (device)
   int heads;
   int head_dim;
   int span;                 // attention_span(max_seq)
@@ -93,7 +98,8 @@ struct LmHeadDecodeArgs {
   uint16_t* logits;        // [vocab] BF16
   float* block_best;       // lm_head_decode_blocks(vocab) (value, index) pairs
   int* counter;            // zero between launches
-  ModelState* state;
+  int* token;              // the argmax is written here
+  ModelState* state;       // with advance: step / pos moved on (else unused)
   int* history;
   int history_len;
   int advance;             // nonzero: record the token and advance step / pos

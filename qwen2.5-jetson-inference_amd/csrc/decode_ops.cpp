@@ -1,0 +1,184 @@
+// C ABI of the fused decode-step operators (include/infer_decode.h): the
+// kernels of decode_kernels.hip, launched exactly as the model's decode step
+// launches them (same rows per wave, grids and kernel instantiations), on
+// caller-owned memory.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "decode_kernels.hpp"
+#include "infer_decode.h"
+#include "model_kernels.hpp"
+#include "status.hpp"
+
+using namespace qlin;
+
+namespace {
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Byte layout of the LM-head workspace: the finishing counter, then one
+// (value, index) pair per workgroup.
+constexpr size_t kLmCounterBytes = 256;
+
+int check_norm_input(const uint16_t* input, const uint16_t* norm_weight, int in_features,
+                     const char* what) {
+  if (!input || !norm_weight) return fail(INFER_HIP_INVALID_ARGUMENT, "%s: null input", what);
+  if (!aligned16(input) || !aligned16(norm_weight)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: input and norm weight must be 16-byte aligned",
+                what);
+  }
+  if (!norm_gemv_w8_supported(in_features)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "%s: in_features %d must be a multiple of 64 in [64, %d]", what, in_features,
+                1024 * kNormGemvMaxSlabs);
+  }
+  return INFER_HIP_OK;
+}
+
+int check_w8(const int8_t* w, const uint16_t* s, const void* out, int n, const char* what) {
+  if (!w || !s || !out) return fail(INFER_HIP_INVALID_ARGUMENT, "%s: null pointer", what);
+  if (!aligned16(w)) return fail(INFER_HIP_INVALID_ARGUMENT, "%s: weight not 16-byte aligned", what);
+  if (n < 1) return fail(INFER_HIP_INVALID_ARGUMENT, "%s: out_features %d < 1", what, n);
+  return INFER_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" int infer_hip_rms_norm_gemv_w8a16(const uint16_t* input, const uint16_t* norm_weight,
+                                             float epsilon, int in_features,
+                                             const infer_hip_norm_gemv* gemvs, int count,
+                                             hipStream_t stream) {
+  const char* what = "rms_norm_gemv_w8a16";
+  int rc = check_norm_input(input, norm_weight, in_features, what);
+  if (rc != INFER_HIP_OK) return rc;
+  if (!gemvs || count < 1 || count > kNormGemvMaxDescs) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: count %d must be in [1, %d]", what, count,
+                kNormGemvMaxDescs);
+  }
+  NormGemvArgs a{input, norm_weight, epsilon, in_features, count, kQkvRowsPerWave, {}};
+  int blocks = 0;
+  for (int i = 0; i < count; ++i) {
+    const infer_hip_norm_gemv& g = gemvs[i];
+    rc = check_w8(g.weight, g.scales, g.output, g.out_features, what);
+    if (rc != INFER_HIP_OK) return rc;
+    a.d[i] = NormGemvDesc{g.weight, g.scales, nullptr, nullptr, g.bias, g.output,
+                          g.out_features, blocks};
+    blocks += norm_gemv_blocks(g.out_features, kQkvRowsPerWave);
+  }
+  launch_norm_gemv_w8(a, blocks, false, stream);
+  return check_launch(what);
+}
+
+extern "C" int infer_hip_rms_norm_gate_up_silu_w8a16(
+    const uint16_t* input, const uint16_t* norm_weight, float epsilon, int in_features,
+    const int8_t* gate_weight, const uint16_t* gate_scales, const int8_t* up_weight,
+    const uint16_t* up_scales, uint16_t* output, int intermediate_size, hipStream_t stream) {
+  const char* what = "rms_norm_gate_up_silu_w8a16";
+  int rc = check_norm_input(input, norm_weight, in_features, what);
+  if (rc == INFER_HIP_OK) rc = check_w8(gate_weight, gate_scales, output, intermediate_size, what);
+  if (rc == INFER_HIP_OK) rc = check_w8(up_weight, up_scales, output, intermediate_size, what);
+  if (rc != INFER_HIP_OK) return rc;
+  NormGemvArgs a{input, norm_weight, epsilon, in_features, 1, kGateUpRowsPerWave, {}};
+  a.d[0] = NormGemvDesc{gate_weight, gate_scales, up_weight, up_scales, nullptr, output,
+                        intermediate_size, 0};
+  launch_norm_gemv_w8(a, norm_gemv_blocks(intermediate_size, kGateUpRowsPerWave), true, stream);
+  return check_launch(what);
+}
+
+extern "C" int infer_hip_gemv_w8a16_rows(const int8_t* weight, const uint16_t* scales,
+                                         const uint16_t* bias, const uint16_t* input,
+                                         uint16_t* output, int out_features, int in_features,
+                                         hipStream_t stream) {
+  const char* what = "gemv_w8a16_rows";
+  int rc = check_w8(weight, scales, output, out_features, what);
+  if (rc != INFER_HIP_OK) return rc;
+  if (!input || !aligned16(input)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: input null or not 16-byte aligned", what);
+  }
+  if (!gemv_w8_rows_supported(in_features)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "%s: in_features %d must be a multiple of 64 in [64, 8192]", what, in_features);
+  }
+  launch_gemv_w8_rows({weight, scales, bias, input, output, out_features, in_features}, stream);
+  return check_launch(what);
+}
+
+extern "C" int infer_hip_attention_decode_span(int max_sequence_length) {
+  return max_sequence_length < 1 ? 0 : attention_span(max_sequence_length);
+}
+
+extern "C" int infer_hip_attention_decode_splits(int max_sequence_length) {
+  return max_sequence_length < 1 ? 0 : attention_splits(max_sequence_length);
+}
+
+extern "C" int infer_hip_attention_merge_o_proj(const float* partials, const int* position,
+                                                int num_heads, int head_dim, int span,
+                                                int max_splits, int max_sequence_length,
+                                                const void* weight, const uint16_t* scales,
+                                                uint16_t* residual, int out_features,
+                                                hipStream_t stream) {
+  const char* what = "attention_merge_o_proj";
+  if (!partials || !position || !weight || !residual) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: null pointer", what);
+  }
+  if (max_sequence_length < 1 || span != attention_span(max_sequence_length) ||
+      max_splits != attention_splits(max_sequence_length)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "%s: span %d / splits %d do not match max_sequence_length %d", what, span,
+                max_splits, max_sequence_length);
+  }
+  if (!attention_head_dim_supported(head_dim) || num_heads < 1) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: head_dim %d (64 or 128), num_heads %d", what,
+                head_dim, num_heads);
+  }
+  const bool w8 = scales != nullptr;
+  const int k = num_heads * head_dim;
+  if (!attn_o_supported(k, num_heads, w8)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: %d heads x %d is not supported", what,
+                num_heads, head_dim);
+  }
+  if (!aligned16(weight)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: weight not 16-byte aligned", what);
+  }
+  if (out_features < 1) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: out_features %d < 1", what, out_features);
+  }
+  launch_attn_o_gemv({partials, position, num_heads, head_dim, span, max_splits,
+                      max_sequence_length, weight, scales, residual, out_features, k},
+                     w8, stream);
+  return check_launch(what);
+}
+
+extern "C" size_t infer_hip_lm_head_decode_workspace_bytes(int vocab) {
+  if (vocab < 1) return 0;
+  return kLmCounterBytes + 8 * static_cast<size_t>(lm_head_decode_blocks(vocab));
+}
+
+extern "C" int infer_hip_rms_norm_lm_head_argmax(const uint16_t* input,
+                                                 const uint16_t* norm_weight, float epsilon,
+                                                 const uint16_t* weight, int vocab,
+                                                 int in_features, uint16_t* logits,
+                                                 void* workspace, int* argmax,
+                                                 hipStream_t stream) {
+  const char* what = "rms_norm_lm_head_argmax";
+  if (!input || !norm_weight || !weight || !logits || !workspace || !argmax) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: null pointer", what);
+  }
+  if (!aligned16(input) || !aligned16(norm_weight) || !aligned16(weight) ||
+      !aligned16(workspace)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "%s: input, norm weight, weight and workspace must be 16-byte aligned", what);
+  }
+  if (vocab < 1 || !lm_head_decode_supported(in_features)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "%s: vocab %d, in_features %d (a multiple of 8 in [8, %d])", what, vocab,
+                in_features, 512 * kLmHeadMaxSlabs);
+  }
+  char* ws = static_cast<char*>(workspace);
+  launch_lm_head_decode({input, norm_weight, epsilon, weight, vocab, in_features, logits,
+                         reinterpret_cast<float*>(ws + kLmCounterBytes),
+                         reinterpret_cast<int*>(ws), argmax, nullptr, nullptr, 0, 0},
+                        stream);
+  return check_launch(what);
+}

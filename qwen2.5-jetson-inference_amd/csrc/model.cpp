@@ -75,9 +75,6 @@ struct Layer {
 // Rows per block of the decode step's grouped GEMVs: one 4-row task per
 // wave, the most blocks a grouped launch can have.
 constexpr int kDecodeRowsPerBlock = 16;
-// Rows (gate|up: row pairs) per wave of the fused RMSNorm + GEMV launches.
-constexpr int kQkvRowsPerWave = 2;
-constexpr int kGateUpRowsPerWave = 2;
 
 constexpr size_t kAlign = 256;
 size_t align_up(size_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
@@ -269,8 +266,9 @@ int lm_head_step(infer_hip_model* m, const uint16_t* row, bool advance) {
   const infer_hip_model_config& c = m->cfg;
   if (m->fused_lm_head) {
     launch_lm_head_decode({row, m->final_norm, c.rms_norm_eps, m->lm_head, c.vocab_size,
-                           c.hidden_size, m->logits, m->lm_best, m->lm_counter, m->state,
-                           m->history, m->max_seq, advance ? 1 : 0},
+                           c.hidden_size, m->logits, m->lm_best, m->lm_counter,
+                           &m->state->token, m->state, m->history, m->max_seq,
+                           advance ? 1 : 0},
                           m->stream);
     return check_launch("lm head");
   }
@@ -338,7 +336,7 @@ int enqueue_decode_step(infer_hip_model* m, int only = -1, hipEvent_t* events = 
     });
     // x = bf16(Wo attn + x), attn merged from the attention's split partials
     run(kKindAttnO, [&] {
-      launch_attn_o_gemv({m->attn_partial, m->state, c.num_heads, m->head_dim,
+      launch_attn_o_gemv({m->attn_partial, &m->state->pos, c.num_heads, m->head_dim,
                           attention_span(m->max_seq), attention_splits(m->max_seq), m->max_seq,
                           L.o.w, L.o.s, m->x, hidden, hidden},
                          m->w8, s);
@@ -1055,6 +1053,25 @@ extern "C" int infer_hip_model_decode_next(infer_hip_model* m, int token, int* n
   if (rc != INFER_HIP_OK) return rc;
   ++m->position;
   m->last_token = *next_token;
+  return ok();
+}
+
+extern "C" int infer_hip_model_rewind(infer_hip_model* m, int position, int token) {
+  if (!m) return fail(INFER_HIP_INVALID_ARGUMENT, "rewind: null model");
+  if (!m->has_prefilled) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "rewind requires a successful prefill");
+  }
+  if (position < 1 || position > m->position) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "rewind: position %d outside [1, %d]", position,
+                m->position);
+  }
+  if (token < 0 || token >= m->cfg.vocab_size) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "input token out of range");
+  }
+  // Every decode entry point sets the device state from these two values
+  // before its first step, so nothing on the device needs to change here.
+  m->position = position;
+  m->last_token = token;
   return ok();
 }
 

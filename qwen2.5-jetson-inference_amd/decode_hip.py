@@ -1,0 +1,117 @@
+"""Python binding of the fused decode-step operators (include/infer_decode.h).
+
+Each function launches one of the kernels the HIP decode runtime runs for a
+token, on caller-owned device memory: arguments are device pointers
+(``int``) or contiguous torch CUDA tensors, ``None`` is a null pointer, and
+a nonzero status raises :class:`linear_hip.InferError`.  They replace short
+sequences of the reference's per-op calls on its decode path
+(src/qwen2.cpp:597-674, Greedy-cy/qwen2.5-jetson-inference); the header
+names the sequence each one stands for.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import linear_hip
+from linear_hip import _check, _ptr, _stream
+
+# Every symbol include/infer_decode.h declares.
+EXPORTED_SYMBOLS = (
+    "infer_hip_rms_norm_gemv_w8a16",
+    "infer_hip_rms_norm_gate_up_silu_w8a16",
+    "infer_hip_gemv_w8a16_rows",
+    "infer_hip_attention_decode_span",
+    "infer_hip_attention_decode_splits",
+    "infer_hip_attention_merge_o_proj",
+    "infer_hip_lm_head_decode_workspace_bytes",
+    "infer_hip_rms_norm_lm_head_argmax",
+)
+
+
+class NormGemv(ctypes.Structure):
+    """infer_hip_norm_gemv."""
+    _fields_ = [("weight", ctypes.c_void_p), ("scales", ctypes.c_void_p),
+                ("bias", ctypes.c_void_p), ("output", ctypes.c_void_p),
+                ("out_features", ctypes.c_int)]
+
+
+_bound = False
+
+
+def load():
+    global _bound
+    lib = linear_hip.load()
+    if _bound:
+        return lib
+    p, i, f = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+    sigs = {
+        "infer_hip_rms_norm_gemv_w8a16": ([p, p, f, i, ctypes.POINTER(NormGemv), i, p], i),
+        "infer_hip_rms_norm_gate_up_silu_w8a16": ([p, p, f, i, p, p, p, p, p, i, p], i),
+        "infer_hip_gemv_w8a16_rows": ([p, p, p, p, p, i, i, p], i),
+        "infer_hip_attention_decode_span": ([i], i),
+        "infer_hip_attention_decode_splits": ([i], i),
+        "infer_hip_attention_merge_o_proj": ([p, p, i, i, i, i, i, p, p, p, i, p], i),
+        "infer_hip_lm_head_decode_workspace_bytes": ([i], ctypes.c_size_t),
+        "infer_hip_rms_norm_lm_head_argmax": ([p, p, f, p, i, i, p, p, p, p], i),
+    }
+    for name, (args, res) in sigs.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    _bound = True
+    return lib
+
+
+def rms_norm_gemv_w8a16(input, norm_weight, epsilon: float, in_features: int, gemvs,
+                        stream=None) -> None:
+    """gemvs: up to three (weight, scales, bias, output, out_features)."""
+    arr = (NormGemv * max(1, len(gemvs)))()
+    for k, (w, s, b, y, n) in enumerate(gemvs):
+        arr[k] = NormGemv(_ptr(w), _ptr(s), _ptr(b), _ptr(y), int(n))
+    _check(load().infer_hip_rms_norm_gemv_w8a16(_ptr(input), _ptr(norm_weight), epsilon,
+                                                in_features, arr, len(gemvs),
+                                                _stream(stream)))
+
+
+def rms_norm_gate_up_silu_w8a16(input, norm_weight, epsilon: float, in_features: int,
+                                gate_weight, gate_scales, up_weight, up_scales, output,
+                                intermediate_size: int, stream=None) -> None:
+    _check(load().infer_hip_rms_norm_gate_up_silu_w8a16(
+        _ptr(input), _ptr(norm_weight), epsilon, in_features, _ptr(gate_weight),
+        _ptr(gate_scales), _ptr(up_weight), _ptr(up_scales), _ptr(output),
+        intermediate_size, _stream(stream)))
+
+
+def gemv_w8a16_rows(weight, scales, bias, input, output, out_features: int,
+                    in_features: int, stream=None) -> None:
+    _check(load().infer_hip_gemv_w8a16_rows(_ptr(weight), _ptr(scales), _ptr(bias),
+                                            _ptr(input), _ptr(output), out_features,
+                                            in_features, _stream(stream)))
+
+
+def attention_decode_span(max_sequence_length: int) -> int:
+    return load().infer_hip_attention_decode_span(max_sequence_length)
+
+
+def attention_decode_splits(max_sequence_length: int) -> int:
+    return load().infer_hip_attention_decode_splits(max_sequence_length)
+
+
+def attention_merge_o_proj(partials, position, num_heads: int, head_dim: int, span: int,
+                           max_splits: int, max_sequence_length: int, weight, scales,
+                           residual, out_features: int, stream=None) -> None:
+    _check(load().infer_hip_attention_merge_o_proj(
+        _ptr(partials), _ptr(position), num_heads, head_dim, span, max_splits,
+        max_sequence_length, _ptr(weight), _ptr(scales), _ptr(residual), out_features,
+        _stream(stream)))
+
+
+def lm_head_decode_workspace_bytes(vocab: int) -> int:
+    return load().infer_hip_lm_head_decode_workspace_bytes(vocab)
+
+
+def rms_norm_lm_head_argmax(input, norm_weight, epsilon: float, weight, vocab: int,
+                            in_features: int, logits, workspace, argmax, stream=None) -> None:
+    _check(load().infer_hip_rms_norm_lm_head_argmax(
+        _ptr(input), _ptr(norm_weight), epsilon, _ptr(weight), vocab, in_features,
+        _ptr(logits), _ptr(workspace), _ptr(argmax), _stream(stream)))

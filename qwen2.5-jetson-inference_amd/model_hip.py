@@ -32,6 +32,7 @@ EXPORTED_SYMBOLS = (
     "infer_hip_model_prefill",
     "infer_hip_model_decode_next",
     "infer_hip_model_decode_steps",
+    "infer_hip_model_rewind",
     "infer_hip_model_generate",
     "infer_hip_model_last_logits",
     "infer_hip_model_position",
@@ -114,6 +115,7 @@ def load():
         "infer_hip_model_prefill": ([p, ip, i, ip], i),
         "infer_hip_model_decode_next": ([p, i, ip], i),
         "infer_hip_model_decode_steps": ([p, i, ip], i),
+        "infer_hip_model_rewind": ([p, i, i], i),
         "infer_hip_model_generate": ([p, ip, i, i, i, ip, ip, ctypes.POINTER(_Stats)], i),
         "infer_hip_model_last_logits": ([p, ctypes.POINTER(ctypes.c_float)], i),
         "infer_hip_model_position": ([p], i),
@@ -266,6 +268,11 @@ class Qwen2Model:
         buf = (ctypes.c_int * max(1, steps))()
         _check(self._lib.infer_hip_model_decode_steps(self._h, steps, buf))
         return list(buf[:steps])
+
+    def rewind(self, position: int, token: int) -> None:
+        """Keep the first `position` positions of the context and decode
+        `token` next (infer_hip_model_rewind)."""
+        _check(self._lib.infer_hip_model_rewind(self._h, int(position), int(token)))
 
     def generate(self, prompt_tokens, max_new_tokens: int, stop_on_eos: bool = True):
         toks = _int_array(prompt_tokens)

@@ -162,6 +162,7 @@ def test_model_null_handles_are_rejected(hip):
     assert lib.infer_hip_model_prefill(None, None, 0, ctypes.byref(out)) == hip.INVALID_ARGUMENT
     assert lib.infer_hip_model_decode_next(None, 0, ctypes.byref(out)) == hip.INVALID_ARGUMENT
     assert lib.infer_hip_model_decode_steps(None, 1, None) == hip.INVALID_ARGUMENT
+    assert lib.infer_hip_model_rewind(None, 1, 1) == hip.INVALID_ARGUMENT
     assert lib.infer_hip_model_position(None) == -1
     assert lib.infer_hip_model_destroy(None) == hip.OK
 
@@ -176,3 +177,69 @@ def test_attention_prefill_rejects_bad_arguments_on_host(hip):
     assert f(16, 16, 16, 16, 9, 2, 1, 64, 8, None) == hip.INVALID_ARGUMENT
     assert f(16, 16, 16, 16, 4, 3, 2, 64, 8, None) == hip.INVALID_ARGUMENT
     assert f(16, 16, 16, 16, 0, 2, 1, 64, 8, None) == hip.INVALID_ARGUMENT
+
+
+def test_library_exports_every_decode_symbol(hip):
+    import decode_hip
+    lib = decode_hip.load()
+    text = open(os.path.join(ROOT, "include", "infer_decode.h")).read()
+    declared = sorted(set(re.findall(r"\b(infer_hip_\w+)\s*\(", text)))
+    assert declared
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert sorted(decode_hip.EXPORTED_SYMBOLS) == declared
+
+
+def test_decode_ops_reject_bad_arguments_on_host(hip):
+    # Every check runs before any HIP call; fake 16-byte aligned addresses
+    # are never dereferenced.
+    import ctypes
+    import decode_hip
+    lib = decode_hip.load()
+    bad = hip.INVALID_ARGUMENT
+    err = lambda: lib.infer_hip_last_error().decode()  # noqa: E731
+    g = (decode_hip.NormGemv * 1)(decode_hip.NormGemv(4096, 4096, None, 4096, 896))
+    f = lib.infer_hip_rms_norm_gemv_w8a16
+    assert f(None, 4096, 1e-6, 896, g, 1, None) == bad
+    assert f(4104, 4096, 1e-6, 896, g, 1, None) == bad and "aligned" in err()
+    assert f(4096, 4096, 1e-6, 900, g, 1, None) == bad and "multiple of 64" in err()
+    assert f(4096, 4096, 1e-6, 8192, g, 1, None) == bad
+    assert f(4096, 4096, 1e-6, 896, g, 0, None) == bad and "count" in err()
+    assert f(4096, 4096, 1e-6, 896, g, 4, None) == bad
+    g[0].weight = 4097
+    assert f(4096, 4096, 1e-6, 896, g, 1, None) == bad and "weight" in err()
+    g[0].weight, g[0].out_features = 4096, 0
+    assert f(4096, 4096, 1e-6, 896, g, 1, None) == bad
+    f = lib.infer_hip_rms_norm_gate_up_silu_w8a16
+    assert f(4096, 4096, 1e-6, 896, 4096, None, 4096, 4096, 4096, 4864, None) == bad
+    assert f(4096, 4096, 1e-6, 896, 4096, 4096, 4096, 4096, 4096, -1, None) == bad
+    f = lib.infer_hip_gemv_w8a16_rows
+    assert f(4096, 4096, None, 4096, 4096, 896, 8256, None) == bad and "8192" in err()
+    assert f(4096, 4096, None, 4098, 4096, 896, 4864, None) == bad
+    assert f(4096, 4096, None, None, 4096, 896, 4864, None) == bad
+    f = lib.infer_hip_attention_merge_o_proj
+    assert f(4096, 4096, 14, 64, 64, 8, 1024, 4096, 4096, 4096, 896, None) == bad
+    assert "span" in err()
+    assert f(4096, 4096, 14, 32, 128, 8, 1024, 4096, 4096, 4096, 896, None) == bad
+    assert f(4096, 4096, 33, 64, 128, 8, 1024, 4096, 4096, 4096, 896, None) == bad
+    assert f(4096, None, 14, 64, 128, 8, 1024, 4096, 4096, 4096, 896, None) == bad
+    assert f(4096, 4096, 14, 64, 128, 8, 1024, 4104, 4096, 4096, 896, None) == bad
+    f = lib.infer_hip_rms_norm_lm_head_argmax
+    assert f(4096, 4096, 1e-6, 4096, 151936, 900, 4096, 4096, 4096, None) == bad
+    assert f(4096, 4096, 1e-6, 4096, 0, 896, 4096, 4096, 4096, None) == bad
+    assert f(4096, 4096, 1e-6, 4096, 151936, 896, 4096, 4100, 4096, None) == bad
+    assert f(4096, 4096, 1e-6, 4096, 151936, 896, 4096, 4096, None, None) == bad
+    assert lib.infer_hip_lm_head_decode_workspace_bytes(0) == 0
+    assert lib.infer_hip_lm_head_decode_workspace_bytes(151936) >= 256 + 8
+
+
+def test_attention_decode_span_closed_form(hip):
+    # span: 128-position multiples covering max_seq in at most 8 splits
+    import decode_hip
+    for max_seq in (1, 7, 128, 129, 1000, 1024, 1025, 4096, 32768):
+        span = decode_hip.attention_decode_span(max_seq)
+        splits = decode_hip.attention_decode_splits(max_seq)
+        assert span % 128 == 0 and 1 <= splits <= 8, (max_seq, span, splits)
+        assert span * (splits - 1) < max_seq <= span * splits
+        assert span == 128 or (span - 128) * 8 < max_seq  # the smallest that fits 8 splits
+    assert decode_hip.attention_decode_span(0) == 0

@@ -119,8 +119,10 @@ def test_teacher_forced_decode(orc, dev, cfg, precision, graph):
 
 
 def test_long_context_decode_spans_many_chunks(orc, dev):
-    # Positions up to 330: the decode attention splits the context over six
-    # 64-position chunks and merges them.  Weights of a realistic scale
+    # Positions up to 330 at max_seq 1024: the decode attention splits the
+    # context over three 128-position spans and merges them (the 14-head
+    # case over up to eight spans is test_qwen_shaped_decode_across_eight_
+    # spans).  Weights of a realistic scale
     # (attention scores of order one): with the hotter test weights the
     # BF16 rounding of q and k alone moves long-context softmax weights by
     # a few percent.
@@ -265,37 +267,6 @@ def test_model_rejects_bad_shapes(dev):
         model_hip.Qwen2Model(TINY, {k: v for k, v in t.items() if "o_proj" not in k}, "w8a16")
 
 
-def test_qwen25_full_size_teacher_forced(orc, dev):
-    """Config 4's model (24 layers, vocab 151936, W8A16 export of a random
-    init) against the FP32 oracle on the dequantized weights."""
-    cfg = S.QWEN25_0_5B
-    t = S.random_model(cfg, "w8a16", seed=4)
-    print("full-size model generated", flush=True)
-    g = model_hip.Qwen2Model(cfg, t, "w8a16", max_sequence_length=64)
-    fp32 = S.dequantized_fp32(t, cfg)
-    o = oracle_model(orc, cfg, fp32, 64)
-    p = prompt(16, cfg.vocab_size, seed=4)
-    tok = g.prefill(p)
-    ref_tok, ref_logits = o.prefill(p, logits=True)
-    check_step(tok, g.last_logits_host(), ref_tok, ref_logits, 0.999, "prefill")
-    agree, first_divergence, worst = int(tok == ref_tok), None, 1.0
-    for step in range(16):
-        token = ref_tok
-        tok = g.decode_next(token)
-        ref_tok, ref_logits = o.decode(token, len(p) + step, logits=True)
-        same, cos = check_step(tok, g.last_logits_host(), ref_tok, ref_logits, 0.999,
-                               f"step {step}")
-        agree += same
-        worst = min(worst, cos)
-        if not same and first_divergence is None:
-            first_divergence = step
-    print(f"full-size teacher-forced argmax agreement {agree}/17, first divergence "
-          f"{first_divergence}, worst logits cosine {worst:.6f}", flush=True)
-    assert agree >= 15
-    g.close()
-    o.close()
-
-
 def test_kernel_times_reports_every_launch_kind_and_resets(dev):
     t, _ = weights(TINY, "w8a16")
     g = model_hip.Qwen2Model(TINY, t, "w8a16", max_sequence_length=64)
@@ -317,4 +288,150 @@ def test_kernel_times_reports_every_launch_kind_and_resets(dev):
     g.reset()
     with pytest.raises(model_hip.InferError):
         g.kernel_times(5)  # not prefilled
+    g.close()
+
+
+# ------------------------------------------------ BASELINE configs 0 and 4 --
+
+_full = {}
+
+
+def full_size(orc, max_seq):
+    """The config 0 / 4 model: Qwen2.5-0.5B shape, FP32 init N(0, 0.02) with
+    norm weights 1 and biases 0 (a freshly built model), group-64 W8A16;
+    the GPU runtime and the FP32 oracle on the same dequantised weights."""
+    cfg = S.QWEN25_0_5B
+    if "t" not in _full:
+        _full["t"] = S.random_model(cfg, "w8a16", seed=4, plain_init=True)
+        _full["fp32"] = S.dequantized_fp32(_full["t"], cfg)
+        print("full-size model generated", flush=True)
+    g = model_hip.Qwen2Model(cfg, _full["t"], "w8a16", max_sequence_length=max_seq)
+    o = oracle_model(orc, cfg, _full["fp32"], max_seq)
+    return cfg, g, o
+
+
+def teacher_forced(g, o, p, steps, min_cos, what):
+    """Prefill p on both, then `steps` decode steps each consuming the
+    oracle's token; every step must satisfy check_step.  Returns
+    (agreement, steps + 1, worst cosine)."""
+    tok = g.prefill(p)
+    ref_tok, ref_logits = o.prefill(p, logits=True)
+    same, worst = check_step(tok, g.last_logits_host(), ref_tok, ref_logits, min_cos,
+                             f"{what} prefill")
+    agree = int(same)
+    for step in range(steps):
+        token = ref_tok
+        tok = g.decode_next(token)
+        ref_tok, ref_logits = o.decode(token, len(p) + step, logits=True)
+        same, cos = check_step(tok, g.last_logits_host(), ref_tok, ref_logits, min_cos,
+                               f"{what} step {step} (context {len(p) + step + 1})")
+        agree += same
+        worst = min(worst, cos)
+    return agree, steps + 1, worst
+
+
+def test_config0_workload_teacher_forced(orc, dev):
+    """Config 0's workload on the HIP path: prompt of 32 uniform-random
+    tokens (seed 0), 128 greedy steps teacher-forced from the FP32 oracle,
+    max_seq 256 (tests/test_qwen2.cpp:513-535 restated at full size)."""
+    cfg, g, o = full_size(orc, 256)
+    p = prompt(32, cfg.vocab_size, seed=0)
+    agree, total, worst = teacher_forced(g, o, p, 127, 0.999, "config 0")
+    print(f"config 0: argmax agreement {agree}/{total}, worst logits cosine {worst:.6f}",
+          flush=True)
+    assert agree >= 0.9 * total
+    assert g.position == 32 + 127
+    g.close()
+    o.close()
+
+
+def test_config4_workload_teacher_forced(orc, dev):
+    """Config 4's workload: prompt of 512 uniform-random tokens (seed 4),
+    max_seq 1024, then teacher-forced decode to context 1023 (511 steps),
+    every step against the FP32 oracle: the prefill's grouped MFMA launches
+    at 512 rows and the decode attention over 5 to 8 context spans."""
+    cfg, g, o = full_size(orc, 1024)
+    p = prompt(512, cfg.vocab_size, seed=4)
+    agree, total, worst = teacher_forced(g, o, p, 511, 0.999, "config 4")
+    print(f"config 4: argmax agreement {agree}/{total}, worst logits cosine {worst:.6f}",
+          flush=True)
+    assert agree >= 0.9 * total
+    assert g.position == 1023
+    g.close()
+    o.close()
+
+
+def test_qwen_shaped_decode_across_eight_spans(orc, dev):
+    """14 query / 2 KV heads at max_seq 1024 (spans of 128 positions):
+    teacher-forced decode from position 500 to 1019, so the o-projection
+    merges 4, 5, 6, 7 and 8 spans of every head."""
+    cfg, precision = QWEN_SHAPED, "w8a16"
+    t = S.random_model(cfg, precision, seed=13, std=0.05)
+    fp32 = S.dequantized_fp32(t, cfg)
+    g = model_hip.Qwen2Model(cfg, t, precision, max_sequence_length=1024, use_graph=True)
+    o = oracle_model(orc, cfg, fp32, 1024)
+    p = prompt(500, cfg.vocab_size, seed=14)
+    agree, total, worst = teacher_forced(g, o, p, 520, 0.999, "8 spans")
+    print(f"qwen-shaped long context: agreement {agree}/{total}, worst cosine {worst:.6f}",
+          flush=True)
+    assert agree >= 0.85 * total
+    g.close()
+    o.close()
+
+
+# Gate|up of this shape at 512 tokens has 2 x 32 x 2 = 128 tiles of 256 x 128
+# (enough for the 256 CUs, so the wide tile) and K = 1024 = 16 stages, split
+# into 2 parts of 8: the prefill's wide-tile grouped kernel with its in-arena
+# split-K reduction.  q|k|v, o and down (K = 4096) take split 64 x 64 tiles.
+WIDE_SPLIT = S.ModelConfig(hidden_size=1024, intermediate_size=4096, num_layers=2,
+                           num_heads=16, num_kv_heads=2, vocab_size=2048)
+
+
+@pytest.mark.parametrize("cfg,precision", [(QWEN_SHAPED, "w8a16"), (QWEN_SHAPED, "w16a16"),
+                                           (WIDE_SPLIT, "w8a16"), (WIDE_SPLIT, "w16a16")],
+                         ids=["qwen_w8a16", "qwen_w16a16", "wide_split_w8a16",
+                              "wide_split_w16a16"])
+def test_prefill_512_tokens_grouped_mfma(orc, dev, cfg, precision):
+    """Prefill of 512 tokens (config 4's prompt length): grouped MFMA
+    launches at M = 512 (the 256 x 128 tile for gate|up), then decode steps
+    on the KV cache it wrote."""
+    t = S.random_model(cfg, precision, seed=15, std=0.04)
+    fp32 = S.dequantized_fp32(t, cfg)
+    g = model_hip.Qwen2Model(cfg, t, precision, max_sequence_length=1024, use_graph=True)
+    o = oracle_model(orc, cfg, fp32, 1024)
+    p = prompt(512, cfg.vocab_size, seed=16)
+    agree, total, worst = teacher_forced(g, o, p, 8, 0.999, f"prefill 512 {precision}")
+    print(f"prefill 512 {cfg.hidden_size}/{precision}: agreement {agree}/{total}, "
+          f"worst cosine {worst:.6f}", flush=True)
+    assert agree >= total - 2
+    g.close()
+    o.close()
+
+
+def test_rewind_replays_the_same_decode(dev):
+    t, _ = weights(TINY, "w8a16")
+    g = model_hip.Qwen2Model(TINY, t, "w8a16", max_sequence_length=64)
+    p = prompt(20, TINY.vocab_size, seed=21)
+    first = g.prefill(p)
+    a = g.decode_steps(10)
+    logits_a = g.last_logits_host()
+    assert g.position == 30
+    g.rewind(20, first)               # back to the prompt: the same decode again
+    assert g.position == 20 and g.has_prefilled
+    assert g.decode_steps(10) == a
+    np.testing.assert_array_equal(g.last_logits_host(), logits_a)
+    g.rewind(25, a[4])                # mid-way: the rest of the same sequence
+    assert g.decode_steps(5) == a[5:]
+    g.rewind(25, a[4])
+    assert g.decode_next(a[4]) == a[5] and g.position == 26
+    err = model_hip.InferError
+    with pytest.raises(err):
+        g.rewind(27, 1)               # past the decoded context
+    with pytest.raises(err):
+        g.rewind(0, 1)
+    with pytest.raises(err):
+        g.rewind(5, TINY.vocab_size)
+    g.reset()
+    with pytest.raises(err):
+        g.rewind(1, 1)                # not prefilled
     g.close()
