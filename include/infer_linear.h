@@ -83,6 +83,23 @@ int infer_hip_lm_head_bf16(const uint16_t* weight, const uint16_t* bias,
                            int* argmax, int vocab, int in_features,
                            hipStream_t stream);
 
+/* infer_hip_lm_head_bf16 without the workspace arguments: the first-stage
+ * block winners go to a static device array of the library (65536 (value,
+ * index) pairs, 512 KiB per GPU, held until the process ends) instead of
+ * caller memory, so the call allocates nothing and needs nothing but its
+ * inputs and outputs.  No counterpart in the reference: it is for callers
+ * that cannot allocate or size a workspace (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Limit:
+ * infer_hip_lm_head_workspace_entries(vocab, in_features) <= 65536, which
+ * holds for every vocab <= 1048576; larger shapes return
+ * INFER_HIP_INVALID_ARGUMENT.  All calls on one GPU share its array: calls
+ * that overlap on one GPU (concurrent streams, threads) race.  Each call
+ * writes every entry it reads, so nothing needs clearing between calls.
+ * The stream must belong to the current device. */
+int infer_hip_lm_head_bf16_noalloc(const uint16_t* weight, const uint16_t* bias,
+                                   const uint16_t* input, uint16_t* logits, int* argmax,
+                                   int vocab, int in_features, hipStream_t stream);
+
 /* Entries of block_max_value / block_max_index infer_hip_lm_head_bf16 uses
  * for this shape (0 for invalid shapes).  No reference counterpart: the
  * reference sizes its workspace inline (src/qwen2.cpp:193-198). */

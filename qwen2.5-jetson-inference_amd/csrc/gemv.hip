@@ -23,6 +23,8 @@
 #include <limits.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "device_common.hpp"
 #include "linear_kernels.hpp"
 #include "status.hpp"
@@ -788,18 +790,14 @@ extern "C" size_t infer_hip_lm_head_workspace_entries(int vocab, int in_features
   return fast > slow ? fast : slow;
 }
 
-extern "C" int infer_hip_lm_head_bf16(const uint16_t* weight, const uint16_t* bias,
-                                      const uint16_t* input, uint16_t* logits,
-                                      float* block_max_value, int* block_max_index, int* argmax,
-                                      int vocab, int in_features, hipStream_t stream) {
-  if (vocab <= 0 || in_features < 0) {
-    return fail(INFER_HIP_INVALID_ARGUMENT, "lm_head_bf16: bad shape V=%d K=%d", vocab,
-                in_features);
-  }
-  if (!logits || !block_max_value || !block_max_index || !argmax ||
-      (in_features > 0 && (!weight || !input))) {
-    return fail(INFER_HIP_INVALID_ARGUMENT, "lm_head_bf16: null required pointer");
-  }
+namespace {
+
+// The LM head after argument checks: the first stage (logits and one
+// (value, index) winner per block into block_max_value / block_max_index),
+// then the single-block argmax over those winners.
+int launch_lm_head(const uint16_t* weight, const uint16_t* bias, const uint16_t* input,
+                   uint16_t* logits, float* block_max_value, int* block_max_index, int* argmax,
+                   int vocab, int in_features, hipStream_t stream) {
   int blocks;
   if (bf16_fast_ok(weight, input, in_features)) {
     blocks = dispatch_bf16<true>({weight, bias, input, logits, vocab, in_features},
@@ -816,4 +814,97 @@ extern "C" int infer_hip_lm_head_bf16(const uint16_t* weight, const uint16_t* bi
   hipLaunchKernelGGL(argmax_reduce_kernel, dim3(1), dim3(kReduceThreads), 0, stream,
                      block_max_value, block_max_index, blocks, argmax);
   return check_launch("lm_head_bf16 argmax");
+}
+
+int check_lm_head_args(const uint16_t* weight, const uint16_t* input, const uint16_t* logits,
+                       const int* argmax, int vocab, int in_features, const char* what) {
+  if (vocab <= 0 || in_features < 0) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: bad shape V=%d K=%d", what, vocab,
+                in_features);
+  }
+  if (!logits || !argmax || (in_features > 0 && (!weight || !input))) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: null required pointer", what);
+  }
+  return INFER_HIP_OK;
+}
+
+// ------------------------------------------- static scratch (no allocation) --
+//
+// The winners of infer_hip_lm_head_bf16_noalloc's first stage live in this
+// file-scope device array instead of a caller workspace: kNoAllocEntries
+// (value, index) pairs, values in the first half and indices in the second,
+// 512 KiB per GPU, held until the process ends.  Every call on one GPU uses
+// that GPU's copy; each call writes every entry it then reads, so nothing
+// needs clearing between calls, and calls that overlap on one GPU race.
+// 65536 entries hold the first stage of every vocab <= 2^20: at most one
+// block per 16 rows (fast path, vocab >= 65536) or 65536 blocks (generic).
+constexpr int kNoAllocEntries = 65536;
+static __device__ __align__(256) uint32_t scratch[2 * kNoAllocEntries];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device, looked up once per
+// device with that device current (each GPU holds its own copy at its own
+// address; in host code the array's name is only a stand-in for it).
+int scratch_for_current_device(void** out) {
+  int device = 0;
+  hipError_t st = hipGetDevice(&device);
+  if (st != hipSuccess) {
+    return fail(INFER_HIP_RUNTIME_ERROR, "lm_head_bf16_noalloc: %s", hipGetErrorString(st));
+  }
+  if (device < 0 || device >= kMaxDevices) {
+    return fail(INFER_HIP_RUNTIME_ERROR, "lm_head_bf16_noalloc: device %d beyond %d", device,
+                kMaxDevices);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[device]) {
+    void* ptr = nullptr;
+    st = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (st != hipSuccess || !ptr) {
+      return fail(INFER_HIP_RUNTIME_ERROR, "lm_head_bf16_noalloc: scratch address: %s",
+                  hipGetErrorString(st));
+    }
+    g_scratch_ptr[device] = ptr;
+  }
+  *out = g_scratch_ptr[device];
+  return INFER_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" int infer_hip_lm_head_bf16(const uint16_t* weight, const uint16_t* bias,
+                                      const uint16_t* input, uint16_t* logits,
+                                      float* block_max_value, int* block_max_index, int* argmax,
+                                      int vocab, int in_features, hipStream_t stream) {
+  int rc = check_lm_head_args(weight, input, logits, argmax, vocab, in_features, "lm_head_bf16");
+  if (rc != INFER_HIP_OK) return rc;
+  if (!block_max_value || !block_max_index) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "lm_head_bf16: null required pointer");
+  }
+  return launch_lm_head(weight, bias, input, logits, block_max_value, block_max_index, argmax,
+                        vocab, in_features, stream);
+}
+
+extern "C" int infer_hip_lm_head_bf16_noalloc(const uint16_t* weight, const uint16_t* bias,
+                                              const uint16_t* input, uint16_t* logits,
+                                              int* argmax, int vocab, int in_features,
+                                              hipStream_t stream) {
+  const char* what = "lm_head_bf16_noalloc";
+  int rc = check_lm_head_args(weight, input, logits, argmax, vocab, in_features, what);
+  if (rc != INFER_HIP_OK) return rc;
+  const size_t entries = infer_hip_lm_head_workspace_entries(vocab, in_features);
+  if (entries > static_cast<size_t>(kNoAllocEntries)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "%s: V=%d needs %zu scratch entries, more than the static %d (V <= %d)", what,
+                vocab, entries, kNoAllocEntries, 16 * kNoAllocEntries);
+  }
+  void* ptr = nullptr;
+  rc = scratch_for_current_device(&ptr);
+  if (rc != INFER_HIP_OK) return rc;
+  float* values = static_cast<float*>(ptr);
+  int* indices = static_cast<int*>(ptr) + kNoAllocEntries;
+  return launch_lm_head(weight, bias, input, logits, values, indices, argmax, vocab, in_features,
+                        stream);
 }

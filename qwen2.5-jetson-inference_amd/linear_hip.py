@@ -30,6 +30,7 @@ EXPORTED_SYMBOLS = (
     "infer_hip_gemv_bf16",
     "infer_hip_gemm_bf16",
     "infer_hip_lm_head_bf16",
+    "infer_hip_lm_head_bf16_noalloc",
     "infer_hip_lm_head_workspace_entries",
     "infer_hip_gemv_w8a16",
     "infer_hip_gemm_w8a16",
@@ -126,6 +127,7 @@ def load() -> ctypes.CDLL:
         "infer_hip_gemv_bf16": [p, p, p, p, i, i, p],
         "infer_hip_gemm_bf16": [p, p, p, p, i, i, i, p],
         "infer_hip_lm_head_bf16": [p, p, p, p, p, p, p, i, i, p],
+        "infer_hip_lm_head_bf16_noalloc": [p, p, p, p, p, i, i, p],
         "infer_hip_gemv_w8a16": [p, p, i, p, p, p, i, i, p],
         "infer_hip_gemm_w8a16": [p, p, i, p, p, p, i, i, i, p],
         "infer_hip_gemm_w8a16_tile": [p, p, i, p, p, p, i, i, i, i, p],
@@ -212,6 +214,15 @@ def lm_head_bf16(weight, bias, input, logits, block_max_value,
     _check(load().infer_hip_lm_head_bf16(
         _ptr(weight), _ptr(bias), _ptr(input), _ptr(logits),
         _ptr(block_max_value), _ptr(block_max_index), _ptr(argmax), vocab,
+        in_features, _stream(stream)))
+
+
+def lm_head_bf16_noalloc(weight, bias, input, logits, argmax, vocab, in_features,
+                         stream=None):
+    """lm_head_bf16 with the library's static device scratch instead of a
+    workspace (infer_hip_lm_head_bf16_noalloc; vocab <= 1048576)."""
+    _check(load().infer_hip_lm_head_bf16_noalloc(
+        _ptr(weight), _ptr(bias), _ptr(input), _ptr(logits), _ptr(argmax), vocab,
         in_features, _stream(stream)))
 
 
