@@ -92,10 +92,14 @@ int infer_hip_gemv_w8a16_rows(const int8_t* weight, const uint16_t* scales,
                               int out_features, int in_features, hipStream_t stream);
 
 /* Context span and split count of the decode attention at a KV capacity of
- * max_sequence_length positions: split i covers positions
- * [i * span, (i + 1) * span).  0 for max_sequence_length < 1. */
-int infer_hip_attention_decode_span(int max_sequence_length);
-int infer_hip_attention_decode_splits(int max_sequence_length);
+ * max_sequence_length positions and head_dim (64 or 128): split i covers
+ * positions [i * span, (i + 1) * span).  At head_dim 64 with up to 1024
+ * positions the decode step runs one workgroup per head over the whole
+ * context (span 1024, 1 split) and its o-projection is a plain GEMV;
+ * otherwise at most 8 splits, whose partials the o-projection merges.
+ * 0 for max_sequence_length < 1 or another head_dim. */
+int infer_hip_attention_decode_span(int max_sequence_length, int head_dim);
+int infer_hip_attention_decode_splits(int max_sequence_length, int head_dim);
 
 /* Merge of a context-split decode attention, then the o-projection with the
  * residual add:
@@ -110,7 +114,7 @@ int infer_hip_attention_decode_splits(int max_sequence_length);
  * >= S are not read.  weight is [out_features, num_heads * head_dim], int8
  * with BF16 group-64 scales, or BF16 when scales is NULL.  span and
  * max_splits must be infer_hip_attention_decode_span / _splits of
- * max_sequence_length; num_heads <= 32, head_dim 64 or 128. */
+ * (max_sequence_length, head_dim); num_heads <= 32, head_dim 64 or 128. */
 int infer_hip_attention_merge_o_proj(const float* partials, const int* position,
                                      int num_heads, int head_dim, int span, int max_splits,
                                      int max_sequence_length, const void* weight,

@@ -215,6 +215,84 @@ __global__ __launch_bounds__(kBlock) void norm_gemv_w8_kernel(NormGemvArgs a) {
   }
 }
 
+// q|k|v with the RMSNorm in front and the RoPE and KV-cache store behind
+// (QkvRopeArgs).  One wave per pair of output rows, all loads issued
+// before the first wait: (i, i + head_dim / 2) of a q or k head (the pair
+// the rotation mixes, so a lane holds both sums), or two consecutive rows
+// of v.  Tasks are the q pairs, then the k pairs, then the v pairs.  The
+// position is read at entry and its (cos, sin) requested once it arrives,
+// behind the weight loads, so the rotation waits on no extra round trip.
+template <int SLABS>
+__global__ __launch_bounds__(kBlock) void norm_qkv_rope_w8_kernel(QkvRopeArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int half = a.head_dim / 2;
+  const int qt = a.heads * half, kt = a.kv_heads * half;
+  const int total = qt + 2 * kt;
+  // wave-uniform (scalar registers for the task's pointers and rows)
+  const int task = __builtin_amdgcn_readfirstlane(
+      min(static_cast<int>(blockIdx.x) * kWaves + static_cast<int>(threadIdx.x) / kWave,
+          total - 1));
+  const int region = task < qt ? 0 : task < qt + kt ? 1 : 2;  // q, k, v
+  const int t = task - (region == 0 ? 0 : region == 1 ? qt : qt + kt);
+  const int8_t* w = region == 0 ? a.wq : region == 1 ? a.wk : a.wv;
+  const uint16_t* sc = region == 0 ? a.sq : region == 1 ? a.sk : a.sv;
+  const uint16_t* bias = region == 0 ? a.bq : region == 1 ? a.bk : a.bv;
+  const int n = region == 0 ? a.heads * a.head_dim : a.kv_heads * a.head_dim;
+  // rows of the pair: (head * hd + i, + half) for q and k, (2 t, 2 t + 1) for v
+  const int head = t / half, i = t % half;
+  const int r0 = region == 2 ? 2 * t : head * a.head_dim + i;
+  const int r1 = region == 2 ? 2 * t + 1 : r0 + half;
+  const int pos = min(*a.pos, a.max_seq - 1);
+  uint4 w0[SLABS], w1[SLABS];
+  uint32_t s0[SLABS], s1[SLABS];
+  load_w8_row<SLABS>(w, sc, r0, n, a.k, lane, w0, s0);
+  load_w8_row<SLABS>(w, sc, r1, n, a.k, lane, w1, s1);
+  // the biases of r0 and r1 (an absent bias reads weight bytes instead, discarded)
+  const uint16_t* bsrc = bias ? bias : reinterpret_cast<const uint16_t*>(w);
+  const uint16_t bias_raw0 = gload(bsrc + r0), bias_raw1 = gload(bsrc + r1);
+  uint4 xr[SLABS][2], nr[SLABS][2];
+  {
+    uint4 lo[SLABS], hi[SLABS];
+    load_vec16_raw<SLABS>(a.x, a.k, lane, lo, hi);
+#pragma unroll
+    for (int s = 0; s < SLABS; ++s) {
+      xr[s][0] = lo[s];
+      xr[s][1] = hi[s];
+    }
+    load_vec16_raw<SLABS>(a.norm_w, a.k, lane, lo, hi);
+#pragma unroll
+    for (int s = 0; s < SLABS; ++s) {
+      nr[s][0] = lo[s];
+      nr[s][1] = hi[s];
+    }
+  }
+  const float2 cs = a.rope_row[i];
+  __builtin_amdgcn_sched_barrier(0);  // every load is in flight
+  float xn[SLABS][16];
+  wave_rms_norm<SLABS, 16>(xr, nr, a.k, a.eps, lane, xn);
+  const float v0 = w8_row_dot<SLABS>(w0, s0, xn, true, a.k, lane);
+  const float v1 = w8_row_dot<SLABS>(w1, s1, xn, true, a.k, lane);
+  const float b = bias ? bf16_to_f32(bias_raw0) : 0.0f;
+  const float b1 = bias ? bf16_to_f32(bias_raw1) : 0.0f;
+  if (lane == 0 && static_cast<int>(blockIdx.x) * kWaves + static_cast<int>(threadIdx.x) / kWave <
+                       total) {
+    float y0 = bf16_to_f32(f32_to_bf16(v0 + b));
+    float y1 = bf16_to_f32(f32_to_bf16(v1 + b1));
+    if (region != 2) rope_pair(y0, y1, cs);
+    const uint16_t o0 = f32_to_bf16(y0), o1 = f32_to_bf16(y1);
+    if (region == 0) {
+      gstore(a.q_out + r0, o0);
+      gstore(a.q_out + r1, o1);
+    } else {
+      // row r of k or v is dimension r % head_dim of kv head r / head_dim
+      uint16_t* cache = region == 1 ? a.key_cache : a.value_cache;
+      const size_t base = (static_cast<size_t>(r0 / a.head_dim) * a.max_seq + pos) * a.head_dim;
+      gstore(cache + base + r0 % a.head_dim, o0);
+      gstore(cache + base + r1 % a.head_dim, o1);
+    }
+  }
+}
+
 // One W8A16 GEMV row per wave, all K chunks of the row requested at once
 // (lane l: chunks l, l + 64, ...), with the residual add: y[row] =
 // bf16(W[row] . x + bias[row]); bias may alias y (each element is read and
@@ -290,6 +368,14 @@ __global__ __launch_bounds__(kBlock) void lm_head_decode_kernel(LmHeadDecodeArgs
     for (int s = 0; s < SLABS; ++s) nr[s][0] = raw[s];
     __builtin_amdgcn_sched_barrier(0);  // every load is in flight
     wave_rms_norm<SLABS, 8>(xr, nr, a.k, a.eps, lane, xn);
+  }
+  // The (cos, sin) row of the next position, for the last workgroup when it
+  // advances the state (requested by every workgroup, long before needed).
+  const bool keep_rope = a.advance && a.rope.row && static_cast<int>(threadIdx.x) < a.rope.half;
+  float2 rope_next = make_float2(0.0f, 0.0f);
+  if (keep_rope) {
+    rope_next = a.rope.table[static_cast<size_t>(min(a.state->pos + 1, a.rope.max_seq - 1)) *
+                                 a.rope.half + threadIdx.x];
   }
   float best_v = -FLT_MAX;
   int best_i = INT_MAX;
@@ -380,6 +466,7 @@ __global__ __launch_bounds__(kBlock) void lm_head_decode_kernel(LmHeadDecodeArgs
     }
     __hip_atomic_store(a.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  if (keep_rope) a.rope.row[threadIdx.x] = rope_next;
 }
 
 
@@ -535,6 +622,31 @@ void launch_gemv_w8_rows(const GemvRowsArgs& a, hipStream_t stream) {
 }
 
 int norm_gemv_w8_slabs(int k) { return (k + 1023) / 1024; }
+
+int norm_qkv_rope_blocks(int heads, int kv_heads, int head_dim) {
+  const int tasks = (heads + 2 * kv_heads) * (head_dim / 2);
+  return (tasks + kWaves - 1) / kWaves;
+}
+
+bool norm_qkv_rope_supported(int k, int head_dim) {
+  return k >= 64 && k % 64 == 0 && norm_gemv_w8_slabs(k) <= kNormGemvMaxSlabs &&
+         head_dim % 2 == 0 && head_dim >= 2;
+}
+
+void launch_norm_qkv_rope_w8(const QkvRopeArgs& a, hipStream_t stream) {
+  const dim3 grid(norm_qkv_rope_blocks(a.heads, a.kv_heads, a.head_dim)), block(kBlock);
+  switch (norm_gemv_w8_slabs(a.k)) {
+    case 1:
+      hipLaunchKernelGGL(norm_qkv_rope_w8_kernel<1>, grid, block, 0, stream, a);
+      break;
+    case 2:
+      hipLaunchKernelGGL(norm_qkv_rope_w8_kernel<2>, grid, block, 0, stream, a);
+      break;
+    default:
+      hipLaunchKernelGGL(norm_qkv_rope_w8_kernel<4>, grid, block, 0, stream, a);
+      break;
+  }
+}
 
 bool norm_gemv_w8_supported(int k) {
   return k >= 64 && k % 64 == 0 && norm_gemv_w8_slabs(k) <= kNormGemvMaxSlabs;

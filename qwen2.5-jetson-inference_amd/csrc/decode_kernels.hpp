@@ -48,6 +48,42 @@ bool norm_gemv_w8_supported(int k);
 int norm_gemv_blocks(int n, int rows_per_wave);
 void launch_norm_gemv_w8(const NormGemvArgs& a, int blocks, bool pair, hipStream_t stream);
 
+// The decode step's q|k|v launch with the RoPE and the KV-cache store
+// folded in: xn = bf16(rms_norm(x) * norm_w); q = bf16(Wq xn + bq),
+// k = bf16(Wk xn + bk), v = bf16(Wv xn + bv); q and k rotated by the angles
+// of position *pos (pairs (i, i + head_dim / 2) of a head; rope_row holds
+// that position's (cos, sin), see RopeCursor) and rounded to BF16;
+// q_out <- rotated q, the caches' row *pos <- rotated k and v.
+struct QkvRopeArgs {
+  const uint16_t* x;       // [k] BF16 residual stream
+  const uint16_t* norm_w;  // [k] BF16 input RMSNorm weight
+  float eps;
+  int k;
+  const int8_t* wq;
+  const uint16_t* sq;
+  const uint16_t* bq;      // [heads * head_dim] or nullptr
+  const int8_t* wk;
+  const uint16_t* sk;
+  const uint16_t* bk;      // [kv_heads * head_dim] or nullptr
+  const int8_t* wv;
+  const uint16_t* sv;
+  const uint16_t* bv;
+  uint16_t* q_out;         // [heads * head_dim]
+  uint16_t* key_cache;     // the layer's [kv_heads][max_seq][head_dim]
+  uint16_t* value_cache;
+  const float2* rope_row;  // [head_dim / 2] (cos, sin) of position *pos
+  const int* pos;          // position of the token (device)
+  int heads;
+  int kv_heads;
+  int head_dim;
+  int max_seq;
+};
+
+// Workgroups of a launch (one wave per pair of output rows).
+int norm_qkv_rope_blocks(int heads, int kv_heads, int head_dim);
+bool norm_qkv_rope_supported(int k, int head_dim);
+void launch_norm_qkv_rope_w8(const QkvRopeArgs& a, hipStream_t stream);
+
 // One W8A16 GEMV row per wave with the whole row's loads in flight at once:
 // y[row] = bf16(W[row] . x + bias[row]), bias may alias y (the residual add).
 // K % 64 == 0, K <= 8192, 16-byte aligned w and x.
@@ -103,6 +139,7 @@ struct LmHeadDecodeArgs {
   int* history;
   int history_len;
   int advance;             // nonzero: record the token and advance step / pos
+  RopeCursor rope;         // with advance: the row follows pos
 };
 
 constexpr int kLmHeadRows = 4;  // rows per wave task

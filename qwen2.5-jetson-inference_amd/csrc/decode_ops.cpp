@@ -104,12 +104,14 @@ extern "C" int infer_hip_gemv_w8a16_rows(const int8_t* weight, const uint16_t* s
   return check_launch(what);
 }
 
-extern "C" int infer_hip_attention_decode_span(int max_sequence_length) {
-  return max_sequence_length < 1 ? 0 : attention_span(max_sequence_length);
+extern "C" int infer_hip_attention_decode_span(int max_sequence_length, int head_dim) {
+  if (max_sequence_length < 1 || !attention_head_dim_supported(head_dim)) return 0;
+  return attention_span(max_sequence_length, head_dim);
 }
 
-extern "C" int infer_hip_attention_decode_splits(int max_sequence_length) {
-  return max_sequence_length < 1 ? 0 : attention_splits(max_sequence_length);
+extern "C" int infer_hip_attention_decode_splits(int max_sequence_length, int head_dim) {
+  if (max_sequence_length < 1 || !attention_head_dim_supported(head_dim)) return 0;
+  return attention_splits(max_sequence_length, head_dim);
 }
 
 extern "C" int infer_hip_attention_merge_o_proj(const float* partials, const int* position,
@@ -122,15 +124,15 @@ extern "C" int infer_hip_attention_merge_o_proj(const float* partials, const int
   if (!partials || !position || !weight || !residual) {
     return fail(INFER_HIP_INVALID_ARGUMENT, "%s: null pointer", what);
   }
-  if (max_sequence_length < 1 || span != attention_span(max_sequence_length) ||
-      max_splits != attention_splits(max_sequence_length)) {
-    return fail(INFER_HIP_INVALID_ARGUMENT,
-                "%s: span %d / splits %d do not match max_sequence_length %d", what, span,
-                max_splits, max_sequence_length);
-  }
   if (!attention_head_dim_supported(head_dim) || num_heads < 1) {
     return fail(INFER_HIP_INVALID_ARGUMENT, "%s: head_dim %d (64 or 128), num_heads %d", what,
                 head_dim, num_heads);
+  }
+  if (max_sequence_length < 1 || span != attention_span(max_sequence_length, head_dim) ||
+      max_splits != attention_splits(max_sequence_length, head_dim)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "%s: span %d / splits %d do not match max_sequence_length %d", what, span,
+                max_splits, max_sequence_length);
   }
   const bool w8 = scales != nullptr;
   const int k = num_heads * head_dim;
@@ -178,7 +180,8 @@ extern "C" int infer_hip_rms_norm_lm_head_argmax(const uint16_t* input,
   char* ws = static_cast<char*>(workspace);
   launch_lm_head_decode({input, norm_weight, epsilon, weight, vocab, in_features, logits,
                          reinterpret_cast<float*>(ws + kLmCounterBytes),
-                         reinterpret_cast<int*>(ws), argmax, nullptr, nullptr, 0, 0},
+                         reinterpret_cast<int*>(ws), argmax, nullptr, nullptr, 0, 0,
+                         RopeCursor{nullptr, nullptr, 0, 0}},
                         stream);
   return check_launch(what);
 }

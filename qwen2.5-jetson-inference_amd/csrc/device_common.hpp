@@ -193,6 +193,14 @@ __device__ __forceinline__ bool is_row_writer(int lane) {
   return (lane & (kWave / RB - 1)) == 0;
 }
 
+// RoPE of one pair (a, b) = (x[i], x[i + head_dim / 2]) of a head by the
+// angle whose (cos, sin) is cs (src/cpu_ops.cpp:33-56).
+__device__ __forceinline__ void rope_pair(float& a, float& b, float2 cs) {
+  const float first = a, second = b;
+  a = first * cs.x - second * cs.y;
+  b = second * cs.x + first * cs.y;
+}
+
 // Global-address-space access.  Pointers that reach a kernel through memory
 // (a descriptor table) are generic to the compiler, which would then emit
 // FLAT instructions; these casts keep every access a global_* instruction.

@@ -67,6 +67,7 @@ struct Layer {
   int gate_up_blocks = 0;
   // The fused path: RMSNorm + q|k|v, RMSNorm + gate|up + SiLU-mul.
   NormGemvArgs qkv_args{};
+  QkvRopeArgs qkv_rope_args{};  // q|k|v + RoPE + KV store (whole-context attention)
   NormGemvArgs gate_up_args{};
   int qkv_fused_blocks = 0;
   int gate_up_fused_blocks = 0;
@@ -95,6 +96,9 @@ struct infer_hip_model {
   bool use_graph = false;
   bool fused_norm_gemv = false;  // W8A16 with hidden % 64 == 0, hidden <= 4096
   bool fused_lm_head = false;    // hidden % 8 == 0, hidden <= 4096
+  // the fused q|k|v launch also rotates q, k and stores k, v (W8A16 with the
+  // whole-context decode attention: head_dim 64, max_seq <= 1024)
+  bool fused_qkv_rope = false;
   int max_seq = 0;
   int head_dim = 0;
   int kv_dim = 0;
@@ -116,7 +120,9 @@ struct infer_hip_model {
   float* lm_best = nullptr;   // fused LM head: per-workgroup (value, index)
   int* lm_counter = nullptr;
   float2* rope = nullptr;
+  float2* rope_cur = nullptr;  // (cos, sin) of the decode position (RopeCursor)
   float* attn_partial = nullptr;  // decode attention split partials
+  uint16_t* attn = nullptr;       // decode attention output (whole-context form)
   // split-K scratch of the prefill's grouped GEMM launches (sized at creation
   // for every prompt length up to max_seq)
   float* gemm_partial = nullptr;
@@ -260,6 +266,11 @@ void prefill_scratch_needs(const infer_hip_model_config& c, int head_dim, int ma
   }
 }
 
+// The model's RoPE cursor: its table and the row of the decode position.
+RopeCursor rope_cursor(const infer_hip_model* m) {
+  return RopeCursor{m->rope, m->rope_cur, m->head_dim / 2, m->max_seq};
+}
+
 // Final RMSNorm of `row` and the LM head with its argmax into state->token;
 // with `advance` the step's bookkeeping too (history, step, position).
 int lm_head_step(infer_hip_model* m, const uint16_t* row, bool advance) {
@@ -268,7 +279,7 @@ int lm_head_step(infer_hip_model* m, const uint16_t* row, bool advance) {
     launch_lm_head_decode({row, m->final_norm, c.rms_norm_eps, m->lm_head, c.vocab_size,
                            c.hidden_size, m->logits, m->lm_best, m->lm_counter,
                            &m->state->token, m->state, m->history, m->max_seq,
-                           advance ? 1 : 0},
+                           advance ? 1 : 0, rope_cursor(m)},
                           m->stream);
     return check_launch("lm head");
   }
@@ -277,7 +288,7 @@ int lm_head_step(infer_hip_model* m, const uint16_t* row, bool advance) {
                                         m->lm_index, &m->state->token, c.vocab_size,
                                         c.hidden_size, m->stream);
   if (rc != INFER_HIP_OK || !advance) return rc;
-  launch_advance(m->state, m->history, m->max_seq, m->stream);
+  launch_advance(m->state, m->history, m->max_seq, rope_cursor(m), m->stream);
   return check_launch("decode step advance");
 }
 
@@ -317,7 +328,11 @@ int enqueue_decode_step(infer_hip_model* m, int only = -1, hipEvent_t* events = 
       [&] { launch_embedding(m->embed, &m->state->token, 1, c.vocab_size, hidden, m->x, s); });
   for (const Layer& L : m->layers) {
     if (m->fused_norm_gemv) {
-      run(kKindQkv, [&] { launch_norm_gemv_w8(L.qkv_args, L.qkv_fused_blocks, false, s); });
+      if (m->fused_qkv_rope) {
+        run(kKindQkv, [&] { launch_norm_qkv_rope_w8(L.qkv_rope_args, s); });
+      } else {
+        run(kKindQkv, [&] { launch_norm_gemv_w8(L.qkv_args, L.qkv_fused_blocks, false, s); });
+      }
     } else {
       run(kKindNorm,
           [&] { launch_rms_norm(m->x, L.in_norm, m->norm, 1, hidden, c.rms_norm_eps, s); });
@@ -332,14 +347,22 @@ int enqueue_decode_step(infer_hip_model* m, int only = -1, hipEvent_t* events = 
     run(kKindAttention, [&] {
       launch_attention_decode(m->q, m->k, m->v, L.key_cache, L.value_cache, m->rope, m->state,
                               c.num_heads, c.num_kv_heads, m->head_dim, m->max_seq,
-                              m->attn_partial, s);
+                              m->fused_qkv_rope, m->attn_partial, m->attn, s);
     });
-    // x = bf16(Wo attn + x), attn merged from the attention's split partials
+    // x = bf16(Wo attn + x): attn is the whole-context attention's output,
+    // or merged here from the split attention's partials
     run(kKindAttnO, [&] {
-      launch_attn_o_gemv({m->attn_partial, &m->state->pos, c.num_heads, m->head_dim,
-                          attention_span(m->max_seq), attention_splits(m->max_seq), m->max_seq,
-                          L.o.w, L.o.s, m->x, hidden, hidden},
-                         m->w8, s);
+      if (!attention_whole(m->max_seq, m->head_dim)) {
+        launch_attn_o_gemv({m->attn_partial, &m->state->pos, c.num_heads, m->head_dim,
+                            attention_span(m->max_seq, m->head_dim),
+                            attention_splits(m->max_seq, m->head_dim), m->max_seq, L.o.w, L.o.s,
+                            m->x, hidden, hidden},
+                           m->w8, s);
+      } else if (m->w8 && gemv_w8_rows_supported(hidden)) {
+        launch_gemv_w8_rows({L.o.w, L.o.s, m->x, m->attn, m->x, hidden, hidden}, s);
+      } else {
+        gemv(m, L.o, m->x, m->attn, m->x);
+      }
     });
     if (m->fused_norm_gemv) {
       run(kKindGateUp,
@@ -381,8 +404,11 @@ double kind_bytes(const infer_hip_model* m, int kind, int ctx, int* launches) {
   auto linear = [&](double n, double k) {
     return n * k * wb + (m->w8 ? 2.0 * n * (k / 64) : 0.0);
   };
-  const double splits = (ctx + attention_span(m->max_seq) - 1) / attention_span(m->max_seq);
-  const double partials = c.num_heads * splits * (hd + 2) * 4;
+  // the attention's output: split partials, or the BF16 head outputs
+  const int span = attention_span(m->max_seq, m->head_dim);
+  const double splits = (ctx + span - 1) / span;
+  const double partials =
+      attention_whole(m->max_seq, m->head_dim) ? 2 * H : c.num_heads * splits * (hd + 2) * 4;
   const bool fused = m->fused_norm_gemv;
   const bool bf16_split = !m->w8;  // separate q, k, v (and gate, up) launches
   int n = 0;
@@ -403,8 +429,12 @@ double kind_bytes(const infer_hip_model* m, int kind, int ctx, int* launches) {
       break;
     case kKindAttention:
       n = c.num_layers;
-      b = nl * (2 * c.num_kv_heads * (ctx - 1) * hd * 2 /* cached K, V */ +
-                2 * H /* q */ + 4 * KV /* new k, v */ + 4 * KV /* their store */ + partials);
+      b = m->fused_qkv_rope
+              ? nl * (2 * c.num_kv_heads * ctx * hd * 2 /* K, V rows, the new one included */ +
+                      2 * H /* q */ + partials)
+              : nl * (2 * c.num_kv_heads * (ctx - 1) * hd * 2 /* cached K, V */ +
+                      2 * H /* q */ + 4 * KV /* new k, v */ + 4 * KV /* their store */ +
+                      partials);
       break;
     case kKindAttnO:
       n = c.num_layers;
@@ -514,7 +544,7 @@ int run_prefill(infer_hip_model* m, const int* tokens, int count, int* next) {
   if (rc != INFER_HIP_OK) return rc;
   rc = lm_head_step(m, m->px + static_cast<size_t>(count - 1) * hidden, false);
   if (rc != INFER_HIP_OK) return rc;
-  launch_set_state(m->state, -1, count, 0, s);
+  launch_set_state(m->state, -1, count, 0, rope_cursor(m), s);
   rc = check_launch("prefill state");
   if (rc != INFER_HIP_OK) return rc;
   return read_token(m, next);
@@ -643,6 +673,8 @@ extern "C" int infer_hip_model_create(const infer_hip_model_config* config,
   m->lm_head = lm_head;
   m->fused_norm_gemv = w8 && norm_gemv_w8_supported(hidden);
   m->fused_lm_head = lm_head_decode_supported(hidden);
+  m->fused_qkv_rope = m->fused_norm_gemv && attention_whole(max_seq, head_dim) &&
+                      norm_qkv_rope_supported(hidden, head_dim);
 
   // Arena layout.
   size_t cursor = 0;
@@ -664,8 +696,10 @@ extern "C" int infer_hip_model_create(const infer_hip_model_config* config,
   const size_t o_lmbest = take(8 * static_cast<size_t>(lm_head_decode_blocks(c.vocab_size)));
   const size_t o_lmcounter = take(sizeof(int));
   const size_t o_rope = take(sizeof(float2) * ms * (head_dim / 2));
-  const size_t o_partial = take(sizeof(float) * c.num_heads * attention_splits(max_seq) *
-                                (head_dim + 2));
+  const size_t o_rope_cur = take(sizeof(float2) * (head_dim / 2));
+  const size_t o_partial = take(sizeof(float) * c.num_heads *
+                                attention_splits(max_seq, head_dim) * (head_dim + 2));
+  const size_t o_attn = take(2 * hidden);
   const size_t o_px = take(2 * ms * hidden), o_pnorm = take(2 * ms * hidden);
   const size_t o_pq = take(2 * ms * hidden), o_pk = take(2 * ms * kv_dim);
   const size_t o_pv = take(2 * ms * kv_dim), o_pattn = take(2 * ms * hidden);
@@ -714,7 +748,9 @@ extern "C" int infer_hip_model_create(const infer_hip_model_config* config,
   m->lm_best = reinterpret_cast<float*>(a + o_lmbest);
   m->lm_counter = reinterpret_cast<int*>(a + o_lmcounter);
   m->rope = reinterpret_cast<float2*>(a + o_rope);
+  m->rope_cur = reinterpret_cast<float2*>(a + o_rope_cur);
   m->attn_partial = reinterpret_cast<float*>(a + o_partial);
+  m->attn = reinterpret_cast<uint16_t*>(a + o_attn);
   m->px = bf(o_px); m->pnorm = bf(o_pnorm); m->pq = bf(o_pq); m->pk = bf(o_pk); m->pv = bf(o_pv);
   m->pattn = bf(o_pattn); m->ptmp = bf(o_ptmp); m->pgate = bf(o_pgate); m->pup = bf(o_pup);
   m->pmlp = bf(o_pmlp);
@@ -787,6 +823,13 @@ extern "C" int infer_hip_model_create(const infer_hip_model_config* config,
       L.qkv_args.d[0] = fdesc(L.q, nullptr, m->q, kQkvRowsPerWave, L.qkv_fused_blocks);
       L.qkv_args.d[1] = fdesc(L.k, nullptr, m->k, kQkvRowsPerWave, L.qkv_fused_blocks);
       L.qkv_args.d[2] = fdesc(L.v, nullptr, m->v, kQkvRowsPerWave, L.qkv_fused_blocks);
+      L.qkv_rope_args = QkvRopeArgs{m->x, L.in_norm, c.rms_norm_eps, hidden,
+                                    static_cast<const int8_t*>(L.q.w), L.q.s, L.q.b,
+                                    static_cast<const int8_t*>(L.k.w), L.k.s, L.k.b,
+                                    static_cast<const int8_t*>(L.v.w), L.v.s, L.v.b,
+                                    m->q, L.key_cache, L.value_cache, m->rope_cur,
+                                    &m->state->pos,
+                                    c.num_heads, c.num_kv_heads, head_dim, max_seq};
       L.gate_up_args =
           NormGemvArgs{m->x, L.post_norm, c.rms_norm_eps, hidden, 1, kGateUpRowsPerWave, {}};
       L.gate_up_args.d[0] =
@@ -1046,7 +1089,7 @@ extern "C" int infer_hip_model_decode_next(infer_hip_model* m, int token, int* n
     return fail(INFER_HIP_INVALID_ARGUMENT, "KV cache capacity exceeded");
   }
   DeviceGuard guard(m->device);
-  launch_set_state(m->state, token, m->position, 0, m->stream);
+  launch_set_state(m->state, token, m->position, 0, rope_cursor(m), m->stream);
   int rc = check_launch("decode state");
   if (rc == INFER_HIP_OK) rc = run_decode_step(m);
   if (rc == INFER_HIP_OK) rc = read_token(m, next_token);
@@ -1085,7 +1128,7 @@ extern "C" int infer_hip_model_decode_steps(infer_hip_model* m, int steps, int* 
   }
   if (steps == 0) return ok();
   DeviceGuard guard(m->device);
-  launch_set_state(m->state, m->last_token, m->position, 0, m->stream);
+  launch_set_state(m->state, m->last_token, m->position, 0, rope_cursor(m), m->stream);
   int rc = check_launch("decode state");
   for (int i = 0; i < steps && rc == INFER_HIP_OK; ++i) rc = run_decode_step(m);
   if (rc != INFER_HIP_OK) return rc;
@@ -1265,7 +1308,7 @@ extern "C" int infer_hip_model_kernel_times(infer_hip_model* m, int position, in
       if (st != hipSuccess) rc = hip_fail(st, "kernel_times instantiate");
     }
     if (rc == INFER_HIP_OK) {
-      launch_set_state(m->state, m->last_token, position, 0, m->stream);
+      launch_set_state(m->state, m->last_token, position, 0, rope_cursor(m), m->stream);
       st = hipGraphLaunch(exec, m->stream);  // warm-up
       if (st == hipSuccess) st = hipEventRecord(start, m->stream);
       for (int r = 0; r < reps && st == hipSuccess; ++r) st = hipGraphLaunch(exec, m->stream);

@@ -129,13 +129,6 @@ __global__ __launch_bounds__(kThreads) void add_rms_norm_kernel(uint16_t* __rest
 
 // ------------------------------------------------------- RoPE + KV store --
 
-// Rotate one head (head_dim values, pairs (i, i + half)) by the angles of
-// `position`; `rope` holds (cos, sin) for [position][i].
-__device__ __forceinline__ void rope_pair(float& a, float& b, float2 cs) {
-  const float first = a, second = b;
-  a = first * cs.x - second * cs.y;
-  b = second * cs.x + first * cs.y;
-}
 
 // Prefill: tokens t < count at positions start + t.  q [count][heads][d]
 // and k [count][kv_heads][d] are rotated in place (BF16 rounding, as the
@@ -173,20 +166,24 @@ __global__ __launch_bounds__(kThreads) void rope_store_kernel(
 
 // ------------------------------------------------------ decode attention --
 
-// One decode step's attention, split over the context.  Workgroup (c, h)
-// takes the positions [c span, (c + 1) span) of the context [0, pos] for
-// query head h (kv head g = h / group).  Its kAttnWaves waves take 64-
-// position tiles of the span in turn; in a tile lane p holds position p's
-// key and value rows (16-byte buffer loads whose range ends at the context,
-// so rows past it read as zeros without a branch around the loads), scores
-// it against the rotated q (in LDS), and the tile's value rows go through
-// the wave's LDS slice so that lane d can accumulate output dimension d
-// (and d + 64 when HD = 128).  The softmax runs online across a wave's
-// tiles; the waves are merged in LDS and the workgroup stores the head's
-// (acc[HD], max, sum) partial for its span at
-// partial[(h * max_splits + c) * (HD + 2)].  The o-projection kernel merges
-// the partials of the ceil((pos + 1) / span) spans (attn_o_gemv_kernel).
-// The query heads of a kv head read the same rows; they meet in L2.
+// One decode step's attention over the context [0, pos] of query head h
+// (kv head g = h / group), in one of two forms:
+//  - whole (HD = 64, max_seq <= kAttnWholeMax): one workgroup per query
+//    head over the whole context, writing the head's normalised output
+//    bf16(sum p v / sum p) (attention_decode_whole_kernel below); the
+//    o-projection is then a plain GEMV on it.
+//  - split: workgroup (c, h) takes the positions [c span, (c + 1) span)
+//    with kAttnWaves waves and stores the span's (acc[HD], max, sum)
+//    partial at partial[(h * max_splits + c) * (HD + 2)]; the o-projection
+//    kernel merges the partials of the ceil((pos + 1) / span) spans
+//    (attn_o_gemv_kernel).  This keeps long contexts spread over many CUs.
+// In a tile lane p holds position p's key and value rows (16-byte buffer
+// loads whose range ends at the context, so rows past it read as zeros
+// without a branch around the loads), scores it against the rotated q (in
+// LDS), and the tile's value rows go through the wave's LDS slice so that
+// lane d can accumulate output dimension d (and d + 64 when HD = 128).
+// The softmax runs online across a wave's tiles.  The query heads of a kv
+// head read the same rows; they meet in L2 or the memory-side cache.
 //
 // Latency: a wave's first tile is requested at kernel entry, before the q
 // rotation, and (HD = 64) each next tile before the current one is
@@ -375,6 +372,322 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void attention_decode_kernel(
       rec[HD] = mm;
       rec[HD + 1] = ll;
     }
+  }
+}
+
+// The whole-context form at HD = 64: one workgroup of W waves per query
+// head h, wave w taking the 64-position tiles w, w + W, ... of the context.
+// Pre-rotated (the q|k|v launch rotated q and stored the token's k and v):
+// the tiles cover [0, pos]; otherwise (q and the new k rotated here) the
+// cached positions [0, pos).  8 waves of two tiles each up to
+// kAttnWholeMax positions, both tiles requested at entry.
+//  - Loads are coalesced: instruction j of a wave reads rows 8 j .. 8 j + 7
+//    of its tile, 1 KiB contiguous, lane l taking row 8 j + l / 8 and its
+//    16-byte piece l % 8 (dimensions 8 (l % 8) .. + 7).  (One row per lane
+//    touches 64 cache lines per instruction and re-reads each 8 times,
+//    which overflows the CU's L1 with every wave's rows in flight.)
+//  - Each wave rotates q and the new k itself, lane l from its piece l % 8
+//    and the rotation partner piece of lane l ^ 4: no barrier before the
+//    tile loop.  These small loads are issued before the tile loads, so
+//    waiting for them does not wait for the tiles.
+//  - A row's score is the sum of its 8 lanes' partial dot products, taken
+//    by a reduce-scatter in the 8-lane group (DPP) that leaves lane l with
+//    the score of row 8 (l % 8) + l / 8.  Its softmax weight goes back to
+//    the 8 lanes holding that row's value pieces (ds_swizzle broadcast),
+//    each lane sums weight x value over its 8 rows for its 8 dimensions,
+//    and a reduce-scatter over the 8 row groups (permlane swaps, DPP)
+//    leaves lane l with dimension 8 (l % 8) + l / 8 of the wave's sum.
+//  - The new token (position pos) is not read from the cache: its score
+//    q . k_new and value v_new enter the merge as one more (max, sum, acc)
+//    record.  The waves' records are merged in LDS and the workgroup writes
+//    bf16(sum p v / sum p) to out[h * 64 + d].
+constexpr int kWholeWaves = kAttnWholeMax / kTile / 2;
+
+constexpr int kDppRowRor8 = 0x128;  // row_ror:8, lane i of a row of 16 reads lane i ^ 8
+
+// Lane (l & ~7) | J of the lane's group of 8 (ds_swizzle, bit-mask mode).
+template <int J>
+__device__ __forceinline__ float group8_lane(float v) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x18 | (J << 5)));
+}
+
+// Sum over the lane's group of 8 lanes; every lane of the group gets it.
+__device__ __forceinline__ float group8_sum(float v) {
+  v += dpp_from<kDppRowHalfMirror>(v);
+  v += dpp_from<kDppQuadSwap2>(v);
+  return v + dpp_from<kDppQuadSwap1>(v);
+}
+
+// Reduce-scatter of v[0..8) over the lane's group of 8: returns the group
+// total of v[l % 8].  The first step pairs lane i with 7 - i (half-row
+// mirror); they differ in bit 2, which picks the half each keeps.
+__device__ __forceinline__ float group8_reduce_scatter(float (&v)[8], int lane) {
+  {
+    const bool up = (lane & 4) != 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float send = up ? v[i] : v[i + 4];
+      const float keep = up ? v[i + 4] : v[i];
+      v[i] = keep + dpp_from<kDppRowHalfMirror>(send);
+    }
+  }
+  {
+    const bool up = (lane & 2) != 0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const float send = up ? v[i] : v[i + 2];
+      const float keep = up ? v[i + 2] : v[i];
+      v[i] = keep + dpp_from<kDppQuadSwap2>(send);
+    }
+  }
+  const bool up = (lane & 1) != 0;
+  const float send = up ? v[0] : v[1];
+  const float keep = up ? v[1] : v[0];
+  return keep + dpp_from<kDppQuadSwap1>(send);
+}
+
+// Reduce-scatter of v[0..8) over the 8 lanes l % 8 + 8 g (g = 0..7):
+// returns the total of v[l / 8] over those lanes.
+__device__ __forceinline__ float rows8_reduce_scatter(float (&v)[8], int lane) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = swap32_sum(v[i], v[i + 4]);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) v[i] = swap16_sum(v[i], v[i + 2]);
+  const bool up = (lane & 8) != 0;
+  const float send = up ? v[0] : v[1];
+  const float keep = up ? v[1] : v[0];
+  return keep + dpp_from<kDppRowRor8>(send);
+}
+
+// Sum over 8 dimensions of q * k, both BF16 pairs packed in 32-bit words
+// (v_dot2c_f32_bf16: the products are exact, FP32 accumulation).
+__device__ __forceinline__ float dot8_packed_bf16(const uint32_t (&q)[4], const uint4 k) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  float d = 0.0f;
+  d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, q[0]),
+                                      __builtin_bit_cast(bf16x2, k.x), d, false);
+  d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, q[1]),
+                                      __builtin_bit_cast(bf16x2, k.y), d, false);
+  d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, q[2]),
+                                      __builtin_bit_cast(bf16x2, k.z), d, false);
+  d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, q[3]),
+                                      __builtin_bit_cast(bf16x2, k.w), d, false);
+  return d;
+}
+
+__device__ __forceinline__ void unpack8_bf16(const uint4 w, float (&o)[8]) {
+  o[0] = bf16_lo(w.x); o[1] = bf16_hi(w.x); o[2] = bf16_lo(w.y); o[3] = bf16_hi(w.y);
+  o[4] = bf16_lo(w.z); o[5] = bf16_hi(w.z); o[6] = bf16_lo(w.w); o[7] = bf16_hi(w.w);
+}
+
+// The lane l ^ 4 (ds_swizzle, bit-mask mode): the lane holding the
+// rotation partner piece.
+__device__ __forceinline__ uint32_t partner4(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v), 0x1F | (4 << 10)));
+}
+
+// RoPE of the lane's 8 dimensions from its piece and the partner lane's
+// (piece pc ^ 4), rounded to BF16: out[t] as a value, words[t] as BF16 bits.
+__device__ __forceinline__ void rope_piece(const uint4 mine, const float2* cs, bool second,
+                                           float (&out)[8], uint32_t (&words)[4]) {
+  const uint4 other = make_uint4(partner4(mine.x), partner4(mine.y), partner4(mine.z),
+                                 partner4(mine.w));
+  float a[8], b[8];
+  unpack8_bf16(mine, a);
+  unpack8_bf16(other, b);
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    // first half: a c - b s; second half (partner in the first): a c + b s
+    const float r = second ? a[t] * cs[t].x + b[t] * cs[t].y : a[t] * cs[t].x - b[t] * cs[t].y;
+    const uint16_t w = f32_to_bf16(r);
+    out[t] = bf16_to_f32(w);
+    if (t & 1) {
+      words[t / 2] |= static_cast<uint32_t>(w) << 16;
+    } else {
+      words[t / 2] = w;
+    }
+  }
+}
+
+// Waves of the whole-context workgroup (two tiles each, both in flight).
+// Measured at contexts 256-1023 (pre-rotated, us per launch): 8 waves x 2
+// tiles 4.4-6.4, 16 x 1 4.3-8.3, 4 x 4 5.0-7.7.
+template <bool ROPED>
+constexpr int whole_waves() {
+  return kWholeWaves;
+}
+
+template <bool ROPED>
+__global__ __launch_bounds__(whole_waves<ROPED>() * kWave) void attention_decode_whole_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_new,
+    const uint16_t* __restrict__ v_new, uint16_t* __restrict__ key_cache,
+    uint16_t* __restrict__ value_cache, const float2* __restrict__ rope,
+    const ModelState* __restrict__ state, int heads, int kv_heads, int max_seq,
+    uint16_t* __restrict__ out) {
+  constexpr int HD = 64, W = whole_waves<ROPED>(), half = HD / 2;
+  constexpr int kPieces = HD / 8;            // 16-byte pieces per row (8)
+  constexpr int kRowsPer = kWave / kPieces;  // rows per load instruction (8)
+  constexpr bool kPrefetch = true;           // a second tile per wave
+  static_assert(W * kTile * 2 >= kAttnWholeMax, "tiles cover the context");
+  const int h = blockIdx.x;
+  const int group = heads / kv_heads;
+  const int g = h / group;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int pc = lane % kPieces, rg = lane / kPieces;  // piece, row within instruction
+  const size_t head_base = static_cast<size_t>(g) * max_seq * HD;
+  const uint4* qh = reinterpret_cast<const uint4*>(q + static_cast<size_t>(h) * HD);
+  const uint4 q_mine = qh[pc];
+  uint4 k_mine = make_uint4(0, 0, 0, 0), v_mine = make_uint4(0, 0, 0, 0);
+  float2 cs[8];
+  int pos, rows;  // rows: the cache rows the tiles may read
+  if constexpr (ROPED) {
+    // q is rotated and the new token's k and v are in the caches already:
+    // the tiles cover [0, pos] and go out before pos is known (rows past
+    // the context are masked below).
+    rows = max_seq;
+    pos = 0;
+  } else {
+    // Small loads first: the kv head's new k and v, the angles of pos.
+    k_mine = reinterpret_cast<const uint4*>(k_new + static_cast<size_t>(g) * HD)[pc];
+    v_mine = reinterpret_cast<const uint4*>(v_new + static_cast<size_t>(g) * HD)[pc];
+    pos = min(state->pos, max_seq - 1);
+    const float2* r = rope + static_cast<size_t>(pos) * half + 8 * (pc & 3);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) cs[t] = r[t];
+    rows = pos;  // the new token's row comes from k_new / v_new
+  }
+  __builtin_amdgcn_sched_barrier(0);  // the small loads go out before the tiles
+  const __amdgpu_buffer_rsrc_t kr_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(key_cache + head_base, 0, rows * HD * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vr_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(value_cache + head_base, 0, rows * HD * 2, 0x00020000);
+  auto load_tile = [&](int t0, uint4 (&kr)[kPieces], uint4 (&vr)[kPieces]) {
+#pragma unroll
+    for (int j = 0; j < kPieces; ++j) {
+      const uint32_t off = static_cast<uint32_t>((t0 + kRowsPer * j + rg) * HD * 2 + 16 * pc);
+      kr[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kr_rsrc, off, 0, 0));
+    }
+#pragma unroll
+    for (int j = 0; j < kPieces; ++j) {
+      const uint32_t off = static_cast<uint32_t>((t0 + kRowsPer * j + rg) * HD * 2 + 16 * pc);
+      vr[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr_rsrc, off, 0, 0));
+    }
+  };
+  uint4 kr[kPieces], vr[kPieces], kn[kPieces], vn[kPieces];
+  load_tile(wave * kTile, kr, vr);
+  if (kPrefetch) load_tile((wave + W) * kTile, kn, vn);
+  if constexpr (ROPED) pos = min(state->pos, max_seq - 1);
+  // Positions [0, end) come from the tiles.
+  const int end = ROPED ? pos + 1 : pos;
+
+  const float scale = 1.0f / sqrtf(static_cast<float>(HD));
+  uint32_t qw[4];  // the lane's 8 q dimensions, BF16 pairs
+  float snew = 0.0f;
+  if constexpr (ROPED) {
+    qw[0] = q_mine.x;
+    qw[1] = q_mine.y;
+    qw[2] = q_mine.z;
+    qw[3] = q_mine.w;
+  } else {
+    // q and the new k rotated and rounded to BF16 (as the reference's rope
+    // kernel stores them), each lane its 8 dimensions.
+    const bool second = pc >= kPieces / 2;  // dimensions of the second half
+    float qv[8], kv[8];
+    uint32_t kw[4];
+    rope_piece(q_mine, cs, second, qv, qw);
+    rope_piece(k_mine, cs, second, kv, kw);
+    if (h % group == 0 && wave == 0 && rg == 0) {
+      // The kv head's first query head stores the new token's k and v.
+      const size_t at = head_base + static_cast<size_t>(pos) * HD + 8 * pc;
+      *reinterpret_cast<uint4*>(key_cache + at) = make_uint4(kw[0], kw[1], kw[2], kw[3]);
+      *reinterpret_cast<uint4*>(value_cache + at) = v_mine;
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) snew = fmaf(qv[t], kv[t], snew);
+    snew = group8_sum(snew) * scale;
+  }
+
+  float m = -INFINITY, l = 0.0f;
+  float acc8[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) acc8[t] = 0.0f;
+  // One 64-position tile into the wave's online softmax (wave-uniform: a
+  // tile past the context is skipped whole).
+  auto tile = [&](int t0, const uint4 (&kt)[kPieces], const uint4 (&vt)[kPieces]) {
+    if (t0 >= end) return;
+    float part[kPieces];
+#pragma unroll
+    for (int j = 0; j < kPieces; ++j) part[j] = dot8_packed_bf16(qw, kt[j]);
+    const float score = group8_reduce_scatter(part, lane);  // row 8 pc + rg
+    const bool valid = t0 + kRowsPer * pc + rg < end;
+    const float sc = valid ? score * scale : -INFINITY;
+    const float nm = fmaxf(m, wave_max(sc));
+    const float e = valid ? expf(sc - nm) : 0.0f;
+    const float f = expf(m - nm);  // m = -inf on a wave's first tile: f = 0
+    l = fmaf(l, f, wave_sum(e));
+    m = nm;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc8[t] *= f;
+    // the weight of row 8 j + rg is in lane 8 rg + j
+    float ej[kPieces];
+    ej[0] = group8_lane<0>(e);
+    ej[1] = group8_lane<1>(e);
+    ej[2] = group8_lane<2>(e);
+    ej[3] = group8_lane<3>(e);
+    ej[4] = group8_lane<4>(e);
+    ej[5] = group8_lane<5>(e);
+    ej[6] = group8_lane<6>(e);
+    ej[7] = group8_lane<7>(e);
+#pragma unroll
+    for (int j = 0; j < kPieces; ++j) {
+      // rows past the context hold whatever the cache held: never summed
+      const bool row_ok = t0 + kRowsPer * j + rg < end;
+      float vf[8];
+      unpack8_bf16(vt[j], vf);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) acc8[t] = row_ok ? fmaf(ej[j], vf[t], acc8[t]) : acc8[t];
+      // one row's values unpacked at a time (registers)
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  tile(wave * kTile, kr, vr);
+  if (kPrefetch) tile((wave + W) * kTile, kn, vn);
+  const float mine = rows8_reduce_scatter(acc8, lane);  // dimension 8 pc + rg
+
+  __shared__ float wm[W + 1], wl[W + 1];
+  __shared__ float wacc[W + 1][HD];
+  if (lane == 0) {
+    wm[wave] = m;
+    wl[wave] = l;
+  }
+  wacc[wave][8 * pc + rg] = mine;
+  if (wave == 0 && rg == 0) {
+    // the new token's record (max = its score, sum = 1, acc = its value),
+    // when it did not come from the tiles
+    if constexpr (!ROPED) {
+      float vf[8];
+      unpack8_bf16(v_mine, vf);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) wacc[W][8 * pc + t] = vf[t];
+    }
+    if (pc == 0) {
+      wm[W] = ROPED ? -INFINITY : snew;
+      wl[W] = ROPED ? 0.0f : 1.0f;
+    }
+  }
+  __syncthreads();
+  if (tid < HD) {
+    float mm = wm[W];
+#pragma unroll
+    for (int w = 0; w < W; ++w) mm = fmaxf(mm, wm[w]);
+    float ll = 0.0f, aa = 0.0f;
+#pragma unroll
+    for (int w = 0; w <= W; ++w) {
+      const float f = wl[w] > 0.0f ? expf(wm[w] - mm) : 0.0f;
+      ll = fmaf(wl[w], f, ll);
+      aa = fmaf(wacc[w][tid], f, aa);
+    }
+    out[static_cast<size_t>(h) * HD + tid] = f32_to_bf16(aa / ll);
   }
 }
 
@@ -695,22 +1008,32 @@ __global__ __launch_bounds__(kThreads) void add_kernel(uint16_t* __restrict__ x,
 
 // Host-chosen decode state (a kernel, not a copy, so that it can sit in a
 // captured graph).  token < 0 keeps the current token.
-__global__ void set_state_kernel(ModelState* state, int token, int pos, int step) {
+__global__ void set_state_kernel(ModelState* state, int token, int pos, int step,
+                                 RopeCursor rope) {
   if (threadIdx.x == 0 && blockIdx.x == 0) {
     if (token >= 0) state->token = token;
     state->pos = pos;
     state->step = step;
   }
+  if (rope.row && static_cast<int>(threadIdx.x) < rope.half) {
+    rope.row[threadIdx.x] =
+        rope.table[static_cast<size_t>(min(pos, rope.max_seq - 1)) * rope.half + threadIdx.x];
+  }
 }
-
-// The end of a decode step: record the token the LM head chose and move to
-// the next position.
-__global__ void advance_kernel(ModelState* state, int* __restrict__ history, int history_len) {
+__global__ void advance_kernel(ModelState* state, int* __restrict__ history, int history_len,
+                               RopeCursor rope) {
+  const int pos = state->pos;
+  if (rope.row && static_cast<int>(threadIdx.x) < rope.half) {
+    rope.row[threadIdx.x] =
+        rope.table[static_cast<size_t>(min(pos + 1, rope.max_seq - 1)) * rope.half +
+                   threadIdx.x];
+  }
+  __syncthreads();  // every lane has read pos before thread 0 moves it on
   if (threadIdx.x == 0 && blockIdx.x == 0) {
     const int step = state->step;
     if (step < history_len) history[step] = state->token;
     state->step = step + 1;
-    state->pos = state->pos + 1;
+    state->pos = pos + 1;
   }
 }
 
@@ -752,7 +1075,12 @@ void launch_rope_store(uint16_t* q, uint16_t* k, const uint16_t* v, uint16_t* ke
 
 bool attention_head_dim_supported(int head_dim) { return head_dim == 64 || head_dim == 128; }
 
-int attention_span(int max_seq) {
+bool attention_whole(int max_seq, int head_dim) {
+  return head_dim == 64 && max_seq <= kAttnWholeMax;
+}
+
+int attention_span(int max_seq, int head_dim) {
+  if (attention_whole(max_seq, head_dim)) return kAttnWholeMax;
   // Spans of kAttnWaves 64-position tiles (one tile per wave), widened so
   // that a context has at most kAttnMaxSplits spans.
   const int base = kAttnWaves * kTile;
@@ -761,17 +1089,30 @@ int attention_span(int max_seq) {
   return base * (tiles > 1 ? tiles : 1);
 }
 
-int attention_splits(int max_seq) {
-  const int span = attention_span(max_seq);
+int attention_splits(int max_seq, int head_dim) {
+  const int span = attention_span(max_seq, head_dim);
   return (max_seq + span - 1) / span;
 }
 
 void launch_attention_decode(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
                              uint16_t* key_cache, uint16_t* value_cache, const float2* rope,
                              const ModelState* state, int heads, int kv_heads, int head_dim,
-                             int max_seq, float* partial, hipStream_t stream) {
-  const int span = attention_span(max_seq);
-  const int splits = attention_splits(max_seq);
+                             int max_seq, bool roped, float* partial, uint16_t* out,
+                             hipStream_t stream) {
+  if (attention_whole(max_seq, head_dim)) {
+    if (roped) {
+      hipLaunchKernelGGL(attention_decode_whole_kernel<true>, dim3(heads),
+                         dim3(whole_waves<true>() * kWave), 0, stream, q, k_new, v_new,
+                         key_cache, value_cache, rope, state, heads, kv_heads, max_seq, out);
+    } else {
+      hipLaunchKernelGGL(attention_decode_whole_kernel<false>, dim3(heads),
+                         dim3(whole_waves<false>() * kWave), 0, stream, q, k_new, v_new,
+                         key_cache, value_cache, rope, state, heads, kv_heads, max_seq, out);
+    }
+    return;
+  }
+  const int span = attention_span(max_seq, head_dim);
+  const int splits = attention_splits(max_seq, head_dim);
   const dim3 grid(splits, heads), block(kAttnWaves * kWave);
   if (head_dim == 64) {
     hipLaunchKernelGGL(attention_decode_kernel<64>, grid, block, 0, stream, q, k_new, v_new,
@@ -822,13 +1163,16 @@ void launch_add(uint16_t* x, const uint16_t* y, long long n, hipStream_t stream)
   hipLaunchKernelGGL(add_kernel, dim3(grid_for(n)), dim3(kThreads), 0, stream, x, y, n);
 }
 
-void launch_set_state(ModelState* state, int token, int pos, int step, hipStream_t stream) {
-  hipLaunchKernelGGL(set_state_kernel, dim3(1), dim3(kWave), 0, stream, state, token, pos, step);
+void launch_set_state(ModelState* state, int token, int pos, int step, RopeCursor rope,
+                      hipStream_t stream) {
+  hipLaunchKernelGGL(set_state_kernel, dim3(1), dim3(kWave * 2), 0, stream, state, token, pos,
+                     step, rope);
 }
 
-void launch_advance(ModelState* state, int* history, int history_len, hipStream_t stream) {
-  hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(kWave), 0, stream, state, history,
-                     history_len);
+void launch_advance(ModelState* state, int* history, int history_len, RopeCursor rope,
+                    hipStream_t stream) {
+  hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(kWave * 2), 0, stream, state, history,
+                     history_len, rope);
 }
 
 }  // namespace qlin

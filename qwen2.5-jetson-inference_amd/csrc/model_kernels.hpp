@@ -29,18 +29,29 @@ void launch_rms_norm(const uint16_t* x, const uint16_t* w, uint16_t* out, int ro
 void launch_rope_store(uint16_t* q, uint16_t* k, const uint16_t* v, uint16_t* key_cache,
                        uint16_t* value_cache, const float2* rope, int count, int start,
                        int heads, int kv_heads, int head_dim, int max_seq, hipStream_t stream);
-// Decode attention split over the context (see attention_decode_kernel):
-// one workgroup per (span, query head), spans of attention_span(max_seq)
-// positions, at most attention_splits(max_seq) of them; partial holds
-// heads x attention_splits() x (head_dim + 2) floats.
+// Decode attention (see attention_decode_kernel).  head_dim 64 with up to
+// kAttnWholeMax positions of KV capacity: one workgroup per query head over
+// the whole context, writing the BF16 attention output to out (heads x
+// head_dim); otherwise one workgroup per (span, query head), spans of
+// attention_span() positions, at most kAttnMaxSplits of them, writing
+// partial (heads x attention_splits() x (head_dim + 2) floats) for the
+// o-projection to merge.  In the whole form span = kAttnWholeMax and
+// splits = 1.
 constexpr int kAttnWaves = 2;
 constexpr int kAttnMaxSplits = 8;
-int attention_span(int max_seq);
-int attention_splits(int max_seq);
+constexpr int kAttnWholeMax = 1024;
+bool attention_whole(int max_seq, int head_dim);
+int attention_span(int max_seq, int head_dim);
+int attention_splits(int max_seq, int head_dim);
+// roped (whole form only): q is already rotated and the token's k and v are
+// in the caches at pos (the fused q|k|v launch did both); otherwise q and
+// k_new are rotated here and the first query head of each kv head stores
+// k_new and v_new at pos.
 void launch_attention_decode(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
                              uint16_t* key_cache, uint16_t* value_cache, const float2* rope,
                              const ModelState* state, int heads, int kv_heads, int head_dim,
-                             int max_seq, float* partial, hipStream_t stream);
+                             int max_seq, bool roped, float* partial, uint16_t* out,
+                             hipStream_t stream);
 void launch_attention_prefill(const uint16_t* q, const uint16_t* key_cache,
                               const uint16_t* value_cache, uint16_t* out, int count, int heads,
                               int kv_heads, int head_dim, int max_seq, hipStream_t stream);
@@ -50,7 +61,20 @@ void launch_add(uint16_t* x, const uint16_t* y, long long n, hipStream_t stream)
 // x += y (BF16, in place) and out = rms_norm(x) * w, rows of hidden <= 4096.
 void launch_add_rms_norm(uint16_t* x, const uint16_t* y, const uint16_t* w, uint16_t* out,
                          int rows, int hidden, float eps, hipStream_t stream);
-void launch_set_state(ModelState* state, int token, int pos, int step, hipStream_t stream);
-void launch_advance(ModelState* state, int* history, int history_len, hipStream_t stream);
+// The (cos, sin) row of the decode position, kept beside it: whatever sets
+// or advances ModelState::pos also copies table[pos] (half pairs) into row,
+// so a kernel that rotates at the current position loads a fixed address
+// with its other inputs instead of waiting for pos first.  row == nullptr:
+// no row is kept.
+struct RopeCursor {
+  const float2* table;  // [max_seq][half]
+  float2* row;          // [half]
+  int half;
+  int max_seq;
+};
+void launch_set_state(ModelState* state, int token, int pos, int step, RopeCursor rope,
+                      hipStream_t stream);
+void launch_advance(ModelState* state, int* history, int history_len, RopeCursor rope,
+                    hipStream_t stream);
 
 }  // namespace qlin

@@ -48,8 +48,8 @@ def load():
         "infer_hip_rms_norm_gemv_w8a16": ([p, p, f, i, ctypes.POINTER(NormGemv), i, p], i),
         "infer_hip_rms_norm_gate_up_silu_w8a16": ([p, p, f, i, p, p, p, p, p, i, p], i),
         "infer_hip_gemv_w8a16_rows": ([p, p, p, p, p, i, i, p], i),
-        "infer_hip_attention_decode_span": ([i], i),
-        "infer_hip_attention_decode_splits": ([i], i),
+        "infer_hip_attention_decode_span": ([i, i], i),
+        "infer_hip_attention_decode_splits": ([i, i], i),
         "infer_hip_attention_merge_o_proj": ([p, p, i, i, i, i, i, p, p, p, i, p], i),
         "infer_hip_lm_head_decode_workspace_bytes": ([i], ctypes.c_size_t),
         "infer_hip_rms_norm_lm_head_argmax": ([p, p, f, p, i, i, p, p, p, p], i),
@@ -89,12 +89,12 @@ def gemv_w8a16_rows(weight, scales, bias, input, output, out_features: int,
                                             in_features, _stream(stream)))
 
 
-def attention_decode_span(max_sequence_length: int) -> int:
-    return load().infer_hip_attention_decode_span(max_sequence_length)
+def attention_decode_span(max_sequence_length: int, head_dim: int = 64) -> int:
+    return load().infer_hip_attention_decode_span(max_sequence_length, head_dim)
 
 
-def attention_decode_splits(max_sequence_length: int) -> int:
-    return load().infer_hip_attention_decode_splits(max_sequence_length)
+def attention_decode_splits(max_sequence_length: int, head_dim: int = 64) -> int:
+    return load().infer_hip_attention_decode_splits(max_sequence_length, head_dim)
 
 
 def attention_merge_o_proj(partials, position, num_heads: int, head_dim: int, span: int,

@@ -218,12 +218,12 @@ def test_decode_ops_reject_bad_arguments_on_host(hip):
     assert f(4096, 4096, None, 4098, 4096, 896, 4864, None) == bad
     assert f(4096, 4096, None, None, 4096, 896, 4864, None) == bad
     f = lib.infer_hip_attention_merge_o_proj
-    assert f(4096, 4096, 14, 64, 64, 8, 1024, 4096, 4096, 4096, 896, None) == bad
+    assert f(4096, 4096, 14, 64, 128, 8, 1024, 4096, 4096, 4096, 896, None) == bad
     assert "span" in err()
     assert f(4096, 4096, 14, 32, 128, 8, 1024, 4096, 4096, 4096, 896, None) == bad
-    assert f(4096, 4096, 33, 64, 128, 8, 1024, 4096, 4096, 4096, 896, None) == bad
-    assert f(4096, None, 14, 64, 128, 8, 1024, 4096, 4096, 4096, 896, None) == bad
-    assert f(4096, 4096, 14, 64, 128, 8, 1024, 4104, 4096, 4096, 896, None) == bad
+    assert f(4096, 4096, 33, 64, 256, 8, 2048, 4096, 4096, 4096, 896, None) == bad
+    assert f(4096, None, 14, 64, 256, 8, 2048, 4096, 4096, 4096, 896, None) == bad
+    assert f(4096, 4096, 14, 64, 256, 8, 2048, 4104, 4096, 4096, 896, None) == bad
     f = lib.infer_hip_rms_norm_lm_head_argmax
     assert f(4096, 4096, 1e-6, 4096, 151936, 900, 4096, 4096, 4096, None) == bad
     assert f(4096, 4096, 1e-6, 4096, 0, 896, 4096, 4096, 4096, None) == bad
@@ -234,12 +234,21 @@ def test_decode_ops_reject_bad_arguments_on_host(hip):
 
 
 def test_attention_decode_span_closed_form(hip):
-    # span: 128-position multiples covering max_seq in at most 8 splits
+    # head_dim 64 with up to 1024 positions of capacity: one span of 1024
+    # (the whole-context form); otherwise the smallest multiple of 128 that
+    # covers max_seq in at most 8 splits.
     import decode_hip
-    for max_seq in (1, 7, 128, 129, 1000, 1024, 1025, 4096, 32768):
-        span = decode_hip.attention_decode_span(max_seq)
-        splits = decode_hip.attention_decode_splits(max_seq)
+    for max_seq in (1, 7, 128, 129, 1000, 1024):
+        assert decode_hip.attention_decode_span(max_seq, 64) == 1024
+        assert decode_hip.attention_decode_splits(max_seq, 64) == 1
+    for max_seq, hd in [(m, 64) for m in (1025, 1500, 2048, 2049, 4096, 32768)] + \
+                       [(m, 128) for m in (1, 7, 128, 129, 1000, 1024, 1025, 4096)]:
+        span = decode_hip.attention_decode_span(max_seq, hd)
+        splits = decode_hip.attention_decode_splits(max_seq, hd)
         assert span % 128 == 0 and 1 <= splits <= 8, (max_seq, span, splits)
         assert span * (splits - 1) < max_seq <= span * splits
         assert span == 128 or (span - 128) * 8 < max_seq  # the smallest that fits 8 splits
-    assert decode_hip.attention_decode_span(0) == 0
+    assert decode_hip.attention_decode_span(2048, 64) == 256
+    assert decode_hip.attention_decode_span(1024, 128) == 128
+    assert decode_hip.attention_decode_span(0, 64) == 0
+    assert decode_hip.attention_decode_span(1024, 32) == 0

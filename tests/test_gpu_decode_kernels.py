@@ -239,14 +239,20 @@ def test_gemv_w8a16_rows_bit_exact(dec, dev, k, n, bias):
 
 # --------------------------- split-attention merge + o GEMV + residual --
 
-MERGE_POSITIONS = (0, 1, 127, 128, 255, 256, 511, 512, 600, 767, 768, 895, 896, 1022, 1023,
-                   1500)
+# At max_seq 2048 the split attention has 8 spans of 256 positions: these
+# positions give 1 to 8 splits, their edges, and one past the capacity
+# (clamped to 2047).  At max_seq 1024 the split form has 8 spans of 128 at
+# head_dim 128; at head_dim 64 the decode step uses the whole-context
+# attention there, and the merge entry point normalises a single record.
+MERGE_POSITIONS = {2048: (0, 1, 255, 256, 511, 512, 1023, 1024, 1200, 1535, 1536, 1791, 1792,
+                          2046, 2047, 3000),
+                   1024: (0, 1, 127, 128, 511, 600, 895, 896, 1023, 1500)}
 
 
 def merge_case(heads, hd, max_seq, rng, exact):
     import decode_hip
-    span = decode_hip.attention_decode_span(max_seq)
-    splits = decode_hip.attention_decode_splits(max_seq)
+    span = decode_hip.attention_decode_span(max_seq, hd)
+    splits = decode_hip.attention_decode_splits(max_seq, hd)
     rec = hd + 2
     part = np.full((heads, splits, rec), np.nan, np.float32)  # unused records: NaN
     if exact:
@@ -274,14 +280,14 @@ def merge_expected(part, pos, span, max_seq, hd):
     return a.reshape(-1)
 
 
+@pytest.mark.parametrize("max_seq", [2048, 1024])
 @pytest.mark.parametrize("heads,hd,n,w8", [(14, 64, 896, True), (14, 64, 896, False),
                                            (2, 128, 130, True), (32, 64, 64, True),
                                            (4, 128, 9, False)])
-def test_attention_merge_o_proj_bit_exact(dec, dev, heads, hd, n, w8):
+def test_attention_merge_o_proj_bit_exact(dec, dev, heads, hd, n, w8, max_seq):
     import torch
     rng = rc.philox(400 + heads * hd + n)
     k = heads * hd
-    max_seq = 1024
     if w8:
         wq = w8_rows(rng, n, k)
         s = pow2_scales(n, k, 3)
@@ -294,7 +300,7 @@ def test_attention_merge_o_proj_bit_exact(dec, dev, heads, hd, n, w8):
     part, span, splits = merge_case(heads, hd, max_seq, rng, exact=True)
     dpart = torch.from_numpy(part.reshape(-1)).to(dev)
     x0 = rc.bf16_normal(rng, (n,))
-    for pos in MERGE_POSITIONS:
+    for pos in MERGE_POSITIONS[max_seq]:
         attn = merge_expected(part, pos, span, max_seq, hd)
         assert np.all(rc.bf16_values(bf16(attn)) == attn)  # exact in BF16 by design
         terms = deq * attn[None, :]
@@ -317,7 +323,7 @@ def test_attention_merge_o_proj_softmax_weights(dec, dev, w8):
     # the only coarse step: bound 2^-8 |a| per element through the GEMV).
     import torch
     rng = rc.philox(500 + w8)
-    heads, hd, n, max_seq = 14, 64, 896, 1024
+    heads, hd, n, max_seq = 14, 64, 896, 2048
     k = heads * hd
     if w8:
         q, s = rc.w8a16_synthetic(rng, n, k)
@@ -330,7 +336,7 @@ def test_attention_merge_o_proj_softmax_weights(dec, dev, w8):
     part, span, splits = merge_case(heads, hd, max_seq, rng, exact=False)
     dpart = torch.from_numpy(part.reshape(-1)).to(dev)
     x0 = rc.bf16_normal(rng, (n,))
-    for pos in MERGE_POSITIONS:
+    for pos in MERGE_POSITIONS[max_seq]:
         attn = merge_expected(part, pos, span, max_seq, hd)
         y = deq @ attn + rc.bf16_values(x0)
         bound = np.abs(deq) @ (np.abs(attn) * 2.0 ** -8) + 2.0 ** -8 * np.abs(y) + 1e-6

@@ -361,20 +361,42 @@ def test_config4_workload_teacher_forced(orc, dev):
     o.close()
 
 
-def test_qwen_shaped_decode_across_eight_spans(orc, dev):
-    """14 query / 2 KV heads at max_seq 1024 (spans of 128 positions):
-    teacher-forced decode from position 500 to 1019, so the o-projection
-    merges 4, 5, 6, 7 and 8 spans of every head."""
-    cfg, precision = QWEN_SHAPED, "w8a16"
+@pytest.mark.parametrize("cfg,precision,start,steps",
+                         [(QWEN_SHAPED, "w8a16", 1100, 900), (HD128, "w16a16", 1500, 40)],
+                         ids=["qwen_w8a16", "hd128_w16a16"])
+def test_split_attention_decode_across_eight_spans(orc, dev, cfg, precision, start, steps):
+    """KV capacity 2048 (more than the whole-context form's 1024): the
+    decode attention runs in spans of 256 positions and the o-projection
+    merges them.  Teacher-forced decode from `start` covers 5 to 8 spans of
+    every head (14 query / 2 KV heads; and head_dim 128)."""
     t = S.random_model(cfg, precision, seed=13, std=0.05)
+    fp32 = S.dequantized_fp32(t, cfg)
+    g = model_hip.Qwen2Model(cfg, t, precision, max_sequence_length=2048, use_graph=True)
+    o = oracle_model(orc, cfg, fp32, 2048)
+    p = prompt(start, cfg.vocab_size, seed=14)
+    agree, total, worst = teacher_forced(g, o, p, steps, 0.999, "split spans")
+    print(f"split attention {cfg.hidden_size}/{precision}: agreement {agree}/{total}, "
+          f"worst cosine {worst:.6f}", flush=True)
+    assert agree >= 0.85 * total
+    g.close()
+    o.close()
+
+
+def test_whole_context_attention_qwen_shaped(orc, dev):
+    """KV capacity 1024: one workgroup per query head over the whole
+    context, up to position 1023 (every one of its 16 waves busy), with
+    14 query / 2 KV heads."""
+    cfg, precision = QWEN_SHAPED, "w8a16"
+    t = S.random_model(cfg, precision, seed=17, std=0.05)
     fp32 = S.dequantized_fp32(t, cfg)
     g = model_hip.Qwen2Model(cfg, t, precision, max_sequence_length=1024, use_graph=True)
     o = oracle_model(orc, cfg, fp32, 1024)
-    p = prompt(500, cfg.vocab_size, seed=14)
-    agree, total, worst = teacher_forced(g, o, p, 520, 0.999, "8 spans")
-    print(f"qwen-shaped long context: agreement {agree}/{total}, worst cosine {worst:.6f}",
+    p = prompt(900, cfg.vocab_size, seed=18)
+    agree, total, worst = teacher_forced(g, o, p, 123, 0.999, "whole context")
+    print(f"whole-context attention: agreement {agree}/{total}, worst cosine {worst:.6f}",
           flush=True)
     assert agree >= 0.85 * total
+    assert g.position == 1023
     g.close()
     o.close()
 
