@@ -15,6 +15,12 @@
  *                                      rms_norm_bf16 + gemv_w8a16 (gate, up) +
  *                                      silu_mul_bf16 (cuda_ops.hpp:100-101;
  *                                      qwen2.cpp:643-654)
+ *   infer_hip_rms_norm_qkv_rope_w8a16  rms_norm_bf16 + gemv_w8a16 for q, k, v +
+ *                                      rope_bf16 + store_kv_bf16 (cuda_ops.hpp:
+ *                                      70-79; qwen2.cpp:612-633)
+ *   infer_hip_attention_decode_bf16    attention_decode_bf16 (cuda_ops.hpp:86-91;
+ *                                      qwen2.cpp:633-636) on rotated q and a
+ *                                      cache that holds the token
  *   infer_hip_gemv_w8a16_rows          gemv_w8a16 + add_inplace_bf16 (cuda_ops.hpp:
  *                                      98-99) for down_proj and the residual
  *                                      (qwen2.cpp:655-659)
@@ -81,6 +87,52 @@ int infer_hip_rms_norm_gate_up_silu_w8a16(const uint16_t* input, const uint16_t*
                                           const int8_t* up_weight, const uint16_t* up_scales,
                                           uint16_t* output, int intermediate_size,
                                           hipStream_t stream);
+
+/* The decode step's q|k|v launch (W8A16, group 64): xn as above;
+ * q = bf16(Wq xn + bq), k = bf16(Wk xn + bk), v = bf16(Wv xn + bv); q and k
+ * rotated (pairs (i, i + head_dim / 2) of each head: a c - b s, b c + a s
+ * with (c, s) = rope_row[i], the (cos, sin) of the token's position) and
+ * rounded to BF16; q_out <- rotated q ([num_heads][head_dim]); row p =
+ * min(*position, max_sequence_length - 1) of key_cache / value_cache
+ * ([num_kv_heads][max_sequence_length][head_dim] BF16) <- rotated k, v.
+ * q, k and v weights are [heads x head_dim, in_features] int8 with BF16
+ * scales; biases may be NULL.  in_features <= 4096, head_dim even.  One
+ * launch. */
+typedef struct infer_hip_w8a16_weight {
+  const int8_t* weight;   /* int8 [out_features, in_features] */
+  const uint16_t* scales; /* BF16 [out_features, in_features / 64] */
+  const uint16_t* bias;   /* BF16 [out_features] or NULL */
+} infer_hip_w8a16_weight;
+
+int infer_hip_rms_norm_qkv_rope_w8a16(const uint16_t* input, const uint16_t* norm_weight,
+                                      float epsilon, int in_features,
+                                      const infer_hip_w8a16_weight* q_proj,
+                                      const infer_hip_w8a16_weight* k_proj,
+                                      const infer_hip_w8a16_weight* v_proj, uint16_t* q_out,
+                                      uint16_t* key_cache, uint16_t* value_cache,
+                                      const float* rope_row, const int* position,
+                                      int num_heads, int num_kv_heads, int head_dim,
+                                      int max_sequence_length, hipStream_t stream);
+
+/* (cos, sin) of position * theta^(-2 i / head_dim) for i < head_dim / 2,
+ * in FP32 with the CPU path's arithmetic (src/cpu_ops.cpp:38-41):
+ * out[2 i] = cos, out[2 i + 1] = sin (host memory, head_dim floats).  The
+ * rope_row of infer_hip_rms_norm_qkv_rope_w8a16.  Host only; 0 on success. */
+int infer_hip_rope_row(float theta, int head_dim, int position, float* out);
+
+/* Decode attention of the token at p = min(*position, max_sequence_length
+ * - 1) (device memory): for each query head h (kv head h / (num_heads /
+ * num_kv_heads)) output[h] = bf16(softmax(q[h] K^T / sqrt(head_dim)) V)
+ * over the cache rows [0, p], q already rotated ([num_heads][head_dim]
+ * BF16), the caches already holding row p (as
+ * infer_hip_rms_norm_qkv_rope_w8a16 leaves them).  FP32 softmax and
+ * accumulation.  head_dim 64, max_sequence_length <= 1024: one workgroup
+ * per head over the whole context.  Rows past p are never summed, whatever
+ * they hold. */
+int infer_hip_attention_decode_bf16(const uint16_t* q, const uint16_t* key_cache,
+                                    const uint16_t* value_cache, const int* position,
+                                    uint16_t* output, int num_heads, int num_kv_heads,
+                                    int head_dim, int max_sequence_length, hipStream_t stream);
 
 /* output[n] = bf16(sum_k q[n,k] s[n,k/64] input[k] + bias[n]) with one
  * wave per output row and the whole row in flight at once.  bias may be

@@ -185,3 +185,79 @@ extern "C" int infer_hip_rms_norm_lm_head_argmax(const uint16_t* input,
                         stream);
   return check_launch(what);
 }
+
+extern "C" int infer_hip_rms_norm_qkv_rope_w8a16(
+    const uint16_t* input, const uint16_t* norm_weight, float epsilon, int in_features,
+    const infer_hip_w8a16_weight* q_proj, const infer_hip_w8a16_weight* k_proj,
+    const infer_hip_w8a16_weight* v_proj, uint16_t* q_out, uint16_t* key_cache,
+    uint16_t* value_cache, const float* rope_row, const int* position, int num_heads,
+    int num_kv_heads, int head_dim, int max_sequence_length, hipStream_t stream) {
+  const char* what = "rms_norm_qkv_rope_w8a16";
+  int rc = check_norm_input(input, norm_weight, in_features, what);
+  if (rc != INFER_HIP_OK) return rc;
+  if (!q_proj || !k_proj || !v_proj || !q_out || !key_cache || !value_cache || !rope_row ||
+      !position) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: null pointer", what);
+  }
+  if (num_heads < 1 || num_kv_heads < 1 || num_heads % num_kv_heads != 0 || head_dim < 2 ||
+      head_dim % 2 != 0 || max_sequence_length < 1 ||
+      !norm_qkv_rope_supported(in_features, head_dim)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "%s: bad shape (heads %d, kv heads %d, head_dim %d, max_seq %d, in %d)", what,
+                num_heads, num_kv_heads, head_dim, max_sequence_length, in_features);
+  }
+  const int nq = num_heads * head_dim, nkv = num_kv_heads * head_dim;
+  rc = check_w8(q_proj->weight, q_proj->scales, q_out, nq, what);
+  if (rc == INFER_HIP_OK) rc = check_w8(k_proj->weight, k_proj->scales, key_cache, nkv, what);
+  if (rc == INFER_HIP_OK) rc = check_w8(v_proj->weight, v_proj->scales, value_cache, nkv, what);
+  if (rc != INFER_HIP_OK) return rc;
+  const QkvRopeArgs a{input, norm_weight, epsilon, in_features,
+                      q_proj->weight, q_proj->scales, q_proj->bias,
+                      k_proj->weight, k_proj->scales, k_proj->bias,
+                      v_proj->weight, v_proj->scales, v_proj->bias,
+                      q_out, key_cache, value_cache, reinterpret_cast<const float2*>(rope_row),
+                      position, num_heads, num_kv_heads, head_dim, max_sequence_length};
+  launch_norm_qkv_rope_w8(a, stream);
+  return check_launch(what);
+}
+
+extern "C" int infer_hip_rope_row(float theta, int head_dim, int position, float* out) {
+  if (!out || head_dim < 2 || head_dim % 2 != 0 || position < 0) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "rope_row: bad arguments (head_dim %d, position %d)",
+                head_dim, position);
+  }
+  for (int i = 0; i < head_dim / 2; ++i) {
+    const float2 cs = rope_angle(theta, head_dim, position, i);
+    out[2 * i] = cs.x;
+    out[2 * i + 1] = cs.y;
+  }
+  return ok();
+}
+
+extern "C" int infer_hip_attention_decode_bf16(const uint16_t* q, const uint16_t* key_cache,
+                                               const uint16_t* value_cache, const int* position,
+                                               uint16_t* output, int num_heads, int num_kv_heads,
+                                               int head_dim, int max_sequence_length,
+                                               hipStream_t stream) {
+  const char* what = "attention_decode_bf16";
+  if (!q || !key_cache || !value_cache || !position || !output) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: null pointer", what);
+  }
+  if (num_heads < 1 || num_kv_heads < 1 || num_heads % num_kv_heads != 0) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: %d heads, %d kv heads", what, num_heads,
+                num_kv_heads);
+  }
+  if (max_sequence_length < 1 || !attention_whole(max_sequence_length, head_dim)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "%s: head_dim %d, max_sequence_length %d (head_dim 64, at most %d)", what,
+                head_dim, max_sequence_length, kAttnWholeMax);
+  }
+  if (!aligned16(q) || !aligned16(key_cache) || !aligned16(value_cache)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: q and caches must be 16-byte aligned", what);
+  }
+  launch_attention_decode(q, nullptr, nullptr, const_cast<uint16_t*>(key_cache),
+                          const_cast<uint16_t*>(value_cache), nullptr, position, num_heads,
+                          num_kv_heads, head_dim, max_sequence_length, true, nullptr, output,
+                          stream);
+  return check_launch(what);
+}

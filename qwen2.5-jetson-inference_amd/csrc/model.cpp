@@ -146,6 +146,16 @@ struct infer_hip_model {
   int last_token = -1;
 };
 
+namespace qlin {
+
+float2 rope_angle(float theta, int head_dim, int position, int i) {
+  const float frequency = std::pow(theta, -2.0f * static_cast<float>(i) / head_dim);
+  const float angle = static_cast<float>(position) * frequency;
+  return make_float2(std::cos(angle), std::sin(angle));
+}
+
+}  // namespace qlin
+
 namespace {
 
 int hip_fail(hipError_t st, const char* what) {
@@ -345,7 +355,8 @@ int enqueue_decode_step(infer_hip_model* m, int only = -1, hipEvent_t* events = 
       }
     }
     run(kKindAttention, [&] {
-      launch_attention_decode(m->q, m->k, m->v, L.key_cache, L.value_cache, m->rope, m->state,
+      launch_attention_decode(m->q, m->k, m->v, L.key_cache, L.value_cache, m->rope,
+                              &m->state->pos,
                               c.num_heads, c.num_kv_heads, m->head_dim, m->max_seq,
                               m->fused_qkv_rope, m->attn_partial, m->attn, s);
     });
@@ -768,9 +779,7 @@ extern "C" int infer_hip_model_create(const infer_hip_model_config* config,
   std::vector<float2> rope(ms * half);
   for (int p = 0; p < max_seq; ++p) {
     for (int i = 0; i < half; ++i) {
-      const float frequency = std::pow(c.rope_theta, -2.0f * static_cast<float>(i) / head_dim);
-      const float angle = static_cast<float>(p) * frequency;
-      rope[static_cast<size_t>(p) * half + i] = make_float2(std::cos(angle), std::sin(angle));
+      rope[static_cast<size_t>(p) * half + i] = rope_angle(c.rope_theta, head_dim, p, i);
     }
   }
   st = hipMemcpy(m->rope, rope.data(), sizeof(float2) * rope.size(), hipMemcpyHostToDevice);

@@ -217,7 +217,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void attention_decode_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_new,
     const uint16_t* __restrict__ v_new, uint16_t* __restrict__ key_cache,
     uint16_t* __restrict__ value_cache, const float2* __restrict__ rope,
-    const ModelState* __restrict__ state, int heads, int kv_heads, int max_seq, int span,
+    const int* __restrict__ pos_ptr, int heads, int kv_heads, int max_seq, int span,
     int max_splits, float* __restrict__ partial) {
   constexpr int W = kAttnWaves;
   constexpr int half = HD / 2;
@@ -227,7 +227,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void attention_decode_kernel(
   constexpr bool kPrefetch = HD <= 64;  // register budget
   const int c = blockIdx.x;
   const int h = blockIdx.y;
-  const int pos = min(state->pos, max_seq - 1);
+  const int pos = min(*pos_ptr, max_seq - 1);
   const int seq = pos + 1;
   const int begin = c * span;
   if (begin >= seq) return;  // the grid covers max_seq; spans past the context exit
@@ -522,7 +522,7 @@ __global__ __launch_bounds__(whole_waves<ROPED>() * kWave) void attention_decode
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_new,
     const uint16_t* __restrict__ v_new, uint16_t* __restrict__ key_cache,
     uint16_t* __restrict__ value_cache, const float2* __restrict__ rope,
-    const ModelState* __restrict__ state, int heads, int kv_heads, int max_seq,
+    const int* __restrict__ pos_ptr, int heads, int kv_heads, int max_seq,
     uint16_t* __restrict__ out) {
   constexpr int HD = 64, W = whole_waves<ROPED>(), half = HD / 2;
   constexpr int kPieces = HD / 8;            // 16-byte pieces per row (8)
@@ -550,7 +550,7 @@ __global__ __launch_bounds__(whole_waves<ROPED>() * kWave) void attention_decode
     // Small loads first: the kv head's new k and v, the angles of pos.
     k_mine = reinterpret_cast<const uint4*>(k_new + static_cast<size_t>(g) * HD)[pc];
     v_mine = reinterpret_cast<const uint4*>(v_new + static_cast<size_t>(g) * HD)[pc];
-    pos = min(state->pos, max_seq - 1);
+    pos = min(*pos_ptr, max_seq - 1);
     const float2* r = rope + static_cast<size_t>(pos) * half + 8 * (pc & 3);
 #pragma unroll
     for (int t = 0; t < 8; ++t) cs[t] = r[t];
@@ -576,7 +576,7 @@ __global__ __launch_bounds__(whole_waves<ROPED>() * kWave) void attention_decode
   uint4 kr[kPieces], vr[kPieces], kn[kPieces], vn[kPieces];
   load_tile(wave * kTile, kr, vr);
   if (kPrefetch) load_tile((wave + W) * kTile, kn, vn);
-  if constexpr (ROPED) pos = min(state->pos, max_seq - 1);
+  if constexpr (ROPED) pos = min(*pos_ptr, max_seq - 1);
   // Positions [0, end) come from the tiles.
   const int end = ROPED ? pos + 1 : pos;
 
@@ -1096,18 +1096,18 @@ int attention_splits(int max_seq, int head_dim) {
 
 void launch_attention_decode(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
                              uint16_t* key_cache, uint16_t* value_cache, const float2* rope,
-                             const ModelState* state, int heads, int kv_heads, int head_dim,
+                             const int* pos, int heads, int kv_heads, int head_dim,
                              int max_seq, bool roped, float* partial, uint16_t* out,
                              hipStream_t stream) {
   if (attention_whole(max_seq, head_dim)) {
     if (roped) {
       hipLaunchKernelGGL(attention_decode_whole_kernel<true>, dim3(heads),
                          dim3(whole_waves<true>() * kWave), 0, stream, q, k_new, v_new,
-                         key_cache, value_cache, rope, state, heads, kv_heads, max_seq, out);
+                         key_cache, value_cache, rope, pos, heads, kv_heads, max_seq, out);
     } else {
       hipLaunchKernelGGL(attention_decode_whole_kernel<false>, dim3(heads),
                          dim3(whole_waves<false>() * kWave), 0, stream, q, k_new, v_new,
-                         key_cache, value_cache, rope, state, heads, kv_heads, max_seq, out);
+                         key_cache, value_cache, rope, pos, heads, kv_heads, max_seq, out);
     }
     return;
   }
@@ -1116,11 +1116,11 @@ void launch_attention_decode(const uint16_t* q, const uint16_t* k_new, const uin
   const dim3 grid(splits, heads), block(kAttnWaves * kWave);
   if (head_dim == 64) {
     hipLaunchKernelGGL(attention_decode_kernel<64>, grid, block, 0, stream, q, k_new, v_new,
-                       key_cache, value_cache, rope, state, heads, kv_heads, max_seq, span,
+                       key_cache, value_cache, rope, pos, heads, kv_heads, max_seq, span,
                        splits, partial);
   } else {
     hipLaunchKernelGGL(attention_decode_kernel<128>, grid, block, 0, stream, q, k_new, v_new,
-                       key_cache, value_cache, rope, state, heads, kv_heads, max_seq, span,
+                       key_cache, value_cache, rope, pos, heads, kv_heads, max_seq, span,
                        splits, partial);
   }
 }

@@ -22,6 +22,10 @@ struct ModelState {
 // Head dimensions the attention kernels are built for.
 bool attention_head_dim_supported(int head_dim);
 
+// (cos, sin) of position * theta^(-2 i / head_dim), FP32 with the CPU
+// path's arithmetic (src/cpu_ops.cpp:38-41); host code.
+float2 rope_angle(float theta, int head_dim, int position, int i);
+
 void launch_embedding(const uint16_t* table, const int* tokens, int count, int vocab, int hidden,
                       uint16_t* out, hipStream_t stream);
 void launch_rms_norm(const uint16_t* x, const uint16_t* w, uint16_t* out, int rows, int hidden,
@@ -47,9 +51,10 @@ int attention_splits(int max_seq, int head_dim);
 // in the caches at pos (the fused q|k|v launch did both); otherwise q and
 // k_new are rotated here and the first query head of each kv head stores
 // k_new and v_new at pos.
+// pos: the token's position (device memory).
 void launch_attention_decode(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
                              uint16_t* key_cache, uint16_t* value_cache, const float2* rope,
-                             const ModelState* state, int heads, int kv_heads, int head_dim,
+                             const int* pos, int heads, int kv_heads, int head_dim,
                              int max_seq, bool roped, float* partial, uint16_t* out,
                              hipStream_t stream);
 void launch_attention_prefill(const uint16_t* q, const uint16_t* key_cache,

@@ -19,6 +19,9 @@ from linear_hip import _check, _ptr, _stream
 EXPORTED_SYMBOLS = (
     "infer_hip_rms_norm_gemv_w8a16",
     "infer_hip_rms_norm_gate_up_silu_w8a16",
+    "infer_hip_rms_norm_qkv_rope_w8a16",
+    "infer_hip_rope_row",
+    "infer_hip_attention_decode_bf16",
     "infer_hip_gemv_w8a16_rows",
     "infer_hip_attention_decode_span",
     "infer_hip_attention_decode_splits",
@@ -26,6 +29,12 @@ EXPORTED_SYMBOLS = (
     "infer_hip_lm_head_decode_workspace_bytes",
     "infer_hip_rms_norm_lm_head_argmax",
 )
+
+
+class W8A16Weight(ctypes.Structure):
+    """infer_hip_w8a16_weight."""
+    _fields_ = [("weight", ctypes.c_void_p), ("scales", ctypes.c_void_p),
+                ("bias", ctypes.c_void_p)]
 
 
 class NormGemv(ctypes.Structure):
@@ -47,6 +56,12 @@ def load():
     sigs = {
         "infer_hip_rms_norm_gemv_w8a16": ([p, p, f, i, ctypes.POINTER(NormGemv), i, p], i),
         "infer_hip_rms_norm_gate_up_silu_w8a16": ([p, p, f, i, p, p, p, p, p, i, p], i),
+        "infer_hip_rms_norm_qkv_rope_w8a16": ([p, p, f, i, ctypes.POINTER(W8A16Weight),
+                                               ctypes.POINTER(W8A16Weight),
+                                               ctypes.POINTER(W8A16Weight), p, p, p, p, p,
+                                               i, i, i, i, p], i),
+        "infer_hip_rope_row": ([f, i, i, ctypes.POINTER(ctypes.c_float)], i),
+        "infer_hip_attention_decode_bf16": ([p, p, p, p, p, i, i, i, i, p], i),
         "infer_hip_gemv_w8a16_rows": ([p, p, p, p, p, i, i, p], i),
         "infer_hip_attention_decode_span": ([i, i], i),
         "infer_hip_attention_decode_splits": ([i, i], i),
@@ -80,6 +95,36 @@ def rms_norm_gate_up_silu_w8a16(input, norm_weight, epsilon: float, in_features:
         _ptr(input), _ptr(norm_weight), epsilon, in_features, _ptr(gate_weight),
         _ptr(gate_scales), _ptr(up_weight), _ptr(up_scales), _ptr(output),
         intermediate_size, _stream(stream)))
+
+
+def rms_norm_qkv_rope_w8a16(input, norm_weight, epsilon: float, in_features: int, q_proj,
+                            k_proj, v_proj, q_out, key_cache, value_cache, rope_row, position,
+                            num_heads: int, num_kv_heads: int, head_dim: int,
+                            max_sequence_length: int, stream=None) -> None:
+    """q_proj / k_proj / v_proj: (weight, scales, bias) each."""
+    ws = [W8A16Weight(_ptr(w), _ptr(s), _ptr(b)) for (w, s, b) in (q_proj, k_proj, v_proj)]
+    _check(load().infer_hip_rms_norm_qkv_rope_w8a16(
+        _ptr(input), _ptr(norm_weight), epsilon, in_features, ctypes.byref(ws[0]),
+        ctypes.byref(ws[1]), ctypes.byref(ws[2]), _ptr(q_out), _ptr(key_cache),
+        _ptr(value_cache), _ptr(rope_row), _ptr(position), num_heads, num_kv_heads, head_dim,
+        max_sequence_length, _stream(stream)))
+
+
+def rope_row(theta: float, head_dim: int, position: int):
+    """(cos, sin) pairs of one position as a float32 array [head_dim / 2, 2]."""
+    import numpy as np
+    out = np.empty(head_dim, np.float32)
+    _check(load().infer_hip_rope_row(theta, head_dim, position,
+                                     out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
+    return out.reshape(-1, 2)
+
+
+def attention_decode_bf16(q, key_cache, value_cache, position, output, num_heads: int,
+                          num_kv_heads: int, head_dim: int, max_sequence_length: int,
+                          stream=None) -> None:
+    _check(load().infer_hip_attention_decode_bf16(
+        _ptr(q), _ptr(key_cache), _ptr(value_cache), _ptr(position), _ptr(output), num_heads,
+        num_kv_heads, head_dim, max_sequence_length, _stream(stream)))
 
 
 def gemv_w8a16_rows(weight, scales, bias, input, output, out_features: int,

@@ -252,3 +252,50 @@ def test_attention_decode_span_closed_form(hip):
     assert decode_hip.attention_decode_span(1024, 128) == 128
     assert decode_hip.attention_decode_span(0, 64) == 0
     assert decode_hip.attention_decode_span(1024, 32) == 0
+
+
+@pytest.mark.parametrize("theta,head_dim", [(1e6, 64), (1e4, 128), (1e6, 2)])
+def test_rope_row_equals_the_oracle_rotation(hip, orc, theta, head_dim):
+    # Rotating the unit vector e_i (dims i and i + half = 1, 0) by the
+    # oracle's rope (cpu_ops.cpp:33-56 restated) yields exactly (cos, sin)
+    # of pair i: the library's row must equal it bit for bit.
+    import numpy as np
+    import decode_hip
+    half = head_dim // 2
+    for position in (0, 1, 7, 100, 1023, 32767):
+        row = decode_hip.rope_row(theta, head_dim, position)
+        q = np.zeros((half, head_dim), np.float32)
+        q[np.arange(half), np.arange(half)] = 1.0
+        rq, _ = orc.rope(q.reshape(-1), np.zeros(head_dim, np.float32), half, 1, head_dim,
+                         position, theta)
+        rq = rq.reshape(half, head_dim)
+        np.testing.assert_array_equal(row[:, 0], rq[np.arange(half), np.arange(half)])
+        np.testing.assert_array_equal(row[:, 1], rq[np.arange(half), np.arange(half) + half])
+        if position == 0:
+            assert np.all(row[:, 0] == 1.0) and np.all(row[:, 1] == 0.0)
+
+
+def test_rope_row_and_new_decode_ops_reject_bad_arguments(hip):
+    import ctypes
+    import decode_hip
+    lib = decode_hip.load()
+    bad = hip.INVALID_ARGUMENT
+    buf = (ctypes.c_float * 64)()
+    assert lib.infer_hip_rope_row(1e6, 63, 0, buf) == bad
+    assert lib.infer_hip_rope_row(1e6, 64, -1, buf) == bad
+    assert lib.infer_hip_rope_row(1e6, 64, 0, None) == bad
+    f = lib.infer_hip_attention_decode_bf16
+    assert f(4096, 4096, 4096, 4096, 4096, 14, 2, 64, 2048, None) == bad  # split form only
+    assert "1024" in lib.infer_hip_last_error().decode()
+    assert f(4096, 4096, 4096, 4096, 4096, 14, 2, 128, 512, None) == bad
+    assert f(4096, 4096, 4096, 4096, 4096, 14, 3, 64, 512, None) == bad
+    assert f(4104, 4096, 4096, 4096, 4096, 14, 2, 64, 512, None) == bad
+    assert f(4096, 4096, None, 4096, 4096, 14, 2, 64, 512, None) == bad
+    w = decode_hip.W8A16Weight(4096, 4096, None)
+    g = lib.infer_hip_rms_norm_qkv_rope_w8a16
+    args = [4096, 4096, 1e-6, 896, ctypes.byref(w), ctypes.byref(w), ctypes.byref(w), 4096, 4096,
+            4096, 4096, 4096, 14, 2, 64, 1024, None]
+    for i, v in ((3, 900), (12, 0), (13, 3), (14, 63), (15, 0), (11, None), (4, None)):
+        a = list(args)
+        a[i] = v
+        assert g(*a) == bad, (i, v)

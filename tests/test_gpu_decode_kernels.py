@@ -443,3 +443,107 @@ def test_lm_head_decode_tie_cases(dec, dev, case):
                                     k, logits, ws, am)
         assert int(am.cpu().item()) == ta
         np.testing.assert_array_equal(words(logits), bf16(l64))
+
+
+# ------------------------------------- RMSNorm + q|k|v + RoPE + KV store --
+
+def rope_candidates(a_words, b_words, cs):
+    """BF16 words the rotated pair may round to: (a c - b s, b c + a s) with
+    FP32 products rounded separately, or with either product fused into
+    the add (FMA contraction), or exactly."""
+    a = rc.bf16_values(a_words).astype(np.float64)
+    b = rc.bf16_values(b_words).astype(np.float64)
+    c, s = cs[:, 0].astype(np.float64), cs[:, 1].astype(np.float64)
+    f32 = lambda v: np.asarray(v, np.float64).astype(np.float32)  # noqa: E731
+    r32 = lambda v: f32(v).astype(np.float64)  # one FP32 rounding  # noqa: E731
+
+    def forms(x, y, sign):  # x c + sign * y s
+        return [rc.bf16_words(f32(r32(x * c) + sign * r32(y * s))),
+                rc.bf16_words(f32(x * c + sign * r32(y * s))),
+                rc.bf16_words(f32(r32(x * c) + sign * y * s)),
+                rc.bf16_words(f32(x * c + sign * y * s))]
+    return forms(a, b, -1.0), forms(b, a, 1.0)
+
+
+QKV_ROPE_SHAPES = [  # (in_features, heads, kv_heads, head_dim, max_seq)
+    (896, 14, 2, 64, 1024),     # Qwen2.5-0.5B
+    (1024, 4, 1, 128, 64),      # head_dim 128, GQA 4
+    (512, 8, 8, 64, 16),        # no grouping
+]
+
+
+@pytest.mark.parametrize("shape", QKV_ROPE_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_rms_norm_qkv_rope(dec, dev, shape):
+    import torch
+    k, heads, kvh, hd, max_seq = shape
+    half = hd // 2
+    rng = rc.philox(700 + k + heads)
+    nq, nkv = heads * hd, kvh * hd
+    w = {n: w8_rows(rng, m, k) for n, m in (("q", nq), ("k", nkv), ("v", nkv))}
+    s = {n: pow2_scales(w[n].shape[0], k, salt=i) for i, n in enumerate("qkv")}
+    b = {n: dyadic_bias(rng, w[n].shape[0]) for n in "qkv"}
+    b["v"] = None  # a null bias too
+    dw = {n: (to_dev(w[n], dev), to_dev(s[n], dev), to_dev(b[n], dev) if b[n] is not None
+              else None) for n in "qkv"}
+    sentinel = np.uint16(0x7FC0)  # NaN: every row but the token's must keep it
+    for position in (0, 5, max_seq - 1, max_seq + 100):
+        p = min(position, max_seq - 1)
+        xw, nw, xn = norm_input(k, position % 16, rng)
+        y = {n: bf16(exact_gemv(w[n], s[n], xn, b[n])) for n in "qkv"}  # before the rotation
+        cs = dec.rope_row(1e6, hd, p)
+        kc = torch.full((kvh * max_seq * hd,), -1, dtype=torch.int16, device=dev)
+        kc.fill_(int(sentinel.view(np.int16)))
+        vc = kc.clone()
+        q_out = bf16_out((nq,), dev)
+        dpos = torch.tensor([position], dtype=torch.int32, device=dev)
+        dec.rms_norm_qkv_rope_w8a16(to_dev(xw, dev), to_dev(nw, dev), EPS, k, dw["q"], dw["k"],
+                                    dw["v"], q_out, kc, vc, torch.from_numpy(cs.copy()).to(dev),
+                                    dpos, heads, kvh, hd, max_seq)
+        kcache = kc.cpu().numpy().view(np.uint16).reshape(kvh, max_seq, hd)
+        vcache = vc.cpu().numpy().view(np.uint16).reshape(kvh, max_seq, hd)
+        other = np.ones(max_seq, bool)
+        other[p] = False
+        assert np.all(kcache[:, other] == sentinel) and np.all(vcache[:, other] == sentinel)
+        np.testing.assert_array_equal(vcache[:, p].reshape(-1), y["v"])  # v: not rotated
+        for name, got in (("q", words(q_out).reshape(-1, hd)), ("k", kcache[:, p])):
+            yy = y[name].reshape(-1, hd)
+            if p == 0:  # cos 1, sin 0: the rotation is exact
+                np.testing.assert_array_equal(got, yy)
+                continue
+            first, second = rope_candidates(yy[:, :half], yy[:, half:], cs)
+            ok1 = np.any([got[:, :half] == c for c in first], axis=0)
+            ok2 = np.any([got[:, half:] == c for c in second], axis=0)
+            assert ok1.all() and ok2.all(), (name, position, np.argwhere(~ok1)[:3],
+                                             np.argwhere(~ok2)[:3])
+
+
+# ------------------------------------------- whole-context decode attention --
+
+@pytest.mark.parametrize("heads,kvh", [(14, 2), (4, 4), (8, 1)])
+def test_attention_decode_bf16_matches_oracle(dec, orc, dev, heads, kvh):
+    """Against the oracle's attention (cpu_ops.cpp:58-91 restated) on the
+    same BF16 values: q rotated already, the caches holding rows [0, p];
+    rows past p hold NaN and must not matter."""
+    import torch
+    hd, max_seq = 64, 1024
+    rng = rc.philox(800 + heads)
+    q = rc.bf16_normal(rng, (heads * hd,), 0.5)
+    kcache = rc.bf16_normal(rng, (kvh, max_seq, hd))
+    vcache = rc.bf16_normal(rng, (kvh, max_seq, hd))
+    for position in (0, 1, 63, 64, 127, 511, 512, 767, 1022, 1023, 2000):
+        p = min(position, max_seq - 1)
+        kc, vc = kcache.copy(), vcache.copy()
+        kc[:, p + 1:] = 0x7FC0
+        vc[:, p + 1:] = 0x7FC0
+        exp = orc.attention_decode(rc.bf16_values(q), rc.bf16_values(kcache),
+                                   rc.bf16_values(vcache), heads, kvh, hd, p + 1, max_seq)
+        out = bf16_out((heads * hd,), dev)
+        dpos = torch.tensor([position], dtype=torch.int32, device=dev)
+        dec.attention_decode_bf16(to_dev(q, dev), to_dev(kc, dev), to_dev(vc, dev), dpos, out,
+                                  heads, kvh, hd, max_seq)
+        got = rc.bf16_values(words(out)).astype(np.float64)
+        e = np.asarray(exp, dtype=np.float64)
+        # BF16 output rounding plus FP32 softmax / accumulation error
+        tol = 2.0 ** -8 * np.abs(e) + 1e-4 * np.max(np.abs(e))
+        assert np.all(np.isfinite(got)), position
+        assert np.all(np.abs(got - e) <= tol), (position, float(np.max(np.abs(got - e) / tol)))
