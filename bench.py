@@ -77,6 +77,9 @@ def parse():
                     help="e2e: config 4 decode (the headline); gemv: config 1; "
                          "prefill: config 3 GEMMs")
     ap.add_argument("--prompt", type=int, default=512, help="e2e prompt length")
+    ap.add_argument("--decode-tokens", type=int, default=0,
+                    help="e2e: decode steps per bench step (default: to context 1023, the "
+                         "whole of config 4's decode; fewer for counter runs)")
     ap.add_argument("--graph", choices=("on", "off"), default="on",
                     help="e2e: replay each decode step from a HIP graph (on) or launch its "
                          "kernels one by one (off; no per-kernel timing, for counter runs)")
@@ -599,6 +602,8 @@ def e2e_main(args, dev):
     max_seq = 1024
     prompt_len = args.prompt
     decode_len = max_seq - 1 - prompt_len   # config 4: 512 generated = 1 + 511 decode steps
+    if args.decode_tokens > 0:
+        decode_len = min(decode_len, args.decode_tokens)
     if decode_len < 1:
         print(f"bench.py: prompt {prompt_len} leaves no decode step at max_seq {max_seq}",
               file=sys.stderr)

@@ -134,9 +134,79 @@ def export(tensors: dict, precision: str, group_size: int = 64, source: str = ""
     return head + b"\0" * (DATA_OFFSET - len(head)) + bytes(payload)
 
 
+MAX_DEPTH = 64   # deepest value of the metadata JSON (the top level is 0)
+MAX_DIMS = 8     # infer_hip_tensor_record's shape capacity (infer_archive.h)
+_I64 = (-2 ** 63, 2 ** 63 - 1)
+_I32 = (-2 ** 31, 2 ** 31 - 1)
+
+
+class _Pairs(list):
+    """An object's (key, value) pairs in file order, before duplicates fold."""
+
+
+def _reject_constant(name):
+    raise ValueError("bad number: " + name)
+
+
+def parse_json(raw: bytes):
+    """JSON text as strictly as nlohmann::json::parse reads it (the
+    reference's metadata and config.json parser): RFC 8259 numbers and
+    literals only (no NaN or Infinity), UTF-8 checked, \\u escapes only as
+    characters or whole surrogate pairs; a repeated key keeps its last value.
+    The C++ parser also bounds the nesting at MAX_DEPTH.  Raises ValueError."""
+    try:
+        tree = json.loads(raw.decode("utf-8"), parse_constant=_reject_constant,
+                          object_pairs_hook=_Pairs)
+    except (UnicodeDecodeError, ValueError, RecursionError) as e:
+        raise ValueError(str(e)) from None
+
+    def fold(v, depth):
+        if depth > MAX_DEPTH:
+            raise ValueError("metadata nested too deeply")
+        if isinstance(v, str):
+            try:
+                v.encode("utf-8")
+            except UnicodeEncodeError:
+                raise ValueError("bad surrogate pair") from None
+            return v
+        if isinstance(v, _Pairs):
+            out = {}
+            for k, x in v:
+                fold(k, depth + 1)
+                out[k] = fold(x, depth + 1)
+            return out
+        if isinstance(v, list):
+            return [fold(x, depth + 1) for x in v]
+        return v
+
+    return fold(tree, 0)
+
+
+def parse_metadata(raw: bytes):
+    """parse_json for the archive metadata: raises ValueError("archive
+    metadata: ...")."""
+    try:
+        return parse_json(raw)
+    except ValueError as e:
+        raise ValueError("archive metadata: " + str(e)) from None
+
+
+def _integer(v, bounds):
+    """A JSON integer token within bounds (bool and float tokens are not)."""
+    return isinstance(v, int) and not isinstance(v, bool) and bounds[0] <= v <= bounds[1]
+
+
 def read(blob: bytes) -> dict:
     """ModelArchive::open (src/archive.cpp:49-102) over bytes: name ->
-    (record, numpy payload); raises ValueError with the reference's message."""
+    (record, numpy payload); raises ValueError with the reference's message.
+
+    Field checks run in the reference's order: name, shape, dtype, offset
+    and nbytes, the size and bounds checks, the quant record, duplicates.
+    A missing key or a value of the wrong JSON type raises there (nlohmann's
+    at() and get<T>()); it raises "archive metadata: ..." here.  Where the
+    reference's conversions would truncate a fractional size or wrap a
+    negative one, both readers here reject the value, and shape products are
+    exact (no 64-bit wrap)."""
     if len(blob) == 0:
         raise ValueError("cannot mmap archive")
     if len(blob) < FILE_HEADER.size:
@@ -150,21 +220,46 @@ def read(blob: bytes) -> dict:
         raise ValueError("bad archive JSON size")
     if data_offset >= len(blob):
         raise ValueError("bad archive data offset")
-    meta = json.loads(blob[FILE_HEADER.size:FILE_HEADER.size + json_size])
+    meta = parse_metadata(blob[FILE_HEADER.size:FILE_HEADER.size + json_size])
+    tensors = meta.get("tensors") if isinstance(meta, dict) else None
+    if not isinstance(tensors, list):
+        raise ValueError("archive metadata: no tensors array")
     out = {}
     np_types = {"float32": "<f4", "bfloat16": "<u2", "int8": "i1"}
-    for item in meta["tensors"]:
-        dtype = item["dtype"]
+    for item in tensors:
+        item = item if isinstance(item, dict) else {}
+        name = item.get("name")
+        if not isinstance(name, str):
+            raise ValueError("archive metadata: tensor without a name")
+        shape = item.get("shape")
+        if (not isinstance(shape, list) or len(shape) > MAX_DIMS
+                or not all(_integer(d, (0, _I64[1])) for d in shape)):
+            raise ValueError("archive metadata: bad shape of " + name)
+        dtype = item.get("dtype")
+        dtype = dtype if isinstance(dtype, str) else ""
         if dtype not in DTYPE_BYTES:
             raise ValueError("unsupported archive dtype: " + dtype)
-        numel = int(np.prod(item["shape"], dtype=np.int64))
-        if item["nbytes"] != numel * DTYPE_BYTES[dtype]:
-            raise ValueError("tensor size mismatch: " + item["name"])
-        begin = data_offset + item["offset"]
-        if begin + item["nbytes"] > len(blob):
-            raise ValueError("tensor lies outside archive: " + item["name"])
-        if item["name"] in out:
-            raise ValueError("duplicate tensor: " + item["name"])
+        offset, nbytes = item.get("offset"), item.get("nbytes")
+        if not (_integer(offset, (0, _I64[1])) and _integer(nbytes, (0, _I64[1]))):
+            raise ValueError("archive metadata: bad offset or nbytes of " + name)
+        numel = 1
+        for d in shape:
+            numel *= d
+        if nbytes != numel * DTYPE_BYTES[dtype]:
+            raise ValueError("tensor size mismatch: " + name)
+        begin = data_offset + offset
+        if begin + nbytes > len(blob):
+            raise ValueError("tensor lies outside archive: " + name)
+        if "quant" in item:
+            q = item["quant"] if isinstance(item["quant"], dict) else {}
+            group = q.get("group_size")
+            if (not _integer(group, _I32) or group <= 0
+                    or not isinstance(q.get("scale_tensor"), str)):
+                raise ValueError("archive metadata: bad quant record of " + name)
+            if "axis" in q and not _integer(q["axis"], _I32):
+                raise ValueError("archive metadata: bad quant axis of " + name)
+        if name in out:
+            raise ValueError("duplicate tensor: " + name)
         data = np.frombuffer(blob, dtype=np_types[dtype], count=numel, offset=begin)
-        out[item["name"]] = (item, data.reshape(item["shape"]))
+        out[name] = (item, data.reshape(shape))
     return out

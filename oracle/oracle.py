@@ -17,12 +17,18 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "liblinear_oracle.so")
+# INFER_ORACLE_LIBRARY names another build of the oracle (its sanitizer
+# build, which is never built on demand); by default the in-tree build.
+_LIB_PATH = os.environ.get("INFER_ORACLE_LIBRARY") or os.path.join(_HERE, "liblinear_oracle.so")
 _lib = None
 
 
 def build(force: bool = False) -> str:
     """Compile the oracle with its Makefile (gcc, OpenMP)."""
+    if os.environ.get("INFER_ORACLE_LIBRARY"):
+        if not os.path.exists(_LIB_PATH):
+            raise FileNotFoundError(_LIB_PATH)
+        return _LIB_PATH
     if force or not os.path.exists(_LIB_PATH):
         subprocess.run(["make", "-B" if force else "all", "-C", _HERE],
                        check=True, stdout=subprocess.DEVNULL)

@@ -31,8 +31,9 @@ using namespace qlin;
 namespace {
 
 // ----------------------------------------------------------------- JSON --
-// The metadata subset: objects, arrays, strings (with \uXXXX escapes, kept as
-// UTF-8), numbers (integers exact to 2^63), true, false, null.
+// RFC 8259 JSON: objects, arrays, strings (UTF-8 checked, \uXXXX escapes
+// and surrogate pairs decoded to UTF-8), numbers in the strict grammar
+// (integers exact to 2^63), true, false, null; at most 64 levels deep.
 struct Json {
   enum Kind { kNull, kBool, kNumber, kString, kArray, kObject } kind = kNull;
   bool b = false;
@@ -43,10 +44,12 @@ struct Json {
   std::vector<Json> items;
   std::vector<std::pair<std::string, Json>> members;
 
+  // The last member of that name: a repeated key overrides the earlier one,
+  // as in nlohmann::json (which the reference parses with) and Python's json.
   const Json* get(const char* key) const {
     if (kind != kObject) return nullptr;
-    for (const auto& m : members) {
-      if (m.first == key) return &m.second;
+    for (auto m = members.rbegin(); m != members.rend(); ++m) {
+      if (m->first == key) return &m->second;
     }
     return nullptr;
   }
@@ -117,6 +120,35 @@ class JsonParser {
     }
     return true;
   }
+  // One RFC 3629 sequence whose lead byte `lead` (>= 0x80) was just read:
+  // appended to s, or false for an ill-formed one (a stray continuation
+  // byte, an overlong form, a surrogate, a code point past U+10FFFF or a cut
+  // sequence).
+  bool utf8_sequence(std::string& s, unsigned lead) {
+    int more;
+    unsigned lo = 0x80, hi = 0xBF;
+    if (lead >= 0xC2 && lead <= 0xDF) {
+      more = 1;
+    } else if (lead >= 0xE0 && lead <= 0xEF) {
+      more = 2;
+      if (lead == 0xE0) lo = 0xA0;
+      if (lead == 0xED) hi = 0x9F;
+    } else if (lead >= 0xF0 && lead <= 0xF4) {
+      more = 3;
+      if (lead == 0xF0) lo = 0x90;
+      if (lead == 0xF4) hi = 0x8F;
+    } else {
+      return false;
+    }
+    if (end_ - p_ < more) return false;
+    s.push_back(static_cast<char>(lead));
+    for (int i = 0; i < more; ++i) {
+      const unsigned b = static_cast<unsigned char>(*p_++);
+      if (b < (i == 0 ? lo : 0x80u) || b > (i == 0 ? hi : 0xBFu)) return false;
+      s.push_back(static_cast<char>(b));
+    }
+    return true;
+  }
   bool string(std::string& s) {
     if (p_ >= end_ || *p_ != '"') return bad("expected a string");
     ++p_;
@@ -125,6 +157,12 @@ class JsonParser {
       const char c = *p_++;
       if (c == '"') return true;
       if (static_cast<unsigned char>(c) < 0x20) return bad("control character in a string");
+      if (static_cast<unsigned char>(c) >= 0x80) {
+        if (!utf8_sequence(s, static_cast<unsigned char>(c))) {
+          return bad("ill-formed UTF-8 in a string");
+        }
+        continue;
+      }
       if (c != '\\') {
         s.push_back(c);
         continue;
@@ -143,6 +181,7 @@ class JsonParser {
         case 'u': {
           unsigned cp;
           if (!hex4(cp)) return bad("bad \\u escape");
+          if (cp >= 0xDC00 && cp < 0xE000) return bad("bad surrogate pair");
           if (cp >= 0xD800 && cp < 0xDC00) {  // surrogate pair
             unsigned lo;
             if (!lit("\\u") || !hex4(lo) || lo < 0xDC00 || lo >= 0xE000) {
@@ -157,22 +196,37 @@ class JsonParser {
       }
     }
   }
+  // -? (0 | [1-9][0-9]*) (. [0-9]+)? ([eE] [+-]? [0-9]+)?
   bool number(Json& out) {
     const char* start = p_;
+    auto digits = [this] {
+      const char* from = p_;
+      while (p_ < end_ && *p_ >= '0' && *p_ <= '9') ++p_;
+      return p_ != from;
+    };
     if (p_ < end_ && *p_ == '-') ++p_;
-    bool frac = false;
-    while (p_ < end_ && ((*p_ >= '0' && *p_ <= '9') || *p_ == '.' || *p_ == 'e' || *p_ == 'E' ||
-                         *p_ == '+' || *p_ == '-')) {
-      if (*p_ == '.' || *p_ == 'e' || *p_ == 'E') frac = true;
+    if (p_ < end_ && *p_ == '0') {
       ++p_;
+    } else if (!digits()) {
+      return bad("bad number");
+    }
+    bool frac = false;
+    if (p_ < end_ && *p_ == '.') {
+      ++p_;
+      frac = true;
+      if (!digits()) return bad("bad number");
+    }
+    if (p_ < end_ && (*p_ == 'e' || *p_ == 'E')) {
+      ++p_;
+      frac = true;
+      if (p_ < end_ && (*p_ == '+' || *p_ == '-')) ++p_;
+      if (!digits()) return bad("bad number");
     }
     const std::string text(start, p_);
-    if (text.empty() || text == "-") return bad("bad number");
-    char* stop = nullptr;
     out.kind = Json::kNumber;
-    out.num = std::strtod(text.c_str(), &stop);
-    if (*stop != '\0') return bad("bad number");
+    out.num = std::strtod(text.c_str(), nullptr);
     if (!frac) {
+      char* stop = nullptr;
       errno = 0;
       out.integer = std::strtoll(text.c_str(), &stop, 10);
       out.integral = errno == 0 && *stop == '\0';
@@ -527,7 +581,10 @@ extern "C" int infer_hip_archive_open(const char* path, infer_hip_archive** out)
       return fail(INFER_HIP_INVALID_ARGUMENT, "archive metadata: bad shape of %s",
                   rec.name.c_str());
     }
+    // numel exactly: `huge` marks a product past 2^64 (then no nbytes
+    // matches it); a zero extent makes it 0 whatever the others are.
     uint64_t numel = 1;
+    bool huge = false;
     for (const Json& d : shape->items) {
       uint64_t v;
       if (!as_u64(&d, v)) {
@@ -535,7 +592,11 @@ extern "C" int infer_hip_archive_open(const char* path, infer_hip_archive** out)
                     rec.name.c_str());
       }
       rec.shape.push_back(static_cast<int64_t>(v));
+      if (numel != 0 && v > UINT64_MAX / numel) huge = true;
       numel *= v;
+    }
+    for (const int64_t v : rec.shape) {
+      if (v == 0) huge = false;
     }
     const Json* dtype = item.get("dtype");
     const std::string dt = dtype && dtype->kind == Json::kString ? dtype->str : "";
@@ -552,7 +613,8 @@ extern "C" int infer_hip_archive_open(const char* path, infer_hip_archive** out)
       return fail(INFER_HIP_INVALID_ARGUMENT, "archive metadata: bad offset or nbytes of %s",
                   rec.name.c_str());
     }
-    if (rec.nbytes != numel * dtype_size(rec.dtype)) {
+    const uint64_t elem = dtype_size(rec.dtype);
+    if (huge || numel > UINT64_MAX / elem || rec.nbytes != numel * elem) {
       return fail(INFER_HIP_INVALID_ARGUMENT, "tensor size mismatch: %s", rec.name.c_str());
     }
     if (a->data_offset + rec.offset + rec.nbytes > a->mapped_bytes ||
@@ -877,17 +939,34 @@ extern "C" int infer_hip_model_config_load(const char* path, infer_hip_model_con
       !as_int(j.get("max_position_embeddings"), max_pos)) {
     return fail(INFER_HIP_INVALID_ARGUMENT, "model config: missing or non-integer field");
   }
+  // The optional fields (model_config.cpp:30-34): absent takes the default;
+  // present with another JSON type (null included) is an error, as
+  // nlohmann's value() raises for it.  bos_token_id and tie_word_embeddings
+  // are checked and not kept (the reference keeps them but never reads them).
   c.eos_token_id = -1;
-  if (const Json* e = j.get("eos_token_id"); e && e->kind != Json::kNull && !as_int(e, c.eos_token_id)) {
+  if (const Json* e = j.get("eos_token_id"); e && !as_int(e, c.eos_token_id)) {
     return fail(INFER_HIP_INVALID_ARGUMENT, "model config: bad eos_token_id");
   }
+  int bos_token_id = -1;
+  if (const Json* e = j.get("bos_token_id"); e && !as_int(e, bos_token_id)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "model config: bad bos_token_id");
+  }
   c.rms_norm_eps = 1e-6f;
-  if (const Json* e = j.get("rms_norm_eps"); e && e->kind == Json::kNumber) {
+  if (const Json* e = j.get("rms_norm_eps")) {
+    if (e->kind != Json::kNumber) {
+      return fail(INFER_HIP_INVALID_ARGUMENT, "model config: bad rms_norm_eps");
+    }
     c.rms_norm_eps = static_cast<float>(e->num);
   }
   c.rope_theta = 1e6f;
-  if (const Json* e = j.get("rope_theta"); e && e->kind == Json::kNumber) {
+  if (const Json* e = j.get("rope_theta")) {
+    if (e->kind != Json::kNumber) {
+      return fail(INFER_HIP_INVALID_ARGUMENT, "model config: bad rope_theta");
+    }
     c.rope_theta = static_cast<float>(e->num);
+  }
+  if (const Json* e = j.get("tie_word_embeddings"); e && e->kind != Json::kBool) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "model config: bad tie_word_embeddings");
   }
   // model_config.cpp:39-46
   if (c.hidden_size <= 0 || c.intermediate_size <= 0 || c.num_layers <= 0) {

@@ -16,7 +16,9 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libinfer_linear.so")
+# INFER_HIP_LIBRARY names another build of the same library (the host-only
+# sanitizer build the CPU tests load); by default the in-tree build.
+LIB_PATH = os.environ.get("INFER_HIP_LIBRARY") or os.path.join(_HERE, "libinfer_linear.so")
 
 OK = 0
 INVALID_ARGUMENT = 1
