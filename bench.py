@@ -92,9 +92,6 @@ def parse():
                     help="write per-shape and per-mode measurements to this JSON file")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic.json"),
                     help="committed HBM traffic per launch measured with rocprofv3 --pmc")
-    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
-                    help="after timing, run one device-to-device copy of this many MiB "
-                         "(the known-size reference for rocprofv3 --pmc byte counters)")
     args = ap.parse_args()
     if args.steps is None:
         args.steps = 10 if args.workload == "e2e" else 200
@@ -529,8 +526,10 @@ def linear_calls_detail(dev) -> dict:
     """tools/linear_benchmark.cpp:230-550 on the HIP path: each of the seven
     Linears of a layer as its own call (the reference's per-Linear call
     pattern), M = 1 (GEMV) and M = 32 / 128 / 512 (GEMM), W8A16 and BF16,
-    weights rotated over 4 layers' distinct tensors; per shape the mean
-    launch time over 100 calls after 20, and the layer's sum."""
+    weights rotated over 4 layers' distinct tensors.  The calls of a shape
+    are captured as one HIP graph of 24 calls and replayed, so a call's time
+    is its kernel plus the gap to the next launch (no host overhead); per
+    shape the mean over 10 replays after 3, and the layer's sum."""
     import torch
     import linear_hip as hip
     out = {}
@@ -561,13 +560,20 @@ def linear_calls_detail(dev) -> dict:
                 fn = ({(True, True): hip.gemv_w8a16, (True, False): hip.gemm_w8a16,
                        (False, True): hip.gemv_bf16, (False, False): hip.gemm_bf16}
                       [(w8, m == 1)])
-                idx = [0]
+                per_graph = 24
+                for i in range(layers):  # eager once: argument checks, warm caches
+                    fn(*calls[i])
+                torch.cuda.synchronize()
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    for i in range(per_graph):
+                        fn(*calls[i % layers])
 
-                def one(ev, calls=calls, fn=fn):
-                    fn(*calls[idx[0] % layers])
-                    idx[0] += 1
-                t, _ = time_steps(one, 100, 20)
-                us = t / 100 * 1e3
+                def one(ev, graph=graph):
+                    graph.replay()
+                t, _ = time_steps(one, 10, 3)
+                us = t / (10 * per_graph) * 1e3
+                del graph
                 total_us += us
                 cell = {"us_per_call": round(us, 2)}
                 if m == 1:
@@ -581,9 +587,10 @@ def linear_calls_detail(dev) -> dict:
     return out
 
 
-def hbm_read_ceiling(dev) -> dict:
-    """A library streaming read (torch sum over 1 GiB of FP32, more than the
-    256 MB last-level cache) as the practical read-bandwidth reference."""
+def torch_sum_read(dev) -> dict:
+    """A library streaming read for comparison: torch's sum over 1 GiB of
+    FP32 (more than the 256 MB last-level cache).  A reduction kernel, not a
+    bandwidth ceiling: the Linear GEMV plan reads faster."""
     import torch
     x = torch.ones((1 << 28,), dtype=torch.float32, device=dev)
     t, _ = time_steps(lambda ev: x.sum(), 20, 3)
@@ -690,7 +697,7 @@ def e2e_main(args, dev):
         detail = None
         if args.detail:
             detail = {"e2e": e2e_detail(workdirs, cfg), "linear_calls": linear_calls_detail(dev),
-                      "lm_head": lm_head_detail(dev, hip), "hbm_read_ceiling": hbm_read_ceiling(dev)}
+                      "lm_head": lm_head_detail(dev, hip), "torch_sum_read": torch_sum_read(dev)}
     finally:
         for wd in workdirs.values():
             shutil.rmtree(wd, ignore_errors=True)
@@ -814,13 +821,6 @@ def main() -> int:
 
     if args.detail:
         detail["lm_head"] = lm_head_detail(dev, hip)
-    if args.copy_calibration > 0:
-        src = torch.empty(args.copy_calibration << 20, dtype=torch.uint8, device=dev).fill_(1)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
 
     cpu = None
     if args.cpu_seconds > 0:

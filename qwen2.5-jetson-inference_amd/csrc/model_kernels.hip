@@ -509,6 +509,28 @@ __device__ __forceinline__ void rope_piece(const uint4 mine, const float2* cs, b
   }
 }
 
+// Workgroups of the whole-context attention.  Workgroup b runs on XCD
+// b % kXcds (the dispatcher deals workgroups to the XCDs in turn), and each
+// XCD has its own L2: the query heads that share a kv head are given
+// workgroups of one XCD, so that kv head's cache rows come from HBM once and
+// from that L2 for the others (with one workgroup per head in order, the
+// seven heads of a kv head sat on seven XCDs and each fetched the rows from
+// HBM: 9.4x the kernel's compulsory bytes).  Workgroups past the last kv
+// head exit at once.
+constexpr int kXcds = 8;
+
+int whole_attention_blocks(int heads, int kv_heads) {
+  return kXcds * ((kv_heads + kXcds - 1) / kXcds) * (heads / kv_heads);
+}
+
+// The query head of workgroup b, or -1 for a workgroup with none.
+__device__ inline int whole_attention_head(int b, int heads, int kv_heads) {
+  const int group = heads / kv_heads;
+  const int x = b % kXcds, t = b / kXcds;
+  const int g = (t / group) * kXcds + x;
+  return g < kv_heads ? g * group + t % group : -1;
+}
+
 // Waves of the whole-context workgroup (two tiles each, both in flight).
 // Measured at contexts 256-1023 (pre-rotated, us per launch): 8 waves x 2
 // tiles 4.4-6.4, 16 x 1 4.3-8.3, 4 x 4 5.0-7.7.
@@ -529,7 +551,8 @@ __global__ __launch_bounds__(whole_waves<ROPED>() * kWave) void attention_decode
   constexpr int kRowsPer = kWave / kPieces;  // rows per load instruction (8)
   constexpr bool kPrefetch = true;           // a second tile per wave
   static_assert(W * kTile * 2 >= kAttnWholeMax, "tiles cover the context");
-  const int h = blockIdx.x;
+  const int h = whole_attention_head(blockIdx.x, heads, kv_heads);
+  if (h < 0) return;
   const int group = heads / kv_heads;
   const int g = h / group;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
@@ -561,24 +584,35 @@ __global__ __launch_bounds__(whole_waves<ROPED>() * kWave) void attention_decode
       __builtin_amdgcn_make_buffer_rsrc(key_cache + head_base, 0, rows * HD * 2, 0x00020000);
   const __amdgpu_buffer_rsrc_t vr_rsrc =
       __builtin_amdgcn_make_buffer_rsrc(value_cache + head_base, 0, rows * HD * 2, 0x00020000);
-  auto load_tile = [&](int t0, uint4 (&kr)[kPieces], uint4 (&vr)[kPieces]) {
+  auto load_tile = [&](int t0, __amdgpu_buffer_rsrc_t krs, __amdgpu_buffer_rsrc_t vrs,
+                       uint4 (&kr)[kPieces], uint4 (&vr)[kPieces]) {
 #pragma unroll
     for (int j = 0; j < kPieces; ++j) {
       const uint32_t off = static_cast<uint32_t>((t0 + kRowsPer * j + rg) * HD * 2 + 16 * pc);
-      kr[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kr_rsrc, off, 0, 0));
+      kr[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, 0));
     }
 #pragma unroll
     for (int j = 0; j < kPieces; ++j) {
       const uint32_t off = static_cast<uint32_t>((t0 + kRowsPer * j + rg) * HD * 2 + 16 * pc);
-      vr[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr_rsrc, off, 0, 0));
+      vr[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vrs, off, 0, 0));
     }
   };
   uint4 kr[kPieces], vr[kPieces], kn[kPieces], vn[kPieces];
-  load_tile(wave * kTile, kr, vr);
-  if (kPrefetch) load_tile((wave + W) * kTile, kn, vn);
+  load_tile(wave * kTile, kr_rsrc, vr_rsrc, kr, vr);
   if constexpr (ROPED) pos = min(*pos_ptr, max_seq - 1);
   // Positions [0, end) come from the tiles.
   const int end = ROPED ? pos + 1 : pos;
+  if (kPrefetch) {
+    // The first tiles went out before the position arrived.  The second
+    // tiles are bounded by the context: rows past it read as 0 without a
+    // memory access (and are masked below), so the CU takes in only the
+    // context's rows beyond the first W tiles.
+    const uint32_t bytes = static_cast<uint32_t>(ROPED ? end : rows) * HD * 2;
+    load_tile((wave + W) * kTile,
+              __builtin_amdgcn_make_buffer_rsrc(key_cache + head_base, 0, bytes, 0x00020000),
+              __builtin_amdgcn_make_buffer_rsrc(value_cache + head_base, 0, bytes, 0x00020000),
+              kn, vn);
+  }
 
   const float scale = 1.0f / sqrtf(static_cast<float>(HD));
   uint32_t qw[4];  // the lane's 8 q dimensions, BF16 pairs
@@ -1101,11 +1135,13 @@ void launch_attention_decode(const uint16_t* q, const uint16_t* k_new, const uin
                              hipStream_t stream) {
   if (attention_whole(max_seq, head_dim)) {
     if (roped) {
-      hipLaunchKernelGGL(attention_decode_whole_kernel<true>, dim3(heads),
+      hipLaunchKernelGGL(attention_decode_whole_kernel<true>,
+                         dim3(whole_attention_blocks(heads, kv_heads)),
                          dim3(whole_waves<true>() * kWave), 0, stream, q, k_new, v_new,
                          key_cache, value_cache, rope, pos, heads, kv_heads, max_seq, out);
     } else {
-      hipLaunchKernelGGL(attention_decode_whole_kernel<false>, dim3(heads),
+      hipLaunchKernelGGL(attention_decode_whole_kernel<false>,
+                         dim3(whole_attention_blocks(heads, kv_heads)),
                          dim3(whole_waves<false>() * kWave), 0, stream, q, k_new, v_new,
                          key_cache, value_cache, rope, pos, heads, kv_heads, max_seq, out);
     }

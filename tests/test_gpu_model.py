@@ -349,7 +349,7 @@ def test_config4_workload_teacher_forced(orc, dev):
     """Config 4's workload: prompt of 512 uniform-random tokens (seed 4),
     max_seq 1024, then teacher-forced decode to context 1023 (511 steps),
     every step against the FP32 oracle: the prefill's grouped MFMA launches
-    at 512 rows and the decode attention over 5 to 8 context spans."""
+    at 512 rows and the whole-context decode attention."""
     cfg, g, o = full_size(orc, 1024)
     p = prompt(512, cfg.vocab_size, seed=4)
     agree, total, worst = teacher_forced(g, o, p, 511, 0.999, "config 4")
