@@ -21,6 +21,12 @@
  *   infer_hip_attention_decode_bf16    attention_decode_bf16 (cuda_ops.hpp:86-91;
  *                                      qwen2.cpp:633-636) on rotated q and a
  *                                      cache that holds the token
+ *   infer_hip_attention_decode_halves_bf16
+ *                                      the same, split into two context halves
+ *                                      whose records
+ *   infer_hip_attention_halves_o_proj_w8a16
+ *                                      merges before gemv_w8a16 (o_proj) +
+ *                                      add_inplace_bf16 (qwen2.cpp:633-641)
  *   infer_hip_gemv_w8a16_rows          gemv_w8a16 + add_inplace_bf16 (cuda_ops.hpp:
  *                                      98-99) for down_proj and the residual
  *                                      (qwen2.cpp:655-659)
@@ -133,6 +139,33 @@ int infer_hip_attention_decode_bf16(const uint16_t* q, const uint16_t* key_cache
                                     const uint16_t* value_cache, const int* position,
                                     uint16_t* output, int num_heads, int num_kv_heads,
                                     int head_dim, int max_sequence_length, hipStream_t stream);
+
+/* The same attention in two halves, as the decode step runs it: for query
+ * head h and half sp (positions [512 sp, 512 sp + 512) of [0, p]) one
+ * workgroup stores the record records[(h * 2 + sp) * 68 + i]: i < 64 the
+ * half's unnormalised sum of e^(score - m) v, i = 64 m (the half's largest
+ * score), i = 65 the sum of e^(score - m).  A half past the context stores
+ * nothing.  Same preconditions as infer_hip_attention_decode_bf16; records
+ * holds num_heads x 2 x 68 floats, 16-byte aligned. */
+int infer_hip_attention_decode_halves_bf16(const uint16_t* q, const uint16_t* key_cache,
+                                           const uint16_t* value_cache, const int* position,
+                                           float* records, int num_heads, int num_kv_heads,
+                                           int head_dim, int max_sequence_length,
+                                           hipStream_t stream);
+
+/* The decode step's o-projection over those records (attention_decode_bf16
+ * + gemv_w8a16 o_proj + add_inplace_bf16, cuda_ops.hpp:86-99, qwen2.cpp:
+ * 633-641): with p = min(*position, max_sequence_length - 1), halves
+ * S = {0} for p < 512, else {0, 1}, M = max_{sp in S} m_sp,
+ *   a[64 h + d] = bf16( sum_sp acc_sp[d] e^(m_sp - M) * (1 / sum_sp l_sp e^(m_sp - M)) ),
+ *   residual[n] = bf16(W[n] . a + residual[n]).
+ * W8A16 weight [out_features, num_heads * 64] with BF16 group-64 scales;
+ * num_heads * 64 <= 4096; a second half outside S is never summed. */
+int infer_hip_attention_halves_o_proj_w8a16(const float* records, const int* position,
+                                            int num_heads, int max_sequence_length,
+                                            const int8_t* weight, const uint16_t* scales,
+                                            uint16_t* residual, int out_features,
+                                            hipStream_t stream);
 
 /* output[n] = bf16(sum_k q[n,k] s[n,k/64] input[k] + bias[n]) with one
  * wave per output row and the whole row in flight at once.  bias may be

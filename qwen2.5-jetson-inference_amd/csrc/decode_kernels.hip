@@ -22,6 +22,7 @@
 #include <stdint.h>
 
 #include "decode_kernels.hpp"
+#include "model_kernels.hpp"
 #include "device_common.hpp"
 
 namespace qlin {
@@ -322,6 +323,85 @@ __global__ __launch_bounds__(kBlock) void gemv_w8_rows_kernel(GemvRowsArgs a) {
   if (lane == 0 && row < a.n) {
     const float b = a.bias ? bf16_to_f32(bias_raw) : 0.0f;
     gstore(a.y + row, f32_to_bf16(v + b));
+  }
+}
+
+// The o-projection with the merge of the attention's two halves (see
+// decode_kernels.hpp).  One wave per row, the whole row's loads, both
+// records' pieces and the residual in flight at once.  Lane l's chunk c
+// (16 inputs) is head c / 4, dimensions 16 (c % 4) .. + 15.  A second half
+// that the context has not reached is never summed (select, so stale values
+// cannot reach the result).
+template <int SLABS>
+__global__ __launch_bounds__(kBlock) void attn_o_halves_kernel(AttnOHalvesArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int row = blockIdx.x * kWaves + threadIdx.x / kWave;
+  uint4 wq[SLABS];
+  uint32_t sc[SLABS];
+  load_w8_row<SLABS>(a.w, a.s, row, a.n, a.k, lane, wq, sc);
+  const uint16_t res_raw = gload(a.x + min(row, a.n - 1));
+  const int chunks = a.k >> 4;
+  const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(a.partial), 0, a.heads * 2 * kAttnHalfRecord * 4, 0x00020000);
+  uint4 r0[SLABS][4], r1[SLABS][4];
+  float2 ml0[SLABS], ml1[SLABS];
+#pragma unroll
+  for (int s = 0; s < SLABS; ++s) {
+    const int c = min(s * kWave + lane, chunks - 1);
+    const uint32_t b0 = static_cast<uint32_t>((c >> 2) * 2 * kAttnHalfRecord) * 4u;
+    const uint32_t b1 = b0 + kAttnHalfRecord * 4u;
+    const uint32_t d = static_cast<uint32_t>((c & 3) * 16) * 4u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      r0[s][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(pr, b0 + d + 16u * j, 0, 0));
+      r1[s][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(pr, b1 + d + 16u * j, 0, 0));
+    }
+    ml0[s] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(pr, b0 + 64u * 4u, 0, 0));
+    ml1[s] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(pr, b1 + 64u * 4u, 0, 0));
+  }
+  const int pos = min(*a.pos, a.max_seq - 1);
+  __builtin_amdgcn_sched_barrier(0);  // every load is in flight
+  const bool two = pos >= kAttnHalfSpan;
+  float xv[SLABS][16];
+#pragma unroll
+  for (int s = 0; s < SLABS; ++s) {
+    const bool keep = s * kWave + lane < chunks;
+    const float m = two ? fmaxf(ml0[s].x, ml1[s].x) : ml0[s].x;
+    const float w0 = expf(ml0[s].x - m);
+    const float w1 = two ? expf(ml1[s].x - m) : 0.0f;
+    const float l0w = ml0[s].y * w0;
+    const float ll = two ? fmaf(ml1[s].y, w1, l0w) : l0w;
+    const float inv = 1.0f / ll;  // one division per lane, then products
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float a0[4] = {__uint_as_float(r0[s][j].x), __uint_as_float(r0[s][j].y),
+                           __uint_as_float(r0[s][j].z), __uint_as_float(r0[s][j].w)};
+      const float a1[4] = {__uint_as_float(r1[s][j].x), __uint_as_float(r1[s][j].y),
+                           __uint_as_float(r1[s][j].z), __uint_as_float(r1[s][j].w)};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float a0w = a0[t] * w0;
+        const float aa = two ? fmaf(a1[t], w1, a0w) : a0w;
+        // the attention's output is BF16, as attention_decode_bf16 stores it
+        xv[s][4 * j + t] = keep ? bf16_to_f32(f32_to_bf16(aa * inv)) : 0.0f;
+      }
+    }
+  }
+  const float v = w8_row_dot<SLABS>(wq, sc, xv, row < a.n, a.k, lane);
+  if (lane == 0 && row < a.n) gstore(a.x + row, f32_to_bf16(v + bf16_to_f32(res_raw)));
+}
+
+bool attn_o_halves_supported(int k) { return k % 64 == 0 && k <= 4 * kWave * 16; }
+
+void launch_attn_o_halves(const AttnOHalvesArgs& a, hipStream_t stream) {
+  const dim3 grid((a.n + kWaves - 1) / kWaves), block(kBlock);
+  const int slabs = (a.k + kWave * 16 - 1) / (kWave * 16);
+  if (slabs <= 1) {
+    hipLaunchKernelGGL((attn_o_halves_kernel<1>), grid, block, 0, stream, a);
+  } else if (slabs <= 2) {
+    hipLaunchKernelGGL((attn_o_halves_kernel<2>), grid, block, 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((attn_o_halves_kernel<4>), grid, block, 0, stream, a);
   }
 }
 

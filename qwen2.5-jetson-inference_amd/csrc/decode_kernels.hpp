@@ -120,6 +120,27 @@ struct AttnOArgs {
 };
 
 bool attn_o_supported(int k, int heads, bool w8);
+
+// The fused decode step's o-projection (W8A16, group 64) with the merge of
+// the attention's two halves (launch_attention_decode_halves):
+//   a[i] = bf16( sum_sp acc_sp[i] e^(m_sp - M) / sum_sp l_sp e^(m_sp - M) ),
+//   M = max_sp m_sp over the halves [0, pos / kAttnHalfSpan],
+//   x[row] = bf16(Wo[row] . a + x[row]).
+// Lane l's inputs (16 per 16-byte weight chunk) come from one head, so it
+// merges them from the two records in registers: no LDS, no barrier.
+struct AttnOHalvesArgs {
+  const float* partial;  // heads x 2 records of kAttnHalfRecord floats
+  const int* pos;        // position of the decoded token (device)
+  int heads;
+  int max_seq;
+  const int8_t* w;       // [n, k] int8
+  const uint16_t* s;     // [n, k / 64] BF16 scales
+  uint16_t* x;           // [n] residual stream, updated in place
+  int n;
+  int k;                 // heads x 64
+};
+bool attn_o_halves_supported(int k);
+void launch_attn_o_halves(const AttnOHalvesArgs& a, hipStream_t stream);
 void launch_attn_o_gemv(const AttnOArgs& a, bool w8, hipStream_t stream);
 
 constexpr int kLmHeadMaxSlabs = 8;  // K <= 4096

@@ -86,6 +86,59 @@ extern "C" int infer_hip_rms_norm_gate_up_silu_w8a16(
   return check_launch(what);
 }
 
+extern "C" int infer_hip_attention_decode_halves_bf16(
+    const uint16_t* q, const uint16_t* key_cache, const uint16_t* value_cache,
+    const int* position, float* records, int num_heads, int num_kv_heads, int head_dim,
+    int max_sequence_length, hipStream_t stream) {
+  const char* what = "attention_decode_halves_bf16";
+  if (!q || !key_cache || !value_cache || !position || !records) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: null pointer", what);
+  }
+  if (num_heads < 1 || num_kv_heads < 1 || num_heads % num_kv_heads != 0) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: %d heads, %d kv heads", what, num_heads,
+                num_kv_heads);
+  }
+  if (max_sequence_length < 1 || !attention_whole(max_sequence_length, head_dim)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "%s: head_dim %d, max_sequence_length %d (head_dim 64, at most %d)", what,
+                head_dim, max_sequence_length, kAttnWholeMax);
+  }
+  if (!aligned16(q) || !aligned16(key_cache) || !aligned16(value_cache) ||
+      !aligned16(records)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: q, caches and records must be 16-byte aligned",
+                what);
+  }
+  launch_attention_decode_halves(q, key_cache, value_cache, position, num_heads, num_kv_heads,
+                                 max_sequence_length, records, stream);
+  return check_launch(what);
+}
+
+extern "C" int infer_hip_attention_halves_o_proj_w8a16(
+    const float* records, const int* position, int num_heads, int max_sequence_length,
+    const int8_t* weight, const uint16_t* scales, uint16_t* residual, int out_features,
+    hipStream_t stream) {
+  const char* what = "attention_halves_o_proj_w8a16";
+  if (!records || !position || !weight || !scales || !residual) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: null pointer", what);
+  }
+  const int in_features = num_heads * 64;
+  if (num_heads < 1 || out_features < 1 || max_sequence_length < 1 ||
+      max_sequence_length > kAttnWholeMax || !attn_o_halves_supported(in_features)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "%s: %d heads (in_features %d: multiple of 64, at most 4096), %d outputs, "
+                "max_sequence_length %d (at most %d)",
+                what, num_heads, in_features, out_features, max_sequence_length, kAttnWholeMax);
+  }
+  if (!aligned16(records) || !aligned16(weight)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: records and weight must be 16-byte aligned",
+                what);
+  }
+  launch_attn_o_halves({records, position, num_heads, max_sequence_length, weight, scales,
+                        residual, out_features, in_features},
+                       stream);
+  return check_launch(what);
+}
+
 extern "C" int infer_hip_gemv_w8a16_rows(const int8_t* weight, const uint16_t* scales,
                                          const uint16_t* bias, const uint16_t* input,
                                          uint16_t* output, int out_features, int in_features,

@@ -355,15 +355,25 @@ int enqueue_decode_step(infer_hip_model* m, int only = -1, hipEvent_t* events = 
       }
     }
     run(kKindAttention, [&] {
-      launch_attention_decode(m->q, m->k, m->v, L.key_cache, L.value_cache, m->rope,
-                              &m->state->pos,
-                              c.num_heads, c.num_kv_heads, m->head_dim, m->max_seq,
-                              m->fused_qkv_rope, m->attn_partial, m->attn, s);
+      if (m->fused_qkv_rope) {
+        launch_attention_decode_halves(m->q, L.key_cache, L.value_cache, &m->state->pos,
+                                       c.num_heads, c.num_kv_heads, m->max_seq,
+                                       m->attn_partial, s);
+      } else {
+        launch_attention_decode(m->q, m->k, m->v, L.key_cache, L.value_cache, m->rope,
+                                &m->state->pos, c.num_heads, c.num_kv_heads, m->head_dim,
+                                m->max_seq, false, m->attn_partial, m->attn, s);
+      }
     });
-    // x = bf16(Wo attn + x): attn is the whole-context attention's output,
-    // or merged here from the split attention's partials
+    // x = bf16(Wo attn + x): attn is merged here from the attention's
+    // partials (the two halves, or the spans of the split form), or is the
+    // whole-context attention's output
     run(kKindAttnO, [&] {
-      if (!attention_whole(m->max_seq, m->head_dim)) {
+      if (m->fused_qkv_rope) {
+        launch_attn_o_halves({m->attn_partial, &m->state->pos, c.num_heads, m->max_seq,
+                              static_cast<const int8_t*>(L.o.w), L.o.s, m->x, hidden, hidden},
+                             s);
+      } else if (!attention_whole(m->max_seq, m->head_dim)) {
         launch_attn_o_gemv({m->attn_partial, &m->state->pos, c.num_heads, m->head_dim,
                             attention_span(m->max_seq, m->head_dim),
                             attention_splits(m->max_seq, m->head_dim), m->max_seq, L.o.w, L.o.s,
@@ -415,11 +425,13 @@ double kind_bytes(const infer_hip_model* m, int kind, int ctx, int* launches) {
   auto linear = [&](double n, double k) {
     return n * k * wb + (m->w8 ? 2.0 * n * (k / 64) : 0.0);
   };
-  // the attention's output: split partials, or the BF16 head outputs
-  const int span = attention_span(m->max_seq, m->head_dim);
+  // the attention's output: the records of the halves or of the split
+  // form's spans, or the BF16 head outputs of the whole-context form
+  const int span = m->fused_qkv_rope ? kAttnHalfSpan : attention_span(m->max_seq, m->head_dim);
   const double splits = (ctx + span - 1) / span;
-  const double partials =
-      attention_whole(m->max_seq, m->head_dim) ? 2 * H : c.num_heads * splits * (hd + 2) * 4;
+  const double partials = (attention_whole(m->max_seq, m->head_dim) && !m->fused_qkv_rope)
+                              ? 2 * H
+                              : c.num_heads * splits * (hd + 2) * 4;
   const bool fused = m->fused_norm_gemv;
   const bool bf16_split = !m->w8;  // separate q, k, v (and gate, up) launches
   int n = 0;
@@ -685,7 +697,8 @@ extern "C" int infer_hip_model_create(const infer_hip_model_config* config,
   m->fused_norm_gemv = w8 && norm_gemv_w8_supported(hidden);
   m->fused_lm_head = lm_head_decode_supported(hidden);
   m->fused_qkv_rope = m->fused_norm_gemv && attention_whole(max_seq, head_dim) &&
-                      norm_qkv_rope_supported(hidden, head_dim);
+                      norm_qkv_rope_supported(hidden, head_dim) &&
+                      attn_o_halves_supported(hidden);
 
   // Arena layout.
   size_t cursor = 0;
@@ -708,8 +721,11 @@ extern "C" int infer_hip_model_create(const infer_hip_model_config* config,
   const size_t o_lmcounter = take(sizeof(int));
   const size_t o_rope = take(sizeof(float2) * ms * (head_dim / 2));
   const size_t o_rope_cur = take(sizeof(float2) * (head_dim / 2));
+  // (the fused step's two halves: 2 records of kAttnHalfRecord floats per head)
   const size_t o_partial = take(sizeof(float) * c.num_heads *
-                                attention_splits(max_seq, head_dim) * (head_dim + 2));
+                                std::max<size_t>(2 * kAttnHalfRecord,
+                                                 static_cast<size_t>(attention_splits(
+                                                     max_seq, head_dim)) * (head_dim + 2)));
   const size_t o_attn = take(2 * hidden);
   const size_t o_px = take(2 * ms * hidden), o_pnorm = take(2 * ms * hidden);
   const size_t o_pq = take(2 * ms * hidden), o_pk = take(2 * ms * kv_dim);

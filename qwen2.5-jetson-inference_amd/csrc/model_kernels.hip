@@ -725,6 +725,140 @@ __global__ __launch_bounds__(whole_waves<ROPED>() * kWave) void attention_decode
   }
 }
 
+// The whole-context attention in two halves: workgroup (query head h, half
+// sp) takes the positions [sp * kAttnHalfSpan, (sp + 1) * kAttnHalfSpan) of
+// the context, one 64-position tile per wave, all requested at kernel entry,
+// and stores the half's (acc[HD], max, sum) record for the o-projection to
+// merge (partial[(h * 2 + sp) * kAttnHalfRecord]).  A half past the context
+// exits without a
+// record; the merge reads only halves [0, pos / kAttnHalfSpan].  q is
+// rotated and the caches hold the token's row (as the fused q|k|v launch
+// leaves them).  Workgroups: the two halves of kv head g on XCDs 2 g and
+// 2 g + 1, each shared by the kv head's query heads (as
+// whole_attention_head does for one workgroup per head).
+int half_attention_blocks(int heads, int kv_heads) {
+  const int units = 2 * kv_heads;
+  return kXcds * ((units + kXcds - 1) / kXcds) * (heads / kv_heads);
+}
+
+__device__ inline int half_attention_unit(int b, int heads, int kv_heads, int& h) {
+  const int group = heads / kv_heads;
+  const int x = b % kXcds, t = b / kXcds;
+  const int u = (t / group) * kXcds + x;  // 2 g + sp
+  h = (u >> 1) * group + t % group;
+  return u < 2 * kv_heads ? u : -1;
+}
+
+__global__ __launch_bounds__(kWholeWaves * kWave) void attention_decode_halves_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ key_cache,
+    const uint16_t* __restrict__ value_cache, const int* __restrict__ pos_ptr, int heads,
+    int kv_heads, int max_seq, float* __restrict__ partial) {
+  constexpr int HD = 64, W = kWholeWaves;
+  constexpr int kPieces = HD / 8;            // 16-byte pieces per row (8)
+  constexpr int kRowsPer = kWave / kPieces;  // rows per load instruction (8)
+  static_assert(W * kTile == kAttnHalfSpan, "one tile per wave covers a half");
+  int h;
+  const int u = half_attention_unit(blockIdx.x, heads, kv_heads, h);
+  if (u < 0) return;
+  const int g = u >> 1, sp = u & 1;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int pc = lane % kPieces, rg = lane / kPieces;
+  const size_t head_base = static_cast<size_t>(g) * max_seq * HD;
+  const uint4 q_mine = reinterpret_cast<const uint4*>(q + static_cast<size_t>(h) * HD)[pc];
+  // The tile goes out before the position arrives: rows past max_seq read 0,
+  // rows past the context are masked below.
+  const __amdgpu_buffer_rsrc_t kr_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(key_cache) + head_base, 0, max_seq * HD * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vr_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(value_cache) + head_base, 0, max_seq * HD * 2, 0x00020000);
+  const int t0 = sp * kAttnHalfSpan + wave * kTile;
+  uint4 kt[kPieces], vt[kPieces];
+#pragma unroll
+  for (int j = 0; j < kPieces; ++j) {
+    const uint32_t off = static_cast<uint32_t>((t0 + kRowsPer * j + rg) * HD * 2 + 16 * pc);
+    kt[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kr_rsrc, off, 0, 0));
+  }
+#pragma unroll
+  for (int j = 0; j < kPieces; ++j) {
+    const uint32_t off = static_cast<uint32_t>((t0 + kRowsPer * j + rg) * HD * 2 + 16 * pc);
+    vt[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr_rsrc, off, 0, 0));
+  }
+  const int end = min(*pos_ptr, max_seq - 1) + 1;  // positions [0, end)
+  if (sp * kAttnHalfSpan >= end) return;           // a half past the context
+  const float scale = 1.0f / sqrtf(static_cast<float>(HD));
+  const uint32_t qw[4] = {q_mine.x, q_mine.y, q_mine.z, q_mine.w};
+  float m = -INFINITY, l = 0.0f;
+  float acc8[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) acc8[t] = 0.0f;
+  if (t0 < end) {  // wave-uniform: a tile past the context is skipped whole
+    float part[kPieces];
+#pragma unroll
+    for (int j = 0; j < kPieces; ++j) part[j] = dot8_packed_bf16(qw, kt[j]);
+    const float score = group8_reduce_scatter(part, lane);  // row 8 pc + rg
+    const bool valid = t0 + kRowsPer * pc + rg < end;
+    const float sc = valid ? score * scale : -INFINITY;
+    m = wave_max(sc);
+    const float e = valid ? expf(sc - m) : 0.0f;
+    l = wave_sum(e);
+    float ej[kPieces];
+    ej[0] = group8_lane<0>(e);
+    ej[1] = group8_lane<1>(e);
+    ej[2] = group8_lane<2>(e);
+    ej[3] = group8_lane<3>(e);
+    ej[4] = group8_lane<4>(e);
+    ej[5] = group8_lane<5>(e);
+    ej[6] = group8_lane<6>(e);
+    ej[7] = group8_lane<7>(e);
+#pragma unroll
+    for (int j = 0; j < kPieces; ++j) {
+      // rows past the context hold whatever the cache held: never summed
+      const bool row_ok = t0 + kRowsPer * j + rg < end;
+      float vf[8];
+      unpack8_bf16(vt[j], vf);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) acc8[t] = row_ok ? fmaf(ej[j], vf[t], acc8[t]) : acc8[t];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  const float mine = rows8_reduce_scatter(acc8, lane);  // dimension 8 pc + rg
+  __shared__ float wm[W], wl[W];
+  __shared__ float wacc[W][HD];
+  if (lane == 0) {
+    wm[wave] = m;
+    wl[wave] = l;
+  }
+  wacc[wave][8 * pc + rg] = mine;
+  __syncthreads();
+  if (tid < HD) {
+    float mm = wm[0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) mm = fmaxf(mm, wm[w]);
+    float ll = 0.0f, aa = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const float f = wl[w] > 0.0f ? expf(wm[w] - mm) : 0.0f;
+      ll = fmaf(wl[w], f, ll);
+      aa = fmaf(wacc[w][tid], f, aa);
+    }
+    float* rec = partial + static_cast<size_t>(h * 2 + sp) * kAttnHalfRecord;
+    rec[tid] = aa;
+    if (tid == 0) {
+      rec[HD] = mm;
+      rec[HD + 1] = ll;
+    }
+  }
+}
+
+void launch_attention_decode_halves(const uint16_t* q, const uint16_t* key_cache,
+                                    const uint16_t* value_cache, const int* pos, int heads,
+                                    int kv_heads, int max_seq, float* partial,
+                                    hipStream_t stream) {
+  hipLaunchKernelGGL(attention_decode_halves_kernel, dim3(half_attention_blocks(heads, kv_heads)),
+                     dim3(kWholeWaves * kWave), 0, stream, q, key_cache, value_cache, pos, heads,
+                     kv_heads, max_seq, partial);
+}
+
 // ----------------------------------------------------- prefill attention --
 
 // Causal attention of count tokens (positions 0 .. count - 1, already in

@@ -45,6 +45,19 @@ constexpr int kAttnWaves = 2;
 constexpr int kAttnMaxSplits = 8;
 constexpr int kAttnWholeMax = 1024;
 bool attention_whole(int max_seq, int head_dim);
+
+// The whole-context attention of the fused decode step (rotated q, k and v
+// already in the caches) in two halves of kAttnHalfSpan positions: each
+// (query head, half) workgroup stores an (acc[64], max, sum) record at
+// partial[(head * 2 + half) * kAttnHalfRecord], merged by
+// launch_attn_o_halves.  head_dim 64, max_seq <= kAttnWholeMax.
+constexpr int kAttnHalfSpan = kAttnWholeMax / 2;
+// Floats per (head, half) record: acc[64], max, sum, 2 pad (16-byte aligned).
+constexpr int kAttnHalfRecord = 68;
+void launch_attention_decode_halves(const uint16_t* q, const uint16_t* key_cache,
+                                    const uint16_t* value_cache, const int* pos, int heads,
+                                    int kv_heads, int max_seq, float* partial,
+                                    hipStream_t stream);
 int attention_span(int max_seq, int head_dim);
 int attention_splits(int max_seq, int head_dim);
 // roped (whole form only): q is already rotated and the token's k and v are

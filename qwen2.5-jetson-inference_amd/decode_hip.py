@@ -22,6 +22,8 @@ EXPORTED_SYMBOLS = (
     "infer_hip_rms_norm_qkv_rope_w8a16",
     "infer_hip_rope_row",
     "infer_hip_attention_decode_bf16",
+    "infer_hip_attention_decode_halves_bf16",
+    "infer_hip_attention_halves_o_proj_w8a16",
     "infer_hip_gemv_w8a16_rows",
     "infer_hip_attention_decode_span",
     "infer_hip_attention_decode_splits",
@@ -62,6 +64,8 @@ def load():
                                                i, i, i, i, p], i),
         "infer_hip_rope_row": ([f, i, i, ctypes.POINTER(ctypes.c_float)], i),
         "infer_hip_attention_decode_bf16": ([p, p, p, p, p, i, i, i, i, p], i),
+        "infer_hip_attention_decode_halves_bf16": ([p, p, p, p, p, i, i, i, i, p], i),
+        "infer_hip_attention_halves_o_proj_w8a16": ([p, p, i, i, p, p, p, i, p], i),
         "infer_hip_gemv_w8a16_rows": ([p, p, p, p, p, i, i, p], i),
         "infer_hip_attention_decode_span": ([i, i], i),
         "infer_hip_attention_decode_splits": ([i, i], i),
@@ -125,6 +129,26 @@ def attention_decode_bf16(q, key_cache, value_cache, position, output, num_heads
     _check(load().infer_hip_attention_decode_bf16(
         _ptr(q), _ptr(key_cache), _ptr(value_cache), _ptr(position), _ptr(output), num_heads,
         num_kv_heads, head_dim, max_sequence_length, _stream(stream)))
+
+
+HALF_RECORD = 68  # floats per (head, half) record of the two-halves attention
+
+
+def attention_decode_halves_bf16(q, key_cache, value_cache, position, records,
+                                 num_heads: int, num_kv_heads: int, head_dim: int,
+                                 max_sequence_length: int, stream=None) -> None:
+    """records: float32 [num_heads, 2, HALF_RECORD]."""
+    _check(load().infer_hip_attention_decode_halves_bf16(
+        _ptr(q), _ptr(key_cache), _ptr(value_cache), _ptr(position), _ptr(records), num_heads,
+        num_kv_heads, head_dim, max_sequence_length, _stream(stream)))
+
+
+def attention_halves_o_proj_w8a16(records, position, num_heads: int, max_sequence_length: int,
+                                  weight, scales, residual, out_features: int,
+                                  stream=None) -> None:
+    _check(load().infer_hip_attention_halves_o_proj_w8a16(
+        _ptr(records), _ptr(position), num_heads, max_sequence_length, _ptr(weight),
+        _ptr(scales), _ptr(residual), out_features, _stream(stream)))
 
 
 def gemv_w8a16_rows(weight, scales, bias, input, output, out_features: int,

@@ -299,3 +299,22 @@ def test_rope_row_and_new_decode_ops_reject_bad_arguments(hip):
         a = list(args)
         a[i] = v
         assert g(*a) == bad, (i, v)
+
+
+def test_halves_attention_ops_reject_bad_arguments(hip):
+    import decode_hip
+    lib = decode_hip.load()
+    bad = hip.INVALID_ARGUMENT
+    f = lib.infer_hip_attention_decode_halves_bf16
+    assert f(4096, 4096, 4096, 4096, 4096, 14, 2, 64, 2048, None) == bad  # at most 1024
+    assert f(4096, 4096, 4096, 4096, 4096, 14, 2, 128, 512, None) == bad  # head_dim 64
+    assert f(4096, 4096, 4096, 4096, 4096, 14, 3, 64, 512, None) == bad  # GQA
+    assert f(4096, 4096, 4096, 4096, 4100, 14, 2, 64, 512, None) == bad  # records aligned
+    assert f(4096, 4096, 4096, None, 4096, 14, 2, 64, 512, None) == bad
+    g = lib.infer_hip_attention_halves_o_proj_w8a16
+    assert g(4096, 4096, 65, 1024, 4096, 4096, 4096, 896, None) == bad   # 65 x 64 > 4096
+    assert g(4096, 4096, 14, 1025, 4096, 4096, 4096, 896, None) == bad   # max_seq
+    assert g(4096, 4096, 14, 1024, 4096, 4096, 4096, 0, None) == bad     # no outputs
+    assert g(4100, 4096, 14, 1024, 4096, 4096, 4096, 896, None) == bad   # records aligned
+    assert g(4096, 4096, 14, 1024, 4104, 4096, 4096, 896, None) == bad   # weight aligned
+    assert g(4096, None, 14, 1024, 4096, 4096, 4096, 896, None) == bad

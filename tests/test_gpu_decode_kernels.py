@@ -547,3 +547,85 @@ def test_attention_decode_bf16_matches_oracle(dec, orc, dev, heads, kvh):
         tol = 2.0 ** -8 * np.abs(e) + 1e-4 * np.max(np.abs(e))
         assert np.all(np.isfinite(got)), position
         assert np.all(np.abs(got - e) <= tol), (position, float(np.max(np.abs(got - e) / tol)))
+
+
+# ------------------------ two-halves attention + merge in the o GEMV --
+
+HALF_POSITIONS = (0, 1, 63, 64, 511, 512, 513, 767, 1022, 1023, 2000)
+
+
+@pytest.mark.parametrize("heads,kvh", [(14, 2), (8, 1), (4, 4)])
+def test_attention_decode_halves_matches_oracle(dec, orc, dev, heads, kvh):
+    """Each half's record against the oracle's attention (cpu_ops.cpp:58-91
+    restated): merged on the host in float64 they give the whole context's
+    output; rows past p hold NaN and must not matter, and a half past the
+    context leaves its record untouched."""
+    import torch
+    hd, max_seq, R = 64, 1024, dec.HALF_RECORD
+    rng = rc.philox(900 + heads)
+    q = rc.bf16_normal(rng, (heads * hd,), 0.5)
+    kcache = rc.bf16_normal(rng, (kvh, max_seq, hd))
+    vcache = rc.bf16_normal(rng, (kvh, max_seq, hd))
+    for position in HALF_POSITIONS:
+        p = min(position, max_seq - 1)
+        kc, vc = kcache.copy(), vcache.copy()
+        kc[:, p + 1:] = 0x7FC0
+        vc[:, p + 1:] = 0x7FC0
+        exp = np.asarray(orc.attention_decode(rc.bf16_values(q), rc.bf16_values(kcache),
+                                              rc.bf16_values(vcache), heads, kvh, hd, p + 1,
+                                              max_seq), dtype=np.float64)
+        rec = torch.full((heads, 2, R), float("nan"), dtype=torch.float32, device=dev)
+        dpos = torch.tensor([position], dtype=torch.int32, device=dev)
+        dec.attention_decode_halves_bf16(to_dev(q, dev), to_dev(kc, dev), to_dev(vc, dev),
+                                         dpos, rec, heads, kvh, hd, max_seq)
+        r = rec.cpu().numpy().astype(np.float64)
+        used = 1 if p < 512 else 2
+        assert np.all(np.isfinite(r[:, :used, :hd + 2])), position
+        if used == 1:
+            assert np.all(np.isnan(r[:, 1])), f"position {position}: second half written"
+        m = r[:, :used, hd]
+        big = m.max(axis=1, keepdims=True)
+        e = np.exp(m - big)
+        got = ((r[:, :used, :hd] * e[:, :, None]).sum(axis=1) /
+               (r[:, :used, hd + 1] * e).sum(axis=1)[:, None]).reshape(-1)
+        tol = 2.0 ** -12 * np.abs(exp) + 1e-5 * np.max(np.abs(exp))  # FP32 softmax / sums
+        assert np.all(np.abs(got - exp) <= tol), (position, float(np.max(np.abs(got - exp) / tol)))
+
+
+@pytest.mark.parametrize("heads,n", [(14, 896), (2, 130), (64, 65)])
+def test_attention_halves_o_proj_bit_exact(dec, dev, heads, n):
+    """Merge weights exactly 1 (m = 0; l = 1 in the first half, 0 in the
+    second) and accumulators in multiples of 1/8: the merged attention and
+    the o GEMV with power-of-two scales are exact, so the result is compared
+    bit for bit.  Below position 512 the second half's records hold NaN and
+    must not reach the output."""
+    import torch
+    hd, max_seq, R = 64, 1024, dec.HALF_RECORD
+    rng = rc.philox(950 + heads + n)
+    k = heads * hd
+    wq = w8_rows(rng, n, k)
+    s = pow2_scales(n, k, 5)
+    deq = wq.astype(np.float64) * np.repeat(rc.bf16_values(s).astype(np.float64), 64, 1)
+    dw, ds = to_dev(wq, dev), to_dev(s, dev)
+    acc = rng.integers(-1, 2, size=(heads, 2, hd)) / 8.0
+    x0 = rc.bf16_normal(rng, (n,))
+    for pos in (0, 1, 511, 512, 513, 1023, 2000):
+        two = min(pos, max_seq - 1) >= 512
+        part = np.full((heads, 2, R), np.nan, np.float32)
+        part[:, 0, :hd] = acc[:, 0]
+        part[:, 0, hd], part[:, 0, hd + 1] = 0.0, 1.0
+        if two:
+            part[:, 1, :hd] = acc[:, 1]
+            part[:, 1, hd], part[:, 1, hd + 1] = 0.0, 0.0
+        attn = (acc[:, 0] + (acc[:, 1] if two else 0.0)).reshape(-1)
+        assert np.all(rc.bf16_values(bf16(attn)) == attn)  # exact in BF16 by design
+        terms = deq * attn[None, :]
+        assert np.all(np.abs(terms).sum(axis=1) * 2 ** 10 < 2 ** 24), "design not exact"
+        exp = rc.bf16_words(terms.sum(axis=1).astype(np.float32) + rc.bf16_values(x0))
+        x = to_dev(x0, dev)
+        dpos = torch.tensor([pos], dtype=torch.int32, device=dev)
+        dec.attention_halves_o_proj_w8a16(torch.from_numpy(part.reshape(-1)).to(dev), dpos, heads,
+                                          max_seq, dw, ds, x, n)
+        got = words(x)
+        bad = np.nonzero(got != exp)[0]
+        assert bad.size == 0, f"pos {pos}: {bad.size}/{n} rows differ, first {bad[0]}"
