@@ -37,6 +37,13 @@ Workloads (--workload):
   prefill.  One layer's 7 GEMMs at M = --tokens as one
       grouped launch; value = TFLOP/s.
 
+  ttft.  Config 4's model and prompt (--prompt tokens, seed 4, max_seq
+      1024): one step = reset + the whole prefill of the prompt (embedding,
+      24 layers with grouped MFMA GEMMs and the MFMA causal attention, final
+      RMSNorm, LM head and argmax) and the host readback of the first token,
+      timed on the host as the reference times TTFT.  value = median ms per
+      prefill.  For kernel traces of the model's prefill.
+
 Prints ONE JSON line.  All inputs are resident in HBM before timing.
 """
 from __future__ import annotations
@@ -73,10 +80,10 @@ def parse():
     ap.add_argument("--warmup", type=int, default=None,
                     help="untimed steps (default: e2e 2, else 20)")
     ap.add_argument("--launch", choices=("plan", "calls"), default="plan")
-    ap.add_argument("--workload", choices=("e2e", "gemv", "prefill"), default="e2e",
+    ap.add_argument("--workload", choices=("e2e", "gemv", "prefill", "ttft"), default="e2e",
                     help="e2e: config 4 decode (the headline); gemv: config 1; "
-                         "prefill: config 3 GEMMs")
-    ap.add_argument("--prompt", type=int, default=512, help="e2e prompt length")
+                         "prefill: config 3 GEMMs; ttft: config 4's prompt prefill")
+    ap.add_argument("--prompt", type=int, default=512, help="e2e and ttft prompt length")
     ap.add_argument("--decode-tokens", type=int, default=0,
                     help="e2e: decode steps per bench step (default: to context 1023, the "
                          "whole of config 4's decode; fewer for counter runs)")
@@ -94,9 +101,9 @@ def parse():
                     help="committed HBM traffic per launch measured with rocprofv3 --pmc")
     args = ap.parse_args()
     if args.steps is None:
-        args.steps = 10 if args.workload == "e2e" else 200
+        args.steps = {"e2e": 10, "ttft": 20}.get(args.workload, 200)
     if args.warmup is None:
-        args.warmup = 2 if args.workload == "e2e" else 20
+        args.warmup = {"e2e": 2, "ttft": 5}.get(args.workload, 20)
     return args
 
 
@@ -119,6 +126,11 @@ class Layers:
                 self.names.append((layer, name))
         torch.cuda.synchronize()
         self.bytes = sum(gemv_bytes(c[6], c[7]) for c in self.calls)
+
+
+def progress(msg: str) -> None:
+    """One line on stderr per long phase (stdout carries only the JSON line)."""
+    print(f"bench.py: {msg}", file=sys.stderr, flush=True)
 
 
 def time_steps(step, steps: int, warmup: int):
@@ -494,6 +506,7 @@ def e2e_detail(workdirs: dict, cfg, warmup: int = 5, repeat: int = 20) -> dict:
         res = {}
 
         def run(max_seq, prompt_len, new_tokens):
+            progress(f"detail {precision}: prompt {prompt_len} + {new_tokens}, max_seq {max_seq}")
             prompt = [int(v) for v in
                       np.random.default_rng(0).integers(0, cfg.vocab_size, prompt_len)]
             m = model_hip.Qwen2Model.open(wd, precision, max_sequence_length=max_seq)
@@ -625,14 +638,17 @@ def e2e_main(args, dev):
     workdirs = {p: tempfile.mkdtemp(prefix=f"qwen-{p}-") for p in ("w8a16", "w16a16")}
     try:
         t0 = time.perf_counter()
+        progress("random FP32 checkpoint (seed 4)")
         checkpoint = S.random_checkpoint(cfg, seed=4, std=0.02, plain_init=True)
         t1 = time.perf_counter()
+        progress("export to W8A16 QWENBIN1")
         report = export_model_dir(cfg, checkpoint, workdirs["w8a16"], "w8a16")
         t2 = time.perf_counter()
         if args.detail:
             export_model_dir(cfg, checkpoint, workdirs["w16a16"], "w16a16")
         del checkpoint
         t3 = time.perf_counter()
+        progress("open the model directory")
         model = model_hip.Qwen2Model.open(workdirs["w8a16"], "w8a16",
                                           max_sequence_length=max_seq, use_graph=graph)
         t4 = time.perf_counter()
@@ -647,6 +663,7 @@ def e2e_main(args, dev):
                   np.random.default_rng(4).integers(0, cfg.vocab_size, prompt_len)]
         torch.cuda.synchronize()
         t0 = time.perf_counter()
+        progress(f"prefill {prompt_len} tokens")
         first = model.prefill(prompt)
         ttft_ms = (time.perf_counter() - t0) * 1e3
         # One step = config 4's whole decode: back to the end of the prompt
@@ -657,6 +674,7 @@ def e2e_main(args, dev):
         def step():
             model.rewind(prompt_len, first)
             tokens.append(model.decode_steps(decode_len))
+        progress(f"{args.warmup} + {args.steps} decodes of {decode_len} tokens")
         for _ in range(args.warmup):
             step()
         torch.cuda.synchronize()
@@ -672,6 +690,7 @@ def e2e_main(args, dev):
         mid = prompt_len + decode_len // 2
         roofline = None
         if graph:
+            progress("per-kind launch timing")
             roofline = e2e_roofline(model, mid, ms_per_token, args.traffic)
         # Config 1 beside it: the 168 Linear GEMVs of a token as one grouped plan.
         import linear_hip as hip
@@ -692,10 +711,12 @@ def e2e_main(args, dev):
         del layers
         cpu = None
         if args.cpu_seconds > 0:
+            progress("CPU baseline sample")
             cpu = e2e_cpu_baseline(cfg, tensors, model, args.cpu_seconds)
         model.close()
         detail = None
         if args.detail:
+            progress("detail sweeps")
             detail = {"e2e": e2e_detail(workdirs, cfg), "linear_calls": linear_calls_detail(dev),
                       "lm_head": lm_head_detail(dev, hip), "torch_sum_read": torch_sum_read(dev)}
     finally:
@@ -744,6 +765,66 @@ def e2e_main(args, dev):
     return 0
 
 
+def ttft_main(args, dev) -> int:
+    """Config 4's prompt prefill on the HIP runtime, host-timed per prefill
+    (the reference's TTFT, docs/performance.md:44-52): the model is reset,
+    then Qwen2Model.prefill runs the prompt and reads back the first token."""
+    import shutil
+    import tempfile
+    import numpy as np
+    import model_hip
+    import synthetic as S
+    cfg = S.QWEN25_0_5B
+    max_seq = 1024
+    if not 1 <= args.prompt < max_seq:
+        print(f"bench.py: prompt {args.prompt} does not fit max_seq {max_seq}", file=sys.stderr)
+        return 2
+    workdir = tempfile.mkdtemp(prefix="qwen-w8a16-")
+    try:
+        checkpoint = S.random_checkpoint(cfg, seed=4, std=0.02, plain_init=True)
+        export_model_dir(cfg, checkpoint, workdir, "w8a16")
+        del checkpoint
+        model = model_hip.Qwen2Model.open(workdir, "w8a16", max_sequence_length=max_seq)
+        prompt = [int(v) for v in
+                  np.random.default_rng(4).integers(0, cfg.vocab_size, args.prompt)]
+        firsts, times = [], []
+        for i in range(args.warmup + args.steps):
+            model.reset()
+            t0 = time.perf_counter()
+            firsts.append(model.prefill(prompt))
+            if i >= args.warmup:
+                times.append((time.perf_counter() - t0) * 1e3)
+        model.close()
+    finally:
+        shutil.rmtree(workdir, ignore_errors=True)
+    if any(f != firsts[0] for f in firsts):
+        raise SystemExit("bench: repeated prefills of one prompt gave different tokens")
+    line = {
+        "metric": f"W8A16 prefill latency (TTFT) of a {args.prompt}-token prompt, "
+                  "Qwen2.5-0.5B b=1",
+        "value": round(float(np.median(times)), 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(float(np.mean(times)), 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "w8a16: int8 weights x bf16 activations, fp32 accumulate",
+        "data": "synthetic",
+        "config": {"workload": f"config 4's model (seed 4) and {args.prompt}-token prompt, "
+                               f"max_seq {max_seq}: reset + prefill + first-token readback",
+                   "prefill_ms": stats_of(times), "first_token": firsts[0],
+                   "prefill_tok_s": round(args.prompt / float(np.median(times)) * 1e3, 1),
+                   "parallelism": "single GPU"},
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line))
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -760,6 +841,8 @@ def main() -> int:
         return prefill_main(args, dev, hip)
     if args.workload == "e2e":
         return e2e_main(args, dev)
+    if args.workload == "ttft":
+        return ttft_main(args, dev)
     layers = Layers(dev)
     plan = hip.W8A16GemvPlan(layers.calls)
     assert abs(plan.bytes - layers.bytes) < 1, (plan.bytes, layers.bytes)
