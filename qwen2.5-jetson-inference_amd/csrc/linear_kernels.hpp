@@ -131,8 +131,10 @@ struct GemmGroupLaunch {
 // CUs.  The tile is 256 x 128 once every GEMM has 256 rows or more (with
 // `fill`, also only when the group has wide tiles for half the CUs), else
 // 64 x 64.  K is split so that no unit is much longer than the group's
-// shortest reduction (at least 8 stages); with `fill`, for a lone or long-K
-// group of one launch, into at most 4 parts of at least 14 stages instead.
+// shortest reduction (at least 8 stages), with parts lengthened until the
+// units fit the device at once (one per CU on the wide tile, two on 64 x 64);
+// with `fill`, for a lone or long-K group of one launch, into at most 4
+// parts of at least 14 stages instead.
 // Returns the tile; *blocks, *partial_floats and *counters receive the
 // launch size and its split-K scratch needs.
 int layout_gemm_group(GemmGroupDesc* descs, int count, int cus, bool fill, int* blocks,

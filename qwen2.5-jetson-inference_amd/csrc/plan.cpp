@@ -180,12 +180,20 @@ int layout_gemm_group(GemmGroupDesc* table, int count, int cus, bool fill, int* 
   // M = 128-512, down (76 stages) is fastest in 4 parts of 19 on 64 x 64
   // tiles (16.2 us at M = 512, 448 units), and 14-stage GEMMs gain nothing
   // from a split.
+  // A 64 x 64 plan likewise raises the part length until its units fit two
+  // per CU: at M = 128 a layer's 7 GEMMs (368 whole tiles) with down in 5
+  // parts of 16 (508 units) take 15.8 us against 18.5 us with 6 parts of 13
+  // (536 units, the last 24 in a second round).  Shorter parts lose: at
+  // M = 32, 2-4 stage parts of every GEMM take 19.4 us against 13.8 us,
+  // their in-kernel hand-offs costing more than the shorter chains save.
   int target = std::max(8, min_stages);
   if (fill) {
     target = std::min(max_stages, std::max(14, (max_stages + 3) / 4));
     while (target < max_stages && units_for(target) > 2ll * cus) ++target;
   } else if (tile == kGemmTile256x128) {
     while (target < max_stages && units_for(target) > cus) ++target;
+  } else {
+    while (target < max_stages && units_for(target) > 2ll * cus) ++target;
   }
   size_t pf = 0, cc = 0;
   for (int i = 0; i < count; ++i) {
