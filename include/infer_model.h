@@ -120,7 +120,8 @@ int infer_hip_model_reset(infer_hip_model* model);
 
 /* Qwen2Model::prefill (src/qwen2.cpp:716-734): tokens is host memory;
  * requires a fresh state; writes the argmax of the last token's logits to
- * *next_token (synchronizes). */
+ * *next_token (synchronizes).  A one-token prompt runs as the decode step
+ * at position 0 (the same launches as decode_next). */
 int infer_hip_model_prefill(infer_hip_model* model, const int* tokens, int count,
                             int* next_token);
 

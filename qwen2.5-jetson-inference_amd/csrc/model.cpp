@@ -532,6 +532,16 @@ int run_prefill(infer_hip_model* m, const int* tokens, int count, int* next) {
   const infer_hip_model_config& c = m->cfg;
   const int hidden = c.hidden_size, inter = c.intermediate_size;
   hipStream_t s = m->stream;
+  if (count == 1) {
+    // A one-token prompt is the decode step at position 0 (one graph
+    // replay, 5 launches per layer) rather than the M = 1 prefill (9 per
+    // layer): 0.5 ms instead of 1.0 ms for Qwen2.5-0.5B.
+    launch_set_state(m->state, tokens[0], 0, 0, rope_cursor(m), s);
+    int rc = check_launch("prefill state");
+    if (rc == INFER_HIP_OK) rc = run_decode_step(m);
+    if (rc == INFER_HIP_OK) rc = read_token(m, next);
+    return rc;
+  }
   hipError_t st = hipMemcpyAsync(m->prompt, tokens, sizeof(int) * count, hipMemcpyHostToDevice, s);
   if (st != hipSuccess) return hip_fail(st, "prefill token upload");
   launch_embedding(m->embed, m->prompt, count, c.vocab_size, hidden, m->px, s);
