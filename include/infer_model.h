@@ -178,6 +178,29 @@ int infer_hip_attention_prefill_bf16(const uint16_t* q, const uint16_t* key_cach
                                      int token_count, int num_heads, int num_kv_heads,
                                      int head_dim, int max_sequence_length, hipStream_t stream);
 
+/* gemm_w8a16 (include/infer/cuda_ops.hpp:51-55) for mlp.gate_proj and
+ * mlp.up_proj of one input, then silu_mul_bf16 (cuda_ops.hpp:100-101), as
+ * the prefill calls them (src/qwen2.cpp:560-568), in one launch:
+ *   output[t][n] = bf16(silu(g) * u),  g = bf16(input[t] . gate[n] + gate_bias[n]),
+ *                                      u = bf16(input[t] . up[n] + up_bias[n]),
+ * the unfused ops' roundings and SiLU-mul expression.  input [tokens][hidden],
+ * gate and up [intermediate][hidden] (W8A16: int8 with BF16 group-64 scales
+ * [intermediate][hidden / 64]), output [tokens][intermediate]; biases may be
+ * null.  256-token x 64-column tiles of both GEMMs on MFMA, built for prefills
+ * of 256 tokens or more (fewer tokens are computed correctly on partly empty
+ * tiles).  Needs hidden % 64 == 0 and 16-byte aligned weights and input.
+ * Stream-ordered, allocates nothing. */
+int infer_hip_gemm_gate_up_silu_w8a16(const int8_t* gate_weight, const uint16_t* gate_scales,
+                                      const uint16_t* gate_bias, const int8_t* up_weight,
+                                      const uint16_t* up_scales, const uint16_t* up_bias,
+                                      int group_size, const uint16_t* input, uint16_t* output,
+                                      int tokens, int intermediate, int hidden,
+                                      hipStream_t stream);
+int infer_hip_gemm_gate_up_silu_bf16(const uint16_t* gate_weight, const uint16_t* gate_bias,
+                                     const uint16_t* up_weight, const uint16_t* up_bias,
+                                     const uint16_t* input, uint16_t* output, int tokens,
+                                     int intermediate, int hidden, hipStream_t stream);
+
 /* The stream every kernel of the model runs on (infer::cuda::Context). */
 hipStream_t infer_hip_model_stream(const infer_hip_model* model);
 

@@ -535,9 +535,22 @@ __device__ __forceinline__ uint2 buffer_load8(__amdgpu_buffer_rsrc_t r, uint32_t
   return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, voffset, soffset, 0));
 }
 
+// The up_proj half of a gate|up pair tile (null w2: a plain tile).
+struct WidePair {
+  const void* w2 = nullptr;
+  const uint16_t* s2 = nullptr;
+  const uint16_t* bias2 = nullptr;
+};
+
+// A plain tile covers columns n0 .. n0 + 127 of Y.  A pair tile (pair.w2
+// set, a.n the pair's width) covers rows n0 .. n0 + 63 of a.w (gate) in
+// its columns 0-63 and the same rows of pair.w2 (up) in columns 64-127, and
+// writes columns n0 .. n0 + 63 of Y = bf16(silu(bf16(gate)) * bf16(up)),
+// the arithmetic of silu_mul_kernel on the two GEMMs' BF16 outputs.
 template <bool W8>
 __device__ __forceinline__ void gemm_wide_tile(const GemmArgs& a, int m0, int n0,
-                                               const SplitK& split = SplitK{}) {
+                                               const SplitK& split = SplitK{},
+                                               const WidePair& pair = WidePair{}) {
   constexpr int BM = kWideRows, BN = kWideCols, NT = kWideThreads, RS = kWideRowStride;
   constexpr int A_LD = BM * kRowChunks / NT;  // X chunks per thread per stage (4)
   constexpr int B_LD = BN * kRowChunks / NT;  // W chunks per thread per stage (2)
@@ -556,10 +569,19 @@ __device__ __forceinline__ void gemm_wide_tile(const GemmArgs& a, int m0, int n0
 
   // Branch-free buffer loads as in gemm_tile: rows past M or N read zero.
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, static_cast<uint32_t>(a.m) * a.k * 2u);
-  const __amdgpu_buffer_rsrc_t wr =
-      make_rsrc(a.w, static_cast<uint32_t>(a.n) * a.k * (W8 ? 1u : 2u));
+  const bool paired = pair.w2 != nullptr;
+  const uint32_t wbytes = static_cast<uint32_t>(a.n) * a.k * (W8 ? 1u : 2u);
+  const uint32_t sbytes = W8 ? static_cast<uint32_t>(a.n) * groups * 2u : 0u;
+  // W rows 0-63 of the tile come from wr, rows 64-127 from wr_hi: the same
+  // tensor 64 rows on for a plain tile, up_proj's same rows for a pair.
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, wbytes);
+  const __amdgpu_buffer_rsrc_t wr_hi = paired ? make_rsrc(pair.w2, wbytes) : wr;
+  // The scales of this wave's columns (wave-uniform: waves 4-7 hold
+  // columns 64-127).
+  const bool hi_wave = __builtin_amdgcn_readfirstlane(wn) == 1;
   const __amdgpu_buffer_rsrc_t sr =
-      make_rsrc(a.s, W8 ? static_cast<uint32_t>(a.n) * groups * 2u : 0u);
+      make_rsrc(paired && hi_wave ? pair.s2 : a.s, sbytes);
+  const int col0 = paired ? n0 : n0 + wn * 64;  // W row of this wave's first column
   uint32_t xoff[A_LD], woff[B_LD];
 #pragma unroll
   for (int i = 0; i < A_LD; ++i) {
@@ -568,14 +590,16 @@ __device__ __forceinline__ void gemm_wide_tile(const GemmArgs& a, int m0, int n0
   }
 #pragma unroll
   for (int i = 0; i < B_LD; ++i) {
-    const int c = tid + NT * i;
-    woff[i] = ((static_cast<uint32_t>(n0) + (c >> 3)) * a.k + (c & 7) * 8) * (W8 ? 1u : 2u);
+    const int c = tid + NT * i;  // W row (c >> 3) of the tile: 64 i .. 64 i + 63
+    const int row = paired ? n0 + (c >> 3) - 64 * i : n0 + (c >> 3);
+    woff[i] = ((static_cast<uint32_t>(row)) * a.k + (c & 7) * 8) * (W8 ? 1u : 2u);
   }
+  static_assert(B_LD == 2, "W rows 0-63 and 64-127 of the tile: one load each");
   // W8: scale rows of this lane's two output columns
   uint32_t soff[2];
 #pragma unroll
   for (int fn = 0; fn < 2; ++fn)
-    soff[fn] = (static_cast<uint32_t>(n0 + wn * 64 + fn * 32 + r) * groups) * 2u;
+    soff[fn] = (static_cast<uint32_t>(col0 + fn * 32 + r) * groups) * 2u;
   const int fa_base[2] = {(wm * 64 + r) * RS + 4 * h, (wm * 64 + 32 + r) * RS + 4 * h};
   const int fb_base[2] = {(wn * 64 + r) * RS + 4 * h, (wn * 64 + 32 + r) * RS + 4 * h};
 
@@ -593,9 +617,9 @@ __device__ __forceinline__ void gemm_wide_tile(const GemmArgs& a, int m0, int n0
 #pragma unroll
     for (int i = 0; i < B_LD; ++i) {
       if (W8) {
-        d.q[i] = buffer_load8(wr, woff[i], gc * kStageK);
+        d.q[i] = buffer_load8(i == 0 ? wr : wr_hi, woff[i], gc * kStageK);
       } else {
-        d.b[i] = buffer_load16(wr, woff[i], gc * kStageK * 2u);
+        d.b[i] = buffer_load16(i == 0 ? wr : wr_hi, woff[i], gc * kStageK * 2u);
       }
     }
   };
@@ -730,6 +754,57 @@ __device__ __forceinline__ void gemm_wide_tile(const GemmArgs& a, int m0, int n0
   __syncthreads();
   constexpr int kChunksPerRow = BN / 8;
   constexpr int kChunks = BM * kChunksPerRow / NT;  // 8 per thread
+  if (paired) {
+    // 64 output columns: gate in tile columns 0-63, up in 64-127.  Each
+    // thread takes 8 consecutive columns of 4 rows.  (Pair tiles are never
+    // split over K.)
+    constexpr int kPairPerRow = 64 / 8;
+    constexpr int kPairChunks = BM * kPairPerRow / NT;  // 4 per thread
+    const int col = (tid % kPairPerRow) * 8;
+    const int n = n0 + col;
+    float bg[8], bu[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const bool in = n + j < a.n;
+      bg[j] = (a.bias && in) ? bf16_to_f32(gload(a.bias + n + j)) : 0.0f;
+      bu[j] = (pair.bias2 && in) ? bf16_to_f32(gload(pair.bias2 + n + j)) : 0.0f;
+    }
+    const bool vec = (a.n % 8) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15u) == 0;
+#pragma unroll
+    for (int i = 0; i < kPairChunks; ++i) {
+      const int row = (tid + NT * i) / kPairPerRow;
+      const int m = m0 + row;
+      if (m >= a.m || n >= a.n) continue;
+      const int idx = row * (kWideEpStride / 4) + col / 4;
+      const uint4 g0 = lds_raw[idx], g1 = lds_raw[idx + 1];
+      const uint4 u0 = lds_raw[idx + 16], u1 = lds_raw[idx + 17];  // 64 columns on
+      const float gf[8] = {__uint_as_float(g0.x), __uint_as_float(g0.y), __uint_as_float(g0.z),
+                           __uint_as_float(g0.w), __uint_as_float(g1.x), __uint_as_float(g1.y),
+                           __uint_as_float(g1.z), __uint_as_float(g1.w)};
+      const float uf[8] = {__uint_as_float(u0.x), __uint_as_float(u0.y), __uint_as_float(u0.z),
+                           __uint_as_float(u0.w), __uint_as_float(u1.x), __uint_as_float(u1.y),
+                           __uint_as_float(u1.z), __uint_as_float(u1.w)};
+      float o[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        // the two GEMMs' BF16 outputs, then silu_mul_kernel's expression
+        const float g = bf16_to_f32(f32_to_bf16(gf[j] + bg[j]));
+        const float u = bf16_to_f32(f32_to_bf16(uf[j] + bu[j]));
+        o[j] = g / (1.0f + expf(-g)) * u;
+      }
+      uint16_t* dst = a.y + static_cast<size_t>(m) * a.n + n;
+      if (vec) {
+        store_nt16(dst, u32x4{pack2_bf16(o[0], o[1]), pack2_bf16(o[2], o[3]),
+                              pack2_bf16(o[4], o[5]), pack2_bf16(o[6], o[7])});
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (n + j < a.n) gstore(dst + j, f32_to_bf16(o[j]));
+        }
+      }
+    }
+    return;
+  }
   if (split.parts > 1) {
     // One part of a tile split over K: its FP32 tile, row-major, for the
     // plan's reduction launch (the launch boundary orders these stores
@@ -799,6 +874,13 @@ __global__ __launch_bounds__(kWideThreads) void gemm_wide_kernel(GemmArgs a) {
 template <bool W8>
 __device__ __forceinline__ void gemm_wide_unit(const GemmGroupDesc& d, int u) {
   const int tile = u / d.splits;
+  if (d.w2) {
+    // A gate|up pair: d.n counts both halves; each tile 64 columns of each.
+    const GemmArgs a{d.w, d.s, d.bias, d.x, d.y, d.m, d.n / 2, d.k};
+    gemm_wide_tile<W8>(a, (tile % d.tiles_m) * kWideRows, (tile / d.tiles_m) * (kWideCols / 2),
+                       SplitK{}, WidePair{d.w2, d.s2, d.bias2});
+    return;
+  }
   const GemmArgs a{d.w, d.s, d.bias, d.x, d.y, d.m, d.n, d.k};
   SplitK sp;
   if (d.splits > 1) {
@@ -1080,6 +1162,28 @@ void launch_gemm_group_inline(const GemmGroupLaunch& l, hipStream_t stream) {
   }
 }
 
+bool gate_up_silu_supported(const void* gate_w, const void* up_w, const uint16_t* x, int m,
+                            int inter, int hidden) {
+  return m > 0 && inter > 0 && gemm_mfma_supported(gate_w, x, m, inter, hidden) &&
+         gemm_mfma_supported(up_w, x, m, inter, hidden);
+}
+
+void launch_gate_up_silu(bool w8, const void* gate_w, const uint16_t* gate_s,
+                         const uint16_t* gate_b, const void* up_w, const uint16_t* up_s,
+                         const uint16_t* up_b, const uint16_t* x, uint16_t* y, int m, int inter,
+                         int hidden, hipStream_t stream) {
+  GemmGroupLaunch l{};
+  GemmGroupDesc& d = l.g.d[0];
+  d = GemmGroupDesc{gate_w, gate_s, gate_b, x, y, m, 2 * inter, hidden, 0, 0, 1, hidden / kStageK,
+                    nullptr, nullptr, up_w, up_s, up_b};
+  d.tiles_m = (m + kWideRows - 1) / kWideRows;
+  l.g.count = 1;
+  l.w8 = w8;
+  l.tile = kGemmTile256x128;
+  l.blocks = d.tiles_m * ((inter + kWideCols / 2 - 1) / (kWideCols / 2));
+  launch_gemm_group_inline(l, stream);
+}
+
 void launch_gemm_mfma(int tile, bool w8, const GemmArgs& a, hipStream_t stream) {
   if (w8) {
     launch_config<true>(tile, a, stream);
@@ -1151,7 +1255,53 @@ int gemm_bf16_impl(const uint16_t* weight, const uint16_t* bias, const uint16_t*
   return check_launch("gemm_bf16");
 }
 
+int gate_up_silu_impl(bool w8, const void* gate_w, const uint16_t* gate_s,
+                      const uint16_t* gate_b, const void* up_w, const uint16_t* up_s,
+                      const uint16_t* up_b, int group_size, const uint16_t* input,
+                      uint16_t* output, int tokens, int inter, int hidden, hipStream_t stream) {
+  const char* what = w8 ? "gemm_gate_up_silu_w8a16" : "gemm_gate_up_silu_bf16";
+  if (w8 && group_size != 64) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "w8a16 group size must be 64 (got %d)", group_size);
+  }
+  if (tokens <= 0 || inter <= 0 || hidden <= 0) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: bad shape M=%d intermediate=%d hidden=%d", what,
+                tokens, inter, hidden);
+  }
+  if (!gate_w || !up_w || !input || !output || (w8 && (!gate_s || !up_s))) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: null required pointer", what);
+  }
+  if (!gate_up_silu_supported(gate_w, up_w, input, tokens, inter, hidden)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "%s: needs hidden %% 64 == 0, 16-byte aligned weights and input, and operands "
+                "under 2 GiB",
+                what);
+  }
+  launch_gate_up_silu(w8, gate_w, gate_s, gate_b, up_w, up_s, up_b, input, output, tokens, inter,
+                      hidden, stream);
+  return check_launch(what);
+}
+
 }  // namespace
+
+extern "C" int infer_hip_gemm_gate_up_silu_w8a16(
+    const int8_t* gate_weight, const uint16_t* gate_scales, const uint16_t* gate_bias,
+    const int8_t* up_weight, const uint16_t* up_scales, const uint16_t* up_bias, int group_size,
+    const uint16_t* input, uint16_t* output, int tokens, int intermediate, int hidden,
+    hipStream_t stream) {
+  return gate_up_silu_impl(true, gate_weight, gate_scales, gate_bias, up_weight, up_scales,
+                           up_bias, group_size, input, output, tokens, intermediate, hidden,
+                           stream);
+}
+
+extern "C" int infer_hip_gemm_gate_up_silu_bf16(const uint16_t* gate_weight,
+                                                const uint16_t* gate_bias,
+                                                const uint16_t* up_weight,
+                                                const uint16_t* up_bias, const uint16_t* input,
+                                                uint16_t* output, int tokens, int intermediate,
+                                                int hidden, hipStream_t stream) {
+  return gate_up_silu_impl(false, gate_weight, nullptr, gate_bias, up_weight, nullptr, up_bias,
+                           64, input, output, tokens, intermediate, hidden, stream);
+}
 
 extern "C" int infer_hip_gemm_w8a16(const int8_t* weight, const uint16_t* scales,
                                     int group_size, const uint16_t* bias,

@@ -85,6 +85,13 @@ struct GemmGroupDesc {
   int split_stages;
   float* partial;
   int* counters;
+  // A gate|up pair (wide tile only, never split): w, s, bias are gate_proj,
+  // w2, s2, bias2 up_proj, both [n / 2, k]; each 256 x 128 tile computes
+  // 64 columns of both and writes y[:, 64 t ..] = bf16(silu(bf16(gate)) *
+  // bf16(up)), y being [m, n / 2].  Null w2: a plain GEMM.
+  const void* w2 = nullptr;
+  const uint16_t* s2 = nullptr;
+  const uint16_t* bias2 = nullptr;
 };
 // Split-K in the wide-tile grouped launch.  A GEMM whose wide tiles are
 // split over K in `parts` parts writes each part's FP32 tile, row-major
@@ -146,6 +153,17 @@ int layout_gemm_group(GemmGroupDesc* descs, int count, int cus, bool fill, int* 
 int bind_gemm_group(GemmGroupDesc* descs, int count, int tile, float* partial, int* counters,
                     SplitReduceDesc* reduce, int* reducers);
 void launch_gemm_group_inline(const GemmGroupLaunch& l, hipStream_t stream);
+
+// gemm.hip: gate_proj and up_proj of the same input, then SiLU-mul, as one
+// launch of gate|up pair tiles (256 x 128 tiles, 64 columns of each; never
+// split): y[m, n] = bf16(silu(bf16(x gate^T + gate_b)) * bf16(x up^T +
+// up_b)), y [m, inter].  Supported when both GEMMs take the MFMA path.
+bool gate_up_silu_supported(const void* gate_w, const void* up_w, const uint16_t* x, int m,
+                            int inter, int hidden);
+void launch_gate_up_silu(bool w8, const void* gate_w, const uint16_t* gate_s,
+                         const uint16_t* gate_b, const void* up_w, const uint16_t* up_s,
+                         const uint16_t* up_b, const uint16_t* x, uint16_t* y, int m, int inter,
+                         int hidden, hipStream_t stream);
 
 // The wide-tile grouped launch (`units` blocks over descs) and, when some
 // GEMM is split, its reduction launch (`reducers` blocks over rdescs).

@@ -246,6 +246,25 @@ void linear_group(const infer_hip_model* m, const GemmItem* items, int count, in
   launch_gemm_group_inline(g, m->stream);
 }
 
+// gate|up + SiLU-mul of the prefill as one launch of pair tiles: where the
+// two GEMMs' own grouped launch would take the wide tile unsplit (prompts
+// over 256 tokens at the Qwen2.5-0.5B shapes), so the same tiles also
+// write the SiLU-mul instead of two BF16 outputs and a third launch.
+bool fuse_gate_up(const infer_hip_model* m, const Layer& L, int tokens) {
+  if (!gate_up_silu_supported(L.gate.w, L.up.w, m->pnorm, tokens, L.gate.n, L.gate.k)) {
+    return false;
+  }
+  GemmGroupDesc d[2] = {
+      {L.gate.w, L.gate.s, L.gate.b, m->pnorm, m->pgate, tokens, L.gate.n, L.gate.k, 0, 0, 1,
+       L.gate.k / 64, nullptr, nullptr},
+      {L.up.w, L.up.s, L.up.b, m->pnorm, m->pup, tokens, L.up.n, L.up.k, 0, 0, 1, L.up.k / 64,
+       nullptr, nullptr}};
+  int blocks = 0;
+  size_t pf = 0, cc = 0;
+  const int tile = layout_gemm_group(d, 2, m->cus, true, &blocks, &pf, &cc);
+  return tile == kGemmTile256x128 && d[0].splits == 1 && d[1].splits == 1;
+}
+
 // The split-K scratch the prefill's groups (q|k|v, o, gate|up, down) need at
 // any prompt length up to max_seq.
 void prefill_scratch_needs(const infer_hip_model_config& c, int head_dim, int max_seq, int cus,
@@ -561,9 +580,14 @@ int run_prefill(infer_hip_model* m, const int* tokens, int count, int* next) {
     const GemmItem o[1] = {{&L.o, m->pattn, m->ptmp}};
     linear_group(m, o, 1, count);
     launch_add_rms_norm(m->px, m->ptmp, L.post_norm, m->pnorm, count, hidden, c.rms_norm_eps, s);
-    const GemmItem gate_up[2] = {{&L.gate, m->pnorm, m->pgate}, {&L.up, m->pnorm, m->pup}};
-    linear_group(m, gate_up, 2, count);
-    launch_silu_mul(m->pgate, m->pup, m->pmlp, static_cast<long long>(count) * inter, s);
+    if (fuse_gate_up(m, L, count)) {
+      launch_gate_up_silu(m->w8, L.gate.w, L.gate.s, L.gate.b, L.up.w, L.up.s, L.up.b, m->pnorm,
+                          m->pmlp, count, inter, hidden, s);
+    } else {
+      const GemmItem gate_up[2] = {{&L.gate, m->pnorm, m->pgate}, {&L.up, m->pnorm, m->pup}};
+      linear_group(m, gate_up, 2, count);
+      launch_silu_mul(m->pgate, m->pup, m->pmlp, static_cast<long long>(count) * inter, s);
+    }
     const GemmItem down[1] = {{&L.down, m->pmlp, m->ptmp}};
     linear_group(m, down, 1, count);
     if (l + 1 < m->layers.size()) {

@@ -43,6 +43,8 @@ EXPORTED_SYMBOLS = (
     "infer_hip_model_kernel_times",
     "infer_hip_model_kernel_name",
     "infer_hip_attention_prefill_bf16",
+    "infer_hip_gemm_gate_up_silu_w8a16",
+    "infer_hip_gemm_gate_up_silu_bf16",
 )
 KERNEL_KINDS = 9
 
@@ -127,6 +129,8 @@ def load():
                                           ctypes.POINTER(ctypes.c_double), ip, i], i),
         "infer_hip_model_kernel_name": ([i], ctypes.c_char_p),
         "infer_hip_attention_prefill_bf16": ([p, p, p, p, i, i, i, i, i, p], i),
+        "infer_hip_gemm_gate_up_silu_w8a16": ([p, p, p, p, p, p, i, p, p, i, i, i, p], i),
+        "infer_hip_gemm_gate_up_silu_bf16": ([p, p, p, p, p, p, i, i, i, p], i),
         "infer_hip_model_open": ([ctypes.c_char_p, ctypes.POINTER(_Options), ctypes.POINTER(p)],
                                  i),
     }
@@ -148,6 +152,28 @@ def attention_prefill_bf16(q, key_cache, value_cache, output, token_count: int,
         linear_hip._ptr(q), linear_hip._ptr(key_cache), linear_hip._ptr(value_cache),
         linear_hip._ptr(output), token_count, num_heads, num_kv_heads, head_dim,
         max_sequence_length, linear_hip._stream(stream)))
+
+
+def gemm_gate_up_silu_w8a16(gate_w, gate_s, gate_b, up_w, up_s, up_b, group_size: int,
+                            x, y, tokens: int, intermediate: int, hidden: int,
+                            stream=None) -> None:
+    """gate_proj and up_proj of x, then SiLU-mul, in one launch
+    (infer_hip_gemm_gate_up_silu_w8a16); biases may be None."""
+    lib = load()
+    P = linear_hip._ptr
+    _check(lib.infer_hip_gemm_gate_up_silu_w8a16(
+        P(gate_w), P(gate_s), P(gate_b), P(up_w), P(up_s), P(up_b), group_size, P(x), P(y),
+        tokens, intermediate, hidden, linear_hip._stream(stream)))
+
+
+def gemm_gate_up_silu_bf16(gate_w, gate_b, up_w, up_b, x, y, tokens: int, intermediate: int,
+                           hidden: int, stream=None) -> None:
+    """The BF16-weight form of gemm_gate_up_silu_w8a16."""
+    lib = load()
+    P = linear_hip._ptr
+    _check(lib.infer_hip_gemm_gate_up_silu_bf16(
+        P(gate_w), P(gate_b), P(up_w), P(up_b), P(x), P(y), tokens, intermediate, hidden,
+        linear_hip._stream(stream)))
 
 
 def _dtype_name(t) -> str:

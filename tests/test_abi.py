@@ -318,3 +318,37 @@ def test_halves_attention_ops_reject_bad_arguments(hip):
     assert g(4100, 4096, 14, 1024, 4096, 4096, 4096, 896, None) == bad   # records aligned
     assert g(4096, 4096, 14, 1024, 4104, 4096, 4096, 896, None) == bad   # weight aligned
     assert g(4096, None, 14, 1024, 4096, 4096, 4096, 896, None) == bad
+
+
+def test_gate_up_silu_rejects_bad_arguments(hip):
+    """infer_hip_gemm_gate_up_silu_*: the group size, shapes, null pointers,
+    K % 64 and alignment are checked on the host; nothing is launched."""
+    import model_hip
+    a = 256  # a 16-byte aligned stand-in address (never dereferenced)
+
+    def w8(**kw):
+        args = dict(gate_w=a, gate_s=a, gate_b=None, up_w=a, up_s=a, up_b=None, group_size=64,
+                    x=a, y=a, tokens=4, intermediate=128, hidden=128)
+        args.update(kw)
+        model_hip.gemm_gate_up_silu_w8a16(**args, stream=0)
+
+    def bf16(**kw):
+        args = dict(gate_w=a, gate_b=None, up_w=a, up_b=None, x=a, y=a, tokens=4,
+                    intermediate=128, hidden=128)
+        args.update(kw)
+        model_hip.gemm_gate_up_silu_bf16(**args, stream=0)
+
+    cases = [(w8, dict(group_size=32), "group size must be 64"),
+             (w8, dict(tokens=0), "bad shape"), (w8, dict(intermediate=-1), "bad shape"),
+             (w8, dict(hidden=0), "bad shape"), (w8, dict(gate_s=None), "null"),
+             (w8, dict(up_w=None), "null"), (w8, dict(y=None), "null"),
+             (w8, dict(hidden=96), "hidden % 64"), (w8, dict(up_w=a + 8), "aligned"),
+             (w8, dict(x=a + 2), "aligned"),
+             (w8, dict(tokens=1 << 21, hidden=1024), "2 GiB"),
+             (bf16, dict(tokens=-3), "bad shape"), (bf16, dict(gate_w=None), "null"),
+             (bf16, dict(hidden=100), "hidden % 64"), (bf16, dict(gate_w=a + 4), "aligned")]
+    for fn, kw, text in cases:
+        with pytest.raises(hip.InferError) as err:
+            fn(**kw)
+        assert err.value.status == hip.INVALID_ARGUMENT, kw
+        assert text in str(err.value), (kw, str(err.value))
