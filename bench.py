@@ -574,27 +574,40 @@ def linear_calls_detail(dev) -> dict:
                        (False, True): hip.gemv_bf16, (False, False): hip.gemm_bf16}
                       [(w8, m == 1)])
                 per_graph = 24
-                for i in range(layers):  # eager once: argument checks, warm caches
-                    fn(*calls[i])
-                torch.cuda.synchronize()
-                graph = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(graph):
-                    for i in range(per_graph):
-                        fn(*calls[i % layers])
 
-                def one(ev, graph=graph):
-                    graph.replay()
-                t, _ = time_steps(one, 10, 3)
-                us = t / (10 * per_graph) * 1e3
-                del graph
+                def timed(fn, calls):
+                    for i in range(layers):  # eager once: argument checks, warm caches
+                        fn(*calls[i])
+                    torch.cuda.synchronize()
+                    graph = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(graph):
+                        for i in range(per_graph):
+                            fn(*calls[i % layers])
+
+                    def one(ev, graph=graph):
+                        graph.replay()
+                    t, _ = time_steps(one, 10, 3)
+                    return t / (10 * per_graph) * 1e3
+
+                def cell_of(us):
+                    if m == 1:
+                        nbytes = (gemv_bytes(n, k) if w8 else 2 * n * k + 2 * k + 2 * n)
+                        return {"us_per_call": round(us, 2),
+                                "GBs": round(nbytes / (us * 1e-6) / 1e9, 1)}
+                    return {"us_per_call": round(us, 2),
+                            "TFLOPs": round(2.0 * m * n * k / (us * 1e-6) / 1e12, 2)}
+                us = timed(fn, calls)
                 total_us += us
-                cell = {"us_per_call": round(us, 2)}
-                if m == 1:
-                    nbytes = (gemv_bytes(n, k) if w8 else 2 * n * k + 2 * k + 2 * n)
-                    cell["GBs"] = round(nbytes / (us * 1e-6) / 1e9, 1)
-                else:
-                    cell["TFLOPs"] = round(2.0 * m * n * k / (us * 1e-6) / 1e12, 2)
-                per[name] = cell
+                per[name] = cell_of(us)
+                # A Linear whose lone call splits K with a workspace
+                # (infer_hip_gemm_*_ws): the same call on a zeroed workspace.
+                need = hip.gemm_workspace_bytes(m, n, k) if m > 1 else 0
+                if need:
+                    ws = torch.zeros(need // 4 + 1, dtype=torch.int32, device=dev)
+                    wfn = hip.gemm_w8a16_ws if w8 else hip.gemm_bf16_ws
+                    per[name + "_with_workspace"] = cell_of(
+                        timed(wfn, [c + (ws,) for c in calls]))
+                    del ws
             out[f"{'w8a16' if w8 else 'bf16'}_M{m}"] = {"per_shape": per,
                                                         "layer_us": round(total_us, 2)}
     return out

@@ -7,6 +7,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <vector>
 
@@ -58,6 +59,51 @@ inline void linear_batch(const LinearWeight& w, const uint16_t* input, uint16_t*
   } else if (w.dtype == DType::kBFloat16) {
     gemm_bf16(static_cast<const uint16_t*>(w.weight), w.bias, input, output, token_count,
               w.out_features, w.in_features, stream);
+  } else {
+    throw Error("batched BF16 linear requires BF16 or INT8 weights");
+  }
+}
+
+// Split-K scratch for linear_batch on lone long-K Linears (down_proj),
+// sized at set-up for every token count up to max_tokens and every weight
+// it will serve (the sum of their sizes); zeroed once.  The token loop
+// allocates nothing.
+class GemmWorkspace {
+ public:
+  GemmWorkspace(int max_tokens, const std::vector<const LinearWeight*>& weights) {
+    for (const LinearWeight* w : weights) {
+      bytes_ += gemm_workspace_bytes(max_tokens, w->out_features, w->in_features);
+    }
+    if (bytes_ > 0) {
+      check_hip(hipMalloc(&data_, bytes_), "hipMalloc");
+      check_hip(hipMemset(data_, 0, bytes_), "hipMemset");
+    }
+  }
+  ~GemmWorkspace() {
+    if (data_) (void)hipFree(data_);
+  }
+  GemmWorkspace(const GemmWorkspace&) = delete;
+  GemmWorkspace& operator=(const GemmWorkspace&) = delete;
+  void* data() const { return data_; }
+  size_t bytes() const { return bytes_; }
+
+ private:
+  void* data_{nullptr};
+  size_t bytes_{0};
+};
+
+// linear_batch with a workspace: the same computation, with long-K
+// Linears split over K (calls sharing the workspace must not overlap).
+inline void linear_batch(const LinearWeight& w, const uint16_t* input, uint16_t* output,
+                         int token_count, const GemmWorkspace& ws, hipStream_t stream) {
+  if (w.dtype == DType::kInt8) {
+    if (!w.scales) throw Error("W8A16 tensor lacks quantization metadata");
+    gemm_w8a16(static_cast<const int8_t*>(w.weight), w.scales, w.group_size, w.bias, input,
+               output, token_count, w.out_features, w.in_features, ws.data(), ws.bytes(),
+               stream);
+  } else if (w.dtype == DType::kBFloat16) {
+    gemm_bf16(static_cast<const uint16_t*>(w.weight), w.bias, input, output, token_count,
+              w.out_features, w.in_features, ws.data(), ws.bytes(), stream);
   } else {
     throw Error("batched BF16 linear requires BF16 or INT8 weights");
   }

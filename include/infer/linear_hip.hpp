@@ -102,6 +102,25 @@ inline void gemm_w8a16(const int8_t* weight, const uint16_t* scales, int group_s
                              out_features, in_features, stream));
 }
 
+// gemm_w8a16 / gemm_bf16 with a caller workspace (infer_hip_gemm_*_ws): a
+// lone long-K call splits K over the idle CUs.  No reference counterpart.
+inline size_t gemm_workspace_bytes(int max_tokens, int out_features, int in_features) {
+  return infer_hip_gemm_workspace_bytes(max_tokens, out_features, in_features);
+}
+inline void gemm_w8a16(const int8_t* weight, const uint16_t* scales, int group_size,
+                       const uint16_t* bias, const uint16_t* input, uint16_t* output,
+                       int tokens, int out_features, int in_features, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream) {
+  check(infer_hip_gemm_w8a16_ws(weight, scales, group_size, bias, input, output, tokens,
+                                out_features, in_features, workspace, workspace_bytes, stream));
+}
+inline void gemm_bf16(const uint16_t* weight, const uint16_t* bias, const uint16_t* input,
+                      uint16_t* output, int tokens, int out_features, int in_features,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  check(infer_hip_gemm_bf16_ws(weight, bias, input, output, tokens, out_features, in_features,
+                               workspace, workspace_bytes, stream));
+}
+
 // A grouped W8A16 GEMV plan (RAII): many independent gemv_w8a16 calls in
 // one launch, resolved once.  No single reference counterpart.
 class W8A16GemvPlan {

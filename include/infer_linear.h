@@ -147,6 +147,33 @@ int infer_hip_gemm_bf16_tile(const uint16_t* weight, const uint16_t* bias,
                              int out_features, int in_features, int tile,
                              hipStream_t stream);
 
+/* ---- Lone GEMMs with a caller workspace ---------------------------------
+ * No reference counterpart: for a caller that keeps the reference's
+ * one-call-per-Linear prefill (src/qwen2.cpp:300-330) and can hold a
+ * workspace, as Qwen2Model holds its LM-head scratch (qwen2.cpp:191-199).
+ * The same computation as infer_hip_gemm_w8a16 / infer_hip_gemm_bf16; a
+ * GEMM whose lone launch would leave CUs idle on a long K (down_proj,
+ * K = 4864, at tokens <= 512) is split over K in up to 4 parts whose FP32
+ * partial tiles go to the workspace and are summed in part order.
+ *
+ * infer_hip_gemm_workspace_bytes: bytes that cover every token count from 2
+ * to max_tokens for this [out_features, in_features] weight on the current
+ * device (0: no such call splits); a workspace shared by several weights
+ * needs the sum of theirs.  The workspace (device memory, 16-byte aligned)
+ * must be zeroed once before its first use; every call leaves it ready for
+ * the next (its arrival counters sit at fixed places and return to zero).
+ * Calls that share a workspace must not overlap (one stream, or ordered
+ * across streams).  A workspace smaller than a call needs is rejected
+ * (status 1); null with 0 bytes is accepted for calls that do not split. */
+size_t infer_hip_gemm_workspace_bytes(int max_tokens, int out_features, int in_features);
+int infer_hip_gemm_w8a16_ws(const int8_t* weight, const uint16_t* scales, int group_size,
+                            const uint16_t* bias, const uint16_t* input, uint16_t* output,
+                            int tokens, int out_features, int in_features, void* workspace,
+                            size_t workspace_bytes, hipStream_t stream);
+int infer_hip_gemm_bf16_ws(const uint16_t* weight, const uint16_t* bias, const uint16_t* input,
+                           uint16_t* output, int tokens, int out_features, int in_features,
+                           void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* ---- Grouped W8A16 GEMV plans ------------------------------------------
  * No single reference counterpart: a plan is the multi-matrix form of
  * infer_hip_gemv_w8a16 for GEMVs that are independent of each other, such

@@ -34,6 +34,8 @@
 // dispatch sends them to linear_w8a16_kernel (1324-1387).
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "device_common.hpp"
 #include "linear_kernels.hpp"
 #include "status.hpp"
@@ -1200,9 +1202,95 @@ using namespace qlin;
 
 namespace {
 
+// ---- lone GEMMs with a caller workspace ----
+// The layout of a lone call: the one-GEMM group of the prefill's inline
+// launches (layout_gemm_group with fill), so its split rule is theirs.  In
+// the workspace the split tiles' arrival counters start at its beginning,
+// counter t at int t, and the FP32 partial tiles end (256-byte aligned) at
+// its end.  So counter t has one address for every call on the workspace,
+// and as long as the workspace covers the largest partials plus the most
+// counters of the calls made on it (what infer_hip_gemm_workspace_bytes
+// returns), no call's partials overwrite a counter, which every call
+// leaves at zero.
+struct LoneLayout {
+  GemmGroupLaunch l{};
+  size_t partial_bytes = 0;  // 0: no split
+  size_t counter_bytes = 0;
+};
+
+size_t round256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
+
+int current_cus(int* cus) {
+  int device = 0;
+  hipError_t st = hipGetDevice(&device);
+  if (st == hipSuccess) {
+    st = hipDeviceGetAttribute(cus, hipDeviceAttributeMultiprocessorCount, device);
+  }
+  if (st != hipSuccess || *cus <= 0) {
+    (void)hipGetLastError();
+    return fail(INFER_HIP_RUNTIME_ERROR, "gemm workspace: no device to lay the call out for");
+  }
+  return INFER_HIP_OK;
+}
+
+LoneLayout lone_layout(bool w8, const void* w, const uint16_t* s, const uint16_t* bias,
+                       const uint16_t* x, uint16_t* y, int m, int n, int k, int cus) {
+  LoneLayout o;
+  GemmGroupDesc& d = o.l.g.d[0];
+  d = GemmGroupDesc{w, s, bias, x, y, m, n, k, 0, 0, 1, k / kStageK, nullptr, nullptr};
+  size_t pf = 0, cc = 0;
+  o.l.tile = layout_gemm_group(&d, 1, cus, true, &o.l.blocks, &pf, &cc);
+  o.l.g.count = 1;
+  o.l.w8 = w8;
+  if (d.splits > 1) {
+    o.partial_bytes = round256(pf * sizeof(float));
+    o.counter_bytes = round256(cc * sizeof(int));
+  }
+  return o;
+}
+
+// Runs a lone call split over K on the workspace; *done is false when the
+// call does not split (the caller then takes the plain path).
+int launch_lone_split(bool w8, const void* w, const uint16_t* s, const uint16_t* bias,
+                      const uint16_t* x, uint16_t* y, int m, int n, int k, void* ws,
+                      size_t ws_bytes, hipStream_t stream, bool* done) {
+  *done = false;
+  int cus = 0;
+  const int rc = current_cus(&cus);
+  if (rc != INFER_HIP_OK) return rc;
+  LoneLayout o = lone_layout(w8, w, s, bias, x, y, m, n, k, cus);
+  if (o.partial_bytes == 0 || o.l.blocks <= 0) return INFER_HIP_OK;
+  if (!ws) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "gemm: this call splits K and needs a workspace of %zu bytes (none given)",
+                o.partial_bytes + o.counter_bytes + 256);
+  }
+  if (!aligned16(ws)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "gemm: the workspace must be 16-byte aligned");
+  }
+  const uintptr_t begin = reinterpret_cast<uintptr_t>(ws);
+  const uintptr_t end = begin + ws_bytes;
+  const uintptr_t pbase =
+      ws_bytes >= o.partial_bytes ? (end - o.partial_bytes) & ~static_cast<uintptr_t>(255) : 0;
+  if (ws_bytes < o.partial_bytes || pbase < begin + o.counter_bytes) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "gemm: this call splits K and needs a workspace of %zu bytes (%zu given)",
+                o.partial_bytes + o.counter_bytes + 256, ws_bytes);
+  }
+  int* counters = static_cast<int*>(ws);
+  float* partial = reinterpret_cast<float*>(pbase);
+  o.l.r.count = bind_gemm_group(o.l.g.d, 1, o.l.tile, partial, counters, o.l.r.d,
+                                &o.l.reducers);
+  launch_gemm_group_inline(o.l, stream);
+  *done = true;
+  return INFER_HIP_OK;
+}
+
+// ws_mode: the caller passed a workspace (the _ws entry points).
 int gemm_w8a16_impl(const int8_t* weight, const uint16_t* scales, int group_size,
                     const uint16_t* bias, const uint16_t* input, uint16_t* output, int tokens,
-                    int out_features, int in_features, int tile, hipStream_t stream) {
+                    int out_features, int in_features, int tile, hipStream_t stream,
+                    bool ws_mode = false, void* ws = nullptr, size_t ws_bytes = 0) {
   // kernels.cu:1661 — the only supported group size.
   if (group_size != 64) {
     return fail(INFER_HIP_INVALID_ARGUMENT, "w8a16 group size must be 64 (got %d)", group_size);
@@ -1221,8 +1309,16 @@ int gemm_w8a16_impl(const int8_t* weight, const uint16_t* scales, int group_size
     launch_w8a16_gemv_fast({weight, scales, bias, input, output, out_features, in_features},
                            stream);
   } else if (tokens > 1 && gemm_mfma_supported(weight, input, tokens, out_features, in_features)) {
-    const GemmArgs a{weight, scales, bias, input, output, tokens, out_features, in_features};
-    launch_gemm_mfma(tile < 0 ? gemm_pick_tile(tokens, out_features) : tile, true, a, stream);
+    bool done = false;
+    if (ws_mode) {
+      const int rc = launch_lone_split(true, weight, scales, bias, input, output, tokens,
+                                       out_features, in_features, ws, ws_bytes, stream, &done);
+      if (rc != INFER_HIP_OK) return rc;
+    }
+    if (!done) {
+      const GemmArgs a{weight, scales, bias, input, output, tokens, out_features, in_features};
+      launch_gemm_mfma(tile < 0 ? gemm_pick_tile(tokens, out_features) : tile, true, a, stream);
+    }
   } else {
     launch_w8a16_linear_generic(weight, scales, group_size, bias, input, output, tokens,
                                 out_features, in_features, stream);
@@ -1232,7 +1328,8 @@ int gemm_w8a16_impl(const int8_t* weight, const uint16_t* scales, int group_size
 
 int gemm_bf16_impl(const uint16_t* weight, const uint16_t* bias, const uint16_t* input,
                    uint16_t* output, int tokens, int out_features, int in_features, int tile,
-                   hipStream_t stream) {
+                   hipStream_t stream, bool ws_mode = false, void* ws = nullptr,
+                   size_t ws_bytes = 0) {
   if (tokens <= 0 || out_features <= 0 || in_features < 0) {
     return fail(INFER_HIP_INVALID_ARGUMENT, "gemm_bf16: bad shape M=%d N=%d K=%d", tokens,
                 out_features, in_features);
@@ -1246,8 +1343,16 @@ int gemm_bf16_impl(const uint16_t* weight, const uint16_t* bias, const uint16_t*
   if (tokens == 1 && bf16_gemv_fast_supported(weight, input, in_features)) {
     launch_bf16_gemv_fast({weight, bias, input, output, out_features, in_features}, stream);
   } else if (tokens > 1 && gemm_mfma_supported(weight, input, tokens, out_features, in_features)) {
-    const GemmArgs a{weight, nullptr, bias, input, output, tokens, out_features, in_features};
-    launch_gemm_mfma(tile < 0 ? gemm_pick_tile(tokens, out_features) : tile, false, a, stream);
+    bool done = false;
+    if (ws_mode) {
+      const int rc = launch_lone_split(false, weight, nullptr, bias, input, output, tokens,
+                                       out_features, in_features, ws, ws_bytes, stream, &done);
+      if (rc != INFER_HIP_OK) return rc;
+    }
+    if (!done) {
+      const GemmArgs a{weight, nullptr, bias, input, output, tokens, out_features, in_features};
+      launch_gemm_mfma(tile < 0 ? gemm_pick_tile(tokens, out_features) : tile, false, a, stream);
+    }
   } else {
     launch_bf16_linear_generic(weight, bias, input, output, tokens, out_features, in_features,
                                stream);
@@ -1319,6 +1424,42 @@ extern "C" int infer_hip_gemm_bf16(const uint16_t* weight, const uint16_t* bias,
 }
 
 extern "C" int infer_hip_gemm_tile_count(void) { return kGemmTileCount; }
+
+extern "C" size_t infer_hip_gemm_workspace_bytes(int max_tokens, int out_features,
+                                                 int in_features) {
+  if (max_tokens < 2 || out_features <= 0 || in_features < kStageK ||
+      in_features % kStageK != 0) {
+    return 0;
+  }
+  int cus = 0;
+  if (current_cus(&cus) != INFER_HIP_OK) return 0;
+  size_t partials = 0, counters = 0;
+  for (int m = 2; m <= max_tokens; ++m) {
+    const LoneLayout o = lone_layout(false, nullptr, nullptr, nullptr, nullptr, nullptr, m,
+                                     out_features, in_features, cus);
+    partials = std::max(partials, o.partial_bytes);
+    counters = std::max(counters, o.counter_bytes);
+  }
+  if (partials == 0) return 0;       // no call splits
+  return partials + counters + 256;  // 256: the partials' alignment at the end
+}
+
+extern "C" int infer_hip_gemm_w8a16_ws(const int8_t* weight, const uint16_t* scales,
+                                       int group_size, const uint16_t* bias,
+                                       const uint16_t* input, uint16_t* output, int tokens,
+                                       int out_features, int in_features, void* workspace,
+                                       size_t workspace_bytes, hipStream_t stream) {
+  return gemm_w8a16_impl(weight, scales, group_size, bias, input, output, tokens, out_features,
+                         in_features, -1, stream, true, workspace, workspace_bytes);
+}
+
+extern "C" int infer_hip_gemm_bf16_ws(const uint16_t* weight, const uint16_t* bias,
+                                      const uint16_t* input, uint16_t* output, int tokens,
+                                      int out_features, int in_features, void* workspace,
+                                      size_t workspace_bytes, hipStream_t stream) {
+  return gemm_bf16_impl(weight, bias, input, output, tokens, out_features, in_features, -1,
+                        stream, true, workspace, workspace_bytes);
+}
 
 extern "C" int infer_hip_gemm_w8a16_tile(const int8_t* weight, const uint16_t* scales,
                                          int group_size, const uint16_t* bias,

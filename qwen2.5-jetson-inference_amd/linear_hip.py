@@ -39,6 +39,9 @@ EXPORTED_SYMBOLS = (
     "infer_hip_gemm_tile_count",
     "infer_hip_gemm_w8a16_tile",
     "infer_hip_gemm_bf16_tile",
+    "infer_hip_gemm_workspace_bytes",
+    "infer_hip_gemm_w8a16_ws",
+    "infer_hip_gemm_bf16_ws",
     "infer_hip_w8a16_gemv_plan_create",
     "infer_hip_w8a16_gemv_plan_launch",
     "infer_hip_w8a16_gemv_plan_bytes",
@@ -134,6 +137,8 @@ def load() -> ctypes.CDLL:
         "infer_hip_gemm_w8a16": [p, p, i, p, p, p, i, i, i, p],
         "infer_hip_gemm_w8a16_tile": [p, p, i, p, p, p, i, i, i, i, p],
         "infer_hip_gemm_bf16_tile": [p, p, p, p, i, i, i, i, p],
+        "infer_hip_gemm_w8a16_ws": [p, p, i, p, p, p, i, i, i, p, ctypes.c_size_t, p],
+        "infer_hip_gemm_bf16_ws": [p, p, p, p, i, i, i, p, ctypes.c_size_t, p],
     }
     for name, args in sigs.items():
         fn = getattr(lib, name)
@@ -141,6 +146,8 @@ def load() -> ctypes.CDLL:
         fn.restype = i
     lib.infer_hip_gemm_tile_count.argtypes = []
     lib.infer_hip_gemm_tile_count.restype = i
+    lib.infer_hip_gemm_workspace_bytes.argtypes = [i, i, i]
+    lib.infer_hip_gemm_workspace_bytes.restype = ctypes.c_size_t
     lib.infer_hip_lm_head_workspace_entries.argtypes = [i, i]
     lib.infer_hip_lm_head_workspace_entries.restype = ctypes.c_size_t
     lib.infer_hip_w8a16_gemv_plan_create.argtypes = [p, i, ctypes.POINTER(p)]
@@ -269,6 +276,38 @@ def gemm_bf16_tile(weight, bias, input, output, tokens, out_features,
     _check(load().infer_hip_gemm_bf16_tile(_ptr(weight), _ptr(bias), _ptr(input),
                                            _ptr(output), tokens, out_features,
                                            in_features, tile, _stream(stream)))
+
+
+def gemm_workspace_bytes(max_tokens, out_features, in_features) -> int:
+    """Workspace bytes of gemm_*_ws for every token count up to max_tokens
+    (0: no such call splits K)."""
+    return int(load().infer_hip_gemm_workspace_bytes(max_tokens, out_features, in_features))
+
+
+def _ws_args(workspace):
+    """(pointer, bytes) of a workspace tensor (or None)."""
+    if workspace is None:
+        return None, 0
+    return _ptr(workspace), workspace.numel() * workspace.element_size()
+
+
+def gemm_w8a16_ws(weight, scales, group_size, bias, input, output, tokens, out_features,
+                  in_features, workspace, stream=None):
+    """gemm_w8a16 with a caller workspace (a zeroed device tensor of at
+    least gemm_workspace_bytes bytes): long-K calls split over K."""
+    wp, wb = _ws_args(workspace)
+    _check(load().infer_hip_gemm_w8a16_ws(_ptr(weight), _ptr(scales), group_size, _ptr(bias),
+                                          _ptr(input), _ptr(output), tokens, out_features,
+                                          in_features, wp, wb, _stream(stream)))
+
+
+def gemm_bf16_ws(weight, bias, input, output, tokens, out_features, in_features, workspace,
+                 stream=None):
+    """gemm_bf16 with a caller workspace (see gemm_w8a16_ws)."""
+    wp, wb = _ws_args(workspace)
+    _check(load().infer_hip_gemm_bf16_ws(_ptr(weight), _ptr(bias), _ptr(input), _ptr(output),
+                                         tokens, out_features, in_features, wp, wb,
+                                         _stream(stream)))
 
 
 class W8A16GemvPlan:

@@ -195,6 +195,48 @@ void dispatch_and_plan(infer::hip::Context& ctx) {
   EXPECT(threw, "FP32 weights must be rejected by the BF16 dispatch");
 }
 
+// linear_batch with a GemmWorkspace on a down_proj-shaped weight (K = 4864,
+// split over K) equals the plain linear_batch within the reference's W8A16
+// tolerance at several token counts sharing one workspace; a weight that
+// never splits needs none.
+void workspace_batch(infer::hip::Context& ctx) {
+  const int n = 896, k = 4864, max_tokens = 64;
+  std::vector<int8_t> q(static_cast<size_t>(n) * k);
+  std::vector<uint16_t> s(static_cast<size_t>(n) * (k / 64)), x(static_cast<size_t>(max_tokens) * k);
+  for (size_t j = 0; j < q.size(); ++j) q[j] = static_cast<int8_t>((j * 7919 + 3) % 255 - 127);
+  for (size_t j = 0; j < s.size(); ++j) s[j] = to_bf16(1e-4f * (1 + j % 11));
+  for (size_t j = 0; j < x.size(); ++j) x[j] = to_bf16(std::sin(0.013f * static_cast<float>(j)));
+  Dev<int8_t> dq(q);
+  Dev<uint16_t> ds(s), dx(x), dy(static_cast<size_t>(max_tokens) * n),
+      dr(static_cast<size_t>(max_tokens) * n);
+  const infer::LinearWeight w{infer::DType::kInt8, dq.p, ds.p, 64, nullptr, n, k};
+  const infer::LinearWeight shortk{infer::DType::kInt8, dq.p, ds.p, 64, nullptr, n, 896};
+  infer::hip::GemmWorkspace ws(max_tokens, {&w});
+  infer::hip::GemmWorkspace none(max_tokens, {&shortk});
+  EXPECT(ws.bytes() > 0, "a K = 4864 weight splits at %d tokens", max_tokens);
+  EXPECT(none.bytes() == 0, "a K = 896 weight needs no workspace (%zu bytes)", none.bytes());
+  for (int tokens : {2, 33, 64, 17}) {
+    infer::hip::linear_batch(w, dx.p, dy.p, tokens, ws, ctx.stream());
+    infer::hip::linear_batch(w, dx.p, dr.p, tokens, ctx.stream());
+    ctx.synchronize();
+    const auto a = dy.host(), r = dr.host();
+    int bad = 0;
+    for (size_t j = 0; j < static_cast<size_t>(tokens) * n; ++j) {
+      const float fa = from_bf16(a[j]), fr = from_bf16(r[j]);
+      bad += !(std::fabs(fa - fr) <= std::max(1.0f / 64, 0.01f * std::fabs(fr)));
+    }
+    EXPECT(bad == 0, "workspace linear_batch at %d tokens: %d outputs off", tokens, bad);
+  }
+  bool threw = false;
+  try {  // a workspace smaller than the call needs
+    infer::hip::gemm_w8a16(dq.p, ds.p, 64, nullptr, dx.p, dy.p, max_tokens, n, k, ws.data(), 16,
+                           ctx.stream());
+  } catch (const infer::Error& e) {
+    threw = std::strstr(e.what(), "workspace") != nullptr;
+  }
+  EXPECT(threw, "a too small workspace must throw infer::Error");
+}
+
 }  // namespace
 
 int main() {
@@ -218,6 +260,7 @@ int main() {
     lm_head_case(ctx, 1002, 64, 7, 71);
     lm_head_case(ctx, 64, 896, 1, 31);
     dispatch_and_plan(ctx);
+    workspace_batch(ctx);
   } catch (const std::exception& e) {
     std::printf("FAIL: exception %s\n", e.what());
     return 2;

@@ -196,3 +196,47 @@ def test_gemm_plan_rejects_unsupported_descriptors(hip, dev):
         hip.GemmPlan([(q64, s, 64, None, x64, y, 1, 4, 64)])
     with pytest.raises(hip.InferError):  # mixed weight types
         hip.GemmPlan([(q64, s, 64, None, x64, y, 2, 4, 64), (w64, None, x64, y, 2, 4, 64)])
+
+
+@pytest.mark.parametrize("w8", [True, False], ids=["w8a16", "bf16"])
+def test_lone_gemm_with_workspace_splits_long_k(hip, orc, dev, w8):
+    """infer_hip_gemm_*_ws: down_proj (K = 4864) at M = 2 .. 512 splits K
+    over the workspace; every call sharing one workspace (sized for M <= 512,
+    zeroed once) meets the oracle bar, a shape that never splits needs none,
+    and a workspace smaller than a call needs is rejected."""
+    import torch
+    n, k = 896, 4864
+    need = hip.gemm_workspace_bytes(512, n, k)
+    assert need > 0
+    assert hip.gemm_workspace_bytes(512, 896, 896) == 0      # 14 stages: never split
+    assert hip.gemm_workspace_bytes(1, n, k) == 0            # one token: the GEMV
+    ws = torch.zeros(need // 4 + 1, dtype=torch.int32, device=dev)
+    rng = rc.philox(4864 + w8)
+    if w8:
+        q, s = rc.w8a16_synthetic(rng, n, k)
+        wd, sd = to_dev(q, dev), to_dev(s, dev)
+        weights = orc.dequant_w8a16(q, s)
+    else:
+        w = rc.bf16_normal(rng, (n, k), 0.02)
+        wd = to_dev(w, dev)
+        weights = rc.bf16_values(w)
+    b = rc.bf16_normal(rng, (n,))
+    for m in (2, 32, 128, 512, 65):
+        print(f"gemm ws w8={w8} M={m}", flush=True)
+        x = rc.bf16_normal(rng, (m, k))
+        exp = orc.linear_fp32_batch(weights, rc.bf16_values(b), rc.bf16_values(x))
+        y = bf16_out((m, n), dev)
+        if w8:
+            hip.gemm_w8a16_ws(wd, sd, 64, to_dev(b, dev), to_dev(x, dev), y, m, n, k, ws)
+        else:
+            hip.gemm_bf16_ws(wd, to_dev(b, dev), to_dev(x, dev), y, m, n, k, ws)
+        stats = check_close(words(y), exp, what=f"gemm ws w8={w8} M={m}")
+        assert stats["bit_identical"] > 0.95, stats
+    small = ws[:4]
+    x = to_dev(rc.bf16_normal(rng, (32, k)), dev)
+    with pytest.raises(hip.InferError) as err:
+        if w8:
+            hip.gemm_w8a16_ws(wd, sd, 64, None, x, bf16_out((32, n), dev), 32, n, k, small)
+        else:
+            hip.gemm_bf16_ws(wd, None, x, bf16_out((32, n), dev), 32, n, k, small)
+    assert err.value.status == hip.INVALID_ARGUMENT and "workspace" in str(err.value)
