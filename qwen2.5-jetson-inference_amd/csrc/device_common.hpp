@@ -223,6 +223,11 @@ __device__ __forceinline__ uint4 load_global16(const void* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// 16-byte global store.
+__device__ __forceinline__ void store_global16(void* p, uint4 v) {
+  *(QLIN_GLOBAL u32x4*)(p) = u32x4{v.x, v.y, v.z, v.w};
+}
+
 // 16-byte global load marked as streaming (the weights are read once per
 // call, so they should not displace reused lines).
 __device__ __forceinline__ uint4 load_stream16(const void* p) {

@@ -127,6 +127,113 @@ __global__ __launch_bounds__(kThreads) void add_rms_norm_kernel(uint16_t* __rest
   }
 }
 
+// RMSNorm rows (with ADD: after the residual add x = bf16(x + y), in place),
+// one wave per row and four rows per block: lane l takes the 8-element
+// chunks l, l + 64, ... of the row with 16-byte loads and stores, and the
+// sum of squares is reduced across the wave (DPP/permlane) with no LDS or
+// barrier.  The elementwise arithmetic is rms_norm_kernel's and
+// add_rms_norm_kernel's; the sum of squares is added in another order.
+// hidden % 8 == 0, hidden <= 512 * CH, 16-byte aligned rows.
+template <int CH, bool ADD>
+__global__ __launch_bounds__(kThreads) void norm_rows_kernel(uint16_t* __restrict__ x,
+                                                             const uint16_t* __restrict__ y,
+                                                             const uint16_t* __restrict__ w,
+                                                             uint16_t* __restrict__ out,
+                                                             int rows, int hidden, float eps) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int row = blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
+  if (row >= rows) return;  // the whole wave
+  const int chunks = hidden >> 3;
+  uint4* xr = reinterpret_cast<uint4*>(x + static_cast<size_t>(row) * hidden);
+  const uint4* yr = ADD ? reinterpret_cast<const uint4*>(y + static_cast<size_t>(row) * hidden)
+                        : nullptr;
+  const uint4* wr = reinterpret_cast<const uint4*>(w);
+  uint4* orow = reinterpret_cast<uint4*>(out + static_cast<size_t>(row) * hidden);
+  uint4 xa[CH], ya[CH], wa[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {  // every load in flight at once (clamped, masked below)
+    const int i = min(lane + kWave * c, chunks - 1);
+    xa[c] = load_global16(xr + i);
+    if (ADD) ya[c] = load_global16(yr + i);
+    wa[c] = load_global16(wr + i);
+  }
+  float v[CH][8];
+  float sum = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const bool live = lane + kWave * c < chunks;
+    const uint32_t xs[4] = {xa[c].x, xa[c].y, xa[c].z, xa[c].w};
+    const uint32_t ys[4] = {ADD ? ya[c].x : 0u, ADD ? ya[c].y : 0u, ADD ? ya[c].z : 0u,
+                            ADD ? ya[c].w : 0u};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float a0 = bf16_lo(xs[e]), a1 = bf16_hi(xs[e]);
+      if (ADD) {
+        a0 = bf16_to_f32(f32_to_bf16(a0 + bf16_lo(ys[e])));
+        a1 = bf16_to_f32(f32_to_bf16(a1 + bf16_hi(ys[e])));
+      }
+      v[c][2 * e] = a0;
+      v[c][2 * e + 1] = a1;
+      if (live) sum = fmaf(a1, a1, fmaf(a0, a0, sum));
+    }
+    if (ADD && live) {
+      store_global16(xr + lane + kWave * c, make_uint4(pack2_bf16(v[c][0], v[c][1]),
+                                                       pack2_bf16(v[c][2], v[c][3]),
+                                                       pack2_bf16(v[c][4], v[c][5]),
+                                                       pack2_bf16(v[c][6], v[c][7])));
+    }
+  }
+  sum = wave_sum(sum);
+  const float scale = 1.0f / sqrtf(sum / hidden + eps);
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    if (lane + kWave * c >= chunks) continue;
+    const uint32_t ws[4] = {wa[c].x, wa[c].y, wa[c].z, wa[c].w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o[e] = pack2_bf16(v[c][2 * e] * scale * bf16_lo(ws[e]),
+                        v[c][2 * e + 1] * scale * bf16_hi(ws[e]));
+    }
+    store_global16(orow + lane + kWave * c, make_uint4(o[0], o[1], o[2], o[3]));
+  }
+}
+
+// The wave-per-row form applies (16-byte aligned rows of whole chunks);
+// chunks per lane for it, 0 if it does not.
+int norm_rows_chunks(const void* x, const void* y, const void* w, const void* out, int hidden) {
+  const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  if (hidden <= 0 || hidden % 8 != 0 || !a16(x) || (y && !a16(y)) || !a16(w) || !a16(out)) {
+    return 0;
+  }
+  const int per = (hidden / 8 + kWave - 1) / kWave;
+  return per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : per <= 8 ? 8 : 0;
+}
+
+template <bool ADD>
+void launch_norm_rows(int ch, uint16_t* x, const uint16_t* y, const uint16_t* w, uint16_t* out,
+                      int rows, int hidden, float eps, hipStream_t stream) {
+  const dim3 grid((rows + kThreads / kWave - 1) / (kThreads / kWave)), block(kThreads);
+  switch (ch) {
+    case 1:
+      hipLaunchKernelGGL((norm_rows_kernel<1, ADD>), grid, block, 0, stream, x, y, w, out, rows,
+                         hidden, eps);
+      break;
+    case 2:
+      hipLaunchKernelGGL((norm_rows_kernel<2, ADD>), grid, block, 0, stream, x, y, w, out, rows,
+                         hidden, eps);
+      break;
+    case 4:
+      hipLaunchKernelGGL((norm_rows_kernel<4, ADD>), grid, block, 0, stream, x, y, w, out, rows,
+                         hidden, eps);
+      break;
+    default:
+      hipLaunchKernelGGL((norm_rows_kernel<8, ADD>), grid, block, 0, stream, x, y, w, out, rows,
+                         hidden, eps);
+      break;
+  }
+}
+
 // ------------------------------------------------------- RoPE + KV store --
 
 
@@ -1222,12 +1329,21 @@ void launch_embedding(const uint16_t* table, const int* tokens, int count, int v
 
 void launch_rms_norm(const uint16_t* x, const uint16_t* w, uint16_t* out, int rows, int hidden,
                      float eps, hipStream_t stream) {
+  if (const int ch = norm_rows_chunks(x, nullptr, w, out, hidden)) {
+    launch_norm_rows<false>(ch, const_cast<uint16_t*>(x), nullptr, w, out, rows, hidden, eps,
+                            stream);
+    return;
+  }
   hipLaunchKernelGGL(rms_norm_kernel, dim3(rows), dim3(kThreads), 0, stream, x, w, out, rows,
                      hidden, eps);
 }
 
 void launch_add_rms_norm(uint16_t* x, const uint16_t* y, const uint16_t* w, uint16_t* out,
                          int rows, int hidden, float eps, hipStream_t stream) {
+  if (const int ch = norm_rows_chunks(x, y, w, out, hidden)) {
+    launch_norm_rows<true>(ch, x, y, w, out, rows, hidden, eps, stream);
+    return;
+  }
   hipLaunchKernelGGL(add_rms_norm_kernel, dim3(rows), dim3(kThreads), 0, stream, x, y, w, out,
                      rows, hidden, eps);
 }
