@@ -271,6 +271,71 @@ __global__ __launch_bounds__(kThreads) void rope_store_kernel(
   }
 }
 
+// The same, one wave per token and four tokens per block, with 16-byte
+// accesses: a unit is chunk c (8 dimensions) of the first half of a q or k
+// head and its rotation partner, chunk c + half / 8, so a lane loads both,
+// rotates its 8 pairs (rope_pair, as rope_store_kernel) and stores both; a
+// k head's rotated chunks go to the key cache from the same registers, and
+// v's chunks are copied to the value cache 16 bytes at a time.  head_dim % 16
+// == 0 and 16-byte aligned tensors.
+__global__ __launch_bounds__(kThreads) void rope_store_rows_kernel(
+    uint16_t* __restrict__ q, uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    uint16_t* __restrict__ key_cache, uint16_t* __restrict__ value_cache,
+    const float2* __restrict__ rope, int count, int start, int heads, int kv_heads,
+    int head_dim, int max_seq) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int t = blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
+  const int pos = start + t;
+  if (t >= count || pos >= max_seq) return;  // the whole wave
+  const int half_chunks = head_dim / 16;     // chunks in half a head
+  const int units = (heads + kv_heads) * half_chunks;
+  const float2* cs = rope + static_cast<size_t>(pos) * (head_dim / 2);
+  for (int u = lane; u < units; u += kWave) {
+    const int head = u / half_chunks, c = u % half_chunks;
+    const bool is_k = head >= heads;
+    uint16_t* base = is_k ? k + (static_cast<size_t>(t) * kv_heads + head - heads) * head_dim
+                          : q + (static_cast<size_t>(t) * heads + head) * head_dim;
+    const uint4 lo = load_global16(base + 8 * c);
+    const uint4 hi = load_global16(base + head_dim / 2 + 8 * c);
+    float2 r[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float4 two = *reinterpret_cast<const float4*>(cs + 8 * c + 2 * j);
+      r[2 * j] = make_float2(two.x, two.y);
+      r[2 * j + 1] = make_float2(two.z, two.w);
+    }
+    const uint32_t l4[4] = {lo.x, lo.y, lo.z, lo.w}, h4[4] = {hi.x, hi.y, hi.z, hi.w};
+    uint32_t ol[4], oh[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float a0 = bf16_lo(l4[e]), b0 = bf16_lo(h4[e]);
+      float a1 = bf16_hi(l4[e]), b1 = bf16_hi(h4[e]);
+      rope_pair(a0, b0, r[2 * e]);
+      rope_pair(a1, b1, r[2 * e + 1]);
+      ol[e] = pack2_bf16(a0, a1);
+      oh[e] = pack2_bf16(b0, b1);
+    }
+    const uint4 nl = make_uint4(ol[0], ol[1], ol[2], ol[3]);
+    const uint4 nh = make_uint4(oh[0], oh[1], oh[2], oh[3]);
+    store_global16(base + 8 * c, nl);
+    store_global16(base + head_dim / 2 + 8 * c, nh);
+    if (is_k) {
+      uint16_t* row =
+          key_cache + (static_cast<size_t>(head - heads) * max_seq + pos) * head_dim;
+      store_global16(row + 8 * c, nl);
+      store_global16(row + head_dim / 2 + 8 * c, nh);
+    }
+  }
+  const int v_chunks = kv_heads * head_dim / 8;
+  for (int u = lane; u < v_chunks; u += kWave) {
+    const int g = u / (head_dim / 8), c = u % (head_dim / 8);
+    const uint4 val =
+        load_global16(v + (static_cast<size_t>(t) * kv_heads + g) * head_dim + 8 * c);
+    store_global16(value_cache + (static_cast<size_t>(g) * max_seq + pos) * head_dim + 8 * c,
+                   val);
+  }
+}
+
 // ------------------------------------------------------ decode attention --
 
 // One decode step's attention over the context [0, pos] of query head h
@@ -1352,6 +1417,15 @@ void launch_rope_store(uint16_t* q, uint16_t* k, const uint16_t* v, uint16_t* ke
                        uint16_t* value_cache, const float2* rope, int count, int start,
                        int heads, int kv_heads, int head_dim, int max_seq,
                        hipStream_t stream) {
+  const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  if (head_dim % 16 == 0 && a16(q) && a16(k) && a16(v) && a16(key_cache) &&
+      a16(value_cache) && a16(rope)) {
+    hipLaunchKernelGGL(rope_store_rows_kernel,
+                       dim3((count + kThreads / kWave - 1) / (kThreads / kWave)), dim3(kThreads),
+                       0, stream, q, k, v, key_cache, value_cache, rope, count, start, heads,
+                       kv_heads, head_dim, max_seq);
+    return;
+  }
   hipLaunchKernelGGL(rope_store_kernel, dim3(count), dim3(kThreads), 0, stream, q, k, v,
                      key_cache, value_cache, rope, count, start, heads, kv_heads, head_dim,
                      max_seq);
