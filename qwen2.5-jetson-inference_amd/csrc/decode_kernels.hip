@@ -1,14 +1,15 @@
-// Fused decode-step kernels for gfx950: the W8A16 GEMVs of a decode step with
-// the RMSNorm in front of them (and the SiLU-mul behind gate/up) folded in,
-// and the tied LM head with the final RMSNorm, the argmax and the step's
-// bookkeeping folded in.
+// Fused decode-step kernels for gfx950: the GEMVs of a decode step (W8A16 or
+// BF16 weights) with the RMSNorm in front of them (and the SiLU-mul behind
+// gate/up) folded in, and the tied LM head with the final RMSNorm, the argmax
+// and the step's bookkeeping folded in.
 //
 // A decode step is latency-bound: every kernel starts on a cold L2 and each
 // dependent global round trip costs about a microsecond, so these kernels
 // are built to need one round trip: a wave issues its weight loads, then its
 // activation and norm-weight loads (all independent), and only then waits.
-// With K <= 1024 x SLABS, the 64 lanes of one wave hold the whole input
-// vector (lane l owns 16-element chunks l, l + 64, ...), so each wave
+// With K <= 64 C x SLABS, the 64 lanes of one wave hold the whole input
+// vector (lane l owns C-element chunks l, l + 64, ..., where C = 16 for
+// int8 weights and 8 for BF16: one 16-byte weight load each), so each wave
 // computes the RMSNorm of x by itself: no workgroup reduction, no extra
 // launch, no normalized copy in memory.
 //
@@ -62,6 +63,26 @@ __device__ __forceinline__ void load_vec16_raw(const uint16_t* v, int k, int lan
     const int c = min(s * kWave + lane, chunks - 1);
     lo[s] = load_global16(v + 16 * c);
     hi[s] = load_global16(v + 16 * c + 8);
+  }
+}
+
+// Raw chunks of C values (C = 8 or 16: C / 8 16-byte pieces per chunk).
+template <int C, int SLABS>
+__device__ __forceinline__ void load_vec_raw(const uint16_t* v, int k, int lane,
+                                             uint4 (&raw)[SLABS][C / 8]) {
+  if constexpr (C == 16) {
+    uint4 lo[SLABS], hi[SLABS];
+    load_vec16_raw<SLABS>(v, k, lane, lo, hi);
+#pragma unroll
+    for (int s = 0; s < SLABS; ++s) {
+      raw[s][0] = lo[s];
+      raw[s][1] = hi[s];
+    }
+  } else {
+    uint4 r[SLABS];
+    load_vec8_raw<SLABS>(v, k, lane, r);
+#pragma unroll
+    for (int s = 0; s < SLABS; ++s) raw[s][0] = r[s];
   }
 }
 
@@ -134,6 +155,66 @@ __device__ __forceinline__ float w8_row_dot(const uint4 (&wq)[SLABS], const uint
   return wave_sum(acc);
 }
 
+// Weight formats of the fused GEMVs.  A row is read as 16-byte chunks, lane
+// l holding chunks l, l + 64, ... (SLABS of them), all requested at once.
+//
+// W8A16: 16 int8 weights per chunk and the BF16 scale of its 64-group;
+// chunk sums are scaled per chunk (dot16_i8, then the scale), as the
+// unfused W8A16 GEMV does.
+struct W8Fmt {
+  static constexpr int C = 16;
+  template <int SLABS>
+  struct Row {
+    uint4 q[SLABS];
+    uint32_t s[SLABS];
+  };
+  template <int SLABS>
+  static __device__ __forceinline__ void load(const void* w, const uint16_t* s, int row, int n,
+                                              int k, int lane, Row<SLABS>& r) {
+    load_w8_row<SLABS>(static_cast<const int8_t*>(w), s, row, n, k, lane, r.q, r.s);
+  }
+  template <int SLABS>
+  static __device__ __forceinline__ float dot(const Row<SLABS>& r, const float (&x)[SLABS][C],
+                                              bool row_ok, int k, int lane) {
+    return w8_row_dot<SLABS>(r.q, r.s, x, row_ok, k, lane);
+  }
+};
+
+// BF16: 8 weights per chunk, no scales.  Chunks past K (or a row past the
+// matrix) re-read the last chunk (row) and are discarded by a select, so
+// whatever they hold cannot reach the sum.
+struct Bf16Fmt {
+  static constexpr int C = 8;
+  template <int SLABS>
+  struct Row {
+    uint4 q[SLABS];
+  };
+  template <int SLABS>
+  static __device__ __forceinline__ void load(const void* w, const uint16_t*, int row, int n,
+                                              int k, int lane, Row<SLABS>& r) {
+    const uint16_t* wb = static_cast<const uint16_t*>(w);
+    const int chunks = k >> 3;
+    const int rr = min(row, n - 1);
+#pragma unroll
+    for (int i = 0; i < SLABS; ++i) {
+      const int c = min(i * kWave + lane, chunks - 1);
+      r.q[i] = load_stream16(wb + static_cast<size_t>(rr) * k + 8 * c);
+    }
+  }
+  template <int SLABS>
+  static __device__ __forceinline__ float dot(const Row<SLABS>& r, const float (&x)[SLABS][C],
+                                              bool row_ok, int k, int lane) {
+    const int chunks = k >> 3;
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < SLABS; ++i) {
+      const float next = dot8_bf16(r.q[i], x[i], acc);
+      acc = row_ok && i * kWave + lane < chunks ? next : acc;
+    }
+    return wave_sum(acc);
+  }
+};
+
 // Descriptor of the workgroup: the last one whose block_begin <= b.
 __device__ __forceinline__ NormGemvDesc pick_desc(const NormGemvArgs& a, int b) {
   NormGemvDesc d = a.d[0];
@@ -144,53 +225,41 @@ __device__ __forceinline__ NormGemvDesc pick_desc(const NormGemvArgs& a, int b) 
 
 }  // namespace
 
-// y = bf16(W8A16(rms_norm(x)) + bias) for up to three GEMVs on the same
+// y = bf16(W(rms_norm(x)) + bias) for up to three GEMVs on the same
 // normalized input (q|k|v), or with PAIR mlp = bf16(silu(bf16(gate)) *
 // bf16(up)) from the gate (w, s) and up (w2, s2) rows of the same index.
 // Each wave computes R consecutive output rows (all their loads in flight
-// together); 4 R rows per workgroup.
-template <int SLABS, bool PAIR, int R>
-__global__ __launch_bounds__(kBlock) void norm_gemv_w8_kernel(NormGemvArgs a) {
+// together); 4 R rows per workgroup.  F is the weight format (W8Fmt,
+// Bf16Fmt).
+template <class F, int SLABS, bool PAIR, int R>
+__global__ __launch_bounds__(kBlock) void norm_gemv_kernel(NormGemvArgs a) {
+  constexpr int C = F::C;
   const NormGemvDesc d = pick_desc(a, blockIdx.x);
   const int lane = threadIdx.x & (kWave - 1);
   const int row0 = ((blockIdx.x - d.block_begin) * kWaves + threadIdx.x / kWave) * R;
-  uint4 w1[R][SLABS], w2[R][SLABS];
-  uint32_t s1[R][SLABS], s2[R][SLABS];
+  typename F::template Row<SLABS> w1[R], w2[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    load_w8_row<SLABS>(d.w, d.s, row0 + r, d.n, a.k, lane, w1[r], s1[r]);
-    if (PAIR) load_w8_row<SLABS>(d.w2, d.s2, row0 + r, d.n, a.k, lane, w2[r], s2[r]);
+    F::template load<SLABS>(d.w, d.s, row0 + r, d.n, a.k, lane, w1[r]);
+    if (PAIR) F::template load<SLABS>(d.w2, d.s2, row0 + r, d.n, a.k, lane, w2[r]);
   }
   // The bias of the row this lane writes (lane r < R), requested with the
   // weights so the store at the end waits on no further round trip; an
   // absent bias reads y instead and is discarded.
   const int brow = min(row0 + min(lane, R - 1), d.n - 1);
   const uint16_t bias_raw = gload((d.bias && !PAIR ? d.bias : d.y) + brow);
-  uint4 xr[SLABS][2], nr[SLABS][2];
-  {
-    uint4 lo[SLABS], hi[SLABS];
-    load_vec16_raw<SLABS>(a.x, a.k, lane, lo, hi);
-#pragma unroll
-    for (int s = 0; s < SLABS; ++s) {
-      xr[s][0] = lo[s];
-      xr[s][1] = hi[s];
-    }
-    load_vec16_raw<SLABS>(a.norm_w, a.k, lane, lo, hi);
-#pragma unroll
-    for (int s = 0; s < SLABS; ++s) {
-      nr[s][0] = lo[s];
-      nr[s][1] = hi[s];
-    }
-  }
+  uint4 xr[SLABS][C / 8], nr[SLABS][C / 8];
+  load_vec_raw<C, SLABS>(a.x, a.k, lane, xr);
+  load_vec_raw<C, SLABS>(a.norm_w, a.k, lane, nr);
   __builtin_amdgcn_sched_barrier(0);  // every load is in flight
-  float xn[SLABS][16];
-  wave_rms_norm<SLABS, 16>(xr, nr, a.k, a.eps, lane, xn);
+  float xn[SLABS][C];
+  wave_rms_norm<SLABS, C>(xr, nr, a.k, a.eps, lane, xn);
   float v1[R], v2[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const bool ok = row0 + r < d.n;
-    v1[r] = w8_row_dot<SLABS>(w1[r], s1[r], xn, ok, a.k, lane);
-    if (PAIR) v2[r] = w8_row_dot<SLABS>(w2[r], s2[r], xn, ok, a.k, lane);
+    v1[r] = F::template dot<SLABS>(w1[r], xn, ok, a.k, lane);
+    if (PAIR) v2[r] = F::template dot<SLABS>(w2[r], xn, ok, a.k, lane);
   }
   if (lane < R) {
     // Lane r writes row row0 + r (every lane holds every total).
@@ -223,8 +292,10 @@ __global__ __launch_bounds__(kBlock) void norm_gemv_w8_kernel(NormGemvArgs a) {
 // of v.  Tasks are the q pairs, then the k pairs, then the v pairs.  The
 // position is read at entry and its (cos, sin) requested once it arrives,
 // behind the weight loads, so the rotation waits on no extra round trip.
-template <int SLABS>
-__global__ __launch_bounds__(kBlock) void norm_qkv_rope_w8_kernel(QkvRopeArgs a) {
+// F is the weight format (W8Fmt, Bf16Fmt).
+template <class F, int SLABS>
+__global__ __launch_bounds__(kBlock) void norm_qkv_rope_kernel(QkvRopeArgs a) {
+  constexpr int C = F::C;
   const int lane = threadIdx.x & (kWave - 1);
   const int half = a.head_dim / 2;
   const int qt = a.heads * half, kt = a.kv_heads * half;
@@ -235,7 +306,7 @@ __global__ __launch_bounds__(kBlock) void norm_qkv_rope_w8_kernel(QkvRopeArgs a)
           total - 1));
   const int region = task < qt ? 0 : task < qt + kt ? 1 : 2;  // q, k, v
   const int t = task - (region == 0 ? 0 : region == 1 ? qt : qt + kt);
-  const int8_t* w = region == 0 ? a.wq : region == 1 ? a.wk : a.wv;
+  const void* w = region == 0 ? a.wq : region == 1 ? a.wk : a.wv;
   const uint16_t* sc = region == 0 ? a.sq : region == 1 ? a.sk : a.sv;
   const uint16_t* bias = region == 0 ? a.bq : region == 1 ? a.bk : a.bv;
   const int n = region == 0 ? a.heads * a.head_dim : a.kv_heads * a.head_dim;
@@ -244,35 +315,21 @@ __global__ __launch_bounds__(kBlock) void norm_qkv_rope_w8_kernel(QkvRopeArgs a)
   const int r0 = region == 2 ? 2 * t : head * a.head_dim + i;
   const int r1 = region == 2 ? 2 * t + 1 : r0 + half;
   const int pos = min(*a.pos, a.max_seq - 1);
-  uint4 w0[SLABS], w1[SLABS];
-  uint32_t s0[SLABS], s1[SLABS];
-  load_w8_row<SLABS>(w, sc, r0, n, a.k, lane, w0, s0);
-  load_w8_row<SLABS>(w, sc, r1, n, a.k, lane, w1, s1);
+  typename F::template Row<SLABS> w0, w1;
+  F::template load<SLABS>(w, sc, r0, n, a.k, lane, w0);
+  F::template load<SLABS>(w, sc, r1, n, a.k, lane, w1);
   // the biases of r0 and r1 (an absent bias reads weight bytes instead, discarded)
-  const uint16_t* bsrc = bias ? bias : reinterpret_cast<const uint16_t*>(w);
+  const uint16_t* bsrc = bias ? bias : static_cast<const uint16_t*>(w);
   const uint16_t bias_raw0 = gload(bsrc + r0), bias_raw1 = gload(bsrc + r1);
-  uint4 xr[SLABS][2], nr[SLABS][2];
-  {
-    uint4 lo[SLABS], hi[SLABS];
-    load_vec16_raw<SLABS>(a.x, a.k, lane, lo, hi);
-#pragma unroll
-    for (int s = 0; s < SLABS; ++s) {
-      xr[s][0] = lo[s];
-      xr[s][1] = hi[s];
-    }
-    load_vec16_raw<SLABS>(a.norm_w, a.k, lane, lo, hi);
-#pragma unroll
-    for (int s = 0; s < SLABS; ++s) {
-      nr[s][0] = lo[s];
-      nr[s][1] = hi[s];
-    }
-  }
+  uint4 xr[SLABS][C / 8], nr[SLABS][C / 8];
+  load_vec_raw<C, SLABS>(a.x, a.k, lane, xr);
+  load_vec_raw<C, SLABS>(a.norm_w, a.k, lane, nr);
   const float2 cs = a.rope_row[i];
   __builtin_amdgcn_sched_barrier(0);  // every load is in flight
-  float xn[SLABS][16];
-  wave_rms_norm<SLABS, 16>(xr, nr, a.k, a.eps, lane, xn);
-  const float v0 = w8_row_dot<SLABS>(w0, s0, xn, true, a.k, lane);
-  const float v1 = w8_row_dot<SLABS>(w1, s1, xn, true, a.k, lane);
+  float xn[SLABS][C];
+  wave_rms_norm<SLABS, C>(xr, nr, a.k, a.eps, lane, xn);
+  const float v0 = F::template dot<SLABS>(w0, xn, true, a.k, lane);
+  const float v1 = F::template dot<SLABS>(w1, xn, true, a.k, lane);
   const float b = bias ? bf16_to_f32(bias_raw0) : 0.0f;
   const float b1 = bias ? bf16_to_f32(bias_raw1) : 0.0f;
   if (lane == 0 && static_cast<int>(blockIdx.x) * kWaves + static_cast<int>(threadIdx.x) / kWave <
@@ -294,32 +351,32 @@ __global__ __launch_bounds__(kBlock) void norm_qkv_rope_w8_kernel(QkvRopeArgs a)
   }
 }
 
-// One W8A16 GEMV row per wave, all K chunks of the row requested at once
-// (lane l: chunks l, l + 64, ...), with the residual add: y[row] =
-// bf16(W[row] . x + bias[row]); bias may alias y (each element is read and
-// then written by the same lane).
-template <int SLABS>
-__global__ __launch_bounds__(kBlock) void gemv_w8_rows_kernel(GemvRowsArgs a) {
+// One GEMV row per wave, all K chunks of the row requested at once (lane
+// l: chunks l, l + 64, ...), with the residual add: y[row] = bf16(W[row] .
+// x + bias[row]); bias may alias y (each element is read and then written
+// by the same lane).  F is the weight format (W8Fmt, Bf16Fmt).
+template <class F, int SLABS>
+__global__ __launch_bounds__(kBlock) void gemv_rows_kernel(GemvRowsArgs a) {
+  constexpr int C = F::C;
   const int lane = threadIdx.x & (kWave - 1);
   const int row = blockIdx.x * kWaves + threadIdx.x / kWave;
-  uint4 wq[SLABS];
-  uint32_t sc[SLABS];
-  load_w8_row<SLABS>(static_cast<const int8_t*>(a.w), a.s, row, a.n, a.k, lane, wq, sc);
+  typename F::template Row<SLABS> wr;
+  F::template load<SLABS>(a.w, a.s, row, a.n, a.k, lane, wr);
   // the bias (the residual, which this lane alone overwrites at the end)
   // with the other loads; an absent bias reads y instead and is discarded
   const uint16_t bias_raw = gload((a.bias ? a.bias : a.y) + min(row, a.n - 1));
-  uint4 lo[SLABS], hi[SLABS];
-  load_vec16_raw<SLABS>(a.x, a.k, lane, lo, hi);
+  uint4 xr[SLABS][C / 8];
+  load_vec_raw<C, SLABS>(a.x, a.k, lane, xr);
   __builtin_amdgcn_sched_barrier(0);  // every load is in flight
-  const int chunks = a.k >> 4;
-  float xv[SLABS][16];
+  const int chunks = a.k >> (C == 16 ? 4 : 3);
+  float xv[SLABS][C];
 #pragma unroll
   for (int s = 0; s < SLABS; ++s) {
     const bool keep = s * kWave + lane < chunks;
-    unpack8(lo[s], keep, &xv[s][0]);
-    unpack8(hi[s], keep, &xv[s][8]);
+#pragma unroll
+    for (int h = 0; h < C / 8; ++h) unpack8(xr[s][h], keep, &xv[s][8 * h]);
   }
-  const float v = w8_row_dot<SLABS>(wq, sc, xv, row < a.n, a.k, lane);
+  const float v = F::template dot<SLABS>(wr, xv, row < a.n, a.k, lane);
   if (lane == 0 && row < a.n) {
     const float b = a.bias ? bf16_to_f32(bias_raw) : 0.0f;
     gstore(a.y + row, f32_to_bf16(v + b));
@@ -329,30 +386,32 @@ __global__ __launch_bounds__(kBlock) void gemv_w8_rows_kernel(GemvRowsArgs a) {
 // The o-projection with the merge of the attention's two halves (see
 // decode_kernels.hpp).  One wave per row, the whole row's loads, both
 // records' pieces and the residual in flight at once.  Lane l's chunk c
-// (16 inputs) is head c / 4, dimensions 16 (c % 4) .. + 15.  A second half
-// that the context has not reached is never summed (select, so stale values
-// cannot reach the result).
-template <int SLABS>
+// (C = 16 inputs for int8 weights, 8 for BF16) is head c / (64 / C),
+// dimensions C (c % (64 / C)) .. + C - 1.  A second half that the context
+// has not reached is never summed (select, so stale values cannot reach the
+// result).  F is the weight format (W8Fmt, Bf16Fmt).
+template <class F, int SLABS>
 __global__ __launch_bounds__(kBlock) void attn_o_halves_kernel(AttnOHalvesArgs a) {
+  constexpr int C = F::C, J = C / 4;  // 16-byte record pieces per chunk
+  constexpr uint32_t kPerHead = 64 / C;  // chunks per head
   const int lane = threadIdx.x & (kWave - 1);
   const int row = blockIdx.x * kWaves + threadIdx.x / kWave;
-  uint4 wq[SLABS];
-  uint32_t sc[SLABS];
-  load_w8_row<SLABS>(a.w, a.s, row, a.n, a.k, lane, wq, sc);
+  typename F::template Row<SLABS> wr;
+  F::template load<SLABS>(a.w, a.s, row, a.n, a.k, lane, wr);
   const uint16_t res_raw = gload(a.x + min(row, a.n - 1));
-  const int chunks = a.k >> 4;
+  const int chunks = a.k >> (C == 16 ? 4 : 3);
   const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float*>(a.partial), 0, a.heads * 2 * kAttnHalfRecord * 4, 0x00020000);
-  uint4 r0[SLABS][4], r1[SLABS][4];
+  uint4 r0[SLABS][J], r1[SLABS][J];
   float2 ml0[SLABS], ml1[SLABS];
 #pragma unroll
   for (int s = 0; s < SLABS; ++s) {
-    const int c = min(s * kWave + lane, chunks - 1);
-    const uint32_t b0 = static_cast<uint32_t>((c >> 2) * 2 * kAttnHalfRecord) * 4u;
+    const uint32_t c = static_cast<uint32_t>(min(s * kWave + lane, chunks - 1));
+    const uint32_t b0 = (c / kPerHead) * 2u * kAttnHalfRecord * 4u;
     const uint32_t b1 = b0 + kAttnHalfRecord * 4u;
-    const uint32_t d = static_cast<uint32_t>((c & 3) * 16) * 4u;
+    const uint32_t d = (c % kPerHead) * C * 4u;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < J; ++j) {
       r0[s][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(pr, b0 + d + 16u * j, 0, 0));
       r1[s][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(pr, b1 + d + 16u * j, 0, 0));
     }
@@ -362,7 +421,7 @@ __global__ __launch_bounds__(kBlock) void attn_o_halves_kernel(AttnOHalvesArgs a
   const int pos = min(*a.pos, a.max_seq - 1);
   __builtin_amdgcn_sched_barrier(0);  // every load is in flight
   const bool two = pos >= kAttnHalfSpan;
-  float xv[SLABS][16];
+  float xv[SLABS][C];
 #pragma unroll
   for (int s = 0; s < SLABS; ++s) {
     const bool keep = s * kWave + lane < chunks;
@@ -373,7 +432,7 @@ __global__ __launch_bounds__(kBlock) void attn_o_halves_kernel(AttnOHalvesArgs a
     const float ll = two ? fmaf(ml1[s].y, w1, l0w) : l0w;
     const float inv = 1.0f / ll;  // one division per lane, then products
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < J; ++j) {
       const float a0[4] = {__uint_as_float(r0[s][j].x), __uint_as_float(r0[s][j].y),
                            __uint_as_float(r0[s][j].z), __uint_as_float(r0[s][j].w)};
       const float a1[4] = {__uint_as_float(r1[s][j].x), __uint_as_float(r1[s][j].y),
@@ -387,22 +446,44 @@ __global__ __launch_bounds__(kBlock) void attn_o_halves_kernel(AttnOHalvesArgs a
       }
     }
   }
-  const float v = w8_row_dot<SLABS>(wq, sc, xv, row < a.n, a.k, lane);
+  const float v = F::template dot<SLABS>(wr, xv, row < a.n, a.k, lane);
   if (lane == 0 && row < a.n) gstore(a.x + row, f32_to_bf16(v + bf16_to_f32(res_raw)));
 }
 
-bool attn_o_halves_supported(int k) { return k % 64 == 0 && k <= 4 * kWave * 16; }
+// Slabs of 64 16-byte weight chunks spanning K (1024 int8 or 512 BF16
+// weights each).
+static int fused_slabs(int k, bool w8) {
+  const int per_slab = kWave * (w8 ? W8Fmt::C : Bf16Fmt::C);
+  return (k + per_slab - 1) / per_slab;
+}
 
-void launch_attn_o_halves(const AttnOHalvesArgs& a, hipStream_t stream) {
+bool attn_o_halves_supported(int k, bool w8) {
+  return k >= 64 && k % 64 == 0 && fused_slabs(k, w8) <= 4;
+}
+bool attn_o_halves_supported(int k) { return attn_o_halves_supported(k, true); }
+
+template <class F>
+static void launch_attn_o_halves_fmt(const AttnOHalvesArgs& a, hipStream_t stream) {
   const dim3 grid((a.n + kWaves - 1) / kWaves), block(kBlock);
-  const int slabs = (a.k + kWave * 16 - 1) / (kWave * 16);
+  const int slabs = fused_slabs(a.k, F::C == W8Fmt::C);
   if (slabs <= 1) {
-    hipLaunchKernelGGL((attn_o_halves_kernel<1>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((attn_o_halves_kernel<F, 1>), grid, block, 0, stream, a);
   } else if (slabs <= 2) {
-    hipLaunchKernelGGL((attn_o_halves_kernel<2>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((attn_o_halves_kernel<F, 2>), grid, block, 0, stream, a);
   } else {
-    hipLaunchKernelGGL((attn_o_halves_kernel<4>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((attn_o_halves_kernel<F, 4>), grid, block, 0, stream, a);
   }
+}
+
+void launch_attn_o_halves(const AttnOHalvesArgs& a, bool w8, hipStream_t stream) {
+  if (w8) {
+    launch_attn_o_halves_fmt<W8Fmt>(a, stream);
+  } else {
+    launch_attn_o_halves_fmt<Bf16Fmt>(a, stream);
+  }
+}
+void launch_attn_o_halves(const AttnOHalvesArgs& a, hipStream_t stream) {
+  launch_attn_o_halves(a, true, stream);
 }
 
 // The tied LM head of a decode step: logits = bf16(E rms_norm(x)) with the
@@ -680,12 +761,19 @@ __global__ __launch_bounds__(kBlock) void attn_o_gemv_kernel(AttnOArgs a) {
 
 bool gemv_w8_rows_supported(int k) { return k >= 64 && k % 64 == 0 && k <= 8192; }
 
-void launch_gemv_w8_rows(const GemvRowsArgs& a, hipStream_t stream) {
+// BF16 rows: up to 10 slabs of 512 weights (K <= 5120, the 4864 of the
+// Qwen2.5-0.5B down projection included).
+bool gemv_rows_supported(int k, bool w8) {
+  return w8 ? gemv_w8_rows_supported(k) : k >= 64 && k % 64 == 0 && k <= 10 * 512;
+}
+
+template <class F, int MAXS>
+static void launch_gemv_rows_fmt(const GemvRowsArgs& a, hipStream_t stream) {
   const dim3 grid((a.n + kWaves - 1) / kWaves), block(kBlock);
-  switch ((a.k + 1023) / 1024) {
+  switch (fused_slabs(a.k, F::C == W8Fmt::C)) {
 #define QLIN_ROWS(S)                                                                    \
   case S:                                                                               \
-    hipLaunchKernelGGL(gemv_w8_rows_kernel<S>, grid, block, 0, stream, a);              \
+    hipLaunchKernelGGL((gemv_rows_kernel<F, S>), grid, block, 0, stream, a);            \
     break;
     QLIN_ROWS(1)
     QLIN_ROWS(2)
@@ -694,42 +782,72 @@ void launch_gemv_w8_rows(const GemvRowsArgs& a, hipStream_t stream) {
     QLIN_ROWS(5)
     QLIN_ROWS(6)
     QLIN_ROWS(7)
+    QLIN_ROWS(8)
+    QLIN_ROWS(9)
     default:
-      hipLaunchKernelGGL(gemv_w8_rows_kernel<8>, grid, block, 0, stream, a);
+      hipLaunchKernelGGL((gemv_rows_kernel<F, MAXS>), grid, block, 0, stream, a);
       break;
 #undef QLIN_ROWS
   }
 }
 
-int norm_gemv_w8_slabs(int k) { return (k + 1023) / 1024; }
+void launch_gemv_rows(const GemvRowsArgs& a, bool w8, hipStream_t stream) {
+  if (w8) {
+    launch_gemv_rows_fmt<W8Fmt, 8>(a, stream);
+  } else {
+    launch_gemv_rows_fmt<Bf16Fmt, 10>(a, stream);
+  }
+}
+
+void launch_gemv_w8_rows(const GemvRowsArgs& a, hipStream_t stream) {
+  launch_gemv_rows(a, true, stream);
+}
+
+int norm_gemv_slabs(int k, bool w8) { return fused_slabs(k, w8); }
+int norm_gemv_w8_slabs(int k) { return norm_gemv_slabs(k, true); }
 
 int norm_qkv_rope_blocks(int heads, int kv_heads, int head_dim) {
   const int tasks = (heads + 2 * kv_heads) * (head_dim / 2);
   return (tasks + kWaves - 1) / kWaves;
 }
 
+bool norm_gemv_supported(int k, bool w8) {
+  return k >= 64 && k % 64 == 0 && norm_gemv_slabs(k, w8) <= kNormGemvMaxSlabs;
+}
+bool norm_gemv_w8_supported(int k) { return norm_gemv_supported(k, true); }
+
+bool norm_qkv_rope_supported(int k, int head_dim, bool w8) {
+  return norm_gemv_supported(k, w8) && head_dim % 2 == 0 && head_dim >= 2;
+}
 bool norm_qkv_rope_supported(int k, int head_dim) {
-  return k >= 64 && k % 64 == 0 && norm_gemv_w8_slabs(k) <= kNormGemvMaxSlabs &&
-         head_dim % 2 == 0 && head_dim >= 2;
+  return norm_qkv_rope_supported(k, head_dim, true);
 }
 
-void launch_norm_qkv_rope_w8(const QkvRopeArgs& a, hipStream_t stream) {
+template <class F>
+static void launch_norm_qkv_rope_fmt(const QkvRopeArgs& a, hipStream_t stream) {
   const dim3 grid(norm_qkv_rope_blocks(a.heads, a.kv_heads, a.head_dim)), block(kBlock);
-  switch (norm_gemv_w8_slabs(a.k)) {
+  switch (fused_slabs(a.k, F::C == W8Fmt::C)) {
     case 1:
-      hipLaunchKernelGGL(norm_qkv_rope_w8_kernel<1>, grid, block, 0, stream, a);
+      hipLaunchKernelGGL((norm_qkv_rope_kernel<F, 1>), grid, block, 0, stream, a);
       break;
     case 2:
-      hipLaunchKernelGGL(norm_qkv_rope_w8_kernel<2>, grid, block, 0, stream, a);
+      hipLaunchKernelGGL((norm_qkv_rope_kernel<F, 2>), grid, block, 0, stream, a);
       break;
     default:
-      hipLaunchKernelGGL(norm_qkv_rope_w8_kernel<4>, grid, block, 0, stream, a);
+      hipLaunchKernelGGL((norm_qkv_rope_kernel<F, 4>), grid, block, 0, stream, a);
       break;
   }
 }
 
-bool norm_gemv_w8_supported(int k) {
-  return k >= 64 && k % 64 == 0 && norm_gemv_w8_slabs(k) <= kNormGemvMaxSlabs;
+void launch_norm_qkv_rope(const QkvRopeArgs& a, bool w8, hipStream_t stream) {
+  if (w8) {
+    launch_norm_qkv_rope_fmt<W8Fmt>(a, stream);
+  } else {
+    launch_norm_qkv_rope_fmt<Bf16Fmt>(a, stream);
+  }
+}
+void launch_norm_qkv_rope_w8(const QkvRopeArgs& a, hipStream_t stream) {
+  launch_norm_qkv_rope(a, true, stream);
 }
 
 int norm_gemv_blocks(int n, int rows_per_wave) {
@@ -737,45 +855,58 @@ int norm_gemv_blocks(int n, int rows_per_wave) {
   return (n + rows - 1) / rows;
 }
 
-template <int SLABS, bool PAIR>
+template <class F, int SLABS, bool PAIR>
 static void launch_norm_gemv_rows(const NormGemvArgs& a, int blocks, hipStream_t stream) {
   switch (a.rows_per_wave) {
     case 4:
-      hipLaunchKernelGGL((norm_gemv_w8_kernel<SLABS, PAIR, 4>), dim3(blocks), dim3(kBlock), 0,
+      hipLaunchKernelGGL((norm_gemv_kernel<F, SLABS, PAIR, 4>), dim3(blocks), dim3(kBlock), 0,
                          stream, a);
       break;
     case 2:
-      hipLaunchKernelGGL((norm_gemv_w8_kernel<SLABS, PAIR, 2>), dim3(blocks), dim3(kBlock), 0,
+      hipLaunchKernelGGL((norm_gemv_kernel<F, SLABS, PAIR, 2>), dim3(blocks), dim3(kBlock), 0,
                          stream, a);
       break;
     default:
-      hipLaunchKernelGGL((norm_gemv_w8_kernel<SLABS, PAIR, 1>), dim3(blocks), dim3(kBlock), 0,
+      hipLaunchKernelGGL((norm_gemv_kernel<F, SLABS, PAIR, 1>), dim3(blocks), dim3(kBlock), 0,
                          stream, a);
       break;
   }
 }
 
-template <bool PAIR>
-static void launch_norm_gemv(const NormGemvArgs& a, int blocks, hipStream_t stream) {
-  switch (norm_gemv_w8_slabs(a.k)) {
+template <class F, bool PAIR>
+static void launch_norm_gemv_fmt(const NormGemvArgs& a, int blocks, hipStream_t stream) {
+  switch (fused_slabs(a.k, F::C == W8Fmt::C)) {
     case 1:
-      launch_norm_gemv_rows<1, PAIR>(a, blocks, stream);
+      launch_norm_gemv_rows<F, 1, PAIR>(a, blocks, stream);
       break;
     case 2:
-      launch_norm_gemv_rows<2, PAIR>(a, blocks, stream);
+      launch_norm_gemv_rows<F, 2, PAIR>(a, blocks, stream);
       break;
     default:
-      launch_norm_gemv_rows<4, PAIR>(a, blocks, stream);
+      launch_norm_gemv_rows<F, 4, PAIR>(a, blocks, stream);
       break;
+  }
+}
+
+void launch_norm_gemv(const NormGemvArgs& a, int blocks, bool pair, bool w8,
+                      hipStream_t stream) {
+  if (w8) {
+    if (pair) {
+      launch_norm_gemv_fmt<W8Fmt, true>(a, blocks, stream);
+    } else {
+      launch_norm_gemv_fmt<W8Fmt, false>(a, blocks, stream);
+    }
+  } else {
+    if (pair) {
+      launch_norm_gemv_fmt<Bf16Fmt, true>(a, blocks, stream);
+    } else {
+      launch_norm_gemv_fmt<Bf16Fmt, false>(a, blocks, stream);
+    }
   }
 }
 
 void launch_norm_gemv_w8(const NormGemvArgs& a, int blocks, bool pair, hipStream_t stream) {
-  if (pair) {
-    launch_norm_gemv<true>(a, blocks, stream);
-  } else {
-    launch_norm_gemv<false>(a, blocks, stream);
-  }
+  launch_norm_gemv(a, blocks, pair, true, stream);
 }
 
 int attn_o_slabs(int k, bool w8) {

@@ -9,15 +9,16 @@
 
 namespace qlin {
 
-// One GEMV of a fused RMSNorm + W8A16 GEMV launch.  Rows are 4 x
+// One GEMV of a fused RMSNorm + GEMV launch (W8A16: int8 weights and BF16
+// group-64 scales; BF16: BF16 weights, no scales).  Rows are 4 x
 // rows_per_wave per workgroup; block_begin is the launch's first workgroup
 // for this GEMV.
 // With the PAIR form, (w, s) are gate_proj, (w2, s2) up_proj and y the
 // SiLU-mul output; bias is unused.
 struct NormGemvDesc {
-  const int8_t* w;
+  const void* w;
   const uint16_t* s;
-  const int8_t* w2;
+  const void* w2;
   const uint16_t* s2;
   const uint16_t* bias;
   uint16_t* y;
@@ -26,12 +27,15 @@ struct NormGemvDesc {
 };
 
 constexpr int kNormGemvMaxDescs = 3;
-constexpr int kNormGemvMaxSlabs = 4;  // K <= 4096
+constexpr int kNormGemvMaxSlabs = 4;  // K <= 4096 int8 or 2048 BF16 weights
 // Rows (gate|up: row pairs) per wave of the decode step's fused launches:
-// measured at the Qwen2.5-0.5B shapes, two beat one (q|k|v 3.26 -> 3.07 us,
-// gate|up 5.14 -> 4.95 us per launch).
+// measured at the Qwen2.5-0.5B shapes, two beat one on int8 weights (q|k|v
+// 3.26 -> 3.07 us, gate|up 5.14 -> 4.95 us per launch); on BF16 weights
+// (rows twice as long) one row pair per wave is fastest (gate|up 5.70 us,
+// against 6.02 with two and 7.06 with four).
 constexpr int kQkvRowsPerWave = 2;
 constexpr int kGateUpRowsPerWave = 2;
+constexpr int kGateUpRowsPerWaveBf16 = 1;
 
 struct NormGemvArgs {
   const uint16_t* x;       // [k] BF16 (the residual stream)
@@ -43,9 +47,15 @@ struct NormGemvArgs {
   NormGemvDesc d[kNormGemvMaxDescs];
 };
 
+// Slabs of 64 16-byte chunks a row of K weights spans (W8A16: 1024
+// weights per slab, BF16: 512).
+int norm_gemv_slabs(int k, bool w8);
 int norm_gemv_w8_slabs(int k);
+bool norm_gemv_supported(int k, bool w8);
 bool norm_gemv_w8_supported(int k);
 int norm_gemv_blocks(int n, int rows_per_wave);
+void launch_norm_gemv(const NormGemvArgs& a, int blocks, bool pair, bool w8,
+                      hipStream_t stream);
 void launch_norm_gemv_w8(const NormGemvArgs& a, int blocks, bool pair, hipStream_t stream);
 
 // The decode step's q|k|v launch with the RoPE and the KV-cache store
@@ -59,13 +69,13 @@ struct QkvRopeArgs {
   const uint16_t* norm_w;  // [k] BF16 input RMSNorm weight
   float eps;
   int k;
-  const int8_t* wq;
-  const uint16_t* sq;
+  const void* wq;          // int8 (W8A16) or BF16
+  const uint16_t* sq;      // W8A16 group scales, else unused
   const uint16_t* bq;      // [heads * head_dim] or nullptr
-  const int8_t* wk;
+  const void* wk;
   const uint16_t* sk;
   const uint16_t* bk;      // [kv_heads * head_dim] or nullptr
-  const int8_t* wv;
+  const void* wv;
   const uint16_t* sv;
   const uint16_t* bv;
   uint16_t* q_out;         // [heads * head_dim]
@@ -81,15 +91,18 @@ struct QkvRopeArgs {
 
 // Workgroups of a launch (one wave per pair of output rows).
 int norm_qkv_rope_blocks(int heads, int kv_heads, int head_dim);
-bool norm_qkv_rope_supported(int k, int head_dim);
+bool norm_qkv_rope_supported(int k, int head_dim, bool w8);
+bool norm_qkv_rope_supported(int k, int head_dim);  // W8A16
+void launch_norm_qkv_rope(const QkvRopeArgs& a, bool w8, hipStream_t stream);
 void launch_norm_qkv_rope_w8(const QkvRopeArgs& a, hipStream_t stream);
 
-// One W8A16 GEMV row per wave with the whole row's loads in flight at once:
+// One GEMV row per wave with the whole row's loads in flight at once:
 // y[row] = bf16(W[row] . x + bias[row]), bias may alias y (the residual add).
-// K % 64 == 0, K <= 8192, 16-byte aligned w and x.
+// K % 64 == 0, 16-byte aligned w and x; K <= 8192 for W8A16 weights, K <=
+// 5120 for BF16 weights.
 struct GemvRowsArgs {
-  const void* w;         // [n, k] int8
-  const uint16_t* s;     // [n, k / 64] BF16 scales
+  const void* w;         // [n, k] int8 (W8A16) or BF16
+  const uint16_t* s;     // [n, k / 64] BF16 scales (W8A16)
   const uint16_t* bias;  // [n] BF16 or nullptr
   const uint16_t* x;     // [k] BF16
   uint16_t* y;           // [n] BF16
@@ -98,7 +111,9 @@ struct GemvRowsArgs {
 };
 
 bool gemv_w8_rows_supported(int k);
+bool gemv_rows_supported(int k, bool w8);
 void launch_gemv_w8_rows(const GemvRowsArgs& a, hipStream_t stream);
+void launch_gemv_rows(const GemvRowsArgs& a, bool w8, hipStream_t stream);
 
 // o-projection fused with the decode attention's split merge and the
 // residual add (x = bf16(Wo attn + x)).
@@ -121,26 +136,29 @@ struct AttnOArgs {
 
 bool attn_o_supported(int k, int heads, bool w8);
 
-// The fused decode step's o-projection (W8A16, group 64) with the merge of
-// the attention's two halves (launch_attention_decode_halves):
+// The fused decode step's o-projection (W8A16 group 64, or BF16) with the
+// merge of the attention's two halves (launch_attention_decode_halves):
 //   a[i] = bf16( sum_sp acc_sp[i] e^(m_sp - M) / sum_sp l_sp e^(m_sp - M) ),
 //   M = max_sp m_sp over the halves [0, pos / kAttnHalfSpan],
 //   x[row] = bf16(Wo[row] . a + x[row]).
-// Lane l's inputs (16 per 16-byte weight chunk) come from one head, so it
-// merges them from the two records in registers: no LDS, no barrier.
+// Lane l's inputs (16 per 16-byte weight chunk for W8A16, 8 for BF16) come
+// from one head, so it merges them from the two records in registers: no
+// LDS, no barrier.
 struct AttnOHalvesArgs {
   const float* partial;  // heads x 2 records of kAttnHalfRecord floats
   const int* pos;        // position of the decoded token (device)
   int heads;
   int max_seq;
-  const int8_t* w;       // [n, k] int8
-  const uint16_t* s;     // [n, k / 64] BF16 scales
+  const void* w;         // [n, k] int8 (W8A16) or BF16
+  const uint16_t* s;     // [n, k / 64] BF16 scales (W8A16)
   uint16_t* x;           // [n] residual stream, updated in place
   int n;
   int k;                 // heads x 64
 };
-bool attn_o_halves_supported(int k);
-void launch_attn_o_halves(const AttnOHalvesArgs& a, hipStream_t stream);
+bool attn_o_halves_supported(int k, bool w8);
+bool attn_o_halves_supported(int k);  // W8A16
+void launch_attn_o_halves(const AttnOHalvesArgs& a, bool w8, hipStream_t stream);
+void launch_attn_o_halves(const AttnOHalvesArgs& a, hipStream_t stream);  // W8A16
 void launch_attn_o_gemv(const AttnOArgs& a, bool w8, hipStream_t stream);
 
 constexpr int kLmHeadMaxSlabs = 8;  // K <= 4096

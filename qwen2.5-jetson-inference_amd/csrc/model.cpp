@@ -8,18 +8,20 @@
 // KV cache; it is allocated once at creation, and no prefill or decode call
 // allocates.
 //
-// Decode step (one token, position and token read from ModelState), W8A16:
+// Decode step (one token, position and token read from ModelState), W8A16
+// or W16A16 (the same launches, on int8 or BF16 weights):
 //   embedding; per layer five launches:
-//     RMSNorm + q|k|v GEMV (norm_gemv_w8),
-//     RoPE + KV store + attention split over the context (partials),
-//     split merge + o GEMV + residual (attn_o_gemv),
-//     RMSNorm + gate|up GEMV + SiLU-mul (norm_gemv_w8, paired rows),
-//     down GEMV + residual;
+//     RMSNorm + q|k|v GEMV + RoPE + KV store (norm_qkv_rope),
+//     attention over the context in two halves (partials),
+//     merge of the halves + o GEMV + residual (attn_o_halves),
+//     RMSNorm + gate|up GEMV + SiLU-mul (norm_gemv, paired rows),
+//     down GEMV + residual (gemv_rows);
 //   final RMSNorm + LM head + argmax + step bookkeeping (lm_head_decode).
 // Every launch is built to wait on one round of global loads: a decode
-// step is latency-bound, not bandwidth-bound.  W16A16 runs the unfused
-// norm / GEMV / SiLU-mul launches around the same attention, o and LM head
-// kernels.  The down GEMV's residual add rides on the GEMV's bias operand
+// step is latency-bound, not bandwidth-bound.  Shapes outside the fused
+// kernels' limits (hidden > 4096 int8 or 2048 BF16 weights, head_dim other
+// than 64, max_seq over 1024) run unfused norm / GEMV / SiLU-mul launches
+// around the split attention.  The down GEMV's residual add rides on the GEMV's bias operand
 // (bias = output = the residual stream): each output element is read as
 // bias and then written by the same lane, so the aliasing is safe.  With
 // use_graph the step is captured once and replayed per token.
@@ -94,9 +96,10 @@ struct infer_hip_model {
   infer_hip_model_config cfg{};
   bool w8 = false;
   bool use_graph = false;
-  bool fused_norm_gemv = false;  // W8A16 with hidden % 64 == 0, hidden <= 4096
+  // hidden % 64 == 0, hidden <= 4096 (W8A16) or 2048 (W16A16)
+  bool fused_norm_gemv = false;
   bool fused_lm_head = false;    // hidden % 8 == 0, hidden <= 4096
-  // the fused q|k|v launch also rotates q, k and stores k, v (W8A16 with the
+  // the fused q|k|v launch also rotates q, k and stores k, v (with the
   // whole-context decode attention: head_dim 64, max_seq <= 1024)
   bool fused_qkv_rope = false;
   int max_seq = 0;
@@ -358,9 +361,10 @@ int enqueue_decode_step(infer_hip_model* m, int only = -1, hipEvent_t* events = 
   for (const Layer& L : m->layers) {
     if (m->fused_norm_gemv) {
       if (m->fused_qkv_rope) {
-        run(kKindQkv, [&] { launch_norm_qkv_rope_w8(L.qkv_rope_args, s); });
+        run(kKindQkv, [&] { launch_norm_qkv_rope(L.qkv_rope_args, m->w8, s); });
       } else {
-        run(kKindQkv, [&] { launch_norm_gemv_w8(L.qkv_args, L.qkv_fused_blocks, false, s); });
+        run(kKindQkv,
+            [&] { launch_norm_gemv(L.qkv_args, L.qkv_fused_blocks, false, m->w8, s); });
       }
     } else {
       run(kKindNorm,
@@ -385,28 +389,23 @@ int enqueue_decode_step(infer_hip_model* m, int only = -1, hipEvent_t* events = 
       }
     });
     // x = bf16(Wo attn + x): attn is merged here from the attention's
-    // partials (the two halves, or the spans of the split form), or is the
-    // whole-context attention's output
+    // partials (the two halves, or the spans of the split form)
     run(kKindAttnO, [&] {
       if (m->fused_qkv_rope) {
-        launch_attn_o_halves({m->attn_partial, &m->state->pos, c.num_heads, m->max_seq,
-                              static_cast<const int8_t*>(L.o.w), L.o.s, m->x, hidden, hidden},
-                             s);
-      } else if (!attention_whole(m->max_seq, m->head_dim)) {
+        launch_attn_o_halves({m->attn_partial, &m->state->pos, c.num_heads, m->max_seq, L.o.w,
+                              L.o.s, m->x, hidden, hidden},
+                             m->w8, s);
+      } else {
         launch_attn_o_gemv({m->attn_partial, &m->state->pos, c.num_heads, m->head_dim,
                             attention_span(m->max_seq, m->head_dim),
                             attention_splits(m->max_seq, m->head_dim), m->max_seq, L.o.w, L.o.s,
                             m->x, hidden, hidden},
                            m->w8, s);
-      } else if (m->w8 && gemv_w8_rows_supported(hidden)) {
-        launch_gemv_w8_rows({L.o.w, L.o.s, m->x, m->attn, m->x, hidden, hidden}, s);
-      } else {
-        gemv(m, L.o, m->x, m->attn, m->x);
       }
     });
     if (m->fused_norm_gemv) {
       run(kKindGateUp,
-          [&] { launch_norm_gemv_w8(L.gate_up_args, L.gate_up_fused_blocks, true, s); });
+          [&] { launch_norm_gemv(L.gate_up_args, L.gate_up_fused_blocks, true, m->w8, s); });
     } else {
       run(kKindNorm,
           [&] { launch_rms_norm(m->x, L.post_norm, m->norm, 1, hidden, c.rms_norm_eps, s); });
@@ -421,8 +420,9 @@ int enqueue_decode_step(infer_hip_model* m, int only = -1, hipEvent_t* events = 
           [&] { launch_silu_mul(m->gate, m->up, m->mlp, c.intermediate_size, s); });
     }
     run(kKindDown, [&] {  // x = bf16(Wd mlp + x)
-      if (m->w8 && gemv_w8_rows_supported(L.down.k)) {
-        launch_gemv_w8_rows({L.down.w, L.down.s, m->x, m->mlp, m->x, L.down.n, L.down.k}, s);
+      if (gemv_rows_supported(L.down.k, m->w8)) {
+        launch_gemv_rows({L.down.w, L.down.s, m->x, m->mlp, m->x, L.down.n, L.down.k}, m->w8,
+                         s);
       } else {
         gemv(m, L.down, m->x, m->mlp, m->x);
       }
@@ -444,15 +444,13 @@ double kind_bytes(const infer_hip_model* m, int kind, int ctx, int* launches) {
   auto linear = [&](double n, double k) {
     return n * k * wb + (m->w8 ? 2.0 * n * (k / 64) : 0.0);
   };
-  // the attention's output: the records of the halves or of the split
-  // form's spans, or the BF16 head outputs of the whole-context form
+  // the attention's output: the (acc, max, sum) records of the halves or
+  // of the split form's spans (a record's padding is not counted)
   const int span = m->fused_qkv_rope ? kAttnHalfSpan : attention_span(m->max_seq, m->head_dim);
   const double splits = (ctx + span - 1) / span;
-  const double partials = (attention_whole(m->max_seq, m->head_dim) && !m->fused_qkv_rope)
-                              ? 2 * H
-                              : c.num_heads * splits * (hd + 2) * 4;
+  const double partials = c.num_heads * splits * (hd + 2) * 4;
   const bool fused = m->fused_norm_gemv;
-  const bool bf16_split = !m->w8;  // separate q, k, v (and gate, up) launches
+  const bool bf16_split = !m->w8 && !fused;  // separate q, k, v (and gate, up) launches
   int n = 0;
   double b = 0.0;
   switch (kind) {
@@ -728,11 +726,18 @@ extern "C" int infer_hip_model_create(const infer_hip_model_config* config,
   m->embed = weights->embed_tokens;
   m->final_norm = weights->norm;
   m->lm_head = lm_head;
-  m->fused_norm_gemv = w8 && norm_gemv_w8_supported(hidden);
+  m->fused_norm_gemv = norm_gemv_supported(hidden, w8);
   m->fused_lm_head = lm_head_decode_supported(hidden);
   m->fused_qkv_rope = m->fused_norm_gemv && attention_whole(max_seq, head_dim) &&
-                      norm_qkv_rope_supported(hidden, head_dim) &&
-                      attn_o_halves_supported(hidden);
+                      norm_qkv_rope_supported(hidden, head_dim, w8) &&
+                      attn_o_halves_supported(hidden, w8);
+  // The unfused step runs the split attention, which needs head_dim 128 or
+  // more than kAttnWholeMax positions; head_dim 64 means at most 32 x 64 =
+  // 2048 hidden, always within the fused launches' limits.
+  if (attention_whole(max_seq, head_dim) && !m->fused_qkv_rope) {
+    destroy_model(m);
+    return fail(INFER_HIP_RUNTIME_ERROR, "model: no decode attention form for this shape");
+  }
 
   // Arena layout.
   size_t cursor = 0;
@@ -870,11 +875,11 @@ extern "C" int infer_hip_model_create(const infer_hip_model_config* config,
       host_tables.push_back(desc(L.up, m->norm, m->up, L.gate_up_blocks));
     }
     if (m->fused_norm_gemv) {
+      const int gate_up_rows = w8 ? kGateUpRowsPerWave : kGateUpRowsPerWaveBf16;
       auto fdesc = [](const Linear& li, const Linear* pair, uint16_t* y, int rows_per_wave,
                       int& blocks) {
-        NormGemvDesc d{static_cast<const int8_t*>(li.w), li.s,
-                       pair ? static_cast<const int8_t*>(pair->w) : nullptr,
-                       pair ? pair->s : nullptr, li.b, y, li.n, blocks};
+        NormGemvDesc d{li.w, li.s, pair ? pair->w : nullptr, pair ? pair->s : nullptr, li.b, y,
+                       li.n, blocks};
         blocks += norm_gemv_blocks(li.n, rows_per_wave);
         return d;
       };
@@ -883,16 +888,14 @@ extern "C" int infer_hip_model_create(const infer_hip_model_config* config,
       L.qkv_args.d[1] = fdesc(L.k, nullptr, m->k, kQkvRowsPerWave, L.qkv_fused_blocks);
       L.qkv_args.d[2] = fdesc(L.v, nullptr, m->v, kQkvRowsPerWave, L.qkv_fused_blocks);
       L.qkv_rope_args = QkvRopeArgs{m->x, L.in_norm, c.rms_norm_eps, hidden,
-                                    static_cast<const int8_t*>(L.q.w), L.q.s, L.q.b,
-                                    static_cast<const int8_t*>(L.k.w), L.k.s, L.k.b,
-                                    static_cast<const int8_t*>(L.v.w), L.v.s, L.v.b,
+                                    L.q.w, L.q.s, L.q.b, L.k.w, L.k.s, L.k.b, L.v.w, L.v.s, L.v.b,
                                     m->q, L.key_cache, L.value_cache, m->rope_cur,
                                     &m->state->pos,
                                     c.num_heads, c.num_kv_heads, head_dim, max_seq};
       L.gate_up_args =
-          NormGemvArgs{m->x, L.post_norm, c.rms_norm_eps, hidden, 1, kGateUpRowsPerWave, {}};
+          NormGemvArgs{m->x, L.post_norm, c.rms_norm_eps, hidden, 1, gate_up_rows, {}};
       L.gate_up_args.d[0] =
-          fdesc(L.gate, &L.up, m->mlp, kGateUpRowsPerWave, L.gate_up_fused_blocks);
+          fdesc(L.gate, &L.up, m->mlp, gate_up_rows, L.gate_up_fused_blocks);
     }
   }
   // Every region the kernels write must lie inside the arena.

@@ -583,13 +583,6 @@ __device__ __forceinline__ float group8_lane(float v) {
   return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x18 | (J << 5)));
 }
 
-// Sum over the lane's group of 8 lanes; every lane of the group gets it.
-__device__ __forceinline__ float group8_sum(float v) {
-  v += dpp_from<kDppRowHalfMirror>(v);
-  v += dpp_from<kDppQuadSwap2>(v);
-  return v + dpp_from<kDppQuadSwap1>(v);
-}
-
 // Reduce-scatter of v[0..8) over the lane's group of 8: returns the group
 // total of v[l % 8].  The first step pairs lane i with 7 - i (half-row
 // mirror); they differ in bit 2, which picks the half each keeps.
@@ -652,35 +645,6 @@ __device__ __forceinline__ void unpack8_bf16(const uint4 w, float (&o)[8]) {
   o[4] = bf16_lo(w.z); o[5] = bf16_hi(w.z); o[6] = bf16_lo(w.w); o[7] = bf16_hi(w.w);
 }
 
-// The lane l ^ 4 (ds_swizzle, bit-mask mode): the lane holding the
-// rotation partner piece.
-__device__ __forceinline__ uint32_t partner4(uint32_t v) {
-  return static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v), 0x1F | (4 << 10)));
-}
-
-// RoPE of the lane's 8 dimensions from its piece and the partner lane's
-// (piece pc ^ 4), rounded to BF16: out[t] as a value, words[t] as BF16 bits.
-__device__ __forceinline__ void rope_piece(const uint4 mine, const float2* cs, bool second,
-                                           float (&out)[8], uint32_t (&words)[4]) {
-  const uint4 other = make_uint4(partner4(mine.x), partner4(mine.y), partner4(mine.z),
-                                 partner4(mine.w));
-  float a[8], b[8];
-  unpack8_bf16(mine, a);
-  unpack8_bf16(other, b);
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    // first half: a c - b s; second half (partner in the first): a c + b s
-    const float r = second ? a[t] * cs[t].x + b[t] * cs[t].y : a[t] * cs[t].x - b[t] * cs[t].y;
-    const uint16_t w = f32_to_bf16(r);
-    out[t] = bf16_to_f32(w);
-    if (t & 1) {
-      words[t / 2] |= static_cast<uint32_t>(w) << 16;
-    } else {
-      words[t / 2] = w;
-    }
-  }
-}
-
 // Workgroups of the whole-context attention.  Workgroup b runs on XCD
 // b % kXcds (the dispatcher deals workgroups to the XCDs in turn), and each
 // XCD has its own L2: the query heads that share a kv head are given
@@ -703,22 +667,16 @@ __device__ inline int whole_attention_head(int b, int heads, int kv_heads) {
   return g < kv_heads ? g * group + t % group : -1;
 }
 
-// Waves of the whole-context workgroup (two tiles each, both in flight).
-// Measured at contexts 256-1023 (pre-rotated, us per launch): 8 waves x 2
-// tiles 4.4-6.4, 16 x 1 4.3-8.3, 4 x 4 5.0-7.7.
-template <bool ROPED>
-constexpr int whole_waves() {
-  return kWholeWaves;
-}
-
-template <bool ROPED>
-__global__ __launch_bounds__(whole_waves<ROPED>() * kWave) void attention_decode_whole_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_new,
-    const uint16_t* __restrict__ v_new, uint16_t* __restrict__ key_cache,
-    uint16_t* __restrict__ value_cache, const float2* __restrict__ rope,
-    const int* __restrict__ pos_ptr, int heads, int kv_heads, int max_seq,
-    uint16_t* __restrict__ out) {
-  constexpr int HD = 64, W = whole_waves<ROPED>(), half = HD / 2;
+// The whole-context attention of a pre-rotated q over caches that hold the
+// new token's k and v already (attention_decode_bf16, kernels.cu:400-490).
+// Waves of the workgroup: kWholeWaves, two tiles each, both in flight.
+// Measured at contexts 256-1023 (us per launch): 8 waves x 2 tiles
+// 4.4-6.4, 16 x 1 4.3-8.3, 4 x 4 5.0-7.7.
+__global__ __launch_bounds__(kWholeWaves * kWave) void attention_decode_whole_kernel(
+    const uint16_t* __restrict__ q, uint16_t* __restrict__ key_cache,
+    uint16_t* __restrict__ value_cache, const int* __restrict__ pos_ptr, int heads,
+    int kv_heads, int max_seq, uint16_t* __restrict__ out) {
+  constexpr int HD = 64, W = kWholeWaves;
   constexpr int kPieces = HD / 8;            // 16-byte pieces per row (8)
   constexpr int kRowsPer = kWave / kPieces;  // rows per load instruction (8)
   constexpr bool kPrefetch = true;           // a second tile per wave
@@ -732,25 +690,9 @@ __global__ __launch_bounds__(whole_waves<ROPED>() * kWave) void attention_decode
   const size_t head_base = static_cast<size_t>(g) * max_seq * HD;
   const uint4* qh = reinterpret_cast<const uint4*>(q + static_cast<size_t>(h) * HD);
   const uint4 q_mine = qh[pc];
-  uint4 k_mine = make_uint4(0, 0, 0, 0), v_mine = make_uint4(0, 0, 0, 0);
-  float2 cs[8];
-  int pos, rows;  // rows: the cache rows the tiles may read
-  if constexpr (ROPED) {
-    // q is rotated and the new token's k and v are in the caches already:
-    // the tiles cover [0, pos] and go out before pos is known (rows past
-    // the context are masked below).
-    rows = max_seq;
-    pos = 0;
-  } else {
-    // Small loads first: the kv head's new k and v, the angles of pos.
-    k_mine = reinterpret_cast<const uint4*>(k_new + static_cast<size_t>(g) * HD)[pc];
-    v_mine = reinterpret_cast<const uint4*>(v_new + static_cast<size_t>(g) * HD)[pc];
-    pos = min(*pos_ptr, max_seq - 1);
-    const float2* r = rope + static_cast<size_t>(pos) * half + 8 * (pc & 3);
-#pragma unroll
-    for (int t = 0; t < 8; ++t) cs[t] = r[t];
-    rows = pos;  // the new token's row comes from k_new / v_new
-  }
+  // The tiles cover [0, pos] and go out before pos is known (rows past the
+  // context are masked below).
+  const int rows = max_seq;  // the cache rows the tiles may read
   __builtin_amdgcn_sched_barrier(0);  // the small loads go out before the tiles
   const __amdgpu_buffer_rsrc_t kr_rsrc =
       __builtin_amdgcn_make_buffer_rsrc(key_cache + head_base, 0, rows * HD * 2, 0x00020000);
@@ -771,15 +713,15 @@ __global__ __launch_bounds__(whole_waves<ROPED>() * kWave) void attention_decode
   };
   uint4 kr[kPieces], vr[kPieces], kn[kPieces], vn[kPieces];
   load_tile(wave * kTile, kr_rsrc, vr_rsrc, kr, vr);
-  if constexpr (ROPED) pos = min(*pos_ptr, max_seq - 1);
+  const int pos = min(*pos_ptr, max_seq - 1);
   // Positions [0, end) come from the tiles.
-  const int end = ROPED ? pos + 1 : pos;
+  const int end = pos + 1;
   if (kPrefetch) {
     // The first tiles went out before the position arrived.  The second
     // tiles are bounded by the context: rows past it read as 0 without a
     // memory access (and are masked below), so the CU takes in only the
     // context's rows beyond the first W tiles.
-    const uint32_t bytes = static_cast<uint32_t>(ROPED ? end : rows) * HD * 2;
+    const uint32_t bytes = static_cast<uint32_t>(end) * HD * 2;
     load_tile((wave + W) * kTile,
               __builtin_amdgcn_make_buffer_rsrc(key_cache + head_base, 0, bytes, 0x00020000),
               __builtin_amdgcn_make_buffer_rsrc(value_cache + head_base, 0, bytes, 0x00020000),
@@ -787,31 +729,7 @@ __global__ __launch_bounds__(whole_waves<ROPED>() * kWave) void attention_decode
   }
 
   const float scale = 1.0f / sqrtf(static_cast<float>(HD));
-  uint32_t qw[4];  // the lane's 8 q dimensions, BF16 pairs
-  float snew = 0.0f;
-  if constexpr (ROPED) {
-    qw[0] = q_mine.x;
-    qw[1] = q_mine.y;
-    qw[2] = q_mine.z;
-    qw[3] = q_mine.w;
-  } else {
-    // q and the new k rotated and rounded to BF16 (as the reference's rope
-    // kernel stores them), each lane its 8 dimensions.
-    const bool second = pc >= kPieces / 2;  // dimensions of the second half
-    float qv[8], kv[8];
-    uint32_t kw[4];
-    rope_piece(q_mine, cs, second, qv, qw);
-    rope_piece(k_mine, cs, second, kv, kw);
-    if (h % group == 0 && wave == 0 && rg == 0) {
-      // The kv head's first query head stores the new token's k and v.
-      const size_t at = head_base + static_cast<size_t>(pos) * HD + 8 * pc;
-      *reinterpret_cast<uint4*>(key_cache + at) = make_uint4(kw[0], kw[1], kw[2], kw[3]);
-      *reinterpret_cast<uint4*>(value_cache + at) = v_mine;
-    }
-#pragma unroll
-    for (int t = 0; t < 8; ++t) snew = fmaf(qv[t], kv[t], snew);
-    snew = group8_sum(snew) * scale;
-  }
+  const uint32_t qw[4] = {q_mine.x, q_mine.y, q_mine.z, q_mine.w};  // 8 q dimensions
 
   float m = -INFINITY, l = 0.0f;
   float acc8[8];
@@ -860,35 +778,21 @@ __global__ __launch_bounds__(whole_waves<ROPED>() * kWave) void attention_decode
   if (kPrefetch) tile((wave + W) * kTile, kn, vn);
   const float mine = rows8_reduce_scatter(acc8, lane);  // dimension 8 pc + rg
 
-  __shared__ float wm[W + 1], wl[W + 1];
-  __shared__ float wacc[W + 1][HD];
+  __shared__ float wm[W], wl[W];
+  __shared__ float wacc[W][HD];
   if (lane == 0) {
     wm[wave] = m;
     wl[wave] = l;
   }
   wacc[wave][8 * pc + rg] = mine;
-  if (wave == 0 && rg == 0) {
-    // the new token's record (max = its score, sum = 1, acc = its value),
-    // when it did not come from the tiles
-    if constexpr (!ROPED) {
-      float vf[8];
-      unpack8_bf16(v_mine, vf);
-#pragma unroll
-      for (int t = 0; t < 8; ++t) wacc[W][8 * pc + t] = vf[t];
-    }
-    if (pc == 0) {
-      wm[W] = ROPED ? -INFINITY : snew;
-      wl[W] = ROPED ? 0.0f : 1.0f;
-    }
-  }
   __syncthreads();
   if (tid < HD) {
-    float mm = wm[W];
+    float mm = wm[0];
 #pragma unroll
-    for (int w = 0; w < W; ++w) mm = fmaxf(mm, wm[w]);
+    for (int w = 1; w < W; ++w) mm = fmaxf(mm, wm[w]);
     float ll = 0.0f, aa = 0.0f;
 #pragma unroll
-    for (int w = 0; w <= W; ++w) {
+    for (int w = 0; w < W; ++w) {
       const float f = wl[w] > 0.0f ? expf(wm[w] - mm) : 0.0f;
       ll = fmaf(wl[w], f, ll);
       aa = fmaf(wacc[w][tid], f, aa);
@@ -1457,18 +1361,10 @@ void launch_attention_decode(const uint16_t* q, const uint16_t* k_new, const uin
                              const int* pos, int heads, int kv_heads, int head_dim,
                              int max_seq, bool roped, float* partial, uint16_t* out,
                              hipStream_t stream) {
-  if (attention_whole(max_seq, head_dim)) {
-    if (roped) {
-      hipLaunchKernelGGL(attention_decode_whole_kernel<true>,
-                         dim3(whole_attention_blocks(heads, kv_heads)),
-                         dim3(whole_waves<true>() * kWave), 0, stream, q, k_new, v_new,
-                         key_cache, value_cache, rope, pos, heads, kv_heads, max_seq, out);
-    } else {
-      hipLaunchKernelGGL(attention_decode_whole_kernel<false>,
-                         dim3(whole_attention_blocks(heads, kv_heads)),
-                         dim3(whole_waves<false>() * kWave), 0, stream, q, k_new, v_new,
-                         key_cache, value_cache, rope, pos, heads, kv_heads, max_seq, out);
-    }
+  if (attention_whole(max_seq, head_dim) && roped) {
+    hipLaunchKernelGGL(attention_decode_whole_kernel,
+                       dim3(whole_attention_blocks(heads, kv_heads)), dim3(kWholeWaves * kWave),
+                       0, stream, q, key_cache, value_cache, pos, heads, kv_heads, max_seq, out);
     return;
   }
   const int span = attention_span(max_seq, head_dim);

@@ -33,14 +33,16 @@ void launch_rms_norm(const uint16_t* x, const uint16_t* w, uint16_t* out, int ro
 void launch_rope_store(uint16_t* q, uint16_t* k, const uint16_t* v, uint16_t* key_cache,
                        uint16_t* value_cache, const float2* rope, int count, int start,
                        int heads, int kv_heads, int head_dim, int max_seq, hipStream_t stream);
-// Decode attention (see attention_decode_kernel).  head_dim 64 with up to
-// kAttnWholeMax positions of KV capacity: one workgroup per query head over
-// the whole context, writing the BF16 attention output to out (heads x
-// head_dim); otherwise one workgroup per (span, query head), spans of
-// attention_span() positions, at most kAttnMaxSplits of them, writing
-// partial (heads x attention_splits() x (head_dim + 2) floats) for the
-// o-projection to merge.  In the whole form span = kAttnWholeMax and
-// splits = 1.
+// Decode attention (see attention_decode_kernel).  roped, head_dim 64 and
+// up to kAttnWholeMax positions of KV capacity: one workgroup per query head
+// over the whole context, writing the BF16 attention output to out (heads x
+// head_dim; the attention_decode_bf16 operator).  Otherwise one workgroup
+// per (span, query head), spans of attention_span() positions, at most
+// kAttnMaxSplits of them, writing partial (heads x attention_splits() x
+// (head_dim + 2) floats) for the o-projection to merge (the decode step of
+// models outside the fused kernels' limits, whose attention is never the
+// whole form: those have head_dim 128 or more than kAttnWholeMax
+// positions).
 constexpr int kAttnWaves = 2;
 constexpr int kAttnMaxSplits = 8;
 constexpr int kAttnWholeMax = 1024;
@@ -60,10 +62,9 @@ void launch_attention_decode_halves(const uint16_t* q, const uint16_t* key_cache
                                     hipStream_t stream);
 int attention_span(int max_seq, int head_dim);
 int attention_splits(int max_seq, int head_dim);
-// roped (whole form only): q is already rotated and the token's k and v are
-// in the caches at pos (the fused q|k|v launch did both); otherwise q and
-// k_new are rotated here and the first query head of each kv head stores
-// k_new and v_new at pos.
+// roped (whole form): q is already rotated and the token's k and v are in
+// the caches at pos; otherwise (split form) q and k_new are rotated here and
+// the first query head of each kv head stores k_new and v_new at pos.
 // pos: the token's position (device memory).
 void launch_attention_decode(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
                              uint16_t* key_cache, uint16_t* value_cache, const float2* rope,

@@ -29,10 +29,15 @@ GROUP8 = S.ModelConfig(hidden_size=1024, intermediate_size=512, num_layers=1, nu
                        num_kv_heads=2, vocab_size=512)
 QWEN_SHAPED = S.ModelConfig(hidden_size=896, intermediate_size=4864, num_layers=2,
                             num_heads=14, num_kv_heads=2, vocab_size=4096)
+# hidden 2560: past the fused decode GEMVs' BF16 limit (2048), so W16A16
+# decodes with the separate RMSNorm / GEMV / SiLU-mul launches (W8A16 stays
+# fused up to 4096).
+WIDE_BF16 = S.ModelConfig(hidden_size=2560, intermediate_size=512, num_layers=1, num_heads=20,
+                          num_kv_heads=4, vocab_size=512)
 
 # Larger weights than a real init so that attention is peaked (scores of a
 # few units): a wrong position, rotation or head mapping changes the output.
-STD = {TINY: 0.15, HD128: 0.06, GROUP8: 0.05, QWEN_SHAPED: 0.05}
+STD = {TINY: 0.15, HD128: 0.06, GROUP8: 0.05, QWEN_SHAPED: 0.05, WIDE_BF16: 0.04}
 
 _cache = {}
 
@@ -89,8 +94,8 @@ def test_prefill_matches_oracle(orc, dev, precision, length):
     g.close()
 
 
-@pytest.mark.parametrize("cfg", [TINY, HD128, GROUP8, QWEN_SHAPED],
-                         ids=["tiny", "hd128", "group8", "qwen_shaped"])
+@pytest.mark.parametrize("cfg", [TINY, HD128, GROUP8, QWEN_SHAPED, WIDE_BF16],
+                         ids=["tiny", "hd128", "group8", "qwen_shaped", "wide_bf16"])
 @pytest.mark.parametrize("precision", ["w8a16", "w16a16"])
 @pytest.mark.parametrize("graph", [True, False], ids=["graph", "eager"])
 def test_teacher_forced_decode(orc, dev, cfg, precision, graph):
@@ -383,9 +388,10 @@ def test_split_attention_decode_across_eight_spans(orc, dev, cfg, precision, sta
 
 
 def test_whole_context_attention_qwen_shaped(orc, dev):
-    """KV capacity 1024: one workgroup per query head over the whole
-    context, up to position 1023 (every one of its 16 waves busy), with
-    14 query / 2 KV heads."""
+    """KV capacity 1024: the attention in two halves of 512 positions (one
+    workgroup per query head and half, merged in the o-projection), up to
+    position 1023 (every wave of both halves busy), with 14 query / 2 KV
+    heads."""
     cfg, precision = QWEN_SHAPED, "w8a16"
     t = S.random_model(cfg, precision, seed=17, std=0.05)
     fp32 = S.dequantized_fp32(t, cfg)
