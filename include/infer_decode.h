@@ -37,6 +37,14 @@
  *   infer_hip_rms_norm_lm_head_argmax  rms_norm_bf16 + lm_head_bf16
  *                                      (cuda_ops.hpp:42-45; qwen2.cpp:660-667)
  *
+ * The _w8a16 operators have _bf16 siblings for BF16 weights (the W16A16
+ * decode step, with gemv_bf16, cuda_ops.hpp:24-26, in place of gemv_w8a16):
+ * infer_hip_rms_norm_gemv_bf16, infer_hip_rms_norm_gate_up_silu_bf16,
+ * infer_hip_rms_norm_qkv_rope_bf16, infer_hip_attention_halves_o_proj_bf16
+ * and infer_hip_gemv_bf16_rows.  They run the same kernels instantiated for
+ * 8 BF16 weights per 16-byte chunk instead of 16 int8 ones, so their K
+ * limits are half the W8A16 ones.
+ *
  * Numerics are those of the unfused ops: the normalised activations are
  * rounded to BF16 as rms_norm_bf16 stores them, gate and up are rounded to
  * BF16 before SiLU-mul, sums are FP32 and outputs BF16 round-to-nearest-
@@ -46,7 +54,7 @@
  * std::max_element (src/cpu_ops.cpp:175-177).
  *
  * Preconditions, checked on the host (status INFER_HIP_INVALID_ARGUMENT):
- * in_features % 64 == 0 for the W8A16 operators, 16-byte aligned weight,
+ * in_features % 64 == 0 for the Linear operators, 16-byte aligned weight,
  * input and norm-weight pointers, and the size limits of each entry point.
  * Every entry point is asynchronous on `stream`, allocates nothing and
  * returns an infer_linear.h status, with the message in
@@ -83,6 +91,21 @@ int infer_hip_rms_norm_gemv_w8a16(const uint16_t* input, const uint16_t* norm_we
                                   const infer_hip_norm_gemv* gemvs, int count,
                                   hipStream_t stream);
 
+/* One GEMV of infer_hip_rms_norm_gemv_bf16 (BF16 weights). */
+typedef struct infer_hip_norm_gemv_bf16 {
+  const uint16_t* weight; /* BF16 [out_features, in_features] */
+  const uint16_t* bias;   /* BF16 [out_features] or NULL */
+  uint16_t* output;       /* BF16 [out_features] */
+  int out_features;
+} infer_hip_norm_gemv_bf16;
+
+/* infer_hip_rms_norm_gemv_w8a16 on BF16 weights (the W16A16 decode step):
+ * output = bf16(W xn + bias).  in_features <= 2048. */
+int infer_hip_rms_norm_gemv_bf16(const uint16_t* input, const uint16_t* norm_weight,
+                                 float epsilon, int in_features,
+                                 const infer_hip_norm_gemv_bf16* gemvs, int count,
+                                 hipStream_t stream);
+
 /* xn as above; output[i] = bf16(silu(g) * u) with g = bf16(gate_i . xn),
  * u = bf16(up_i . xn) (src/cpu_ops.cpp:168-173 on BF16 operands), one
  * launch.  in_features <= 4096. */
@@ -93,6 +116,14 @@ int infer_hip_rms_norm_gate_up_silu_w8a16(const uint16_t* input, const uint16_t*
                                           const int8_t* up_weight, const uint16_t* up_scales,
                                           uint16_t* output, int intermediate_size,
                                           hipStream_t stream);
+
+/* The same on BF16 gate and up weights ([intermediate_size, in_features]).
+ * in_features <= 2048. */
+int infer_hip_rms_norm_gate_up_silu_bf16(const uint16_t* input, const uint16_t* norm_weight,
+                                         float epsilon, int in_features,
+                                         const uint16_t* gate_weight,
+                                         const uint16_t* up_weight, uint16_t* output,
+                                         int intermediate_size, hipStream_t stream);
 
 /* The decode step's q|k|v launch (W8A16, group 64): xn as above;
  * q = bf16(Wq xn + bq), k = bf16(Wk xn + bk), v = bf16(Wv xn + bv); q and k
@@ -119,6 +150,23 @@ int infer_hip_rms_norm_qkv_rope_w8a16(const uint16_t* input, const uint16_t* nor
                                       const float* rope_row, const int* position,
                                       int num_heads, int num_kv_heads, int head_dim,
                                       int max_sequence_length, hipStream_t stream);
+
+/* The same q|k|v launch on BF16 weights ([heads x head_dim, in_features]).
+ * in_features <= 2048. */
+typedef struct infer_hip_bf16_weight {
+  const uint16_t* weight; /* BF16 [out_features, in_features] */
+  const uint16_t* bias;   /* BF16 [out_features] or NULL */
+} infer_hip_bf16_weight;
+
+int infer_hip_rms_norm_qkv_rope_bf16(const uint16_t* input, const uint16_t* norm_weight,
+                                     float epsilon, int in_features,
+                                     const infer_hip_bf16_weight* q_proj,
+                                     const infer_hip_bf16_weight* k_proj,
+                                     const infer_hip_bf16_weight* v_proj, uint16_t* q_out,
+                                     uint16_t* key_cache, uint16_t* value_cache,
+                                     const float* rope_row, const int* position,
+                                     int num_heads, int num_kv_heads, int head_dim,
+                                     int max_sequence_length, hipStream_t stream);
 
 /* (cos, sin) of position * theta^(-2 i / head_dim) for i < head_dim / 2,
  * in FP32 with the CPU path's arithmetic (src/cpu_ops.cpp:38-41):
@@ -167,6 +215,13 @@ int infer_hip_attention_halves_o_proj_w8a16(const float* records, const int* pos
                                             uint16_t* residual, int out_features,
                                             hipStream_t stream);
 
+/* The same on a BF16 weight [out_features, num_heads * 64];
+ * num_heads * 64 <= 2048. */
+int infer_hip_attention_halves_o_proj_bf16(const float* records, const int* position,
+                                           int num_heads, int max_sequence_length,
+                                           const uint16_t* weight, uint16_t* residual,
+                                           int out_features, hipStream_t stream);
+
 /* output[n] = bf16(sum_k q[n,k] s[n,k/64] input[k] + bias[n]) with one
  * wave per output row and the whole row in flight at once.  bias may be
  * NULL or equal to output (the in-place residual add of the decode step:
@@ -176,11 +231,17 @@ int infer_hip_gemv_w8a16_rows(const int8_t* weight, const uint16_t* scales,
                               const uint16_t* bias, const uint16_t* input, uint16_t* output,
                               int out_features, int in_features, hipStream_t stream);
 
+/* The same on a BF16 weight [out_features, in_features]:
+ * output[n] = bf16(sum_k w[n,k] input[k] + bias[n]).  in_features <= 5120. */
+int infer_hip_gemv_bf16_rows(const uint16_t* weight, const uint16_t* bias,
+                             const uint16_t* input, uint16_t* output, int out_features,
+                             int in_features, hipStream_t stream);
+
 /* Context span and split count of the decode attention at a KV capacity of
  * max_sequence_length positions and head_dim (64 or 128): split i covers
  * positions [i * span, (i + 1) * span).  At head_dim 64 with up to 1024
- * positions the decode step runs one workgroup per head over the whole
- * context (span 1024, 1 split) and its o-projection is a plain GEMV;
+ * positions the context is covered whole (span 1024, 1 split: the decode
+ * step then runs the two halves of infer_hip_attention_decode_halves_bf16);
  * otherwise at most 8 splits, whose partials the o-projection merges.
  * 0 for max_sequence_length < 1 or another head_dim. */
 int infer_hip_attention_decode_span(int max_sequence_length, int head_dim);

@@ -460,7 +460,6 @@ static int fused_slabs(int k, bool w8) {
 bool attn_o_halves_supported(int k, bool w8) {
   return k >= 64 && k % 64 == 0 && fused_slabs(k, w8) <= 4;
 }
-bool attn_o_halves_supported(int k) { return attn_o_halves_supported(k, true); }
 
 template <class F>
 static void launch_attn_o_halves_fmt(const AttnOHalvesArgs& a, hipStream_t stream) {
@@ -481,9 +480,6 @@ void launch_attn_o_halves(const AttnOHalvesArgs& a, bool w8, hipStream_t stream)
   } else {
     launch_attn_o_halves_fmt<Bf16Fmt>(a, stream);
   }
-}
-void launch_attn_o_halves(const AttnOHalvesArgs& a, hipStream_t stream) {
-  launch_attn_o_halves(a, true, stream);
 }
 
 // The tied LM head of a decode step: logits = bf16(E rms_norm(x)) with the
@@ -759,12 +755,11 @@ __global__ __launch_bounds__(kBlock) void attn_o_gemv_kernel(AttnOArgs a) {
 
 // ------------------------------------------------------------ launchers --
 
-bool gemv_w8_rows_supported(int k) { return k >= 64 && k % 64 == 0 && k <= 8192; }
-
-// BF16 rows: up to 10 slabs of 512 weights (K <= 5120, the 4864 of the
-// Qwen2.5-0.5B down projection included).
+// int8 rows: up to 8 slabs of 1024 weights (K <= 8192); BF16 rows: up to 10
+// slabs of 512 (K <= 5120, the 4864 of the Qwen2.5-0.5B down projection
+// included).
 bool gemv_rows_supported(int k, bool w8) {
-  return w8 ? gemv_w8_rows_supported(k) : k >= 64 && k % 64 == 0 && k <= 10 * 512;
+  return k >= 64 && k % 64 == 0 && k <= (w8 ? 8 * 1024 : 10 * 512);
 }
 
 template <class F, int MAXS>
@@ -799,12 +794,7 @@ void launch_gemv_rows(const GemvRowsArgs& a, bool w8, hipStream_t stream) {
   }
 }
 
-void launch_gemv_w8_rows(const GemvRowsArgs& a, hipStream_t stream) {
-  launch_gemv_rows(a, true, stream);
-}
-
 int norm_gemv_slabs(int k, bool w8) { return fused_slabs(k, w8); }
-int norm_gemv_w8_slabs(int k) { return norm_gemv_slabs(k, true); }
 
 int norm_qkv_rope_blocks(int heads, int kv_heads, int head_dim) {
   const int tasks = (heads + 2 * kv_heads) * (head_dim / 2);
@@ -814,13 +804,9 @@ int norm_qkv_rope_blocks(int heads, int kv_heads, int head_dim) {
 bool norm_gemv_supported(int k, bool w8) {
   return k >= 64 && k % 64 == 0 && norm_gemv_slabs(k, w8) <= kNormGemvMaxSlabs;
 }
-bool norm_gemv_w8_supported(int k) { return norm_gemv_supported(k, true); }
 
 bool norm_qkv_rope_supported(int k, int head_dim, bool w8) {
   return norm_gemv_supported(k, w8) && head_dim % 2 == 0 && head_dim >= 2;
-}
-bool norm_qkv_rope_supported(int k, int head_dim) {
-  return norm_qkv_rope_supported(k, head_dim, true);
 }
 
 template <class F>
@@ -845,9 +831,6 @@ void launch_norm_qkv_rope(const QkvRopeArgs& a, bool w8, hipStream_t stream) {
   } else {
     launch_norm_qkv_rope_fmt<Bf16Fmt>(a, stream);
   }
-}
-void launch_norm_qkv_rope_w8(const QkvRopeArgs& a, hipStream_t stream) {
-  launch_norm_qkv_rope(a, true, stream);
 }
 
 int norm_gemv_blocks(int n, int rows_per_wave) {
@@ -903,10 +886,6 @@ void launch_norm_gemv(const NormGemvArgs& a, int blocks, bool pair, bool w8,
       launch_norm_gemv_fmt<Bf16Fmt, false>(a, blocks, stream);
     }
   }
-}
-
-void launch_norm_gemv_w8(const NormGemvArgs& a, int blocks, bool pair, hipStream_t stream) {
-  launch_norm_gemv(a, blocks, pair, true, stream);
 }
 
 int attn_o_slabs(int k, bool w8) {

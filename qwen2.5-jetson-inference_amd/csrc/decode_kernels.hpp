@@ -50,13 +50,10 @@ struct NormGemvArgs {
 // Slabs of 64 16-byte chunks a row of K weights spans (W8A16: 1024
 // weights per slab, BF16: 512).
 int norm_gemv_slabs(int k, bool w8);
-int norm_gemv_w8_slabs(int k);
 bool norm_gemv_supported(int k, bool w8);
-bool norm_gemv_w8_supported(int k);
 int norm_gemv_blocks(int n, int rows_per_wave);
 void launch_norm_gemv(const NormGemvArgs& a, int blocks, bool pair, bool w8,
                       hipStream_t stream);
-void launch_norm_gemv_w8(const NormGemvArgs& a, int blocks, bool pair, hipStream_t stream);
 
 // The decode step's q|k|v launch with the RoPE and the KV-cache store
 // folded in: xn = bf16(rms_norm(x) * norm_w); q = bf16(Wq xn + bq),
@@ -92,9 +89,7 @@ struct QkvRopeArgs {
 // Workgroups of a launch (one wave per pair of output rows).
 int norm_qkv_rope_blocks(int heads, int kv_heads, int head_dim);
 bool norm_qkv_rope_supported(int k, int head_dim, bool w8);
-bool norm_qkv_rope_supported(int k, int head_dim);  // W8A16
 void launch_norm_qkv_rope(const QkvRopeArgs& a, bool w8, hipStream_t stream);
-void launch_norm_qkv_rope_w8(const QkvRopeArgs& a, hipStream_t stream);
 
 // One GEMV row per wave with the whole row's loads in flight at once:
 // y[row] = bf16(W[row] . x + bias[row]), bias may alias y (the residual add).
@@ -110,9 +105,7 @@ struct GemvRowsArgs {
   int k;
 };
 
-bool gemv_w8_rows_supported(int k);
 bool gemv_rows_supported(int k, bool w8);
-void launch_gemv_w8_rows(const GemvRowsArgs& a, hipStream_t stream);
 void launch_gemv_rows(const GemvRowsArgs& a, bool w8, hipStream_t stream);
 
 // o-projection fused with the decode attention's split merge and the
@@ -156,9 +149,7 @@ struct AttnOHalvesArgs {
   int k;                 // heads x 64
 };
 bool attn_o_halves_supported(int k, bool w8);
-bool attn_o_halves_supported(int k);  // W8A16
 void launch_attn_o_halves(const AttnOHalvesArgs& a, bool w8, hipStream_t stream);
-void launch_attn_o_halves(const AttnOHalvesArgs& a, hipStream_t stream);  // W8A16
 void launch_attn_o_gemv(const AttnOArgs& a, bool w8, hipStream_t stream);
 
 constexpr int kLmHeadMaxSlabs = 8;  // K <= 4096

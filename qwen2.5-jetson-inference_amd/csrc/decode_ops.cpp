@@ -1,7 +1,9 @@
 // C ABI of the fused decode-step operators (include/infer_decode.h): the
 // kernels of decode_kernels.hip, launched exactly as the model's decode step
 // launches them (same rows per wave, grids and kernel instantiations), on
-// caller-owned memory.
+// caller-owned memory.  Each Linear-bearing operator has a W8A16 entry point
+// (int8 weights, BF16 group-64 scales) and a BF16 one; both go through one
+// implementation here that takes the weight format.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -21,26 +23,172 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 // (value, index) pair per workgroup.
 constexpr size_t kLmCounterBytes = 256;
 
+// Weights per 16-byte chunk: 16 int8 or 8 BF16.
+int chunk_values(bool w8) { return w8 ? 16 : 8; }
+
 int check_norm_input(const uint16_t* input, const uint16_t* norm_weight, int in_features,
-                     const char* what) {
+                     bool w8, const char* what) {
   if (!input || !norm_weight) return fail(INFER_HIP_INVALID_ARGUMENT, "%s: null input", what);
   if (!aligned16(input) || !aligned16(norm_weight)) {
     return fail(INFER_HIP_INVALID_ARGUMENT, "%s: input and norm weight must be 16-byte aligned",
                 what);
   }
-  if (!norm_gemv_w8_supported(in_features)) {
+  if (!norm_gemv_supported(in_features, w8)) {
     return fail(INFER_HIP_INVALID_ARGUMENT,
                 "%s: in_features %d must be a multiple of 64 in [64, %d]", what, in_features,
-                1024 * kNormGemvMaxSlabs);
+                64 * chunk_values(w8) * kNormGemvMaxSlabs);
   }
   return INFER_HIP_OK;
 }
 
-int check_w8(const int8_t* w, const uint16_t* s, const void* out, int n, const char* what) {
-  if (!w || !s || !out) return fail(INFER_HIP_INVALID_ARGUMENT, "%s: null pointer", what);
+// A Linear's weight (and, for W8A16, its scales) and output.
+int check_weight(const void* w, const uint16_t* s, bool w8, const void* out, int n,
+                 const char* what) {
+  if (!w || (w8 && !s) || !out) return fail(INFER_HIP_INVALID_ARGUMENT, "%s: null pointer", what);
   if (!aligned16(w)) return fail(INFER_HIP_INVALID_ARGUMENT, "%s: weight not 16-byte aligned", what);
   if (n < 1) return fail(INFER_HIP_INVALID_ARGUMENT, "%s: out_features %d < 1", what, n);
   return INFER_HIP_OK;
+}
+
+// One GEMV of rms_norm_gemv in either format.
+struct NormGemvIn {
+  const void* weight;
+  const uint16_t* scales;
+  const uint16_t* bias;
+  uint16_t* output;
+  int out_features;
+};
+
+int rms_norm_gemv(const uint16_t* input, const uint16_t* norm_weight, float epsilon,
+                  int in_features, const NormGemvIn* gemvs, int count, bool w8,
+                  hipStream_t stream, const char* what) {
+  int rc = check_norm_input(input, norm_weight, in_features, w8, what);
+  if (rc != INFER_HIP_OK) return rc;
+  if (count < 1 || count > kNormGemvMaxDescs) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: count %d must be in [1, %d]", what, count,
+                kNormGemvMaxDescs);
+  }
+  NormGemvArgs a{input, norm_weight, epsilon, in_features, count, kQkvRowsPerWave, {}};
+  int blocks = 0;
+  for (int i = 0; i < count; ++i) {
+    const NormGemvIn& g = gemvs[i];
+    rc = check_weight(g.weight, g.scales, w8, g.output, g.out_features, what);
+    if (rc != INFER_HIP_OK) return rc;
+    a.d[i] = NormGemvDesc{g.weight, w8 ? g.scales : nullptr, nullptr, nullptr, g.bias,
+                          g.output, g.out_features, blocks};
+    blocks += norm_gemv_blocks(g.out_features, kQkvRowsPerWave);
+  }
+  launch_norm_gemv(a, blocks, false, w8, stream);
+  return check_launch(what);
+}
+
+int rms_norm_gate_up_silu(const uint16_t* input, const uint16_t* norm_weight, float epsilon,
+                          int in_features, const void* gate_weight, const uint16_t* gate_scales,
+                          const void* up_weight, const uint16_t* up_scales, uint16_t* output,
+                          int intermediate_size, bool w8, hipStream_t stream,
+                          const char* what) {
+  int rc = check_norm_input(input, norm_weight, in_features, w8, what);
+  if (rc == INFER_HIP_OK) {
+    rc = check_weight(gate_weight, gate_scales, w8, output, intermediate_size, what);
+  }
+  if (rc == INFER_HIP_OK) rc = check_weight(up_weight, up_scales, w8, output, intermediate_size, what);
+  if (rc != INFER_HIP_OK) return rc;
+  // the row pairs per wave of the model's decode step for this format
+  const int rows = w8 ? kGateUpRowsPerWave : kGateUpRowsPerWaveBf16;
+  NormGemvArgs a{input, norm_weight, epsilon, in_features, 1, rows, {}};
+  a.d[0] = NormGemvDesc{gate_weight, w8 ? gate_scales : nullptr, up_weight,
+                        w8 ? up_scales : nullptr, nullptr, output, intermediate_size, 0};
+  launch_norm_gemv(a, norm_gemv_blocks(intermediate_size, rows), true, w8, stream);
+  return check_launch(what);
+}
+
+// One of q, k, v of rms_norm_qkv_rope in either format.
+struct QkvWeightIn {
+  const void* weight;
+  const uint16_t* scales;
+  const uint16_t* bias;
+};
+
+int rms_norm_qkv_rope(const uint16_t* input, const uint16_t* norm_weight, float epsilon,
+                      int in_features, const QkvWeightIn& q_proj, const QkvWeightIn& k_proj,
+                      const QkvWeightIn& v_proj, uint16_t* q_out, uint16_t* key_cache,
+                      uint16_t* value_cache, const float* rope_row, const int* position,
+                      int num_heads, int num_kv_heads, int head_dim, int max_sequence_length,
+                      bool w8, hipStream_t stream, const char* what) {
+  int rc = check_norm_input(input, norm_weight, in_features, w8, what);
+  if (rc != INFER_HIP_OK) return rc;
+  if (!q_out || !key_cache || !value_cache || !rope_row || !position) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: null pointer", what);
+  }
+  if (num_heads < 1 || num_kv_heads < 1 || num_heads % num_kv_heads != 0 || head_dim < 2 ||
+      head_dim % 2 != 0 || max_sequence_length < 1 ||
+      !norm_qkv_rope_supported(in_features, head_dim, w8)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "%s: bad shape (heads %d, kv heads %d, head_dim %d, max_seq %d, in %d)", what,
+                num_heads, num_kv_heads, head_dim, max_sequence_length, in_features);
+  }
+  const int nq = num_heads * head_dim, nkv = num_kv_heads * head_dim;
+  rc = check_weight(q_proj.weight, q_proj.scales, w8, q_out, nq, what);
+  if (rc == INFER_HIP_OK) {
+    rc = check_weight(k_proj.weight, k_proj.scales, w8, key_cache, nkv, what);
+  }
+  if (rc == INFER_HIP_OK) {
+    rc = check_weight(v_proj.weight, v_proj.scales, w8, value_cache, nkv, what);
+  }
+  if (rc != INFER_HIP_OK) return rc;
+  const QkvRopeArgs a{input, norm_weight, epsilon, in_features,
+                      q_proj.weight, w8 ? q_proj.scales : nullptr, q_proj.bias,
+                      k_proj.weight, w8 ? k_proj.scales : nullptr, k_proj.bias,
+                      v_proj.weight, w8 ? v_proj.scales : nullptr, v_proj.bias,
+                      q_out, key_cache, value_cache, reinterpret_cast<const float2*>(rope_row),
+                      position, num_heads, num_kv_heads, head_dim, max_sequence_length};
+  launch_norm_qkv_rope(a, w8, stream);
+  return check_launch(what);
+}
+
+int attention_halves_o_proj(const float* records, const int* position, int num_heads,
+                            int max_sequence_length, const void* weight,
+                            const uint16_t* scales, uint16_t* residual, int out_features,
+                            bool w8, hipStream_t stream, const char* what) {
+  if (!records || !position || !weight || (w8 && !scales) || !residual) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: null pointer", what);
+  }
+  const int in_features = num_heads * 64;
+  if (num_heads < 1 || out_features < 1 || max_sequence_length < 1 ||
+      max_sequence_length > kAttnWholeMax || !attn_o_halves_supported(in_features, w8)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "%s: %d heads (in_features %d: multiple of 64, at most %d), %d outputs, "
+                "max_sequence_length %d (at most %d)",
+                what, num_heads, in_features, 256 * chunk_values(w8), out_features,
+                max_sequence_length, kAttnWholeMax);
+  }
+  if (!aligned16(records) || !aligned16(weight)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: records and weight must be 16-byte aligned",
+                what);
+  }
+  launch_attn_o_halves({records, position, num_heads, max_sequence_length, weight,
+                        w8 ? scales : nullptr, residual, out_features, in_features},
+                       w8, stream);
+  return check_launch(what);
+}
+
+int gemv_rows(const void* weight, const uint16_t* scales, const uint16_t* bias,
+              const uint16_t* input, uint16_t* output, int out_features, int in_features,
+              bool w8, hipStream_t stream, const char* what) {
+  int rc = check_weight(weight, scales, w8, output, out_features, what);
+  if (rc != INFER_HIP_OK) return rc;
+  if (!input || !aligned16(input)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: input null or not 16-byte aligned", what);
+  }
+  if (!gemv_rows_supported(in_features, w8)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "%s: in_features %d must be a multiple of 64 in [64, %d]", what, in_features,
+                w8 ? 8192 : 5120);
+  }
+  launch_gemv_rows({weight, w8 ? scales : nullptr, bias, input, output, out_features,
+                    in_features},
+                   w8, stream);
+  return check_launch(what);
 }
 
 }  // namespace
@@ -50,40 +198,45 @@ extern "C" int infer_hip_rms_norm_gemv_w8a16(const uint16_t* input, const uint16
                                              const infer_hip_norm_gemv* gemvs, int count,
                                              hipStream_t stream) {
   const char* what = "rms_norm_gemv_w8a16";
-  int rc = check_norm_input(input, norm_weight, in_features, what);
-  if (rc != INFER_HIP_OK) return rc;
-  if (!gemvs || count < 1 || count > kNormGemvMaxDescs) {
-    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: count %d must be in [1, %d]", what, count,
-                kNormGemvMaxDescs);
+  if (!gemvs) return fail(INFER_HIP_INVALID_ARGUMENT, "%s: null gemvs", what);
+  NormGemvIn in[kNormGemvMaxDescs] = {};
+  for (int i = 0; i < count && i < kNormGemvMaxDescs; ++i) {
+    in[i] = NormGemvIn{gemvs[i].weight, gemvs[i].scales, gemvs[i].bias, gemvs[i].output,
+                       gemvs[i].out_features};
   }
-  NormGemvArgs a{input, norm_weight, epsilon, in_features, count, kQkvRowsPerWave, {}};
-  int blocks = 0;
-  for (int i = 0; i < count; ++i) {
-    const infer_hip_norm_gemv& g = gemvs[i];
-    rc = check_w8(g.weight, g.scales, g.output, g.out_features, what);
-    if (rc != INFER_HIP_OK) return rc;
-    a.d[i] = NormGemvDesc{g.weight, g.scales, nullptr, nullptr, g.bias, g.output,
-                          g.out_features, blocks};
-    blocks += norm_gemv_blocks(g.out_features, kQkvRowsPerWave);
+  return rms_norm_gemv(input, norm_weight, epsilon, in_features, in, count, true, stream, what);
+}
+
+extern "C" int infer_hip_rms_norm_gemv_bf16(const uint16_t* input, const uint16_t* norm_weight,
+                                            float epsilon, int in_features,
+                                            const infer_hip_norm_gemv_bf16* gemvs, int count,
+                                            hipStream_t stream) {
+  const char* what = "rms_norm_gemv_bf16";
+  if (!gemvs) return fail(INFER_HIP_INVALID_ARGUMENT, "%s: null gemvs", what);
+  NormGemvIn in[kNormGemvMaxDescs] = {};
+  for (int i = 0; i < count && i < kNormGemvMaxDescs; ++i) {
+    in[i] = NormGemvIn{gemvs[i].weight, nullptr, gemvs[i].bias, gemvs[i].output,
+                       gemvs[i].out_features};
   }
-  launch_norm_gemv_w8(a, blocks, false, stream);
-  return check_launch(what);
+  return rms_norm_gemv(input, norm_weight, epsilon, in_features, in, count, false, stream, what);
 }
 
 extern "C" int infer_hip_rms_norm_gate_up_silu_w8a16(
     const uint16_t* input, const uint16_t* norm_weight, float epsilon, int in_features,
     const int8_t* gate_weight, const uint16_t* gate_scales, const int8_t* up_weight,
     const uint16_t* up_scales, uint16_t* output, int intermediate_size, hipStream_t stream) {
-  const char* what = "rms_norm_gate_up_silu_w8a16";
-  int rc = check_norm_input(input, norm_weight, in_features, what);
-  if (rc == INFER_HIP_OK) rc = check_w8(gate_weight, gate_scales, output, intermediate_size, what);
-  if (rc == INFER_HIP_OK) rc = check_w8(up_weight, up_scales, output, intermediate_size, what);
-  if (rc != INFER_HIP_OK) return rc;
-  NormGemvArgs a{input, norm_weight, epsilon, in_features, 1, kGateUpRowsPerWave, {}};
-  a.d[0] = NormGemvDesc{gate_weight, gate_scales, up_weight, up_scales, nullptr, output,
-                        intermediate_size, 0};
-  launch_norm_gemv_w8(a, norm_gemv_blocks(intermediate_size, kGateUpRowsPerWave), true, stream);
-  return check_launch(what);
+  return rms_norm_gate_up_silu(input, norm_weight, epsilon, in_features, gate_weight,
+                               gate_scales, up_weight, up_scales, output, intermediate_size,
+                               true, stream, "rms_norm_gate_up_silu_w8a16");
+}
+
+extern "C" int infer_hip_rms_norm_gate_up_silu_bf16(
+    const uint16_t* input, const uint16_t* norm_weight, float epsilon, int in_features,
+    const uint16_t* gate_weight, const uint16_t* up_weight, uint16_t* output,
+    int intermediate_size, hipStream_t stream) {
+  return rms_norm_gate_up_silu(input, norm_weight, epsilon, in_features, gate_weight, nullptr,
+                               up_weight, nullptr, output, intermediate_size, false, stream,
+                               "rms_norm_gate_up_silu_bf16");
 }
 
 extern "C" int infer_hip_attention_decode_halves_bf16(
@@ -117,44 +270,32 @@ extern "C" int infer_hip_attention_halves_o_proj_w8a16(
     const float* records, const int* position, int num_heads, int max_sequence_length,
     const int8_t* weight, const uint16_t* scales, uint16_t* residual, int out_features,
     hipStream_t stream) {
-  const char* what = "attention_halves_o_proj_w8a16";
-  if (!records || !position || !weight || !scales || !residual) {
-    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: null pointer", what);
-  }
-  const int in_features = num_heads * 64;
-  if (num_heads < 1 || out_features < 1 || max_sequence_length < 1 ||
-      max_sequence_length > kAttnWholeMax || !attn_o_halves_supported(in_features)) {
-    return fail(INFER_HIP_INVALID_ARGUMENT,
-                "%s: %d heads (in_features %d: multiple of 64, at most 4096), %d outputs, "
-                "max_sequence_length %d (at most %d)",
-                what, num_heads, in_features, out_features, max_sequence_length, kAttnWholeMax);
-  }
-  if (!aligned16(records) || !aligned16(weight)) {
-    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: records and weight must be 16-byte aligned",
-                what);
-  }
-  launch_attn_o_halves({records, position, num_heads, max_sequence_length, weight, scales,
-                        residual, out_features, in_features},
-                       stream);
-  return check_launch(what);
+  return attention_halves_o_proj(records, position, num_heads, max_sequence_length, weight,
+                                 scales, residual, out_features, true, stream,
+                                 "attention_halves_o_proj_w8a16");
+}
+
+extern "C" int infer_hip_attention_halves_o_proj_bf16(
+    const float* records, const int* position, int num_heads, int max_sequence_length,
+    const uint16_t* weight, uint16_t* residual, int out_features, hipStream_t stream) {
+  return attention_halves_o_proj(records, position, num_heads, max_sequence_length, weight,
+                                 nullptr, residual, out_features, false, stream,
+                                 "attention_halves_o_proj_bf16");
 }
 
 extern "C" int infer_hip_gemv_w8a16_rows(const int8_t* weight, const uint16_t* scales,
                                          const uint16_t* bias, const uint16_t* input,
                                          uint16_t* output, int out_features, int in_features,
                                          hipStream_t stream) {
-  const char* what = "gemv_w8a16_rows";
-  int rc = check_w8(weight, scales, output, out_features, what);
-  if (rc != INFER_HIP_OK) return rc;
-  if (!input || !aligned16(input)) {
-    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: input null or not 16-byte aligned", what);
-  }
-  if (!gemv_w8_rows_supported(in_features)) {
-    return fail(INFER_HIP_INVALID_ARGUMENT,
-                "%s: in_features %d must be a multiple of 64 in [64, 8192]", what, in_features);
-  }
-  launch_gemv_w8_rows({weight, scales, bias, input, output, out_features, in_features}, stream);
-  return check_launch(what);
+  return gemv_rows(weight, scales, bias, input, output, out_features, in_features, true, stream,
+                   "gemv_w8a16_rows");
+}
+
+extern "C" int infer_hip_gemv_bf16_rows(const uint16_t* weight, const uint16_t* bias,
+                                        const uint16_t* input, uint16_t* output,
+                                        int out_features, int in_features, hipStream_t stream) {
+  return gemv_rows(weight, nullptr, bias, input, output, out_features, in_features, false,
+                   stream, "gemv_bf16_rows");
 }
 
 extern "C" int infer_hip_attention_decode_span(int max_sequence_length, int head_dim) {
@@ -246,32 +387,33 @@ extern "C" int infer_hip_rms_norm_qkv_rope_w8a16(
     uint16_t* value_cache, const float* rope_row, const int* position, int num_heads,
     int num_kv_heads, int head_dim, int max_sequence_length, hipStream_t stream) {
   const char* what = "rms_norm_qkv_rope_w8a16";
-  int rc = check_norm_input(input, norm_weight, in_features, what);
-  if (rc != INFER_HIP_OK) return rc;
-  if (!q_proj || !k_proj || !v_proj || !q_out || !key_cache || !value_cache || !rope_row ||
-      !position) {
+  if (!q_proj || !k_proj || !v_proj) {
     return fail(INFER_HIP_INVALID_ARGUMENT, "%s: null pointer", what);
   }
-  if (num_heads < 1 || num_kv_heads < 1 || num_heads % num_kv_heads != 0 || head_dim < 2 ||
-      head_dim % 2 != 0 || max_sequence_length < 1 ||
-      !norm_qkv_rope_supported(in_features, head_dim)) {
-    return fail(INFER_HIP_INVALID_ARGUMENT,
-                "%s: bad shape (heads %d, kv heads %d, head_dim %d, max_seq %d, in %d)", what,
-                num_heads, num_kv_heads, head_dim, max_sequence_length, in_features);
+  return rms_norm_qkv_rope(input, norm_weight, epsilon, in_features,
+                           {q_proj->weight, q_proj->scales, q_proj->bias},
+                           {k_proj->weight, k_proj->scales, k_proj->bias},
+                           {v_proj->weight, v_proj->scales, v_proj->bias}, q_out, key_cache,
+                           value_cache, rope_row, position, num_heads, num_kv_heads, head_dim,
+                           max_sequence_length, true, stream, what);
+}
+
+extern "C" int infer_hip_rms_norm_qkv_rope_bf16(
+    const uint16_t* input, const uint16_t* norm_weight, float epsilon, int in_features,
+    const infer_hip_bf16_weight* q_proj, const infer_hip_bf16_weight* k_proj,
+    const infer_hip_bf16_weight* v_proj, uint16_t* q_out, uint16_t* key_cache,
+    uint16_t* value_cache, const float* rope_row, const int* position, int num_heads,
+    int num_kv_heads, int head_dim, int max_sequence_length, hipStream_t stream) {
+  const char* what = "rms_norm_qkv_rope_bf16";
+  if (!q_proj || !k_proj || !v_proj) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: null pointer", what);
   }
-  const int nq = num_heads * head_dim, nkv = num_kv_heads * head_dim;
-  rc = check_w8(q_proj->weight, q_proj->scales, q_out, nq, what);
-  if (rc == INFER_HIP_OK) rc = check_w8(k_proj->weight, k_proj->scales, key_cache, nkv, what);
-  if (rc == INFER_HIP_OK) rc = check_w8(v_proj->weight, v_proj->scales, value_cache, nkv, what);
-  if (rc != INFER_HIP_OK) return rc;
-  const QkvRopeArgs a{input, norm_weight, epsilon, in_features,
-                      q_proj->weight, q_proj->scales, q_proj->bias,
-                      k_proj->weight, k_proj->scales, k_proj->bias,
-                      v_proj->weight, v_proj->scales, v_proj->bias,
-                      q_out, key_cache, value_cache, reinterpret_cast<const float2*>(rope_row),
-                      position, num_heads, num_kv_heads, head_dim, max_sequence_length};
-  launch_norm_qkv_rope_w8(a, stream);
-  return check_launch(what);
+  return rms_norm_qkv_rope(input, norm_weight, epsilon, in_features,
+                           {q_proj->weight, nullptr, q_proj->bias},
+                           {k_proj->weight, nullptr, k_proj->bias},
+                           {v_proj->weight, nullptr, v_proj->bias}, q_out, key_cache,
+                           value_cache, rope_row, position, num_heads, num_kv_heads, head_dim,
+                           max_sequence_length, false, stream, what);
 }
 
 extern "C" int infer_hip_rope_row(float theta, int head_dim, int position, float* out) {

@@ -320,6 +320,46 @@ def test_halves_attention_ops_reject_bad_arguments(hip):
     assert g(4096, None, 14, 1024, 4096, 4096, 4096, 896, None) == bad
 
 
+def test_bf16_decode_ops_reject_bad_arguments(hip):
+    """The BF16 siblings of the fused decode operators: K limits half the
+    W8A16 ones (8 BF16 weights per 16-byte chunk), no scales needed; checked
+    on the host, nothing launched."""
+    import ctypes
+    import decode_hip
+    lib = decode_hip.load()
+    bad = hip.INVALID_ARGUMENT
+    err = lambda: lib.infer_hip_last_error().decode()  # noqa: E731
+    g = (decode_hip.NormGemvBf16 * 1)(decode_hip.NormGemvBf16(4096, None, 4096, 896))
+    f = lib.infer_hip_rms_norm_gemv_bf16
+    assert f(4096, 4096, 1e-6, 2112, g, 1, None) == bad and "2048" in err()
+    assert f(4096, 4096, 1e-6, 900, g, 1, None) == bad and "multiple of 64" in err()
+    assert f(4096, 4096, 1e-6, 896, None, 1, None) == bad
+    assert f(4096, 4096, 1e-6, 896, g, 0, None) == bad and "count" in err()
+    g[0].weight = 4104
+    assert f(4096, 4096, 1e-6, 896, g, 1, None) == bad and "aligned" in err()
+    f = lib.infer_hip_rms_norm_gate_up_silu_bf16
+    assert f(4096, 4096, 1e-6, 2112, 4096, 4096, 4096, 4864, None) == bad
+    assert f(4096, 4096, 1e-6, 896, 4096, None, 4096, 4864, None) == bad
+    assert f(4096, 4096, 1e-6, 896, 4096, 4096, 4096, 0, None) == bad
+    w = decode_hip.Bf16Weight(4096, None)
+    q = lib.infer_hip_rms_norm_qkv_rope_bf16
+    args = [4096, 4096, 1e-6, 896, ctypes.byref(w), ctypes.byref(w), ctypes.byref(w), 4096, 4096,
+            4096, 4096, 4096, 14, 2, 64, 1024, None]
+    for i, v in ((3, 2112), (3, 900), (12, 0), (13, 3), (14, 63), (11, None), (4, None)):
+        a = list(args)
+        a[i] = v
+        assert q(*a) == bad, (i, v)
+    o = lib.infer_hip_attention_halves_o_proj_bf16
+    assert o(4096, 4096, 33, 1024, 4096, 4096, 896, None) == bad   # 33 x 64 > 2048
+    assert o(4096, 4096, 14, 1025, 4096, 4096, 896, None) == bad   # max_seq
+    assert o(4096, 4096, 14, 1024, 4104, 4096, 896, None) == bad   # weight aligned
+    assert o(4096, 4096, 14, 1024, None, 4096, 896, None) == bad
+    r = lib.infer_hip_gemv_bf16_rows
+    assert r(4096, None, 4096, 4096, 896, 5184, None) == bad and "5120" in err()
+    assert r(4096, None, 4098, 4096, 896, 4864, None) == bad
+    assert r(4096, None, 4096, 4096, 0, 4864, None) == bad
+
+
 def test_gate_up_silu_rejects_bad_arguments(hip):
     """infer_hip_gemm_gate_up_silu_*: the group size, shapes, null pointers,
     K % 64 and alignment are checked on the host; nothing is launched."""

@@ -629,3 +629,189 @@ def test_attention_halves_o_proj_bit_exact(dec, dev, heads, n):
         got = words(x)
         bad = np.nonzero(got != exp)[0]
         assert bad.size == 0, f"pos {pos}: {bad.size}/{n} rows differ, first {bad[0]}"
+
+
+# ------------------------------------ the same launches on BF16 weights --
+#
+# The W16A16 decode step runs the kernels above instantiated for 8 BF16
+# weights per 16-byte chunk (include/infer_decode.h's _bf16 siblings).  The
+# bit-exact design carries over: weights are integers / 64 (at most 7
+# significant bits, exact in BF16), so with the sparse +-1 / +-2 inputs
+# every FP32 partial sum is exact and the BF16 output must equal
+# bf16(exact).  Rotating the nonzero slot over 16 positions puts every
+# weight of a row into some output (a BF16 chunk holds 8 of them, so each
+# chunk is hit by two of the 16 slots), checking the BF16 unpacking and the
+# chunk -> input mapping at the K limits of this format (512 weights per
+# slab: 1, 2 and 4 slabs for the norm launches, 10 for the rows launch).
+
+def bf16_rows(rng, n, k, div=64.0):
+    """BF16 words of integers in [-127, 127] / div, and their values."""
+    w = bf16(rng.integers(-127, 128, size=(n, k)) / div)
+    return w, rc.bf16_values(w).astype(np.float64)
+
+
+def exact_dot(deq, xv, bias_words=None, grid_bits=6):
+    terms = deq * xv.astype(np.float64)[None, :]
+    assert np.all(np.abs(terms).sum(axis=1) * 2 ** grid_bits < 2 ** 24), "design not exact"
+    y = terms.sum(axis=1)
+    if bias_words is not None:
+        y = y + rc.bf16_values(bias_words).astype(np.float64)
+    return y
+
+
+NORM_GEMV_BF16_SHAPES = [
+    (896, (896, 128, 128)),    # the decode step's q|k|v (2 slabs)
+    (64, (3, 5, 130)),
+    (512, (1, 897)),           # one slab
+    (576, (257,)),             # two slabs, the second mostly past K
+    (2048, (64, 2, 33)),       # four slabs, the limit
+]
+
+
+@pytest.mark.parametrize("shape", NORM_GEMV_BF16_SHAPES,
+                         ids=lambda s: f"k{s[0]}_n{'-'.join(map(str, s[1]))}")
+def test_rms_norm_gemv_bf16_bit_exact(dec, dev, shape):
+    k, ns = shape
+    rng = rc.philox(1100 + k)
+    ws = [bf16_rows(rng, n, k) for n in ns]
+    bs = [dyadic_bias(rng, n) if i != 1 else None for i, n in enumerate(ns)]
+    dws = [to_dev(w, dev) for w, _ in ws]
+    dbs = [to_dev(b, dev) if b is not None else None for b in bs]
+    for t in (range(16) if k in (896, 64) else (0, 7, 8, 15)):
+        xw, nw, xn = norm_input(k, t, rng)
+        outs = [bf16_out((n,), dev) for n in ns]
+        dec.rms_norm_gemv_bf16(to_dev(xw, dev), to_dev(nw, dev), EPS, k,
+                               [(dws[i], dbs[i], outs[i], n) for i, n in enumerate(ns)])
+        for i, n in enumerate(ns):
+            exp = bf16(exact_dot(ws[i][1], xn, bs[i]))
+            got = words(outs[i])
+            bad = np.nonzero(got != exp)[0]
+            assert bad.size == 0, (f"K={k} gemv {i} slot {t}: {bad.size}/{n} rows differ, "
+                                   f"first row {bad[0]}: {got[bad[0]]:#06x} vs {exp[bad[0]]:#06x}")
+
+
+@pytest.mark.parametrize("k,n", [(896, 4864), (64, 5), (1024, 33), (2048, 130)])
+def test_rms_norm_gate_up_silu_bf16(dec, dev, k, n):
+    rng = rc.philox(1200 + k)
+    # integers / 1024 keep |gate| well inside expf's range
+    (wg, dg), (wu, du) = bf16_rows(rng, n, k, 1024.0), bf16_rows(rng, n, k, 1024.0)
+    dwg, dwu = to_dev(wg, dev), to_dev(wu, dev)
+    ambiguous = 0
+    for t in (range(16) if n == 4864 else (0, 9)):
+        xw, nw, xn = norm_input(k, t, rng)
+        g = bf16(exact_dot(dg, xn, grid_bits=10))
+        u = bf16(exact_dot(du, xn, grid_bits=10))
+        a, b = silu_mul_expected(g, u)
+        out = bf16_out((n,), dev)
+        dec.rms_norm_gate_up_silu_bf16(to_dev(xw, dev), to_dev(nw, dev), EPS, k, dwg, dwu, out, n)
+        got = words(out)
+        ok = (got == a) | (got == b)
+        assert ok.all(), (f"K={k} slot {t}: {np.sum(~ok)} rows differ, first "
+                          f"{np.nonzero(~ok)[0][0]}")
+        ambiguous += int(np.sum(a != b))
+    assert ambiguous <= max(2, n // 100), ambiguous
+
+
+@pytest.mark.parametrize("k,n", [(4864, 896), (64, 3), (896, 897), (512, 4), (576, 65),
+                                 (4096, 33), (5120, 7)])
+@pytest.mark.parametrize("bias", ["none", "separate", "residual"])
+def test_gemv_bf16_rows_bit_exact(dec, dev, k, n, bias):
+    rng = rc.philox(1300 + k + n)
+    w, deq = bf16_rows(rng, n, k)
+    dw = to_dev(w, dev)
+    b = dyadic_bias(rng, n) if bias != "none" else None
+    for t in ((0, 3, 8, 15) if k == 4864 else (0, 11)):
+        pos = sparse_positions(k, t)
+        xv = np.zeros(k, np.float64)
+        xv[pos] = rng.choice([-2.0, -1.0, 1.0, 2.0], size=pos.size)
+        y = bf16_out((n,), dev)
+        if bias == "residual":
+            y.copy_(to_dev(b, dev))   # the output holds the residual and is updated in place
+            dec.gemv_bf16_rows(dw, y, to_dev(bf16(xv), dev), y, n, k)
+        else:
+            dec.gemv_bf16_rows(dw, to_dev(b, dev) if b is not None else None,
+                               to_dev(bf16(xv), dev), y, n, k)
+        exp = bf16(exact_dot(deq, xv, b))
+        got = words(y)
+        bad = np.nonzero(got != exp)[0]
+        assert bad.size == 0, (f"K={k} n={n} slot {t}: {bad.size} rows differ, first {bad[0]}: "
+                               f"{got[bad[0]]:#06x} vs {exp[bad[0]]:#06x}")
+
+
+@pytest.mark.parametrize("shape", QKV_ROPE_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_rms_norm_qkv_rope_bf16(dec, dev, shape):
+    import torch
+    k, heads, kvh, hd, max_seq = shape
+    half = hd // 2
+    rng = rc.philox(1400 + k + heads)
+    nq, nkv = heads * hd, kvh * hd
+    w = {n: bf16_rows(rng, m, k) for n, m in (("q", nq), ("k", nkv), ("v", nkv))}
+    b = {n: dyadic_bias(rng, w[n][0].shape[0]) for n in "qkv"}
+    b["k"] = None  # a null bias too
+    dw = {n: (to_dev(w[n][0], dev), to_dev(b[n], dev) if b[n] is not None else None)
+          for n in "qkv"}
+    sentinel = np.uint16(0x7FC0)
+    for position in (0, 5, max_seq - 1, max_seq + 100):
+        p = min(position, max_seq - 1)
+        xw, nw, xn = norm_input(k, (3 * position) % 16, rng)
+        y = {n: bf16(exact_dot(w[n][1], xn, b[n])) for n in "qkv"}
+        cs = dec.rope_row(1e6, hd, p)
+        kc = torch.full((kvh * max_seq * hd,), int(sentinel.view(np.int16)), dtype=torch.int16,
+                        device=dev)
+        vc = kc.clone()
+        q_out = bf16_out((nq,), dev)
+        dpos = torch.tensor([position], dtype=torch.int32, device=dev)
+        dec.rms_norm_qkv_rope_bf16(to_dev(xw, dev), to_dev(nw, dev), EPS, k, dw["q"], dw["k"],
+                                   dw["v"], q_out, kc, vc, torch.from_numpy(cs.copy()).to(dev),
+                                   dpos, heads, kvh, hd, max_seq)
+        kcache = kc.cpu().numpy().view(np.uint16).reshape(kvh, max_seq, hd)
+        vcache = vc.cpu().numpy().view(np.uint16).reshape(kvh, max_seq, hd)
+        other = np.ones(max_seq, bool)
+        other[p] = False
+        assert np.all(kcache[:, other] == sentinel) and np.all(vcache[:, other] == sentinel)
+        np.testing.assert_array_equal(vcache[:, p].reshape(-1), y["v"])
+        for name, got in (("q", words(q_out).reshape(-1, hd)), ("k", kcache[:, p])):
+            yy = y[name].reshape(-1, hd)
+            if p == 0:
+                np.testing.assert_array_equal(got, yy)
+                continue
+            first, second = rope_candidates(yy[:, :half], yy[:, half:], cs)
+            ok1 = np.any([got[:, :half] == c for c in first], axis=0)
+            ok2 = np.any([got[:, half:] == c for c in second], axis=0)
+            assert ok1.all() and ok2.all(), (name, position, np.argwhere(~ok1)[:3],
+                                             np.argwhere(~ok2)[:3])
+
+
+@pytest.mark.parametrize("heads,n", [(14, 896), (2, 130), (32, 65)])
+def test_attention_halves_o_proj_bf16_bit_exact(dec, dev, heads, n):
+    """As test_attention_halves_o_proj_bit_exact on a BF16 weight: lane
+    chunks of 8 inputs, eight per head, each reading two 16-byte pieces of
+    both records.  32 heads is the format's K limit (2048)."""
+    import torch
+    hd, max_seq, R = 64, 1024, dec.HALF_RECORD
+    rng = rc.philox(1500 + heads + n)
+    k = heads * hd
+    w, deq = bf16_rows(rng, n, k)
+    dw = to_dev(w, dev)
+    acc = rng.integers(-1, 2, size=(heads, 2, hd)) / 8.0
+    x0 = rc.bf16_normal(rng, (n,))
+    for pos in (0, 1, 511, 512, 513, 1023, 2000):
+        two = min(pos, max_seq - 1) >= 512
+        part = np.full((heads, 2, R), np.nan, np.float32)
+        part[:, 0, :hd] = acc[:, 0]
+        part[:, 0, hd], part[:, 0, hd + 1] = 0.0, 1.0
+        if two:
+            part[:, 1, :hd] = acc[:, 1]
+            part[:, 1, hd], part[:, 1, hd + 1] = 0.0, 0.0
+        attn = (acc[:, 0] + (acc[:, 1] if two else 0.0)).reshape(-1)
+        assert np.all(rc.bf16_values(bf16(attn)) == attn)
+        terms = deq * attn[None, :]
+        assert np.all(np.abs(terms).sum(axis=1) * 2 ** 10 < 2 ** 24), "design not exact"
+        exp = rc.bf16_words(terms.sum(axis=1).astype(np.float32) + rc.bf16_values(x0))
+        x = to_dev(x0, dev)
+        dpos = torch.tensor([pos], dtype=torch.int32, device=dev)
+        dec.attention_halves_o_proj_bf16(torch.from_numpy(part.reshape(-1)).to(dev), dpos, heads,
+                                         max_seq, dw, x, n)
+        got = words(x)
+        bad = np.nonzero(got != exp)[0]
+        assert bad.size == 0, f"pos {pos}: {bad.size}/{n} rows differ, first {bad[0]}"
