@@ -613,6 +613,44 @@ def linear_calls_detail(dev) -> dict:
     return out
 
 
+def torch_mm_detail(dev) -> dict:
+    """The vendor library on the same GEMM shapes, for comparison: torch.mm
+    (hipBLASLt) of BF16 X [M, K] by a contiguous BF16 W^T [K, N], each
+    shape's 24 calls (4 layers' tensors rotated) captured as one HIP graph
+    and replayed, as linear_calls_detail times this library's calls.  Not a
+    Linear of the reference: plain BF16, no bias, no W8A16."""
+    import torch
+    out = {}
+    g = torch.Generator(device=dev)
+    g.manual_seed(6)
+    layers, per_graph = 4, 24
+    for m in (32, 128, 512):
+        per = {}
+        total_us = 0.0
+        for name, n, k in SHAPES:
+            calls = []
+            for _ in range(layers):
+                x = torch.randn((m, k), device=dev, generator=g).to(torch.bfloat16)
+                wt = (torch.randn((k, n), device=dev, generator=g) * 0.02).to(torch.bfloat16)
+                calls.append((x, wt, torch.empty((m, n), dtype=torch.bfloat16, device=dev)))
+            for x, wt, y in calls:
+                torch.mm(x, wt, out=y)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for i in range(per_graph):
+                    x, wt, y = calls[i % layers]
+                    torch.mm(x, wt, out=y)
+            t, _ = time_steps(lambda ev: graph.replay(), 10, 3)
+            us = t / (10 * per_graph) * 1e3
+            total_us += us
+            per[name] = {"us_per_call": round(us, 2),
+                         "TFLOPs": round(2.0 * m * n * k / (us * 1e-6) / 1e12, 2)}
+            del graph, calls
+        out[f"bf16_M{m}"] = {"per_shape": per, "layer_us": round(total_us, 2)}
+    return out
+
+
 def torch_sum_read(dev) -> dict:
     """A library streaming read for comparison: torch's sum over 1 GiB of
     FP32 (more than the 256 MB last-level cache).  A reduction kernel, not a
@@ -731,6 +769,7 @@ def e2e_main(args, dev):
         if args.detail:
             progress("detail sweeps")
             detail = {"e2e": e2e_detail(workdirs, cfg), "linear_calls": linear_calls_detail(dev),
+                      "torch_mm_bf16": torch_mm_detail(dev),
                       "lm_head": lm_head_detail(dev, hip), "torch_sum_read": torch_sum_read(dev)}
     finally:
         for wd in workdirs.values():
