@@ -1076,6 +1076,265 @@ void launch_config(int config, const GemmArgs& a, hipStream_t stream) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// ------------------------------------------------------------------------
+// Skinny GEMM: Y[m, n] for m <= 32 tokens, the weights streamed once.
+//
+// With a few tokens a GEMM is bound by reading its weights (15.4 MB of int8
+// per Qwen2.5-0.5B layer), not by MFMA: staging 64 x 64 tiles through LDS
+// leaves a few dozen workgroups walking 14 dependent stages each.  Here a
+// workgroup owns 32 weight rows of one Linear (the MFMA's 32 columns) and
+// all the tokens (its 32 rows); its KW waves split K, each loading its
+// groups' weight and activation chunks straight into registers (all of a
+// round's loads in flight at once, no LDS, no barrier), then the waves'
+// accumulators are summed in LDS in wave order.
+//
+// Lane (r, h) feeds MFMA k-step ks of group g with chunk 4 h + ks of the
+// group (K 64 g + 32 h + 8 ks .. + 7), for the A fragment of token r and
+// the B fragment of weight row n0 + r: the fragments the 64 x 64 tile
+// kernel reads from LDS, so a group's MFMA partial is the same, and its
+// W8A16 scale (row n0 + r, group g) is one value per lane.  Accumulator
+// element e is token 8 (e / 4) + 4 h + e % 4 of row n0 + r.  Buffer loads
+// whose offset is past the operand (tokens >= m, rows >= n) read zeros.
+//
+// PAIR: the workgroup computes gate (w, s, bias) and up (w2, s2, bias2)
+// rows n0 .. n0 + 31 and writes bf16(silu(bf16(gate)) * bf16(up)).
+// A GEMM split over K (d.parts > 1) runs `parts` workgroups per row block;
+// their wave 0s hand off through d.partial as the 64 x 64 tiles' split-K
+// does (device-coherent stores, an agent-scope arrival count, the last one
+// summing the parts in index order and resetting the count), with no
+// workgroup barrier: only wave 0 takes part.
+template <bool W8, bool PAIR, int KW>
+__global__ __launch_bounds__(kWave * KW) void gemm_skinny_kernel(SkinnyArgs a) {
+  constexpr int kRound = 4;  // groups per wave per round of loads
+  const int b = blockIdx.x;
+  SkinnyDesc d = a.d[0];  // the last descriptor whose block_begin <= b
+#pragma unroll
+  for (int i = 1; i < kSkinnyMaxDescs; ++i) {
+    if (i < a.count && a.d[i].block_begin <= b) d = a.d[i];
+  }
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int r = lane & 31, h = lane >> 5;
+  const int rb = (b - d.block_begin) / d.parts, part = (b - d.block_begin) % d.parts;
+  const int n0 = rb * 32;
+  const int groups = d.k / kStageK;
+  // this part's groups, then this wave's share of them
+  const int per_part = (groups + d.parts - 1) / d.parts;
+  const int p_begin = min(groups, part * per_part), p_end = min(groups, p_begin + per_part);
+  const int per = (p_end - p_begin + KW - 1) / KW;
+  const int g_begin = min(p_end, p_begin + wave * per), g_end = min(p_end, g_begin + per);
+  const uint32_t wbytes = W8 ? 1u : 2u;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(d.x, static_cast<uint32_t>(a.m) * d.k * 2u);
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(d.w, static_cast<uint32_t>(d.n) * d.k * wbytes);
+  const __amdgpu_buffer_rsrc_t wr2 =
+      make_rsrc(PAIR ? d.w2 : d.w, static_cast<uint32_t>(d.n) * d.k * wbytes);
+  // Lane offsets of group 0; group g adds 64 g columns (a scalar offset).
+  const uint32_t xoff = (static_cast<uint32_t>(r) * d.k + 32u * h) * 2u;
+  const uint32_t woff = (static_cast<uint32_t>(n0 + r) * d.k + 32u * h) * wbytes;
+  const int srow = min(n0 + r, d.n - 1);  // scales: clamped row, its value unused past N
+  const uint16_t* s1 = W8 ? d.s + static_cast<size_t>(srow) * groups : nullptr;
+  const uint16_t* s2 = W8 && PAIR ? d.s2 + static_cast<size_t>(srow) * groups : nullptr;
+
+  f32x16_t acc = {}, acc2 = {};
+  for (int g0 = g_begin; g0 < g_end; g0 += kRound) {
+    // One round: the loads of up to kRound groups, issued together (groups
+    // past g_end re-read the round's first group and are not used).
+    uint4 xa[kRound][4], wq[kRound][W8 ? 2 : 4], wq2[kRound][PAIR ? (W8 ? 2 : 4) : 1];
+    uint32_t sc[kRound], sc2[kRound];
+#pragma unroll
+    for (int j = 0; j < kRound; ++j) {
+      const uint32_t g = static_cast<uint32_t>(g0 + j < g_end ? g0 + j : g0);
+#pragma unroll
+      for (int ks = 0; ks < (W8 ? 2 : 4); ++ks) {
+        wq[j][ks] = buffer_load16(wr, woff + 16u * ks, g * kStageK * wbytes);
+        if (PAIR) wq2[j][ks] = buffer_load16(wr2, woff + 16u * ks, g * kStageK * wbytes);
+      }
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) xa[j][ks] = buffer_load16(xr, xoff + 16u * ks, g * kStageK * 2u);
+      if (W8) {
+        sc[j] = gload(s1 + g);
+        if (PAIR) sc2[j] = gload(s2 + g);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kRound; ++j) {
+      if (g0 + j >= g_end) break;
+      bf16x8_t fb[4], fb2[4];
+      if (W8) {
+        uint4 lo, hi;
+        i8x16_to_bf16(wq[j][0], lo, hi);
+        fb[0] = as_bf16x8(lo);
+        fb[1] = as_bf16x8(hi);
+        i8x16_to_bf16(wq[j][1], lo, hi);
+        fb[2] = as_bf16x8(lo);
+        fb[3] = as_bf16x8(hi);
+        if (PAIR) {
+          i8x16_to_bf16(wq2[j][0], lo, hi);
+          fb2[0] = as_bf16x8(lo);
+          fb2[1] = as_bf16x8(hi);
+          i8x16_to_bf16(wq2[j][1], lo, hi);
+          fb2[2] = as_bf16x8(lo);
+          fb2[3] = as_bf16x8(hi);
+        }
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          fb[ks] = as_bf16x8(wq[j][ks]);
+          if (PAIR) fb2[ks] = as_bf16x8(wq2[PAIR ? j : 0][PAIR ? ks : 0]);
+        }
+      }
+      if (W8) {
+        const f32x16_t zero = {};
+        f32x16_t part = zero, part2 = zero;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          part = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(xa[j][ks]), fb[ks],
+                                                         ks == 0 ? zero : part, 0, 0, 0);
+          if (PAIR) {
+            part2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(xa[j][ks]), fb2[ks],
+                                                            ks == 0 ? zero : part2, 0, 0, 0);
+          }
+        }
+        const float s = bf16_to_f32(sc[j]);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] = fmaf(part[e], s, acc[e]);
+        if (PAIR) {
+          const float t = bf16_to_f32(sc2[j]);
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc2[e] = fmaf(part2[e], t, acc2[e]);
+        }
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(xa[j][ks]), fb[ks], acc, 0,
+                                                        0, 0);
+          if (PAIR) {
+            acc2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(xa[j][ks]), fb2[ks], acc2,
+                                                           0, 0, 0);
+          }
+        }
+      }
+    }
+  }
+
+  // The waves' accumulators, summed in wave order by wave 0.
+  if (KW > 1) {
+    __shared__ f32x4_t red[KW > 1 ? KW : 1][PAIR ? 2 : 1][4][kWave];
+    if (wave > 0) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        red[wave][0][q][lane] = f32x4_t{acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]};
+        if (PAIR) {
+          red[wave][PAIR ? 1 : 0][q][lane] =
+              f32x4_t{acc2[4 * q], acc2[4 * q + 1], acc2[4 * q + 2], acc2[4 * q + 3]};
+        }
+      }
+    }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int w = 1; w < KW; ++w) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4_t v = red[w][0][q][lane];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[4 * q + t] += v[t];
+        if (PAIR) {
+          const f32x4_t v2 = red[w][PAIR ? 1 : 0][q][lane];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) acc2[4 * q + t] += v2[t];
+        }
+      }
+    }
+  }
+
+  if (!PAIR && d.parts > 1) {
+    // Split-K hand-off (wave 0 only).  Lane l's 16 values are 4 16-byte
+    // vectors at [(q * 64 + l) * 4] of the part's 1024 floats.
+    const __amdgpu_buffer_rsrc_t pr =
+        make_rsrc(d.partial + static_cast<size_t>(rb) * d.parts * 1024,
+                  static_cast<uint32_t>(d.parts) * 4096u);
+    const uint32_t mine = static_cast<uint32_t>(part) * 4096u;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const f32x4_t v = {acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]};
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), pr,
+                                             mine + (q * kWave + lane) * 16u, 0, kCoherent);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this lane's part is stored
+    int arrived = 0;
+    if (lane == 0) {
+      arrived = __hip_atomic_fetch_add(d.counters + rb, 1, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (__builtin_amdgcn_readfirstlane(arrived) != d.parts - 1) return;
+    f32x16_t sum;
+    for (int p = 0; p < d.parts; ++p) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        f32x4_t v;
+        if (p == part) {
+          v = f32x4_t{acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]};
+        } else {
+          v = __builtin_bit_cast(
+              f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                           pr, static_cast<uint32_t>(p) * 4096u + (q * kWave + lane) * 16u, 0,
+                           kCoherent));
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) sum[4 * q + c] = p == 0 ? v[c] : sum[4 * q + c] + v[c];
+      }
+    }
+    acc = sum;
+    if (lane == 0) {  // ready for the next launch
+      __hip_atomic_store(d.counters + rb, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+
+  const int n = n0 + r;
+  if (n >= d.n) return;
+  const float bias = d.bias ? bf16_to_f32(gload(d.bias + n)) : 0.0f;
+  const float bias2 = PAIR && d.bias2 ? bf16_to_f32(gload(d.bias2 + n)) : 0.0f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int m = 8 * (e >> 2) + 4 * h + (e & 3);
+    if (m >= a.m) continue;
+    float v;
+    if (PAIR) {
+      // as silu_mul_bf16 on the two BF16 GEMM outputs
+      const float gv = bf16_to_f32(f32_to_bf16(acc[e] + bias));
+      const float uv = bf16_to_f32(f32_to_bf16(acc2[e] + bias2));
+      v = gv / (1.0f + expf(-gv)) * uv;
+    } else {
+      v = acc[e] + bias;
+    }
+    gstore(d.y + static_cast<size_t>(m) * d.n + n, f32_to_bf16(v));
+  }
+}
+
+template <bool W8, bool PAIR>
+void launch_skinny_kw(const SkinnyArgs& a, int blocks, int kw, hipStream_t stream) {
+  switch (kw) {
+    case 1:
+      hipLaunchKernelGGL((gemm_skinny_kernel<W8, PAIR, 1>), dim3(blocks), dim3(kWave), 0, stream, a);
+      break;
+    case 2:
+      hipLaunchKernelGGL((gemm_skinny_kernel<W8, PAIR, 2>), dim3(blocks), dim3(2 * kWave), 0,
+                         stream, a);
+      break;
+    case 4:
+      hipLaunchKernelGGL((gemm_skinny_kernel<W8, PAIR, 4>), dim3(blocks), dim3(4 * kWave), 0,
+                         stream, a);
+      break;
+    default:
+      // (a pair holds twice the registers: at most 4 waves, 256 each)
+      if constexpr (!PAIR) {
+        hipLaunchKernelGGL((gemm_skinny_kernel<W8, PAIR, 8>), dim3(blocks), dim3(8 * kWave), 0,
+                           stream, a);
+      }
+      break;
+  }
+}
+
 }  // namespace
 
 bool gemm_mfma_supported(const void* w, const uint16_t* x, int m, int n, int k) {
@@ -1083,6 +1342,84 @@ bool gemm_mfma_supported(const void* w, const uint16_t* x, int m, int n, int k) 
   const long long limit = 0x7FFFFFFFll;
   return k >= kStageK && k % kStageK == 0 && aligned16(w) && aligned16(x) &&
          2ll * m * k < limit && 2ll * n * k < limit;
+}
+
+bool gemm_skinny_supported(const void* w, const uint16_t* x, int m, int n, int k) {
+  return m >= 1 && m <= kSkinnyMaxTokens && n >= 1 && gemm_mfma_supported(w, x, m, n, k);
+}
+
+int layout_skinny(SkinnyArgs& a, bool split) {
+  // About four groups of 64 per wave: one round of loads.  Without a split,
+  // up to 8 waves per workgroup (two per SIMD keep 256 registers per wave;
+  // 4 for a pair, whose rounds hold both weights).  With it, 4 waves and a
+  // GEMM longer than 16 groups in parts of at most 16: a lone row block per
+  // CU cannot pull its weights and activations fast enough (down_proj at 32
+  // tokens: 28 workgroups of 8 waves took 16.9 us).
+  const bool pair = a.d[0].w2 != nullptr;
+  int groups = 0;
+  for (int i = 0; i < a.count; ++i) groups = std::max(groups, a.d[i].k / kStageK);
+  int kw = 1;
+  if (split && !pair) {
+    kw = 4;
+  } else {
+    while (kw < (pair ? 4 : 8) && kw * 4 < groups) kw *= 2;
+  }
+  a.waves = kw;
+  int blocks = 0;
+  for (int i = 0; i < a.count; ++i) {
+    SkinnyDesc& d = a.d[i];
+    const int g = d.k / kStageK;
+    d.parts = split && !pair && g > 16 ? (g + 15) / 16 : 1;
+    d.partial = nullptr;
+    d.counters = nullptr;
+    d.block_begin = blocks;
+    blocks += (d.n + 31) / 32 * d.parts;
+  }
+  return blocks;
+}
+
+void skinny_scratch(const SkinnyArgs& a, size_t* partial_floats, size_t* counters) {
+  size_t pf = 0, cc = 0;
+  for (int i = 0; i < a.count; ++i) {
+    if (a.d[i].parts > 1) {
+      const size_t blocks = static_cast<size_t>(a.d[i].n + 31) / 32;
+      pf += blocks * a.d[i].parts * 1024;
+      cc += blocks;
+    }
+  }
+  *partial_floats = pf;
+  *counters = cc;
+}
+
+void bind_skinny(SkinnyArgs& a, float* partial, int* counters) {
+  for (int i = 0; i < a.count; ++i) {
+    SkinnyDesc& d = a.d[i];
+    if (d.parts > 1) {
+      const size_t blocks = static_cast<size_t>(d.n + 31) / 32;
+      d.partial = partial;
+      d.counters = counters;
+      partial += blocks * d.parts * 1024;
+      counters += blocks;
+    }
+  }
+}
+
+void launch_gemm_skinny(bool w8, const SkinnyArgs& a, int blocks, hipStream_t stream) {
+  const bool pair = a.d[0].w2 != nullptr;
+  const int kw = a.waves;
+  if (w8) {
+    if (pair) {
+      launch_skinny_kw<true, true>(a, blocks, kw, stream);
+    } else {
+      launch_skinny_kw<true, false>(a, blocks, kw, stream);
+    }
+  } else {
+    if (pair) {
+      launch_skinny_kw<false, true>(a, blocks, kw, stream);
+    } else {
+      launch_skinny_kw<false, false>(a, blocks, kw, stream);
+    }
+  }
 }
 
 int gemm_pick_tile(int m, int n) {
@@ -1212,8 +1549,13 @@ namespace {
 // counters of the calls made on it (what infer_hip_gemm_workspace_bytes
 // returns), no call's partials overwrite a counter, which every call
 // leaves at zero.
+// Calls of at most kSkinnyMaxTokens tokens run the skinny kernel, split over
+// K into workgroups (long K) on the same workspace layout.
 struct LoneLayout {
   GemmGroupLaunch l{};
+  bool skinny = false;
+  SkinnyArgs sk{};
+  int sk_blocks = 0;
   size_t partial_bytes = 0;  // 0: no split
   size_t counter_bytes = 0;
 };
@@ -1236,6 +1578,20 @@ int current_cus(int* cus) {
 LoneLayout lone_layout(bool w8, const void* w, const uint16_t* s, const uint16_t* bias,
                        const uint16_t* x, uint16_t* y, int m, int n, int k, int cus) {
   LoneLayout o;
+  if (m >= 2 && m <= kSkinnyMaxTokens && gemm_skinny_supported(w, x, m, n, k)) {
+    o.skinny = true;
+    o.sk.count = 1;
+    o.sk.m = m;
+    o.sk.d[0] = SkinnyDesc{w, w8 ? s : nullptr, bias, nullptr, nullptr, nullptr, x, y, n, k, 0};
+    o.sk_blocks = layout_skinny(o.sk, true);
+    size_t pf = 0, cc = 0;
+    skinny_scratch(o.sk, &pf, &cc);
+    if (pf > 0) {
+      o.partial_bytes = round256(pf * sizeof(float));
+      o.counter_bytes = round256(cc * sizeof(int));
+    }
+    return o;
+  }
   GemmGroupDesc& d = o.l.g.d[0];
   d = GemmGroupDesc{w, s, bias, x, y, m, n, k, 0, 0, 1, k / kStageK, nullptr, nullptr};
   size_t pf = 0, cc = 0;
@@ -1259,7 +1615,7 @@ int launch_lone_split(bool w8, const void* w, const uint16_t* s, const uint16_t*
   const int rc = current_cus(&cus);
   if (rc != INFER_HIP_OK) return rc;
   LoneLayout o = lone_layout(w8, w, s, bias, x, y, m, n, k, cus);
-  if (o.partial_bytes == 0 || o.l.blocks <= 0) return INFER_HIP_OK;
+  if (o.partial_bytes == 0 || (!o.skinny && o.l.blocks <= 0)) return INFER_HIP_OK;
   if (!ws) {
     return fail(INFER_HIP_INVALID_ARGUMENT,
                 "gemm: this call splits K and needs a workspace of %zu bytes (none given)",
@@ -1279,14 +1635,33 @@ int launch_lone_split(bool w8, const void* w, const uint16_t* s, const uint16_t*
   }
   int* counters = static_cast<int*>(ws);
   float* partial = reinterpret_cast<float*>(pbase);
-  o.l.r.count = bind_gemm_group(o.l.g.d, 1, o.l.tile, partial, counters, o.l.r.d,
-                                &o.l.reducers);
-  launch_gemm_group_inline(o.l, stream);
+  if (o.skinny) {
+    bind_skinny(o.sk, partial, counters);
+    launch_gemm_skinny(w8, o.sk, o.sk_blocks, stream);
+  } else {
+    o.l.r.count = bind_gemm_group(o.l.g.d, 1, o.l.tile, partial, counters, o.l.r.d,
+                                  &o.l.reducers);
+    launch_gemm_group_inline(o.l, stream);
+  }
   *done = true;
   return INFER_HIP_OK;
 }
 
 // ws_mode: the caller passed a workspace (the _ws entry points).
+// A lone GEMM of at most kSkinnyMaxTokens tokens without a workspace: one
+// skinny launch, K split only over each workgroup's waves.
+void launch_lone_skinny(bool w8, const void* weight, const uint16_t* scales,
+                        const uint16_t* bias, const uint16_t* input, uint16_t* output, int tokens,
+                        int n, int k, hipStream_t stream) {
+  SkinnyArgs a{};
+  a.count = 1;
+  a.m = tokens;
+  a.d[0] = SkinnyDesc{weight, w8 ? scales : nullptr, bias, nullptr, nullptr, nullptr, input,
+                      output, n, k, 0};
+  const int blocks = layout_skinny(a, false);
+  launch_gemm_skinny(w8, a, blocks, stream);
+}
+
 int gemm_w8a16_impl(const int8_t* weight, const uint16_t* scales, int group_size,
                     const uint16_t* bias, const uint16_t* input, uint16_t* output, int tokens,
                     int out_features, int in_features, int tile, hipStream_t stream,
@@ -1308,6 +1683,18 @@ int gemm_w8a16_impl(const int8_t* weight, const uint16_t* scales, int group_size
   if (tokens == 1 && w8a16_gemv_fast_supported(weight, input, in_features)) {
     launch_w8a16_gemv_fast({weight, scales, bias, input, output, out_features, in_features},
                            stream);
+  } else if (tile < 0 && tokens > 1 &&
+             gemm_skinny_supported(weight, input, tokens, out_features, in_features)) {
+    bool done = false;
+    if (ws_mode) {  // long K: split over workgroups on the workspace
+      const int rc = launch_lone_split(true, weight, scales, bias, input, output, tokens,
+                                       out_features, in_features, ws, ws_bytes, stream, &done);
+      if (rc != INFER_HIP_OK) return rc;
+    }
+    if (!done) {
+      launch_lone_skinny(true, weight, scales, bias, input, output, tokens, out_features,
+                         in_features, stream);
+    }
   } else if (tokens > 1 && gemm_mfma_supported(weight, input, tokens, out_features, in_features)) {
     bool done = false;
     if (ws_mode) {
@@ -1342,6 +1729,18 @@ int gemm_bf16_impl(const uint16_t* weight, const uint16_t* bias, const uint16_t*
   }
   if (tokens == 1 && bf16_gemv_fast_supported(weight, input, in_features)) {
     launch_bf16_gemv_fast({weight, bias, input, output, out_features, in_features}, stream);
+  } else if (tile < 0 && tokens > 1 &&
+             gemm_skinny_supported(weight, input, tokens, out_features, in_features)) {
+    bool done = false;
+    if (ws_mode) {  // long K: split over workgroups on the workspace
+      const int rc = launch_lone_split(false, weight, nullptr, bias, input, output, tokens,
+                                       out_features, in_features, ws, ws_bytes, stream, &done);
+      if (rc != INFER_HIP_OK) return rc;
+    }
+    if (!done) {
+      launch_lone_skinny(false, weight, nullptr, bias, input, output, tokens, out_features,
+                         in_features, stream);
+    }
   } else if (tokens > 1 && gemm_mfma_supported(weight, input, tokens, out_features, in_features)) {
     bool done = false;
     if (ws_mode) {
@@ -1381,8 +1780,18 @@ int gate_up_silu_impl(bool w8, const void* gate_w, const uint16_t* gate_s,
                 "under 2 GiB",
                 what);
   }
-  launch_gate_up_silu(w8, gate_w, gate_s, gate_b, up_w, up_s, up_b, input, output, tokens, inter,
-                      hidden, stream);
+  if (tokens <= kSkinnyMaxTokens) {
+    SkinnyArgs a{};
+    a.count = 1;
+    a.m = tokens;
+    a.d[0] = SkinnyDesc{gate_w, w8 ? gate_s : nullptr, gate_b, up_w, w8 ? up_s : nullptr, up_b,
+                        input, output, inter, hidden, 0};
+    const int blocks = layout_skinny(a, false);  // a pair is never split
+    launch_gemm_skinny(w8, a, blocks, stream);
+  } else {
+    launch_gate_up_silu(w8, gate_w, gate_s, gate_b, up_w, up_s, up_b, input, output, tokens,
+                        inter, hidden, stream);
+  }
   return check_launch(what);
 }
 

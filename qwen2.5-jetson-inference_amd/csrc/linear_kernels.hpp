@@ -54,6 +54,50 @@ struct GemmArgs {
   int k;
 };
 
+// Skinny GEMM for a few tokens (m <= kSkinnyMaxTokens): each workgroup
+// streams 32 weight rows of one GEMM once, its waves splitting K.  Up to
+// kSkinnyMaxDescs GEMMs per launch (each on its own x and y), or one
+// gate|up pair (w2, s2, bias2 set) writing bf16(silu(bf16(gate)) *
+// bf16(up)).  block_begin is set by layout_skinny.  All GEMMs of a launch
+// share m.
+constexpr int kSkinnyMaxTokens = 32;
+constexpr int kSkinnyMaxDescs = 8;
+struct SkinnyDesc {
+  const void* w;          // [n, k] int8 or BF16
+  const uint16_t* s;      // [n, k / 64] BF16 scales (W8A16)
+  const uint16_t* bias;   // [n] or nullptr
+  const void* w2;         // pair: up_proj weight, else nullptr
+  const uint16_t* s2;
+  const uint16_t* bias2;
+  const uint16_t* x;      // [m, k] BF16
+  uint16_t* y;            // [m, n] BF16
+  int n;
+  int k;
+  int block_begin;
+  // K split over `parts` workgroups per 32-row block (layout_skinny): each
+  // leaves a 32 x 32 FP32 partial in partial[(block * parts + part) *
+  // 1024]; the last to arrive (counters[block], zero between launches)
+  // sums them in part order.
+  int parts;
+  float* partial;
+  int* counters;
+};
+struct SkinnyArgs {
+  SkinnyDesc d[kSkinnyMaxDescs];
+  int count;
+  int m;
+  int waves;  // per workgroup: 1, 2, 4 or 8 (layout_skinny)
+};
+bool gemm_skinny_supported(const void* w, const uint16_t* x, int m, int n, int k);
+// Chooses the waves per workgroup and, with `split`, the K parts of long
+// GEMMs (never of a pair); sets block_begin; returns the workgroup count.
+// The split needs skinny_scratch() floats and counters, bound by
+// bind_skinny().
+int layout_skinny(SkinnyArgs& a, bool split);
+void skinny_scratch(const SkinnyArgs& a, size_t* partial_floats, size_t* counters);
+void bind_skinny(SkinnyArgs& a, float* partial, int* counters);
+void launch_gemm_skinny(bool w8, const SkinnyArgs& a, int blocks, hipStream_t stream);
+
 // MFMA GEMM workgroup tiles (rows x columns of Y).
 enum GemmTile {
   kGemmTile128x128 = 0,

@@ -221,7 +221,48 @@ struct GemmItem {
   uint16_t* y;
 };
 
+// Up to kSkinnyMaxDescs Linears (or one gate|up pair with the SiLU-mul,
+// pair_up set) as one skinny launch, for prompts of at most
+// kSkinnyMaxTokens tokens: the weights streamed once, no tiles.  False
+// where the skinny kernel does not apply.
+bool skinny_group(const infer_hip_model* m, const GemmItem* items, int count, int tokens,
+                  const Linear* pair_up = nullptr) {
+  if (tokens < 2 || count > kSkinnyMaxDescs) return false;
+  SkinnyArgs a{};
+  a.count = count;
+  a.m = tokens;
+  for (int i = 0; i < count; ++i) {
+    const Linear& l = *items[i].l;
+    if (!gemm_skinny_supported(l.w, items[i].x, tokens, l.n, l.k)) return false;
+    a.d[i] = SkinnyDesc{l.w, m->w8 ? l.s : nullptr, l.b, nullptr, nullptr, nullptr,
+                        items[i].x, items[i].y, l.n, l.k, 0};
+  }
+  if (pair_up) {
+    if (count != 1 || pair_up->n != items[0].l->n || pair_up->k != items[0].l->k ||
+        !gemm_skinny_supported(pair_up->w, items[0].x, tokens, pair_up->n, pair_up->k)) {
+      return false;
+    }
+    a.d[0].w2 = pair_up->w;
+    a.d[0].s2 = m->w8 ? pair_up->s : nullptr;
+    a.d[0].bias2 = pair_up->b;
+  }
+  // K parts through the arena's split-K scratch (sized for them by
+  // prefill_scratch_needs), shared with the tiled launches: one launch at
+  // a time on the model's stream, and every counter back at zero after it.
+  int blocks = layout_skinny(a, true);
+  size_t pf = 0, cc = 0;
+  skinny_scratch(a, &pf, &cc);
+  if (pf <= m->gemm_partial_floats && cc <= m->gemm_counter_count) {
+    bind_skinny(a, m->gemm_partial, m->gemm_counters);
+  } else {
+    blocks = layout_skinny(a, false);
+  }
+  launch_gemm_skinny(m->w8, a, blocks, m->stream);
+  return true;
+}
+
 void linear_group(const infer_hip_model* m, const GemmItem* items, int count, int tokens) {
+  if (tokens <= kSkinnyMaxTokens && skinny_group(m, items, count, tokens)) return;
   bool grouped = tokens > 1 && count <= kInlineGroupMax;
   for (int i = 0; i < count && grouped; ++i) {
     grouped = gemm_mfma_supported(items[i].l->w, items[i].x, tokens, items[i].l->n,
@@ -295,6 +336,22 @@ void prefill_scratch_needs(const infer_hip_model_config& c, int head_dim, int ma
       *partial_floats = std::max(*partial_floats, pf);
       *counters = std::max(*counters, cc);
     }
+  }
+  // The skinny launches' K parts (prompts of 2 .. kSkinnyMaxTokens tokens;
+  // their layout does not depend on the token count).
+  for (int g = 0; g < 4; ++g) {
+    SkinnyArgs a{};
+    a.count = counts[g];
+    a.m = 2;
+    for (int i = 0; i < counts[g]; ++i) {
+      a.d[i].n = shapes[g][i][0];
+      a.d[i].k = shapes[g][i][1];
+    }
+    (void)layout_skinny(a, true);
+    size_t pf = 0, cc = 0;
+    skinny_scratch(a, &pf, &cc);
+    *partial_floats = std::max(*partial_floats, pf);
+    *counters = std::max(*counters, cc);
   }
 }
 
@@ -578,9 +635,12 @@ int run_prefill(infer_hip_model* m, const int* tokens, int count, int* next) {
     const GemmItem o[1] = {{&L.o, m->pattn, m->ptmp}};
     linear_group(m, o, 1, count);
     launch_add_rms_norm(m->px, m->ptmp, L.post_norm, m->pnorm, count, hidden, c.rms_norm_eps, s);
+    const GemmItem gate_silu[1] = {{&L.gate, m->pnorm, m->pmlp}};
     if (fuse_gate_up(m, L, count)) {
       launch_gate_up_silu(m->w8, L.gate.w, L.gate.s, L.gate.b, L.up.w, L.up.s, L.up.b, m->pnorm,
                           m->pmlp, count, inter, hidden, s);
+    } else if (count <= kSkinnyMaxTokens && skinny_group(m, gate_silu, 1, count, &L.up)) {
+      // gate|up + SiLU-mul as one skinny pair launch
     } else {
       const GemmItem gate_up[2] = {{&L.gate, m->pnorm, m->pgate}, {&L.up, m->pnorm, m->pup}};
       linear_group(m, gate_up, 2, count);

@@ -265,6 +265,10 @@ struct infer_hip_gemm_plan {
   int tile = kGemmTile64x64;
   bool w8 = false;
   double flops = 0.0;
+  // A plan of at most kSkinnyMaxDescs GEMMs of one token count up to
+  // kSkinnyMaxTokens runs as one skinny launch (no table, no scratch).
+  bool skinny = false;
+  SkinnyArgs skinny_args{};
 };
 
 extern "C" int infer_hip_gemm_plan_create(const infer_hip_gemm_desc* descs, int count,
@@ -310,6 +314,47 @@ extern "C" int infer_hip_gemm_plan_create(const infer_hip_gemm_desc* descs, int 
   if (hipGetDevice(&device) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) {
     return fail(INFER_HIP_RUNTIME_ERROR, "gemm plan: cannot query the device");
+  }
+  bool skinny = count <= kSkinnyMaxDescs;
+  for (int i = 0; i < count && skinny; ++i) {
+    skinny = descs[i].tokens == descs[0].tokens &&
+             gemm_skinny_supported(descs[i].weight, descs[i].input, descs[i].tokens,
+                                   descs[i].out_features, descs[i].in_features);
+  }
+  if (skinny) {
+    auto* plan = new (std::nothrow) infer_hip_gemm_plan();
+    if (!plan) return fail(INFER_HIP_RUNTIME_ERROR, "gemm plan: out of host memory");
+    plan->count = count;
+    plan->w8 = w8;
+    plan->flops = flops;
+    plan->device = device;
+    plan->skinny = true;
+    plan->skinny_args.count = count;
+    plan->skinny_args.m = descs[0].tokens;
+    for (int i = 0; i < count; ++i) {
+      const infer_hip_gemm_desc& d = descs[i];
+      plan->skinny_args.d[i] = SkinnyDesc{d.weight, w8 ? d.scales : nullptr, d.bias, nullptr,
+                                          nullptr, nullptr, d.input, d.output, d.out_features,
+                                          d.in_features, 0};
+    }
+    plan->blocks = layout_skinny(plan->skinny_args, true);
+    size_t pf = 0, cc = 0;
+    skinny_scratch(plan->skinny_args, &pf, &cc);
+    hipError_t st = hipSuccess;
+    if (pf > 0) {
+      st = hipMalloc(&plan->partial, pf * sizeof(float));
+      if (st == hipSuccess) st = hipMalloc(&plan->counters, cc * sizeof(int));
+      if (st == hipSuccess) st = hipMemset(plan->counters, 0, cc * sizeof(int));
+      if (st == hipSuccess) bind_skinny(plan->skinny_args, plan->partial, plan->counters);
+    }
+    if (st != hipSuccess) {
+      if (plan->partial) (void)hipFree(plan->partial);
+      if (plan->counters) (void)hipFree(plan->counters);
+      delete plan;
+      return fail(INFER_HIP_RUNTIME_ERROR, "gemm plan: %s", hipGetErrorString(st));
+    }
+    *plan_out = plan;
+    return ok();
   }
   int blocks = 0;
   size_t partial_floats = 0, counter_count = 0;
@@ -369,7 +414,9 @@ extern "C" int infer_hip_gemm_plan_create(const infer_hip_gemm_desc* descs, int 
 
 extern "C" int infer_hip_gemm_plan_launch(const infer_hip_gemm_plan* plan, hipStream_t stream) {
   if (!plan) return fail(INFER_HIP_INVALID_ARGUMENT, "gemm plan: null plan");
-  if (plan->tile == kGemmTile256x128) {
+  if (plan->skinny) {
+    launch_gemm_skinny(plan->w8, plan->skinny_args, plan->blocks, stream);
+  } else if (plan->tile == kGemmTile256x128) {
     launch_gemm_wide_grouped(plan->w8, plan->table, plan->count, plan->blocks, plan->reduce,
                              plan->reduce_count, plan->reduce_blocks, stream);
   } else {
@@ -387,7 +434,7 @@ extern "C" int infer_hip_gemm_plan_destroy(infer_hip_gemm_plan* plan) {
   int prev = 0;
   hipError_t st = hipGetDevice(&prev);
   if (st == hipSuccess && prev != plan->device) st = hipSetDevice(plan->device);
-  if (st == hipSuccess) st = hipFree(plan->table);
+  if (st == hipSuccess && plan->table) st = hipFree(plan->table);
   if (st == hipSuccess && plan->partial) st = hipFree(plan->partial);
   if (st == hipSuccess && plan->counters) st = hipFree(plan->counters);
   if (st == hipSuccess && plan->reduce) st = hipFree(plan->reduce);

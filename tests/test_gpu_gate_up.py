@@ -1,6 +1,7 @@
 """infer_hip_gemm_gate_up_silu_{w8a16,bf16}: gate_proj and up_proj of one
 input plus SiLU-mul in one launch of gate|up pair tiles (the model's prefill
-runs it for prompts over 256 tokens).
+runs it for prompts over 256 tokens), or for at most 32 tokens of the skinny
+kernel's pair form (each workgroup streams 32 gate rows and 32 up rows).
 
 The reference computes the same thing as two GEMM calls and silu_mul_bf16
 (src/qwen2.cpp:560-568).  So does this test, on the device: both GEMMs
@@ -45,7 +46,9 @@ def _case(torch, dev, tokens, inter, hidden, w8, bias, seed):
     (300, 4864, 896, False),   # a partly filled second row of tiles
     (257, 200, 128, True),     # a 64-column tail (200 = 3 x 64 + 8) and biases
     (64, 64, 64, True),        # one tile, mostly empty rows
-    (2, 136, 192, False),      # two tokens; K of 3 groups
+    (2, 136, 192, False),      # two tokens; K of 3 groups (the skinny pair, up to 32)
+    (32, 4864, 896, False),    # config 0's 32-token prompt: skinny pair, 4 waves
+    (17, 200, 128, True),      # skinny pair: ragged rows, biases
 ])
 def test_gate_up_silu_matches_separate_ops(hip, dev, w8, tokens, inter, hidden, bias):
     import model_hip

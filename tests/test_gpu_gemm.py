@@ -232,11 +232,135 @@ def test_lone_gemm_with_workspace_splits_long_k(hip, orc, dev, w8):
             hip.gemm_bf16_ws(wd, to_dev(b, dev), to_dev(x, dev), y, m, n, k, ws)
         stats = check_close(words(y), exp, what=f"gemm ws w8={w8} M={m}")
         assert stats["bit_identical"] > 0.95, stats
+    # (at M <= 32 the call runs the skinny kernel, which needs no workspace)
     small = ws[:4]
-    x = to_dev(rc.bf16_normal(rng, (32, k)), dev)
+    x = to_dev(rc.bf16_normal(rng, (128, k)), dev)
     with pytest.raises(hip.InferError) as err:
         if w8:
-            hip.gemm_w8a16_ws(wd, sd, 64, None, x, bf16_out((32, n), dev), 32, n, k, small)
+            hip.gemm_w8a16_ws(wd, sd, 64, None, x, bf16_out((128, n), dev), 128, n, k, small)
         else:
-            hip.gemm_bf16_ws(wd, None, x, bf16_out((32, n), dev), 32, n, k, small)
+            hip.gemm_bf16_ws(wd, None, x, bf16_out((128, n), dev), 128, n, k, small)
     assert err.value.status == hip.INVALID_ARGUMENT and "workspace" in str(err.value)
+
+
+# ------------------------------------------- skinny GEMM (M <= 32 tokens) --
+#
+# A lone call (automatic tile) or a plan of at most 8 GEMMs of 2..32 tokens
+# runs the skinny kernel: each workgroup streams 32 weight rows once, its
+# waves splitting K (1, 2, 4 or 8 waves of about four 64-column groups each)
+# and summing their accumulators in LDS.  Its MFMA fragments per group are
+# the 64 x 64 tile's, so with exact sums it must agree with the tile bit for
+# bit; otherwise only the association of the waves' sums differs.
+
+def test_skinny_gemm_dequant_is_bit_exact(hip, dev):
+    """One-hot activation rows (19 tokens) through the automatic path: Y[i,
+    n] = bf16(q[n, j_i] s[n, j_i / 64]) exactly, for every chunk slot, lane
+    half, group edge and wave of the K split (K = 1216: 19 groups over 8
+    waves of 3, the last wave with none)."""
+    n, k = 160, 1216
+    rng = rc.philox(91)
+    q, s = rc.w8a16_synthetic(rng, n, k)
+    q[0, :] = 127
+    q[1, :] = -127
+    cols = sorted({0, 1, 7, 8, 15, 16, 31, 32, 33, 63, 64, 65, 127, 128, 600, 1151, 1152,
+                   1200, 1215})
+    x = np.zeros((len(cols), k), np.uint16)
+    for i, j in enumerate(cols):
+        x[i, j] = 0x3F80  # BF16 1.0
+    y = bf16_out((len(cols), n), dev)
+    hip.gemm_w8a16(to_dev(q, dev), to_dev(s, dev), 64, None, to_dev(x, dev), y, len(cols), n, k)
+    got = words(y)
+    w = rc.bf16_words((rng.integers(-127, 128, size=(n, k)) / 64.0).astype(np.float32))
+    yb = bf16_out((len(cols), n), dev)
+    hip.gemm_bf16(to_dev(w, dev), None, to_dev(x, dev), yb, len(cols), n, k)
+    gotb = words(yb)
+    for i, j in enumerate(cols):
+        expect = rc.bf16_words((q[:, j].astype(np.float32)
+                                * rc.bf16_values(s[:, j // 64])).astype(np.float32))
+        np.testing.assert_array_equal(got[i], expect, err_msg=f"w8a16 column {j}")
+        np.testing.assert_array_equal(gotb[i], w[:, j], err_msg=f"bf16 column {j}")
+
+
+SKINNY_SHAPES = ((2, 100, 128), (17, 33, 192), (32, 70, 4864), (32, 4864, 896), (5, 896, 896),
+                 (31, 257, 1024))
+
+
+@pytest.mark.parametrize("mnk", SKINNY_SHAPES, ids=lambda c: "x".join(map(str, c)))
+@pytest.mark.parametrize("w8", [True, False], ids=["w8a16", "bf16"])
+def test_skinny_gemm_matches_oracle_and_tile(hip, orc, dev, mnk, w8):
+    """Ragged M and N, bias on, K from 2 to 76 groups (1 to 8 waves, several
+    rounds of loads per wave): the oracle's bar, and the 64 x 64 tile's
+    result within the reference's GEMV-vs-GEMM bound max(1/64, 1 %)."""
+    m, n, k = mnk
+    print(f"skinny w8={w8} {m}x{n}x{k}", flush=True)
+    rng = rc.philox(1000 + m + n + k + w8)
+    x = rc.bf16_normal(rng, (m, k))
+    b = rc.bf16_normal(rng, (n,))
+    dx, db = to_dev(x, dev), to_dev(b, dev)
+    y, yt = bf16_out((m, n), dev), bf16_out((m, n), dev)
+    if w8:
+        q, s = rc.w8a16_synthetic(rng, n, k)
+        exp, _ = orc.w8a16_reference(q, s, 64, b, x)
+        dq, ds = to_dev(q, dev), to_dev(s, dev)
+        hip.gemm_w8a16(dq, ds, 64, db, dx, y, m, n, k)
+        hip.gemm_w8a16_tile(dq, ds, 64, db, dx, yt, m, n, k, 3)
+    else:
+        w = rc.bf16_normal(rng, (n, k), 0.02)
+        exp = orc.bf16_linear_reference(w, b, x)
+        dw = to_dev(w, dev)
+        hip.gemm_bf16(dw, db, dx, y, m, n, k)
+        hip.gemm_bf16_tile(dw, db, dx, yt, m, n, k, 3)
+    got = words(y)
+    stats = check_close(got, exp, what=f"skinny w8={w8} {m}x{n}x{k}")
+    assert stats["bit_identical"] > 0.95, stats
+    a, t = rc.bf16_values(got), rc.bf16_values(words(yt))
+    assert np.all(np.abs(a - t) <= np.maximum(1.0 / 64, 0.01 * np.abs(t)))
+
+
+@pytest.mark.parametrize("w8", [True, False], ids=["w8a16", "bf16"])
+def test_gemm_plan_skinny_matches_single_calls(hip, orc, dev, w8):
+    """Config 3's seven Linears at M = 24 as one plan: one skinny launch of
+    seven descriptors (K split over 8 waves for all, from down's 76 groups),
+    against the oracle and the single calls (which split q..up over 4
+    waves: another association of the same partial sums), and bit-identical
+    across launches."""
+    import torch
+    m = 24
+    rng = rc.philox(2400 + w8)
+    calls, expected, singles = [], [], []
+    for (name, n, k, bias) in rc.QWEN_LINEARS:
+        x = rc.bf16_normal(rng, (m, k))
+        b = rc.bf16_normal(rng, (n,)) if bias else None
+        dx, db = to_dev(x, dev), (to_dev(b, dev) if bias else None)
+        y, y1 = bf16_out((m, n), dev), bf16_out((m, n), dev)
+        if w8:
+            q, s = rc.w8a16_synthetic(rng, n, k)
+            exp, _ = orc.w8a16_reference(q, s, 64, b, x)
+            dq, ds = to_dev(q, dev), to_dev(s, dev)
+            calls.append((dq, ds, 64, db, dx, y, m, n, k))
+            hip.gemm_w8a16(dq, ds, 64, db, dx, y1, m, n, k)
+        else:
+            w = rc.bf16_normal(rng, (n, k), 0.02)
+            exp = orc.bf16_linear_reference(w, b, x)
+            dw = to_dev(w, dev)
+            calls.append((dw, db, dx, y, m, n, k))
+            hip.gemm_bf16(dw, db, dx, y1, m, n, k)
+        expected.append(exp)
+        singles.append(y1)
+    plan = hip.GemmPlan(calls)
+    try:
+        first = None
+        for _ in range(3):
+            plan.launch()
+            torch.cuda.synchronize()
+            got = [words(c[5] if w8 else c[3]) for c in calls]
+            for g, e, y1 in zip(got, expected, singles):
+                check_close(g, e, what="skinny plan")
+                a, b1 = rc.bf16_values(g), rc.bf16_values(words(y1))
+                assert np.all(np.abs(a - b1) <= np.maximum(1.0 / 64, 0.01 * np.abs(b1)))
+            if first is None:
+                first = got
+            for g, f in zip(got, first):
+                np.testing.assert_array_equal(g, f)
+    finally:
+        plan.close()
