@@ -1092,7 +1092,10 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 // group (K 64 g + 32 h + 8 ks .. + 7), for the A fragment of token r and
 // the B fragment of weight row n0 + r: the fragments the 64 x 64 tile
 // kernel reads from LDS, so a group's MFMA partial is the same, and its
-// W8A16 scale (row n0 + r, group g) is one value per lane.  Accumulator
+// W8A16 scale (row n0 + r, group g) is one value per lane.  The loads
+// themselves are coalesced (whole 64-column rows of a group across
+// consecutive lanes) and the fragments are read back from the wave's own
+// slice of LDS.  Accumulator
 // element e is token 8 (e / 4) + 4 h + e % 4 of row n0 + r.  Buffer loads
 // whose offset is past the operand (tokens >= m, rows >= n) read zeros.
 //
@@ -1128,8 +1131,28 @@ __global__ __launch_bounds__(kWave * KW) void gemm_skinny_kernel(SkinnyArgs a) {
   const __amdgpu_buffer_rsrc_t wr2 =
       make_rsrc(PAIR ? d.w2 : d.w, static_cast<uint32_t>(d.n) * d.k * wbytes);
   // Lane offsets of group 0; group g adds 64 g columns (a scalar offset).
-  const uint32_t xoff = (static_cast<uint32_t>(r) * d.k + 32u * h) * 2u;
-  const uint32_t woff = (static_cast<uint32_t>(n0 + r) * d.k + 32u * h) * wbytes;
+  // X goes through this wave's LDS slice: load i of a group brings tokens
+  // 8 i .. 8 i + 7, lane l chunk l % 8 of token 8 i + l / 8 (eight lanes per
+  // 128-byte row: one cache line per eight lanes, where loading fragments
+  // directly touches a line per lane), and the fragments are read back from
+  // LDS, one group at a time through one 4 KB slot per wave.  The wave's own
+  // LDS accesses execute in order: no barrier.
+  __shared__ uint4 lds_x[KW][32 * kRowChunks];
+  const uint32_t xoff =
+      (static_cast<uint32_t>(lane >> 3) * d.k + 8u * (lane & 7)) * 2u;  // + 8 i rows
+  const uint32_t xrow8 = 8u * d.k * 2u;
+  // W likewise: int8 rows of a group are 64 bytes, four lanes per row,
+  // loads of 16 rows (pieces swizzled in LDS against bank conflicts); BF16
+  // rows as X's, loads of 8 rows.
+  constexpr int kWSlots = W8 ? 32 * 4 : 32 * kRowChunks;
+  __shared__ uint4 lds_w[KW][PAIR ? 2 : 1][kWSlots];
+  const uint32_t woff =
+      W8 ? static_cast<uint32_t>(n0 + (lane >> 2)) * d.k + 16u * (lane & 3)
+         : (static_cast<uint32_t>(n0 + (lane >> 3)) * d.k + 8u * (lane & 7)) * 2u;
+  const uint32_t wrows = (W8 ? 16u : 8u) * d.k * wbytes;  // between a group's loads
+  auto w_slot = [](int row, int piece) {
+    return W8 ? row * 4 + (piece ^ ((row >> 2) & 3)) : lds_slot(row, piece);
+  };
   const int srow = min(n0 + r, d.n - 1);  // scales: clamped row, its value unused past N
   const uint16_t* s1 = W8 ? d.s + static_cast<size_t>(srow) * groups : nullptr;
   const uint16_t* s2 = W8 && PAIR ? d.s2 + static_cast<size_t>(srow) * groups : nullptr;
@@ -1144,12 +1167,12 @@ __global__ __launch_bounds__(kWave * KW) void gemm_skinny_kernel(SkinnyArgs a) {
     for (int j = 0; j < kRound; ++j) {
       const uint32_t g = static_cast<uint32_t>(g0 + j < g_end ? g0 + j : g0);
 #pragma unroll
-      for (int ks = 0; ks < (W8 ? 2 : 4); ++ks) {
-        wq[j][ks] = buffer_load16(wr, woff + 16u * ks, g * kStageK * wbytes);
-        if (PAIR) wq2[j][ks] = buffer_load16(wr2, woff + 16u * ks, g * kStageK * wbytes);
+      for (int i = 0; i < (W8 ? 2 : 4); ++i) {
+        wq[j][i] = buffer_load16(wr, woff + wrows * i, g * kStageK * wbytes);
+        if (PAIR) wq2[j][i] = buffer_load16(wr2, woff + wrows * i, g * kStageK * wbytes);
       }
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) xa[j][ks] = buffer_load16(xr, xoff + 16u * ks, g * kStageK * 2u);
+      for (int i = 0; i < 4; ++i) xa[j][i] = buffer_load16(xr, xoff + xrow8 * i, g * kStageK * 2u);
       if (W8) {
         sc[j] = gload(s1 + g);
         if (PAIR) sc2[j] = gload(s2 + g);
@@ -1158,6 +1181,26 @@ __global__ __launch_bounds__(kWave * KW) void gemm_skinny_kernel(SkinnyArgs a) {
 #pragma unroll
     for (int j = 0; j < kRound; ++j) {
       if (g0 + j >= g_end) break;
+      // X: the coalesced pieces into LDS, the fragments back out
+#pragma unroll
+      for (int i = 0; i < 4; ++i) lds_x[wave][lds_slot(8 * i + (lane >> 3), lane & 7)] = xa[j][i];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) xa[j][ks] = lds_x[wave][lds_slot(r, 4 * h + ks)];
+      // W: the same; a lane then holds int8 pieces 2 h, 2 h + 1 (chunks
+      // 4 h .. 4 h + 3) or BF16 chunks 4 h .. 4 h + 3 of row n0 + r
+      constexpr int kRowsPerLoad = W8 ? 16 : 8, kLanesPerRow = W8 ? 4 : 8;
+#pragma unroll
+      for (int i = 0; i < (W8 ? 2 : 4); ++i) {
+        const int slot = w_slot(kRowsPerLoad * i + lane / kLanesPerRow, lane % kLanesPerRow);
+        lds_w[wave][0][slot] = wq[j][i];
+        if (PAIR) lds_w[wave][PAIR ? 1 : 0][slot] = wq2[PAIR ? j : 0][PAIR ? i : 0];
+      }
+#pragma unroll
+      for (int i = 0; i < (W8 ? 2 : 4); ++i) {
+        const int slot = w_slot(r, (W8 ? 2 : 4) * h + i);
+        wq[j][i] = lds_w[wave][0][slot];
+        if (PAIR) wq2[PAIR ? j : 0][PAIR ? i : 0] = lds_w[wave][PAIR ? 1 : 0][slot];
+      }
       bf16x8_t fb[4], fb2[4];
       if (W8) {
         uint4 lo, hi;
