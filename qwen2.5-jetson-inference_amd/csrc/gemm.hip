@@ -35,6 +35,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <initializer_list>
 
 #include "device_common.hpp"
 #include "linear_kernels.hpp"
@@ -1117,8 +1118,13 @@ __global__ __launch_bounds__(kWave * KW) void gemm_skinny_kernel(SkinnyArgs a) {
   }
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int r = lane & 31, h = lane >> 5;
-  const int rb = (b - d.block_begin) / d.parts, part = (b - d.block_begin) % d.parts;
-  const int n0 = rb * 32;
+  // workgroup = (row block, token tile of 32, K part), part fastest
+  const int tiles_t = (a.m + 31) / 32;
+  const int local = b - d.block_begin;
+  const int part = local % d.parts, tt = local / d.parts % tiles_t;
+  const int rb = local / d.parts / tiles_t;
+  const int n0 = rb * 32, m0 = tt * 32;
+  const int tile = rb * tiles_t + tt;  // split-K counter and partials
   const int groups = d.k / kStageK;
   // this part's groups, then this wave's share of them
   const int per_part = (groups + d.parts - 1) / d.parts;
@@ -1126,7 +1132,8 @@ __global__ __launch_bounds__(kWave * KW) void gemm_skinny_kernel(SkinnyArgs a) {
   const int per = (p_end - p_begin + KW - 1) / KW;
   const int g_begin = min(p_end, p_begin + wave * per), g_end = min(p_end, g_begin + per);
   const uint32_t wbytes = W8 ? 1u : 2u;
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(d.x, static_cast<uint32_t>(a.m) * d.k * 2u);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(d.x + static_cast<size_t>(m0) * d.k,
+                                              static_cast<uint32_t>(a.m - m0) * d.k * 2u);
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(d.w, static_cast<uint32_t>(d.n) * d.k * wbytes);
   const __amdgpu_buffer_rsrc_t wr2 =
       make_rsrc(PAIR ? d.w2 : d.w, static_cast<uint32_t>(d.n) * d.k * wbytes);
@@ -1294,7 +1301,7 @@ __global__ __launch_bounds__(kWave * KW) void gemm_skinny_kernel(SkinnyArgs a) {
     // Split-K hand-off (wave 0 only).  Lane l's 16 values are 4 16-byte
     // vectors at [(q * 64 + l) * 4] of the part's 1024 floats.
     const __amdgpu_buffer_rsrc_t pr =
-        make_rsrc(d.partial + static_cast<size_t>(rb) * d.parts * 1024,
+        make_rsrc(d.partial + static_cast<size_t>(tile) * d.parts * 1024,
                   static_cast<uint32_t>(d.parts) * 4096u);
     const uint32_t mine = static_cast<uint32_t>(part) * 4096u;
 #pragma unroll
@@ -1306,7 +1313,7 @@ __global__ __launch_bounds__(kWave * KW) void gemm_skinny_kernel(SkinnyArgs a) {
     __builtin_amdgcn_s_waitcnt(0);  // this lane's part is stored
     int arrived = 0;
     if (lane == 0) {
-      arrived = __hip_atomic_fetch_add(d.counters + rb, 1, __ATOMIC_RELAXED,
+      arrived = __hip_atomic_fetch_add(d.counters + tile, 1, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
     }
     if (__builtin_amdgcn_readfirstlane(arrived) != d.parts - 1) return;
@@ -1329,7 +1336,7 @@ __global__ __launch_bounds__(kWave * KW) void gemm_skinny_kernel(SkinnyArgs a) {
     }
     acc = sum;
     if (lane == 0) {  // ready for the next launch
-      __hip_atomic_store(d.counters + rb, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(d.counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 
@@ -1339,7 +1346,7 @@ __global__ __launch_bounds__(kWave * KW) void gemm_skinny_kernel(SkinnyArgs a) {
   const float bias2 = PAIR && d.bias2 ? bf16_to_f32(gload(d.bias2 + n)) : 0.0f;
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
-    const int m = 8 * (e >> 2) + 4 * h + (e & 3);
+    const int m = m0 + 8 * (e >> 2) + 4 * h + (e & 3);
     if (m >= a.m) continue;
     float v;
     if (PAIR) {
@@ -1391,6 +1398,16 @@ bool gemm_skinny_supported(const void* w, const uint16_t* x, int m, int n, int k
   return m >= 1 && m <= kSkinnyMaxTokens && n >= 1 && gemm_mfma_supported(w, x, m, n, k);
 }
 
+bool gemm_skinny_preferred(bool w8, int m, int n, int k) {
+  // Single calls on MI355X, us (skinny / 64 x 64 tile), W8A16: M = 32 q
+  // 5.1 / 7.1, gate 5.6 / 7.1, down 11.7 / 29.1; M = 64 gate 6.9 / 7.1;
+  // M = 128 q 5.2 / 7.1, gate 8.5 / 8.1, down 12.5 / 30.0.  BF16: M = 64 q
+  // 5.0 / 5.4, gate 7.2 / 6.5; M = 128 q 5.9 / 5.5, down 12.4 / 22.8.
+  if (m <= 32 || (w8 && m <= 64)) return true;
+  if (m > kSkinnyMaxTokens || n > 1024) return false;
+  return w8 || m <= 64 || k >= 2048;
+}
+
 int layout_skinny(SkinnyArgs& a, bool split) {
   // About four groups of 64 per wave: one round of loads.  Without a split,
   // up to 8 waves per workgroup (two per SIMD keep 256 registers per wave;
@@ -1416,7 +1433,7 @@ int layout_skinny(SkinnyArgs& a, bool split) {
     d.partial = nullptr;
     d.counters = nullptr;
     d.block_begin = blocks;
-    blocks += (d.n + 31) / 32 * d.parts;
+    blocks += (d.n + 31) / 32 * ((a.m + 31) / 32) * d.parts;
   }
   return blocks;
 }
@@ -1425,9 +1442,9 @@ void skinny_scratch(const SkinnyArgs& a, size_t* partial_floats, size_t* counter
   size_t pf = 0, cc = 0;
   for (int i = 0; i < a.count; ++i) {
     if (a.d[i].parts > 1) {
-      const size_t blocks = static_cast<size_t>(a.d[i].n + 31) / 32;
-      pf += blocks * a.d[i].parts * 1024;
-      cc += blocks;
+      const size_t tiles = static_cast<size_t>(a.d[i].n + 31) / 32 * ((a.m + 31) / 32);
+      pf += tiles * a.d[i].parts * 1024;
+      cc += tiles;
     }
   }
   *partial_floats = pf;
@@ -1438,11 +1455,11 @@ void bind_skinny(SkinnyArgs& a, float* partial, int* counters) {
   for (int i = 0; i < a.count; ++i) {
     SkinnyDesc& d = a.d[i];
     if (d.parts > 1) {
-      const size_t blocks = static_cast<size_t>(d.n + 31) / 32;
+      const size_t tiles = static_cast<size_t>(d.n + 31) / 32 * ((a.m + 31) / 32);
       d.partial = partial;
       d.counters = counters;
-      partial += blocks * d.parts * 1024;
-      counters += blocks;
+      partial += tiles * d.parts * 1024;
+      counters += tiles;
     }
   }
 }
@@ -1621,7 +1638,7 @@ int current_cus(int* cus) {
 LoneLayout lone_layout(bool w8, const void* w, const uint16_t* s, const uint16_t* bias,
                        const uint16_t* x, uint16_t* y, int m, int n, int k, int cus) {
   LoneLayout o;
-  if (m >= 2 && m <= kSkinnyMaxTokens && gemm_skinny_supported(w, x, m, n, k)) {
+  if (m >= 2 && gemm_skinny_supported(w, x, m, n, k) && gemm_skinny_preferred(w8, m, n, k)) {
     o.skinny = true;
     o.sk.count = 1;
     o.sk.m = m;
@@ -1727,7 +1744,8 @@ int gemm_w8a16_impl(const int8_t* weight, const uint16_t* scales, int group_size
     launch_w8a16_gemv_fast({weight, scales, bias, input, output, out_features, in_features},
                            stream);
   } else if (tile < 0 && tokens > 1 &&
-             gemm_skinny_supported(weight, input, tokens, out_features, in_features)) {
+             gemm_skinny_supported(weight, input, tokens, out_features, in_features) &&
+             gemm_skinny_preferred(true, tokens, out_features, in_features)) {
     bool done = false;
     if (ws_mode) {  // long K: split over workgroups on the workspace
       const int rc = launch_lone_split(true, weight, scales, bias, input, output, tokens,
@@ -1773,7 +1791,8 @@ int gemm_bf16_impl(const uint16_t* weight, const uint16_t* bias, const uint16_t*
   if (tokens == 1 && bf16_gemv_fast_supported(weight, input, in_features)) {
     launch_bf16_gemv_fast({weight, bias, input, output, out_features, in_features}, stream);
   } else if (tile < 0 && tokens > 1 &&
-             gemm_skinny_supported(weight, input, tokens, out_features, in_features)) {
+             gemm_skinny_supported(weight, input, tokens, out_features, in_features) &&
+             gemm_skinny_preferred(false, tokens, out_features, in_features)) {
     bool done = false;
     if (ws_mode) {  // long K: split over workgroups on the workspace
       const int rc = launch_lone_split(false, weight, nullptr, bias, input, output, tokens,
@@ -1823,7 +1842,7 @@ int gate_up_silu_impl(bool w8, const void* gate_w, const uint16_t* gate_s,
                 "under 2 GiB",
                 what);
   }
-  if (tokens <= kSkinnyMaxTokens) {
+  if (gemm_skinny_preferred(w8, tokens, 2 * inter, hidden)) {  // the pair: two GEMMs' rows
     SkinnyArgs a{};
     a.count = 1;
     a.m = tokens;
@@ -1887,10 +1906,12 @@ extern "C" size_t infer_hip_gemm_workspace_bytes(int max_tokens, int out_feature
   if (current_cus(&cus) != INFER_HIP_OK) return 0;
   size_t partials = 0, counters = 0;
   for (int m = 2; m <= max_tokens; ++m) {
-    const LoneLayout o = lone_layout(false, nullptr, nullptr, nullptr, nullptr, nullptr, m,
-                                     out_features, in_features, cus);
-    partials = std::max(partials, o.partial_bytes);
-    counters = std::max(counters, o.counter_bytes);
+    for (const bool w8 : {false, true}) {  // (the two may pick different kernels)
+      const LoneLayout o = lone_layout(w8, nullptr, nullptr, nullptr, nullptr, nullptr, m,
+                                       out_features, in_features, cus);
+      partials = std::max(partials, o.partial_bytes);
+      counters = std::max(counters, o.counter_bytes);
+    }
   }
   if (partials == 0) return 0;       // no call splits
   return partials + counters + 256;  // 256: the partials' alignment at the end

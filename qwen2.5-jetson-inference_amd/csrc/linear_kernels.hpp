@@ -55,12 +55,13 @@ struct GemmArgs {
 };
 
 // Skinny GEMM for a few tokens (m <= kSkinnyMaxTokens): each workgroup
-// streams 32 weight rows of one GEMM once, its waves splitting K.  Up to
+// streams 32 weight rows of one GEMM for 32 tokens, its waves splitting K
+// (one workgroup per 32-token tile).  Up to
 // kSkinnyMaxDescs GEMMs per launch (each on its own x and y), or one
 // gate|up pair (w2, s2, bias2 set) writing bf16(silu(bf16(gate)) *
 // bf16(up)).  block_begin is set by layout_skinny.  All GEMMs of a launch
 // share m.
-constexpr int kSkinnyMaxTokens = 32;
+constexpr int kSkinnyMaxTokens = 128;
 constexpr int kSkinnyMaxDescs = 8;
 struct SkinnyDesc {
   const void* w;          // [n, k] int8 or BF16
@@ -89,6 +90,12 @@ struct SkinnyArgs {
   int waves;  // per workgroup: 1, 2, 4 or 8 (layout_skinny)
 };
 bool gemm_skinny_supported(const void* w, const uint16_t* x, int m, int n, int k);
+// Where the skinny kernel beats the 64 x 64 tiles (measured): up to 32
+// tokens always, up to 64 on int8 weights; up to kSkinnyMaxTokens for
+// narrow GEMMs (N <= 1024), on BF16 weights only up to 64 tokens unless K
+// is long.  A token tile of 32 re-reads the weights, which wide GEMMs
+// cannot afford.
+bool gemm_skinny_preferred(bool w8, int m, int n, int k);
 // Chooses the waves per workgroup and, with `split`, the K parts of long
 // GEMMs (never of a pair); sets block_begin; returns the workgroup count.
 // The split needs skinny_scratch() floats and counters, bound by

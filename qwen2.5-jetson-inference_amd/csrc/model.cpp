@@ -222,9 +222,9 @@ struct GemmItem {
 };
 
 // Up to kSkinnyMaxDescs Linears (or one gate|up pair with the SiLU-mul,
-// pair_up set) as one skinny launch, for prompts of at most
-// kSkinnyMaxTokens tokens: the weights streamed once, no tiles.  False
-// where the skinny kernel does not apply.
+// pair_up set) as one skinny launch, for short prompts: the weights
+// streamed once per 32 tokens, no tiles.  False where the skinny kernel does
+// not apply or is not preferred (gemm_skinny_preferred).
 bool skinny_group(const infer_hip_model* m, const GemmItem* items, int count, int tokens,
                   const Linear* pair_up = nullptr) {
   if (tokens < 2 || count > kSkinnyMaxDescs) return false;
@@ -233,7 +233,10 @@ bool skinny_group(const infer_hip_model* m, const GemmItem* items, int count, in
   a.m = tokens;
   for (int i = 0; i < count; ++i) {
     const Linear& l = *items[i].l;
-    if (!gemm_skinny_supported(l.w, items[i].x, tokens, l.n, l.k)) return false;
+    if (!gemm_skinny_supported(l.w, items[i].x, tokens, l.n, l.k) ||
+        !gemm_skinny_preferred(m->w8, tokens, pair_up ? 2 * l.n : l.n, l.k)) {
+      return false;
+    }
     a.d[i] = SkinnyDesc{l.w, m->w8 ? l.s : nullptr, l.b, nullptr, nullptr, nullptr,
                         items[i].x, items[i].y, l.n, l.k, 0};
   }
@@ -262,7 +265,7 @@ bool skinny_group(const infer_hip_model* m, const GemmItem* items, int count, in
 }
 
 void linear_group(const infer_hip_model* m, const GemmItem* items, int count, int tokens) {
-  if (tokens <= kSkinnyMaxTokens && skinny_group(m, items, count, tokens)) return;
+  if (skinny_group(m, items, count, tokens)) return;
   bool grouped = tokens > 1 && count <= kInlineGroupMax;
   for (int i = 0; i < count && grouped; ++i) {
     grouped = gemm_mfma_supported(items[i].l->w, items[i].x, tokens, items[i].l->n,
@@ -338,11 +341,11 @@ void prefill_scratch_needs(const infer_hip_model_config& c, int head_dim, int ma
     }
   }
   // The skinny launches' K parts (prompts of 2 .. kSkinnyMaxTokens tokens;
-  // their layout does not depend on the token count).
+  // the most at the most tokens: one tile of parts per 32 tokens).
   for (int g = 0; g < 4; ++g) {
     SkinnyArgs a{};
     a.count = counts[g];
-    a.m = 2;
+    a.m = std::min(max_seq, kSkinnyMaxTokens);
     for (int i = 0; i < counts[g]; ++i) {
       a.d[i].n = shapes[g][i][0];
       a.d[i].k = shapes[g][i][1];
@@ -639,7 +642,7 @@ int run_prefill(infer_hip_model* m, const int* tokens, int count, int* next) {
     if (fuse_gate_up(m, L, count)) {
       launch_gate_up_silu(m->w8, L.gate.w, L.gate.s, L.gate.b, L.up.w, L.up.s, L.up.b, m->pnorm,
                           m->pmlp, count, inter, hidden, s);
-    } else if (count <= kSkinnyMaxTokens && skinny_group(m, gate_silu, 1, count, &L.up)) {
+    } else if (skinny_group(m, gate_silu, 1, count, &L.up)) {
       // gate|up + SiLU-mul as one skinny pair launch
     } else {
       const GemmItem gate_up[2] = {{&L.gate, m->pnorm, m->pgate}, {&L.up, m->pnorm, m->pup}};

@@ -265,8 +265,9 @@ struct infer_hip_gemm_plan {
   int tile = kGemmTile64x64;
   bool w8 = false;
   double flops = 0.0;
-  // A plan of at most kSkinnyMaxDescs GEMMs of one token count up to
-  // kSkinnyMaxTokens runs as one skinny launch (no table, no scratch).
+  // A plan of at most kSkinnyMaxDescs GEMMs of one token count where the
+  // skinny kernel is preferred for every one of them runs as one skinny
+  // launch (no table; scratch only for K parts).
   bool skinny = false;
   SkinnyArgs skinny_args{};
 };
@@ -319,7 +320,9 @@ extern "C" int infer_hip_gemm_plan_create(const infer_hip_gemm_desc* descs, int 
   for (int i = 0; i < count && skinny; ++i) {
     skinny = descs[i].tokens == descs[0].tokens &&
              gemm_skinny_supported(descs[i].weight, descs[i].input, descs[i].tokens,
-                                   descs[i].out_features, descs[i].in_features);
+                                   descs[i].out_features, descs[i].in_features) &&
+             gemm_skinny_preferred(w8, descs[i].tokens, descs[i].out_features,
+                                   descs[i].in_features);
   }
   if (skinny) {
     auto* plan = new (std::nothrow) infer_hip_gemm_plan();

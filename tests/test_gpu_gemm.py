@@ -282,7 +282,10 @@ def test_skinny_gemm_dequant_is_bit_exact(hip, dev):
 
 
 SKINNY_SHAPES = ((2, 100, 128), (17, 33, 192), (32, 70, 4864), (32, 4864, 896), (5, 896, 896),
-                 (31, 257, 1024))
+                 (31, 257, 1024),
+                 # token tiles of 32 (narrow GEMMs up to 128 tokens; BF16 up to 64
+                 # unless K is long, the tile otherwise)
+                 (64, 896, 896), (100, 130, 1024), (128, 896, 4864), (77, 1000, 128))
 
 
 @pytest.mark.parametrize("mnk", SKINNY_SHAPES, ids=lambda c: "x".join(map(str, c)))
@@ -315,6 +318,43 @@ def test_skinny_gemm_matches_oracle_and_tile(hip, orc, dev, mnk, w8):
     assert stats["bit_identical"] > 0.95, stats
     a, t = rc.bf16_values(got), rc.bf16_values(words(yt))
     assert np.all(np.abs(a - t) <= np.maximum(1.0 / 64, 0.01 * np.abs(t)))
+
+
+def test_gemm_plan_skinny_token_tiles(hip, orc, dev):
+    """A plan of the five narrow Linears (q, k, v, o, down) at M = 100
+    tokens: one skinny launch of four 32-token tiles per row block, down
+    split over K into parts per (row block, token tile) — against the
+    oracle, and bit-identical across launches."""
+    import torch
+    m = 100
+    rng = rc.philox(2500)
+    calls, expected = [], []
+    for (name, n, k, bias) in rc.QWEN_LINEARS:
+        if n > 1024:
+            continue
+        x = rc.bf16_normal(rng, (m, k))
+        b = rc.bf16_normal(rng, (n,)) if bias else None
+        q, s = rc.w8a16_synthetic(rng, n, k)
+        exp, _ = orc.w8a16_reference(q, s, 64, b, x)
+        calls.append((to_dev(q, dev), to_dev(s, dev), 64, to_dev(b, dev) if bias else None,
+                      to_dev(x, dev), bf16_out((m, n), dev), m, n, k))
+        expected.append(exp)
+    plan = hip.GemmPlan(calls)
+    try:
+        first = None
+        for _ in range(3):
+            plan.launch()
+            torch.cuda.synchronize()
+            got = [words(c[5]) for c in calls]
+            for g, e in zip(got, expected):
+                stats = check_close(g, e, what="skinny plan, token tiles")
+                assert stats["bit_identical"] > 0.95, stats
+            if first is None:
+                first = got
+            for g, f in zip(got, first):
+                np.testing.assert_array_equal(g, f)
+    finally:
+        plan.close()
 
 
 @pytest.mark.parametrize("w8", [True, False], ids=["w8a16", "bf16"])
