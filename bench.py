@@ -315,7 +315,10 @@ def prefill_main(args, dev, hip) -> int:
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": ("gemm_wide_grouped_kernel + splitk_reduce_kernel (7 GEMMs of one layer; "
+            # (the plan's kernel: gemm_skinny_preferred for all 7 shapes, else tiles)
+            "kernel": ("gemm_skinny_kernel (7 GEMMs of one layer; 32 weight rows per "
+                       "workgroup, down_proj split over K)" if m <= (64 if w8 else 32) else
+                       "gemm_wide_grouped_kernel + splitk_reduce_kernel (7 GEMMs of one layer; "
                        "256 x 128 tiles, down_proj split over K)" if m >= 256 else
                        "gemm_grouped_kernel (7 GEMMs of one layer; 64 x 64 tiles)"),
             "achieved": round(tflops, 1),
