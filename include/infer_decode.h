@@ -30,7 +30,11 @@
  *   infer_hip_gemv_w8a16_rows          gemv_w8a16 + add_inplace_bf16 (cuda_ops.hpp:
  *                                      98-99) for down_proj and the residual
  *                                      (qwen2.cpp:655-659)
- *   infer_hip_attention_merge_o_proj   the merge of a context-split
+ *   infer_hip_attention_decode_spans_bf16
+ *                                      attention_decode_bf16 in context spans
+ *                                      (any capacity, head_dim 64 or 128), whose
+ *                                      records
+ *   infer_hip_attention_merge_o_proj   merges: the merge of a context-split
  *                                      attention_decode_bf16 (cuda_ops.hpp:86-91)
  *                                      + gemv (o_proj) + add_inplace_bf16
  *                                      (qwen2.cpp:633-641)
@@ -236,6 +240,24 @@ int infer_hip_gemv_w8a16_rows(const int8_t* weight, const uint16_t* scales,
 int infer_hip_gemv_bf16_rows(const uint16_t* weight, const uint16_t* bias,
                              const uint16_t* input, uint16_t* output, int out_features,
                              int in_features, hipStream_t stream);
+
+/* The decode attention in context spans, for any KV capacity and head_dim
+ * 64 or 128 (the form the decode step runs beyond 1024 positions or at
+ * head_dim 128): q rotated ([num_heads][head_dim] BF16), the caches holding
+ * rows [0, p], p = min(*position, max_sequence_length - 1), as for
+ * infer_hip_attention_decode_bf16.  For query head h and span c <= p / span
+ * (span and splits from infer_hip_attention_decode_span / _splits) one
+ * workgroup stores the record partials[(h * splits + c) * (head_dim + 2) +
+ * i]: i < head_dim the span's unnormalised sum of e^(score - m) v, then m
+ * (its largest score) and l (its sum of e^(score - m)); spans past the
+ * context store nothing.  infer_hip_attention_merge_o_proj merges them.
+ * Rows past p are never summed.  Replaces attention_decode_bf16
+ * (cuda_ops.hpp:86-91) for contexts the whole-context entry does not take. */
+int infer_hip_attention_decode_spans_bf16(const uint16_t* q, const uint16_t* key_cache,
+                                          const uint16_t* value_cache, const int* position,
+                                          float* partials, int num_heads, int num_kv_heads,
+                                          int head_dim, int max_sequence_length,
+                                          hipStream_t stream);
 
 /* Context span and split count of the decode attention at a KV capacity of
  * max_sequence_length positions and head_dim (64 or 128): split i covers

@@ -298,6 +298,34 @@ extern "C" int infer_hip_gemv_bf16_rows(const uint16_t* weight, const uint16_t* 
                    stream, "gemv_bf16_rows");
 }
 
+extern "C" int infer_hip_attention_decode_spans_bf16(
+    const uint16_t* q, const uint16_t* key_cache, const uint16_t* value_cache,
+    const int* position, float* partials, int num_heads, int num_kv_heads, int head_dim,
+    int max_sequence_length, hipStream_t stream) {
+  const char* what = "attention_decode_spans_bf16";
+  if (!q || !key_cache || !value_cache || !position || !partials) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: null pointer", what);
+  }
+  if (num_heads < 1 || num_kv_heads < 1 || num_heads % num_kv_heads != 0) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: %d heads, %d kv heads", what, num_heads,
+                num_kv_heads);
+  }
+  if (!attention_head_dim_supported(head_dim) || max_sequence_length < 1) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "%s: head_dim %d (64 or 128), max_sequence_length %d", what, head_dim,
+                max_sequence_length);
+  }
+  if (!aligned16(key_cache) || !aligned16(value_cache)) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: caches must be 16-byte aligned", what);
+  }
+  if (2ll * num_kv_heads * max_sequence_length * head_dim >= 0x7FFFFFFFll) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: caches over 2 GiB", what);
+  }
+  launch_attention_decode_spans(q, key_cache, value_cache, position, num_heads, num_kv_heads,
+                                head_dim, max_sequence_length, partials, stream);
+  return check_launch(what);
+}
+
 extern "C" int infer_hip_attention_decode_span(int max_sequence_length, int head_dim) {
   if (max_sequence_length < 1 || !attention_head_dim_supported(head_dim)) return 0;
   return attention_span(max_sequence_length, head_dim);

@@ -384,7 +384,10 @@ __device__ __forceinline__ void load_tile_rows(__amdgpu_buffer_rsrc_t kr_rsrc,
   }
 }
 
-template <int HD>
+// ROPED: q is rotated already and the caches hold the token's k and v at
+// pos (the attention_decode_bf16 contract); otherwise q and k_new are
+// rotated here and the token's k and v stored (the model's decode step).
+template <int HD, bool ROPED>
 __global__ __launch_bounds__(kAttnWaves * kWave) void attention_decode_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_new,
     const uint16_t* __restrict__ v_new, uint16_t* __restrict__ key_cache,
@@ -426,8 +429,10 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void attention_decode_kernel(
 
   // q of head h and this token's k, rotated and rounded to BF16 (as the
   // reference's rope kernel stores them), and this token's v.
-  const float2* cs = rope + static_cast<size_t>(pos) * half;
-  if (tid < half) {
+  if (ROPED) {
+    if (tid < HD) qs[tid] = load_bf16(q + static_cast<size_t>(h) * HD + tid);
+  } else if (tid < half) {
+    const float2* cs = rope + static_cast<size_t>(pos) * half;
     const uint16_t* qh = q + static_cast<size_t>(h) * HD;
     const uint16_t* kh = k_new + static_cast<size_t>(g) * HD;
     const float2 r = cs[tid];
@@ -445,7 +450,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void attention_decode_kernel(
         reinterpret_cast<const uint4*>(v_new + static_cast<size_t>(g) * HD)[j];
   }
   __syncthreads();
-  if (h % group == 0 && pos >= begin && pos < end && tid < 2 * kPieces) {
+  if (!ROPED && h % group == 0 && pos >= begin && pos < end && tid < 2 * kPieces) {
     // The kv head's first query head, in the span holding pos, stores the
     // new token's k and v.
     const int j = tid % kPieces;
@@ -466,7 +471,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void attention_decode_kernel(
     if (kPrefetch && t0 + W * kTile < end) {
       load_tile_rows<HD>(kr_rsrc, vr_rsrc, p + W * kTile, kn, vn);
     }
-    if (p == pos) {
+    if (!ROPED && p == pos) {
 #pragma unroll
       for (int j = 0; j < kPieces; ++j) {
         kr[j] = reinterpret_cast<const uint4*>(knew)[j];
@@ -1370,14 +1375,45 @@ void launch_attention_decode(const uint16_t* q, const uint16_t* k_new, const uin
   const int span = attention_span(max_seq, head_dim);
   const int splits = attention_splits(max_seq, head_dim);
   const dim3 grid(splits, heads), block(kAttnWaves * kWave);
+#define QLIN_SPANS(HDV, R)                                                                      \
+  hipLaunchKernelGGL((attention_decode_kernel<HDV, R>), grid, block, 0, stream, q, k_new, v_new, \
+                     key_cache, value_cache, rope, pos, heads, kv_heads, max_seq, span, splits,  \
+                     partial)
   if (head_dim == 64) {
-    hipLaunchKernelGGL(attention_decode_kernel<64>, grid, block, 0, stream, q, k_new, v_new,
-                       key_cache, value_cache, rope, pos, heads, kv_heads, max_seq, span,
-                       splits, partial);
+    if (roped) {
+      QLIN_SPANS(64, true);
+    } else {
+      QLIN_SPANS(64, false);
+    }
   } else {
-    hipLaunchKernelGGL(attention_decode_kernel<128>, grid, block, 0, stream, q, k_new, v_new,
-                       key_cache, value_cache, rope, pos, heads, kv_heads, max_seq, span,
-                       splits, partial);
+    if (roped) {
+      QLIN_SPANS(128, true);
+    } else {
+      QLIN_SPANS(128, false);
+    }
+  }
+#undef QLIN_SPANS
+}
+
+void launch_attention_decode_spans(const uint16_t* q, const uint16_t* key_cache,
+                                   const uint16_t* value_cache, const int* pos, int heads,
+                                   int kv_heads, int head_dim, int max_seq, float* partial,
+                                   hipStream_t stream) {
+  // the split form even where the whole-context one applies (span
+  // kAttnWholeMax, one split), pre-rotated
+  const int span = attention_span(max_seq, head_dim);
+  const int splits = attention_splits(max_seq, head_dim);
+  const dim3 grid(splits, heads), block(kAttnWaves * kWave);
+  uint16_t* kc = const_cast<uint16_t*>(key_cache);
+  uint16_t* vc = const_cast<uint16_t*>(value_cache);
+  if (head_dim == 64) {
+    hipLaunchKernelGGL((attention_decode_kernel<64, true>), grid, block, 0, stream, q, nullptr,
+                       nullptr, kc, vc, nullptr, pos, heads, kv_heads, max_seq, span, splits,
+                       partial);
+  } else {
+    hipLaunchKernelGGL((attention_decode_kernel<128, true>), grid, block, 0, stream, q, nullptr,
+                       nullptr, kc, vc, nullptr, pos, heads, kv_heads, max_seq, span, splits,
+                       partial);
   }
 }
 

@@ -62,15 +62,24 @@ void launch_attention_decode_halves(const uint16_t* q, const uint16_t* key_cache
                                     hipStream_t stream);
 int attention_span(int max_seq, int head_dim);
 int attention_splits(int max_seq, int head_dim);
-// roped (whole form): q is already rotated and the token's k and v are in
-// the caches at pos; otherwise (split form) q and k_new are rotated here and
-// the first query head of each kv head stores k_new and v_new at pos.
+// roped: q is already rotated and the token's k and v are in the caches at
+// pos (the whole form where it applies, else the split form); otherwise
+// (split form) q and k_new are rotated here and the first query head of
+// each kv head stores k_new and v_new at pos.
 // pos: the token's position (device memory).
 void launch_attention_decode(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
                              uint16_t* key_cache, uint16_t* value_cache, const float2* rope,
                              const int* pos, int heads, int kv_heads, int head_dim,
                              int max_seq, bool roped, float* partial, uint16_t* out,
                              hipStream_t stream);
+// The split form on a pre-rotated q and caches holding the token (the
+// attention_decode_bf16 contract), at any KV capacity: one (acc, max, sum)
+// record per (head, span) in partial (heads x attention_splits() x
+// (head_dim + 2) floats); spans past the context write nothing.
+void launch_attention_decode_spans(const uint16_t* q, const uint16_t* key_cache,
+                                   const uint16_t* value_cache, const int* pos, int heads,
+                                   int kv_heads, int head_dim, int max_seq, float* partial,
+                                   hipStream_t stream);
 void launch_attention_prefill(const uint16_t* q, const uint16_t* key_cache,
                               const uint16_t* value_cache, uint16_t* out, int count, int heads,
                               int kv_heads, int head_dim, int max_seq, hipStream_t stream);

@@ -30,6 +30,7 @@ EXPORTED_SYMBOLS = (
     "infer_hip_attention_halves_o_proj_bf16",
     "infer_hip_gemv_w8a16_rows",
     "infer_hip_gemv_bf16_rows",
+    "infer_hip_attention_decode_spans_bf16",
     "infer_hip_attention_decode_span",
     "infer_hip_attention_decode_splits",
     "infer_hip_attention_merge_o_proj",
@@ -91,6 +92,7 @@ def load():
         "infer_hip_attention_halves_o_proj_bf16": ([p, p, i, i, p, p, i, p], i),
         "infer_hip_gemv_w8a16_rows": ([p, p, p, p, p, i, i, p], i),
         "infer_hip_gemv_bf16_rows": ([p, p, p, p, i, i, p], i),
+        "infer_hip_attention_decode_spans_bf16": ([p, p, p, p, p, i, i, i, i, p], i),
         "infer_hip_attention_decode_span": ([i, i], i),
         "infer_hip_attention_decode_splits": ([i, i], i),
         "infer_hip_attention_merge_o_proj": ([p, p, i, i, i, i, i, p, p, p, i, p], i),
@@ -224,6 +226,15 @@ def gemv_bf16_rows(weight, bias, input, output, out_features: int, in_features: 
                    stream=None) -> None:
     _check(load().infer_hip_gemv_bf16_rows(_ptr(weight), _ptr(bias), _ptr(input), _ptr(output),
                                            out_features, in_features, _stream(stream)))
+
+
+def attention_decode_spans_bf16(q, key_cache, value_cache, position, partials, num_heads: int,
+                                num_kv_heads: int, head_dim: int, max_sequence_length: int,
+                                stream=None) -> None:
+    """partials: float32 [num_heads, attention_decode_splits(), head_dim + 2]."""
+    _check(load().infer_hip_attention_decode_spans_bf16(
+        _ptr(q), _ptr(key_cache), _ptr(value_cache), _ptr(position), _ptr(partials), num_heads,
+        num_kv_heads, head_dim, max_sequence_length, _stream(stream)))
 
 
 def attention_decode_span(max_sequence_length: int, head_dim: int = 64) -> int:

@@ -320,6 +320,21 @@ def test_halves_attention_ops_reject_bad_arguments(hip):
     assert g(4096, None, 14, 1024, 4096, 4096, 4096, 896, None) == bad
 
 
+def test_attention_spans_rejects_bad_arguments(hip):
+    """infer_hip_attention_decode_spans_bf16: shapes, nulls and alignment are
+    checked on the host; nothing is launched."""
+    import decode_hip
+    lib = decode_hip.load()
+    bad = hip.INVALID_ARGUMENT
+    f = lib.infer_hip_attention_decode_spans_bf16
+    assert f(4096, 4096, 4096, 4096, 4096, 14, 2, 96, 2048, None) == bad   # head_dim
+    assert f(4096, 4096, 4096, 4096, 4096, 14, 3, 64, 2048, None) == bad   # GQA
+    assert f(4096, 4096, 4096, 4096, 4096, 14, 2, 64, 0, None) == bad      # capacity
+    assert f(4096, 4100, 4096, 4096, 4096, 14, 2, 64, 2048, None) == bad   # cache aligned
+    assert f(4096, 4096, 4096, None, 4096, 14, 2, 64, 2048, None) == bad
+    assert f(4096, 4096, 4096, 4096, None, 14, 2, 64, 2048, None) == bad
+
+
 def test_bf16_decode_ops_reject_bad_arguments(hip):
     """The BF16 siblings of the fused decode operators: K limits half the
     W8A16 ones (8 BF16 weights per 16-byte chunk), no scales needed; checked

@@ -592,6 +592,62 @@ def test_attention_decode_halves_matches_oracle(dec, orc, dev, heads, kvh):
         assert np.all(np.abs(got - exp) <= tol), (position, float(np.max(np.abs(got - exp) / tol)))
 
 
+@pytest.mark.parametrize("heads,kvh,hd,max_seq", [(14, 2, 64, 2048), (4, 1, 128, 1024),
+                                                (8, 8, 64, 512), (16, 2, 128, 2048)])
+def test_attention_decode_spans_matches_oracle(dec, orc, dev, heads, kvh, hd, max_seq):
+    """infer_hip_attention_decode_spans_bf16 (the split form on a rotated q and
+    a cache holding the token): each span's record against the oracle's
+    attention (cpu_ops.cpp:58-91 restated), merged on the host in float64;
+    rows past p hold NaN and must not matter, spans past the context leave
+    their records untouched.  Then the records through
+    infer_hip_attention_merge_o_proj against the oracle's output through
+    the o-projection (BF16 attention, FP32 GEMV, one rounding with the
+    residual), within the GEMV's bar."""
+    import torch
+    span = dec.attention_decode_span(max_seq, hd)
+    splits = dec.attention_decode_splits(max_seq, hd)
+    rng = rc.philox(1600 + heads + hd + max_seq)
+    q = rc.bf16_normal(rng, (heads * hd,), 0.5)
+    kcache = rc.bf16_normal(rng, (kvh, max_seq, hd))
+    vcache = rc.bf16_normal(rng, (kvh, max_seq, hd))
+    n = 96
+    w = rc.bf16_normal(rng, (n, heads * hd), 0.05)
+    x0 = rc.bf16_normal(rng, (n,))
+    for position in (0, 1, span - 1, span, 2 * span + 5, max_seq - 1, max_seq + 100):
+        p = min(position, max_seq - 1)
+        kc, vc = kcache.copy(), vcache.copy()
+        kc[:, p + 1:] = 0x7FC0
+        vc[:, p + 1:] = 0x7FC0
+        exp = np.asarray(orc.attention_decode(rc.bf16_values(q), rc.bf16_values(kcache),
+                                              rc.bf16_values(vcache), heads, kvh, hd, p + 1,
+                                              max_seq), dtype=np.float64)
+        rec = torch.full((heads, splits, hd + 2), float("nan"), dtype=torch.float32, device=dev)
+        dpos = torch.tensor([position], dtype=torch.int32, device=dev)
+        dec.attention_decode_spans_bf16(to_dev(q, dev), to_dev(kc, dev), to_dev(vc, dev), dpos,
+                                        rec, heads, kvh, hd, max_seq)
+        r = rec.cpu().numpy().astype(np.float64)
+        used = p // span + 1
+        assert np.all(np.isfinite(r[:, :used])), position
+        assert np.all(np.isnan(r[:, used:])), f"position {position}: a span past p written"
+        m = r[:, :used, hd]
+        big = m.max(axis=1, keepdims=True)
+        e = np.exp(m - big)
+        got = ((r[:, :used, :hd] * e[:, :, None]).sum(axis=1) /
+               (r[:, :used, hd + 1] * e).sum(axis=1)[:, None]).reshape(-1)
+        tol = 2.0 ** -12 * np.abs(exp) + 1e-5 * np.max(np.abs(exp))  # FP32 softmax / sums
+        assert np.all(np.abs(got - exp) <= tol), (position, float(np.max(np.abs(got - exp) / tol)))
+        # the records through the exported merge + o-projection + residual
+        if heads * hd <= 4096 and heads <= 32:
+            x = to_dev(x0, dev)
+            dec.attention_merge_o_proj(rec, dpos, heads, hd, span, splits, max_seq, to_dev(w, dev),
+                                       None, x, n)
+            a = rc.bf16_values(rc.bf16_words(exp.astype(np.float32))).astype(np.float64)
+            ref = rc.bf16_values(w).astype(np.float64) @ a + rc.bf16_values(x0)
+            got_x = rc.bf16_values(words(x)).astype(np.float64)
+            bound = np.maximum(1e-2 * np.abs(ref), 2e-2 * np.sqrt(np.mean(ref ** 2)))
+            assert np.all(np.abs(got_x - ref) <= bound), (position, float(np.max(np.abs(got_x - ref))))
+
+
 @pytest.mark.parametrize("heads,n", [(14, 896), (2, 130), (64, 65)])
 def test_attention_halves_o_proj_bit_exact(dec, dev, heads, n):
     """Merge weights exactly 1 (m = 0; l = 1 in the first half, 0 in the
