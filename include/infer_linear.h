@@ -132,10 +132,12 @@ int infer_hip_gemm_w8a16(const int8_t* weight, const uint16_t* scales,
  * workgroup tile of the MFMA kernel named by the caller: tile in
  * [0, infer_hip_gemm_tile_count()) (0 = 128x128, 1 = 128x64, 2 = 64x128,
  * 3 = 64x64, 4 = 32x128, 5 = 256x128 with 8 waves, rows x columns of Y),
- * or -1 for the automatic
- * choice the plain entry points make.  For tuning sweeps and for tests
- * that cover every tile.  Shapes outside the MFMA path (tokens == 1,
- * in_features % 64 != 0, unaligned weight or input) ignore tile. */
+ * or -1 for the automatic choice the plain entry points make (which for a
+ * few tokens — 2 to 32, more for narrow or int8 shapes — is the skinny
+ * kernel: 32 weight rows per workgroup streamed once, no tile).  For
+ * tuning sweeps and for tests that cover every tile.  Shapes outside the
+ * MFMA path (tokens == 1, in_features % 64 != 0, unaligned weight or input)
+ * ignore tile. */
 int infer_hip_gemm_tile_count(void);
 int infer_hip_gemm_w8a16_tile(const int8_t* weight, const uint16_t* scales,
                               int group_size, const uint16_t* bias,
@@ -153,8 +155,10 @@ int infer_hip_gemm_bf16_tile(const uint16_t* weight, const uint16_t* bias,
  * workspace, as Qwen2Model holds its LM-head scratch (qwen2.cpp:191-199).
  * The same computation as infer_hip_gemm_w8a16 / infer_hip_gemm_bf16; a
  * GEMM whose lone launch would leave CUs idle on a long K (down_proj,
- * K = 4864, at tokens <= 512) is split over K in up to 4 parts whose FP32
- * partial tiles go to the workspace and are summed in part order.
+ * K = 4864, at tokens <= 512) is split over K in parts whose FP32 partial
+ * tiles go to the workspace and are summed in part order (up to 4 parts of
+ * 64 x 64 tiles; with few tokens, where the call runs the skinny kernel,
+ * parts of at most 16 groups of 64 per 32-row block and 32-token tile).
  *
  * infer_hip_gemm_workspace_bytes: bytes that cover every token count from 2
  * to max_tokens for this [out_features, in_features] weight on the current
