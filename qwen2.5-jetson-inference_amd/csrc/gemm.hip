@@ -1376,8 +1376,12 @@ void launch_skinny_kw(const SkinnyArgs& a, int blocks, int kw, hipStream_t strea
                          stream, a);
       break;
     default:
-      // (a pair holds twice the registers: at most 4 waves, 256 each)
-      if constexpr (!PAIR) {
+      // (a pair holds twice the registers: at most 4 waves, 256 each;
+      // layout_skinny never asks a pair for more)
+      if constexpr (PAIR) {
+        hipLaunchKernelGGL((gemm_skinny_kernel<W8, PAIR, 4>), dim3(blocks), dim3(4 * kWave), 0,
+                           stream, a);
+      } else {
         hipLaunchKernelGGL((gemm_skinny_kernel<W8, PAIR, 8>), dim3(blocks), dim3(8 * kWave), 0,
                            stream, a);
       }
