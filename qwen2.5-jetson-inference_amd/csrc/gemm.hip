@@ -1078,35 +1078,36 @@ void launch_config(int config, const GemmArgs& a, hipStream_t stream) {
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // ------------------------------------------------------------------------
-// Skinny GEMM: Y[m, n] for m <= 32 tokens, the weights streamed once.
+// Skinny GEMM: Y[m, n] for a few tokens (up to kSkinnyMaxTokens), the
+// weights streamed once per 32 tokens.
 //
 // With a few tokens a GEMM is bound by reading its weights (15.4 MB of int8
 // per Qwen2.5-0.5B layer), not by MFMA: staging 64 x 64 tiles through LDS
 // leaves a few dozen workgroups walking 14 dependent stages each.  Here a
 // workgroup owns 32 weight rows of one Linear (the MFMA's 32 columns) and
-// all the tokens (its 32 rows); its KW waves split K, each loading its
-// groups' weight and activation chunks straight into registers (all of a
-// round's loads in flight at once, no LDS, no barrier), then the waves'
-// accumulators are summed in LDS in wave order.
+// one tile of 32 tokens (its 32 rows); its KW waves split K, each issuing
+// all the weight and activation loads of a round of up to four 64-column
+// groups at once, and the waves' accumulators are summed in LDS in wave
+// order.  The loads are coalesced (a group's 64-column rows across
+// consecutive lanes) and each wave permutes them into MFMA fragments
+// through its own slice of LDS, which needs no workgroup barrier.
 //
 // Lane (r, h) feeds MFMA k-step ks of group g with chunk 4 h + ks of the
 // group (K 64 g + 32 h + 8 ks .. + 7), for the A fragment of token r and
 // the B fragment of weight row n0 + r: the fragments the 64 x 64 tile
 // kernel reads from LDS, so a group's MFMA partial is the same, and its
-// W8A16 scale (row n0 + r, group g) is one value per lane.  The loads
-// themselves are coalesced (whole 64-column rows of a group across
-// consecutive lanes) and the fragments are read back from the wave's own
-// slice of LDS.  Accumulator
-// element e is token 8 (e / 4) + 4 h + e % 4 of row n0 + r.  Buffer loads
-// whose offset is past the operand (tokens >= m, rows >= n) read zeros.
+// W8A16 scale (row n0 + r, group g) is one value per lane.  Accumulator
+// element e is token m0 + 8 (e / 4) + 4 h + e % 4 of row n0 + r.  Buffer
+// loads whose offset is past the operand (tokens >= m, rows >= n) read
+// zeros.
 //
 // PAIR: the workgroup computes gate (w, s, bias) and up (w2, s2, bias2)
 // rows n0 .. n0 + 31 and writes bf16(silu(bf16(gate)) * bf16(up)).
-// A GEMM split over K (d.parts > 1) runs `parts` workgroups per row block;
-// their wave 0s hand off through d.partial as the 64 x 64 tiles' split-K
-// does (device-coherent stores, an agent-scope arrival count, the last one
-// summing the parts in index order and resetting the count), with no
-// workgroup barrier: only wave 0 takes part.
+// A GEMM split over K (d.parts > 1) runs `parts` workgroups per row block
+// and token tile; their wave 0s hand off through d.partial as the 64 x 64
+// tiles' split-K does (device-coherent stores, an agent-scope arrival
+// count, the last one summing the parts in index order and resetting the
+// count), with no workgroup barrier: only wave 0 takes part.
 template <bool W8, bool PAIR, int KW>
 __global__ __launch_bounds__(kWave * KW) void gemm_skinny_kernel(SkinnyArgs a) {
   constexpr int kRound = 4;  // groups per wave per round of loads
