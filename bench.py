@@ -667,6 +667,59 @@ def torch_sum_read(dev) -> dict:
             "GBs": round((1 << 30) / (ms * 1e-3) / 1e9, 1)}
 
 
+def calibration_detail(dev) -> dict:
+    """The floors the rooflines and the decode-step analysis are read against,
+    measured with libinfer_calib.so (csrc/calibration.hip), every kernel
+    replayed in a HIP graph:
+    - hbm_read: a read-only 16-byte streaming kernel over 370,108,416 B (one
+      decode token's Linear weights), 5 per graph, on 512 and on 65536
+      workgroups (the two ends of a sweep over 512-65536, where both read
+      fastest; 2048-4096 read ~15 % slower): the HBM read rate of a kernel
+      that does nothing but read, the best of the two;
+    - launch_floor: an empty kernel of 608 workgroups (the gate|up launch's
+      grid), 48 per graph: the fixed cost of one launch in a replay;
+    - cold_read_gate_up: 48 reads of distinct 8,716,288-byte buffers (a
+      layer's int8 gate and up weights; 418 MB together, more than the
+      256 MB last-level cache) on the same 608-workgroup grid: the launch
+      floor plus the weight stream of the decode step's gate|up launch,
+      without its scales, activations or arithmetic."""
+    import torch
+    import calibration_hip as cal
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = {}
+
+    def per_launch_us(fn, count, replays=10):
+        fn(0)  # eager once
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(count):
+                fn(i)
+        t, _ = time_steps(lambda ev: graph.replay(), replays, 3)
+        del graph
+        return t / (replays * count) * 1e3
+
+    nbytes = 370108416
+    buf = torch.ones(nbytes // 4, dtype=torch.int32, device=dev)
+    grids = {}
+    for blocks in (512, 65536):
+        us = per_launch_us(lambda i: cal.stream_read(buf, sink, blocks), 5)
+        grids[str(blocks)] = {"us": round(us, 2), "GBs": round(nbytes / (us * 1e-6) / 1e9, 1)}
+    out["hbm_read"] = {"bytes": nbytes, "by_grid": grids,
+                       "GBs": max(g["GBs"] for g in grids.values())}
+    del buf
+    out["launch_floor"] = {"blocks": 608,
+                           "us_per_launch": round(per_launch_us(lambda i: cal.empty(608), 48), 2)}
+    per = 8716288
+    bufs = torch.ones((48, per // 4), dtype=torch.int32, device=dev)
+    us = per_launch_us(lambda i: cal.stream_read(bufs[i], sink, 608), 48)
+    out["cold_read_gate_up"] = {"bytes": per, "blocks": 608, "us_per_launch": round(us, 2)}
+    del bufs
+    if int(sink.item()) != 0:
+        raise RuntimeError("calibration read wrote its sink")
+    return out
+
+
 def e2e_main(args, dev):
     import numpy as np
     import torch
@@ -773,7 +826,8 @@ def e2e_main(args, dev):
             progress("detail sweeps")
             detail = {"e2e": e2e_detail(workdirs, cfg), "linear_calls": linear_calls_detail(dev),
                       "torch_mm_bf16": torch_mm_detail(dev),
-                      "lm_head": lm_head_detail(dev, hip), "torch_sum_read": torch_sum_read(dev)}
+                      "lm_head": lm_head_detail(dev, hip), "torch_sum_read": torch_sum_read(dev),
+                      "calibration": calibration_detail(dev)}
     finally:
         for wd in workdirs.values():
             shutil.rmtree(wd, ignore_errors=True)

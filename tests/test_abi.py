@@ -407,3 +407,23 @@ def test_gate_up_silu_rejects_bad_arguments(hip):
             fn(**kw)
         assert err.value.status == hip.INVALID_ARGUMENT, kw
         assert text in str(err.value), (kw, str(err.value))
+
+
+def test_calibration_library_exports_its_symbols():
+    """libinfer_calib.so, bench.py's measurement aids (a streaming read and an
+    empty kernel): built by build() and exporting both entry points, whose
+    argument checks run on the host before any launch."""
+    import ctypes
+    import calibration_hip as cal
+    lib = cal.load()
+    for name in cal.EXPORTED_SYMBOLS:
+        assert hasattr(lib, name), name
+    # rejected before launching: null, misaligned or ragged reads, bad grids
+    assert lib.infer_calib_stream_read(None, 16, ctypes.c_void_p(16), 1, None) == 1
+    assert lib.infer_calib_stream_read(ctypes.c_void_p(32), 16, None, 1, None) == 1
+    assert lib.infer_calib_stream_read(ctypes.c_void_p(36), 16, ctypes.c_void_p(16), 1, None) == 1
+    assert lib.infer_calib_stream_read(ctypes.c_void_p(32), 24, ctypes.c_void_p(16), 1, None) == 1
+    assert lib.infer_calib_stream_read(ctypes.c_void_p(32), 16, ctypes.c_void_p(16), 0, None) == 1
+    assert lib.infer_calib_empty(0, None) == 1
+    assert lib.infer_calib_empty(65537, None) == 1
+
