@@ -237,6 +237,12 @@ __global__ __launch_bounds__(kBlock) void norm_gemv_kernel(NormGemvArgs a) {
   const NormGemvDesc d = pick_desc(a, blockIdx.x);
   const int lane = threadIdx.x & (kWave - 1);
   const int row0 = ((blockIdx.x - d.block_begin) * kWaves + threadIdx.x / kWave) * R;
+  // x and the RMSNorm weight first: loads return in the order they were
+  // issued, so the normalization then runs while the weights stream in
+  // (measured: gate|up 4.95 -> 4.53 us per launch)
+  uint4 xr[SLABS][C / 8], nr[SLABS][C / 8];
+  load_vec_raw<C, SLABS>(a.x, a.k, lane, xr);
+  load_vec_raw<C, SLABS>(a.norm_w, a.k, lane, nr);
   typename F::template Row<SLABS> w1[R], w2[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -248,9 +254,6 @@ __global__ __launch_bounds__(kBlock) void norm_gemv_kernel(NormGemvArgs a) {
   // absent bias reads y instead and is discarded.
   const int brow = min(row0 + min(lane, R - 1), d.n - 1);
   const uint16_t bias_raw = gload((d.bias && !PAIR ? d.bias : d.y) + brow);
-  uint4 xr[SLABS][C / 8], nr[SLABS][C / 8];
-  load_vec_raw<C, SLABS>(a.x, a.k, lane, xr);
-  load_vec_raw<C, SLABS>(a.norm_w, a.k, lane, nr);
   __builtin_amdgcn_sched_barrier(0);  // every load is in flight
   float xn[SLABS][C];
   wave_rms_norm<SLABS, C>(xr, nr, a.k, a.eps, lane, xn);
@@ -315,15 +318,17 @@ __global__ __launch_bounds__(kBlock) void norm_qkv_rope_kernel(QkvRopeArgs a) {
   const int r0 = region == 2 ? 2 * t : head * a.head_dim + i;
   const int r1 = region == 2 ? 2 * t + 1 : r0 + half;
   const int pos = min(*a.pos, a.max_seq - 1);
+  // x and the RMSNorm weight first, so the normalization runs while the
+  // weights stream in (loads return in issue order)
+  uint4 xr[SLABS][C / 8], nr[SLABS][C / 8];
+  load_vec_raw<C, SLABS>(a.x, a.k, lane, xr);
+  load_vec_raw<C, SLABS>(a.norm_w, a.k, lane, nr);
   typename F::template Row<SLABS> w0, w1;
   F::template load<SLABS>(w, sc, r0, n, a.k, lane, w0);
   F::template load<SLABS>(w, sc, r1, n, a.k, lane, w1);
   // the biases of r0 and r1 (an absent bias reads weight bytes instead, discarded)
   const uint16_t* bsrc = bias ? bias : static_cast<const uint16_t*>(w);
   const uint16_t bias_raw0 = gload(bsrc + r0), bias_raw1 = gload(bsrc + r1);
-  uint4 xr[SLABS][C / 8], nr[SLABS][C / 8];
-  load_vec_raw<C, SLABS>(a.x, a.k, lane, xr);
-  load_vec_raw<C, SLABS>(a.norm_w, a.k, lane, nr);
   const float2 cs = a.rope_row[i];
   __builtin_amdgcn_sched_barrier(0);  // every load is in flight
   float xn[SLABS][C];
@@ -360,13 +365,15 @@ __global__ __launch_bounds__(kBlock) void gemv_rows_kernel(GemvRowsArgs a) {
   constexpr int C = F::C;
   const int lane = threadIdx.x & (kWave - 1);
   const int row = blockIdx.x * kWaves + threadIdx.x / kWave;
+  // x first, so its conversion runs while the weights stream in (loads
+  // return in issue order)
+  uint4 xr[SLABS][C / 8];
+  load_vec_raw<C, SLABS>(a.x, a.k, lane, xr);
   typename F::template Row<SLABS> wr;
   F::template load<SLABS>(a.w, a.s, row, a.n, a.k, lane, wr);
   // the bias (the residual, which this lane alone overwrites at the end)
   // with the other loads; an absent bias reads y instead and is discarded
   const uint16_t bias_raw = gload((a.bias ? a.bias : a.y) + min(row, a.n - 1));
-  uint4 xr[SLABS][C / 8];
-  load_vec_raw<C, SLABS>(a.x, a.k, lane, xr);
   __builtin_amdgcn_sched_barrier(0);  // every load is in flight
   const int chunks = a.k >> (C == 16 ? 4 : 3);
   float xv[SLABS][C];
@@ -396,9 +403,6 @@ __global__ __launch_bounds__(kBlock) void attn_o_halves_kernel(AttnOHalvesArgs a
   constexpr uint32_t kPerHead = 64 / C;  // chunks per head
   const int lane = threadIdx.x & (kWave - 1);
   const int row = blockIdx.x * kWaves + threadIdx.x / kWave;
-  typename F::template Row<SLABS> wr;
-  F::template load<SLABS>(a.w, a.s, row, a.n, a.k, lane, wr);
-  const uint16_t res_raw = gload(a.x + min(row, a.n - 1));
   const int chunks = a.k >> (C == 16 ? 4 : 3);
   const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float*>(a.partial), 0, a.heads * 2 * kAttnHalfRecord * 4, 0x00020000);
@@ -418,6 +422,11 @@ __global__ __launch_bounds__(kBlock) void attn_o_halves_kernel(AttnOHalvesArgs a
     ml0[s] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(pr, b0 + 64u * 4u, 0, 0));
     ml1[s] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(pr, b1 + 64u * 4u, 0, 0));
   }
+  // the weights after the records: loads return in issue order, so the
+  // halves' merge runs while the weights stream in
+  typename F::template Row<SLABS> wr;
+  F::template load<SLABS>(a.w, a.s, row, a.n, a.k, lane, wr);
+  const uint16_t res_raw = gload(a.x + min(row, a.n - 1));
   const int pos = min(*a.pos, a.max_seq - 1);
   __builtin_amdgcn_sched_barrier(0);  // every load is in flight
   const bool two = pos >= kAttnHalfSpan;
