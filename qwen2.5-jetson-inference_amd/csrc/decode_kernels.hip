@@ -523,8 +523,9 @@ __global__ __launch_bounds__(kBlock) void lm_head_decode_kernel(LmHeadDecodeArgs
       }
     }
   };
-  load_task(row0, w);
   {
+    // x and the RMSNorm weight before the first task's rows: loads return
+    // in issue order, so the normalization runs while the rows stream in
     uint4 xr[SLABS][1], nr[SLABS][1], raw[SLABS];
     load_vec8_raw<SLABS>(a.x, a.k, lane, raw);
 #pragma unroll
@@ -532,6 +533,7 @@ __global__ __launch_bounds__(kBlock) void lm_head_decode_kernel(LmHeadDecodeArgs
     load_vec8_raw<SLABS>(a.norm_w, a.k, lane, raw);
 #pragma unroll
     for (int s = 0; s < SLABS; ++s) nr[s][0] = raw[s];
+    load_task(row0, w);
     __builtin_amdgcn_sched_barrier(0);  // every load is in flight
     wave_rms_norm<SLABS, 8>(xr, nr, a.k, a.eps, lane, xn);
   }
