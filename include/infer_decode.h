@@ -136,6 +136,8 @@ int infer_hip_rms_norm_gate_up_silu_bf16(const uint16_t* input, const uint16_t* 
  * rounded to BF16; q_out <- rotated q ([num_heads][head_dim]); row p =
  * min(*position, max_sequence_length - 1) of key_cache / value_cache
  * ([num_kv_heads][max_sequence_length][head_dim] BF16) <- rotated k, v.
+ * A negative *position stores nothing in the caches (q_out is still
+ * written), as the attention kernels treat it as an empty context.
  * q, k and v weights are [heads x head_dim, in_features] int8 with BF16
  * scales; biases may be NULL.  in_features <= 4096, head_dim even.  One
  * launch. */

@@ -1,6 +1,6 @@
 """ctypes bindings of libinfer_calib.so, the measurement aids bench.py uses
-next to the Linear library: a read-only streaming kernel and an empty kernel
-(csrc/calibration.hip).  Not part of the Linear ABI.  There is no fallback:
+next to the Linear library: a read-only streaming kernel, an empty kernel and
+the compute-unit probes (csrc/calibration.hip).  Not part of the Linear ABI.  There is no fallback:
 if the library is missing, load() raises."""
 from __future__ import annotations
 
@@ -9,7 +9,7 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libinfer_calib.so")
-EXPORTED_SYMBOLS = ("infer_calib_stream_read", "infer_calib_empty")
+EXPORTED_SYMBOLS = ("infer_calib_stream_read", "infer_calib_empty", "infer_calib_cu_probe")
 _lib = None
 
 
@@ -24,6 +24,10 @@ def load():
         lib.infer_calib_stream_read.restype = ctypes.c_int
         lib.infer_calib_empty.argtypes = [ctypes.c_int, ctypes.c_void_p]
         lib.infer_calib_empty.restype = ctypes.c_int
+        lib.infer_calib_cu_probe.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                             ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                             ctypes.c_void_p, ctypes.c_void_p]
+        lib.infer_calib_cu_probe.restype = ctypes.c_int
         _lib = lib
     return _lib
 
@@ -52,3 +56,36 @@ def empty(blocks: int, stream=None) -> None:
     rc = load().infer_calib_empty(blocks, _stream(stream))
     if rc != 0:
         raise ValueError(f"infer_calib_empty: status {rc}")
+
+
+# Compute-unit probe kinds (csrc/calibration.hip) and, per wave and loop
+# iteration, the LDS bytes they move and the MFMAs and FMAs they issue.
+CU_PROBES = {
+    "lds_read": (0, 8192, 0, 0),
+    "lds_write": (1, 8192, 0, 0),
+    "mfma": (2, 0, 16, 0),
+    "mfma_fold": (3, 0, 16, 64),
+    "mfma_beside_lds_read": (4, 8192, 8, 0),
+    "mfma_fold_4_partials": (5, 0, 16, 64),
+    "mfma_fold_interleaved": (6, 0, 16, 64),
+    "fill_direct_to_lds": (7, 8192, 0, 0),
+    "fill_through_registers": (8, 8192, 0, 0),
+    "lds_write_b64": (9, 4096, 0, 0),
+}
+
+
+def cu_probe(name: str, blocks: int, threads: int, iters: int, cycles, sink, src=None,
+             stream=None) -> None:
+    """Runs probe `name` on `blocks` workgroups of `threads`; `cycles` is an
+    int64 device tensor of 2 * blocks entries that receives each block's
+    shader-clock and 100 MHz-clock deltas; the fill probes read `src`, a
+    device tensor of at least 1 MiB."""
+    if cycles.numel() < 2 * blocks or cycles.element_size() != 8 or sink.numel() < 1:
+        raise ValueError("cu_probe: cycles needs 2 * blocks int64 entries and a sink")
+    if src is not None and src.numel() * src.element_size() < (1 << 20):
+        raise ValueError("cu_probe: src must hold at least 1 MiB")
+    rc = load().infer_calib_cu_probe(CU_PROBES[name][0], blocks, threads, iters,
+                                     src.data_ptr() if src is not None else None,
+                                     cycles.data_ptr(), sink.data_ptr(), _stream(stream))
+    if rc != 0:
+        raise ValueError(f"infer_calib_cu_probe: status {rc}")

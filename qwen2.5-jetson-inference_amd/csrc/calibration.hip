@@ -38,6 +38,264 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restric
 
 __global__ __launch_bounds__(256) void empty_kernel() {}
 
+// ---------------------------------------------------------------------------
+// Compute-unit probes: the rates a GEMM stage is built from, one workgroup
+// per CU, each timing its own loop with the shader clock (s_memtime) and the
+// 100 MHz constant clock (s_memrealtime).  cycles[2 b] and cycles[2 b + 1]
+// receive block b's two deltas.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+enum CuProbe {
+  kProbeLdsRead = 0,   // ds_read_b128, 8 in flight per wave, then a wait
+  kProbeLdsWrite = 1,  // ds_write_b128, 8 in flight per wave, then a wait
+  kProbeMfma = 2,      // v_mfma_f32_32x32x16_bf16, 4 independent chains per wave
+  kProbeMfmaFold = 3,  // the W8A16 stage pattern: 4-MFMA chains from zero, each
+                       // folded into an FP32 total with 16 FMAs
+  kProbeMfmaLds = 4,   // 8 MFMAs with 8 ds_read_b128 in flight beside them
+  kProbeMfmaFold4 = 5, // as kProbeMfmaFold with four partials in rotation, so
+                       // no chain waits on the fold of the one before
+  kProbeFoldInterleaved = 6,  // as kProbeMfmaFold4, the schedule pinned to
+                              // one MFMA then four fold FMAs, two chains
+                              // alternating
+  kProbeFillDirect = 7,   // global_load_lds_dwordx4 of L2-resident data into
+                          // LDS, 8 KiB per wave in flight
+  kProbeFillStaged = 8,   // the same bytes through registers: global_load_dwordx4
+                          // then ds_write_b128
+  kProbeLdsWrite64 = 9,   // ds_write_b64, 8 in flight per wave, then a wait
+  kProbeCount = 10
+};
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  // The low 32 bits of a flat address in the LDS aperture are the LDS offset.
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
+}
+
+#define QCAL_READ8(base)                                                                     \
+  asm volatile(                                                                              \
+      "ds_read_b128 %0, %8\n\tds_read_b128 %1, %8 offset:1024\n\t"                           \
+      "ds_read_b128 %2, %8 offset:2048\n\tds_read_b128 %3, %8 offset:3072\n\t"               \
+      "ds_read_b128 %4, %8 offset:4096\n\tds_read_b128 %5, %8 offset:5120\n\t"               \
+      "ds_read_b128 %6, %8 offset:6144\n\tds_read_b128 %7, %8 offset:7168"                   \
+      : "=v"(r0), "=v"(r1), "=v"(r2), "=v"(r3), "=v"(r4), "=v"(r5), "=v"(r6), "=v"(r7)       \
+      : "v"(base))
+#define QCAL_WAIT_READS()                                                                     \
+  asm volatile("s_waitcnt lgkmcnt(0)"                                                        \
+               : "+v"(r0), "+v"(r1), "+v"(r2), "+v"(r3), "+v"(r4), "+v"(r5), "+v"(r6), "+v"(r7))
+
+// MAX_THREADS bounds the registers a wave may hold (1024: 128, 512: 256).
+template <int MAX_THREADS>
+__global__ __launch_bounds__(MAX_THREADS) void cu_probe_kernel(int kind, int iters,
+                                                               const u32x4* __restrict__ src,
+                                                               unsigned long long* cycles,
+                                                               unsigned* sink) {
+  __shared__ u32x4 lds[4096];  // 64 KiB
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int i = tid; i < 4096; i += blockDim.x) lds[i] = u32x4{unsigned(i), 1u, 2u, 3u};
+  __syncthreads();
+  // Each wave reads or writes its own 8 KiB (waves 8 apart share one), lane
+  // l at byte 16 l of each 1 KiB row: conflict-free 16-byte accesses.
+  const uint32_t base = lds_addr(lds) + ((wave & 7) * 8192u) + lane * 16u;
+  unsigned acc_u = 0;
+  float acc_f = 0.0f;
+  // The whole workgroup is timed (a barrier on either side): waves of one
+  // SIMD do not progress evenly, the oldest is issued first.
+  __syncthreads();
+  const unsigned long long t0 = __builtin_amdgcn_s_memtime();
+  const unsigned long long r0t = __builtin_amdgcn_s_memrealtime();
+  if (kind == kProbeLdsRead) {
+    u32x4 r0, r1, r2, r3, r4, r5, r6, r7;
+    for (int it = 0; it < iters; ++it) {
+      QCAL_READ8(base);
+      QCAL_WAIT_READS();
+      acc_u ^= r0.x ^ r7.w;
+    }
+  } else if (kind == kProbeFillDirect || kind == kProbeFillStaged) {
+    // wave w of block b reads 8 KiB at ((b * 16 + w) mod 128) * 8 KiB of a
+    // 1 MiB source (L2-resident after the first pass) into its LDS slice
+    const u32x4* g = src + (((blockIdx.x * 16u + wave) & 127u) * 512u) + lane;
+    u32x4* dst = lds + (wave & 7) * 512;
+    for (int it = 0; it < iters; ++it) {
+      if (kind == kProbeFillDirect) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          __builtin_amdgcn_global_load_lds(
+              (const void __attribute__((address_space(1)))*)(g + 64 * j),
+              (void __attribute__((address_space(3)))*)(dst + 64 * j), 16, 0, 0);
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      } else {
+        u32x4 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = __builtin_nontemporal_load(g + 64 * j);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dst[64 * j + lane] = v[j];
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      }
+    }
+    acc_u = lds[tid & 4095].x;
+  } else if (kind == kProbeLdsWrite64) {
+    const unsigned long long v = tid;
+    const uint32_t base64 = lds_addr(lds) + ((wave & 7) * 8192u) + lane * 8u;
+    for (int it = 0; it < iters; ++it) {
+      asm volatile(
+          "ds_write_b64 %0, %1\n\tds_write_b64 %0, %1 offset:512\n\t"
+          "ds_write_b64 %0, %1 offset:1024\n\tds_write_b64 %0, %1 offset:1536\n\t"
+          "ds_write_b64 %0, %1 offset:2048\n\tds_write_b64 %0, %1 offset:2560\n\t"
+          "ds_write_b64 %0, %1 offset:3072\n\tds_write_b64 %0, %1 offset:3584\n\t"
+          "s_waitcnt lgkmcnt(0)" ::"v"(base64), "v"(v) : "memory");
+    }
+  } else if (kind == kProbeLdsWrite) {
+    const u32x4 v = {unsigned(tid), 1u, 2u, 3u};
+    for (int it = 0; it < iters; ++it) {
+      asm volatile(
+          "ds_write_b128 %0, %1\n\tds_write_b128 %0, %1 offset:1024\n\t"
+          "ds_write_b128 %0, %1 offset:2048\n\tds_write_b128 %0, %1 offset:3072\n\t"
+          "ds_write_b128 %0, %1 offset:4096\n\tds_write_b128 %0, %1 offset:5120\n\t"
+          "ds_write_b128 %0, %1 offset:6144\n\tds_write_b128 %0, %1 offset:7168\n\t"
+          "s_waitcnt lgkmcnt(0)" ::"v"(base), "v"(v) : "memory");
+    }
+  } else {
+    // distinct operands per chain, so no two chains compute the same values
+    bf16x8_t a, b[4];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      a[e] = static_cast<__bf16>(static_cast<float>((lane + e) & 7) * 0.125f);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        b[j][e] = static_cast<__bf16>(static_cast<float>((lane * 3 + e + j) & 7) * 0.0625f);
+    }
+    f32x16_t c[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) c[j][e] = static_cast<float>(j);
+    if (kind == kProbeMfma) {
+      for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) c[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b[j], c[j], 0, 0, 0);
+      }
+    } else if (kind == kProbeMfmaFold) {
+      const float s = 1.0f + 1.0f / 1024.0f;
+      auto chain = [&](int j, f32x16_t& p) {
+        const f32x16_t zero = {};
+        p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b[j], zero, 0, 0, 0);
+#pragma unroll
+        for (int k = 1; k < 4; ++k) p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b[j], p, 0, 0, 0);
+      };
+      auto fold = [&](int j, const f32x16_t& p) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) c[j][e] = fmaf(p[e], s, c[j][e]);
+      };
+      for (int it = 0; it < iters; ++it) {
+        // four tiles per iteration, as a wave's 2 x 2 block of 32 x 32 tiles
+        // per 64-column stage: 16 MFMAs and 64 fold FMAs, each fold beside
+        // the next chain
+        f32x16_t p0, p1;
+        chain(0, p0);
+        chain(1, p1);
+        fold(0, p0);
+        chain(2, p0);
+        fold(1, p1);
+        chain(3, p1);
+        fold(2, p0);
+        fold(3, p1);
+      }
+    } else if (kind == kProbeMfmaFold4) {
+      const float s = 1.0f + 1.0f / 1024.0f;
+      auto chain = [&](int j, f32x16_t& p) {
+        const f32x16_t zero = {};
+        p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b[j], zero, 0, 0, 0);
+#pragma unroll
+        for (int k = 1; k < 4; ++k) p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b[j], p, 0, 0, 0);
+      };
+      auto fold = [&](int j, const f32x16_t& p) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) c[j][e] = fmaf(p[e], s, c[j][e]);
+      };
+      f32x16_t p[4];
+      chain(0, p[0]);
+      chain(1, p[1]);
+      for (int it = 0; it < iters; ++it) {
+        // steady state: chains j + 2, j + 3 run while tiles j, j + 1 fold
+        chain(2, p[2]);
+        fold(0, p[0]);
+        chain(3, p[3]);
+        fold(1, p[1]);
+        chain(0, p[0]);
+        fold(2, p[2]);
+        chain(1, p[1]);
+        fold(3, p[3]);
+      }
+      fold(0, p[0]);
+      fold(1, p[1]);
+    } else if (kind == kProbeFoldInterleaved) {
+      const float s = 1.0f + 1.0f / 1024.0f;
+      f32x16_t p[4];
+      const f32x16_t zero = {};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) p[j] = zero;
+      for (int it = 0; it < iters; ++it) {
+        // chains 2, 3 (alternating k-steps) while tiles 0, 1 fold, then
+        // chains 0, 1 while tiles 2, 3 fold: each MFMA followed by 4 FMAs
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const int n0 = half == 0 ? 2 : 0, f0 = half == 0 ? 0 : 2;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) c[f0][e] = fmaf(p[f0][e], s, c[f0][e]);
+#pragma unroll
+          for (int e = 0; e < 16; ++e) c[f0 + 1][e] = fmaf(p[f0 + 1][e], s, c[f0 + 1][e]);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            p[n0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b[n0], k == 0 ? zero : p[n0], 0, 0, 0);
+            p[n0 + 1] =
+                __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b[n0 + 1], k == 0 ? zero : p[n0 + 1], 0, 0, 0);
+          }
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // 4 VALU
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) c[j][e] = fmaf(p[j][e], s, c[j][e]);
+    } else {  // kProbeMfmaLds
+      u32x4 r0, r1, r2, r3, r4, r5, r6, r7;
+      for (int it = 0; it < iters; ++it) {
+        QCAL_READ8(base);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) c[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b[j], c[j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        QCAL_WAIT_READS();
+        acc_u ^= r0.x ^ r7.w;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc_f += c[j][e];
+  }
+  __syncthreads();
+  const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+  const unsigned long long r1t = __builtin_amdgcn_s_memrealtime();
+  if (tid == 0) {
+    cycles[2 * blockIdx.x] = t1 - t0;
+    cycles[2 * blockIdx.x + 1] = r1t - r0t;
+  }
+  if (acc_u == 0x9e3779b9u || acc_f == 1234.5f) sink[0] = acc_u;
+}
+#undef QCAL_READ8
+#undef QCAL_WAIT_READS
+
 }  // namespace
 
 extern "C" {
@@ -60,6 +318,31 @@ int infer_calib_stream_read(const void* data, size_t bytes, unsigned* sink, int 
 int infer_calib_empty(int blocks, hipStream_t stream) {
   if (blocks < 1 || blocks > 65536) return 1;
   hipLaunchKernelGGL(empty_kernel, dim3(blocks), dim3(256), 0, stream);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+// Runs compute-unit probe `kind` (the CuProbe values above) on `blocks`
+// workgroups of `threads` (64..1024, a multiple of 64) for `iters` loop
+// iterations; cycles (2 * blocks entries) receives each block's shader-clock
+// and 100 MHz-clock deltas.  Per wave and iteration: kinds 0, 1, 7, 8 move
+// 8 KiB (7 and 8 read them from `src`, 1 MiB, 16-byte aligned), kind 9
+// writes 4 KiB; kind 2 issues 16 MFMAs, 3, 5 and 6 issue 16 MFMAs and 64
+// FMAs, 4 issues 8 MFMAs and reads 8 KiB.
+int infer_calib_cu_probe(int kind, int blocks, int threads, int iters, const void* src,
+                         unsigned long long* cycles, unsigned* sink, hipStream_t stream) {
+  if (kind < 0 || kind >= kProbeCount || blocks < 1 || blocks > 65536 || threads < 64 ||
+      threads > 1024 || threads % 64 != 0 || iters < 1 || !cycles || !sink ||
+      ((kind == kProbeFillDirect || kind == kProbeFillStaged) &&
+       (!src || (reinterpret_cast<uintptr_t>(src) & 15u) != 0))) {
+    return 1;
+  }
+  if (threads <= 512) {
+    hipLaunchKernelGGL(cu_probe_kernel<512>, dim3(blocks), dim3(threads), 0, stream, kind, iters,
+                       static_cast<const u32x4*>(src), cycles, sink);
+  } else {
+    hipLaunchKernelGGL(cu_probe_kernel<1024>, dim3(blocks), dim3(threads), 0, stream, kind, iters,
+                       static_cast<const u32x4*>(src), cycles, sink);
+  }
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 

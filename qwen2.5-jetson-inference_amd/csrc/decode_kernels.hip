@@ -317,7 +317,10 @@ __global__ __launch_bounds__(kBlock) void norm_qkv_rope_kernel(QkvRopeArgs a) {
   const int head = t / half, i = t % half;
   const int r0 = region == 2 ? 2 * t : head * a.head_dim + i;
   const int r1 = region == 2 ? 2 * t + 1 : r0 + half;
-  const int pos = min(*a.pos, a.max_seq - 1);
+  // A negative position is an empty context: k and v are not stored
+  // (the attention kernels read nothing for it either).
+  const int raw_pos = *a.pos;
+  const int pos = min(raw_pos, a.max_seq - 1);
   // x and the RMSNorm weight first, so the normalization runs while the
   // weights stream in (loads return in issue order)
   uint4 xr[SLABS][C / 8], nr[SLABS][C / 8];
@@ -346,7 +349,7 @@ __global__ __launch_bounds__(kBlock) void norm_qkv_rope_kernel(QkvRopeArgs a) {
     if (region == 0) {
       gstore(a.q_out + r0, o0);
       gstore(a.q_out + r1, o1);
-    } else {
+    } else if (raw_pos >= 0) {
       // row r of k or v is dimension r % head_dim of kv head r / head_dim
       uint16_t* cache = region == 1 ? a.key_cache : a.value_cache;
       const size_t base = (static_cast<size_t>(r0 / a.head_dim) * a.max_seq + pos) * a.head_dim;

@@ -18,10 +18,12 @@
 //     down GEMV + residual (gemv_rows);
 //   final RMSNorm + LM head + argmax + step bookkeeping (lm_head_decode).
 // Every launch is built to wait on one round of global loads: a decode
-// step is latency-bound, not bandwidth-bound.  Shapes outside the fused
-// kernels' limits (hidden > 4096 int8 or 2048 BF16 weights, head_dim other
-// than 64, max_seq over 1024) run unfused norm / GEMV / SiLU-mul launches
-// around the split attention.  The down GEMV's residual add rides on the GEMV's bias operand
+// step is latency-bound, not bandwidth-bound.  A head_dim other than 64 or
+// a max_seq over 1024 changes only the attention and the o-projection: the
+// split attention (RoPE applied inside it) and the span-merging o GEMV.  A
+// hidden size beyond the fused kernels' limits (4096 with int8 weights,
+// 2048 with BF16) runs unfused norm / GEMV / SiLU-mul launches around that
+// split attention.  The down GEMV's residual add rides on the GEMV's bias operand
 // (bias = output = the residual stream): each output element is read as
 // bias and then written by the same lane, so the aliasing is safe.  With
 // use_graph the step is captured once and replayed per token.

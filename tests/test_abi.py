@@ -410,9 +410,10 @@ def test_gate_up_silu_rejects_bad_arguments(hip):
 
 
 def test_calibration_library_exports_its_symbols():
-    """libinfer_calib.so, bench.py's measurement aids (a streaming read and an
-    empty kernel): built by build() and exporting both entry points, whose
-    argument checks run on the host before any launch."""
+    """libinfer_calib.so, bench.py's measurement aids (a streaming read, an
+    empty kernel and the compute-unit probes): built by build() and
+    exporting every entry point, whose argument checks run on the host
+    before any launch."""
     import ctypes
     import calibration_hip as cal
     lib = cal.load()
@@ -426,4 +427,15 @@ def test_calibration_library_exports_its_symbols():
     assert lib.infer_calib_stream_read(ctypes.c_void_p(32), 16, ctypes.c_void_p(16), 0, None) == 1
     assert lib.infer_calib_empty(0, None) == 1
     assert lib.infer_calib_empty(65537, None) == 1
+    # compute-unit probes: unknown kind, thread counts off the wave grid, no
+    # cycle buffer, a fill probe without (or with a misaligned) source
+    buf = ctypes.c_void_p(256)
+    assert lib.infer_calib_cu_probe(-1, 1, 256, 1, None, buf, buf, None) == 1
+    assert lib.infer_calib_cu_probe(len(cal.CU_PROBES), 1, 256, 1, None, buf, buf, None) == 1
+    assert lib.infer_calib_cu_probe(0, 1, 96, 1, None, buf, buf, None) == 1
+    assert lib.infer_calib_cu_probe(0, 1, 2048, 1, None, buf, buf, None) == 1
+    assert lib.infer_calib_cu_probe(0, 1, 256, 0, None, buf, buf, None) == 1
+    assert lib.infer_calib_cu_probe(0, 1, 256, 1, None, None, buf, None) == 1
+    assert lib.infer_calib_cu_probe(7, 1, 256, 1, None, buf, buf, None) == 1
+    assert lib.infer_calib_cu_probe(7, 1, 256, 1, ctypes.c_void_p(264), buf, buf, None) == 1
 

@@ -39,3 +39,26 @@ def test_empty_kernel_launches(dev):
     import calibration_hip as cal
     cal.empty(608)
     torch.cuda.synchronize()
+
+
+def test_cu_probes_run_and_time_their_loops(dev):
+    """Every compute-unit probe runs to completion on a few workgroups and
+    reports a positive loop time on both clocks; a longer loop takes
+    longer."""
+    import torch
+    import calibration_hip as cal
+    cycles = torch.zeros(2 * 4, dtype=torch.int64, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    src = torch.ones(1 << 18, dtype=torch.int32, device=dev)  # 1 MiB
+    for name in cal.CU_PROBES:
+        for threads in (256, 512):
+            spans = []
+            for iters in (4, 64):
+                print(f"cu_probe {name} threads={threads} iters={iters}", flush=True)
+                cycles.zero_()
+                cal.cu_probe(name, 4, threads, iters, cycles, sink, src)
+                torch.cuda.synchronize()
+                c = cycles.view(4, 2).cpu()
+                assert bool((c > 0).all()), (name, threads, iters, c)
+                spans.append(int(c[:, 0].min()))
+            assert spans[1] > spans[0], (name, threads, spans)

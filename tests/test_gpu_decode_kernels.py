@@ -517,6 +517,44 @@ def test_rms_norm_qkv_rope(dec, dev, shape):
                                              np.argwhere(~ok2)[:3])
 
 
+@pytest.mark.parametrize("weights", ["w8a16", "bf16"])
+def test_rms_norm_qkv_rope_negative_position_stores_nothing(dec, dev, weights):
+    """A negative position is an empty context: the launch writes q_out and
+    nothing in the caches.  The caches are carved out of one tensor with
+    guard rows in front of and behind them, which must stay untouched."""
+    import torch
+    k, heads, kvh, hd, max_seq = 896, 14, 2, 64, 32
+    rng = rc.philox(4242)
+    nq, nkv = heads * hd, kvh * hd
+    xw, nw, xn = norm_input(k, 3, rng)
+    cs = dec.rope_row(1e6, hd, 0)  # cos 1, sin 0: q_out is the GEMV itself
+    if weights == "w8a16":
+        w = {n: w8_rows(rng, m, k) for n, m in (("q", nq), ("k", nkv), ("v", nkv))}
+        sc = {n: pow2_scales(w[n].shape[0], k, salt=i) for i, n in enumerate("qkv")}
+        dw = {n: (to_dev(w[n], dev), to_dev(sc[n], dev), None) for n in "qkv"}
+        exp_q = bf16(exact_gemv(w["q"], sc["q"], xn, None))
+    else:
+        w = {n: bf16_rows(rng, m, k) for n, m in (("q", nq), ("k", nkv), ("v", nkv))}
+        dw = {n: (to_dev(w[n][0], dev), None) for n in "qkv"}
+        exp_q = bf16(exact_dot(w["q"][1], xn))
+    sentinel = np.uint16(0x7FC0)
+    cache_words = kvh * max_seq * hd
+    guard = 2 * hd  # guard words on either side of each cache
+    buf = torch.full((2 * (cache_words + 2 * guard),), int(sentinel.view(np.int16)),
+                     dtype=torch.int16, device=dev)
+    kc = buf[guard:guard + cache_words]
+    vc = buf[3 * guard + cache_words:3 * guard + 2 * cache_words]
+    q_out = bf16_out((nq,), dev)
+    dpos = torch.tensor([-1], dtype=torch.int32, device=dev)
+    print(f"qkv_rope negative position weights={weights}", flush=True)
+    fn = dec.rms_norm_qkv_rope_w8a16 if weights == "w8a16" else dec.rms_norm_qkv_rope_bf16
+    fn(to_dev(xw, dev), to_dev(nw, dev), EPS, k, dw["q"], dw["k"], dw["v"], q_out, kc, vc,
+       torch.from_numpy(cs.copy()).to(dev), dpos, heads, kvh, hd, max_seq)
+    torch.cuda.synchronize()
+    assert np.all(buf.cpu().numpy().view(np.uint16) == sentinel), "a cache or guard row changed"
+    np.testing.assert_array_equal(words(q_out), exp_q)
+
+
 # ------------------------------------------- whole-context decode attention --
 
 @pytest.mark.parametrize("heads,kvh", [(14, 2), (4, 4), (8, 1)])

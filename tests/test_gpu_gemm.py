@@ -232,7 +232,9 @@ def test_lone_gemm_with_workspace_splits_long_k(hip, orc, dev, w8):
             hip.gemm_bf16_ws(wd, to_dev(b, dev), to_dev(x, dev), y, m, n, k, ws)
         stats = check_close(words(y), exp, what=f"gemm ws w8={w8} M={m}")
         assert stats["bit_identical"] > 0.95, stats
-    # (at M <= 32 the call runs the skinny kernel, which needs no workspace)
+    # A workspace too small for the call is rejected.  Skinny calls of long K
+    # split over the workspace too (down_proj, K = 4864: 5 K-parts at M = 2
+    # and 32), so this rejection exercises that path as well.
     small = ws[:4]
     x = to_dev(rc.bf16_normal(rng, (128, k)), dev)
     with pytest.raises(hip.InferError) as err:
