@@ -18,12 +18,17 @@ Workloads (--workload):
       for the decode step's dominant kernel (largest time per token), timed
       launch by launch with HIP events on the model's stream at the middle
       of the decoded context; `decode_linear` is the step's Linear launches
-      combined, `linear_gemv_plan` config 1's figure (below).  cpu_baseline
-      is the CPU FP32 oracle model (a C restatement of the reference's
-      cpu_ops.cpp + qwen2.cpp CPU path) on the same dequantised weights,
-      config 0's workload (prompt 32, greedy decode), a bounded sample,
-      with the first greedy divergence from the GPU checked by the
-      near-tie rule.  --detail FILE adds the reference's sweeps
+      combined, `linear_gemv_plan` config 1's figure (below),
+      `prefill_m512` config 3's layer plan (W8A16 at M = 32/128/512, BF16 at
+      512) against the MFMA peak and `lm_head` config 2's standalone LM
+      head.  cpu_baseline is config 0: its own seed-0 model, the CPU FP32
+      oracle model (a C restatement of the reference's cpu_ops.cpp +
+      qwen2.cpp CPU path) on the same dequantised weights as the GPU's,
+      prompt 32 + 128 greedy tokens, 3 timed samples (mean/p50/p95), the
+      GPU's rate on the same workload beside it, and the first greedy
+      divergence from the GPU checked by the near-tie rule;
+      `other_configs` holds the CPU FP32 Linear path on configs 1, 2 and 3
+      with the GPU time of the same work.  --detail FILE adds the reference's sweeps
       (canonical, prefill, decode context; W8A16 and W16A16), the
       per-Linear single calls and the LM head.
 
@@ -157,10 +162,7 @@ def cpu_baseline(layers, seconds: float):
     import numpy as np
     import oracle  # test infrastructure: the CPU baseline leg only
     oracle.build()
-    threads = len(os.sched_getaffinity(0))
-    env = os.environ.get("OMP_NUM_THREADS")
-    if env and env.isdigit():
-        threads = min(threads, int(env))
+    threads = cpu_threads()
     import torch
     host = []
     for (q, s, _, _, x, y, n, k) in layers.calls:
@@ -205,9 +207,11 @@ def check_outputs(layers, cpu_outs):
     return worst
 
 
-def lm_head_detail(dev, hip):
+def lm_head_detail(dev, hip, keep_inputs: bool = False):
     """Config 2: the fused LM head over two distinct 151936 x 896 BF16
-    embedding copies (545 MB, alternated so no call is served from cache)."""
+    embedding copies (545 MB, alternated so no call is served from cache).
+    keep_inputs returns the first copy and the hidden vector as well (keys
+    "e" and "h", for the CPU baseline)."""
     import torch
     vocab, k = 151936, 896
     g = torch.Generator(device=dev)
@@ -228,8 +232,11 @@ def lm_head_detail(dev, hip):
     t, _ = time_steps(step, 100, 10)
     nbytes = 2 * vocab * k + 2 * k + 2 * vocab + 4
     us = t / 100 * 1e3
-    return {"us_per_call": round(us, 2), "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
-            "bytes": nbytes}
+    out = {"us_per_call": round(us, 2), "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
+           "bytes": nbytes}
+    if keep_inputs:
+        out["e"], out["h"] = emb[0], h
+    return out
 
 
 MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense BF16
@@ -264,6 +271,34 @@ class PrefillLayers:
             self.plans.append(hip.GemmPlan(layer))
         torch.cuda.synchronize()
         self.flops_per_layer = sum(2.0 * m * n * k for _, n, k in SHAPES)
+
+
+def prefill_roofline(dev, hip, steps: int = 100) -> tuple:
+    """Config 3 for the default bench line: one layer's 7 Linear GEMMs as
+    one grouped plan launch, 4 layers of distinct weights rotated, W8A16 at
+    M = 32, 128 and 512 and BF16 at M = 512; TFLOP/s of the layer's FLOPs
+    over the launch time, against the 2.5 PFLOP/s BF16 MFMA peak.  Also
+    returns the W8A16 layers (the CPU baseline's inputs) and plan times."""
+    out, sets = {}, {}
+    for w8, m in ((True, 512), (False, 512), (True, 128), (True, 32)):
+        pl = PrefillLayers(dev, hip, m, w8)
+        nl = len(pl.plans)
+        calls = [0]
+
+        def step(ev):
+            pl.plans[calls[0] % nl].launch()
+            calls[0] += 1
+        t, _ = time_steps(step, steps, 10)
+        us = t / steps * 1e3
+        tflops = pl.flops_per_layer / (us * 1e-6) / 1e12
+        out[f"{'w8a16' if w8 else 'bf16'}_M{m}"] = {
+            "us_per_layer_plan": round(us, 2), "TFLOPs": round(tflops, 1),
+            "frac": round(tflops / MFMA_PEAK_TFLOPS, 4)}
+        if w8:
+            sets[m] = (pl.calls[0], round(us, 2))
+        for plan in pl.plans:
+            plan.close()
+    return out, sets
 
 
 def prefill_main(args, dev, hip) -> int:
@@ -353,64 +388,201 @@ def near_tie_rule(gpu_logits, ref_logits, gpu_tok: int, ref_tok: int) -> dict:
             "bound": bound, "logits_cosine": round(cos, 6), "near_tie": margin <= bound}
 
 
-def e2e_cpu_baseline(cfg, tensors, gpu_model, seconds: float):
-    """Config 0 on the CPU: the FP32 oracle model on the dequantised weights
-    of the GPU run, prompt of 32 uniform-random tokens (seed 0), greedy
-    decode until `seconds` of decode time or 128 tokens.  Also runs the GPU
-    model on the same prompt, finds where the two greedy sequences first
-    differ and checks that step with the per-step near-tie rule (both
-    models teacher-forced to the common prefix); a difference that is not
-    a near-tie fails the bench."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import numpy as np
-    import oracle  # test infrastructure: the CPU baseline leg only
-    import synthetic as S
-    oracle.build()
+def cpu_threads() -> int:
+    """Threads for the CPU baselines: the process's affinity mask, capped by
+    OMP_NUM_THREADS when it is set."""
     threads = len(os.sched_getaffinity(0))
     env = os.environ.get("OMP_NUM_THREADS")
     if env and env.isdigit():
         threads = min(threads, int(env))
+    return threads
+
+
+def repeat_for(fn, seconds: float, min_reps: int = 3, max_reps: int = 10000):
+    """Calls fn() at least min_reps times and until `seconds` have passed;
+    returns the per-call times in seconds."""
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < min_reps or (time.perf_counter() < t_end and len(times) < max_reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return times
+
+
+def linear_cpu_baselines(layers, lm, prefill_sets, seconds: float) -> dict:
+    """The reference's CPU FP32 Linear path (cpu_ops.cpp:23-30, 108-123,
+    175-177: the oracle's C/OpenMP restatement) on the host cores, on the
+    same dequantised weights and inputs the GPU figures of this run use:
+    config 1 (the 168 GEMVs of a token), config 2 (the tied LM head + argmax,
+    qwen2.cpp:421-424) and config 3 (one layer's 7 GEMMs at M = 32/128/512).
+    Each is timed for about `seconds` (at least 3 calls): mean/p50/p95 per
+    call, beside the GPU's time for the same work."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import torch
+    import oracle  # test infrastructure: the CPU baseline leg only
+    oracle.build()
+    threads = cpu_threads()
+    out = {"cores": threads, "kind": "port",
+           "what": "FP32 C/OpenMP restatement of cpu_ops.cpp linear_fp32 / linear_fp32_batch / "
+                   "argmax on the dequantised weights"}
+
+    def host_w8(q, sc):
+        qn = q.cpu().numpy()
+        sn = sc.view(torch.int16).cpu().numpy().view(np.uint16)
+        return oracle.dequant_w8a16(qn, sn, 64, threads)
+
+    # config 1
+    ws = [(host_w8(c[0], c[1]), c[4].float().cpu().numpy()) for c in layers["calls"]]
+    wbytes = sum(w.nbytes for w, _ in ws)
+
+    def one_token():
+        for w, x in ws:
+            oracle.linear_fp32(w, None, x, threads)
+    t = repeat_for(one_token, seconds)
+    ms = stats_of([v * 1e3 for v in t])
+    out["config1_gemv_168"] = {
+        "ms_per_token": ms, "fp32_weight_bytes": int(wbytes),
+        "GBs": round(wbytes / (ms["mean"] * 1e-3) / 1e9, 1), "calls": len(t),
+        "gpu_us_same_work": layers["gpu_us"],
+        "gpu_speedup": round(ms["mean"] * 1e3 / layers["gpu_us"], 1)}
+    del ws
+    # config 2
+    e32 = lm["e"].float().cpu().numpy()
+    h32 = lm["h"].float().cpu().numpy()
+
+    def head():
+        oracle.argmax(oracle.linear_fp32(e32, None, h32, threads))
+    t = repeat_for(head, seconds)
+    ms = stats_of([v * 1e3 for v in t])
+    out["config2_lm_head"] = {
+        "ms_per_call": ms, "fp32_weight_bytes": int(e32.nbytes),
+        "GBs": round(e32.nbytes / (ms["mean"] * 1e-3) / 1e9, 1), "calls": len(t),
+        "gpu_us_same_work": lm["gpu_us"],
+        "gpu_speedup": round(ms["mean"] * 1e3 / lm["gpu_us"], 1)}
+    del e32
+    # config 3
+    c3 = {}
+    for m, (calls, gpu_us) in prefill_sets.items():
+        gw = [(host_w8(c[0], c[1]), c[4][:m].float().cpu().numpy()) for c in calls]
+        flops = sum(2.0 * m * w.shape[0] * w.shape[1] for w, _ in gw)
+
+        def layer():
+            for w, x in gw:
+                oracle.linear_fp32_batch(w, None, x, threads)
+        t = repeat_for(layer, seconds / 2)
+        ms = stats_of([v * 1e3 for v in t])
+        c3[f"M{m}"] = {"ms_per_layer": ms, "GFLOPs": round(flops / (ms["mean"] * 1e-3) / 1e9, 1),
+                       "calls": len(t), "gpu_us_same_work": gpu_us,
+                       "gpu_speedup": round(ms["mean"] * 1e3 / gpu_us, 1)}
+        del gw
+    out["config3_gemm_layer_w8a16"] = c3
+    return out
+
+
+def config0_baseline(cfg, seconds: float, samples: int = 3):
+    """Config 0: its own random-init model (seed 0, N(0, 0.02), norm weights
+    1, biases 0) exported to W8A16 and opened on the GPU, and on the CPU the
+    FP32 oracle model on the same dequantised weights (the FP32 work per
+    token of config 0's model).  Workload: prompt of 32 uniform-random
+    tokens (seed 0), 128 greedy tokens, max_seq 256.  The CPU decode is
+    sampled `samples` times after one warm-up (mean/p50/p95 over the
+    samples, per-token latency p50/p95 over all their steps); the GPU
+    decodes the same workload (one graph replay a token).  Where the two
+    greedy sequences first differ, both models are teacher-forced to the
+    common prefix and that step is checked with the per-step near-tie rule;
+    a difference that is not a near-tie fails the bench."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import shutil
+    import tempfile
+    import numpy as np
+    import archive_hip
+    import model_hip
+    import oracle  # test infrastructure: the CPU baseline leg only
+    import synthetic as S
+    oracle.build()
+    threads = cpu_threads()
+    max_seq, prompt_len, out_len = 256, 32, 128
+    workdir = tempfile.mkdtemp(prefix="qwen-config0-")
+    try:
+        checkpoint = S.random_checkpoint(cfg, seed=0, std=0.02, plain_init=True)
+        export_model_dir(cfg, checkpoint, workdir, "w8a16")
+        del checkpoint
+        gpu = model_hip.Qwen2Model.open(workdir, "w8a16", max_sequence_length=max_seq)
+        with archive_hip.ModelArchive(os.path.join(workdir, "model.w8a16.qbin")) as archive:
+            tensors = {r.name: archive.data(r.name) for r in archive.records}
+    finally:
+        shutil.rmtree(workdir, ignore_errors=True)
     fp32 = S.dequantized_fp32(tensors, cfg)
-    max_seq = 256
+    del tensors
     cpu = oracle.Model(fp32, cfg.num_layers, cfg.hidden_size, cfg.num_heads, cfg.num_kv_heads,
                        cfg.intermediate_size, cfg.vocab_size, max_seq, cfg.rms_norm_eps,
                        cfg.rope_theta, threads)
-    prompt = [int(v) for v in np.random.default_rng(0).integers(0, cfg.vocab_size, 32)]
-    t0 = time.perf_counter()
-    tok = cpu.prefill(prompt)
-    prefill_s = time.perf_counter() - t0
-    cpu_tokens = [tok]
-    t0 = time.perf_counter()
-    while len(cpu_tokens) < 128:
-        cpu_tokens.append(cpu.decode(cpu_tokens[-1], len(prompt) + len(cpu_tokens) - 1))
-        if time.perf_counter() - t0 >= seconds:
-            break
-    decode_s = time.perf_counter() - t0
+    del fp32
+    prompt = [int(v) for v in np.random.default_rng(0).integers(0, cfg.vocab_size, prompt_len)]
+    runs = []
+    for r in range(samples + 1):  # the first run warms up
+        t0 = time.perf_counter()
+        tok = cpu.prefill(prompt)
+        prefill_s = time.perf_counter() - t0
+        toks, step_ms = [tok], []
+        t0 = time.perf_counter()
+        while len(toks) < out_len:
+            t1 = time.perf_counter()
+            toks.append(cpu.decode(toks[-1], prompt_len + len(toks) - 1))
+            step_ms.append((time.perf_counter() - t1) * 1e3)
+            if time.perf_counter() - t0 >= seconds:
+                break
+        decode_s = time.perf_counter() - t0
+        if r > 0:
+            runs.append((prefill_s, decode_s, step_ms, toks))
+    cpu_tokens = runs[0][3]
+    if any(rr[3] != cpu_tokens[:len(rr[3])] for rr in runs):
+        raise SystemExit("bench: repeated CPU decodes of one prompt gave different tokens")
+    rates = [len(rr[2]) / rr[1] for rr in runs]
+    steps_all = [v for rr in runs for v in rr[2]]
+    # the GPU on the same workload
+    first = gpu.prefill(prompt)
     steps = len(cpu_tokens) - 1
-    gpu_tokens, _ = gpu_model.generate(prompt, len(cpu_tokens), stop_on_eos=False)
+    gpu_times = []
+    for _ in range(4):
+        gpu.rewind(prompt_len, first)
+        t0 = time.perf_counter()
+        gpu_tokens_tail = gpu.decode_steps(steps)
+        gpu_times.append(time.perf_counter() - t0)
+    gpu_tokens = [first] + list(gpu_tokens_tail)
+    gpu_rate = steps / float(np.median(gpu_times[1:]))
     first_diff = next((i for i, (a, b) in enumerate(zip(gpu_tokens, cpu_tokens)) if a != b),
                       None)
     divergence = None
     if first_diff is not None:
-        # Both models on the common prefix, then the step that differs.
         ref_tok, ref_logits = cpu.prefill(prompt, logits=True)
-        gpu_model.reset()
-        gpu_tok = gpu_model.prefill(prompt)
+        gpu.reset()
+        gpu_tok = gpu.prefill(prompt)
         for i in range(first_diff):
-            ref_tok, ref_logits = cpu.decode(cpu_tokens[i], len(prompt) + i, logits=True)
-            gpu_tok = gpu_model.decode_next(cpu_tokens[i])
-        divergence = near_tie_rule(gpu_model.last_logits_host(), ref_logits, gpu_tok, ref_tok)
+            ref_tok, ref_logits = cpu.decode(cpu_tokens[i], prompt_len + i, logits=True)
+            gpu_tok = gpu.decode_next(cpu_tokens[i])
+        divergence = near_tie_rule(gpu.last_logits_host(), ref_logits, gpu_tok, ref_tok)
         divergence["step"] = first_diff
     cpu.close()
+    gpu.close()
+    st = stats_of(rates)
     return {
-        "value": round(steps / decode_s, 3),
+        "value": st["mean"],
         "unit": "tok/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"config 0 workload: prompt 32 (prefill {32 / prefill_s:.1f} tok/s), then "
-                   f"{steps} greedy decode steps in {decode_s:.1f} s; FP32 C/OpenMP "
-                   f"restatement of cpu_ops.cpp + the qwen2.cpp CPU op order on the "
-                   f"dequantised weights of the GPU run (max_seq {max_seq})"),
+        "sample": (f"config 0: seed-0 random-init model, prompt {prompt_len}, {steps} greedy "
+                   f"decode steps, max_seq {max_seq}; {samples} timed decodes after one "
+                   f"warm-up ({sum(len(rr[2]) for rr in runs)} steps, "
+                   f"{sum(rr[1] for rr in runs):.1f} s); FP32 C/OpenMP restatement of "
+                   f"cpu_ops.cpp + the qwen2.cpp CPU op order on the W8A16-dequantised weights"),
+        "decode_tok_s": st,
+        "decode_ms_per_token": stats_of(steps_all),
+        "prefill_tok_s": stats_of([prompt_len / rr[0] for rr in runs]),
+        "gpu_same_workload_tok_s": round(gpu_rate, 1),
+        "gpu_speedup": round(gpu_rate / st["mean"], 1),
         "greedy_tokens_compared": len(cpu_tokens),
         "first_divergence_vs_gpu": first_diff,
         "divergence_check": divergence,
@@ -759,9 +931,6 @@ def e2e_main(args, dev):
         model = model_hip.Qwen2Model.open(workdirs["w8a16"], "w8a16",
                                           max_sequence_length=max_seq, use_graph=graph)
         t4 = time.perf_counter()
-        with archive_hip.ModelArchive(os.path.join(workdirs["w8a16"],
-                                                   "model.w8a16.qbin")) as archive:
-            tensors = {r.name: archive.data(r.name) for r in archive.records}
         archive_info = {"export_s": round(t2 - t1, 2), "open_s": round(t4 - t3, 2),
                         "archive_bytes": report["bytes"],
                         "max_groupwise_abs_error": report["max_groupwise_abs_error"],
@@ -815,12 +984,41 @@ def e2e_main(args, dev):
         if roofline is not None:
             roofline["linear_gemv_plan"] = plan_line
         plan.close()
-        del layers
+        model.close()
+        # Configs 3 and 2 beside it: the prefill GEMM layer plan at M = 512
+        # (MFMA-bound) and the standalone fused LM head (HBM-bound).
+        progress("config 3 prefill GEMM layer plans")
+        prefill, prefill_sets = prefill_roofline(dev, hip)
+        progress("config 2 LM head")
+        lm = lm_head_detail(dev, hip, keep_inputs=True)
+        if roofline is not None:
+            roofline["prefill_m512"] = {
+                "bound": "mfma",
+                "kernel": ("gemm_wide_grouped_kernel + splitk_reduce_kernel: one layer's 7 "
+                           "Linear GEMMs at M = 512 as one grouped plan launch (config 3)"),
+                "achieved": prefill["w8a16_M512"]["TFLOPs"], "peak": MFMA_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": prefill["w8a16_M512"]["frac"],
+                "avg_launch_us": prefill["w8a16_M512"]["us_per_layer_plan"],
+                "north_star_target_frac": 0.40, "by_config": prefill}
+            roofline["lm_head"] = {
+                "bound": "hbm",
+                "kernel": ("lm_head_bf16 (config 2: fused tied-embedding GEMV + FP32 argmax, "
+                           "151936 x 896, two embedding copies alternated)"),
+                "achieved": lm["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(lm["GBs"] / HBM_PEAK_GBS, 4), "avg_launch_us": lm["us_per_call"],
+                "algorithmic_bytes_per_launch": lm["bytes"]}
         cpu = None
         if args.cpu_seconds > 0:
-            progress("CPU baseline sample")
-            cpu = e2e_cpu_baseline(cfg, tensors, model, args.cpu_seconds)
-        model.close()
+            progress("CPU baseline: config 0 (seed-0 model)")
+            cpu = config0_baseline(cfg, args.cpu_seconds)
+            progress("CPU baselines: configs 1, 2, 3")
+            cpu["other_configs"] = linear_cpu_baselines(
+                {"calls": layers.calls, "gpu_us": plan_line["avg_launch_us"]},
+                {"e": lm["e"], "h": lm["h"], "gpu_us": lm["us_per_call"]},
+                prefill_sets, min(3.0, args.cpu_seconds))
+        del layers, prefill_sets
+        lm.pop("e", None)
+        lm.pop("h", None)
         detail = None
         if args.detail:
             progress("detail sweeps")
