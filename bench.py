@@ -85,9 +85,13 @@ def parse():
     ap.add_argument("--warmup", type=int, default=None,
                     help="untimed steps (default: e2e 2, else 20)")
     ap.add_argument("--launch", choices=("plan", "calls"), default="plan")
-    ap.add_argument("--workload", choices=("e2e", "gemv", "prefill", "ttft"), default="e2e",
+    ap.add_argument("--workload", choices=("e2e", "gemv", "prefill", "ttft", "tile"),
+                    default="e2e",
                     help="e2e: config 4 decode (the headline); gemv: config 1; "
-                         "prefill: config 3 GEMMs; ttft: config 4's prompt prefill")
+                         "prefill: config 3 GEMMs; ttft: config 4's prompt prefill; "
+                         "tile: one GEMM on the prefill's wide MFMA tile")
+    ap.add_argument("--shape", default="256,128,4864",
+                    help="tile: M,N,K of the GEMM (256,128,K is one workgroup on one CU)")
     ap.add_argument("--prompt", type=int, default=512, help="e2e and ttft prompt length")
     ap.add_argument("--decode-tokens", type=int, default=0,
                     help="e2e: decode steps per bench step (default: to context 1023, the "
@@ -299,6 +303,83 @@ def prefill_roofline(dev, hip, steps: int = 100) -> tuple:
         for plan in pl.plans:
             plan.close()
     return out, sets
+
+
+WIDE_TILE = 5  # linear_hip.GEMM_TILES index of the 256 x 128 tile (8 waves)
+
+
+def wide_tile_call(dev, hip, m: int, n: int, k: int, w8: bool, seed: int = 5):
+    """One GEMM on the wide tile (synthetic config-3 distributions): returns
+    a function that makes the call."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    x = torch.randn((m, k), device=dev, generator=g).to(torch.bfloat16)
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+    if w8:
+        q = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev, generator=g)
+        sc = ((torch.randn((n, k // 64), device=dev, generator=g) * 0.02).abs_()
+              / 127.0).to(torch.bfloat16)
+        return lambda: hip.gemm_w8a16_tile(q, sc, 64, None, x, y, m, n, k, WIDE_TILE)
+    w = (torch.randn((n, k), device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    return lambda: hip.gemm_bf16_tile(w, None, x, y, m, n, k, WIDE_TILE)
+
+
+def wide_tile_scaling(dev, hip, steps: int = 30) -> dict:
+    """The wide tile alone and across the chip: one tile (one CU) at K = 896
+    and 4864 separates the per-tile fixed cost from the per-stage cost, and
+    64 / 128 / 152 tiles (K = 896) show the stage on many CUs at once (the
+    clock under full load; rocprofv3 --pmc SQ_BUSY_CYCLES of `--workload
+    tile` gives it)."""
+    out = {}
+    for w8 in (False, True):
+        per = {}
+        for (m, n, k) in ((256, 128, 896), (256, 128, 4864), (2048, 1024, 896),
+                          (4096, 1024, 896), (512, 9728, 896)):
+            call = wide_tile_call(dev, hip, m, n, k, w8)
+            t, _ = time_steps(lambda ev: call(), steps, 5)
+            per[f"{m}x{n}x{k}"] = {"us": round(t / steps * 1e3, 2),
+                                   "tiles": ((m + 255) // 256) * ((n + 127) // 128),
+                                   "stages": k // 64}
+        a, b = per["256x128x896"]["us"], per["256x128x4864"]["us"]
+        stage = (b - a) / (76 - 14)
+        per["lone_tile_fixed_us"] = round(a - 14 * stage, 2)
+        per["lone_tile_us_per_stage"] = round(stage, 3)
+        for key in ("2048x1024x896", "4096x1024x896", "512x9728x896"):
+            per[key]["us_per_stage_beyond_fixed"] = round(
+                (per[key]["us"] - per["lone_tile_fixed_us"]) / 14, 3)
+        out["w8a16" if w8 else "bf16"] = per
+    return out
+
+
+def tile_main(args, dev, hip) -> int:
+    """One GEMM of --shape on the prefill's wide MFMA tile (256 x 128 of Y per
+    workgroup of 8 waves, gemm_*_tile with the tile named): one step = one
+    call; value = TFLOP/s.  For counter runs of the tile alone (one
+    workgroup) and across the chip."""
+    m, n, k = (int(v) for v in args.shape.split(","))
+    w8 = args.dtype == "w8a16"
+    call = wide_tile_call(dev, hip, m, n, k, w8)
+    t, _ = time_steps(lambda ev: call(), args.steps, args.warmup)
+    ms = t / args.steps
+    tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    line = {
+        "metric": f"{'W8A16' if w8 else 'BF16'} GEMM on the wide MFMA tile, M,N,K = {m},{n},{k}",
+        "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 x bf16 -> fp32" if w8 else "bf16 x bf16 -> fp32", "data": "synthetic",
+        "config": {"workload": f"one gemm_{'w8a16' if w8 else 'bf16'}_tile call on the 256 x 128 "
+                               f"tile: {((m + 255) // 256) * ((n + 127) // 128)} workgroups of "
+                               f"{k // 64} stages", "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "kernel": "gemm_wide_kernel", "achieved": round(tflops, 2),
+                     "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                     "avg_launch_us": round(ms * 1e3, 2)},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line))
+    return 0
 
 
 def prefill_main(args, dev, hip) -> int:
@@ -887,8 +968,54 @@ def calibration_detail(dev) -> dict:
     us = per_launch_us(lambda i: cal.stream_read(bufs[i], sink, 608), 48)
     out["cold_read_gate_up"] = {"bytes": per, "blocks": 608, "us_per_launch": round(us, 2)}
     del bufs
+    # XCD L2 contents across kernels: the same buffer read by 32 launches in
+    # a row (a launch's workgroups land on the same XCDs as the previous
+    # one's, whose L2s still hold the lines) against 32 distinct buffers.
+    keep = {}
+    for mb in (8, 16):
+        nb = mb << 20
+        bufs = torch.ones((32, nb // 4), dtype=torch.int32, device=dev)
+        same = per_launch_us(lambda i: cal.stream_read(bufs[0], sink, 1024), 32)
+        distinct = per_launch_us(lambda i: cal.stream_read(bufs[i], sink, 1024), 32)
+        keep[f"{mb}MB"] = {"same_buffer_us": round(same, 2),
+                           "distinct_buffers_us": round(distinct, 2)}
+        del bufs
+    out["l2_across_launches"] = keep
     if int(sink.item()) != 0:
         raise RuntimeError("calibration read wrote its sink")
+    out["cu_rates"] = cu_rates(dev)
+    return out
+
+
+def cu_rates(dev, blocks: int = 256, iters: int = 2000) -> dict:
+    """The compute-unit rates a GEMM stage is built from (csrc/calibration.hip
+    cu_probe_kernel, one workgroup per CU, each timing its whole loop with
+    the shader clock): LDS read and write bytes per clock per CU, cycles per
+    v_mfma_f32_32x32x16_bf16 per SIMD alone and with the W8A16 fold (in
+    blocks after each chain, with four partials in rotation, and pinned one
+    MFMA then four FMAs), MFMAs beside LDS reads, and L2-to-LDS fills
+    directly and through registers; at 4 and 8 waves per CU (1 and 2 per
+    SIMD).  `GHz` is the shader clock over the 100 MHz clock."""
+    import torch
+    import calibration_hip as cal
+    cycles = torch.zeros(2 * blocks, dtype=torch.int64, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    src = torch.ones(1 << 18, dtype=torch.int32, device=dev)
+    out = {}
+    for name, (_, lds_bytes, mfma, _) in cal.CU_PROBES.items():
+        for threads in (256, 512):
+            cal.cu_probe(name, blocks, threads, 10, cycles, sink, src)
+            cal.cu_probe(name, blocks, threads, iters, cycles, sink, src)
+            torch.cuda.synchronize()
+            c = cycles.view(blocks, 2).cpu().double()
+            shader, real = c[:, 0].median().item(), c[:, 1].median().item()
+            waves = threads // 64
+            line = {"GHz": round(shader / (real * 10.0), 3)}
+            if lds_bytes:
+                line["B_per_clk_per_CU"] = round(waves * iters * lds_bytes / shader, 1)
+            if mfma:
+                line["cycles_per_mfma_per_SIMD"] = round(shader / (waves / 4 * iters * mfma), 2)
+            out[f"{name}/{waves}_waves"] = line
     return out
 
 
@@ -1025,6 +1152,7 @@ def e2e_main(args, dev):
             detail = {"e2e": e2e_detail(workdirs, cfg), "linear_calls": linear_calls_detail(dev),
                       "torch_mm_bf16": torch_mm_detail(dev),
                       "lm_head": lm_head_detail(dev, hip), "torch_sum_read": torch_sum_read(dev),
+                      "gemm_wide_tile_scaling": wide_tile_scaling(dev, hip),
                       "calibration": calibration_detail(dev)}
     finally:
         for wd in workdirs.values():
@@ -1150,6 +1278,8 @@ def main() -> int:
         return e2e_main(args, dev)
     if args.workload == "ttft":
         return ttft_main(args, dev)
+    if args.workload == "tile":
+        return tile_main(args, dev, hip)
     layers = Layers(dev)
     plan = hip.W8A16GemvPlan(layers.calls)
     assert abs(plan.bytes - layers.bytes) < 1, (plan.bytes, layers.bytes)

@@ -37,6 +37,8 @@ def test_more_than_one_gpu_is_refused(gpus):
     (["--workload", "prefill", "--tokens", "128", "--dtype", "bf16"],
      {"steps": 200, "tokens": 128, "dtype": "bf16"}),
     (["--workload", "ttft", "--prompt", "32"], {"steps": 20, "warmup": 5, "prompt": 32}),
+    (["--workload", "tile", "--shape", "4096,1024,896", "--dtype", "bf16"],
+     {"workload": "tile", "shape": "4096,1024,896", "dtype": "bf16"}),
     (["--steps", "3", "--warmup", "0", "--graph", "off", "--decode-tokens", "32"],
      {"steps": 3, "warmup": 0, "graph": "off", "decode_tokens": 32}),
 ])
