@@ -306,6 +306,89 @@ def prefill_roofline(dev, hip, steps: int = 100) -> tuple:
 
 
 WIDE_TILE = 5  # linear_hip.GEMM_TILES index of the 256 x 128 tile (8 waves)
+UNIT_KINDS = {0: "whole_tile", 1: "split_part", 2: "gate_up_pair"}
+
+
+def wide_timeline(plans, launches: int = 12) -> dict:
+    """Where a wide-tile plan's launch spends its time: each workgroup's
+    s_memrealtime stamps (entry, first stage loaded, epilogue start, end;
+    100 MHz) and shader cycles from the plan's timeline launch
+    (infer_hip_gemm_plan_timeline), over `launches` launches rotating the
+    plans; medians over launches of per-kind medians, in microseconds."""
+    import numpy as np
+    import torch
+    wg = plans[0].workgroups()
+    words = plans[0].TIMELINE_WORDS
+    stamps = torch.zeros(words * wg, dtype=torch.int64, device="cuda")
+    per = []
+    for i in range(launches + 2):
+        for p in plans:  # warm: the plan's previous launch just ran
+            p.launch()
+        plans[i % len(plans)].launch_timeline(stamps)
+        torch.cuda.synchronize()
+        if i >= 2:
+            per.append(stamps.cpu().numpy().reshape(wg, words).astype(np.int64))
+    def summarize(a):
+        entry, loop, epi, end = (a[:, j].astype(np.float64) for j in range(4))
+        t0 = entry.min()
+        unit = a[:, 6]
+        stages = (unit >> 16) & 0xFF
+        kind = (unit >> 24) & 0xFF
+        us = 0.01  # one 100 MHz tick
+        res = {"kernel_span_us": (end.max() - t0) * us,
+               "last_entry_us": (entry.max() - t0) * us,
+               "xcd_is_workgroup_mod_8": float(np.mean(a[:, 4] == np.arange(wg) % 8)),
+               "ghz_median": float(np.median(a[:, 7] / ((end - entry) * 10.0)))}
+        for kcode, kname in UNIT_KINDS.items():
+            sel = kind == kcode
+            if not sel.any():
+                continue
+            res[kname] = {
+                "units": int(sel.sum()),
+                "stages": int(np.median(stages[sel])),
+                "start_us": float(np.median(entry[sel] - t0) * us),
+                "prologue_us": float(np.median(loop[sel] - entry[sel]) * us),
+                "us_per_stage": float(np.median((epi[sel] - loop[sel]) / stages[sel]) * us),
+                "epilogue_us": float(np.median(end[sel] - epi[sel]) * us),
+                "end_us": float(np.median(end[sel] - t0) * us),
+                "end_max_us": float((end[sel] - t0).max() * us),
+            }
+            if kname == "split_part" and np.any(a[sel, 8] != 0):
+                # the in-launch hand-off: partial stored, all parts arrived,
+                # slices summed
+                st, ar, rd = (a[sel, j].astype(np.float64) for j in (8, 9, 10))
+                res[kname]["store_partial_us"] = float(np.median(st - epi[sel]) * us)
+                res[kname]["wait_parts_us"] = float(np.median(ar - st) * us)
+                res[kname]["sum_slices_us"] = float(np.median(rd - ar) * us)
+        return res
+    rows = [summarize(a) for a in per]
+    def med(path):
+        vals = []
+        for r in rows:
+            v = r
+            for key in path:
+                v = v.get(key) if isinstance(v, dict) else None
+            if v is not None:
+                vals.append(v)
+        return round(float(np.median(vals)), 3) if vals else None
+    out = {"workgroups": wg, "launches": len(rows)}
+    for key in ("kernel_span_us", "last_entry_us", "xcd_is_workgroup_mod_8", "ghz_median"):
+        out[key] = med((key,))
+    for kname in UNIT_KINDS.values():
+        if kname in rows[0]:
+            out[kname] = {f: med((kname, f)) for f in rows[0][kname]}
+    return out
+
+
+def wide_timeline_detail(dev, hip, m: int = 512) -> dict:
+    """wide_timeline of the config-3 layer plans at M = 512, both dtypes."""
+    out = {}
+    for w8 in (True, False):
+        pl = PrefillLayers(dev, hip, m, w8)
+        out[f"{'w8a16' if w8 else 'bf16'}_M{m}"] = wide_timeline(pl.plans)
+        for p in pl.plans:
+            p.close()
+    return out
 
 
 def wide_tile_call(dev, hip, m: int, n: int, k: int, w8: bool, seed: int = 5):
@@ -447,6 +530,8 @@ def prefill_main(args, dev, hip) -> int:
         },
         "cpu_baseline": None,
     }
+    if m >= 256:
+        line["roofline"]["timeline"] = wide_timeline(pl.plans)
     print(json.dumps(line))
     for p in pl.plans:
         p.close()
@@ -1153,6 +1238,7 @@ def e2e_main(args, dev):
                       "torch_mm_bf16": torch_mm_detail(dev),
                       "lm_head": lm_head_detail(dev, hip), "torch_sum_read": torch_sum_read(dev),
                       "gemm_wide_tile_scaling": wide_tile_scaling(dev, hip),
+                      "gemm_wide_timeline": wide_timeline_detail(dev, hip),
                       "calibration": calibration_detail(dev)}
     finally:
         for wd in workdirs.values():

@@ -256,6 +256,23 @@ int infer_hip_gemm_plan_launch(const infer_hip_gemm_plan* plan, hipStream_t stre
 double infer_hip_gemm_plan_flops(const infer_hip_gemm_plan* plan);
 int infer_hip_gemm_plan_destroy(infer_hip_gemm_plan* plan);
 
+/* Measurement hook, no counterpart in the reference: launches a plan on the
+ * 256 x 128 tile (every descriptor with 256 tokens or more) with each
+ * workgroup of its GEMM launch writing 16 words to stamps[16 w .. 16 w + 15]
+ * (device memory): entry, first stage loaded, epilogue start and end, in
+ * 100 MHz ticks; the XCC_ID and HW_ID hardware registers; the unit
+ * (logical block | stages << 16 | kind << 24, kind 0 whole tile, 1 split
+ * part, 2 gate|up pair); the shader-clock cycles from entry to end; for a
+ * split part handing off inside the launch, the times its FP32 tile was
+ * stored, every part had arrived and its slices were summed (else 0);
+ * words 11-15 are 0.
+ * *workgroups receives the launch's workgroup count; with stamps null the
+ * call only reports it.  Results are the plan's.  Fails with
+ * INFER_HIP_INVALID_ARGUMENT on other plans or when capacity (workgroups)
+ * is too small. */
+int infer_hip_gemm_plan_timeline(const infer_hip_gemm_plan* plan, unsigned long long* stamps,
+                                 int capacity, int* workgroups, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

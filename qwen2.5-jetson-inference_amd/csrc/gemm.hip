@@ -550,10 +550,181 @@ struct WidePair {
 // its columns 0-63 and the same rows of pair.w2 (up) in columns 64-127, and
 // writes columns n0 .. n0 + 63 of Y = bf16(silu(bf16(gate)) * bf16(up)),
 // the arithmetic of silu_mul_kernel on the two GEMMs' BF16 outputs.
+// Split-K hand-off of a wide tile inside its launch.  The tile's `parts`
+// workgroups each store their FP32 tile row-major (256 x 128) at
+// partial + index * 32768 floats with device-coherent (sc1) stores, wait for
+// them, and count themselves on ctr[0].  Row slice s (rows s * R .. s * R +
+// R - 1, R = ceil(256 / parts)) of the output is then summed over the parts
+// in index order — the arithmetic of splitk_reduce_block, so the result does
+// not depend on which part finished when — plus the bias, and written as
+// BF16, by the workgroup that claims it (bit s of ctr[1], an agent-scope
+// atomic).  A part waits, a bounded number of polls, for every part to
+// arrive and then claims its own slice; the last to arrive claims its own
+// and then every slice still unclaimed.  So each slice is summed exactly
+// once, and no workgroup waits without end even if some part is not
+// resident: a part that gives up leaves its slice to the last arrival.  The
+// last of the parts to leave (ctr[2]) sets ctr[0..2] back to zero for the
+// next launch.  parts <= 32.
+constexpr int kWideArrivePolls = 1 << 16;
+#ifndef QLIN_HANDOFF_FENCE
+#define QLIN_HANDOFF_FENCE 0
+#endif
+
+__device__ __forceinline__ void wide_split_handoff(const GemmArgs& a, int m0, int n0,
+                                                   const SplitK& sp, const uint4* tile_lds,
+                                                   unsigned long long* stamp) {
+  constexpr int BM = kWideRows, BN = kWideCols, NT = kWideThreads;
+  constexpr int kChunksPerRow = BN / 8;
+  constexpr uint32_t kTileBytes = BM * BN * 4;
+  __shared__ int shared_word;
+  const int tid = threadIdx.x;
+  const __amdgpu_buffer_rsrc_t pr =
+      make_rsrc(sp.partial, static_cast<uint32_t>(sp.parts) * kTileBytes);
+  const int c8 = (tid % kChunksPerRow) * 8;
+  {
+    const uint32_t mine = static_cast<uint32_t>(sp.index) * kTileBytes;
+#pragma unroll
+    for (int i = 0; i < BM * kChunksPerRow / NT; ++i) {
+      const int row = (tid + NT * i) / kChunksPerRow;
+      const int idx = row * (kWideEpStride / 4) + c8 / 4;
+      const uint32_t off = mine + static_cast<uint32_t>(row * BN + c8) * 4u;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, tile_lds[idx]), pr, off, 0,
+                                             QLIN_HANDOFF_FENCE ? 0 : kCoherent);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, tile_lds[idx + 1]), pr,
+                                             off + 16u, 0, QLIN_HANDOFF_FENCE ? 0 : kCoherent);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's part is stored
+#if QLIN_HANDOFF_FENCE
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+#endif
+  __syncthreads();
+  int* ctr = sp.counter;
+  if (stamp && tid == 0) stamp[8] = __builtin_amdgcn_s_memrealtime();
+  if (tid == 0) {
+    const int before =
+        __hip_atomic_fetch_add(&ctr[0], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int state = 2;  // 2: last to arrive, 1: all arrived, 0: gave up waiting
+    if (before != sp.parts - 1) {
+      state = 0;
+      for (int poll = 0; poll < kWideArrivePolls; ++poll) {
+        if (__hip_atomic_load(&ctr[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= sp.parts) {
+          state = 1;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
+    shared_word = state;
+  }
+  __syncthreads();
+  const int state = shared_word;
+#if QLIN_HANDOFF_FENCE
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+#endif
+  if (stamp && tid == 0) stamp[9] = __builtin_amdgcn_s_memrealtime();
+  const int rows = (BM + sp.parts - 1) / sp.parts;
+  const bool vec = (a.n % 8) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15u) == 0;
+  const int n = n0 + c8;
+  auto claim = [&](int slice) {
+    __syncthreads();  // shared_word is free again
+    if (tid == 0) {
+      const int bit = 1 << slice;
+      shared_word = (__hip_atomic_fetch_or(&ctr[1], bit, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT) & bit) == 0;
+    }
+    __syncthreads();
+    return shared_word != 0;
+  };
+  auto reduce_slice = [&](int slice) {
+    const int r_begin = slice * rows, r_end = min(BM, r_begin + rows);
+    for (int r0 = r_begin; r0 < r_end; r0 += NT / kChunksPerRow) {
+      const int row = r0 + tid / kChunksPerRow;
+      const int m = m0 + row;
+      if (row >= r_end || m >= a.m || n >= a.n) continue;
+      const uint32_t off = static_cast<uint32_t>(row * BN + c8) * 4u;
+      constexpr int kBatch = 4;  // a batch's loads are all issued before its adds
+      float f[8];
+      for (int p0 = 0; p0 < sp.parts; p0 += kBatch) {
+        u32x4 v[kBatch][2];
+#pragma unroll
+        for (int q = 0; q < kBatch; ++q) {
+          if (p0 + q < sp.parts) {
+            const uint32_t po = static_cast<uint32_t>(p0 + q) * kTileBytes + off;
+            v[q][0] = __builtin_amdgcn_raw_buffer_load_b128(pr, po, 0,
+                                                            QLIN_HANDOFF_FENCE ? 0 : kCoherent);
+            v[q][1] = __builtin_amdgcn_raw_buffer_load_b128(pr, po + 16u, 0,
+                                                            QLIN_HANDOFF_FENCE ? 0 : kCoherent);
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < kBatch; ++q) {
+          if (p0 + q < sp.parts) {
+            const float g[8] = {__uint_as_float(v[q][0].x), __uint_as_float(v[q][0].y),
+                                __uint_as_float(v[q][0].z), __uint_as_float(v[q][0].w),
+                                __uint_as_float(v[q][1].x), __uint_as_float(v[q][1].y),
+                                __uint_as_float(v[q][1].z), __uint_as_float(v[q][1].w)};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) f[j] = (p0 + q) == 0 ? g[j] : f[j] + g[j];
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (a.bias && n + j < a.n) f[j] += bf16_to_f32(gload(a.bias + n + j));
+      }
+      uint16_t* dst = a.y + static_cast<size_t>(m) * a.n + n;
+      if (vec) {
+        store_nt16(dst, u32x4{pack2_bf16(f[0], f[1]), pack2_bf16(f[2], f[3]),
+                              pack2_bf16(f[4], f[5]), pack2_bf16(f[6], f[7])});
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (n + j < a.n) gstore(dst + j, f32_to_bf16(f[j]));
+        }
+      }
+    }
+  };
+  if (state >= 1 && claim(sp.index)) reduce_slice(sp.index);
+  if (state == 2) {
+    for (int s = 0; s < sp.parts; ++s) {
+      if (s != sp.index && claim(s)) reduce_slice(s);
+    }
+  }
+  __syncthreads();
+  if (stamp && tid == 0) stamp[10] = __builtin_amdgcn_s_memrealtime();
+  if (tid == 0 &&
+      __hip_atomic_fetch_add(&ctr[2], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+          sp.parts - 1) {
+    // every part has left: ready for the next launch
+    __hip_atomic_store(&ctr[0], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&ctr[1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&ctr[2], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Timeline slots of one workgroup (gemm_wide_grouped_timeline_kernel), in
+// 100 MHz s_memrealtime ticks unless noted.
+enum WideStamp {
+  kStampEntry = 0,      // first instruction
+  kStampLoop = 1,       // first stage in LDS (end of the prologue)
+  kStampEpilogue = 2,   // last stage's MFMAs issued (start of the epilogue)
+  kStampEnd = 3,        // every thread's stores done
+  kStampXcc = 4,        // XCC_ID hardware register (the XCD)
+  kStampHwId = 5,       // HW_ID hardware register (CU, SIMD, shader engine)
+  kStampUnit = 6,       // logical block | stages << 16 | kind << 24 (0 whole, 1 part, 2 pair)
+  kStampCycles = 7,     // s_memtime (shader clock) from entry to end
+  kStampStored = 8,     // split part: its FP32 tile stored (in-launch hand-off)
+  kStampArrived = 9,    // split part: every part has arrived (or the wait ended)
+  kStampReduced = 10,   // split part: its slices summed and stored
+  kStampSlots = 16
+};
+
 template <bool W8>
 __device__ __forceinline__ void gemm_wide_tile(const GemmArgs& a, int m0, int n0,
                                                const SplitK& split = SplitK{},
-                                               const WidePair& pair = WidePair{}) {
+                                               const WidePair& pair = WidePair{},
+                                               unsigned long long* stamp = nullptr) {
   constexpr int BM = kWideRows, BN = kWideCols, NT = kWideThreads, RS = kWideRowStride;
   constexpr int A_LD = BM * kRowChunks / NT;  // X chunks per thread per stage (4)
   constexpr int B_LD = BN * kRowChunks / NT;  // W chunks per thread per stage (2)
@@ -722,6 +893,7 @@ __device__ __forceinline__ void gemm_wide_tile(const GemmArgs& a, int m0, int n0
   store(0, sl[0]);
   load(2, sl[0]);
   __syncthreads();
+  if (stamp && tid == 0) stamp[kStampLoop] = __builtin_amdgcn_s_memrealtime();
   int g = 0;
   for (; g + 2 < stages; g += 2) {
     compute(0, csa, csb, g + 1, true, 1, &sl[1], true, g + 3);
@@ -744,6 +916,7 @@ __device__ __forceinline__ void gemm_wide_tile(const GemmArgs& a, int m0, int n0
   // writes them as one 16-byte BF16 store.  Scattered 2-byte stores of the
   // accumulator layout cost several microseconds per tile.
   float* ep = reinterpret_cast<float*>(lds_raw);
+  if (stamp && tid == 0) stamp[kStampEpilogue] = __builtin_amdgcn_s_memrealtime();
   __syncthreads();  // every wave is done with the stage buffers
 #pragma unroll
   for (int fm = 0; fm < 2; ++fm)
@@ -808,6 +981,12 @@ __device__ __forceinline__ void gemm_wide_tile(const GemmArgs& a, int m0, int n0
     }
     return;
   }
+#if QLIN_WIDE_INKERNEL
+  if (split.parts > 1) {
+    wide_split_handoff(a, m0, n0, split, lds_raw, stamp);
+    return;
+  }
+#endif
   if (split.parts > 1) {
     // One part of a tile split over K: its FP32 tile, row-major, for the
     // plan's reduction launch (the launch boundary orders these stores
@@ -875,13 +1054,14 @@ __global__ __launch_bounds__(kWideThreads) void gemm_wide_kernel(GemmArgs a) {
 // Grouped form of gemm_wide_kernel (same block -> unit mapping as
 // gemm_grouped_kernel: part u % splits of tile u / splits, M tiles fastest).
 template <bool W8>
-__device__ __forceinline__ void gemm_wide_unit(const GemmGroupDesc& d, int u) {
+__device__ __forceinline__ void gemm_wide_unit(const GemmGroupDesc& d, int u,
+                                               unsigned long long* stamp = nullptr) {
   const int tile = u / d.splits;
   if (d.w2) {
     // A gate|up pair: d.n counts both halves; each tile 64 columns of each.
     const GemmArgs a{d.w, d.s, d.bias, d.x, d.y, d.m, d.n / 2, d.k};
     gemm_wide_tile<W8>(a, (tile % d.tiles_m) * kWideRows, (tile / d.tiles_m) * (kWideCols / 2),
-                       SplitK{}, WidePair{d.w2, d.s2, d.bias2});
+                       SplitK{}, WidePair{d.w2, d.s2, d.bias2}, stamp);
     return;
   }
   const GemmArgs a{d.w, d.s, d.bias, d.x, d.y, d.m, d.n, d.k};
@@ -893,14 +1073,16 @@ __device__ __forceinline__ void gemm_wide_unit(const GemmGroupDesc& d, int u) {
     sp.begin = sp.index * d.split_stages;
     sp.count = min(d.split_stages, groups - sp.begin);
     sp.partial = d.partial + static_cast<size_t>(tile) * d.splits * (kWideRows * kWideCols);
+    sp.counter = d.counters ? d.counters + static_cast<size_t>(tile) * kWideSplitCounterInts : nullptr;
   }
-  gemm_wide_tile<W8>(a, (tile % d.tiles_m) * kWideRows, (tile / d.tiles_m) * kWideCols, sp);
+  gemm_wide_tile<W8>(a, (tile % d.tiles_m) * kWideRows, (tile / d.tiles_m) * kWideCols, sp,
+                     WidePair{}, stamp);
 }
 
 template <bool W8>
 __global__ __launch_bounds__(kWideThreads) void gemm_wide_grouped_kernel(
-    const GemmGroupDesc* __restrict__ descs, int count) {
-  const int b = blockIdx.x;
+    const GemmGroupDesc* __restrict__ descs, int count, WideBlockMap map) {
+  const int b = map.mapped ? map.logical[blockIdx.x] : blockIdx.x;
   int lo = 0, hi = count - 1;
   while (lo < hi) {  // last descriptor whose block_begin <= b
     const int mid = (lo + hi + 1) >> 1;
@@ -909,10 +1091,74 @@ __global__ __launch_bounds__(kWideThreads) void gemm_wide_grouped_kernel(
   gemm_wide_unit<W8>(descs[lo], b - descs[lo].block_begin);
 }
 
+// gemm_wide_grouped_kernel with a timeline: workgroup w writes the
+// WideStamp slots stamps[w * kStampSlots ..] (a measurement launch; the
+// stores and barrier at the end are its only extra work).  t0 and c0 are
+// the clocks read at the kernel's first instruction.
+template <bool W8>
+__device__ __forceinline__ void wide_timeline_unit(const GemmGroupDesc& d, int b,
+                                                   unsigned long long t0, unsigned long long c0,
+                                                   unsigned long long* __restrict__ stamps) {
+  unsigned long long* stamp = stamps + static_cast<size_t>(blockIdx.x) * kStampSlots;
+  const int u = b - d.block_begin;
+  const int groups = d.k / kStageK;
+  const int stages =
+      d.splits > 1 ? min(d.split_stages, groups - (u % d.splits) * d.split_stages) : groups;
+  const int kind = d.w2 ? 2 : (d.splits > 1 ? 1 : 0);
+  if (threadIdx.x == 0) {
+    unsigned xcc, hwid;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hwid));
+    stamp[kStampEntry] = t0;
+    stamp[kStampXcc] = xcc;
+    stamp[kStampHwId] = hwid;
+    stamp[kStampUnit] = static_cast<unsigned long long>(b) |
+                        (static_cast<unsigned long long>(stages) << 16) |
+                        (static_cast<unsigned long long>(kind) << 24);
+  }
+  gemm_wide_unit<W8>(d, u, stamp);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    stamp[kStampEnd] = __builtin_amdgcn_s_memrealtime();
+    stamp[kStampCycles] = __builtin_amdgcn_s_memtime() - c0;
+  }
+}
+
+template <bool W8>
+__global__ __launch_bounds__(kWideThreads) void gemm_wide_grouped_timeline_kernel(
+    const GemmGroupDesc* __restrict__ descs, int count, WideBlockMap map,
+    unsigned long long* __restrict__ stamps) {
+  const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+  const unsigned long long c0 = __builtin_amdgcn_s_memtime();
+  const int b = map.mapped ? map.logical[blockIdx.x] : blockIdx.x;
+  int lo = 0, hi = count - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (descs[mid].block_begin <= b) lo = mid; else hi = mid - 1;
+  }
+  wide_timeline_unit<W8>(descs[lo], b, t0, c0, stamps);
+}
+
+template <bool W8>
+__global__ __launch_bounds__(kWideThreads) void gemm_wide_inline_timeline_kernel(
+    GemmGroupArgs g, WideBlockMap map, unsigned long long* __restrict__ stamps) {
+  const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+  const unsigned long long c0 = __builtin_amdgcn_s_memtime();
+  const int b = map.mapped ? map.logical[blockIdx.x] : blockIdx.x;
+  int lo = 0;
+#pragma unroll
+  for (int i = 1; i < kInlineGroupMax; ++i) {
+    if (i < g.count && g.d[i].block_begin <= b) lo = i;
+  }
+  wide_timeline_unit<W8>(g.d[lo], b, t0, c0, stamps);
+}
+
 // The same with the descriptors in the kernel arguments.
 template <bool W8>
-__global__ __launch_bounds__(kWideThreads) void gemm_wide_inline_kernel(GemmGroupArgs g) {
-  const int b = blockIdx.x;
+__global__ __launch_bounds__(kWideThreads) void gemm_wide_inline_kernel(GemmGroupArgs g,
+                                                                       WideBlockMap map) {
+  const int b = map.mapped ? map.logical[blockIdx.x] : blockIdx.x;
   int lo = 0;
 #pragma unroll
   for (int i = 1; i < kInlineGroupMax; ++i) {
@@ -977,9 +1223,20 @@ __device__ __forceinline__ void splitk_reduce_block(const SplitReduceDesc& d, in
   }
 }
 
+// The logical reduction block of workgroup w (-1: none).  Mapped: XCD w % 8,
+// row block k % 16 of the split tile in slot k / 16 of that XCD (k = w / 8).
+__device__ __forceinline__ int reduce_block(const ReduceBlockMap& map, int w) {
+  if (map.slots == 0) return w;
+  constexpr int kBlocksPerTile = kWideRows / kSplitReduceRows;
+  const int k = w / kXcds;
+  const int t = map.tile[w % kXcds][k / kBlocksPerTile];
+  return t == 0xFF ? -1 : t * kBlocksPerTile + k % kBlocksPerTile;
+}
+
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(
-    const SplitReduceDesc* __restrict__ descs, int count) {
-  const int b = blockIdx.x;
+    const SplitReduceDesc* __restrict__ descs, int count, ReduceBlockMap map) {
+  const int b = reduce_block(map, blockIdx.x);
+  if (b < 0) return;
   int lo = 0, hi = count - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
@@ -988,8 +1245,10 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(
   splitk_reduce_block(descs[lo], b);
 }
 
-__global__ __launch_bounds__(256) void splitk_reduce_inline_kernel(SplitReduceArgs r) {
-  const int b = blockIdx.x;
+__global__ __launch_bounds__(256) void splitk_reduce_inline_kernel(SplitReduceArgs r,
+                                                                   ReduceBlockMap map) {
+  const int b = reduce_block(map, blockIdx.x);
+  if (b < 0) return;
   int lo = 0;
 #pragma unroll
   for (int i = 1; i < kInlineGroupMax; ++i) {
@@ -1529,17 +1788,50 @@ void launch_gemm_grouped(int tile, bool w8, const GemmGroupDesc* device_descs, i
 }
 
 void launch_gemm_wide_grouped(bool w8, const GemmGroupDesc* descs, int count, int units,
-                              const SplitReduceDesc* rdescs, int rcount, int reducers,
-                              hipStream_t stream) {
+                              const WideBlockMap& gmap, const SplitReduceDesc* rdescs, int rcount,
+                              int reducers, const ReduceBlockMap& rmap, hipStream_t stream) {
   if (w8) {
     hipLaunchKernelGGL((gemm_wide_grouped_kernel<true>), dim3(units), dim3(kWideThreads), 0, stream,
-                       descs, count);
+                       descs, count, gmap);
   } else {
     hipLaunchKernelGGL((gemm_wide_grouped_kernel<false>), dim3(units), dim3(kWideThreads), 0,
-                       stream, descs, count);
+                       stream, descs, count, gmap);
   }
   if (rcount > 0) {
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(reducers), dim3(256), 0, stream, rdescs, rcount);
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(reducers), dim3(256), 0, stream, rdescs, rcount,
+                       rmap);
+  }
+}
+
+void launch_gemm_wide_grouped_timeline(bool w8, const GemmGroupDesc* descs, int count, int units,
+                                       const WideBlockMap& gmap, unsigned long long* stamps,
+                                       const SplitReduceDesc* rdescs, int rcount, int reducers,
+                                       const ReduceBlockMap& rmap, hipStream_t stream) {
+  if (w8) {
+    hipLaunchKernelGGL((gemm_wide_grouped_timeline_kernel<true>), dim3(units), dim3(kWideThreads),
+                       0, stream, descs, count, gmap, stamps);
+  } else {
+    hipLaunchKernelGGL((gemm_wide_grouped_timeline_kernel<false>), dim3(units), dim3(kWideThreads),
+                       0, stream, descs, count, gmap, stamps);
+  }
+  if (rcount > 0) {
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(reducers), dim3(256), 0, stream, rdescs, rcount,
+                       rmap);
+  }
+}
+
+void launch_gemm_wide_grouped_timeline(const GemmGroupLaunch& l, unsigned long long* stamps,
+                                       hipStream_t stream) {
+  if (l.w8) {
+    hipLaunchKernelGGL((gemm_wide_inline_timeline_kernel<true>), dim3(l.blocks),
+                       dim3(kWideThreads), 0, stream, l.g, l.gmap, stamps);
+  } else {
+    hipLaunchKernelGGL((gemm_wide_inline_timeline_kernel<false>), dim3(l.blocks),
+                       dim3(kWideThreads), 0, stream, l.g, l.gmap, stamps);
+  }
+  if (l.r.count > 0) {
+    hipLaunchKernelGGL(splitk_reduce_inline_kernel, dim3(l.reducers), dim3(256), 0, stream, l.r,
+                       l.rmap);
   }
 }
 
@@ -1548,14 +1840,14 @@ void launch_gemm_group_inline(const GemmGroupLaunch& l, hipStream_t stream) {
   if (l.tile == kGemmTile256x128) {
     if (l.w8) {
       hipLaunchKernelGGL((gemm_wide_inline_kernel<true>), grid, dim3(kWideThreads), 0, stream,
-                         l.g);
+                         l.g, l.gmap);
     } else {
       hipLaunchKernelGGL((gemm_wide_inline_kernel<false>), grid, dim3(kWideThreads), 0, stream,
-                         l.g);
+                         l.g, l.gmap);
     }
     if (l.r.count > 0) {
       hipLaunchKernelGGL(splitk_reduce_inline_kernel, dim3(l.reducers), dim3(256), 0, stream,
-                         l.r);
+                         l.r, l.rmap);
     }
   } else if (l.w8) {
     hipLaunchKernelGGL((gemm_grouped_inline_kernel<64, 64, 2, true>), grid, dim3(kThreads), 0,

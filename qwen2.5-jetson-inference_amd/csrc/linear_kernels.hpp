@@ -162,10 +162,52 @@ struct SplitReduceDesc {
 };
 constexpr int kSplitReduceRows = 16;  // rows of a tile per reduction block
 
+// XCD placement of a wide-tile plan.  Workgroup b of a launch runs on XCD
+// b % 8, and each XCD has its own L2, so a split tile's parts are kept on one
+// XCD and its reduction blocks on the same one: the FP32 parts are then
+// written to and read back from that XCD's L2.  Both maps are permutations
+// of the launches' logical blocks (any permutation gives the same results).
+//
+// Build options (measured alternatives, off by default; `make EXTRA_DEFS=...`):
+// QLIN_WIDE_INKERNEL=1 sums a wide split tile's parts inside the GEMM launch
+// (gemm.hip, wide_split_handoff) instead of in the reduction launch, with
+// device-coherent (sc1) partial stores and loads, or with QLIN_HANDOFF_FENCE=1
+// with plain accesses between agent-scope release and acquire fences.
+// QLIN_XCD_MAP=0 places workgroups in logical order.
+#ifndef QLIN_XCD_MAP
+#define QLIN_XCD_MAP 1
+#endif
+#ifndef QLIN_WIDE_INKERNEL
+#define QLIN_WIDE_INKERNEL 0
+#endif
+// The in-launch hand-off: 4 ints of counters per split tile, at most 32 parts.
+constexpr int kWideSplitCounterInts = 4;
+constexpr int kWideMaxParts = 32;
+constexpr int kXcds = 8;
+constexpr int kWideMapBlocks = 256;  // plans with more blocks run unmapped
+struct WideBlockMap {
+  int mapped = 0;                       // 0: workgroup b runs logical block b
+  uint8_t logical[kWideMapBlocks] = {};  // workgroup -> logical block
+};
+constexpr int kReduceSlots = 16;
+struct ReduceBlockMap {
+  // split tiles per XCD: the reduction launch has kXcds * slots *
+  // (256 / kSplitReduceRows) workgroups; 0: unmapped
+  int slots = 0;
+  uint8_t tile[kXcds][kReduceSlots] = {};  // split tile of slot s on XCD x, 0xFF: none
+};
+// Places a wide-tile layout (after layout_gemm_group and bind_gemm_group) on
+// the XCDs: each split tile's parts on the XCD with the most free workgroups,
+// the whole tiles in the rest.  Leaves both maps unmapped when the launch has
+// more than kWideMapBlocks blocks, no split tile, or a split tile that fits
+// no XCD; *reducers receives the reduction launch's workgroups.
+void map_wide_group_to_xcds(const GemmGroupDesc* descs, int count, int blocks, WideBlockMap* gmap,
+                            ReduceBlockMap* rmap, int* reducers);
+
 // A grouped launch laid out on the host and passed by value as kernel
 // arguments, for callers whose shapes change from call to call (the model's
 // prefill at the prompt's length): no descriptor table in device memory.
-constexpr int kInlineGroupMax = 4;
+constexpr int kInlineGroupMax = 8;
 struct GemmGroupArgs {
   GemmGroupDesc d[kInlineGroupMax];
   int count;
@@ -181,6 +223,8 @@ struct GemmGroupLaunch {
   int reducers;  // workgroups of the split-K reduction launch (wide tile only)
   GemmGroupArgs g;
   SplitReduceArgs r;
+  WideBlockMap gmap;   // wide tile: workgroup -> unit (map_wide_group_to_xcds)
+  ReduceBlockMap rmap;
 };
 
 // plan.cpp: the layout shared by grouped plans and inline launches.  Sets
@@ -219,8 +263,18 @@ void launch_gate_up_silu(bool w8, const void* gate_w, const uint16_t* gate_s,
 // The wide-tile grouped launch (`units` blocks over descs) and, when some
 // GEMM is split, its reduction launch (`reducers` blocks over rdescs).
 void launch_gemm_wide_grouped(bool w8, const GemmGroupDesc* descs, int count, int units,
-                              const SplitReduceDesc* rdescs, int rcount, int reducers,
-                              hipStream_t stream);
+                              const WideBlockMap& gmap, const SplitReduceDesc* rdescs, int rcount,
+                              int reducers, const ReduceBlockMap& rmap, hipStream_t stream);
+// The same, each workgroup of the GEMM launch writing 16 timeline words
+// (entry, first stage, epilogue, end, XCD, hardware id, unit, shader cycles,
+// and a split part's hand-off times) to stamps[16 b ..].
+void launch_gemm_wide_grouped_timeline(bool w8, const GemmGroupDesc* descs, int count, int units,
+                                       const WideBlockMap& gmap, unsigned long long* stamps,
+                                       const SplitReduceDesc* rdescs, int rcount, int reducers,
+                                       const ReduceBlockMap& rmap, hipStream_t stream);
+// The same for launch_gemm_group_inline's wide-tile launches.
+void launch_gemm_wide_grouped_timeline(const GemmGroupLaunch& l, unsigned long long* stamps,
+                                       hipStream_t stream);
 
 // gemm.hip
 // Grouped launches use kGemmTile64x64, kGemmTile128x128 or kGemmTile256x128.

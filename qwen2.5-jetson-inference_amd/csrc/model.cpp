@@ -292,6 +292,9 @@ void linear_group(const infer_hip_model* m, const GemmItem* items, int count, in
   }
   g.r.count = bind_gemm_group(g.g.d, count, g.tile, m->gemm_partial, m->gemm_counters, g.r.d,
                               &g.reducers);
+  if (g.tile == kGemmTile256x128) {
+    map_wide_group_to_xcds(g.g.d, count, g.blocks, &g.gmap, &g.rmap, &g.reducers);
+  }
   launch_gemm_group_inline(g, m->stream);
 }
 

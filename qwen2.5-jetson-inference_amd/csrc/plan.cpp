@@ -192,9 +192,14 @@ int layout_gemm_group(GemmGroupDesc* table, int count, int cus, bool fill, int* 
     while (target < max_stages && units_for(target) > 2ll * cus) ++target;
   } else if (tile == kGemmTile256x128) {
     while (target < max_stages && units_for(target) > cus) ++target;
+    target = std::max(target, (max_stages + kWideMaxParts - 1) / kWideMaxParts);
   } else {
     while (target < max_stages && units_for(target) > 2ll * cus) ++target;
   }
+  // arrival counters per split tile: the 64 x 64 tiles' last-arrival count;
+  // the wide tile's in-launch hand-off (or none with a reduction launch)
+  const size_t counter_ints =
+      tile != kGemmTile256x128 ? 1 : (QLIN_WIDE_INKERNEL ? kWideSplitCounterInts : 0);
   size_t pf = 0, cc = 0;
   for (int i = 0; i < count; ++i) {
     GemmGroupDesc& d = table[i];
@@ -205,7 +210,7 @@ int layout_gemm_group(GemmGroupDesc* table, int count, int cus, bool fill, int* 
       d.splits = (stages + d.split_stages - 1) / d.split_stages;  // no empty part
       const size_t tiles = static_cast<size_t>(d.tiles_m) * ((d.n + bn - 1) / bn);
       pf += tiles * d.splits * bm * bn;
-      if (tile != kGemmTile256x128) cc += tiles;
+      cc += tiles * counter_ints;
     }
   }
   // Longest units first: they take longest, so starting them earliest
@@ -236,18 +241,90 @@ int bind_gemm_group(GemmGroupDesc* table, int count, int tile, float* partial, i
     if (d.splits <= 1) continue;
     const size_t tiles = static_cast<size_t>(d.tiles_m) * ((d.n + bn - 1) / bn);
     d.partial = partial + pf;
-    if (!wide) d.counters = counters + cc;
-    if (wide) {
+    if (!wide) {
+      d.counters = counters + cc;
+      cc += tiles;
+    } else if (QLIN_WIDE_INKERNEL) {
+      d.counters = counters + cc;
+      cc += tiles * kWideSplitCounterInts;
+    } else {
       reduce[rcount++] =
           SplitReduceDesc{d.partial, d.bias, d.y, d.m, d.n, d.tiles_m, d.splits, rblocks};
       rblocks += static_cast<int>(tiles) * (bm / kSplitReduceRows);
-    } else {
-      cc += tiles;
     }
     pf += tiles * d.splits * bm * bn;
   }
   *reducers = rblocks;
   return rcount;
+}
+
+void map_wide_group_to_xcds(const GemmGroupDesc* table, int count, int blocks, WideBlockMap* gmap,
+                            ReduceBlockMap* rmap, int* reducers) {
+  *gmap = WideBlockMap{};
+  *rmap = ReduceBlockMap{};
+  constexpr int kBlocksPerTile = kWideRowsHost / kSplitReduceRows;
+  int split_tiles = 0;
+  for (int i = 0; i < count; ++i) {
+    if (table[i].splits > 1) {
+      split_tiles += table[i].tiles_m * ((table[i].n + kWideColsHost - 1) / kWideColsHost);
+    }
+  }
+  *reducers = QLIN_WIDE_INKERNEL ? 0 : split_tiles * kBlocksPerTile;
+#if !QLIN_XCD_MAP
+  return;
+#endif
+  if (split_tiles == 0 || blocks <= 0 || blocks > kWideMapBlocks) return;
+  // XCD x runs the workgroups b < blocks with b % 8 == x.
+  int cap[kXcds];
+  for (int x = 0; x < kXcds; ++x) cap[x] = x < blocks ? (blocks - x + kXcds - 1) / kXcds : 0;
+  std::vector<int> on[kXcds];         // logical blocks placed on each XCD
+  std::vector<int> tiles_on[kXcds];   // split tiles (numbered over the plan) on each XCD
+  int tile_id = 0;
+  for (int i = 0; i < count; ++i) {
+    const GemmGroupDesc& d = table[i];
+    if (d.splits <= 1) continue;
+    const int tiles = d.tiles_m * ((d.n + kWideColsHost - 1) / kWideColsHost);
+    for (int t = 0; t < tiles; ++t, ++tile_id) {
+      int best = -1;
+      for (int x = 0; x < kXcds; ++x) {
+        const int free = cap[x] - static_cast<int>(on[x].size());
+        if (free >= d.splits && (best < 0 || free > cap[best] - static_cast<int>(on[best].size()))) {
+          best = x;
+        }
+      }
+      if (best < 0) return;  // unmapped
+      for (int p = 0; p < d.splits; ++p) on[best].push_back(d.block_begin + t * d.splits + p);
+      tiles_on[best].push_back(tile_id);
+    }
+  }
+  // whole tiles fill the remaining workgroups, XCD by XCD
+  int x = 0;
+  for (int i = 0; i < count; ++i) {
+    const GemmGroupDesc& d = table[i];
+    if (d.splits > 1) continue;
+    const int units = d.tiles_m * ((d.n + kWideColsHost - 1) / kWideColsHost);
+    for (int u = 0; u < units; ++u) {
+      while (static_cast<int>(on[x].size()) >= cap[x]) ++x;  // capacities sum to blocks
+      on[x].push_back(d.block_begin + u);
+    }
+  }
+  int slots = 0;
+  for (int y = 0; y < kXcds; ++y) slots = std::max(slots, static_cast<int>(tiles_on[y].size()));
+  for (int y = 0; y < kXcds; ++y) {
+    for (size_t k = 0; k < on[y].size(); ++k) {
+      gmap->logical[k * kXcds + y] = static_cast<uint8_t>(on[y][k]);
+    }
+  }
+  gmap->mapped = 1;
+  if (QLIN_WIDE_INKERNEL || slots > kReduceSlots || tile_id > 0xFE) return;  // reduction unmapped
+  for (int y = 0; y < kXcds; ++y) {
+    for (int k = 0; k < kReduceSlots; ++k) {
+      rmap->tile[y][k] =
+          k < static_cast<int>(tiles_on[y].size()) ? static_cast<uint8_t>(tiles_on[y][k]) : 0xFF;
+    }
+  }
+  rmap->slots = slots;
+  *reducers = kXcds * slots * kBlocksPerTile;
 }
 
 }  // namespace qlin
@@ -257,6 +334,13 @@ struct infer_hip_gemm_plan {
   float* partial = nullptr;        // split-K partial tiles (device)
   int* counters = nullptr;         // split-K arrival counters (device, zeroed)
   SplitReduceDesc* reduce = nullptr;  // split-K reduction table (device; wide tile)
+  WideBlockMap block_map;             // wide tile: workgroup -> unit
+  ReduceBlockMap reduce_map;          // wide tile: workgroup -> reduction block
+  // A wide-tile plan of at most kInlineGroupMax GEMMs launches with its
+  // descriptors in the kernel arguments: no dependent reads of the table
+  // before a workgroup's first loads.
+  bool inline_wide = false;
+  GemmGroupLaunch wide_launch{};
   int reduce_count = 0;
   int reduce_blocks = 0;
   int count = 0;
@@ -391,6 +475,24 @@ extern "C" int infer_hip_gemm_plan_create(const infer_hip_gemm_desc* descs, int 
   }
   reduce.resize(rcount);
   plan->reduce_count = rcount;
+  if (st == hipSuccess && tile == kGemmTile256x128) {
+    map_wide_group_to_xcds(table.data(), count, blocks, &plan->block_map, &plan->reduce_map,
+                           &plan->reduce_blocks);
+    if (count <= kInlineGroupMax) {
+      GemmGroupLaunch& l = plan->wide_launch;
+      l.tile = tile;
+      l.w8 = w8;
+      l.blocks = blocks;
+      l.reducers = plan->reduce_blocks;
+      for (int i = 0; i < count; ++i) l.g.d[i] = table[i];
+      l.g.count = count;
+      for (int i = 0; i < rcount; ++i) l.r.d[i] = reduce[i];
+      l.r.count = rcount;
+      l.gmap = plan->block_map;
+      l.rmap = plan->reduce_map;
+      plan->inline_wide = true;
+    }
+  }
   if (st == hipSuccess && !reduce.empty()) {
     st = hipMalloc(&plan->reduce, reduce.size() * sizeof(SplitReduceDesc));
     if (st == hipSuccess) {
@@ -419,13 +521,44 @@ extern "C" int infer_hip_gemm_plan_launch(const infer_hip_gemm_plan* plan, hipSt
   if (!plan) return fail(INFER_HIP_INVALID_ARGUMENT, "gemm plan: null plan");
   if (plan->skinny) {
     launch_gemm_skinny(plan->w8, plan->skinny_args, plan->blocks, stream);
+  } else if (plan->inline_wide) {
+    launch_gemm_group_inline(plan->wide_launch, stream);
   } else if (plan->tile == kGemmTile256x128) {
-    launch_gemm_wide_grouped(plan->w8, plan->table, plan->count, plan->blocks, plan->reduce,
-                             plan->reduce_count, plan->reduce_blocks, stream);
+    launch_gemm_wide_grouped(plan->w8, plan->table, plan->count, plan->blocks, plan->block_map,
+                             plan->reduce, plan->reduce_count, plan->reduce_blocks,
+                             plan->reduce_map, stream);
   } else {
     launch_gemm_grouped(plan->tile, plan->w8, plan->table, plan->count, plan->blocks, stream);
   }
   return check_launch("gemm plan");
+}
+
+extern "C" int infer_hip_gemm_plan_timeline(const infer_hip_gemm_plan* plan,
+                                            unsigned long long* stamps, int capacity,
+                                            int* workgroups, hipStream_t stream) {
+  if (!plan || !workgroups) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "gemm plan timeline: null plan or output pointer");
+  }
+  if (plan->skinny || plan->tile != kGemmTile256x128) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "gemm plan timeline: only plans on the 256 x 128 tile (every GEMM with 256 "
+                "tokens or more)");
+  }
+  *workgroups = plan->blocks;
+  if (!stamps) return ok();
+  if (capacity < plan->blocks) {
+    return fail(INFER_HIP_INVALID_ARGUMENT,
+                "gemm plan timeline: stamps hold %d workgroups, the launch has %d", capacity,
+                plan->blocks);
+  }
+  if (plan->inline_wide) {
+    launch_gemm_wide_grouped_timeline(plan->wide_launch, stamps, stream);
+  } else {
+    launch_gemm_wide_grouped_timeline(plan->w8, plan->table, plan->count, plan->blocks,
+                                      plan->block_map, stamps, plan->reduce, plan->reduce_count,
+                                      plan->reduce_blocks, plan->reduce_map, stream);
+  }
+  return check_launch("gemm plan timeline");
 }
 
 extern "C" double infer_hip_gemm_plan_flops(const infer_hip_gemm_plan* plan) {

@@ -50,6 +50,7 @@ EXPORTED_SYMBOLS = (
     "infer_hip_gemm_plan_launch",
     "infer_hip_gemm_plan_flops",
     "infer_hip_gemm_plan_destroy",
+    "infer_hip_gemm_plan_timeline",
 )
 
 
@@ -166,6 +167,8 @@ def load() -> ctypes.CDLL:
     lib.infer_hip_gemm_plan_flops.restype = ctypes.c_double
     lib.infer_hip_gemm_plan_destroy.argtypes = [p]
     lib.infer_hip_gemm_plan_destroy.restype = i
+    lib.infer_hip_gemm_plan_timeline.argtypes = [p, p, i, ctypes.POINTER(i), p]
+    lib.infer_hip_gemm_plan_timeline.restype = i
     _lib = lib
     return lib
 
@@ -384,6 +387,22 @@ class GemmPlan:
 
     def launch(self, stream=None) -> None:
         _check(load().infer_hip_gemm_plan_launch(self._handle, _stream(stream)))
+
+    def workgroups(self) -> int:
+        """Workgroups of a wide-tile plan's GEMM launch (raises on other plans)."""
+        n = ctypes.c_int(0)
+        _check(load().infer_hip_gemm_plan_timeline(self._handle, None, 0, ctypes.byref(n), None))
+        return n.value
+
+    TIMELINE_WORDS = 16
+
+    def launch_timeline(self, stamps, stream=None) -> None:
+        """One launch that also writes each workgroup's 16 timeline words
+        (int64 device tensor of 16 * workgroups() entries, zeroed)."""
+        n = ctypes.c_int(0)
+        _check(load().infer_hip_gemm_plan_timeline(
+            self._handle, _ptr(stamps), stamps.numel() // self.TIMELINE_WORDS, ctypes.byref(n),
+            _stream(stream)))
 
     def close(self) -> None:
         if self._handle:

@@ -176,6 +176,35 @@ def test_gemm_plan_matches_single_calls(hip, orc, dev, w8, m):
                 first = got
             for g, f in zip(got, first):
                 np.testing.assert_array_equal(g, f)
+        if tile != 5:
+            with pytest.raises(hip.InferError):  # the timeline is the wide tile's
+                plan.workgroups()
+            return
+        # The timeline launch computes the same outputs and stamps every
+        # workgroup: each logical unit once, its four times in order.
+        wg = plan.workgroups()
+        words_per = hip.GemmPlan.TIMELINE_WORDS
+        stamps = torch.zeros(words_per * wg, dtype=torch.int64, device=dev)
+        for c in calls:
+            (c[5] if w8 else c[3]).zero_()
+        plan.launch_timeline(stamps)
+        torch.cuda.synchronize()
+        for g, f in zip([words(c[5] if w8 else c[3]) for c in calls], first):
+            np.testing.assert_array_equal(g, f)
+        st = stamps.cpu().numpy().reshape(wg, words_per)
+        assert sorted((st[:, 6] & 0xFFFF).tolist()) == list(range(wg))
+        assert np.all(st[:, 0] <= st[:, 1]) and np.all(st[:, 1] <= st[:, 2])
+        assert np.all(st[:, 2] <= st[:, 3]) and np.all(st[:, 7] > 0)
+        kinds = set(((st[:, 6] >> 24) & 0xFF).tolist())
+        assert kinds == {0, 1}  # whole tiles and split parts
+        assert np.all((st[:, 6] >> 16) & 0xFF > 0)
+        parts = ((st[:, 6] >> 24) & 0xFF) == 1
+        if np.any(st[parts, 8] != 0):  # hand-off inside the launch: its times in order
+            h = st[parts]
+            assert np.all(h[:, 2] <= h[:, 8]) and np.all(h[:, 8] <= h[:, 9])
+            assert np.all(h[:, 9] <= h[:, 10]) and np.all(h[:, 10] <= h[:, 3])
+        with pytest.raises(hip.InferError):  # too few slots
+            plan.launch_timeline(stamps[: words_per * (wg - 1)])
     finally:
         plan.close()
 
