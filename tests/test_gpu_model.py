@@ -302,18 +302,49 @@ _full = {}
 
 
 def full_size(orc, max_seq, seed):
-    """The config 0 (seed 0) / config 4 (seed 4) model: Qwen2.5-0.5B shape,
-    FP32 init N(0, 0.02) with norm weights 1 and biases 0 (a freshly built
-    model), group-64 W8A16; the GPU runtime and the FP32 oracle on the same
-    dequantised weights.  One seed's tensors are cached at a time."""
+    """The config 0 (seed 0) / config 4 (seed 4) model as bench.py builds it:
+    a Qwen2.5-0.5B-shaped FP32 checkpoint, init N(0, 0.02) with norm weights
+    1 and biases 0 (a freshly built model), exported to a group-64 W8A16
+    QWENBIN1 model directory by the library's exporter and opened from it
+    (infer_hip_model_open); the FP32 oracle computes with the archive's
+    dequantised weights.  On first use of a seed the opened model is checked
+    bit for bit against the same weights handed over as tensors.  One seed's
+    directory and tensors are kept at a time."""
+    import atexit
+    import os
+    import shutil
+    import sys
+    import tempfile
+
+    import archive_hip
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    if root not in sys.path:
+        sys.path.insert(0, root)
+    import bench  # its export_model_dir: the directory the bench opens
     cfg = S.QWEN25_0_5B
     if _full.get("seed") != seed:
+        if "dir" in _full:
+            shutil.rmtree(_full["dir"], ignore_errors=True)
         _full.clear()
-        _full["t"] = S.random_model(cfg, "w8a16", seed=seed, plain_init=True)
-        _full["fp32"] = S.dequantized_fp32(_full["t"], cfg)
-        _full["seed"] = seed
-        print(f"full-size model generated (seed {seed})", flush=True)
-    g = model_hip.Qwen2Model(cfg, _full["t"], "w8a16", max_sequence_length=max_seq)
+        d = tempfile.mkdtemp(prefix=f"qwen-seed{seed}-")
+        atexit.register(shutil.rmtree, d, True)
+        checkpoint = S.random_checkpoint(cfg, seed=seed, std=0.02, plain_init=True)
+        bench.export_model_dir(cfg, checkpoint, d, "w8a16")
+        del checkpoint
+        with archive_hip.ModelArchive(f"{d}/model.w8a16.qbin") as a:
+            t = {r.name: a.data(r.name) for r in a.records}
+        _full.update(seed=seed, dir=d, t=t, fp32=S.dequantized_fp32(t, cfg))
+        print(f"full-size model exported and read back (seed {seed})", flush=True)
+        opened = model_hip.Qwen2Model.open(d, "w8a16", max_sequence_length=64)
+        given = model_hip.Qwen2Model(cfg, t, "w8a16", max_sequence_length=64)
+        p = prompt(17, cfg.vocab_size, seed=seed)
+        assert opened.prefill(p) == given.prefill(p)
+        np.testing.assert_array_equal(opened.last_logits_host(), given.last_logits_host())
+        assert opened.decode_steps(8) == given.decode_steps(8)
+        np.testing.assert_array_equal(opened.last_logits_host(), given.last_logits_host())
+        opened.close()
+        given.close()
+    g = model_hip.Qwen2Model.open(_full["dir"], "w8a16", max_sequence_length=max_seq)
     o = oracle_model(orc, cfg, _full["fp32"], max_seq)
     return cfg, g, o
 
@@ -340,9 +371,10 @@ def teacher_forced(g, o, p, steps, min_cos, what):
 
 def test_config0_workload_teacher_forced(orc, dev):
     """Config 0 on the HIP path: its own seed-0 random-init model exported
-    to W8A16, prompt of 32 uniform-random tokens (seed 0), 128 greedy steps
-    teacher-forced from the FP32 oracle on the same dequantised weights,
-    max_seq 256 (tests/test_qwen2.cpp:513-535 restated at full size)."""
+    to a W8A16 model directory and opened from it, prompt of 32
+    uniform-random tokens (seed 0), 128 greedy steps teacher-forced from the
+    FP32 oracle on the same dequantised weights, max_seq 256
+    (tests/test_qwen2.cpp:513-535 restated at full size)."""
     cfg, g, o = full_size(orc, 256, seed=0)
     p = prompt(32, cfg.vocab_size, seed=0)
     agree, total, worst = teacher_forced(g, o, p, 127, 0.999, "config 0")
@@ -355,10 +387,11 @@ def test_config0_workload_teacher_forced(orc, dev):
 
 
 def test_config4_workload_teacher_forced(orc, dev):
-    """Config 4's workload: prompt of 512 uniform-random tokens (seed 4),
-    max_seq 1024, then teacher-forced decode to context 1023 (511 steps),
-    every step against the FP32 oracle: the prefill's grouped MFMA launches
-    at 512 rows and the whole-context decode attention."""
+    """Config 4's workload on the bench's own model (seed-4 checkpoint
+    exported and opened from its directory): prompt of 512 uniform-random
+    tokens (seed 4), max_seq 1024, then teacher-forced decode to context 1023
+    (511 steps), every step against the FP32 oracle: the prefill's grouped
+    MFMA launches at 512 rows and the whole-context decode attention."""
     cfg, g, o = full_size(orc, 1024, seed=4)
     p = prompt(512, cfg.vocab_size, seed=4)
     agree, total, worst = teacher_forced(g, o, p, 511, 0.999, "config 4")
