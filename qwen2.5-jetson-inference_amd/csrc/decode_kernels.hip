@@ -542,7 +542,8 @@ __global__ __launch_bounds__(kBlock) void lm_head_decode_kernel(LmHeadDecodeArgs
   }
   // The (cos, sin) row of the next position, for the last workgroup when it
   // advances the state (requested by every workgroup, long before needed).
-  const bool keep_rope = a.advance && a.rope.row && static_cast<int>(threadIdx.x) < a.rope.half;
+  const bool keep_rope =
+      a.advance == 1 && a.rope.row && static_cast<int>(threadIdx.x) < a.rope.half;
   float2 rope_next = make_float2(0.0f, 0.0f);
   if (keep_rope) {
     rope_next = a.rope.table[static_cast<size_t>(min(a.state->pos + 1, a.rope.max_seq - 1)) *
@@ -584,6 +585,26 @@ __global__ __launch_bounds__(kBlock) void lm_head_decode_kernel(LmHeadDecodeArgs
     wi[wave] = best_i;
   }
   __syncthreads();
+  if (a.advance == 2) {
+    if (threadIdx.x == 0) {
+      float v = wv[0];
+      int i = wi[0];
+      for (int k = 1; k < kWaves; ++k) {
+        if (better(wv[k], wi[k], v, i)) {
+          v = wv[k];
+          i = wi[k];
+        }
+      }
+      // a workgroup whose rows never win the comparison (all NaN or -inf)
+      // offers its first row at the lowest key, so such a vocabulary yields
+      // row 0
+      const unsigned long long k =
+          i == INT_MAX ? lm_pack_key(__builtin_nanf(""), blockIdx.x * kWaves * R)
+                       : lm_pack_key(v, i);
+      __hip_atomic_fetch_max(a.key, k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return;
+  }
   const __amdgpu_buffer_rsrc_t cand =
       coherent_rsrc(a.block_best, static_cast<uint32_t>(gridDim.x) * 8u);
   if (threadIdx.x == 0) {

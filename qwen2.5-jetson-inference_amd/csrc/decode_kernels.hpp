@@ -168,8 +168,13 @@ struct LmHeadDecodeArgs {
   ModelState* state;       // with advance: step / pos moved on (else unused)
   int* history;
   int history_len;
-  int advance;             // nonzero: record the token and advance step / pos
-  RopeCursor rope;         // with advance: the row follows pos
+  int advance;             // 1: record the token and advance step / pos
+  RopeCursor rope;         // with advance 1: the row follows pos
+  // advance 2 (the model's decode step): each workgroup folds its best
+  // (value, row) into *key with one 64-bit atomic max (lm_pack_key) and
+  // nothing else; the next decode_entry_kernel applies it.  counter, token,
+  // state, history and rope are then unused.
+  unsigned long long* key = nullptr;
 };
 
 constexpr int kLmHeadRows = 4;  // rows per wave task

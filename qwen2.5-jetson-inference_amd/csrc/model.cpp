@@ -10,13 +10,16 @@
 //
 // Decode step (one token, position and token read from ModelState), W8A16
 // or W16A16 (the same launches, on int8 or BF16 weights):
-//   embedding; per layer five launches:
+//   entry (the previous step's deferred argmax applied to the state, then
+//   the token's embedding row); per layer five launches:
 //     RMSNorm + q|k|v GEMV + RoPE + KV store (norm_qkv_rope),
 //     attention over the context in two halves (partials),
 //     merge of the halves + o GEMV + residual (attn_o_halves),
 //     RMSNorm + gate|up GEMV + SiLU-mul (norm_gemv, paired rows),
 //     down GEMV + residual (gemv_rows);
-//   final RMSNorm + LM head + argmax + step bookkeeping (lm_head_decode).
+//   final RMSNorm + LM head + argmax (lm_head_decode, the argmax left in
+//   lm_key for the next entry launch; a run of steps ends with one more
+//   entry launch that only settles the state).
 // Every launch is built to wait on one round of global loads: a decode
 // step is latency-bound, not bandwidth-bound.  A head_dim other than 64 or
 // a max_seq over 1024 changes only the attention and the o-projection: the
@@ -124,6 +127,9 @@ struct infer_hip_model {
   int* lm_index = nullptr;
   float* lm_best = nullptr;   // fused LM head: per-workgroup (value, index)
   int* lm_counter = nullptr;
+  // fused LM head of the decode step: the argmax deferred to the next
+  // step's entry launch (LmHeadDecodeArgs::key), zero when none is pending
+  unsigned long long* lm_key = nullptr;
   float2* rope = nullptr;
   float2* rope_cur = nullptr;  // (cos, sin) of the decode position (RopeCursor)
   float* attn_partial = nullptr;  // decode attention split partials
@@ -369,15 +375,18 @@ RopeCursor rope_cursor(const infer_hip_model* m) {
 }
 
 // Final RMSNorm of `row` and the LM head with its argmax into state->token;
-// with `advance` the step's bookkeeping too (history, step, position).
-int lm_head_step(infer_hip_model* m, const uint16_t* row, bool advance) {
+// with `advance` the step's bookkeeping too (history, step, position).  The
+// fused LM head of a decode step defers both: its argmax stays in m->lm_key
+// for the next decode_entry launch (enqueue_decode_step, finish_decode).
+int lm_head_step(infer_hip_model* m, const uint16_t* row, bool advance, bool defer = false) {
   const infer_hip_model_config& c = m->cfg;
   if (m->fused_lm_head) {
-    launch_lm_head_decode({row, m->final_norm, c.rms_norm_eps, m->lm_head, c.vocab_size,
-                           c.hidden_size, m->logits, m->lm_best, m->lm_counter,
-                           &m->state->token, m->state, m->history, m->max_seq,
-                           advance ? 1 : 0, rope_cursor(m)},
-                          m->stream);
+    LmHeadDecodeArgs a{row, m->final_norm, c.rms_norm_eps, m->lm_head, c.vocab_size,
+                       c.hidden_size, m->logits, m->lm_best, m->lm_counter,
+                       &m->state->token, m->state, m->history, m->max_seq,
+                       defer ? 2 : (advance ? 1 : 0), rope_cursor(m)};
+    a.key = m->lm_key;
+    launch_lm_head_decode(a, m->stream);
     return check_launch("lm head");
   }
   launch_rms_norm(row, m->final_norm, m->norm, 1, c.hidden_size, c.rms_norm_eps, m->stream);
@@ -387,6 +396,21 @@ int lm_head_step(infer_hip_model* m, const uint16_t* row, bool advance) {
   if (rc != INFER_HIP_OK || !advance) return rc;
   launch_advance(m->state, m->history, m->max_seq, rope_cursor(m), m->stream);
   return check_launch("decode step advance");
+}
+
+// The entry launch of a decode step (and, with out null, the launch that
+// applies the last step's deferred argmax: finish_decode).
+DecodeEntryArgs entry_args(const infer_hip_model* m, uint16_t* out) {
+  return DecodeEntryArgs{m->embed, m->state, m->lm_key, m->history, m->max_seq,
+                         rope_cursor(m), m->cfg.vocab_size, m->cfg.hidden_size, out};
+}
+
+// After the last decode step of a run: the step's deferred argmax applied
+// to the state (token, history, step, position, RoPE row).
+int finish_decode(infer_hip_model* m) {
+  if (!m->fused_lm_head) return ok();
+  launch_decode_entry(entry_args(m, nullptr), m->stream);
+  return check_launch("decode finish");
 }
 
 // Launch kinds of a decode step, for infer_hip_model_kernel_times.
@@ -421,8 +445,13 @@ int enqueue_decode_step(infer_hip_model* m, int only = -1, hipEvent_t* events = 
     launch();
     if (events) (void)hipEventRecord(events[recorded++], s);
   };
-  run(kKindEmbedding,
-      [&] { launch_embedding(m->embed, &m->state->token, 1, c.vocab_size, hidden, m->x, s); });
+  run(kKindEmbedding, [&] {
+    if (m->fused_lm_head) {
+      launch_decode_entry(entry_args(m, m->x), s);
+    } else {
+      launch_embedding(m->embed, &m->state->token, 1, c.vocab_size, hidden, m->x, s);
+    }
+  });
   for (const Layer& L : m->layers) {
     if (m->fused_norm_gemv) {
       if (m->fused_qkv_rope) {
@@ -495,7 +524,7 @@ int enqueue_decode_step(infer_hip_model* m, int only = -1, hipEvent_t* events = 
   }
   int rc = check_launch("decode step");
   if (rc != INFER_HIP_OK) return rc;
-  run(kKindLmHead, [&] { rc = lm_head_step(m, m->x, only < 0); });
+  run(kKindLmHead, [&] { rc = lm_head_step(m, m->x, only < 0, true); });
   return rc;
 }
 
@@ -618,9 +647,10 @@ int run_prefill(infer_hip_model* m, const int* tokens, int count, int* next) {
     // A one-token prompt is the decode step at position 0 (one graph
     // replay, 5 launches per layer) rather than the M = 1 prefill (9 per
     // layer): 0.5 ms instead of 1.0 ms for Qwen2.5-0.5B.
-    launch_set_state(m->state, tokens[0], 0, 0, rope_cursor(m), s);
+    launch_set_state(m->state, tokens[0], 0, 0, rope_cursor(m), s, m->lm_key);
     int rc = check_launch("prefill state");
     if (rc == INFER_HIP_OK) rc = run_decode_step(m);
+    if (rc == INFER_HIP_OK) rc = finish_decode(m);
     if (rc == INFER_HIP_OK) rc = read_token(m, next);
     return rc;
   }
@@ -667,7 +697,7 @@ int run_prefill(infer_hip_model* m, const int* tokens, int count, int* next) {
   if (rc != INFER_HIP_OK) return rc;
   rc = lm_head_step(m, m->px + static_cast<size_t>(count - 1) * hidden, false);
   if (rc != INFER_HIP_OK) return rc;
-  launch_set_state(m->state, -1, count, 0, rope_cursor(m), s);
+  launch_set_state(m->state, -1, count, 0, rope_cursor(m), s, m->lm_key);
   rc = check_launch("prefill state");
   if (rc != INFER_HIP_OK) return rc;
   return read_token(m, next);
@@ -826,6 +856,7 @@ extern "C" int infer_hip_model_create(const infer_hip_model_config* config,
   const size_t o_lmv = take(sizeof(float) * lm_entries), o_lmi = take(sizeof(int) * lm_entries);
   const size_t o_lmbest = take(8 * static_cast<size_t>(lm_head_decode_blocks(c.vocab_size)));
   const size_t o_lmcounter = take(sizeof(int));
+  const size_t o_lmkey = take(sizeof(unsigned long long));
   const size_t o_rope = take(sizeof(float2) * ms * (head_dim / 2));
   const size_t o_rope_cur = take(sizeof(float2) * (head_dim / 2));
   // (the fused step's two halves: 2 records of kAttnHalfRecord floats per head)
@@ -881,6 +912,7 @@ extern "C" int infer_hip_model_create(const infer_hip_model_config* config,
   m->lm_index = reinterpret_cast<int*>(a + o_lmi);
   m->lm_best = reinterpret_cast<float*>(a + o_lmbest);
   m->lm_counter = reinterpret_cast<int*>(a + o_lmcounter);
+  m->lm_key = reinterpret_cast<unsigned long long*>(a + o_lmkey);
   m->rope = reinterpret_cast<float2*>(a + o_rope);
   m->rope_cur = reinterpret_cast<float2*>(a + o_rope_cur);
   m->attn_partial = reinterpret_cast<float*>(a + o_partial);
@@ -1219,9 +1251,10 @@ extern "C" int infer_hip_model_decode_next(infer_hip_model* m, int token, int* n
     return fail(INFER_HIP_INVALID_ARGUMENT, "KV cache capacity exceeded");
   }
   DeviceGuard guard(m->device);
-  launch_set_state(m->state, token, m->position, 0, rope_cursor(m), m->stream);
+  launch_set_state(m->state, token, m->position, 0, rope_cursor(m), m->stream, m->lm_key);
   int rc = check_launch("decode state");
   if (rc == INFER_HIP_OK) rc = run_decode_step(m);
+  if (rc == INFER_HIP_OK) rc = finish_decode(m);
   if (rc == INFER_HIP_OK) rc = read_token(m, next_token);
   if (rc != INFER_HIP_OK) return rc;
   ++m->position;
@@ -1258,9 +1291,11 @@ extern "C" int infer_hip_model_decode_steps(infer_hip_model* m, int steps, int* 
   }
   if (steps == 0) return ok();
   DeviceGuard guard(m->device);
-  launch_set_state(m->state, m->last_token, m->position, 0, rope_cursor(m), m->stream);
+  launch_set_state(m->state, m->last_token, m->position, 0, rope_cursor(m), m->stream,
+                   m->lm_key);
   int rc = check_launch("decode state");
   for (int i = 0; i < steps && rc == INFER_HIP_OK; ++i) rc = run_decode_step(m);
+  if (rc == INFER_HIP_OK) rc = finish_decode(m);
   if (rc != INFER_HIP_OK) return rc;
   hipError_t st = hipSuccess;
   if (tokens_out) {
@@ -1438,7 +1473,8 @@ extern "C" int infer_hip_model_kernel_times(infer_hip_model* m, int position, in
       if (st != hipSuccess) rc = hip_fail(st, "kernel_times instantiate");
     }
     if (rc == INFER_HIP_OK) {
-      launch_set_state(m->state, m->last_token, position, 0, rope_cursor(m), m->stream);
+      launch_set_state(m->state, m->last_token, position, 0, rope_cursor(m), m->stream,
+                       m->lm_key);
       st = hipGraphLaunch(exec, m->stream);  // warm-up
       if (st == hipSuccess) st = hipEventRecord(start, m->stream);
       for (int r = 0; r < reps && st == hipSuccess; ++r) st = hipGraphLaunch(exec, m->stream);

@@ -1258,11 +1258,12 @@ __global__ __launch_bounds__(kThreads) void add_kernel(uint16_t* __restrict__ x,
 // Host-chosen decode state (a kernel, not a copy, so that it can sit in a
 // captured graph).  token < 0 keeps the current token.
 __global__ void set_state_kernel(ModelState* state, int token, int pos, int step,
-                                 RopeCursor rope) {
+                                 RopeCursor rope, unsigned long long* key) {
   if (threadIdx.x == 0 && blockIdx.x == 0) {
     if (token >= 0) state->token = token;
     state->pos = pos;
     state->step = step;
+    if (key) __hip_atomic_store(key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   if (rope.row && static_cast<int>(threadIdx.x) < rope.half) {
     rope.row[threadIdx.x] =
@@ -1456,9 +1457,51 @@ void launch_add(uint16_t* x, const uint16_t* y, long long n, hipStream_t stream)
 }
 
 void launch_set_state(ModelState* state, int token, int pos, int step, RopeCursor rope,
-                      hipStream_t stream) {
+                      hipStream_t stream, unsigned long long* key) {
   hipLaunchKernelGGL(set_state_kernel, dim3(1), dim3(kWave * 2), 0, stream, state, token, pos,
-                     step, rope);
+                     step, rope, key);
+}
+
+__global__ __launch_bounds__(kThreads) void decode_entry_kernel(DecodeEntryArgs a) {
+  __shared__ int s_token, s_pos;
+  if (threadIdx.x == 0) {
+    // the key and the state in one round trip
+    const unsigned long long key =
+        __hip_atomic_load(a.key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ModelState* st = a.state;
+    int token = st->token, pos = st->pos;
+    const int step = st->step;
+    if (key >> 63) {
+      token = lm_key_row(key);
+      if (step < a.history_len) a.history[step] = token;
+      st->step = step + 1;
+      st->token = token;
+      st->pos = ++pos;
+      __hip_atomic_store(a.key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    s_token = token;
+    s_pos = pos;
+  }
+  __syncthreads();
+  if (a.rope.row && static_cast<int>(threadIdx.x) < a.rope.half) {
+    a.rope.row[threadIdx.x] =
+        a.rope.table[static_cast<size_t>(min(s_pos, a.rope.max_seq - 1)) * a.rope.half +
+                     threadIdx.x];
+  }
+  if (!a.out) return;
+  const int token = min(max(s_token, 0), a.vocab - 1);
+  const uint16_t* src = a.table + static_cast<size_t>(token) * a.hidden;
+  if ((a.hidden & 7) == 0) {
+    for (int c = threadIdx.x; c < a.hidden / 8; c += kThreads) {
+      reinterpret_cast<uint4*>(a.out)[c] = reinterpret_cast<const uint4*>(src)[c];
+    }
+  } else {
+    for (int c = threadIdx.x; c < a.hidden; c += kThreads) a.out[c] = src[c];
+  }
+}
+
+void launch_decode_entry(const DecodeEntryArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL(decode_entry_kernel, dim3(1), dim3(kThreads), 0, stream, a);
 }
 
 void launch_advance(ModelState* state, int* history, int history_len, RopeCursor rope,

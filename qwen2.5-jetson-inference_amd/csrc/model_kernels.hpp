@@ -100,9 +100,48 @@ struct RopeCursor {
   int half;
   int max_seq;
 };
+// key (may be null): a pending LM-head key (LmHeadDecodeArgs::key) is
+// cleared with the state.
 void launch_set_state(ModelState* state, int token, int pos, int step, RopeCursor rope,
-                      hipStream_t stream);
+                      hipStream_t stream, unsigned long long* key = nullptr);
 void launch_advance(ModelState* state, int* history, int history_len, RopeCursor rope,
                     hipStream_t stream);
+
+// A decode step's argmax as one 64-bit word that an atomic max folds across
+// workgroups: bit 63 set (a key is pending); bits 31-62 the value as an
+// ordered unsigned integer, where NaN and -inf (which never win the argmax's
+// comparison) order lowest and -0 counts as +0; bits 0-30 0x7FFFFFFF - row,
+// so equal values go to the lowest row.  The largest key is the row the
+// argmax's comparison (higher value, then lower row) picks.
+__host__ __device__ inline unsigned long long lm_pack_key(float v, int row) {
+  unsigned int o = 0;
+  if (v == v && v != -__builtin_inff()) {
+    const unsigned int u = v == 0.0f ? 0u : __builtin_bit_cast(unsigned int, v);
+    o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  }
+  return (1ull << 63) | (static_cast<unsigned long long>(o) << 31) |
+         static_cast<unsigned long long>(0x7FFFFFFF - row);
+}
+__host__ __device__ inline int lm_key_row(unsigned long long key) {
+  return 0x7FFFFFFF - static_cast<int>(key & 0x7FFFFFFFull);
+}
+
+// The first launch of a decode step whose previous step deferred its argmax
+// to `key`: a pending key is applied — the token, its history entry, step
+// and position moved on, the (cos, sin) row of the new position — and
+// cleared; then the token's embedding row goes to out (null: the state
+// only).  With no key pending it is the embedding of state->token.
+struct DecodeEntryArgs {
+  const uint16_t* table;  // [vocab, hidden] BF16
+  ModelState* state;
+  unsigned long long* key;
+  int* history;
+  int history_len;
+  RopeCursor rope;
+  int vocab;
+  int hidden;
+  uint16_t* out;          // [hidden] BF16 or nullptr
+};
+void launch_decode_entry(const DecodeEntryArgs& a, hipStream_t stream);
 
 }  // namespace qlin
