@@ -1015,7 +1015,8 @@ def calibration_detail(dev) -> dict:
       fastest; 2048-4096 read ~15 % slower): the HBM read rate of a kernel
       that does nothing but read, the best of the two;
     - launch_floor: an empty kernel of 608 workgroups (the gate|up launch's
-      grid), 48 per graph: the fixed cost of one launch in a replay;
+      grid), 48 per graph: the fixed cost of one launch in a replay; and the
+      same for 1-4096 workgroups (`by_blocks`);
     - cold_read_gate_up: 48 reads of distinct 8,716,288-byte buffers (a
       layer's int8 gate and up weights; 418 MB together, more than the
       256 MB last-level cache) on the same 608-workgroup grid: the launch
@@ -1046,12 +1047,19 @@ def calibration_detail(dev) -> dict:
     out["hbm_read"] = {"bytes": nbytes, "by_grid": grids,
                        "GBs": max(g["GBs"] for g in grids.values())}
     del buf
-    out["launch_floor"] = {"blocks": 608,
-                           "us_per_launch": round(per_launch_us(lambda i: cal.empty(608), 48), 2)}
+    out["launch_floor"] = {
+        "blocks": 608, "us_per_launch": round(per_launch_us(lambda i: cal.empty(608), 48), 2),
+        "by_blocks": {str(b): round(per_launch_us(lambda i: cal.empty(b), 48), 2)
+                      for b in (1, 64, 256, 1024, 2048, 4096)}}
     per = 8716288
     bufs = torch.ones((48, per // 4), dtype=torch.int32, device=dev)
     us = per_launch_us(lambda i: cal.stream_read(bufs[i], sink, 608), 48)
-    out["cold_read_gate_up"] = {"bytes": per, "blocks": 608, "us_per_launch": round(us, 2)}
+    out["cold_read_gate_up"] = {
+        "bytes": per, "blocks": 608, "us_per_launch": round(us, 2),
+        # the same bytes on other grids: 608 workgroups leave 96 CUs with a
+        # third workgroup
+        "by_blocks": {str(b): round(per_launch_us(
+            lambda i: cal.stream_read(bufs[i], sink, b), 48), 2) for b in (256, 512, 1024, 2048)}}
     del bufs
     # XCD L2 contents across kernels: the same buffer read by 32 launches in
     # a row (a launch's workgroups land on the same XCDs as the previous
