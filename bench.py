@@ -335,9 +335,17 @@ def wide_timeline(plans, launches: int = 12) -> dict:
         stages = (unit >> 16) & 0xFF
         kind = (unit >> 24) & 0xFF
         us = 0.01  # one 100 MHz tick
+        # workgroups are dealt to the XCDs round robin: every workgroup w of
+        # one residue w mod 8 on one XCD, the 8 residues on 8 XCDs (the XCD
+        # numbering itself may be rotated)
+        xcc = a[:, 4] & 0xF
+        per_residue = [set(xcc[np.arange(wg) % 8 == r].tolist()) for r in range(min(8, wg))]
+        round_robin = (all(len(x) == 1 for x in per_residue) and
+                       len(set().union(*per_residue)) == len(per_residue))
         res = {"kernel_span_us": (end.max() - t0) * us,
                "last_entry_us": (entry.max() - t0) * us,
-               "xcd_is_workgroup_mod_8": float(np.mean(a[:, 4] == np.arange(wg) % 8)),
+               "xcd_by_workgroup_mod_8": float(round_robin),
+               "xcc_of_workgroups_0_to_7": [int(v) for v in a[:8, 4]],
                "ghz_median": float(np.median(a[:, 7] / ((end - entry) * 10.0)))}
         for kcode, kname in UNIT_KINDS.items():
             sel = kind == kcode
@@ -371,8 +379,9 @@ def wide_timeline(plans, launches: int = 12) -> dict:
             if v is not None:
                 vals.append(v)
         return round(float(np.median(vals)), 3) if vals else None
-    out = {"workgroups": wg, "launches": len(rows)}
-    for key in ("kernel_span_us", "last_entry_us", "xcd_is_workgroup_mod_8", "ghz_median"):
+    out = {"workgroups": wg, "launches": len(rows),
+           "xcc_of_workgroups_0_to_7": rows[-1]["xcc_of_workgroups_0_to_7"]}
+    for key in ("kernel_span_us", "last_entry_us", "xcd_by_workgroup_mod_8", "ghz_median"):
         out[key] = med((key,))
     for kname in UNIT_KINDS.values():
         if kname in rows[0]:
