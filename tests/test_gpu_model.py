@@ -172,6 +172,38 @@ def test_graph_replay_equals_eager_launches(dev, precision):
     b.close()
 
 
+@pytest.mark.parametrize("graph", [True, False], ids=["graph", "eager"])
+def test_decode_argmax_ties_go_to_the_lower_row(dev, graph):
+    """The decode step's argmax (each workgroup's best folded into one word,
+    applied by the next step's entry launch) on exact ties: the tied
+    embedding row of a token the decode produces is copied to a lower and a
+    higher unused row, so those tokens' logits equal its logits at every
+    step.  The lower copy must win every one of its ties (first-max, as
+    cpu_ops.cpp:175-177 picks) and, having the same embedding, continue the
+    sequence unchanged; the higher copy must never win."""
+    t, _ = weights(TINY, "w8a16")
+    p = prompt(5, TINY.vocab_size, seed=7)
+
+    def run(tensors):
+        g = model_hip.Qwen2Model(TINY, tensors, "w8a16", max_sequence_length=64,
+                                 use_graph=graph)
+        seq = [g.prefill(p)] + g.decode_steps(24)
+        g.close()
+        return seq
+
+    seq = run(t)
+    used = set(p) | set(seq)
+    a = next(tok for tok in seq[1:] if tok > 0 and any(x not in used for x in range(tok)))
+    lower = next(x for x in range(a) if x not in used)
+    higher = next(x for x in range(TINY.vocab_size - 1, a, -1) if x not in used)
+    embed = t["model.embed_tokens.weight"].copy()
+    embed[lower] = embed[a]
+    embed[higher] = embed[a]
+    tied = dict(t)
+    tied["model.embed_tokens.weight"] = embed
+    assert run(tied) == [lower if x == a else x for x in seq]
+
+
 def test_generate_equals_prefill_then_decode_next(dev):
     t, _ = weights(TINY, "w8a16")
     g = model_hip.Qwen2Model(TINY, t, "w8a16", max_sequence_length=64)
