@@ -573,6 +573,18 @@ def cpu_threads() -> int:
     return threads
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), for the CPU baselines."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def repeat_for(fn, seconds: float, min_reps: int = 3, max_reps: int = 10000):
     """Calls fn() at least min_reps times and until `seconds` have passed;
     returns the per-call times in seconds."""
@@ -599,7 +611,8 @@ def linear_cpu_baselines(layers, lm, prefill_sets, seconds: float) -> dict:
     import oracle  # test infrastructure: the CPU baseline leg only
     oracle.build()
     threads = cpu_threads()
-    out = {"cores": threads, "kind": "port",
+    out = {"cores": threads, "kind": "port", "cpu_model": cpu_model(),
+           "blas": "none: the oracle's own FP32 loops (OpenMP), no BLAS library",
            "what": "FP32 C/OpenMP restatement of cpu_ops.cpp linear_fp32 / linear_fp32_batch / "
                    "argmax on the dequantised weights"}
 
@@ -753,9 +766,12 @@ def config0_baseline(cfg, seconds: float, samples: int = 3):
                    f"warm-up ({sum(len(rr[2]) for rr in runs)} steps, "
                    f"{sum(rr[1] for rr in runs):.1f} s); FP32 C/OpenMP restatement of "
                    f"cpu_ops.cpp + the qwen2.cpp CPU op order on the W8A16-dequantised weights"),
+        "cpu_model": cpu_model(),
+        "blas": "none: the oracle's own FP32 loops (OpenMP), no BLAS library",
         "decode_tok_s": st,
         "decode_ms_per_token": stats_of(steps_all),
         "prefill_tok_s": stats_of([prompt_len / rr[0] for rr in runs]),
+        "ttft_ms": stats_of([rr[0] * 1e3 for rr in runs]),
         "gpu_same_workload_tok_s": round(gpu_rate, 1),
         "gpu_speedup": round(gpu_rate / st["mean"], 1),
         "greedy_tokens_compared": len(cpu_tokens),
