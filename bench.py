@@ -189,6 +189,8 @@ def cpu_baseline(layers, seconds: float):
         "unit": "tok/s",
         "cores": threads,
         "kind": "port",
+        "cpu_model": cpu_model(),
+        "blas": "none: the oracle's own FP32 loops (OpenMP), no BLAS library",
         "sample": (f"{passes} full passes (168 FP32 GEMVs each, 24 layers x 7 shapes, "
                    f"1.43 GB of dequantised FP32 weights) in {el:.1f} s; C/OpenMP "
                    f"restatement of cpu_ops.cpp linear_fp32"),
