@@ -859,17 +859,20 @@ __device__ __forceinline__ void gemm_wide_tile(const GemmArgs& a, int m0, int n0
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) A1[ks] = as_bf16x8(lds_a[buf][fa_base[1] + ks]);
     if (W8) {
-      f32x16_t p0, p1;
+      // four partials, each folded once the next chain is issued: no chain
+      // waits for a fold to release its registers (measured: 1.147 -> 1.12-1.13
+      // us per stage, layer plan -2 % against two partials reused)
+      f32x16_t p0, p1, p2, p3;
       chain(A0, B0, p0, true);
       chain(A0, B1, p1, true);
       if (st) store(nbuf, *sd);
+      chain(A1, B0, p2, true);
       fold(acc[0][0], p0, cs[0]);
-      chain(A1, B0, p0, true);
-      fold(acc[0][1], p1, cs[1]);
       if (ld) load(lg, *sd);
-      chain(A1, B1, p1, true);
-      fold(acc[1][0], p0, cs[0]);
-      fold(acc[1][1], p1, cs[1]);
+      chain(A1, B1, p3, true);
+      fold(acc[0][1], p1, cs[1]);
+      fold(acc[1][0], p2, cs[0]);
+      fold(acc[1][1], p3, cs[1]);
     } else {
       chain(A0, B0, acc[0][0], false);
       chain(A0, B1, acc[0][1], false);
