@@ -545,11 +545,23 @@ struct WidePair {
   const uint16_t* bias2 = nullptr;
 };
 
-// A plain tile covers columns n0 .. n0 + 127 of Y.  A pair tile (pair.w2
-// set, a.n the pair's width) covers rows n0 .. n0 + 63 of a.w (gate) in
-// its columns 0-63 and the same rows of pair.w2 (up) in columns 64-127, and
-// writes columns n0 .. n0 + 63 of Y = bf16(silu(bf16(gate)) * bf16(up)),
-// the arithmetic of silu_mul_kernel on the two GEMMs' BF16 outputs.
+// Timeline slots of one workgroup (gemm_wide_grouped_timeline_kernel), in
+// 100 MHz s_memrealtime ticks unless noted.
+enum WideStamp {
+  kStampEntry = 0,      // first instruction
+  kStampLoop = 1,       // first stage in LDS (end of the prologue)
+  kStampEpilogue = 2,   // last stage's MFMAs issued (start of the epilogue)
+  kStampEnd = 3,        // every thread's stores done
+  kStampXcc = 4,        // XCC_ID hardware register (the XCD)
+  kStampHwId = 5,       // HW_ID hardware register (CU, SIMD, shader engine)
+  kStampUnit = 6,       // logical block | stages << 16 | kind << 24 (0 whole, 1 part, 2 pair)
+  kStampCycles = 7,     // s_memtime (shader clock) from entry to end
+  kStampStored = 8,     // split part: its FP32 tile stored (in-launch hand-off)
+  kStampArrived = 9,    // split part: every part has arrived (or the wait ended)
+  kStampReduced = 10,   // split part: its slices summed and stored
+  kStampSlots = 16
+};
+
 // Split-K hand-off of a wide tile inside its launch.  The tile's `parts`
 // workgroups each store their FP32 tile row-major (256 x 128) at
 // partial + index * 32768 floats with device-coherent (sc1) stores, wait for
@@ -600,7 +612,7 @@ __device__ __forceinline__ void wide_split_handoff(const GemmArgs& a, int m0, in
 #endif
   __syncthreads();
   int* ctr = sp.counter;
-  if (stamp && tid == 0) stamp[8] = __builtin_amdgcn_s_memrealtime();
+  if (stamp && tid == 0) stamp[kStampStored] = __builtin_amdgcn_s_memrealtime();
   if (tid == 0) {
     const int before =
         __hip_atomic_fetch_add(&ctr[0], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -622,7 +634,7 @@ __device__ __forceinline__ void wide_split_handoff(const GemmArgs& a, int m0, in
 #if QLIN_HANDOFF_FENCE
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 #endif
-  if (stamp && tid == 0) stamp[9] = __builtin_amdgcn_s_memrealtime();
+  if (stamp && tid == 0) stamp[kStampArrived] = __builtin_amdgcn_s_memrealtime();
   const int rows = (BM + sp.parts - 1) / sp.parts;
   const bool vec = (a.n % 8) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15u) == 0;
   const int n = n0 + c8;
@@ -692,7 +704,7 @@ __device__ __forceinline__ void wide_split_handoff(const GemmArgs& a, int m0, in
     }
   }
   __syncthreads();
-  if (stamp && tid == 0) stamp[10] = __builtin_amdgcn_s_memrealtime();
+  if (stamp && tid == 0) stamp[kStampReduced] = __builtin_amdgcn_s_memrealtime();
   if (tid == 0 &&
       __hip_atomic_fetch_add(&ctr[2], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
           sp.parts - 1) {
@@ -703,23 +715,11 @@ __device__ __forceinline__ void wide_split_handoff(const GemmArgs& a, int m0, in
   }
 }
 
-// Timeline slots of one workgroup (gemm_wide_grouped_timeline_kernel), in
-// 100 MHz s_memrealtime ticks unless noted.
-enum WideStamp {
-  kStampEntry = 0,      // first instruction
-  kStampLoop = 1,       // first stage in LDS (end of the prologue)
-  kStampEpilogue = 2,   // last stage's MFMAs issued (start of the epilogue)
-  kStampEnd = 3,        // every thread's stores done
-  kStampXcc = 4,        // XCC_ID hardware register (the XCD)
-  kStampHwId = 5,       // HW_ID hardware register (CU, SIMD, shader engine)
-  kStampUnit = 6,       // logical block | stages << 16 | kind << 24 (0 whole, 1 part, 2 pair)
-  kStampCycles = 7,     // s_memtime (shader clock) from entry to end
-  kStampStored = 8,     // split part: its FP32 tile stored (in-launch hand-off)
-  kStampArrived = 9,    // split part: every part has arrived (or the wait ended)
-  kStampReduced = 10,   // split part: its slices summed and stored
-  kStampSlots = 16
-};
-
+// A plain tile covers columns n0 .. n0 + 127 of Y.  A pair tile (pair.w2
+// set, a.n the pair's width) covers rows n0 .. n0 + 63 of a.w (gate) in
+// its columns 0-63 and the same rows of pair.w2 (up) in columns 64-127, and
+// writes columns n0 .. n0 + 63 of Y = bf16(silu(bf16(gate)) * bf16(up)),
+// the arithmetic of silu_mul_kernel on the two GEMMs' BF16 outputs.
 template <bool W8>
 __device__ __forceinline__ void gemm_wide_tile(const GemmArgs& a, int m0, int n0,
                                                const SplitK& split = SplitK{},
