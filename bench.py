@@ -476,6 +476,15 @@ def tile_main(args, dev, hip) -> int:
     return 0
 
 
+def committed_traffic(path: str, key: str):
+    """HBM bytes per launch of `key` from the committed rocprofv3 --pmc
+    summary (profiles/traffic.json), or None."""
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get(key)
+
+
 def prefill_main(args, dev, hip) -> int:
     """Config 3: prefill GEMMs at M = --tokens.  One step = one layer's 7
     Linears as one grouped launch (value = GEMM TFLOP/s, i.e. the layer's
@@ -541,6 +550,8 @@ def prefill_main(args, dev, hip) -> int:
         },
         "cpu_baseline": None,
     }
+    if m == 512 and w8:
+        line["roofline"]["traffic"] = committed_traffic(args.traffic, "gemm_wide_plan_w8a16_M512")
     if m >= 256:
         line["roofline"]["timeline"] = wide_timeline(pl.plans)
     print(json.dumps(line))
@@ -1246,6 +1257,7 @@ def e2e_main(args, dev):
                 "achieved": prefill["w8a16_M512"]["TFLOPs"], "peak": MFMA_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": prefill["w8a16_M512"]["frac"],
                 "avg_launch_us": prefill["w8a16_M512"]["us_per_layer_plan"],
+                "traffic": committed_traffic(args.traffic, "gemm_wide_plan_w8a16_M512"),
                 "north_star_target_frac": 0.40, "by_config": prefill}
             roofline["lm_head"] = {
                 "bound": "hbm",
