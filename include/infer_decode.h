@@ -27,6 +27,10 @@
  *   infer_hip_attention_halves_o_proj_w8a16
  *                                      merges before gemv_w8a16 (o_proj) +
  *                                      add_inplace_bf16 (qwen2.cpp:633-641)
+ *   infer_hip_attention_decode_parts_bf16,
+ *   infer_hip_attention_parts_o_proj_w8a16
+ *                                      the same pair in two or four parts
+ *                                      (the model's decode step: four)
  *   infer_hip_gemv_w8a16_rows          gemv_w8a16 + add_inplace_bf16 (cuda_ops.hpp:
  *                                      98-99) for down_proj and the residual
  *                                      (qwen2.cpp:655-659)
@@ -44,8 +48,8 @@
  * The _w8a16 operators have _bf16 siblings for BF16 weights (the W16A16
  * decode step, with gemv_bf16, cuda_ops.hpp:24-26, in place of gemv_w8a16):
  * infer_hip_rms_norm_gemv_bf16, infer_hip_rms_norm_gate_up_silu_bf16,
- * infer_hip_rms_norm_qkv_rope_bf16, infer_hip_attention_halves_o_proj_bf16
- * and infer_hip_gemv_bf16_rows.  They run the same kernels instantiated for
+ * infer_hip_rms_norm_qkv_rope_bf16, infer_hip_attention_halves_o_proj_bf16,
+ * infer_hip_attention_parts_o_proj_bf16 and infer_hip_gemv_bf16_rows.  They run the same kernels instantiated for
  * 8 BF16 weights per 16-byte chunk instead of 16 int8 ones, so their K
  * limits are half the W8A16 ones.
  *
@@ -228,6 +232,33 @@ int infer_hip_attention_halves_o_proj_bf16(const float* records, const int* posi
                                            const uint16_t* weight, uint16_t* residual,
                                            int out_features, hipStream_t stream);
 
+/* The attention and its merge in P = num_parts parts (2 or 4) of
+ * S = 1024 / P positions, as the model's decode step runs it in four
+ * (quarters: a (kv head, quarter) unit per workgroup of 4 waves, twice as
+ * many workgroups as halves, each with half the loads).  Part sp holds
+ * positions [S sp, S sp + S) of [0, p] and stores the record
+ * records[(h * P + sp) * 68 + i] laid out as above; a part past the
+ * context stores nothing.  The o-projection merges the parts
+ * {0 .. p / S} as infer_hip_attention_halves_o_proj_w8a16 merges the
+ * halves; parts past that set are never summed.  num_parts 2 is exactly
+ * the halves operators; records hold num_heads x P x 68 floats.  Same
+ * preconditions otherwise. */
+int infer_hip_attention_decode_parts_bf16(const uint16_t* q, const uint16_t* key_cache,
+                                          const uint16_t* value_cache, const int* position,
+                                          float* records, int num_heads, int num_kv_heads,
+                                          int head_dim, int max_sequence_length,
+                                          int num_parts, hipStream_t stream);
+int infer_hip_attention_parts_o_proj_w8a16(const float* records, const int* position,
+                                           int num_heads, int max_sequence_length,
+                                           int num_parts, const int8_t* weight,
+                                           const uint16_t* scales, uint16_t* residual,
+                                           int out_features, hipStream_t stream);
+int infer_hip_attention_parts_o_proj_bf16(const float* records, const int* position,
+                                          int num_heads, int max_sequence_length,
+                                          int num_parts, const uint16_t* weight,
+                                          uint16_t* residual, int out_features,
+                                          hipStream_t stream);
+
 /* output[n] = bf16(sum_k q[n,k] s[n,k/64] input[k] + bias[n]) with one
  * wave per output row and the whole row in flight at once.  bias may be
  * NULL or equal to output (the in-place residual add of the decode step:
@@ -265,7 +296,7 @@ int infer_hip_attention_decode_spans_bf16(const uint16_t* q, const uint16_t* key
  * max_sequence_length positions and head_dim (64 or 128): split i covers
  * positions [i * span, (i + 1) * span).  At head_dim 64 with up to 1024
  * positions the context is covered whole (span 1024, 1 split: the decode
- * step then runs the two halves of infer_hip_attention_decode_halves_bf16);
+ * step then runs the four parts of infer_hip_attention_decode_parts_bf16);
  * otherwise at most 8 splits, whose partials the o-projection merges.
  * 0 for max_sequence_length < 1 or another head_dim. */
 int infer_hip_attention_decode_span(int max_sequence_length, int head_dim);

@@ -393,75 +393,6 @@ __global__ __launch_bounds__(kBlock) void gemv_rows_kernel(GemvRowsArgs a) {
   }
 }
 
-// The o-projection with the merge of the attention's two halves (see
-// decode_kernels.hpp).  One wave per row, the whole row's loads, both
-// records' pieces and the residual in flight at once.  Lane l's chunk c
-// (C = 16 inputs for int8 weights, 8 for BF16) is head c / (64 / C),
-// dimensions C (c % (64 / C)) .. + C - 1.  A second half that the context
-// has not reached is never summed (select, so stale values cannot reach the
-// result).  F is the weight format (W8Fmt, Bf16Fmt).
-template <class F, int SLABS>
-__global__ __launch_bounds__(kBlock) void attn_o_halves_kernel(AttnOHalvesArgs a) {
-  constexpr int C = F::C, J = C / 4;  // 16-byte record pieces per chunk
-  constexpr uint32_t kPerHead = 64 / C;  // chunks per head
-  const int lane = threadIdx.x & (kWave - 1);
-  const int row = blockIdx.x * kWaves + threadIdx.x / kWave;
-  const int chunks = a.k >> (C == 16 ? 4 : 3);
-  const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(a.partial), 0, a.heads * 2 * kAttnHalfRecord * 4, 0x00020000);
-  uint4 r0[SLABS][J], r1[SLABS][J];
-  float2 ml0[SLABS], ml1[SLABS];
-#pragma unroll
-  for (int s = 0; s < SLABS; ++s) {
-    const uint32_t c = static_cast<uint32_t>(min(s * kWave + lane, chunks - 1));
-    const uint32_t b0 = (c / kPerHead) * 2u * kAttnHalfRecord * 4u;
-    const uint32_t b1 = b0 + kAttnHalfRecord * 4u;
-    const uint32_t d = (c % kPerHead) * C * 4u;
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-      r0[s][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(pr, b0 + d + 16u * j, 0, 0));
-      r1[s][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(pr, b1 + d + 16u * j, 0, 0));
-    }
-    ml0[s] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(pr, b0 + 64u * 4u, 0, 0));
-    ml1[s] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(pr, b1 + 64u * 4u, 0, 0));
-  }
-  // the weights after the records: loads return in issue order, so the
-  // halves' merge runs while the weights stream in
-  typename F::template Row<SLABS> wr;
-  F::template load<SLABS>(a.w, a.s, row, a.n, a.k, lane, wr);
-  const uint16_t res_raw = gload(a.x + min(row, a.n - 1));
-  const int pos = min(*a.pos, a.max_seq - 1);
-  __builtin_amdgcn_sched_barrier(0);  // every load is in flight
-  const bool two = pos >= kAttnHalfSpan;
-  float xv[SLABS][C];
-#pragma unroll
-  for (int s = 0; s < SLABS; ++s) {
-    const bool keep = s * kWave + lane < chunks;
-    const float m = two ? fmaxf(ml0[s].x, ml1[s].x) : ml0[s].x;
-    const float w0 = expf(ml0[s].x - m);
-    const float w1 = two ? expf(ml1[s].x - m) : 0.0f;
-    const float l0w = ml0[s].y * w0;
-    const float ll = two ? fmaf(ml1[s].y, w1, l0w) : l0w;
-    const float inv = 1.0f / ll;  // one division per lane, then products
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const float a0[4] = {__uint_as_float(r0[s][j].x), __uint_as_float(r0[s][j].y),
-                           __uint_as_float(r0[s][j].z), __uint_as_float(r0[s][j].w)};
-      const float a1[4] = {__uint_as_float(r1[s][j].x), __uint_as_float(r1[s][j].y),
-                           __uint_as_float(r1[s][j].z), __uint_as_float(r1[s][j].w)};
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const float a0w = a0[t] * w0;
-        const float aa = two ? fmaf(a1[t], w1, a0w) : a0w;
-        // the attention's output is BF16, as attention_decode_bf16 stores it
-        xv[s][4 * j + t] = keep ? bf16_to_f32(f32_to_bf16(aa * inv)) : 0.0f;
-      }
-    }
-  }
-  const float v = F::template dot<SLABS>(wr, xv, row < a.n, a.k, lane);
-  if (lane == 0 && row < a.n) gstore(a.x + row, f32_to_bf16(v + bf16_to_f32(res_raw)));
-}
-
 // Slabs of 64 16-byte weight chunks spanning K (1024 int8 or 512 BF16
 // weights each).
 static int fused_slabs(int k, bool w8) {
@@ -473,24 +404,132 @@ bool attn_o_halves_supported(int k, bool w8) {
   return k >= 64 && k % 64 == 0 && fused_slabs(k, w8) <= 4;
 }
 
-template <class F>
-static void launch_attn_o_halves_fmt(const AttnOHalvesArgs& a, hipStream_t stream) {
+// The o-projection with the merge of the attention's P parts (two halves or
+// four quarters; see decode_kernels.hpp).  The merge is done once per
+// workgroup: its 256 threads each merge four consecutive attention outputs
+// (rounds of 1024) from the P records, with the records' loads, the
+// weight row's and the residual's in flight at once, and store them as BF16
+// in LDS; after one barrier every wave reads its lanes' inputs from there
+// (lane l's chunk c, C = 16 inputs for int8 weights, 8 for BF16).  A part
+// that the context has not reached is never summed (select, so stale
+// values cannot reach the result).  Measured at config 4 (quarters): 2.92
+// us per launch against 3.37 when each wave merged every head from the
+// records itself (four times the record loads, no barrier).  F is the
+// weight format (W8Fmt, Bf16Fmt).
+template <class F, int SLABS, int P>
+__global__ __launch_bounds__(kBlock) void attn_o_parts_kernel(AttnOPartsArgs a) {
+  constexpr int C = F::C;
+  constexpr int S = kAttnWholeMax / P;  // positions per part
+  constexpr int RQ = (SLABS * kWave * C / 4 + kBlock - 1) / kBlock;  // merge rounds
+  __shared__ __align__(16) uint16_t xs[SLABS * kWave * C];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int row = blockIdx.x * kWaves + tid / kWave;
+  const int chunks = a.k / C, quads = a.k >> 2;
+  const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(a.partial), 0, a.heads * P * kAttnPartRecord * 4, 0x00020000);
+  float4 r[RQ][P];
+  float2 ml[RQ][P];
+#pragma unroll
+  for (int q = 0; q < RQ; ++q) {
+    const uint32_t i = static_cast<uint32_t>(min(q * kBlock + tid, quads - 1));
+    const uint32_t b0 = (i / 16u) * P * kAttnPartRecord * 4u, d = (i % 16u) * 16u;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const uint32_t bp = b0 + p * kAttnPartRecord * 4u;
+      r[q][p] = __builtin_bit_cast(float4,
+                                   __builtin_amdgcn_raw_buffer_load_b128(pr, bp + d, 0, 0));
+      ml[q][p] = __builtin_bit_cast(
+          float2, __builtin_amdgcn_raw_buffer_load_b64(pr, bp + 64u * 4u, 0, 0));
+    }
+  }
+  typename F::template Row<SLABS> wr;
+  F::template load<SLABS>(a.w, a.s, row, a.n, a.k, lane, wr);
+  const uint16_t res_raw = gload(a.x + min(row, a.n - 1));
+  const int pos = min(*a.pos, a.max_seq - 1);
+  __builtin_amdgcn_sched_barrier(0);  // every load is in flight
+  const int live = pos / S + 1;       // parts [0, live) hold records
+#pragma unroll
+  for (int q = 0; q < RQ; ++q) {
+    const int i = q * kBlock + tid;
+    float m = ml[q][0].x;
+#pragma unroll
+    for (int p = 1; p < P; ++p) m = p < live ? fmaxf(m, ml[q][p].x) : m;
+    float w[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) w[p] = p == 0 || p < live ? expf(ml[q][p].x - m) : 0.0f;
+    float ll = ml[q][0].y * w[0];
+#pragma unroll
+    for (int p = 1; p < P; ++p) ll = p < live ? fmaf(ml[q][p].y, w[p], ll) : ll;
+    const float inv = 1.0f / ll;
+    float av[P][4];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      av[p][0] = r[q][p].x;
+      av[p][1] = r[q][p].y;
+      av[p][2] = r[q][p].z;
+      av[p][3] = r[q][p].w;
+    }
+    float o[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      float aa = av[0][t] * w[0];
+#pragma unroll
+      for (int p = 1; p < P; ++p) aa = p < live ? fmaf(av[p][t], w[p], aa) : aa;
+      o[t] = aa * inv;
+    }
+    if (i < quads) {
+      // the attention's output is BF16, as attention_decode_bf16 stores it
+      const uint2 packed = {f32_to_bf16(o[0]) | (static_cast<uint32_t>(f32_to_bf16(o[1])) << 16),
+                            f32_to_bf16(o[2]) | (static_cast<uint32_t>(f32_to_bf16(o[3])) << 16)};
+      *reinterpret_cast<uint2*>(xs + 4 * i) = packed;
+    }
+  }
+  __syncthreads();
+  float xv[SLABS][C];
+#pragma unroll
+  for (int s = 0; s < SLABS; ++s) {
+    const int c = s * kWave + lane;
+    const bool keep = c < chunks;
+    const uint16_t* src = xs + C * min(c, chunks - 1);
+#pragma unroll
+    for (int j = 0; j < C / 8; ++j) {
+      const uint4 u = *reinterpret_cast<const uint4*>(src + 8 * j);
+      const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        xv[s][8 * j + 2 * t] = keep ? bf16_to_f32(wd[t] & 0xFFFFu) : 0.0f;
+        xv[s][8 * j + 2 * t + 1] = keep ? bf16_to_f32(wd[t] >> 16) : 0.0f;
+      }
+    }
+  }
+  const float v = F::template dot<SLABS>(wr, xv, row < a.n, a.k, lane);
+  if (lane == 0 && row < a.n) gstore(a.x + row, f32_to_bf16(v + bf16_to_f32(res_raw)));
+}
+
+template <class F, int P>
+static void launch_attn_o_parts_fmt(const AttnOPartsArgs& a, hipStream_t stream) {
   const dim3 grid((a.n + kWaves - 1) / kWaves), block(kBlock);
   const int slabs = fused_slabs(a.k, F::C == W8Fmt::C);
   if (slabs <= 1) {
-    hipLaunchKernelGGL((attn_o_halves_kernel<F, 1>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((attn_o_parts_kernel<F, 1, P>), grid, block, 0, stream, a);
   } else if (slabs <= 2) {
-    hipLaunchKernelGGL((attn_o_halves_kernel<F, 2>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((attn_o_parts_kernel<F, 2, P>), grid, block, 0, stream, a);
   } else {
-    hipLaunchKernelGGL((attn_o_halves_kernel<F, 4>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((attn_o_parts_kernel<F, 4, P>), grid, block, 0, stream, a);
   }
 }
 
-void launch_attn_o_halves(const AttnOHalvesArgs& a, bool w8, hipStream_t stream) {
-  if (w8) {
-    launch_attn_o_halves_fmt<W8Fmt>(a, stream);
+void launch_attn_o_parts(const AttnOPartsArgs& a, bool w8, hipStream_t stream, int parts) {
+  if (parts == 4) {
+    if (w8) {
+      launch_attn_o_parts_fmt<W8Fmt, 4>(a, stream);
+    } else {
+      launch_attn_o_parts_fmt<Bf16Fmt, 4>(a, stream);
+    }
+  } else if (w8) {
+    launch_attn_o_parts_fmt<W8Fmt, 2>(a, stream);
   } else {
-    launch_attn_o_halves_fmt<Bf16Fmt>(a, stream);
+    launch_attn_o_parts_fmt<Bf16Fmt, 2>(a, stream);
   }
 }
 

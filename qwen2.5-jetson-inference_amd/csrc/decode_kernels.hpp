@@ -130,15 +130,16 @@ struct AttnOArgs {
 bool attn_o_supported(int k, int heads, bool w8);
 
 // The fused decode step's o-projection (W8A16 group 64, or BF16) with the
-// merge of the attention's two halves (launch_attention_decode_halves):
+// merge of the attention's P parts (launch_attention_decode_parts; P = 2
+// halves or 4 quarters of S = kAttnWholeMax / P positions):
 //   a[i] = bf16( sum_sp acc_sp[i] e^(m_sp - M) / sum_sp l_sp e^(m_sp - M) ),
-//   M = max_sp m_sp over the halves [0, pos / kAttnHalfSpan],
+//   M = max_sp m_sp over the parts [0, pos / S],
 //   x[row] = bf16(Wo[row] . a + x[row]).
-// Lane l's inputs (16 per 16-byte weight chunk for W8A16, 8 for BF16) come
-// from one head, so it merges them from the two records in registers: no
-// LDS, no barrier.
-struct AttnOHalvesArgs {
-  const float* partial;  // heads x 2 records of kAttnHalfRecord floats
+// Each workgroup merges the k attention outputs once (each thread four of
+// them) into BF16 in LDS, shared by its four waves (one output row each)
+// after one barrier.
+struct AttnOPartsArgs {
+  const float* partial;  // heads x P records of kAttnPartRecord floats
   const int* pos;        // position of the decoded token (device)
   int heads;
   int max_seq;
@@ -149,7 +150,10 @@ struct AttnOHalvesArgs {
   int k;                 // heads x 64
 };
 bool attn_o_halves_supported(int k, bool w8);
-void launch_attn_o_halves(const AttnOHalvesArgs& a, bool w8, hipStream_t stream);
+// parts: 2 (the halves' records) or 4 (quarters', as
+// launch_attention_decode_parts with parts 4 leaves them).
+void launch_attn_o_parts(const AttnOPartsArgs& a, bool w8, hipStream_t stream,
+                         int parts = 2);
 void launch_attn_o_gemv(const AttnOArgs& a, bool w8, hipStream_t stream);
 
 constexpr int kLmHeadMaxSlabs = 8;  // K <= 4096

@@ -146,12 +146,15 @@ int rms_norm_qkv_rope(const uint16_t* input, const uint16_t* norm_weight, float 
   return check_launch(what);
 }
 
-int attention_halves_o_proj(const float* records, const int* position, int num_heads,
-                            int max_sequence_length, const void* weight,
-                            const uint16_t* scales, uint16_t* residual, int out_features,
-                            bool w8, hipStream_t stream, const char* what) {
+int attention_parts_o_proj(const float* records, const int* position, int num_heads,
+                           int max_sequence_length, int num_parts, const void* weight,
+                           const uint16_t* scales, uint16_t* residual, int out_features,
+                           bool w8, hipStream_t stream, const char* what) {
   if (!records || !position || !weight || (w8 && !scales) || !residual) {
     return fail(INFER_HIP_INVALID_ARGUMENT, "%s: null pointer", what);
+  }
+  if (num_parts != 2 && num_parts != 4) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: num_parts %d (2 or 4)", what, num_parts);
   }
   const int in_features = num_heads * 64;
   if (num_heads < 1 || out_features < 1 || max_sequence_length < 1 ||
@@ -166,9 +169,9 @@ int attention_halves_o_proj(const float* records, const int* position, int num_h
     return fail(INFER_HIP_INVALID_ARGUMENT, "%s: records and weight must be 16-byte aligned",
                 what);
   }
-  launch_attn_o_halves({records, position, num_heads, max_sequence_length, weight,
-                        w8 ? scales : nullptr, residual, out_features, in_features},
-                       w8, stream);
+  launch_attn_o_parts({records, position, num_heads, max_sequence_length, weight,
+                       w8 ? scales : nullptr, residual, out_features, in_features},
+                      w8, stream, num_parts);
   return check_launch(what);
 }
 
@@ -239,13 +242,16 @@ extern "C" int infer_hip_rms_norm_gate_up_silu_bf16(
                                "rms_norm_gate_up_silu_bf16");
 }
 
-extern "C" int infer_hip_attention_decode_halves_bf16(
-    const uint16_t* q, const uint16_t* key_cache, const uint16_t* value_cache,
-    const int* position, float* records, int num_heads, int num_kv_heads, int head_dim,
-    int max_sequence_length, hipStream_t stream) {
-  const char* what = "attention_decode_halves_bf16";
+static int attention_decode_parts(const uint16_t* q, const uint16_t* key_cache,
+                                  const uint16_t* value_cache, const int* position,
+                                  float* records, int num_heads, int num_kv_heads, int head_dim,
+                                  int max_sequence_length, int num_parts, hipStream_t stream,
+                                  const char* what) {
   if (!q || !key_cache || !value_cache || !position || !records) {
     return fail(INFER_HIP_INVALID_ARGUMENT, "%s: null pointer", what);
+  }
+  if (num_parts != 2 && num_parts != 4) {
+    return fail(INFER_HIP_INVALID_ARGUMENT, "%s: num_parts %d (2 or 4)", what, num_parts);
   }
   if (num_heads < 1 || num_kv_heads < 1 || num_heads % num_kv_heads != 0) {
     return fail(INFER_HIP_INVALID_ARGUMENT, "%s: %d heads, %d kv heads", what, num_heads,
@@ -261,26 +267,62 @@ extern "C" int infer_hip_attention_decode_halves_bf16(
     return fail(INFER_HIP_INVALID_ARGUMENT, "%s: q, caches and records must be 16-byte aligned",
                 what);
   }
-  launch_attention_decode_halves(q, key_cache, value_cache, position, num_heads, num_kv_heads,
-                                 max_sequence_length, records, stream);
+  launch_attention_decode_parts(q, key_cache, value_cache, position, num_heads, num_kv_heads,
+                                max_sequence_length, records, stream, num_parts);
   return check_launch(what);
+}
+
+extern "C" int infer_hip_attention_decode_halves_bf16(
+    const uint16_t* q, const uint16_t* key_cache, const uint16_t* value_cache,
+    const int* position, float* records, int num_heads, int num_kv_heads, int head_dim,
+    int max_sequence_length, hipStream_t stream) {
+  return attention_decode_parts(q, key_cache, value_cache, position, records, num_heads,
+                                num_kv_heads, head_dim, max_sequence_length, 2, stream,
+                                "attention_decode_halves_bf16");
+}
+
+extern "C" int infer_hip_attention_decode_parts_bf16(
+    const uint16_t* q, const uint16_t* key_cache, const uint16_t* value_cache,
+    const int* position, float* records, int num_heads, int num_kv_heads, int head_dim,
+    int max_sequence_length, int num_parts, hipStream_t stream) {
+  return attention_decode_parts(q, key_cache, value_cache, position, records, num_heads,
+                                num_kv_heads, head_dim, max_sequence_length, num_parts, stream,
+                                "attention_decode_parts_bf16");
 }
 
 extern "C" int infer_hip_attention_halves_o_proj_w8a16(
     const float* records, const int* position, int num_heads, int max_sequence_length,
     const int8_t* weight, const uint16_t* scales, uint16_t* residual, int out_features,
     hipStream_t stream) {
-  return attention_halves_o_proj(records, position, num_heads, max_sequence_length, weight,
-                                 scales, residual, out_features, true, stream,
-                                 "attention_halves_o_proj_w8a16");
+  return attention_parts_o_proj(records, position, num_heads, max_sequence_length, 2, weight,
+                                scales, residual, out_features, true, stream,
+                                "attention_halves_o_proj_w8a16");
 }
 
 extern "C" int infer_hip_attention_halves_o_proj_bf16(
     const float* records, const int* position, int num_heads, int max_sequence_length,
     const uint16_t* weight, uint16_t* residual, int out_features, hipStream_t stream) {
-  return attention_halves_o_proj(records, position, num_heads, max_sequence_length, weight,
-                                 nullptr, residual, out_features, false, stream,
-                                 "attention_halves_o_proj_bf16");
+  return attention_parts_o_proj(records, position, num_heads, max_sequence_length, 2, weight,
+                                nullptr, residual, out_features, false, stream,
+                                "attention_halves_o_proj_bf16");
+}
+
+extern "C" int infer_hip_attention_parts_o_proj_w8a16(
+    const float* records, const int* position, int num_heads, int max_sequence_length,
+    int num_parts, const int8_t* weight, const uint16_t* scales, uint16_t* residual,
+    int out_features, hipStream_t stream) {
+  return attention_parts_o_proj(records, position, num_heads, max_sequence_length, num_parts,
+                                weight, scales, residual, out_features, true, stream,
+                                "attention_parts_o_proj_w8a16");
+}
+
+extern "C" int infer_hip_attention_parts_o_proj_bf16(
+    const float* records, const int* position, int num_heads, int max_sequence_length,
+    int num_parts, const uint16_t* weight, uint16_t* residual, int out_features,
+    hipStream_t stream) {
+  return attention_parts_o_proj(records, position, num_heads, max_sequence_length, num_parts,
+                                weight, nullptr, residual, out_features, false, stream,
+                                "attention_parts_o_proj_bf16");
 }
 
 extern "C" int infer_hip_gemv_w8a16_rows(const int8_t* weight, const uint16_t* scales,

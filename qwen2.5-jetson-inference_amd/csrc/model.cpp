@@ -473,9 +473,9 @@ int enqueue_decode_step(infer_hip_model* m, int only = -1, hipEvent_t* events = 
     }
     run(kKindAttention, [&] {
       if (m->fused_qkv_rope) {
-        launch_attention_decode_halves(m->q, L.key_cache, L.value_cache, &m->state->pos,
-                                       c.num_heads, c.num_kv_heads, m->max_seq,
-                                       m->attn_partial, s);
+        launch_attention_decode_parts(m->q, L.key_cache, L.value_cache, &m->state->pos,
+                                      c.num_heads, c.num_kv_heads, m->max_seq,
+                                      m->attn_partial, s, kDecodeAttnParts);
       } else {
         launch_attention_decode(m->q, m->k, m->v, L.key_cache, L.value_cache, m->rope,
                                 &m->state->pos, c.num_heads, c.num_kv_heads, m->head_dim,
@@ -483,12 +483,12 @@ int enqueue_decode_step(infer_hip_model* m, int only = -1, hipEvent_t* events = 
       }
     });
     // x = bf16(Wo attn + x): attn is merged here from the attention's
-    // partials (the two halves, or the spans of the split form)
+    // partials (the kDecodeAttnParts parts, or the spans of the split form)
     run(kKindAttnO, [&] {
       if (m->fused_qkv_rope) {
-        launch_attn_o_halves({m->attn_partial, &m->state->pos, c.num_heads, m->max_seq, L.o.w,
-                              L.o.s, m->x, hidden, hidden},
-                             m->w8, s);
+        launch_attn_o_parts({m->attn_partial, &m->state->pos, c.num_heads, m->max_seq, L.o.w,
+                             L.o.s, m->x, hidden, hidden},
+                            m->w8, s, kDecodeAttnParts);
       } else {
         launch_attn_o_gemv({m->attn_partial, &m->state->pos, c.num_heads, m->head_dim,
                             attention_span(m->max_seq, m->head_dim),
@@ -538,9 +538,10 @@ double kind_bytes(const infer_hip_model* m, int kind, int ctx, int* launches) {
   auto linear = [&](double n, double k) {
     return n * k * wb + (m->w8 ? 2.0 * n * (k / 64) : 0.0);
   };
-  // the attention's output: the (acc, max, sum) records of the halves or
+  // the attention's output: the (acc, max, sum) records of the parts or
   // of the split form's spans (a record's padding is not counted)
-  const int span = m->fused_qkv_rope ? kAttnHalfSpan : attention_span(m->max_seq, m->head_dim);
+  const int span = m->fused_qkv_rope ? kAttnWholeMax / kDecodeAttnParts
+                                     : attention_span(m->max_seq, m->head_dim);
   const double splits = (ctx + span - 1) / span;
   const double partials = c.num_heads * splits * (hd + 2) * 4;
   const bool fused = m->fused_norm_gemv;
@@ -859,9 +860,10 @@ extern "C" int infer_hip_model_create(const infer_hip_model_config* config,
   const size_t o_lmkey = take(sizeof(unsigned long long));
   const size_t o_rope = take(sizeof(float2) * ms * (head_dim / 2));
   const size_t o_rope_cur = take(sizeof(float2) * (head_dim / 2));
-  // (the fused step's two halves: 2 records of kAttnHalfRecord floats per head)
+  // (the fused step's parts: kDecodeAttnParts records of kAttnPartRecord
+  // floats per head)
   const size_t o_partial = take(sizeof(float) * c.num_heads *
-                                std::max<size_t>(2 * kAttnHalfRecord,
+                                std::max<size_t>(kDecodeAttnParts * kAttnPartRecord,
                                                  static_cast<size_t>(attention_splits(
                                                      max_seq, head_dim)) * (head_dim + 2)));
   const size_t o_attn = take(2 * hidden);

@@ -806,42 +806,43 @@ __global__ __launch_bounds__(kWholeWaves * kWave) void attention_decode_whole_ke
   }
 }
 
-// The whole-context attention in two halves: workgroup (query head h, half
-// sp) takes the positions [sp * kAttnHalfSpan, (sp + 1) * kAttnHalfSpan) of
-// the context, one 64-position tile per wave, all requested at kernel entry,
-// and stores the half's (acc[HD], max, sum) record for the o-projection to
-// merge (partial[(h * 2 + sp) * kAttnHalfRecord]).  A half past the context
-// exits without a
-// record; the merge reads only halves [0, pos / kAttnHalfSpan].  q is
-// rotated and the caches hold the token's row (as the fused q|k|v launch
-// leaves them).  Workgroups: the two halves of kv head g on XCDs 2 g and
-// 2 g + 1, each shared by the kv head's query heads (as
-// whole_attention_head does for one workgroup per head).
-int half_attention_blocks(int heads, int kv_heads) {
-  const int units = 2 * kv_heads;
+// The whole-context attention in P parts (two halves, or four quarters):
+// workgroup (query head h, part sp) takes the positions [sp * S, (sp + 1) *
+// S) of the context, S = kAttnWholeMax / P, one 64-position tile per wave
+// (S / 64 waves), all requested at kernel entry, and stores the part's
+// (acc[HD], max, sum) record for the o-projection to merge
+// (partial[(h * P + sp) * kAttnPartRecord]).  A part past the context exits
+// without a record; the merge reads only parts [0, pos / S].  q is rotated
+// and the caches hold the token's row (as the fused q|k|v launch leaves
+// them).  Workgroups: part sp of kv head g on XCD (P g + sp) mod 8, each
+// shared by the kv head's query heads (as whole_attention_head does for one
+// workgroup per head).
+int part_attention_blocks(int heads, int kv_heads, int parts) {
+  const int units = parts * kv_heads;
   return kXcds * ((units + kXcds - 1) / kXcds) * (heads / kv_heads);
 }
 
-__device__ inline int half_attention_unit(int b, int heads, int kv_heads, int& h) {
+__device__ inline int part_attention_unit(int b, int heads, int kv_heads, int parts, int& h) {
   const int group = heads / kv_heads;
   const int x = b % kXcds, t = b / kXcds;
-  const int u = (t / group) * kXcds + x;  // 2 g + sp
-  h = (u >> 1) * group + t % group;
-  return u < 2 * kv_heads ? u : -1;
+  const int u = (t / group) * kXcds + x;  // P g + sp
+  h = (u / parts) * group + t % group;
+  return u < parts * kv_heads ? u : -1;
 }
 
-__global__ __launch_bounds__(kWholeWaves * kWave) void attention_decode_halves_kernel(
+template <int P>
+__global__ __launch_bounds__(kAttnWholeMax / P / kTile * kWave) void attention_decode_parts_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ key_cache,
     const uint16_t* __restrict__ value_cache, const int* __restrict__ pos_ptr, int heads,
     int kv_heads, int max_seq, float* __restrict__ partial) {
-  constexpr int HD = 64, W = kWholeWaves;
+  constexpr int HD = 64, S = kAttnWholeMax / P, W = S / kTile;
   constexpr int kPieces = HD / 8;            // 16-byte pieces per row (8)
   constexpr int kRowsPer = kWave / kPieces;  // rows per load instruction (8)
-  static_assert(W * kTile == kAttnHalfSpan, "one tile per wave covers a half");
+  static_assert(W * kTile == S, "one tile per wave covers a part");
   int h;
-  const int u = half_attention_unit(blockIdx.x, heads, kv_heads, h);
+  const int u = part_attention_unit(blockIdx.x, heads, kv_heads, P, h);
   if (u < 0) return;
-  const int g = u >> 1, sp = u & 1;
+  const int g = u / P, sp = u % P;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int pc = lane % kPieces, rg = lane / kPieces;
   const size_t head_base = static_cast<size_t>(g) * max_seq * HD;
@@ -852,7 +853,7 @@ __global__ __launch_bounds__(kWholeWaves * kWave) void attention_decode_halves_k
       const_cast<uint16_t*>(key_cache) + head_base, 0, max_seq * HD * 2, 0x00020000);
   const __amdgpu_buffer_rsrc_t vr_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(value_cache) + head_base, 0, max_seq * HD * 2, 0x00020000);
-  const int t0 = sp * kAttnHalfSpan + wave * kTile;
+  const int t0 = sp * S + wave * kTile;
   uint4 kt[kPieces], vt[kPieces];
 #pragma unroll
   for (int j = 0; j < kPieces; ++j) {
@@ -865,7 +866,7 @@ __global__ __launch_bounds__(kWholeWaves * kWave) void attention_decode_halves_k
     vt[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr_rsrc, off, 0, 0));
   }
   const int end = min(*pos_ptr, max_seq - 1) + 1;  // positions [0, end)
-  if (sp * kAttnHalfSpan >= end) return;           // a half past the context
+  if (sp * S >= end) return;                       // a part past the context
   const float scale = 1.0f / sqrtf(static_cast<float>(HD));
   const uint32_t qw[4] = {q_mine.x, q_mine.y, q_mine.z, q_mine.w};
   float m = -INFINITY, l = 0.0f;
@@ -922,7 +923,7 @@ __global__ __launch_bounds__(kWholeWaves * kWave) void attention_decode_halves_k
       ll = fmaf(wl[w], f, ll);
       aa = fmaf(wacc[w][tid], f, aa);
     }
-    float* rec = partial + static_cast<size_t>(h * 2 + sp) * kAttnHalfRecord;
+    float* rec = partial + static_cast<size_t>(h * P + sp) * kAttnPartRecord;
     rec[tid] = aa;
     if (tid == 0) {
       rec[HD] = mm;
@@ -931,13 +932,21 @@ __global__ __launch_bounds__(kWholeWaves * kWave) void attention_decode_halves_k
   }
 }
 
-void launch_attention_decode_halves(const uint16_t* q, const uint16_t* key_cache,
-                                    const uint16_t* value_cache, const int* pos, int heads,
-                                    int kv_heads, int max_seq, float* partial,
-                                    hipStream_t stream) {
-  hipLaunchKernelGGL(attention_decode_halves_kernel, dim3(half_attention_blocks(heads, kv_heads)),
-                     dim3(kWholeWaves * kWave), 0, stream, q, key_cache, value_cache, pos, heads,
-                     kv_heads, max_seq, partial);
+void launch_attention_decode_parts(const uint16_t* q, const uint16_t* key_cache,
+                                   const uint16_t* value_cache, const int* pos, int heads,
+                                   int kv_heads, int max_seq, float* partial,
+                                   hipStream_t stream, int parts) {
+  if (parts == 4) {
+    hipLaunchKernelGGL(attention_decode_parts_kernel<4>,
+                       dim3(part_attention_blocks(heads, kv_heads, 4)),
+                       dim3(kAttnWholeMax / 4 / kTile * kWave), 0, stream, q, key_cache,
+                       value_cache, pos, heads, kv_heads, max_seq, partial);
+  } else {
+    hipLaunchKernelGGL(attention_decode_parts_kernel<2>,
+                       dim3(part_attention_blocks(heads, kv_heads, 2)),
+                       dim3(kAttnWholeMax / 2 / kTile * kWave), 0, stream, q, key_cache,
+                       value_cache, pos, heads, kv_heads, max_seq, partial);
+  }
 }
 
 // ----------------------------------------------------- prefill attention --

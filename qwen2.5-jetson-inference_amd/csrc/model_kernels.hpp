@@ -49,17 +49,29 @@ constexpr int kAttnWholeMax = 1024;
 bool attention_whole(int max_seq, int head_dim);
 
 // The whole-context attention of the fused decode step (rotated q, k and v
-// already in the caches) in two halves of kAttnHalfSpan positions: each
-// (query head, half) workgroup stores an (acc[64], max, sum) record at
-// partial[(head * 2 + half) * kAttnHalfRecord], merged by
-// launch_attn_o_halves.  head_dim 64, max_seq <= kAttnWholeMax.
-constexpr int kAttnHalfSpan = kAttnWholeMax / 2;
-// Floats per (head, half) record: acc[64], max, sum, 2 pad (16-byte aligned).
-constexpr int kAttnHalfRecord = 68;
-void launch_attention_decode_halves(const uint16_t* q, const uint16_t* key_cache,
-                                    const uint16_t* value_cache, const int* pos, int heads,
-                                    int kv_heads, int max_seq, float* partial,
-                                    hipStream_t stream);
+// already in the caches) in P parts of kAttnWholeMax / P positions (P = 2
+// halves or 4 quarters): each (query head, part) workgroup stores an
+// (acc[64], max, sum) record at partial[(head * P + part) *
+// kAttnPartRecord], merged by launch_attn_o_parts; a part past the context
+// stores nothing.  head_dim 64, max_seq <= kAttnWholeMax.
+// Floats per (head, part) record: acc[64], max, sum, 2 pad (16-byte aligned).
+constexpr int kAttnPartRecord = 68;
+void launch_attention_decode_parts(const uint16_t* q, const uint16_t* key_cache,
+                                   const uint16_t* value_cache, const int* pos, int heads,
+                                   int kv_heads, int max_seq, float* partial,
+                                   hipStream_t stream, int parts = 2);
+#ifndef QLIN_ATTN_PARTS
+#define QLIN_ATTN_PARTS 4
+#endif
+// The parts the model's decode step splits the whole-context attention into.
+// Measured at config 4 (Qwen2.5-0.5B W8A16, 24 layers): quarters (56
+// workgroups of 4 waves over the 8 XCDs) take 3.12 us per layer against
+// 3.86 for halves (28 workgroups of 8 waves) and 2.92 for eighths (112
+// workgroups of 2 waves); the o-projection's merge grows with the parts
+// (2.92 us with quarters, 3.47 with eighths), so quarters give the fastest
+// step (2206 tok/s, eighths 2158).
+constexpr int kDecodeAttnParts = QLIN_ATTN_PARTS;
+static_assert(kDecodeAttnParts == 2 || kDecodeAttnParts == 4, "halves or quarters");
 int attention_span(int max_seq, int head_dim);
 int attention_splits(int max_seq, int head_dim);
 // roped: q is already rotated and the token's k and v are in the caches at

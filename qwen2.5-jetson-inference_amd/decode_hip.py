@@ -28,6 +28,9 @@ EXPORTED_SYMBOLS = (
     "infer_hip_attention_decode_halves_bf16",
     "infer_hip_attention_halves_o_proj_w8a16",
     "infer_hip_attention_halves_o_proj_bf16",
+    "infer_hip_attention_decode_parts_bf16",
+    "infer_hip_attention_parts_o_proj_w8a16",
+    "infer_hip_attention_parts_o_proj_bf16",
     "infer_hip_gemv_w8a16_rows",
     "infer_hip_gemv_bf16_rows",
     "infer_hip_attention_decode_spans_bf16",
@@ -90,6 +93,9 @@ def load():
         "infer_hip_attention_decode_halves_bf16": ([p, p, p, p, p, i, i, i, i, p], i),
         "infer_hip_attention_halves_o_proj_w8a16": ([p, p, i, i, p, p, p, i, p], i),
         "infer_hip_attention_halves_o_proj_bf16": ([p, p, i, i, p, p, i, p], i),
+        "infer_hip_attention_decode_parts_bf16": ([p, p, p, p, p, i, i, i, i, i, p], i),
+        "infer_hip_attention_parts_o_proj_w8a16": ([p, p, i, i, i, p, p, p, i, p], i),
+        "infer_hip_attention_parts_o_proj_bf16": ([p, p, i, i, i, p, p, i, p], i),
         "infer_hip_gemv_w8a16_rows": ([p, p, p, p, p, i, i, p], i),
         "infer_hip_gemv_bf16_rows": ([p, p, p, p, i, i, p], i),
         "infer_hip_attention_decode_spans_bf16": ([p, p, p, p, p, i, i, i, i, p], i),
@@ -188,13 +194,14 @@ def attention_decode_bf16(q, key_cache, value_cache, position, output, num_heads
         num_kv_heads, head_dim, max_sequence_length, _stream(stream)))
 
 
-HALF_RECORD = 68  # floats per (head, half) record of the two-halves attention
+PART_RECORD = 68  # floats per (head, part) record of the halves / parts attention
+HALF_RECORD = PART_RECORD
 
 
 def attention_decode_halves_bf16(q, key_cache, value_cache, position, records,
                                  num_heads: int, num_kv_heads: int, head_dim: int,
                                  max_sequence_length: int, stream=None) -> None:
-    """records: float32 [num_heads, 2, HALF_RECORD]."""
+    """records: float32 [num_heads, 2, PART_RECORD]."""
     _check(load().infer_hip_attention_decode_halves_bf16(
         _ptr(q), _ptr(key_cache), _ptr(value_cache), _ptr(position), _ptr(records), num_heads,
         num_kv_heads, head_dim, max_sequence_length, _stream(stream)))
@@ -212,6 +219,31 @@ def attention_halves_o_proj_bf16(records, position, num_heads: int, max_sequence
                                  weight, residual, out_features: int, stream=None) -> None:
     _check(load().infer_hip_attention_halves_o_proj_bf16(
         _ptr(records), _ptr(position), num_heads, max_sequence_length, _ptr(weight),
+        _ptr(residual), out_features, _stream(stream)))
+
+
+def attention_decode_parts_bf16(q, key_cache, value_cache, position, records,
+                                num_heads: int, num_kv_heads: int, head_dim: int,
+                                max_sequence_length: int, num_parts: int, stream=None) -> None:
+    """records: float32 [num_heads, num_parts, PART_RECORD]; num_parts 2 or 4."""
+    _check(load().infer_hip_attention_decode_parts_bf16(
+        _ptr(q), _ptr(key_cache), _ptr(value_cache), _ptr(position), _ptr(records), num_heads,
+        num_kv_heads, head_dim, max_sequence_length, num_parts, _stream(stream)))
+
+
+def attention_parts_o_proj_w8a16(records, position, num_heads: int, max_sequence_length: int,
+                                 num_parts: int, weight, scales, residual, out_features: int,
+                                 stream=None) -> None:
+    _check(load().infer_hip_attention_parts_o_proj_w8a16(
+        _ptr(records), _ptr(position), num_heads, max_sequence_length, num_parts, _ptr(weight),
+        _ptr(scales), _ptr(residual), out_features, _stream(stream)))
+
+
+def attention_parts_o_proj_bf16(records, position, num_heads: int, max_sequence_length: int,
+                                num_parts: int, weight, residual, out_features: int,
+                                stream=None) -> None:
+    _check(load().infer_hip_attention_parts_o_proj_bf16(
+        _ptr(records), _ptr(position), num_heads, max_sequence_length, num_parts, _ptr(weight),
         _ptr(residual), out_features, _stream(stream)))
 
 

@@ -320,6 +320,32 @@ def test_halves_attention_ops_reject_bad_arguments(hip):
     assert g(4096, None, 14, 1024, 4096, 4096, 4096, 896, None) == bad
 
 
+def test_parts_attention_ops_reject_bad_arguments(hip):
+    """The parts forms: num_parts 2 or 4 only, then the halves' checks."""
+    import decode_hip
+    lib = decode_hip.load()
+    bad = hip.INVALID_ARGUMENT
+    err = lambda: lib.infer_hip_last_error().decode()  # noqa: E731
+    f = lib.infer_hip_attention_decode_parts_bf16
+    for parts in (0, 1, 3, 8):
+        assert f(4096, 4096, 4096, 4096, 4096, 14, 2, 64, 1024, parts, None) == bad
+        assert "num_parts" in err()
+    assert f(4096, 4096, 4096, 4096, 4096, 14, 2, 64, 2048, 4, None) == bad  # at most 1024
+    assert f(4096, 4096, 4096, 4096, 4096, 14, 3, 64, 512, 4, None) == bad   # GQA
+    assert f(4096, 4096, 4096, 4096, 4100, 14, 2, 64, 512, 4, None) == bad   # records aligned
+    g = lib.infer_hip_attention_parts_o_proj_w8a16
+    for parts in (1, 3):
+        assert g(4096, 4096, 14, 1024, parts, 4096, 4096, 4096, 896, None) == bad
+        assert "num_parts" in err()
+    assert g(4096, 4096, 65, 1024, 4, 4096, 4096, 4096, 896, None) == bad   # 65 x 64 > 4096
+    assert g(4096, 4096, 14, 1025, 4, 4096, 4096, 4096, 896, None) == bad   # max_seq
+    assert g(4096, 4096, 14, 1024, 4, 4096, None, 4096, 896, None) == bad   # scales
+    o = lib.infer_hip_attention_parts_o_proj_bf16
+    assert o(4096, 4096, 14, 1024, 3, 4096, 4096, 896, None) == bad
+    assert o(4096, 4096, 33, 1024, 4, 4096, 4096, 896, None) == bad         # 33 x 64 > 2048
+    assert o(4096, 4096, 14, 1024, 4, 4104, 4096, 896, None) == bad         # weight aligned
+
+
 def test_attention_spans_rejects_bad_arguments(hip):
     """infer_hip_attention_decode_spans_bf16: shapes, nulls and alignment are
     checked on the host; nothing is launched."""

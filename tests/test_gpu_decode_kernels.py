@@ -589,17 +589,28 @@ def test_attention_decode_bf16_matches_oracle(dec, orc, dev, heads, kvh):
 
 # ------------------------ two-halves attention + merge in the o GEMV --
 
-HALF_POSITIONS = (0, 1, 63, 64, 511, 512, 513, 767, 1022, 1023, 2000)
+HALF_POSITIONS = (0, 1, 63, 64, 255, 256, 257, 511, 512, 513, 767, 768, 769, 1022, 1023, 2000)
 
 
+def run_attention_parts(dec, parts, q, kc, vc, dpos, rec, heads, kvh, hd, max_seq):
+    """The halves operator for 2 parts, the parts operator otherwise."""
+    if parts == 2:
+        dec.attention_decode_halves_bf16(q, kc, vc, dpos, rec, heads, kvh, hd, max_seq)
+    else:
+        dec.attention_decode_parts_bf16(q, kc, vc, dpos, rec, heads, kvh, hd, max_seq, parts)
+
+
+@pytest.mark.parametrize("parts", [2, 4])
 @pytest.mark.parametrize("heads,kvh", [(14, 2), (8, 1), (4, 4)])
-def test_attention_decode_halves_matches_oracle(dec, orc, dev, heads, kvh):
-    """Each half's record against the oracle's attention (cpu_ops.cpp:58-91
+def test_attention_decode_halves_matches_oracle(dec, orc, dev, heads, kvh, parts):
+    """Each part's record against the oracle's attention (cpu_ops.cpp:58-91
     restated): merged on the host in float64 they give the whole context's
-    output; rows past p hold NaN and must not matter, and a half past the
-    context leaves its record untouched."""
+    output; rows past p hold NaN and must not matter, and a part past the
+    context leaves its record untouched (halves: 512 positions each,
+    quarters: 256)."""
     import torch
-    hd, max_seq, R = 64, 1024, dec.HALF_RECORD
+    hd, max_seq, R = 64, 1024, dec.PART_RECORD
+    span = max_seq // parts
     rng = rc.philox(900 + heads)
     q = rc.bf16_normal(rng, (heads * hd,), 0.5)
     kcache = rc.bf16_normal(rng, (kvh, max_seq, hd))
@@ -612,15 +623,14 @@ def test_attention_decode_halves_matches_oracle(dec, orc, dev, heads, kvh):
         exp = np.asarray(orc.attention_decode(rc.bf16_values(q), rc.bf16_values(kcache),
                                               rc.bf16_values(vcache), heads, kvh, hd, p + 1,
                                               max_seq), dtype=np.float64)
-        rec = torch.full((heads, 2, R), float("nan"), dtype=torch.float32, device=dev)
+        rec = torch.full((heads, parts, R), float("nan"), dtype=torch.float32, device=dev)
         dpos = torch.tensor([position], dtype=torch.int32, device=dev)
-        dec.attention_decode_halves_bf16(to_dev(q, dev), to_dev(kc, dev), to_dev(vc, dev),
-                                         dpos, rec, heads, kvh, hd, max_seq)
+        run_attention_parts(dec, parts, to_dev(q, dev), to_dev(kc, dev), to_dev(vc, dev), dpos,
+                            rec, heads, kvh, hd, max_seq)
         r = rec.cpu().numpy().astype(np.float64)
-        used = 1 if p < 512 else 2
+        used = p // span + 1
         assert np.all(np.isfinite(r[:, :used, :hd + 2])), position
-        if used == 1:
-            assert np.all(np.isnan(r[:, 1])), f"position {position}: second half written"
+        assert np.all(np.isnan(r[:, used:])), f"position {position}: a part past p written"
         m = r[:, :used, hd]
         big = m.max(axis=1, keepdims=True)
         e = np.exp(m - big)
@@ -686,40 +696,55 @@ def test_attention_decode_spans_matches_oracle(dec, orc, dev, heads, kvh, hd, ma
             assert np.all(np.abs(got_x - ref) <= bound), (position, float(np.max(np.abs(got_x - ref))))
 
 
+def exact_part_records(rng, heads, parts, pos, max_seq, hd, R):
+    """Records whose merge is exact: every live part has m = 0, the first
+    l = 1 and the others l = 0 (merge weights exactly 1), accumulators in
+    multiples of 1/8; parts past the context hold NaN.  Returns the records
+    and the merged attention."""
+    acc = rng.integers(-1, 2, size=(heads, parts, hd)) / 8.0
+    live = min(pos, max_seq - 1) // (max_seq // parts) + 1
+    part = np.full((heads, parts, R), np.nan, np.float32)
+    part[:, :live, :hd] = acc[:, :live]
+    part[:, :live, hd] = 0.0
+    part[:, :live, hd + 1] = 0.0
+    part[:, 0, hd + 1] = 1.0
+    attn = acc[:, :live].sum(axis=1).reshape(-1)
+    assert np.all(rc.bf16_values(bf16(attn)) == attn)  # exact in BF16 by design
+    return part, attn
+
+
+PART_O_POSITIONS = (0, 1, 255, 256, 511, 512, 513, 767, 768, 1023, 2000)
+
+
+@pytest.mark.parametrize("parts", [2, 4])
 @pytest.mark.parametrize("heads,n", [(14, 896), (2, 130), (64, 65)])
-def test_attention_halves_o_proj_bit_exact(dec, dev, heads, n):
-    """Merge weights exactly 1 (m = 0; l = 1 in the first half, 0 in the
-    second) and accumulators in multiples of 1/8: the merged attention and
-    the o GEMV with power-of-two scales are exact, so the result is compared
-    bit for bit.  Below position 512 the second half's records hold NaN and
-    must not reach the output."""
+def test_attention_halves_o_proj_bit_exact(dec, dev, heads, n, parts):
+    """Merge weights exactly 1 and accumulators in multiples of 1/8
+    (exact_part_records): the merged attention and the o GEMV with
+    power-of-two scales are exact, so the result is compared bit for bit.
+    Parts past the context hold NaN and must not reach the output.  Two
+    parts through the halves operator, four through the parts operator."""
     import torch
-    hd, max_seq, R = 64, 1024, dec.HALF_RECORD
-    rng = rc.philox(950 + heads + n)
+    hd, max_seq, R = 64, 1024, dec.PART_RECORD
+    rng = rc.philox(950 + heads + n + parts)
     k = heads * hd
     wq = w8_rows(rng, n, k)
     s = pow2_scales(n, k, 5)
     deq = wq.astype(np.float64) * np.repeat(rc.bf16_values(s).astype(np.float64), 64, 1)
     dw, ds = to_dev(wq, dev), to_dev(s, dev)
-    acc = rng.integers(-1, 2, size=(heads, 2, hd)) / 8.0
     x0 = rc.bf16_normal(rng, (n,))
-    for pos in (0, 1, 511, 512, 513, 1023, 2000):
-        two = min(pos, max_seq - 1) >= 512
-        part = np.full((heads, 2, R), np.nan, np.float32)
-        part[:, 0, :hd] = acc[:, 0]
-        part[:, 0, hd], part[:, 0, hd + 1] = 0.0, 1.0
-        if two:
-            part[:, 1, :hd] = acc[:, 1]
-            part[:, 1, hd], part[:, 1, hd + 1] = 0.0, 0.0
-        attn = (acc[:, 0] + (acc[:, 1] if two else 0.0)).reshape(-1)
-        assert np.all(rc.bf16_values(bf16(attn)) == attn)  # exact in BF16 by design
+    for pos in PART_O_POSITIONS:
+        part, attn = exact_part_records(rng, heads, parts, pos, max_seq, hd, R)
         terms = deq * attn[None, :]
         assert np.all(np.abs(terms).sum(axis=1) * 2 ** 10 < 2 ** 24), "design not exact"
         exp = rc.bf16_words(terms.sum(axis=1).astype(np.float32) + rc.bf16_values(x0))
         x = to_dev(x0, dev)
         dpos = torch.tensor([pos], dtype=torch.int32, device=dev)
-        dec.attention_halves_o_proj_w8a16(torch.from_numpy(part.reshape(-1)).to(dev), dpos, heads,
-                                          max_seq, dw, ds, x, n)
+        rec = torch.from_numpy(part.reshape(-1)).to(dev)
+        if parts == 2:
+            dec.attention_halves_o_proj_w8a16(rec, dpos, heads, max_seq, dw, ds, x, n)
+        else:
+            dec.attention_parts_o_proj_w8a16(rec, dpos, heads, max_seq, parts, dw, ds, x, n)
         got = words(x)
         bad = np.nonzero(got != exp)[0]
         assert bad.size == 0, f"pos {pos}: {bad.size}/{n} rows differ, first {bad[0]}"
@@ -876,36 +901,31 @@ def test_rms_norm_qkv_rope_bf16(dec, dev, shape):
                                              np.argwhere(~ok2)[:3])
 
 
+@pytest.mark.parametrize("parts", [2, 4])
 @pytest.mark.parametrize("heads,n", [(14, 896), (2, 130), (32, 65)])
-def test_attention_halves_o_proj_bf16_bit_exact(dec, dev, heads, n):
+def test_attention_halves_o_proj_bf16_bit_exact(dec, dev, heads, n, parts):
     """As test_attention_halves_o_proj_bit_exact on a BF16 weight: lane
     chunks of 8 inputs, eight per head, each reading two 16-byte pieces of
-    both records.  32 heads is the format's K limit (2048)."""
+    every part's record.  32 heads is the format's K limit (2048)."""
     import torch
-    hd, max_seq, R = 64, 1024, dec.HALF_RECORD
-    rng = rc.philox(1500 + heads + n)
+    hd, max_seq, R = 64, 1024, dec.PART_RECORD
+    rng = rc.philox(1500 + heads + n + parts)
     k = heads * hd
     w, deq = bf16_rows(rng, n, k)
     dw = to_dev(w, dev)
-    acc = rng.integers(-1, 2, size=(heads, 2, hd)) / 8.0
     x0 = rc.bf16_normal(rng, (n,))
-    for pos in (0, 1, 511, 512, 513, 1023, 2000):
-        two = min(pos, max_seq - 1) >= 512
-        part = np.full((heads, 2, R), np.nan, np.float32)
-        part[:, 0, :hd] = acc[:, 0]
-        part[:, 0, hd], part[:, 0, hd + 1] = 0.0, 1.0
-        if two:
-            part[:, 1, :hd] = acc[:, 1]
-            part[:, 1, hd], part[:, 1, hd + 1] = 0.0, 0.0
-        attn = (acc[:, 0] + (acc[:, 1] if two else 0.0)).reshape(-1)
-        assert np.all(rc.bf16_values(bf16(attn)) == attn)
+    for pos in PART_O_POSITIONS:
+        part, attn = exact_part_records(rng, heads, parts, pos, max_seq, hd, R)
         terms = deq * attn[None, :]
         assert np.all(np.abs(terms).sum(axis=1) * 2 ** 10 < 2 ** 24), "design not exact"
         exp = rc.bf16_words(terms.sum(axis=1).astype(np.float32) + rc.bf16_values(x0))
         x = to_dev(x0, dev)
         dpos = torch.tensor([pos], dtype=torch.int32, device=dev)
-        dec.attention_halves_o_proj_bf16(torch.from_numpy(part.reshape(-1)).to(dev), dpos, heads,
-                                         max_seq, dw, x, n)
+        rec = torch.from_numpy(part.reshape(-1)).to(dev)
+        if parts == 2:
+            dec.attention_halves_o_proj_bf16(rec, dpos, heads, max_seq, dw, x, n)
+        else:
+            dec.attention_parts_o_proj_bf16(rec, dpos, heads, max_seq, parts, dw, x, n)
         got = words(x)
         bad = np.nonzero(got != exp)[0]
         assert bad.size == 0, f"pos {pos}: {bad.size}/{n} rows differ, first {bad[0]}"

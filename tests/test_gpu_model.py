@@ -457,10 +457,10 @@ def test_split_attention_decode_across_eight_spans(orc, dev, cfg, precision, sta
 
 
 def test_whole_context_attention_qwen_shaped(orc, dev):
-    """KV capacity 1024: the attention in two halves of 512 positions (one
-    workgroup per query head and half, merged in the o-projection), up to
-    position 1023 (every wave of both halves busy), with 14 query / 2 KV
-    heads."""
+    """KV capacity 1024: the attention in four quarters of 256 positions
+    (one workgroup per query head and quarter, merged in the o-projection),
+    up to position 1023 (every wave of every quarter busy), with 14 query /
+    2 KV heads."""
     cfg, precision = QWEN_SHAPED, "w8a16"
     t = S.random_model(cfg, precision, seed=17, std=0.05)
     fp32 = S.dequantized_fp32(t, cfg)
