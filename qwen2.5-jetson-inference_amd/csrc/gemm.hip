@@ -146,6 +146,7 @@ struct SplitK {
   int index = 0;
   float* partial = nullptr;  // this tile's parts, parts * tile_floats floats
   int* counter = nullptr;
+  bool xcd_local = false;    // every part of the tile runs on one XCD
 };
 
 // Split-K hand-off; returns true in the workgroup that finishes the tile
@@ -577,15 +578,27 @@ enum WideStamp {
 // resident: a part that gives up leaves its slice to the last arrival.  The
 // last of the parts to leave (ctr[2]) sets ctr[0..2] back to zero for the
 // next launch.  parts <= 32.
+// kLocal (build option QLIN_HANDOFF_L2, on launches whose block map puts
+// every part of a tile on one XCD): the partial tiles go through that XCD's
+// L2 with plain stores and loads — a part's stores have reached the L2 when
+// its wait for them ends, before it counts itself, and the loads after the
+// arrival count miss the CU's L1, which never held those lines — with the
+// counters still agent-scope atomics.
 constexpr int kWideArrivePolls = 1 << 16;
 #ifndef QLIN_HANDOFF_FENCE
 #define QLIN_HANDOFF_FENCE 0
 #endif
+#ifndef QLIN_HANDOFF_L2
+#define QLIN_HANDOFF_L2 0
+#endif
 
+template <bool kLocal>
 __device__ __forceinline__ void wide_split_handoff(const GemmArgs& a, int m0, int n0,
                                                    const SplitK& sp, const uint4* tile_lds,
                                                    unsigned long long* stamp) {
   constexpr int BM = kWideRows, BN = kWideCols, NT = kWideThreads;
+  constexpr bool kFence = !kLocal && QLIN_HANDOFF_FENCE;
+  constexpr int kPolicy = kLocal || QLIN_HANDOFF_FENCE ? 0 : kCoherent;
   constexpr int kChunksPerRow = BN / 8;
   constexpr uint32_t kTileBytes = BM * BN * 4;
   __shared__ int shared_word;
@@ -601,15 +614,13 @@ __device__ __forceinline__ void wide_split_handoff(const GemmArgs& a, int m0, in
       const int idx = row * (kWideEpStride / 4) + c8 / 4;
       const uint32_t off = mine + static_cast<uint32_t>(row * BN + c8) * 4u;
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, tile_lds[idx]), pr, off, 0,
-                                             QLIN_HANDOFF_FENCE ? 0 : kCoherent);
+                                             kPolicy);
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, tile_lds[idx + 1]), pr,
-                                             off + 16u, 0, QLIN_HANDOFF_FENCE ? 0 : kCoherent);
+                                             off + 16u, 0, kPolicy);
     }
   }
   __builtin_amdgcn_s_waitcnt(0);  // this thread's part is stored
-#if QLIN_HANDOFF_FENCE
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-#endif
+  if constexpr (kFence) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
   __syncthreads();
   int* ctr = sp.counter;
   if (stamp && tid == 0) stamp[kStampStored] = __builtin_amdgcn_s_memrealtime();
@@ -631,9 +642,7 @@ __device__ __forceinline__ void wide_split_handoff(const GemmArgs& a, int m0, in
   }
   __syncthreads();
   const int state = shared_word;
-#if QLIN_HANDOFF_FENCE
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-#endif
+  if constexpr (kFence) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   if (stamp && tid == 0) stamp[kStampArrived] = __builtin_amdgcn_s_memrealtime();
   const int rows = (BM + sp.parts - 1) / sp.parts;
   const bool vec = (a.n % 8) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15u) == 0;
@@ -663,10 +672,8 @@ __device__ __forceinline__ void wide_split_handoff(const GemmArgs& a, int m0, in
         for (int q = 0; q < kBatch; ++q) {
           if (p0 + q < sp.parts) {
             const uint32_t po = static_cast<uint32_t>(p0 + q) * kTileBytes + off;
-            v[q][0] = __builtin_amdgcn_raw_buffer_load_b128(pr, po, 0,
-                                                            QLIN_HANDOFF_FENCE ? 0 : kCoherent);
-            v[q][1] = __builtin_amdgcn_raw_buffer_load_b128(pr, po + 16u, 0,
-                                                            QLIN_HANDOFF_FENCE ? 0 : kCoherent);
+            v[q][0] = __builtin_amdgcn_raw_buffer_load_b128(pr, po, 0, kPolicy);
+            v[q][1] = __builtin_amdgcn_raw_buffer_load_b128(pr, po + 16u, 0, kPolicy);
           }
         }
 #pragma unroll
@@ -986,7 +993,11 @@ __device__ __forceinline__ void gemm_wide_tile(const GemmArgs& a, int m0, int n0
   }
 #if QLIN_WIDE_INKERNEL
   if (split.parts > 1) {
-    wide_split_handoff(a, m0, n0, split, lds_raw, stamp);
+    if (split.xcd_local) {
+      wide_split_handoff<true>(a, m0, n0, split, lds_raw, stamp);
+    } else {
+      wide_split_handoff<false>(a, m0, n0, split, lds_raw, stamp);
+    }
     return;
   }
 #endif
@@ -1057,7 +1068,7 @@ __global__ __launch_bounds__(kWideThreads) void gemm_wide_kernel(GemmArgs a) {
 // Grouped form of gemm_wide_kernel (same block -> unit mapping as
 // gemm_grouped_kernel: part u % splits of tile u / splits, M tiles fastest).
 template <bool W8>
-__device__ __forceinline__ void gemm_wide_unit(const GemmGroupDesc& d, int u,
+__device__ __forceinline__ void gemm_wide_unit(const GemmGroupDesc& d, int u, bool xcd_local,
                                                unsigned long long* stamp = nullptr) {
   const int tile = u / d.splits;
   if (d.w2) {
@@ -1077,6 +1088,7 @@ __device__ __forceinline__ void gemm_wide_unit(const GemmGroupDesc& d, int u,
     sp.count = min(d.split_stages, groups - sp.begin);
     sp.partial = d.partial + static_cast<size_t>(tile) * d.splits * (kWideRows * kWideCols);
     sp.counter = d.counters ? d.counters + static_cast<size_t>(tile) * kWideSplitCounterInts : nullptr;
+    sp.xcd_local = QLIN_HANDOFF_L2 && xcd_local;
   }
   gemm_wide_tile<W8>(a, (tile % d.tiles_m) * kWideRows, (tile / d.tiles_m) * kWideCols, sp,
                      WidePair{}, stamp);
@@ -1091,7 +1103,7 @@ __global__ __launch_bounds__(kWideThreads) void gemm_wide_grouped_kernel(
     const int mid = (lo + hi + 1) >> 1;
     if (descs[mid].block_begin <= b) lo = mid; else hi = mid - 1;
   }
-  gemm_wide_unit<W8>(descs[lo], b - descs[lo].block_begin);
+  gemm_wide_unit<W8>(descs[lo], b - descs[lo].block_begin, map.mapped != 0);
 }
 
 // gemm_wide_grouped_kernel with a timeline: workgroup w writes the
@@ -1099,7 +1111,7 @@ __global__ __launch_bounds__(kWideThreads) void gemm_wide_grouped_kernel(
 // stores and barrier at the end are its only extra work).  t0 and c0 are
 // the clocks read at the kernel's first instruction.
 template <bool W8>
-__device__ __forceinline__ void wide_timeline_unit(const GemmGroupDesc& d, int b,
+__device__ __forceinline__ void wide_timeline_unit(const GemmGroupDesc& d, int b, bool xcd_local,
                                                    unsigned long long t0, unsigned long long c0,
                                                    unsigned long long* __restrict__ stamps) {
   unsigned long long* stamp = stamps + static_cast<size_t>(blockIdx.x) * kStampSlots;
@@ -1119,7 +1131,7 @@ __device__ __forceinline__ void wide_timeline_unit(const GemmGroupDesc& d, int b
                         (static_cast<unsigned long long>(stages) << 16) |
                         (static_cast<unsigned long long>(kind) << 24);
   }
-  gemm_wide_unit<W8>(d, u, stamp);
+  gemm_wide_unit<W8>(d, u, xcd_local, stamp);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -1140,7 +1152,7 @@ __global__ __launch_bounds__(kWideThreads) void gemm_wide_grouped_timeline_kerne
     const int mid = (lo + hi + 1) >> 1;
     if (descs[mid].block_begin <= b) lo = mid; else hi = mid - 1;
   }
-  wide_timeline_unit<W8>(descs[lo], b, t0, c0, stamps);
+  wide_timeline_unit<W8>(descs[lo], b, map.mapped != 0, t0, c0, stamps);
 }
 
 template <bool W8>
@@ -1154,7 +1166,7 @@ __global__ __launch_bounds__(kWideThreads) void gemm_wide_inline_timeline_kernel
   for (int i = 1; i < kInlineGroupMax; ++i) {
     if (i < g.count && g.d[i].block_begin <= b) lo = i;
   }
-  wide_timeline_unit<W8>(g.d[lo], b, t0, c0, stamps);
+  wide_timeline_unit<W8>(g.d[lo], b, map.mapped != 0, t0, c0, stamps);
 }
 
 // The same with the descriptors in the kernel arguments.
@@ -1167,7 +1179,7 @@ __global__ __launch_bounds__(kWideThreads) void gemm_wide_inline_kernel(GemmGrou
   for (int i = 1; i < kInlineGroupMax; ++i) {
     if (i < g.count && g.d[i].block_begin <= b) lo = i;
   }
-  gemm_wide_unit<W8>(g.d[lo], b - g.d[lo].block_begin);
+  gemm_wide_unit<W8>(g.d[lo], b - g.d[lo].block_begin, map.mapped != 0);
 }
 
 // Split-K reduction, the second launch of a wide-tile plan: each block sums

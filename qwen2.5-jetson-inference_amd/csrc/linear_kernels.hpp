@@ -172,7 +172,9 @@ constexpr int kSplitReduceRows = 16;  // rows of a tile per reduction block
 // QLIN_WIDE_INKERNEL=1 sums a wide split tile's parts inside the GEMM launch
 // (gemm.hip, wide_split_handoff) instead of in the reduction launch, with
 // device-coherent (sc1) partial stores and loads, or with QLIN_HANDOFF_FENCE=1
-// with plain accesses between agent-scope release and acquire fences.
+// with plain accesses between agent-scope release and acquire fences, or
+// with QLIN_HANDOFF_L2=1 (launches whose map keeps a tile's parts on one
+// XCD) with plain accesses through that XCD's L2.
 // QLIN_XCD_MAP=0 places workgroups in logical order.
 #ifndef QLIN_XCD_MAP
 #define QLIN_XCD_MAP 1
