@@ -485,6 +485,58 @@ def committed_traffic(path: str, key: str):
         return json.load(f).get(key)
 
 
+def prefill_cpu_baseline(pl, m: int, w8: bool, seconds: float, gpu_us: float) -> dict:
+    """The reference's CPU FP32 prefill GEMMs (cpu_ops.cpp:108-123
+    linear_fp32_batch, the oracle's C/OpenMP restatement) on the host cores,
+    on the first layer's dequantised weights and inputs of this line: the 7
+    GEMMs timed for about `seconds` (at least 3 layers); mean/p50/p95 per
+    layer, TFLOP/s of the mean.  The GPU's BF16 outputs of the same layer
+    (one plan launch) are compared with the CPU's FP32 ones."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import torch
+    import oracle  # test infrastructure: the CPU baseline leg only
+    oracle.build()
+    threads = cpu_threads()
+    host = []
+    for c in pl.calls[0]:
+        if w8:
+            qn = c[0].cpu().numpy()
+            sn = c[1].view(torch.int16).cpu().numpy().view(np.uint16)
+            w = oracle.dequant_w8a16(qn, sn, 64, threads)
+            x = c[4].float().cpu().numpy()
+        else:
+            w = c[0].float().cpu().numpy()
+            x = c[2].float().cpu().numpy()
+        host.append((w, x))
+    outs = [None] * len(host)
+
+    def layer():
+        for i, (w, x) in enumerate(host):
+            outs[i] = oracle.linear_fp32_batch(w, None, x, threads)
+    t = repeat_for(layer, seconds)
+    ms = stats_of([v * 1e3 for v in t])
+    pl.plans[0].launch()
+    torch.cuda.synchronize()
+    worst = 0.0
+    for c, ref in zip(pl.calls[0], outs):
+        got = (c[5] if w8 else c[3]).float().cpu().numpy()
+        scale = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2))) or 1.0
+        worst = max(worst, float(np.max(np.abs(got - ref))) / scale)
+    tflops = pl.flops_per_layer / (ms["mean"] * 1e-3) / 1e12
+    return {
+        "value": round(tflops, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+        "cpu_model": cpu_model(),
+        "blas": "none: the oracle's own FP32 loops (OpenMP), no BLAS library",
+        "sample": (f"{len(t)} layers of the 7 GEMMs at M={m} (layer 0's dequantised FP32 weights "
+                   f"and inputs) in {sum(t):.1f} s; C/OpenMP restatement of cpu_ops.cpp "
+                   f"linear_fp32_batch"),
+        "ms_per_layer": ms, "gpu_us_same_work": round(gpu_us, 2),
+        "gpu_speedup": round(ms["mean"] * 1e3 / gpu_us, 1),
+        "gpu_max_abs_err_over_rms": round(worst, 5),
+    }
+
+
 def prefill_main(args, dev, hip) -> int:
     """Config 3: prefill GEMMs at M = --tokens.  One step = one layer's 7
     Linears as one grouped launch (value = GEMM TFLOP/s, i.e. the layer's
@@ -548,7 +600,8 @@ def prefill_main(args, dev, hip) -> int:
             "avg_launch_us": round(ms * 1e3, 2),
             "per_shape_single_calls": per_shape,
         },
-        "cpu_baseline": None,
+        "cpu_baseline": (prefill_cpu_baseline(pl, m, w8, args.cpu_seconds, ms * 1e3)
+                         if args.cpu_seconds > 0 else None),
     }
     if m == 512 and w8:
         line["roofline"]["traffic"] = committed_traffic(args.traffic, "gemm_wide_plan_w8a16_M512")

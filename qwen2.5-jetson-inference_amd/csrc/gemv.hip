@@ -462,27 +462,31 @@ __global__ __launch_bounds__(kBlock) void bf16_gemv_splitk_kernel(Bf16GemvArgs a
 }
 
 // Second argmax stage: one block of 1024 threads folds the per-block
-// winners, four independent loads in flight per thread.  A block whose rows
-// were all NaN reports INT_MAX; if every block does, the result is 0, which
-// is what std::max_element returns for an all-NaN range.
+// winners, kReduceBatch independent loads in flight per thread (the LM head
+// of V = 151936 has 9,496 winners: one round of loads instead of three with
+// four; the comparison is a total order, so the order of folding does not
+// change the result).  A block whose rows were all NaN reports INT_MAX; if
+// every block does, the result is 0, which is what std::max_element returns
+// for an all-NaN range.
 constexpr int kReduceThreads = 1024;
+constexpr int kReduceBatch = 16;
 
 __global__ __launch_bounds__(kReduceThreads) void argmax_reduce_kernel(
     const float* __restrict__ block_value, const int* __restrict__ block_index,
     int count, int* __restrict__ argmax) {
   float v = -INFINITY;
   int i = INT_MAX;
-  for (int b = threadIdx.x; b < count; b += 4 * kReduceThreads) {
-    float cv[4];
-    int ci[4];
+  for (int b = threadIdx.x; b < count; b += kReduceBatch * kReduceThreads) {
+    float cv[kReduceBatch];
+    int ci[kReduceBatch];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < kReduceBatch; ++u) {
       const int at = b + u * kReduceThreads;
       cv[u] = at < count ? block_value[at] : -INFINITY;
       ci[u] = at < count ? block_index[at] : INT_MAX;
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < kReduceBatch; ++u) {
       if (better(cv[u], ci[u], v, i)) {
         v = cv[u];
         i = ci[u];
