@@ -363,7 +363,17 @@ def wide_timeline(plans, launches: int = 12) -> dict:
                 "end_us": float(np.median(end[sel] - t0) * us),
                 "end_max_us": float((end[sel] - t0).max() * us),
             }
-            if kname == "split_part" and np.any(a[sel, 8] != 0):
+            if np.any(a[sel, 11] != 0):
+                # the in-launch reduction by the XCD's workgroups: own unit
+                # done -> first slice's parts arrived -> slices summed -> end
+                hp = a[sel, 11].astype(np.float64)
+                ar = np.where(a[sel, 9] != 0, a[sel, 9], a[sel, 11]).astype(np.float64)
+                rd = a[sel, 10].astype(np.float64)
+                res[kname]["help_start_us"] = float(np.median(hp - t0) * us)
+                res[kname]["help_wait_us"] = float(np.median(ar - hp) * us)
+                res[kname]["help_sum_us"] = float(np.median(rd - ar) * us)
+                res[kname]["help_leave_us"] = float(np.median(end[sel] - rd) * us)
+            elif kname == "split_part" and np.any(a[sel, 8] != 0):
                 # the in-launch hand-off: partial stored, all parts arrived,
                 # slices summed
                 st, ar, rd = (a[sel, j].astype(np.float64) for j in (8, 9, 10))

@@ -147,6 +147,7 @@ struct SplitK {
   float* partial = nullptr;  // this tile's parts, parts * tile_floats floats
   int* counter = nullptr;
   bool xcd_local = false;    // every part of the tile runs on one XCD
+  bool help = false;         // the launch's own workgroups sum the parts
 };
 
 // Split-K hand-off; returns true in the workgroup that finishes the tile
@@ -560,6 +561,7 @@ enum WideStamp {
   kStampStored = 8,     // split part: its FP32 tile stored (in-launch hand-off)
   kStampArrived = 9,    // split part: every part has arrived (or the wait ended)
   kStampReduced = 10,   // split part: its slices summed and stored
+  kStampHelp = 11,      // own unit done, the in-launch reduction (map.help) begins
   kStampSlots = 16
 };
 
@@ -1004,9 +1006,23 @@ __device__ __forceinline__ void gemm_wide_tile(const GemmArgs& a, int m0, int n0
   if (split.parts > 1) {
     // One part of a tile split over K: its FP32 tile, row-major, for the
     // plan's reduction launch (the launch boundary orders these stores
-    // before its loads).
+    // before its loads) or, with split.help, for the workgroups of this
+    // XCD (plain stores, kept in the XCD's L2; each thread waits for its
+    // stores before wide_split_help counts the part).
     float* dst = split.partial + static_cast<size_t>(split.index) * (BM * BN);
     const int c8 = (tid % kChunksPerRow) * 8;
+    if (split.help) {
+#pragma unroll
+      for (int i = 0; i < kChunks; ++i) {
+        const int row = (tid + NT * i) / kChunksPerRow;
+        const int idx = row * (kWideEpStride / 4) + c8 / 4;
+        *(QLIN_GLOBAL u32x4*)(dst + row * BN + c8) = __builtin_bit_cast(u32x4, lds_raw[idx]);
+        *(QLIN_GLOBAL u32x4*)(dst + row * BN + c8 + 4) =
+            __builtin_bit_cast(u32x4, lds_raw[idx + 1]);
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < kChunks; ++i) {
       const int row = (tid + NT * i) / kChunksPerRow;
@@ -1065,11 +1081,218 @@ __global__ __launch_bounds__(kWideThreads) void gemm_wide_kernel(GemmArgs a) {
   gemm_wide_tile<W8>(a, blockIdx.y * kWideRows, blockIdx.x * kWideCols);
 }
 
+// Row `row`, columns col .. col + 7 of a wide split tile summed over its
+// `parts` FP32 parts (tile_partial: parts x 256 x 128 floats, row-major) in
+// index order, plus the bias, written as BF16 to y[m, n .. n + 7] (y has N
+// columns; m, n the row's and column's place in Y).  The one arithmetic of
+// every wide split-K reduction, whichever workgroup runs it.
+__device__ __forceinline__ void splitk_sum8(const float* tile_partial, int parts, int row,
+                                            int col, const uint16_t* bias, uint16_t* y, int N,
+                                            int m, int n) {
+  const float* src = tile_partial + row * kWideCols + col;
+  // parts in batches of four: a batch's loads are all issued before its adds
+  constexpr int kBatch = 4;
+  float f[8];
+  for (int p0 = 0; p0 < parts; p0 += kBatch) {
+    u32x4 v[kBatch][2];
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      if (p0 + q < parts) {
+        const float* sp = src + static_cast<size_t>(p0 + q) * (kWideRows * kWideCols);
+        v[q][0] = *(const QLIN_GLOBAL u32x4*)(sp);
+        v[q][1] = *(const QLIN_GLOBAL u32x4*)(sp + 4);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      if (p0 + q < parts) {
+        const float g[8] = {__uint_as_float(v[q][0].x), __uint_as_float(v[q][0].y),
+                            __uint_as_float(v[q][0].z), __uint_as_float(v[q][0].w),
+                            __uint_as_float(v[q][1].x), __uint_as_float(v[q][1].y),
+                            __uint_as_float(v[q][1].z), __uint_as_float(v[q][1].w)};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f[j] = (p0 + q) == 0 ? g[j] : f[j] + g[j];
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if (bias && n + j < N) f[j] += bf16_to_f32(gload(bias + n + j));
+  }
+  uint16_t* dst = y + static_cast<size_t>(m) * N + n;
+  if ((N % 8) == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0) {
+    store_nt16(dst, u32x4{pack2_bf16(f[0], f[1]), pack2_bf16(f[2], f[3]), pack2_bf16(f[4], f[5]),
+                          pack2_bf16(f[6], f[7])});
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (n + j < N) gstore(dst + j, f32_to_bf16(f[j]));
+    }
+  }
+}
+
+// The in-launch reduction of a mapped launch's split tiles (map.help): the
+// workgroups of XCD x (workgroup b runs on XCD b mod 8; the map keeps each
+// split tile's parts on one XCD) sum the slices of that XCD's split tiles
+// once their own units are done.  Slices (tile k of the XCD's list, slice s
+// of kHelpSliceRows rows) are dealt round robin to the XCD's whole-tile
+// workgroups by their rank in the map (to every workgroup of the XCD, by
+// rank b / 8, if it has none), so no slice is claimed at run time.  Per tile (one 128-byte
+// line ctr): a part adds 1 to ctr[0] once its FP32 tile is stored; a
+// workgroup with a slice of the tile waits, a bounded number of polls, for
+// every part and sums the slice (splitk_sum8: parts in index order, the
+// reduction launch's arithmetic).  A workgroup that gives up waiting sets
+// its slice's bit in ctr[3] and then adds kHelpAbandon to ctr[0]; if that
+// add finds every part arrived it sums the slice after all.  The part whose
+// add completes the count is the last: if the count it found holds an
+// abandonment, it sums every slice marked in ctr[3].  The adds on ctr[0]
+// are ordered, so each abandoned slice is summed by its workgroup or by the
+// last part (some maybe by both, writing the same bytes), and nobody waits
+// without bound.  Every workgroup of the XCD counts its departure from each
+// of the XCD's tiles on ctr[2]; the last sets the tile's counters back to
+// zero for the next launch.  The partial tiles are written and read with
+// plain stores and loads inside the XCD's L2 (no reader has held those lines
+// in its L1 this launch).
+constexpr int kHelpSliceRows = 32;
+constexpr int kHelpSlices = kWideRows / kHelpSliceRows;  // the bits of ctr[3]
+constexpr int kHelpAbandon = 1 << 16;                      // > parts, x 256 fits an int
+
+__device__ __forceinline__ int help_arrived(int* ctr) {
+  return __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) % kHelpAbandon;
+}
+
+// Descriptor and tile of the launch's split tile T (numbered over the split
+// descriptors in order); false if T is not one of them.
+template <class DescAt>
+__device__ __forceinline__ bool help_locate(DescAt desc_at, int count, int T, int* di, int* t) {
+  int base = 0;
+  for (int i = 0; i < count; ++i) {
+    const GemmGroupDesc& e = desc_at(i);
+    if (e.splits <= 1) continue;
+    const int tiles = e.tiles_m * ((e.n + kWideCols - 1) / kWideCols);
+    if (T < base + tiles) {
+      *di = i;
+      *t = T - base;
+      return true;
+    }
+    base += tiles;
+  }
+  return false;
+}
+
+// Slice `slice` of tile t of d, 32 rows x 128 columns, 8 columns a thread.
+__device__ __forceinline__ void help_sum_slice(const GemmGroupDesc& d, int t, int slice) {
+  static_assert(kHelpSliceRows * (kWideCols / 8) == kWideThreads, "one row chunk a thread");
+  const int tid = threadIdx.x;
+  const int row = slice * kHelpSliceRows + tid / (kWideCols / 8);
+  const int col = (tid % (kWideCols / 8)) * 8;
+  const int m = (t % d.tiles_m) * kWideRows + row;
+  const int n = (t / d.tiles_m) * kWideCols + col;
+  if (m < d.m && n < d.n) {
+    splitk_sum8(d.partial + static_cast<size_t>(t) * d.splits * (kWideRows * kWideCols),
+                d.splits, row, col, d.bias, d.y, d.n, m, n);
+  }
+}
+
+template <class DescAt>
+__device__ __forceinline__ void wide_split_help(DescAt desc_at, int count, const WideBlockMap& map,
+                                                int own, unsigned long long* stamp = nullptr) {
+  __shared__ int word;
+  const int tid = threadIdx.x;
+  const int x = static_cast<int>(blockIdx.x) % kXcds;
+  const int members = (static_cast<int>(gridDim.x) - x + kXcds - 1) / kXcds;
+  const int helpers = map.help_members[x];
+  const int rank = helpers > 0 ? map.help_rank[blockIdx.x] : static_cast<int>(blockIdx.x) / kXcds;
+  const int dealt = helpers > 0 ? helpers : members;
+  int tiles = 0;
+  while (tiles < kHelpTiles && map.help_tiles[x][tiles] != 0xFF) ++tiles;
+  __syncthreads();  // a part: every thread's partial stores are done
+  int own_di = 0, own_t = 0;
+  if (own >= 0 && help_locate(desc_at, count, own, &own_di, &own_t)) {
+    const GemmGroupDesc& d = desc_at(own_di);
+    int* ctr = d.counters + static_cast<size_t>(own_t) * kHelpCounterInts;
+    if (tid == 0) {
+      const int before = __hip_atomic_fetch_add(&ctr[0], 1, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+      // last part, after an abandonment: the abandoned slices (0: none)
+      word = before % kHelpAbandon == d.splits - 1 && before >= kHelpAbandon
+                 ? __hip_atomic_load(&ctr[3], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                 : 0;
+    }
+    __syncthreads();
+    const int abandoned = word;
+    for (int slice = 0; slice < kHelpSlices; ++slice) {
+      if (abandoned & (1 << slice)) help_sum_slice(d, own_t, slice);
+    }
+    __syncthreads();  // `word` is free again
+  }
+  // this workgroup's slices
+  bool first = true;
+  for (int j = rank; rank != 0xFF && j < tiles * kHelpSlices; j += dealt) {
+    int di, t;
+    if (!help_locate(desc_at, count, map.help_tiles[x][j / kHelpSlices], &di, &t)) continue;
+    const GemmGroupDesc& d = desc_at(di);
+    int* ctr = d.counters + static_cast<size_t>(t) * kHelpCounterInts;
+    const int slice = j % kHelpSlices;
+    if (tid == 0) {
+      bool arrived = false;
+      for (int poll = 0; poll < kWideArrivePolls && !arrived; ++poll) {
+        arrived = help_arrived(&ctr[0]) >= d.splits;
+        if (!arrived) __builtin_amdgcn_s_sleep(2);
+      }
+      if (!arrived) {  // give the slice to the last part, unless it has come
+        __hip_atomic_fetch_or(&ctr[3], 1 << slice, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);  // the bit is set before the add is counted
+        arrived = __hip_atomic_fetch_add(&ctr[0], kHelpAbandon, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT) % kHelpAbandon >= d.splits;
+      }
+      word = arrived;
+    }
+    __syncthreads();
+    const bool arrived = word != 0;
+    if (stamp && first && tid == 0) stamp[kStampArrived] = __builtin_amdgcn_s_memrealtime();
+    first = false;
+    if (arrived) help_sum_slice(d, t, slice);
+    __syncthreads();  // every thread has read `word`
+  }
+  if (stamp && tid == 0) stamp[kStampReduced] = __builtin_amdgcn_s_memrealtime();
+  // departures (lanes 0 .. tiles - 1 of wave 0, one tile each, all at once):
+  // the last workgroup of the XCD to leave a tile resets its counters
+  if (tid < tiles) {
+    int di, t;
+    if (help_locate(desc_at, count, map.help_tiles[x][tid], &di, &t)) {
+      int* ctr = desc_at(di).counters + static_cast<size_t>(t) * kHelpCounterInts;
+      if (__hip_atomic_fetch_add(&ctr[2], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+          members - 1) {
+        __hip_atomic_store(&ctr[0], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&ctr[2], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&ctr[3], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+}
+
+// The launch-wide number of split tile `u` of descriptor `lo` (split tiles
+// numbered over the launch's split descriptors in order, as
+// map_wide_group_to_xcds numbers them), or -1 for a whole or pair tile.
+template <class DescAt>
+__device__ __forceinline__ int own_split_tile(DescAt desc_at, int lo, int u) {
+  const GemmGroupDesc& d = desc_at(lo);
+  if (d.splits <= 1) return -1;
+  int base = 0;
+  for (int i = 0; i < lo; ++i) {
+    const GemmGroupDesc& e = desc_at(i);
+    if (e.splits > 1) base += e.tiles_m * ((e.n + kWideCols - 1) / kWideCols);
+  }
+  return base + u / d.splits;
+}
+
 // Grouped form of gemm_wide_kernel (same block -> unit mapping as
 // gemm_grouped_kernel: part u % splits of tile u / splits, M tiles fastest).
 template <bool W8>
 __device__ __forceinline__ void gemm_wide_unit(const GemmGroupDesc& d, int u, bool xcd_local,
-                                               unsigned long long* stamp = nullptr) {
+                                               unsigned long long* stamp = nullptr,
+                                               bool help = false) {
   const int tile = u / d.splits;
   if (d.w2) {
     // A gate|up pair: d.n counts both halves; each tile 64 columns of each.
@@ -1089,6 +1312,7 @@ __device__ __forceinline__ void gemm_wide_unit(const GemmGroupDesc& d, int u, bo
     sp.partial = d.partial + static_cast<size_t>(tile) * d.splits * (kWideRows * kWideCols);
     sp.counter = d.counters ? d.counters + static_cast<size_t>(tile) * kWideSplitCounterInts : nullptr;
     sp.xcd_local = QLIN_HANDOFF_L2 && xcd_local;
+    sp.help = help;
   }
   gemm_wide_tile<W8>(a, (tile % d.tiles_m) * kWideRows, (tile / d.tiles_m) * kWideCols, sp,
                      WidePair{}, stamp);
@@ -1103,17 +1327,25 @@ __global__ __launch_bounds__(kWideThreads) void gemm_wide_grouped_kernel(
     const int mid = (lo + hi + 1) >> 1;
     if (descs[mid].block_begin <= b) lo = mid; else hi = mid - 1;
   }
-  gemm_wide_unit<W8>(descs[lo], b - descs[lo].block_begin, map.mapped != 0);
+  gemm_wide_unit<W8>(descs[lo], b - descs[lo].block_begin, map.mapped != 0, nullptr,
+                     QLIN_WIDE_HELP && map.help);
+  if (QLIN_WIDE_HELP && map.help) {
+    auto at = [&](int i) -> const GemmGroupDesc& { return descs[i]; };
+    wide_split_help(at, count, map, own_split_tile(at, lo, b - descs[lo].block_begin));
+  }
 }
 
 // gemm_wide_grouped_kernel with a timeline: workgroup w writes the
 // WideStamp slots stamps[w * kStampSlots ..] (a measurement launch; the
 // stores and barrier at the end are its only extra work).  t0 and c0 are
 // the clocks read at the kernel's first instruction.
-template <bool W8>
-__device__ __forceinline__ void wide_timeline_unit(const GemmGroupDesc& d, int b, bool xcd_local,
+template <bool W8, class DescAt>
+__device__ __forceinline__ void wide_timeline_unit(DescAt desc_at, int count, int lo, int b,
+                                                   const WideBlockMap& map,
                                                    unsigned long long t0, unsigned long long c0,
                                                    unsigned long long* __restrict__ stamps) {
+  const GemmGroupDesc& d = desc_at(lo);
+  const bool xcd_local = map.mapped != 0;
   unsigned long long* stamp = stamps + static_cast<size_t>(blockIdx.x) * kStampSlots;
   const int u = b - d.block_begin;
   const int groups = d.k / kStageK;
@@ -1131,7 +1363,11 @@ __device__ __forceinline__ void wide_timeline_unit(const GemmGroupDesc& d, int b
                         (static_cast<unsigned long long>(stages) << 16) |
                         (static_cast<unsigned long long>(kind) << 24);
   }
-  gemm_wide_unit<W8>(d, u, xcd_local, stamp);
+  gemm_wide_unit<W8>(d, u, xcd_local, stamp, QLIN_WIDE_HELP && map.help);
+  if (QLIN_WIDE_HELP && map.help) {
+    if (threadIdx.x == 0) stamp[kStampHelp] = __builtin_amdgcn_s_memrealtime();
+    wide_split_help(desc_at, count, map, own_split_tile(desc_at, lo, u), stamp);
+  }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -1152,7 +1388,8 @@ __global__ __launch_bounds__(kWideThreads) void gemm_wide_grouped_timeline_kerne
     const int mid = (lo + hi + 1) >> 1;
     if (descs[mid].block_begin <= b) lo = mid; else hi = mid - 1;
   }
-  wide_timeline_unit<W8>(descs[lo], b, map.mapped != 0, t0, c0, stamps);
+  auto at = [&](int i) -> const GemmGroupDesc& { return descs[i]; };
+  wide_timeline_unit<W8>(at, count, lo, b, map, t0, c0, stamps);
 }
 
 template <bool W8>
@@ -1166,7 +1403,8 @@ __global__ __launch_bounds__(kWideThreads) void gemm_wide_inline_timeline_kernel
   for (int i = 1; i < kInlineGroupMax; ++i) {
     if (i < g.count && g.d[i].block_begin <= b) lo = i;
   }
-  wide_timeline_unit<W8>(g.d[lo], b, map.mapped != 0, t0, c0, stamps);
+  auto at = [&](int i) -> const GemmGroupDesc& { return g.d[i]; };
+  wide_timeline_unit<W8>(at, g.count, lo, b, map, t0, c0, stamps);
 }
 
 // The same with the descriptors in the kernel arguments.
@@ -1179,7 +1417,12 @@ __global__ __launch_bounds__(kWideThreads) void gemm_wide_inline_kernel(GemmGrou
   for (int i = 1; i < kInlineGroupMax; ++i) {
     if (i < g.count && g.d[i].block_begin <= b) lo = i;
   }
-  gemm_wide_unit<W8>(g.d[lo], b - g.d[lo].block_begin, map.mapped != 0);
+  gemm_wide_unit<W8>(g.d[lo], b - g.d[lo].block_begin, map.mapped != 0, nullptr,
+                     QLIN_WIDE_HELP && map.help);
+  if (QLIN_WIDE_HELP && map.help) {
+    auto at = [&](int i) -> const GemmGroupDesc& { return g.d[i]; };
+    wide_split_help(at, g.count, map, own_split_tile(at, lo, b - g.d[lo].block_begin));
+  }
 }
 
 // Split-K reduction, the second launch of a wide-tile plan: each block sums
@@ -1195,47 +1438,8 @@ __device__ __forceinline__ void splitk_reduce_block(const SplitReduceDesc& d, in
   const int m = (tile % d.tiles_m) * kWideRows + row;
   const int n = (tile / d.tiles_m) * kWideCols + col;
   if (m >= d.m || n >= d.n) return;
-  const float* src = d.partial + static_cast<size_t>(tile) * d.parts * (kWideRows * kWideCols) +
-                     row * kWideCols + col;
-  // parts in batches of four: a batch's loads are all issued before its adds
-  constexpr int kBatch = 4;
-  float f[8];
-  for (int p0 = 0; p0 < d.parts; p0 += kBatch) {
-    u32x4 v[kBatch][2];
-#pragma unroll
-    for (int q = 0; q < kBatch; ++q) {
-      if (p0 + q < d.parts) {
-        const float* sp = src + static_cast<size_t>(p0 + q) * (kWideRows * kWideCols);
-        v[q][0] = *(const QLIN_GLOBAL u32x4*)(sp);
-        v[q][1] = *(const QLIN_GLOBAL u32x4*)(sp + 4);
-      }
-    }
-#pragma unroll
-    for (int q = 0; q < kBatch; ++q) {
-      if (p0 + q < d.parts) {
-        const float g[8] = {__uint_as_float(v[q][0].x), __uint_as_float(v[q][0].y),
-                            __uint_as_float(v[q][0].z), __uint_as_float(v[q][0].w),
-                            __uint_as_float(v[q][1].x), __uint_as_float(v[q][1].y),
-                            __uint_as_float(v[q][1].z), __uint_as_float(v[q][1].w)};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) f[j] = (p0 + q) == 0 ? g[j] : f[j] + g[j];
-      }
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    if (d.bias && n + j < d.n) f[j] += bf16_to_f32(gload(d.bias + n + j));
-  }
-  uint16_t* dst = d.y + static_cast<size_t>(m) * d.n + n;
-  if ((d.n % 8) == 0 && (reinterpret_cast<uintptr_t>(d.y) & 15u) == 0) {
-    store_nt16(dst, u32x4{pack2_bf16(f[0], f[1]), pack2_bf16(f[2], f[3]), pack2_bf16(f[4], f[5]),
-                          pack2_bf16(f[6], f[7])});
-  } else {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if (n + j < d.n) gstore(dst + j, f32_to_bf16(f[j]));
-    }
-  }
+  splitk_sum8(d.partial + static_cast<size_t>(tile) * d.parts * (kWideRows * kWideCols), d.parts,
+              row, col, d.bias, d.y, d.n, m, n);
 }
 
 // The logical reduction block of workgroup w (-1: none).  Mapped: XCD w % 8,

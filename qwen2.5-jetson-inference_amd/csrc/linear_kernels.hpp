@@ -175,6 +175,9 @@ constexpr int kSplitReduceRows = 16;  // rows of a tile per reduction block
 // with plain accesses between agent-scope release and acquire fences, or
 // with QLIN_HANDOFF_L2=1 (launches whose map keeps a tile's parts on one
 // XCD) with plain accesses through that XCD's L2.
+// QLIN_WIDE_HELP=1: on a mapped launch, every workgroup on an XCD that holds
+// split tiles sums their slices once its own unit is done (gemm.hip,
+// wide_split_help), so no reduction launch runs.
 // QLIN_XCD_MAP=0 places workgroups in logical order.
 #ifndef QLIN_XCD_MAP
 #define QLIN_XCD_MAP 1
@@ -182,14 +185,30 @@ constexpr int kSplitReduceRows = 16;  // rows of a tile per reduction block
 #ifndef QLIN_WIDE_INKERNEL
 #define QLIN_WIDE_INKERNEL 0
 #endif
+#ifndef QLIN_WIDE_HELP
+#define QLIN_WIDE_HELP 0
+#endif
 // The in-launch hand-off: 4 ints of counters per split tile, at most 32 parts.
 constexpr int kWideSplitCounterInts = 4;
 constexpr int kWideMaxParts = 32;
 constexpr int kXcds = 8;
 constexpr int kWideMapBlocks = 256;  // plans with more blocks run unmapped
+// The in-launch reduction by the XCD's workgroups: a 128-byte line of
+// counters per split tile (arrived parts, next slice, departed workgroups),
+// at most kHelpTiles split tiles per XCD.
+constexpr int kHelpCounterInts = 32;
+constexpr int kHelpTiles = 8;
 struct WideBlockMap {
   int mapped = 0;                       // 0: workgroup b runs logical block b
+  int help = 0;                         // 1: the launch sums its split tiles itself
   uint8_t logical[kWideMapBlocks] = {};  // workgroup -> logical block
+  // help: split tiles (numbered over the launch's split descriptors in
+  // order) whose parts run on XCD x, 0xFF: none
+  uint8_t help_tiles[kXcds][kHelpTiles] = {};
+  // help: workgroup -> its rank among the whole-tile workgroups of its XCD
+  // (0xFF: a split part), and their number on each XCD
+  uint8_t help_rank[kWideMapBlocks] = {};
+  uint8_t help_members[kXcds] = {};
 };
 constexpr int kReduceSlots = 16;
 struct ReduceBlockMap {

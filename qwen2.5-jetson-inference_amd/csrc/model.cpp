@@ -300,6 +300,7 @@ void linear_group(const infer_hip_model* m, const GemmItem* items, int count, in
                               &g.reducers);
   if (g.tile == kGemmTile256x128) {
     map_wide_group_to_xcds(g.g.d, count, g.blocks, &g.gmap, &g.rmap, &g.reducers);
+    if (g.gmap.help) g.r.count = 0;  // the GEMM launch sums its split tiles
   }
   launch_gemm_group_inline(g, m->stream);
 }

@@ -199,7 +199,9 @@ int layout_gemm_group(GemmGroupDesc* table, int count, int cus, bool fill, int* 
   // arrival counters per split tile: the 64 x 64 tiles' last-arrival count;
   // the wide tile's in-launch hand-off (or none with a reduction launch)
   const size_t counter_ints =
-      tile != kGemmTile256x128 ? 1 : (QLIN_WIDE_INKERNEL ? kWideSplitCounterInts : 0);
+      tile != kGemmTile256x128
+          ? 1
+          : (QLIN_WIDE_INKERNEL ? kWideSplitCounterInts : (QLIN_WIDE_HELP ? kHelpCounterInts : 0));
   size_t pf = 0, cc = 0;
   for (int i = 0; i < count; ++i) {
     GemmGroupDesc& d = table[i];
@@ -248,6 +250,10 @@ int bind_gemm_group(GemmGroupDesc* table, int count, int tile, float* partial, i
       d.counters = counters + cc;
       cc += tiles * kWideSplitCounterInts;
     } else {
+      if (QLIN_WIDE_HELP) {  // the reduction launch stays for unmapped launches
+        d.counters = counters + cc;
+        cc += tiles * kHelpCounterInts;
+      }
       reduce[rcount++] =
           SplitReduceDesc{d.partial, d.bias, d.y, d.m, d.n, d.tiles_m, d.splits, rblocks};
       rblocks += static_cast<int>(tiles) * (bm / kSplitReduceRows);
@@ -316,6 +322,30 @@ void map_wide_group_to_xcds(const GemmGroupDesc* table, int count, int blocks, W
     }
   }
   gmap->mapped = 1;
+  if (QLIN_WIDE_HELP && !QLIN_WIDE_INKERNEL && slots <= kHelpTiles && tile_id <= 0xFE) {
+    for (int y = 0; y < kXcds; ++y) {
+      for (int k = 0; k < kHelpTiles; ++k) {
+        gmap->help_tiles[y][k] =
+            k < static_cast<int>(tiles_on[y].size()) ? static_cast<uint8_t>(tiles_on[y][k]) : 0xFF;
+      }
+      // the whole-tile workgroups of XCD y sum its split tiles' slices
+      int helpers = 0;
+      for (size_t k = 0; k < on[y].size(); ++k) {
+        const int logical = on[y][k];
+        bool part = false;
+        for (int i = 0; i < count; ++i) {
+          const GemmGroupDesc& d = table[i];
+          const int units = d.tiles_m * ((d.n + kWideColsHost - 1) / kWideColsHost) * d.splits;
+          if (logical >= d.block_begin && logical < d.block_begin + units) part = d.splits > 1;
+        }
+        gmap->help_rank[k * kXcds + y] = part ? 0xFF : static_cast<uint8_t>(helpers++);
+      }
+      gmap->help_members[y] = static_cast<uint8_t>(helpers);
+    }
+    gmap->help = 1;
+    *reducers = 0;
+    return;
+  }
   if (QLIN_WIDE_INKERNEL || slots > kReduceSlots || tile_id > 0xFE) return;  // reduction unmapped
   for (int y = 0; y < kXcds; ++y) {
     for (int k = 0; k < kReduceSlots; ++k) {
@@ -478,6 +508,11 @@ extern "C" int infer_hip_gemm_plan_create(const infer_hip_gemm_desc* descs, int 
   if (st == hipSuccess && tile == kGemmTile256x128) {
     map_wide_group_to_xcds(table.data(), count, blocks, &plan->block_map, &plan->reduce_map,
                            &plan->reduce_blocks);
+    if (plan->block_map.help) {  // the GEMM launch sums its split tiles
+      rcount = 0;
+      reduce.clear();
+      plan->reduce_count = 0;
+    }
     if (count <= kInlineGroupMax) {
       GemmGroupLaunch& l = plan->wide_launch;
       l.tile = tile;
