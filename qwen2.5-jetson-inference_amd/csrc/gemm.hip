@@ -46,6 +46,17 @@ namespace qlin {
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+// A 16-byte LDS read the compiler does not track (the direct-X loop orders
+// its reads itself: an explicit vmcnt wait and barrier before, an explicit
+// lgkmcnt wait before the first use).
+__device__ __forceinline__ bf16x8_t lds_read16_untracked(const uint4* p) {
+  const uint32_t addr = static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) uint4*)p));
+  bf16x8_t v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
@@ -593,6 +604,10 @@ constexpr int kWideArrivePolls = 1 << 16;
 #ifndef QLIN_HANDOFF_L2
 #define QLIN_HANDOFF_L2 0
 #endif
+// X tiles of the wide tile loaded straight into LDS (buffer_load ... lds).
+#ifndef QLIN_WIDE_DIRECT_A
+#define QLIN_WIDE_DIRECT_A 0
+#endif
 
 template <bool kLocal>
 __device__ __forceinline__ void wide_split_handoff(const GemmArgs& a, int m0, int n0,
@@ -738,10 +753,21 @@ __device__ __forceinline__ void gemm_wide_tile(const GemmArgs& a, int m0, int n0
   constexpr int A_LD = BM * kRowChunks / NT;  // X chunks per thread per stage (4)
   constexpr int B_LD = BN * kRowChunks / NT;  // W chunks per thread per stage (2)
   // LDS: the two stage buffers of X and W; after the main loop the same
-  // bytes stage the FP32 tile for the epilogue.
+  // bytes stage the FP32 tile for the epilogue.  With QLIN_WIDE_DIRECT_A the
+  // X rows are unpadded (AS = 8 chunks), chunk c of row R at chunk
+  // c ^ ((R >> 1) & 7): each 16-lane group of a fragment read (16 rows, one
+  // chunk) then covers all 64 banks once.
+#if QLIN_WIDE_DIRECT_A
+  constexpr int AS = kRowChunks;
+  constexpr int ABUFS = 3;  // X loaded two stages ahead
+#else
+  constexpr int AS = RS;
+  constexpr int ABUFS = 2;
+#endif
+  static_assert(ABUFS * BM * AS + 2 * BN * RS <= kWideLdsChunks, "stage buffers fit");
   __shared__ uint4 lds_raw[kWideLdsChunks];
-  uint4 (*lds_a)[BM * RS] = reinterpret_cast<uint4 (*)[BM * RS]>(lds_raw);
-  uint4 (*lds_b)[BN * RS] = reinterpret_cast<uint4 (*)[BN * RS]>(lds_raw + 2 * BM * RS);
+  uint4 (*lds_a)[BM * AS] = reinterpret_cast<uint4 (*)[BM * AS]>(lds_raw);
+  uint4 (*lds_b)[BN * RS] = reinterpret_cast<uint4 (*)[BN * RS]>(lds_raw + ABUFS * BM * AS);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 3, wn = wave >> 2;
@@ -783,8 +809,44 @@ __device__ __forceinline__ void gemm_wide_tile(const GemmArgs& a, int m0, int n0
 #pragma unroll
   for (int fn = 0; fn < 2; ++fn)
     soff[fn] = (static_cast<uint32_t>(col0 + fn * 32 + r) * groups) * 2u;
-  const int fa_base[2] = {(wm * 64 + r) * RS + 4 * h, (wm * 64 + 32 + r) * RS + 4 * h};
   const int fb_base[2] = {(wn * 64 + r) * RS + 4 * h, (wn * 64 + 32 + r) * RS + 4 * h};
+  // X fragment chunk ks of row group fm: row wm * 64 + 32 fm + r, chunk 4 h + ks
+  int fa[2][4];
+#pragma unroll
+  for (int fm = 0; fm < 2; ++fm) {
+    const int row = wm * 64 + 32 * fm + r;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+#if QLIN_WIDE_DIRECT_A
+      fa[fm][ks] = row * AS + ((4 * h + ks) ^ ((row >> 1) & 7));
+#else
+      fa[fm][ks] = row * AS + 4 * h + ks;
+#endif
+    }
+  }
+#if QLIN_WIDE_DIRECT_A
+  // Direct X fill: wave w writes stage-buffer chunks (4 w + i) * 64 + lane,
+  // i < 4 (row R = chunk / 8, the chunk's swizzled place), loading the X
+  // chunk that belongs there; rows past M read zero.
+  uint32_t xdir[A_LD];
+#pragma unroll
+  for (int i = 0; i < A_LD; ++i) {
+    const int slot = (wave * A_LD + i) * 64 + lane;
+    const int row = slot >> 3;
+    const int c = (slot & 7) ^ ((row >> 1) & 7);
+    xdir[i] = ((static_cast<uint32_t>(m0) + row) * a.k + c * 8) * 2u;
+  }
+  auto load_a_direct = [&](int g, int buf) {
+    const uint32_t gc = static_cast<uint32_t>(min(g, stages - 1) + sbeg);
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          xr, (__attribute__((address_space(3))) void*)(&lds_a[buf][(wave * A_LD + i) * 64]), 16,
+          xdir[i], gc * kStageK * 2u, 0, 0);
+    }
+  };
+  static_assert(A_LD * 64 * (NT / 64) == BM * kRowChunks, "one stage of X: A_LD loads a lane");
+#endif
 
   // Global -> register staging, one slot per stage in flight (2).
   struct Slot {
@@ -795,8 +857,10 @@ __device__ __forceinline__ void gemm_wide_tile(const GemmArgs& a, int m0, int n0
   Slot sl[2];
   auto load = [&](int g, Slot& d) {
     const uint32_t gc = static_cast<uint32_t>(min(g, stages - 1) + sbeg);
+#if !QLIN_WIDE_DIRECT_A
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) d.a[i] = buffer_load16(xr, xoff[i], gc * kStageK * 2u);
+#endif
 #pragma unroll
     for (int i = 0; i < B_LD; ++i) {
       if (W8) {
@@ -807,7 +871,14 @@ __device__ __forceinline__ void gemm_wide_tile(const GemmArgs& a, int m0, int n0
     }
   };
   // W8: the group scales of stage g, loaded one stage ahead
-  auto load_scales = [&](int g, uint32_t (&xs)[2]) {
+  // (the direct-X loop keeps scales as loaded, 16 bits, until folded: a
+  // conversion at load time would wait for the X loads issued after them)
+#if QLIN_WIDE_DIRECT_A
+  using ScaleT = uint16_t;
+#else
+  using ScaleT = uint32_t;
+#endif
+  auto load_scales = [&](int g, ScaleT (&xs)[2]) {
     if (W8) {
       const uint32_t gc = static_cast<uint32_t>(min(g, stages - 1) + sbeg);
 #pragma unroll
@@ -817,11 +888,13 @@ __device__ __forceinline__ void gemm_wide_tile(const GemmArgs& a, int m0, int n0
     }
   };
   auto store = [&](int buf, const Slot& d) {
+#if !QLIN_WIDE_DIRECT_A
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) {
       const int c = tid + NT * i;
       lds_a[buf][(c >> 3) * RS + (c & 7)] = d.a[i];
     }
+#endif
 #pragma unroll
     for (int i = 0; i < B_LD; ++i) {
       const int c = tid + NT * i;
@@ -846,27 +919,71 @@ __device__ __forceinline__ void gemm_wide_tile(const GemmArgs& a, int m0, int n0
       c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ks], fb[ks], c, 0, 0, 0);
     }
   };
-  auto fold = [&](f32x16_t& dst, const f32x16_t& p, uint32_t s) {
-    const float sc = bf16_to_f32(s);
+  auto fold = [&](f32x16_t& dst, const f32x16_t& p, ScaleT s) {
+    const float sc = bf16_to_f32(static_cast<uint32_t>(s));
 #pragma unroll
     for (int e = 0; e < 16; ++e) dst[e] = fmaf(p[e], sc, dst[e]);
   };
   // Stage on LDS buffer buf with scales cs; loads stage sg's scales into ns;
   // the store of the next stage (slot sd into buffer nbuf) and the loads of
   // stage lg (into slot sd) ride in the MFMA stream.
-  auto compute = [&](int buf, const uint32_t (&cs)[2], uint32_t (&ns)[2], int sg, bool st,
-                     int nbuf, Slot* sd, bool ld, int lg) {
+  // abuf: the X buffer of this stage; with QLIN_WIDE_DIRECT_A, X of stage
+  // sg + 1 (if dma) goes into X buffer dbuf.
+  auto compute = [&](int buf, const ScaleT (&cs)[2], ScaleT (&ns)[2], int sg, bool st,
+                     int nbuf, Slot* sd, bool ld, int lg, int abuf, bool dma, int dbuf) {
     load_scales(sg, ns);
     Frag A0, A1, B0, B1;
+#if QLIN_WIDE_DIRECT_A
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      A0[ks] = as_bf16x8(lds_a[buf][fa_base[0] + ks]);
+      A0[ks] = lds_read16_untracked(&lds_a[abuf][fa[0][ks]]);
+      B0[ks] = lds_read16_untracked(&lds_b[buf][fb_base[0] + ks]);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) B1[ks] = lds_read16_untracked(&lds_b[buf][fb_base[1] + ks]);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) A1[ks] = lds_read16_untracked(&lds_a[abuf][fa[1][ks]]);
+#else
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      A0[ks] = as_bf16x8(lds_a[abuf][fa[0][ks]]);
       B0[ks] = as_bf16x8(lds_b[buf][fb_base[0] + ks]);
     }
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) B1[ks] = as_bf16x8(lds_b[buf][fb_base[1] + ks]);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) A1[ks] = as_bf16x8(lds_a[buf][fa_base[1] + ks]);
+    for (int ks = 0; ks < 4; ++ks) A1[ks] = as_bf16x8(lds_a[abuf][fa[1][ks]]);
+#endif
+#if QLIN_WIDE_DIRECT_A
+    // W of stage sg into the other W buffer (free since the last barrier),
+    // then X of stage sg + 1 straight into the X buffer read two stages ago,
+    // so no LDS write of this iteration waits behind those loads
+    if (st) store(nbuf, *sd);
+    __builtin_amdgcn_sched_barrier(0);
+    if (dma) load_a_direct(sg + 1, dbuf);
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the fragments are in
+    __builtin_amdgcn_sched_barrier(0);
+    if (W8) {
+      f32x16_t p0, p1, p2, p3;
+      chain(A0, B0, p0, true);
+      chain(A0, B1, p1, true);
+      chain(A1, B0, p2, true);
+      fold(acc[0][0], p0, cs[0]);
+      if (ld) load(lg, *sd);
+      chain(A1, B1, p3, true);
+      fold(acc[0][1], p1, cs[1]);
+      fold(acc[1][0], p2, cs[0]);
+      fold(acc[1][1], p3, cs[1]);
+    } else {
+      chain(A0, B0, acc[0][0], false);
+      chain(A0, B1, acc[0][1], false);
+      chain(A1, B0, acc[1][0], false);
+      if (ld) load(lg, *sd);
+      chain(A1, B1, acc[1][1], false);
+    }
+    return;
+#endif
     if (W8) {
       // four partials, each folded once the next chain is issued: no chain
       // waits for a fold to release its registers (measured: 1.147 -> 1.12-1.13
@@ -898,7 +1015,47 @@ __device__ __forceinline__ void gemm_wide_tile(const GemmArgs& a, int m0, int n0
   // barrier that ended it — and reloads slot g & 1 with stage g + 2.  The
   // main loop is unrolled by two so buffer and slot indices are constants
   // and the vmcnt waits the compiler derives stay partial.
-  uint32_t csa[2] = {0u, 0u}, csb[2] = {0u, 0u};
+  ScaleT csa[2] = {0u, 0u}, csb[2] = {0u, 0u};
+#if QLIN_WIDE_DIRECT_A
+  // vmcnt(n) (expcnt and lgkmcnt left alone) before the barrier that ends
+  // stage s: X of stage s + 1 was loaded during stage s - 1, followed by that
+  // stage's W loads (B_LD) and, in stage s, the scale loads (W8: 2), the X
+  // loads of stage s + 2 (A_LD) and the W loads (B_LD); loads complete in
+  // issue order.  Six stages per round, so that every X and W buffer index
+  // is a constant and the compiler keeps its waits partial.
+  constexpr int kAfter = B_LD + (W8 ? 2 : 0) + A_LD + B_LD;
+  static_assert(kAfter < 16, "vmcnt's low field");
+  load_a_direct(0, 0);
+  if (stages > 1) load_a_direct(1, 1);
+  load_scales(0, csa);
+  load(0, sl[0]);
+  load(1, sl[1]);
+  store(0, sl[0]);
+  load(2, sl[0]);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // the prologue: everything in
+  __syncthreads();
+  if (stamp && tid == 0) stamp[kStampLoop] = __builtin_amdgcn_s_memrealtime();
+  for (int g = 0; g < stages; g += 6) {
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+      const int st_ = g + k;  // this stage
+      if (st_ >= stages) break;
+      const bool next = st_ + 1 < stages;
+      compute(k & 1, (k & 1) ? csb : csa, (k & 1) ? csa : csb, st_ + 1, next, (k + 1) & 1,
+              &sl[(k + 1) & 1], true, st_ + 3, k % 3, st_ + 2 < stages, (k + 2) % 3);
+      if (!next) break;
+      // the next stage's X in and this stage's LDS accesses done, then a
+      // bare barrier (a fence would also wait for the X loads of stage
+      // st_ + 2, not needed before the barrier after the next)
+      if (st_ + 2 < stages) {
+        __builtin_amdgcn_s_waitcnt(0x0070 | kAfter);
+      } else {
+        __builtin_amdgcn_s_waitcnt(0x0070);
+      }
+      asm volatile("s_barrier" ::: "memory");
+    }
+  }
+#else
   load_scales(0, csa);
   load(0, sl[0]);
   load(1, sl[1]);
@@ -908,19 +1065,20 @@ __device__ __forceinline__ void gemm_wide_tile(const GemmArgs& a, int m0, int n0
   if (stamp && tid == 0) stamp[kStampLoop] = __builtin_amdgcn_s_memrealtime();
   int g = 0;
   for (; g + 2 < stages; g += 2) {
-    compute(0, csa, csb, g + 1, true, 1, &sl[1], true, g + 3);
+    compute(0, csa, csb, g + 1, true, 1, &sl[1], true, g + 3, 0, false, 0);
     __syncthreads();
-    compute(1, csb, csa, g + 2, true, 0, &sl[0], true, g + 4);
+    compute(1, csb, csa, g + 2, true, 0, &sl[0], true, g + 4, 1, false, 0);
     __syncthreads();
   }
   {
     const bool more = g + 1 < stages;
-    compute(0, csa, csb, g + 1, more, 1, &sl[1], false, 0);
+    compute(0, csa, csb, g + 1, more, 1, &sl[1], false, 0, 0, false, 0);
     if (more) {
       __syncthreads();
-      compute(1, csb, csa, g + 2, false, 0, &sl[0], false, 0);
+      compute(1, csb, csa, g + 2, false, 0, &sl[0], false, 0, 1, false, 0);
     }
   }
+#endif
 
   // Epilogue through LDS: the FP32 tile is staged row-major (element e of
   // tile (fm, fn) is row 8 (e / 4) + 4 h + e % 4, column r of that tile),

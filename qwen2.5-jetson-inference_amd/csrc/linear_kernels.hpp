@@ -175,6 +175,8 @@ constexpr int kSplitReduceRows = 16;  // rows of a tile per reduction block
 // with plain accesses between agent-scope release and acquire fences, or
 // with QLIN_HANDOFF_L2=1 (launches whose map keeps a tile's parts on one
 // XCD) with plain accesses through that XCD's L2.
+// QLIN_WIDE_DIRECT_A=1 (gemm.hip): the wide tile's X tiles go straight into
+// LDS (buffer_load ... lds, two stages ahead into three swizzled buffers).
 // QLIN_WIDE_HELP=1: on a mapped launch, every workgroup on an XCD that holds
 // split tiles sums their slices once its own unit is done (gemm.hip,
 // wide_split_help), so no reduction launch runs.
