@@ -218,7 +218,10 @@ int infer_hip_attention_decode_halves_bf16(const uint16_t* q, const uint16_t* ke
  *   a[64 h + d] = bf16( sum_sp acc_sp[d] e^(m_sp - M) * (1 / sum_sp l_sp e^(m_sp - M)) ),
  *   residual[n] = bf16(W[n] . a + residual[n]).
  * W8A16 weight [out_features, num_heads * 64] with BF16 group-64 scales;
- * num_heads * 64 <= 4096; a second half outside S is never summed. */
+ * num_heads * 64 <= 4096; a second half outside S is never summed.
+ * *position >= 0: the context holds at least the token's own row (for a
+ * negative position the attention stores no record, and the output is
+ * undefined). */
 int infer_hip_attention_halves_o_proj_w8a16(const float* records, const int* position,
                                             int num_heads, int max_sequence_length,
                                             const int8_t* weight, const uint16_t* scales,
