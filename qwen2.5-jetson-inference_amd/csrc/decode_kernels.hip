@@ -400,7 +400,7 @@ static int fused_slabs(int k, bool w8) {
   return (k + per_slab - 1) / per_slab;
 }
 
-bool attn_o_halves_supported(int k, bool w8) {
+bool attn_o_parts_supported(int k, bool w8) {
   return k >= 64 && k % 64 == 0 && fused_slabs(k, w8) <= 4;
 }
 

@@ -149,7 +149,7 @@ struct AttnOPartsArgs {
   int n;
   int k;                 // heads x 64
 };
-bool attn_o_halves_supported(int k, bool w8);
+bool attn_o_parts_supported(int k, bool w8);
 // parts: 2 (the halves' records) or 4 (quarters', as
 // launch_attention_decode_parts with parts 4 leaves them).
 void launch_attn_o_parts(const AttnOPartsArgs& a, bool w8, hipStream_t stream,

@@ -158,7 +158,7 @@ int attention_parts_o_proj(const float* records, const int* position, int num_he
   }
   const int in_features = num_heads * 64;
   if (num_heads < 1 || out_features < 1 || max_sequence_length < 1 ||
-      max_sequence_length > kAttnWholeMax || !attn_o_halves_supported(in_features, w8)) {
+      max_sequence_length > kAttnWholeMax || !attn_o_parts_supported(in_features, w8)) {
     return fail(INFER_HIP_INVALID_ARGUMENT,
                 "%s: %d heads (in_features %d: multiple of 64, at most %d), %d outputs, "
                 "max_sequence_length %d (at most %d)",

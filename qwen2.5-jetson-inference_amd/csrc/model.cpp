@@ -13,8 +13,10 @@
 //   entry (the previous step's deferred argmax applied to the state, then
 //   the token's embedding row); per layer five launches:
 //     RMSNorm + q|k|v GEMV + RoPE + KV store (norm_qkv_rope),
-//     attention over the context in two halves (partials),
-//     merge of the halves + o GEMV + residual (attn_o_halves),
+//     attention over the context in kDecodeAttnParts parts (quarters:
+//     one (acc, max, sum) record per head and part),
+//     merge of the parts once per workgroup + o GEMV + residual
+//     (attn_o_parts),
 //     RMSNorm + gate|up GEMV + SiLU-mul (norm_gemv, paired rows),
 //     down GEMV + residual (gemv_rows);
 //   final RMSNorm + LM head + argmax (lm_head_decode, the argmax left in
@@ -830,7 +832,7 @@ extern "C" int infer_hip_model_create(const infer_hip_model_config* config,
   m->fused_lm_head = lm_head_decode_supported(hidden);
   m->fused_qkv_rope = m->fused_norm_gemv && attention_whole(max_seq, head_dim) &&
                       norm_qkv_rope_supported(hidden, head_dim, w8) &&
-                      attn_o_halves_supported(hidden, w8);
+                      attn_o_parts_supported(hidden, w8);
   // The unfused step runs the split attention, which needs head_dim 128 or
   // more than kAttnWholeMax positions; head_dim 64 means at most 32 x 64 =
   // 2048 hidden, always within the fused launches' limits.
