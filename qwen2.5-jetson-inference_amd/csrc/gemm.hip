@@ -270,7 +270,8 @@ struct TileShape {
 // last reader of that buffer.
 template <int BM, int BN, int WAVES_M, bool W8, int D>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int m0, int n0,
-                                          const SplitK& split = SplitK{}) {
+                                          const SplitK& split = SplitK{},
+                                          const GemmGroupDesc* epi = nullptr) {
   using S = TileShape<BM, BN, WAVES_M, W8>;
   constexpr int FM = S::FM, FN = S::FN;
   __shared__ uint4 lds_a[2][BM * kRowChunks];
@@ -475,6 +476,65 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int m0, int n0,
   }
 
   if (split.parts > 1 && !splitk_fixup<FM, FN>(acc, split)) return;
+
+  if constexpr (BM == 64 && BN == 64) {
+    if (epi && epi->rope_kind != 0) {
+      // The q|k|v epilogue (GemmGroupDesc::rope_kind): the tile's BF16 rows
+      // staged as floats in the stage buffers, then each thread one row's
+      // 8 rotation pairs (or 16 values of v), the arithmetic of
+      // rope_store_rows_kernel on the same BF16 values.
+      float* ep = reinterpret_cast<float*>(&lds_a[0][0]);  // 64 x 64 floats
+      static_assert(sizeof(lds_a) == 64 * 64 * sizeof(float), "the staged tile fits");
+      __syncthreads();  // every wave's last fragment reads are done
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+        const int cl = wn * S::TN + fn * 32 + r;
+        const int n = n0 + cl;
+        const float b = a.bias && n < a.n ? bf16_to_f32(gload(a.bias + n)) : 0.0f;
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int rl = wm * S::TM + fm * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+            ep[rl * 64 + cl] = bf16_to_f32(f32_to_bf16(acc[fm][fn][e] + b));
+          }
+        }
+      }
+      __syncthreads();
+      const int rl = tid >> 2, m = m0 + rl, pos = epi->rope_start + m;
+      if (m >= a.m || pos >= epi->max_seq || n0 + 64 > a.n) return;
+      const float* er = ep + rl * 64;
+      uint16_t* cache_row =
+          epi->kv_cache ? epi->kv_cache + (static_cast<size_t>(n0 / 64) * epi->max_seq + pos) * 64
+                        : nullptr;
+      if (epi->rope_kind == 3) {
+        const int c0 = (tid & 3) * 16;
+        uint32_t w[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) w[j] = pack2_bf16(er[c0 + 2 * j], er[c0 + 2 * j + 1]);
+        store_global16(cache_row + c0, make_uint4(w[0], w[1], w[2], w[3]));
+        store_global16(cache_row + c0 + 8, make_uint4(w[4], w[5], w[6], w[7]));
+        return;
+      }
+      const int c0 = (tid & 3) * 8;
+      const float2* cs = epi->rope + static_cast<size_t>(pos) * 32 + c0;
+      float lo[8], hi[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        lo[j] = er[c0 + j];
+        hi[j] = er[c0 + 32 + j];
+        rope_pair(lo[j], hi[j], cs[j]);
+      }
+      const uint4 wl = make_uint4(pack2_bf16(lo[0], lo[1]), pack2_bf16(lo[2], lo[3]),
+                                  pack2_bf16(lo[4], lo[5]), pack2_bf16(lo[6], lo[7]));
+      const uint4 wh = make_uint4(pack2_bf16(hi[0], hi[1]), pack2_bf16(hi[2], hi[3]),
+                                  pack2_bf16(hi[4], hi[5]), pack2_bf16(hi[6], hi[7]));
+      uint16_t* dst = epi->rope_kind == 1 ? a.y + static_cast<size_t>(m) * a.n + n0 : cache_row;
+      store_global16(dst + c0, wl);
+      store_global16(dst + 32 + c0, wh);
+      return;
+    }
+  }
 
   // ---- epilogue: accumulator element e of a 32 x 32 tile is at row
   // 8 (e / 4) + 4 h + e % 4, column r ----
@@ -1660,7 +1720,7 @@ __device__ __forceinline__ void gemm_grouped_unit(const GemmGroupDesc& d, int u)
     sp.counter = d.counters + tile;
   }
   gemm_tile<BM, BN, WAVES_M, W8, kPrefetch>(a, (tile % d.tiles_m) * BM, (tile / d.tiles_m) * BN,
-                                            sp);
+                                            sp, &d);
 }
 
 template <int BM, int BN, int WAVES_M, bool W8>

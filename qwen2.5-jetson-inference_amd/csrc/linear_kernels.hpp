@@ -143,6 +143,18 @@ struct GemmGroupDesc {
   const void* w2 = nullptr;
   const uint16_t* s2 = nullptr;
   const uint16_t* bias2 = nullptr;
+  // The prefill's q|k|v epilogue (64 x 64 tiles, one head of 64 columns per
+  // tile; rope_kind 0: the plain epilogue).  The tile's BF16 rows (bias
+  // added, rounded) are, for kind 1, rotated by RoPE (pairs (i, i + 32),
+  // the (cos, sin) of position rope_start + row at rope[position * 32 + i])
+  // and written to y; kind 2, rotated and written to row rope_start + row of
+  // kv_cache ([n / 64 heads][max_seq][64]); kind 3, written to kv_cache
+  // unrotated.  Rows at or past max_seq are not written.
+  const float2* rope = nullptr;
+  uint16_t* kv_cache = nullptr;
+  int rope_kind = 0;
+  int rope_start = 0;
+  int max_seq = 0;
 };
 // Split-K in the wide-tile grouped launch.  A GEMM whose wide tiles are
 // split over K in `parts` parts writes each part's FP32 tile, row-major

@@ -274,8 +274,21 @@ bool skinny_group(const infer_hip_model* m, const GemmItem* items, int count, in
   return true;
 }
 
-void linear_group(const infer_hip_model* m, const GemmItem* items, int count, int tokens) {
-  if (skinny_group(m, items, count, tokens)) return;
+// The RoPE + KV store a q|k|v group can take into its epilogue (see
+// GemmGroupDesc::rope_kind): items q, k, v in that order, head_dim 64.
+struct QkvRope {
+  const float2* table;
+  uint16_t* key_cache;
+  uint16_t* value_cache;
+  int max_seq;
+};
+
+// Returns true when `rope` was given and the launch did the RoPE + KV store
+// in its epilogue (the grouped launch on 64 x 64 tiles); otherwise the
+// caller runs launch_rope_store.
+bool linear_group(const infer_hip_model* m, const GemmItem* items, int count, int tokens,
+                  const QkvRope* rope = nullptr) {
+  if (skinny_group(m, items, count, tokens)) return false;
   bool grouped = tokens > 1 && count <= kInlineGroupMax;
   for (int i = 0; i < count && grouped; ++i) {
     grouped = gemm_mfma_supported(items[i].l->w, items[i].x, tokens, items[i].l->n,
@@ -290,13 +303,23 @@ void linear_group(const infer_hip_model* m, const GemmItem* items, int count, in
     }
     g.g.count = count;
     g.w8 = m->w8;
+    if (rope && count == 3) {  // set before the layout, which reorders the descriptors
+      for (int i = 0; i < 3; ++i) {
+        GemmGroupDesc& d = g.g.d[i];
+        d.rope = rope->table;
+        d.rope_kind = i + 1;  // q rotated in place, k rotated into its cache, v into its cache
+        d.kv_cache = i == 1 ? rope->key_cache : (i == 2 ? rope->value_cache : nullptr);
+        d.rope_start = 0;
+        d.max_seq = rope->max_seq;
+      }
+    }
     size_t pf = 0, cc = 0;
     g.tile = layout_gemm_group(g.g.d, count, m->cus, true, &g.blocks, &pf, &cc);
     grouped = g.blocks > 0 && pf <= m->gemm_partial_floats && cc <= m->gemm_counter_count;
   }
   if (!grouped) {
     for (int i = 0; i < count; ++i) linear_batch(m, *items[i].l, items[i].x, items[i].y, tokens);
-    return;
+    return false;
   }
   g.r.count = bind_gemm_group(g.g.d, count, g.tile, m->gemm_partial, m->gemm_counters, g.r.d,
                               &g.reducers);
@@ -305,6 +328,7 @@ void linear_group(const infer_hip_model* m, const GemmItem* items, int count, in
     if (g.gmap.help) g.r.count = 0;  // the GEMM launch sums its split tiles
   }
   launch_gemm_group_inline(g, m->stream);
+  return rope && count == 3 && g.tile == kGemmTile64x64;
 }
 
 // gate|up + SiLU-mul of the prefill as one launch of pair tiles: where the
@@ -669,9 +693,13 @@ int run_prefill(infer_hip_model* m, const int* tokens, int count, int* next) {
     const Layer& L = m->layers[l];
     const GemmItem qkv[3] = {{&L.q, m->pnorm, m->pq}, {&L.k, m->pnorm, m->pk},
                              {&L.v, m->pnorm, m->pv}};
-    linear_group(m, qkv, 3, count);
-    launch_rope_store(m->pq, m->pk, m->pv, L.key_cache, L.value_cache, m->rope, count, 0,
-                      c.num_heads, c.num_kv_heads, m->head_dim, m->max_seq, s);
+    // RoPE + KV store in the q|k|v launch's epilogue where its tiles hold
+    // whole heads (64 x 64 tiles, head_dim 64), else their own launch
+    const QkvRope rope{m->rope, L.key_cache, L.value_cache, m->max_seq};
+    if (!linear_group(m, qkv, 3, count, m->head_dim == 64 ? &rope : nullptr)) {
+      launch_rope_store(m->pq, m->pk, m->pv, L.key_cache, L.value_cache, m->rope, count, 0,
+                        c.num_heads, c.num_kv_heads, m->head_dim, m->max_seq, s);
+    }
     launch_attention_prefill(m->pq, L.key_cache, L.value_cache, m->pattn, count, c.num_heads,
                              c.num_kv_heads, m->head_dim, m->max_seq, s);
     const GemmItem o[1] = {{&L.o, m->pattn, m->ptmp}};
