@@ -601,17 +601,20 @@ def run_attention_parts(dec, parts, q, kc, vc, dpos, rec, heads, kvh, hd, max_se
 
 
 @pytest.mark.parametrize("parts", [2, 4])
-@pytest.mark.parametrize("heads,kvh", [(14, 2), (8, 1), (4, 4)])
-def test_attention_decode_halves_matches_oracle(dec, orc, dev, heads, kvh, parts):
+@pytest.mark.parametrize("heads,kvh,max_seq", [(14, 2, 1024), (8, 1, 1024), (4, 4, 1024),
+                                               (14, 2, 700), (8, 1, 300)])
+def test_attention_decode_halves_matches_oracle(dec, orc, dev, heads, kvh, max_seq, parts):
     """Each part's record against the oracle's attention (cpu_ops.cpp:58-91
     restated): merged on the host in float64 they give the whole context's
     output; rows past p hold NaN and must not matter, and a part past the
     context leaves its record untouched (halves: 512 positions each,
-    quarters: 256)."""
+    quarters: 256, whatever the KV capacity; at 700 or 300 positions the
+    last live part ends inside the cache's end and the later parts start
+    past it)."""
     import torch
-    hd, max_seq, R = 64, 1024, dec.PART_RECORD
-    span = max_seq // parts
-    rng = rc.philox(900 + heads)
+    hd, R = 64, dec.PART_RECORD
+    span = 1024 // parts
+    rng = rc.philox(900 + heads + max_seq)
     q = rc.bf16_normal(rng, (heads * hd,), 0.5)
     kcache = rc.bf16_normal(rng, (kvh, max_seq, hd))
     vcache = rc.bf16_normal(rng, (kvh, max_seq, hd))
