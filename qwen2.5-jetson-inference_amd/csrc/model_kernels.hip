@@ -1017,8 +1017,8 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_scalar_kernel(
 }
 
 // Causal prefill attention on MFMA (v_mfma_f32_32x32x16_bf16).  Workgroup
-// (query block b, head h) takes the 32 queries 32 b .. 32 b + 31; its four
-// waves take the 32-key blocks 0 .. b round robin (block w, w + 4, ...), each
+// (query block b, head h) takes the 32 queries 32 b .. 32 b + 31; its W
+// waves take the 32-key blocks 0 .. b round robin (block w, w + W, ...), each
 // with its own online softmax, and are merged in LDS at the end.
 //
 // Per key block a wave computes S^T = K Q^T (keys x queries) rather than
@@ -1034,21 +1034,39 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_scalar_kernel(
 // 8-byte write), and each fragment is then two 8-byte reads.  P is split
 // into BF16 hi + lo parts (two MFMAs each), so P V keeps about 16 bits of
 // each probability instead of 8: the result stays within a few FP32 ulps of
-// the reference's FP32 loop rather than BF16 rounding of P.
+// the reference's FP32 loop rather than BF16 rounding of P.  The
+// exponentials are the hardware's 2^x (v_exp_f32) on scores pre-scaled by
+// scale * log2(e), one FMA and one transcendental per score instead of
+// expf's range reduction: the loop is VALU-bound, and this cut a 512-token
+// launch from 8.7 to 6.3 us (errors stay well under the output's BF16
+// rounding).
 typedef __bf16 attn_bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 attn_bf16x4_t __attribute__((ext_vector_type(4)));
 typedef float attn_f32x16_t __attribute__((ext_vector_type(16)));
+typedef float attn_f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 attn_bf16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kPrefillQueries = 32;     // queries per workgroup
-constexpr int kPrefillWaves = 4;
 constexpr int kPrefillVtStride = 36;    // BF16 words per transposed value row (32 keys + pad)
+constexpr float kPrefillLazyLog2 = 8.0f;  // the softmax reference's slack (log2 units)
+#ifndef QLIN_PREFILL_WAVES64
+#define QLIN_PREFILL_WAVES64 4
+#endif
+// Waves per workgroup at head_dim 64 (head_dim 128: 4).  Measured on the
+// 512-token prefill of Qwen2.5-0.5B (16 x 14 workgroups): 6.32 us per launch
+// with 4 waves, 7.04 with 8 (two waves per SIMD add no throughput to a loop
+// that is VALU-bound, and the 8-way merge costs more).
+constexpr int kPrefillWaves64 = QLIN_PREFILL_WAVES64;
 
-template <int HD>
+template <int HD, int W>
 struct alignas(16) PrefillSmem {
-  uint16_t vt[kPrefillWaves][HD * kPrefillVtStride];       // per wave: V^T of one key block
-  float o[kPrefillWaves][HD][kPrefillQueries + 1];         // per wave: O^T at the end
-  float m[kPrefillWaves][kPrefillQueries];
-  float l[kPrefillWaves][kPrefillQueries];
+  // per wave: V^T of one key block while its blocks run, then its O^T
+  union alignas(16) Slice {
+    uint16_t vt[HD * kPrefillVtStride];
+    float o[HD][kPrefillQueries + 1];
+  } w[W];
+  float m[W][kPrefillQueries];
+  float l[W][kPrefillQueries];
 };
 
 __device__ __forceinline__ float swap32_max(float v) {
@@ -1057,8 +1075,8 @@ __device__ __forceinline__ float swap32_max(float v) {
   return fmaxf(__int_as_float(r[0]), __int_as_float(r[1]));
 }
 
-template <int HD>
-__global__ __launch_bounds__(kThreads) void attention_prefill_mfma_kernel(
+template <int HD, int W>
+__global__ __launch_bounds__(W * kWave) void attention_prefill_mfma_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ key_cache,
     const uint16_t* __restrict__ value_cache, uint16_t* __restrict__ out, int count, int heads,
     int kv_heads, int max_seq) {
@@ -1066,14 +1084,16 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_mfma_kernel(
   constexpr int DT = HD / 32;          // 32-dimension row tiles of O^T
   constexpr int kChunks = HD / 8;      // 16-byte chunks per row
   constexpr int VC = 8 * kChunks / 64; // (key quad, chunk) pairs per lane
-  __shared__ PrefillSmem<HD> sm;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __shared__ PrefillSmem<HD, W> sm;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 31, h = lane >> 5;
   const int qb = blockIdx.x, head = blockIdx.y;
   const int g = head / (heads / kv_heads);
   const int q0 = qb * kPrefillQueries;
   const int query = q0 + r;
   const float scale = 1.0f / sqrtf(static_cast<float>(HD));
+  const float scale_log2 = scale * 1.44269504088896340736f;  // scale * log2(e)
 
   // Q^T fragments (B of S^T): lane (r, h) holds dimensions 16 ks + 8 h .. + 7
   // of query r (rows past count are clamped; their results are dropped).
@@ -1084,9 +1104,17 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_mfma_kernel(
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qf[ks] = __builtin_bit_cast(attn_bf16x8_t, load_global16(qp + 16 * ks));
   }
-  const uint16_t* kbase = key_cache + static_cast<size_t>(g) * max_seq * HD;
-  const uint16_t* vbase = value_cache + static_cast<size_t>(g) * max_seq * HD;
-  uint16_t* vt = sm.vt[wave];
+  // The kv head's cache rows as buffer resources: a block's loads are a
+  // scalar offset (its first key) over per-lane offsets fixed for the whole
+  // loop, and rows at or past max_seq read as zero.
+  const uint32_t head_bytes = static_cast<uint32_t>(max_seq) * HD * 2;
+  const __amdgpu_buffer_rsrc_t kres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(key_cache + static_cast<size_t>(g) * max_seq * HD), 0,
+      static_cast<int>(head_bytes), 0x00020000);
+  const __amdgpu_buffer_rsrc_t vres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(value_cache + static_cast<size_t>(g) * max_seq * HD), 0,
+      static_cast<int>(head_bytes), 0x00020000);
+  uint16_t* vt = sm.w[wave].vt;
 
   float m = -INFINITY, l = 0.0f;
   attn_f32x16_t o[DT];
@@ -1097,29 +1125,45 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_mfma_kernel(
 
   // Loads of key block kb: K rows (A of S^T, lane (r, h): key r, dimensions
   // 16 ks + 8 h ..) and the value chunks this lane transposes (pair i:
-  // keys 4 a .. 4 a + 3, dimensions 8 c .. 8 c + 7).  Keys past max_seq are
-  // clamped into the cache; keys past count are masked (K) or zeroed (V).
+  // keys 4 a .. 4 a + 3, dimensions 8 c .. 8 c + 7).  Keys past max_seq
+  // read as zero; keys past count are masked (K) or zeroed (V).
+  const uint32_t koff = static_cast<uint32_t>(r * HD + 8 * h) * 2;
+  uint32_t voff[VC];
+#pragma unroll
+  for (int i = 0; i < VC; ++i) {
+    const int idx = lane + 64 * i;
+    voff[i] = static_cast<uint32_t>(4 * (idx / kChunks) * HD + 8 * (idx % kChunks)) * 2;
+  }
   uint4 kr[KS], vr[VC][4];
   auto load_block = [&](int kb) {
     const int k0 = kb * 32;
-    const uint16_t* kp = kbase + static_cast<size_t>(min(k0 + r, max_seq - 1)) * HD + 8 * h;
+    const uint32_t soff = static_cast<uint32_t>(k0) * HD * 2;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) kr[ks] = load_global16(kp + 16 * ks);
+    for (int ks = 0; ks < KS; ++ks) {
+      kr[ks] = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(kres, koff + 32 * ks, soff, 0));
+    }
 #pragma unroll
-    for (int i = 0; i < VC; ++i) {
-      const int idx = lane + 64 * i, a = idx / kChunks, c = idx % kChunks;
+    for (int i = 0; i < VC; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int key = k0 + 4 * a + j;
-        vr[i][j] = load_global16(vbase + static_cast<size_t>(min(key, max_seq - 1)) * HD + 8 * c);
-        if (key >= count) vr[i][j] = make_uint4(0, 0, 0, 0);
+        vr[i][j] = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(vres, voff[i] + j * HD * 2, soff, 0));
+      }
+    if (k0 + 32 > count) {  // only the last block reaches past count
+#pragma unroll
+      for (int i = 0; i < VC; ++i) {
+        const int a = (lane + 64 * i) / kChunks;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (k0 + 4 * a + j >= count) vr[i][j] = make_uint4(0, 0, 0, 0);
       }
     }
   };
 
   int kb = wave;
   if (kb <= qb) load_block(kb);
-  for (; kb <= qb; kb += kPrefillWaves) {
+  for (; kb <= qb; kb += W) {
     const int k0 = kb * 32;
     // transpose this block's values into vt[d][key]: 4 keys per 8-byte write
     __builtin_amdgcn_wave_barrier();  // the previous block's reads are done
@@ -1152,42 +1196,59 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_mfma_kernel(
       st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(attn_bf16x8_t, kr[ks]),
                                                    qf[ks], st, 0, 0, 0);
     }
-    if (kb + kPrefillWaves <= qb) load_block(kb + kPrefillWaves);  // next block in flight
-    // scale, causal mask, online softmax of query r over this block
-    float bm = -INFINITY;
+    if (kb + W <= qb) load_block(kb + W);  // next block in flight
+    // causal mask (only the diagonal block holds keys past a query), online
+    // softmax of query r over this block in base 2 with x = s * scale *
+    // log2(e): p = 2^(x - m) for a reference m that moves (rescaling l and
+    // the accumulators by 2^(m_old - m_new)) only when a score of the wave's
+    // queries exceeds it by more than kPrefillLazyLog2, so p <= 2^8 and most
+    // blocks skip the rescale.  The final division by l removes m exactly;
+    // the BF16 hi + lo split keeps the same relative precision of p at any
+    // scale.  (max(s) * c = max(s * c) for c > 0, rounding being monotonic.)
+    if (kb == qb) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int key = k0 + 8 * (e >> 2) + 4 * h + (e & 3);
-      st[e] = key <= query ? st[e] * scale : -INFINITY;
-      bm = fmaxf(bm, st[e]);
+      for (int e = 0; e < 16; ++e) {
+        const int key = k0 + 8 * (e >> 2) + 4 * h + (e & 3);
+        if (key > query) st[e] = -INFINITY;
+      }
     }
-    bm = swap32_max(bm);
-    const float mn = fmaxf(m, bm);
-    const float f = expf(m - mn);  // m = -inf on the first block: f = 0
+    float bm = st[0];
+#pragma unroll
+    for (int e = 1; e < 16; ++e) bm = fmaxf(bm, st[e]);
+    bm = swap32_max(bm) * scale_log2;
+    // m = -inf before the first block: every wave rescales there (f = 0)
+    if (__builtin_amdgcn_ballot_w64(bm > m + kPrefillLazyLog2) != 0) {
+      const float mn = fmaxf(m, bm);
+      const float f = __builtin_amdgcn_exp2f(m - mn);
+      l *= f;
+      m = mn;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[dt][e] *= f;
+    }
     float ps = 0.0f;
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      st[e] = expf(st[e] - mn);
+      st[e] = __builtin_amdgcn_exp2f(fmaf(st[e], scale_log2, -m));
       ps += st[e];
     }
-    ps = swap32_sum(ps, ps);
-    l = fmaf(l, f, ps);
-    m = mn;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) o[dt][e] *= f;
+    l += swap32_sum(ps, ps);
     __builtin_amdgcn_wave_barrier();  // vt complete for the whole wave
     // O^T += V^T (P_hi + P_lo)^T
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       attn_bf16x8_t phi, plo;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float p = st[8 * s + j];
-        const __bf16 hi = static_cast<__bf16>(p);
-        phi[j] = hi;
-        plo[j] = static_cast<__bf16>(p - static_cast<float>(hi));
+      for (int j = 0; j < 4; ++j) {  // two probabilities per conversion
+        const attn_f32x2_t p = {st[8 * s + 2 * j], st[8 * s + 2 * j + 1]};
+        const attn_bf16x2_t hi = __builtin_convertvector(p, attn_bf16x2_t);
+        const attn_bf16x2_t lo =
+            __builtin_convertvector(p - __builtin_convertvector(hi, attn_f32x2_t), attn_bf16x2_t);
+        phi[2 * j] = hi[0];
+        phi[2 * j + 1] = hi[1];
+        plo[2 * j] = lo[0];
+        plo[2 * j + 1] = lo[1];
       }
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
@@ -1203,11 +1264,15 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_mfma_kernel(
   }
 
   // merge the waves: O^T element e of tile dt is dimension 32 dt + 8 (e / 4)
-  // + 4 h + e % 4 of query r
+  // + 4 h + e % 4 of query r.  O^T overwrites the wave's V^T slice: the
+  // compiler barrier keeps these stores after the last block's V^T reads
+  // (float and BF16 accesses are otherwise taken as disjoint), and the wave's
+  // LDS operations execute in order.
+  asm volatile("" ::: "memory");
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) sm.o[wave][32 * dt + 8 * (e >> 2) + 4 * h + (e & 3)][r] = o[dt][e];
+    for (int e = 0; e < 16; ++e) sm.w[wave].o[32 * dt + 8 * (e >> 2) + 4 * h + (e & 3)][r] = o[dt][e];
   if (h == 0) {
     sm.m[wave][r] = m;
     sm.l[wave][r] = l;
@@ -1215,25 +1280,26 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_mfma_kernel(
   __syncthreads();
   constexpr int kItems = kPrefillQueries * kChunks;  // (query, 8-dimension chunk)
 #pragma unroll
-  for (int it = threadIdx.x; it < kItems; it += kThreads) {
+  for (int it = threadIdx.x; it < kItems; it += W * kWave) {
     const int qi = it / kChunks, c = it % kChunks;
     if (q0 + qi >= count) continue;
     float mm = sm.m[0][qi];
 #pragma unroll
-    for (int w = 1; w < kPrefillWaves; ++w) mm = fmaxf(mm, sm.m[w][qi]);
-    float cw[kPrefillWaves], den = 0.0f;
+    for (int w = 1; w < W; ++w) mm = fmaxf(mm, sm.m[w][qi]);
+    float cw[W], den = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kPrefillWaves; ++w) {
-      cw[w] = expf(sm.m[w][qi] - mm);  // a wave with no block: m = -inf, weight 0
+    for (int w = 0; w < W; ++w) {
+      cw[w] = __builtin_amdgcn_exp2f(sm.m[w][qi] - mm);  // a wave with no block: m = -inf, weight 0
       den = fmaf(sm.l[w][qi], cw[w], den);
     }
+    const float inv = 1.0f / den;
     float acc[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       float a = 0.0f;
 #pragma unroll
-      for (int w = 0; w < kPrefillWaves; ++w) a = fmaf(sm.o[w][8 * c + j][qi], cw[w], a);
-      acc[j] = a / den;
+      for (int w = 0; w < W; ++w) a = fmaf(sm.w[w].o[8 * c + j][qi], cw[w], a);
+      acc[j] = a * inv;
     }
     uint16_t* dst = out + (static_cast<size_t>(q0 + qi) * heads + head) * HD + 8 * c;
     *reinterpret_cast<uint4*>(dst) =
@@ -1433,14 +1499,19 @@ void launch_attention_prefill(const uint16_t* q, const uint16_t* key_cache,
   const bool aligned = ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(key_cache) |
                          reinterpret_cast<uintptr_t>(value_cache) |
                          reinterpret_cast<uintptr_t>(out)) & 15u) == 0;
-  if (aligned) {
+  // The MFMA kernel addresses a kv head's cache rows through a buffer
+  // resource (32-bit byte offsets).
+  const bool offsets32 =
+      static_cast<long long>(max_seq) * head_dim * 2 <= static_cast<long long>(INT32_MAX);
+  if (aligned && offsets32) {
     const dim3 grid((count + kPrefillQueries - 1) / kPrefillQueries, heads);
     if (head_dim == 64) {
-      hipLaunchKernelGGL(attention_prefill_mfma_kernel<64>, grid, dim3(kThreads), 0, stream, q,
-                         key_cache, value_cache, out, count, heads, kv_heads, max_seq);
+      hipLaunchKernelGGL((attention_prefill_mfma_kernel<64, kPrefillWaves64>), grid,
+                         dim3(kPrefillWaves64 * kWave), 0, stream, q, key_cache, value_cache, out,
+                         count, heads, kv_heads, max_seq);
     } else {
-      hipLaunchKernelGGL(attention_prefill_mfma_kernel<128>, grid, dim3(kThreads), 0, stream, q,
-                         key_cache, value_cache, out, count, heads, kv_heads, max_seq);
+      hipLaunchKernelGGL((attention_prefill_mfma_kernel<128, 4>), grid, dim3(4 * kWave), 0,
+                         stream, q, key_cache, value_cache, out, count, heads, kv_heads, max_seq);
     }
     return;
   }

@@ -112,6 +112,29 @@ def test_prefill_attention_matches_oracle(orc, dev, t, heads, kv_heads, hd, max_
     _check(got, exp, vw, f"t={t}")
 
 
+@pytest.mark.parametrize("slope", [0.0375, 0.005])
+def test_prefill_attention_rising_scores(orc, dev, slope):
+    """Scores that rise along the keys (key p scores about 8 slope p nats
+    above key 0 at head_dim 64) keep moving each query's softmax maximum:
+    by about 14 base-2 units per 32-key block at slope 0.0375, past the
+    kernel's rescale slack (8) every block, and by about 1.8 at 0.005, where
+    the probabilities grow up to 2^8 between rescales."""
+    t, heads, kv_heads, hd, max_seq = 300, 4, 2, 64, 320
+    print(f"attention prefill rising scores slope={slope}", flush=True)
+    rng = np.random.default_rng(11)
+    q = (1.0 + 0.1 * rng.standard_normal(t * heads * hd)).astype(np.float32)
+    ramp = slope * np.arange(max_seq, dtype=np.float32)[None, :, None]
+    k = (ramp + 0.1 * rng.standard_normal((kv_heads, max_seq, hd))).astype(np.float32)
+    v = rng.standard_normal((kv_heads, max_seq, hd)).astype(np.float32)
+    qw = R.bf16_words(q).reshape(t, heads, hd)
+    kw = R.bf16_words(k.reshape(-1)).reshape(kv_heads, max_seq, hd)
+    vw = R.bf16_words(v.reshape(-1)).reshape(kv_heads, max_seq, hd)
+    kw[:, t:, :] = 0x7FC0
+    vw[:, t:, :] = 0x7FC0
+    exp = _expected(orc, qw, kw, vw, heads, kv_heads, hd, max_seq)
+    _check(_run(dev, qw, kw, vw, heads, kv_heads, hd, max_seq), exp, vw, f"slope={slope}")
+
+
 def test_prefill_attention_reference_pattern(orc, dev):
     qw, kw, vw = _case(40, 4, 2, 64, 48, seed=0, pattern=True)
     exp = _expected(orc, qw, kw, vw, 4, 2, 64, 48)
