@@ -505,6 +505,29 @@ def test_prefill_512_tokens_grouped_mfma(orc, dev, cfg, precision):
     o.close()
 
 
+@pytest.mark.parametrize("precision", ["w8a16", "w16a16"])
+@pytest.mark.parametrize("length", [100, 200])
+def test_prefill_ragged_row_blocks(orc, dev, precision, length):
+    """Prompts whose last row block is partial in every prefill launch: 100
+    tokens (W8A16: the skinny kernel's four 32-token tiles, the last of 4
+    rows; W16A16: 64 x 64 tiles, the last block of 36 rows) and 200 tokens
+    (64 x 64 tiles, the last block of 8 rows); then decode steps on the KV
+    cache the prefill wrote."""
+    t = S.random_model(QWEN_SHAPED, precision, seed=21, std=0.04)
+    fp32 = S.dequantized_fp32(t, QWEN_SHAPED)
+    print(f"prefill ragged {precision} length={length}", flush=True)
+    g = model_hip.Qwen2Model(QWEN_SHAPED, t, precision, max_sequence_length=256,
+                             use_graph=True)
+    o = oracle_model(orc, QWEN_SHAPED, fp32, 256)
+    p = prompt(length, QWEN_SHAPED.vocab_size, seed=length)
+    agree, total, worst = teacher_forced(g, o, p, 4, 0.999, f"prefill {length} {precision}")
+    print(f"prefill {length} {precision}: agreement {agree}/{total}, worst cosine {worst:.6f}",
+          flush=True)
+    assert agree >= total - 1
+    g.close()
+    o.close()
+
+
 def test_rewind_replays_the_same_decode(dev):
     t, _ = weights(TINY, "w8a16")
     g = model_hip.Qwen2Model(TINY, t, "w8a16", max_sequence_length=64)
