@@ -1053,9 +1053,10 @@ constexpr float kPrefillLazyLog2 = 8.0f;  // the softmax reference's slack (log2
 #define QLIN_PREFILL_WAVES64 4
 #endif
 // Waves per workgroup at head_dim 64 (head_dim 128: 4).  Measured on the
-// 512-token prefill of Qwen2.5-0.5B (16 x 14 workgroups): 6.32 us per launch
-// with 4 waves, 7.04 with 8 (two waves per SIMD add no throughput to a loop
-// that is VALU-bound, and the 8-way merge costs more).
+// 512-token prefill of Qwen2.5-0.5B (16 x 14 workgroups): 5.72 us per launch
+// with 4 waves, 6.69 with 8 (6.32 against 7.04 with expf and a rescale every
+// block): two waves per SIMD add no throughput to a loop that is VALU-bound,
+// and the 8-way merge costs more.
 constexpr int kPrefillWaves64 = QLIN_PREFILL_WAVES64;
 
 template <int HD, int W>
