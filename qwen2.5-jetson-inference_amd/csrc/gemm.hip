@@ -2286,6 +2286,14 @@ void launch_gemm_group_inline(const GemmGroupLaunch& l, hipStream_t stream) {
       hipLaunchKernelGGL(splitk_reduce_inline_kernel, dim3(l.reducers), dim3(256), 0, stream,
                          l.r, l.rmap);
     }
+  } else if (l.tile == kGemmTile128x128) {
+    if (l.w8) {
+      hipLaunchKernelGGL((gemm_grouped_inline_kernel<128, 128, 2, true>), grid, dim3(kThreads),
+                         0, stream, l.g);
+    } else {
+      hipLaunchKernelGGL((gemm_grouped_inline_kernel<128, 128, 2, false>), grid, dim3(kThreads),
+                         0, stream, l.g);
+    }
   } else if (l.w8) {
     hipLaunchKernelGGL((gemm_grouped_inline_kernel<64, 64, 2, true>), grid, dim3(kThreads), 0,
                        stream, l.g);

@@ -193,6 +193,10 @@ constexpr int kSplitReduceRows = 16;  // rows of a tile per reduction block
 // split tiles sums their slices once its own unit is done (gemm.hip,
 // wide_split_help), so no reduction launch runs.
 // QLIN_XCD_MAP=0 places workgroups in logical order.
+// QLIN_GROUP_TILE128=1 (plan.cpp): a lone long-K GEMM of a `fill` group
+// (K >= 2048, M >= 128: the prefill's down) on 128 x 128 tiles in 8 K parts
+// instead of 64 x 64 tiles in up to 4 (measured at M = 512: 25.2 against
+// 18.4 us per launch; at M = 128 within the run-to-run spread).
 #ifndef QLIN_XCD_MAP
 #define QLIN_XCD_MAP 1
 #endif

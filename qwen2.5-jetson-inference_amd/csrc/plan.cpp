@@ -128,6 +128,11 @@ constexpr int kWideRowsHost = 256;  // gemm_tile_rows(kGemmTile256x128)
 constexpr int kWideColsHost = 128;
 }  // namespace
 
+// 128 x 128 tiles for a lone long-K GEMM (a measured alternative, off by
+// default; see linear_kernels.hpp).
+#ifndef QLIN_GROUP_TILE128
+#define QLIN_GROUP_TILE128 0
+#endif
 int layout_gemm_group(GemmGroupDesc* table, int count, int cus, bool fill, int* blocks_out,
                       size_t* partial_floats, size_t* counters) {
   int min_tokens = table[0].m;
@@ -145,7 +150,10 @@ int layout_gemm_group(GemmGroupDesc* table, int count, int cus, bool fill, int* 
   // tiles against 15-18 us on wide ones, while gate|up (152 wide tiles) takes
   // 18.3 us wide against 20.9 us.
   const bool wide = min_tokens >= kWideRowsHost && (!fill || 2 * wide_tiles >= cus);
-  const int tile = wide ? kGemmTile256x128 : kGemmTile64x64;
+  int tile = wide ? kGemmTile256x128 : kGemmTile64x64;
+  const bool t128 = QLIN_GROUP_TILE128 && fill && !wide && count == 1 && min_tokens >= 128 &&
+                    table[0].k >= 2048;
+  if (t128) tile = kGemmTile128x128;
   const int bm = gemm_tile_rows(tile), bn = gemm_tile_cols(tile);
   int min_stages = 1 << 30, max_stages = 0;
   for (int i = 0; i < count; ++i) {
@@ -187,7 +195,9 @@ int layout_gemm_group(GemmGroupDesc* table, int count, int cus, bool fill, int* 
   // M = 32, 2-4 stage parts of every GEMM take 19.4 us against 13.8 us,
   // their in-kernel hand-offs costing more than the shorter chains save.
   int target = std::max(8, min_stages);
-  if (fill) {
+  if (t128) {
+    target = (max_stages + 7) / 8;  // 8 parts
+  } else if (fill) {
     target = std::min(max_stages, std::max(14, (max_stages + 3) / 4));
     while (target < max_stages && units_for(target) > 2ll * cus) ++target;
   } else if (tile == kGemmTile256x128) {
