@@ -528,6 +528,34 @@ def test_prefill_ragged_row_blocks(orc, dev, precision, length):
     o.close()
 
 
+def test_prefill_graph_replays_equal_direct_launches(dev):
+    """A model with use_graph against one without, prompt lengths repeated:
+    their prefills (and the decode steps on the KV cache they write) must be
+    equal bit for bit, across the skinny (5, 40 tokens) and tiled (100, 130,
+    200 tokens) layouts.  Built with QLIN_PREFILL_GRAPH=1, the graph model
+    captures a length's prefill on its second prefill and replays it after,
+    and its four-entry cache replaces lengths on the way."""
+    t = S.random_model(QWEN_SHAPED, "w8a16", seed=23, std=0.04)
+    g = model_hip.Qwen2Model(QWEN_SHAPED, t, "w8a16", max_sequence_length=256, use_graph=True)
+    e = model_hip.Qwen2Model(QWEN_SHAPED, t, "w8a16", max_sequence_length=256, use_graph=False)
+    for i, length in enumerate([5, 40, 5, 40, 5, 100, 130, 200, 100, 5, 40, 200]):
+        print(f"prefill graph call {i}: {length} tokens", flush=True)
+        p = prompt(length, QWEN_SHAPED.vocab_size, seed=100 + length)
+        g.reset()
+        e.reset()
+        tg, te = g.prefill(p), e.prefill(p)
+        assert tg == te, f"call {i} ({length} tokens): token {tg} vs {te}"
+        assert np.array_equal(g.last_logits_host().view(np.uint32),
+                              e.last_logits_host().view(np.uint32)), f"call {i}: logits"
+        assert g.position == e.position == length
+        for step in range(2):
+            dg, de = g.decode_next(tg), e.decode_next(te)
+            assert dg == de, f"call {i} step {step}: token {dg} vs {de}"
+            tg, te = dg, de
+    g.close()
+    e.close()
+
+
 def test_rewind_replays_the_same_decode(dev):
     t, _ = weights(TINY, "w8a16")
     g = model_hip.Qwen2Model(TINY, t, "w8a16", max_sequence_length=64)
