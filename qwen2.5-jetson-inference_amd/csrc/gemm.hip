@@ -1193,10 +1193,10 @@ __device__ __forceinline__ void gemm_wide_tile(const GemmArgs& a, int m0, int n0
       float o[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        // the two GEMMs' BF16 outputs, then silu_mul_kernel's expression
+        // the two GEMMs' BF16 outputs, then silu(g) * u
         const float g = bf16_to_f32(f32_to_bf16(gf[j] + bg[j]));
         const float u = bf16_to_f32(f32_to_bf16(uf[j] + bu[j]));
-        o[j] = g / (1.0f + expf(-g)) * u;
+        o[j] = silu_mul_fast(g, u);
       }
       uint16_t* dst = a.y + static_cast<size_t>(m) * a.n + n;
       if (vec) {
@@ -2047,10 +2047,10 @@ __global__ __launch_bounds__(kWave * KW) void gemm_skinny_kernel(SkinnyArgs a) {
     if (m >= a.m) continue;
     float v;
     if (PAIR) {
-      // as silu_mul_bf16 on the two BF16 GEMM outputs
+      // silu(g) * u on the two BF16 GEMM outputs
       const float gv = bf16_to_f32(f32_to_bf16(acc[e] + bias));
       const float uv = bf16_to_f32(f32_to_bf16(acc2[e] + bias2));
-      v = gv / (1.0f + expf(-gv)) * uv;
+      v = silu_mul_fast(gv, uv);
     } else {
       v = acc[e] + bias;
     }

@@ -8,9 +8,9 @@ The reference computes the same thing as two GEMM calls and silu_mul_bf16
 through infer_hip_gemm_* (the 64 x 64 tiles, whose per-element arithmetic
 is the pair tile's: the same per-group MFMA partials folded in group order),
 then bf16(g / (1 + exp(-g)) * u) on their BF16 outputs.  The GEMM parts must
-agree exactly; the SiLU's exp is torch's here and the kernel's expf there, so
-an output may differ by one BF16 unit in the last place, on at most 0.5 % of
-the outputs.  The GEMMs themselves are checked against the FP32 oracle
+agree exactly; the SiLU is torch's exp and division here and the kernel's
+hardware 2^x and reciprocal there (a few FP32 ulps apart), so an output may
+differ by one BF16 unit in the last place, on at most 0.5 % of the outputs.  The GEMMs themselves are checked against the FP32 oracle
 elsewhere (tests/test_gpu_gemm.py); the pair tile's layout (rows of gate in
 columns 0-63, up in 64-127, 64-column steps, tails) is what this file pins.
 """
