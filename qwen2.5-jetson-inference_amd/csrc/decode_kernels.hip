@@ -456,7 +456,7 @@ __global__ __launch_bounds__(kBlock) void attn_o_parts_kernel(AttnOPartsArgs a) 
     for (int p = 1; p < P; ++p) m = p < live ? fmaxf(m, ml[q][p].x) : m;
     float w[P];
 #pragma unroll
-    for (int p = 0; p < P; ++p) w[p] = p == 0 || p < live ? expf(ml[q][p].x - m) : 0.0f;
+    for (int p = 0; p < P; ++p) w[p] = p == 0 || p < live ? exp_nonpos_fast(ml[q][p].x - m) : 0.0f;
     float ll = ml[q][0].y * w[0];
 #pragma unroll
     for (int p = 1; p < P; ++p) ll = p < live ? fmaf(ml[q][p].y, w[p], ll) : ll;

@@ -37,6 +37,13 @@ __device__ __forceinline__ uint32_t pack2_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// e^x for x <= 0 (softmax weights) as the hardware's 2^(x log2(e)): two
+// instructions where expf's range reduction takes ~12; within a few FP32
+// ulps of expf (results below 2^-126 may flush to zero).
+__device__ __forceinline__ float exp_nonpos_fast(float x) {
+  return __builtin_amdgcn_exp2f(x * 1.44269504088896340736f);
+}
+
 // silu(g) * u = g / (1 + e^-g) * u on the hardware's 2^x and reciprocal
 // (v_exp_f32 of -g log2(e), v_rcp_f32): six instructions where expf and the
 // correctly rounded division take ~30.  Within a few FP32 ulps of the

@@ -881,7 +881,7 @@ __global__ __launch_bounds__(kAttnWholeMax / P / kTile * kWave) void attention_d
     const bool valid = t0 + kRowsPer * pc + rg < end;
     const float sc = valid ? score * scale : -INFINITY;
     m = wave_max(sc);
-    const float e = valid ? expf(sc - m) : 0.0f;
+    const float e = valid ? exp_nonpos_fast(sc - m) : 0.0f;
     l = wave_sum(e);
     float ej[kPieces];
     ej[0] = group8_lane<0>(e);
@@ -919,7 +919,7 @@ __global__ __launch_bounds__(kAttnWholeMax / P / kTile * kWave) void attention_d
     float ll = 0.0f, aa = 0.0f;
 #pragma unroll
     for (int w = 0; w < W; ++w) {
-      const float f = wl[w] > 0.0f ? expf(wm[w] - mm) : 0.0f;
+      const float f = wl[w] > 0.0f ? exp_nonpos_fast(wm[w] - mm) : 0.0f;
       ll = fmaf(wl[w], f, ll);
       aa = fmaf(wacc[w][tid], f, aa);
     }
