@@ -777,7 +777,7 @@ __global__ __launch_bounds__(kBlock) void attn_o_gemv_kernel(AttnOArgs a) {
     float e[MAXS], ll = 0.0f;
 #pragma unroll
     for (int sp = 0; sp < MAXS; ++sp) {
-      e[sp] = sp < splits ? expf(ms[tid][sp] - mm) : 0.0f;
+      e[sp] = sp < splits ? exp_nonpos_fast(ms[tid][sp] - mm) : 0.0f;
       if (sp < splits) ll = fmaf(ls[tid][sp], e[sp], ll);
     }
 #pragma unroll

@@ -494,8 +494,8 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void attention_decode_kernel(
     const float sc = valid ? dot * scale : -INFINITY;
     const float bm = wave_max(sc);
     const float nm = fmaxf(m, bm);
-    const float e = valid ? expf(sc - nm) : 0.0f;
-    const float f = expf(m - nm);  // m = -inf on a wave's first tile: f = 0
+    const float e = valid ? exp_nonpos_fast(sc - nm) : 0.0f;
+    const float f = exp_nonpos_fast(m - nm);  // m = -inf on a wave's first tile: f = 0
     l = fmaf(l, f, wave_sum(e));
 #pragma unroll
     for (int j = 0; j < kDims; ++j) acc[j] *= f;
@@ -539,7 +539,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void attention_decode_kernel(
     float ll = 0.0f, aa = 0.0f;
 #pragma unroll
     for (int w = 0; w < W; ++w) {
-      const float f = wl[w] > 0.0f ? expf(wm[w] - mm) : 0.0f;
+      const float f = wl[w] > 0.0f ? exp_nonpos_fast(wm[w] - mm) : 0.0f;
       ll = fmaf(wl[w], f, ll);
       aa = fmaf(wacc[w][tid], f, aa);
     }
@@ -751,8 +751,8 @@ __global__ __launch_bounds__(kWholeWaves * kWave) void attention_decode_whole_ke
     const bool valid = t0 + kRowsPer * pc + rg < end;
     const float sc = valid ? score * scale : -INFINITY;
     const float nm = fmaxf(m, wave_max(sc));
-    const float e = valid ? expf(sc - nm) : 0.0f;
-    const float f = expf(m - nm);  // m = -inf on a wave's first tile: f = 0
+    const float e = valid ? exp_nonpos_fast(sc - nm) : 0.0f;
+    const float f = exp_nonpos_fast(m - nm);  // m = -inf on a wave's first tile: f = 0
     l = fmaf(l, f, wave_sum(e));
     m = nm;
 #pragma unroll
@@ -798,7 +798,7 @@ __global__ __launch_bounds__(kWholeWaves * kWave) void attention_decode_whole_ke
     float ll = 0.0f, aa = 0.0f;
 #pragma unroll
     for (int w = 0; w < W; ++w) {
-      const float f = wl[w] > 0.0f ? expf(wm[w] - mm) : 0.0f;
+      const float f = wl[w] > 0.0f ? exp_nonpos_fast(wm[w] - mm) : 0.0f;
       ll = fmaf(wl[w], f, ll);
       aa = fmaf(wacc[w][tid], f, aa);
     }
