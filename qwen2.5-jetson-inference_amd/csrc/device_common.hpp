@@ -49,7 +49,9 @@ __device__ __forceinline__ float exp_nonpos_fast(float x) {
 // correctly rounded division take ~30.  Within a few FP32 ulps of the
 // correctly rounded expression, so its BF16 rounding differs by one unit on
 // about 1e-4 of the outputs; the GEMM epilogues that write many SiLU-mul
-// outputs per thread use it.  g = -inf gives NaN as the division does.
+// outputs per thread use it.  g = -inf gives NaN as the division does; for
+// g below about -87 the reciprocal of e^-g is subnormal and may be flushed,
+// giving 0 where the division gives a value under 1e-36.
 __device__ __forceinline__ float silu_mul_fast(float g, float u) {
   const float e = __builtin_amdgcn_exp2f(g * -1.44269504088896340736f);
   return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
