@@ -568,15 +568,28 @@ __global__ __launch_bounds__(kBlock) void lm_head_decode_kernel(LmHeadDecodeArgs
   {
     // x and the RMSNorm weight before the first task's rows: loads return
     // in issue order, so the normalization runs while the rows stream in
-    uint4 xr[SLABS][1], nr[SLABS][1], raw[SLABS];
+    uint4 xr[SLABS][1], nr[SLABS][1], raw[SLABS], add[SLABS];
     load_vec8_raw<SLABS>(a.x, a.k, lane, raw);
 #pragma unroll
     for (int s = 0; s < SLABS; ++s) xr[s][0] = raw[s];
+    // the residual to add first (x_add); without one, x again (unused): no
+    // branch around a load
+    load_vec8_raw<SLABS>(a.x_add ? a.x_add : a.x, a.k, lane, add);
     load_vec8_raw<SLABS>(a.norm_w, a.k, lane, raw);
 #pragma unroll
     for (int s = 0; s < SLABS; ++s) nr[s][0] = raw[s];
     load_task(row0, w);
     __builtin_amdgcn_sched_barrier(0);  // every load is in flight
+    if (a.x_add) {
+#pragma unroll
+      for (int s = 0; s < SLABS; ++s) {  // bf16(x + x_add), as add_kernel
+        const uint4 x = xr[s][0], y = add[s];
+        xr[s][0] = make_uint4(pack2_bf16(bf16_lo(x.x) + bf16_lo(y.x), bf16_hi(x.x) + bf16_hi(y.x)),
+                              pack2_bf16(bf16_lo(x.y) + bf16_lo(y.y), bf16_hi(x.y) + bf16_hi(y.y)),
+                              pack2_bf16(bf16_lo(x.z) + bf16_lo(y.z), bf16_hi(x.z) + bf16_hi(y.z)),
+                              pack2_bf16(bf16_lo(x.w) + bf16_lo(y.w), bf16_hi(x.w) + bf16_hi(y.w)));
+      }
+    }
     wave_rms_norm<SLABS, 8>(xr, nr, a.k, a.eps, lane, xn);
   }
   // The (cos, sin) row of the next position, for the last workgroup when it

@@ -179,6 +179,9 @@ struct LmHeadDecodeArgs {
   // nothing else; the next decode_entry_kernel applies it.  counter, token,
   // state, history and rope are then unused.
   unsigned long long* key = nullptr;
+  // With x_add ([k] BF16), the row normalized is bf16(x + x_add): the
+  // prefill's last residual add, for the one row the LM head reads.
+  const uint16_t* x_add = nullptr;
 };
 
 constexpr int kLmHeadRows = 4;  // rows per wave task

@@ -429,7 +429,11 @@ RopeCursor rope_cursor(const infer_hip_model* m) {
 // with `advance` the step's bookkeeping too (history, step, position).  The
 // fused LM head of a decode step defers both: its argmax stays in m->lm_key
 // for the next decode_entry launch (enqueue_decode_step, finish_decode).
-int lm_head_step(infer_hip_model* m, const uint16_t* row, bool advance, bool defer = false) {
+// add (optional): the row normalized is bf16(row + add), the residual add
+// the prefill's last layer leaves for the one row read here (the unfused
+// path writes it into the row first).
+int lm_head_step(infer_hip_model* m, const uint16_t* row, bool advance, bool defer = false,
+                 const uint16_t* add = nullptr) {
   const infer_hip_model_config& c = m->cfg;
   if (m->fused_lm_head) {
     LmHeadDecodeArgs a{row, m->final_norm, c.rms_norm_eps, m->lm_head, c.vocab_size,
@@ -437,9 +441,11 @@ int lm_head_step(infer_hip_model* m, const uint16_t* row, bool advance, bool def
                        &m->state->token, m->state, m->history, m->max_seq,
                        defer ? 2 : (advance ? 1 : 0), rope_cursor(m)};
     a.key = m->lm_key;
+    a.x_add = add;
     launch_lm_head_decode(a, m->stream);
     return check_launch("lm head");
   }
+  if (add) launch_add(const_cast<uint16_t*>(row), add, c.hidden_size, m->stream);
   launch_rms_norm(row, m->final_norm, m->norm, 1, c.hidden_size, c.rms_norm_eps, m->stream);
   const int rc = infer_hip_lm_head_bf16(m->lm_head, nullptr, m->norm, m->logits, m->lm_value,
                                         m->lm_index, &m->state->token, c.vocab_size,
@@ -728,11 +734,10 @@ int enqueue_prefill(infer_hip_model* m, int count) {
   const infer_hip_model_config& c = m->cfg;
   const int hidden = c.hidden_size, inter = c.intermediate_size;
   hipStream_t s = m->stream;
-  launch_embedding(m->embed, m->prompt, count, c.vocab_size, hidden, m->px, s);
-  const long long rows_h = static_cast<long long>(count) * hidden;
+  launch_embedding_rms_norm(m->embed, m->prompt, count, c.vocab_size, hidden, m->px,
+                            m->layers[0].in_norm, m->pnorm, c.rms_norm_eps, s);
   // The residual adds ride with the RMSNorm behind them (after o: the
   // post-attention norm; after down: the next layer's input norm).
-  launch_rms_norm(m->px, m->layers[0].in_norm, m->pnorm, count, hidden, c.rms_norm_eps, s);
   for (size_t l = 0; l < m->layers.size(); ++l) {
     const Layer& L = m->layers[l];
     const GemmItem qkv[3] = {{&L.q, m->pnorm, m->pq}, {&L.k, m->pnorm, m->pk},
@@ -762,16 +767,17 @@ int enqueue_prefill(infer_hip_model* m, int count) {
     }
     const GemmItem down[1] = {{&L.down, m->pmlp, m->ptmp}};
     linear_group(m, down, 1, count);
+    // the last layer's residual add is needed for the last row only: the
+    // LM head step takes it
     if (l + 1 < m->layers.size()) {
       launch_add_rms_norm(m->px, m->ptmp, m->layers[l + 1].in_norm, m->pnorm, count, hidden,
                           c.rms_norm_eps, s);
-    } else {
-      launch_add(m->px, m->ptmp, rows_h, s);
     }
   }
   int rc = check_launch("prefill");
   if (rc != INFER_HIP_OK) return rc;
-  rc = lm_head_step(m, m->px + static_cast<size_t>(count - 1) * hidden, false);
+  const size_t last = static_cast<size_t>(count - 1) * hidden;
+  rc = lm_head_step(m, m->px + last, false, false, m->ptmp + last);
   if (rc != INFER_HIP_OK) return rc;
   launch_set_state(m->state, -1, count, 0, rope_cursor(m), s, m->lm_key);
   return check_launch("prefill state");

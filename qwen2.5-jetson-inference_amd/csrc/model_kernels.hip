@@ -133,18 +133,30 @@ __global__ __launch_bounds__(kThreads) void add_rms_norm_kernel(uint16_t* __rest
 // sum of squares is reduced across the wave (DPP/permlane) with no LDS or
 // barrier.  The elementwise arithmetic is rms_norm_kernel's and
 // add_rms_norm_kernel's; the sum of squares is added in another order.
+// With G (the prefill's first launch) the row is gathered from the
+// embedding table (row tokens[row], clamped as embedding_kernel does),
+// stored into x and normalized: the embedding and the first RMSNorm in one
+// launch.
 // hidden % 8 == 0, hidden <= 512 * CH, 16-byte aligned rows.
-template <int CH, bool ADD>
+template <int CH, bool ADD, bool G>
 __global__ __launch_bounds__(kThreads) void norm_rows_kernel(uint16_t* __restrict__ x,
                                                              const uint16_t* __restrict__ y,
                                                              const uint16_t* __restrict__ w,
                                                              uint16_t* __restrict__ out,
-                                                             int rows, int hidden, float eps) {
+                                                             int rows, int hidden, float eps,
+                                                             const uint16_t* __restrict__ table,
+                                                             const int* __restrict__ tokens,
+                                                             int vocab) {
   const int lane = threadIdx.x & (kWave - 1);
   const int row = blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
   if (row >= rows) return;  // the whole wave
   const int chunks = hidden >> 3;
   uint4* xr = reinterpret_cast<uint4*>(x + static_cast<size_t>(row) * hidden);
+  const uint4* src = xr;
+  if (G) {
+    const int token = min(max(tokens[row], 0), vocab - 1);
+    src = reinterpret_cast<const uint4*>(table + static_cast<size_t>(token) * hidden);
+  }
   const uint4* yr = ADD ? reinterpret_cast<const uint4*>(y + static_cast<size_t>(row) * hidden)
                         : nullptr;
   const uint4* wr = reinterpret_cast<const uint4*>(w);
@@ -153,7 +165,7 @@ __global__ __launch_bounds__(kThreads) void norm_rows_kernel(uint16_t* __restric
 #pragma unroll
   for (int c = 0; c < CH; ++c) {  // every load in flight at once (clamped, masked below)
     const int i = min(lane + kWave * c, chunks - 1);
-    xa[c] = load_global16(xr + i);
+    xa[c] = load_global16(src + i);
     if (ADD) ya[c] = load_global16(yr + i);
     wa[c] = load_global16(wr + i);
   }
@@ -176,7 +188,7 @@ __global__ __launch_bounds__(kThreads) void norm_rows_kernel(uint16_t* __restric
       v[c][2 * e + 1] = a1;
       if (live) sum = fmaf(a1, a1, fmaf(a0, a0, sum));
     }
-    if (ADD && live) {
+    if ((ADD || G) && live) {
       store_global16(xr + lane + kWave * c, make_uint4(pack2_bf16(v[c][0], v[c][1]),
                                                        pack2_bf16(v[c][2], v[c][3]),
                                                        pack2_bf16(v[c][4], v[c][5]),
@@ -210,26 +222,29 @@ int norm_rows_chunks(const void* x, const void* y, const void* w, const void* ou
   return per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : per <= 8 ? 8 : 0;
 }
 
-template <bool ADD>
+template <bool ADD, bool GATHER = false>
 void launch_norm_rows(int ch, uint16_t* x, const uint16_t* y, const uint16_t* w, uint16_t* out,
-                      int rows, int hidden, float eps, hipStream_t stream) {
+                      int rows, int hidden, float eps, hipStream_t stream,
+                      const uint16_t* table = nullptr, const int* tokens = nullptr,
+                      int vocab = 0) {
   const dim3 grid((rows + kThreads / kWave - 1) / (kThreads / kWave)), block(kThreads);
+  constexpr bool G = !ADD && GATHER;
   switch (ch) {
     case 1:
-      hipLaunchKernelGGL((norm_rows_kernel<1, ADD>), grid, block, 0, stream, x, y, w, out, rows,
-                         hidden, eps);
+      hipLaunchKernelGGL((norm_rows_kernel<1, ADD, G>), grid, block, 0, stream, x, y, w, out,
+                         rows, hidden, eps, table, tokens, vocab);
       break;
     case 2:
-      hipLaunchKernelGGL((norm_rows_kernel<2, ADD>), grid, block, 0, stream, x, y, w, out, rows,
-                         hidden, eps);
+      hipLaunchKernelGGL((norm_rows_kernel<2, ADD, G>), grid, block, 0, stream, x, y, w, out,
+                         rows, hidden, eps, table, tokens, vocab);
       break;
     case 4:
-      hipLaunchKernelGGL((norm_rows_kernel<4, ADD>), grid, block, 0, stream, x, y, w, out, rows,
-                         hidden, eps);
+      hipLaunchKernelGGL((norm_rows_kernel<4, ADD, G>), grid, block, 0, stream, x, y, w, out,
+                         rows, hidden, eps, table, tokens, vocab);
       break;
     default:
-      hipLaunchKernelGGL((norm_rows_kernel<8, ADD>), grid, block, 0, stream, x, y, w, out, rows,
-                         hidden, eps);
+      hipLaunchKernelGGL((norm_rows_kernel<8, ADD, G>), grid, block, 0, stream, x, y, w, out,
+                         rows, hidden, eps, table, tokens, vocab);
       break;
   }
 }
@@ -1376,6 +1391,20 @@ void launch_embedding(const uint16_t* table, const int* tokens, int count, int v
                       uint16_t* out, hipStream_t stream) {
   hipLaunchKernelGGL(embedding_kernel, dim3(count), dim3(kThreads), 0, stream, table, tokens,
                      count, vocab, hidden, out);
+}
+
+void launch_embedding_rms_norm(const uint16_t* table, const int* tokens, int count, int vocab,
+                               int hidden, uint16_t* x, const uint16_t* w, uint16_t* out,
+                               float eps, hipStream_t stream) {
+  const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  const int ch = a16(table) ? norm_rows_chunks(x, nullptr, w, out, hidden) : 0;
+  if (ch) {
+    launch_norm_rows<false, true>(ch, x, nullptr, w, out, count, hidden, eps, stream, table,
+                                  tokens, vocab);
+    return;
+  }
+  launch_embedding(table, tokens, count, vocab, hidden, x, stream);
+  launch_rms_norm(x, w, out, count, hidden, eps, stream);
 }
 
 void launch_rms_norm(const uint16_t* x, const uint16_t* w, uint16_t* out, int rows, int hidden,

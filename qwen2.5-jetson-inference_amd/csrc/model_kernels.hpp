@@ -30,6 +30,11 @@ void launch_embedding(const uint16_t* table, const int* tokens, int count, int v
                       uint16_t* out, hipStream_t stream);
 void launch_rms_norm(const uint16_t* x, const uint16_t* w, uint16_t* out, int rows, int hidden,
                      float eps, hipStream_t stream);
+// x = the embedding rows of tokens[0 .. count) (launch_embedding) and out =
+// their RMSNorm (launch_rms_norm), as one launch where the rows allow it.
+void launch_embedding_rms_norm(const uint16_t* table, const int* tokens, int count, int vocab,
+                               int hidden, uint16_t* x, const uint16_t* w, uint16_t* out,
+                               float eps, hipStream_t stream);
 void launch_rope_store(uint16_t* q, uint16_t* k, const uint16_t* v, uint16_t* key_cache,
                        uint16_t* value_cache, const float2* rope, int count, int start,
                        int heads, int kv_heads, int head_dim, int max_seq, hipStream_t stream);
