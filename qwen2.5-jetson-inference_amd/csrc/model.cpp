@@ -745,12 +745,19 @@ int enqueue_prefill(infer_hip_model* m, int count) {
     // RoPE + KV store in the q|k|v launch's epilogue where its tiles hold
     // whole heads (64 x 64 tiles, head_dim 64), else their own launch
     const QkvRope rope{m->rope, L.key_cache, L.value_cache, m->max_seq};
-    if (!linear_group(m, qkv, 3, count, m->head_dim == 64 ? &rope : nullptr)) {
+    // (short prompts, whose q|k|v runs on the skinny kernel: inside the
+    // attention launch instead)
+    if (linear_group(m, qkv, 3, count, m->head_dim == 64 ? &rope : nullptr)) {
+      launch_attention_prefill(m->pq, L.key_cache, L.value_cache, m->pattn, count,
+                               c.num_heads, c.num_kv_heads, m->head_dim, m->max_seq, s);
+    } else if (!attention_prefill_rope(m->pq, m->pk, m->pv, L.key_cache, L.value_cache,
+                                       m->rope, m->pattn, count, c.num_heads, c.num_kv_heads,
+                                       m->head_dim, m->max_seq, s)) {
       launch_rope_store(m->pq, m->pk, m->pv, L.key_cache, L.value_cache, m->rope, count, 0,
                         c.num_heads, c.num_kv_heads, m->head_dim, m->max_seq, s);
+      launch_attention_prefill(m->pq, L.key_cache, L.value_cache, m->pattn, count,
+                               c.num_heads, c.num_kv_heads, m->head_dim, m->max_seq, s);
     }
-    launch_attention_prefill(m->pq, L.key_cache, L.value_cache, m->pattn, count, c.num_heads,
-                             c.num_kv_heads, m->head_dim, m->max_seq, s);
     const GemmItem o[1] = {{&L.o, m->pattn, m->ptmp}};
     linear_group(m, o, 1, count);
     launch_add_rms_norm(m->px, m->ptmp, L.post_norm, m->pnorm, count, hidden, c.rms_norm_eps, s);

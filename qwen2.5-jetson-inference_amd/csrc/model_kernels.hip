@@ -1091,11 +1091,41 @@ __device__ __forceinline__ float swap32_max(float v) {
   return fmaxf(__int_as_float(r[0]), __int_as_float(r[1]));
 }
 
-template <int HD, int W>
+// ROPE: q, k and v come unrotated from the q|k|v GEMM (k and v [count]
+// [kv_heads][HD]): q is rotated as it is loaded, each key block as it
+// arrives (rope_store_rows_kernel's arithmetic on the same BF16 values,
+// rounded to BF16), and the workgroup of each kv head's first query head
+// stores its diagonal key block, rotated, and the block's values into the
+// caches.  The prefill's own RoPE + KV store launch then does not run.
+struct PrefillRope {
+  const uint16_t* k = nullptr;
+  const uint16_t* v = nullptr;
+  const float2* table = nullptr;  // [max_seq][HD / 2] (cos, sin)
+};
+
+// (a, b) = (a cos - b sin, b cos + a sin) on each BF16 pair of (lo, hi),
+// rounded to BF16 (rope_store_rows_kernel's arithmetic).
+__device__ __forceinline__ void rope_bf16x8(uint4& lo, uint4& hi, const float2 (&cs)[8]) {
+  const uint32_t l4[4] = {lo.x, lo.y, lo.z, lo.w}, h4[4] = {hi.x, hi.y, hi.z, hi.w};
+  uint32_t ol[4], oh[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float a0 = bf16_lo(l4[e]), b0 = bf16_lo(h4[e]);
+    float a1 = bf16_hi(l4[e]), b1 = bf16_hi(h4[e]);
+    rope_pair(a0, b0, cs[2 * e]);
+    rope_pair(a1, b1, cs[2 * e + 1]);
+    ol[e] = pack2_bf16(a0, a1);
+    oh[e] = pack2_bf16(b0, b1);
+  }
+  lo = make_uint4(ol[0], ol[1], ol[2], ol[3]);
+  hi = make_uint4(oh[0], oh[1], oh[2], oh[3]);
+}
+
+template <int HD, int W, bool ROPE>
 __global__ __launch_bounds__(W * kWave) void attention_prefill_mfma_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ key_cache,
-    const uint16_t* __restrict__ value_cache, uint16_t* __restrict__ out, int count, int heads,
-    int kv_heads, int max_seq) {
+    const uint16_t* __restrict__ q, uint16_t* __restrict__ key_cache,
+    uint16_t* __restrict__ value_cache, uint16_t* __restrict__ out, int count, int heads,
+    int kv_heads, int max_seq, PrefillRope pr) {
   constexpr int KS = HD / 16;          // k-steps of S^T (16 dimensions each)
   constexpr int DT = HD / 32;          // 32-dimension row tiles of O^T
   constexpr int kChunks = HD / 8;      // 16-byte chunks per row
@@ -1117,19 +1147,39 @@ __global__ __launch_bounds__(W * kWave) void attention_prefill_mfma_kernel(
   {
     const uint16_t* qp =
         q + (static_cast<size_t>(min(query, count - 1)) * heads + head) * HD + 8 * h;
+    uint4 qr[KS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[ks] = __builtin_bit_cast(attn_bf16x8_t, load_global16(qp + 16 * ks));
+    for (int ks = 0; ks < KS; ++ks) qr[ks] = load_global16(qp + 16 * ks);
+    if (ROPE) {  // pairs (i, i + HD / 2): chunks ks and ks + KS / 2 of this lane
+      const float2* cs = pr.table + static_cast<size_t>(min(query, count - 1)) * (HD / 2) + 8 * h;
+#pragma unroll
+      for (int ks = 0; ks < KS / 2; ++ks) {
+        float2 c8[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) c8[j] = cs[16 * ks + j];
+        rope_bf16x8(qr[ks], qr[ks + KS / 2], c8);
+      }
+    }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = __builtin_bit_cast(attn_bf16x8_t, qr[ks]);
   }
   // The kv head's cache rows as buffer resources: a block's loads are a
   // scalar offset (its first key) over per-lane offsets fixed for the whole
   // loop, and rows at or past max_seq read as zero.
-  const uint32_t head_bytes = static_cast<uint32_t>(max_seq) * HD * 2;
+  // (ROPE: the q|k|v GEMM's k and v rows of the kv head, kv_heads * HD
+  // apart; rows at or past count read as zero.)
+  const int kv_row = ROPE ? kv_heads * HD : HD;  // elements between key rows
+  const uint32_t head_bytes =
+      ROPE ? static_cast<uint32_t>((count - 1) * kv_row + HD) * 2
+           : static_cast<uint32_t>(max_seq) * HD * 2;
+  const uint16_t* ksrc =
+      ROPE ? pr.k + static_cast<size_t>(g) * HD : key_cache + static_cast<size_t>(g) * max_seq * HD;
+  const uint16_t* vsrc = ROPE ? pr.v + static_cast<size_t>(g) * HD
+                              : value_cache + static_cast<size_t>(g) * max_seq * HD;
   const __amdgpu_buffer_rsrc_t kres = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(key_cache + static_cast<size_t>(g) * max_seq * HD), 0,
-      static_cast<int>(head_bytes), 0x00020000);
+      const_cast<uint16_t*>(ksrc), 0, static_cast<int>(head_bytes), 0x00020000);
   const __amdgpu_buffer_rsrc_t vres = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(value_cache + static_cast<size_t>(g) * max_seq * HD), 0,
-      static_cast<int>(head_bytes), 0x00020000);
+      const_cast<uint16_t*>(vsrc), 0, static_cast<int>(head_bytes), 0x00020000);
   uint16_t* vt = sm.w[wave].vt;
 
   float m = -INFINITY, l = 0.0f;
@@ -1143,17 +1193,18 @@ __global__ __launch_bounds__(W * kWave) void attention_prefill_mfma_kernel(
   // 16 ks + 8 h ..) and the value chunks this lane transposes (pair i:
   // keys 4 a .. 4 a + 3, dimensions 8 c .. 8 c + 7).  Keys past max_seq
   // read as zero; keys past count are masked (K) or zeroed (V).
-  const uint32_t koff = static_cast<uint32_t>(r * HD + 8 * h) * 2;
+  const uint32_t koff = static_cast<uint32_t>(r * kv_row + 8 * h) * 2;
   uint32_t voff[VC];
 #pragma unroll
   for (int i = 0; i < VC; ++i) {
     const int idx = lane + 64 * i;
-    voff[i] = static_cast<uint32_t>(4 * (idx / kChunks) * HD + 8 * (idx % kChunks)) * 2;
+    voff[i] = static_cast<uint32_t>(4 * (idx / kChunks) * kv_row + 8 * (idx % kChunks)) * 2;
   }
   uint4 kr[KS], vr[VC][4];
+  float2 kcs[ROPE ? KS / 2 : 1][8];  // ROPE: (cos, sin) of key row r's pairs
   auto load_block = [&](int kb) {
     const int k0 = kb * 32;
-    const uint32_t soff = static_cast<uint32_t>(k0) * HD * 2;
+    const uint32_t soff = static_cast<uint32_t>(k0) * kv_row * 2;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       kr[ks] = __builtin_bit_cast(
@@ -1164,8 +1215,16 @@ __global__ __launch_bounds__(W * kWave) void attention_prefill_mfma_kernel(
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         vr[i][j] = __builtin_bit_cast(
-            uint4, __builtin_amdgcn_raw_buffer_load_b128(vres, voff[i] + j * HD * 2, soff, 0));
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(vres, voff[i] + j * kv_row * 2, soff, 0));
       }
+    if (ROPE) {
+      const float2* cs =
+          pr.table + static_cast<size_t>(min(k0 + r, count - 1)) * (HD / 2) + 8 * h;
+#pragma unroll
+      for (int ks = 0; ks < KS / 2; ++ks)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) kcs[ks][j] = cs[16 * ks + j];
+    }
     if (k0 + 32 > count) {  // only the last block reaches past count
 #pragma unroll
       for (int i = 0; i < VC; ++i) {
@@ -1181,6 +1240,33 @@ __global__ __launch_bounds__(W * kWave) void attention_prefill_mfma_kernel(
   if (kb <= qb) load_block(kb);
   for (; kb <= qb; kb += W) {
     const int k0 = kb * 32;
+    if (ROPE) {
+#pragma unroll
+      for (int ks = 0; ks < KS / 2; ++ks) rope_bf16x8(kr[ks], kr[ks + KS / 2], kcs[ks]);
+      if (kb == qb && head % (heads / kv_heads) == 0) {
+        // the diagonal block into the caches: rotated key rows, value rows
+        uint16_t* kc = key_cache + static_cast<size_t>(g) * max_seq * HD;
+        uint16_t* vc = value_cache + static_cast<size_t>(g) * max_seq * HD;
+        const int key = k0 + r;
+        if (key < count && key < max_seq) {
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) {
+            store_global16(kc + static_cast<size_t>(key) * HD + 16 * ks + 8 * h, kr[ks]);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < VC; ++i) {
+          const int idx = lane + 64 * i, a = idx / kChunks, c = idx % kChunks;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int vkey = k0 + 4 * a + j;
+            if (vkey < count && vkey < max_seq) {
+              store_global16(vc + static_cast<size_t>(vkey) * HD + 8 * c, vr[i][j]);
+            }
+          }
+        }
+      }
+    }
     // transpose this block's values into vt[d][key]: 4 keys per 8-byte write
     __builtin_amdgcn_wave_barrier();  // the previous block's reads are done
 #pragma unroll
@@ -1523,6 +1609,33 @@ void launch_attention_decode_spans(const uint16_t* q, const uint16_t* key_cache,
   }
 }
 
+bool attention_prefill_rope(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                            uint16_t* key_cache, uint16_t* value_cache, const float2* rope,
+                            uint16_t* out, int count, int heads, int kv_heads, int head_dim,
+                            int max_seq, hipStream_t stream) {
+  const bool aligned =
+      ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+        reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(key_cache) |
+        reinterpret_cast<uintptr_t>(value_cache) | reinterpret_cast<uintptr_t>(rope) |
+        reinterpret_cast<uintptr_t>(out)) & 15u) == 0;
+  if (!aligned || count < 1 || count > kPrefillRopeMaxTokens || count > max_seq ||
+      (head_dim != 64 && head_dim != 128)) {
+    return false;
+  }
+  const dim3 grid((count + kPrefillQueries - 1) / kPrefillQueries, heads);
+  const PrefillRope pr{k, v, rope};
+  if (head_dim == 64) {
+    hipLaunchKernelGGL((attention_prefill_mfma_kernel<64, kPrefillWaves64, true>), grid,
+                       dim3(kPrefillWaves64 * kWave), 0, stream, q, key_cache, value_cache, out,
+                       count, heads, kv_heads, max_seq, pr);
+  } else {
+    hipLaunchKernelGGL((attention_prefill_mfma_kernel<128, 4, true>), grid, dim3(4 * kWave), 0,
+                       stream, q, key_cache, value_cache, out, count, heads, kv_heads, max_seq,
+                       pr);
+  }
+  return true;
+}
+
 void launch_attention_prefill(const uint16_t* q, const uint16_t* key_cache,
                               const uint16_t* value_cache, uint16_t* out, int count, int heads,
                               int kv_heads, int head_dim, int max_seq, hipStream_t stream) {
@@ -1535,13 +1648,16 @@ void launch_attention_prefill(const uint16_t* q, const uint16_t* key_cache,
       static_cast<long long>(max_seq) * head_dim * 2 <= static_cast<long long>(INT32_MAX);
   if (aligned && offsets32) {
     const dim3 grid((count + kPrefillQueries - 1) / kPrefillQueries, heads);
+    uint16_t* kc = const_cast<uint16_t*>(key_cache);
+    uint16_t* vc = const_cast<uint16_t*>(value_cache);
     if (head_dim == 64) {
-      hipLaunchKernelGGL((attention_prefill_mfma_kernel<64, kPrefillWaves64>), grid,
-                         dim3(kPrefillWaves64 * kWave), 0, stream, q, key_cache, value_cache, out,
-                         count, heads, kv_heads, max_seq);
+      hipLaunchKernelGGL((attention_prefill_mfma_kernel<64, kPrefillWaves64, false>), grid,
+                         dim3(kPrefillWaves64 * kWave), 0, stream, q, kc, vc, out, count, heads,
+                         kv_heads, max_seq, PrefillRope{});
     } else {
-      hipLaunchKernelGGL((attention_prefill_mfma_kernel<128, 4>), grid, dim3(4 * kWave), 0,
-                         stream, q, key_cache, value_cache, out, count, heads, kv_heads, max_seq);
+      hipLaunchKernelGGL((attention_prefill_mfma_kernel<128, 4, false>), grid, dim3(4 * kWave),
+                         0, stream, q, kc, vc, out, count, heads, kv_heads, max_seq,
+                         PrefillRope{});
     }
     return;
   }

@@ -100,6 +100,17 @@ void launch_attention_decode_spans(const uint16_t* q, const uint16_t* key_cache,
 void launch_attention_prefill(const uint16_t* q, const uint16_t* key_cache,
                               const uint16_t* value_cache, uint16_t* out, int count, int heads,
                               int kv_heads, int head_dim, int max_seq, hipStream_t stream);
+// The prefill attention of a short prompt (count <= kPrefillRopeMaxTokens,
+// positions 0 .. count - 1) on the q|k|v GEMM's unrotated q, k and v ([count]
+// [heads or kv_heads][head_dim]): the RoPE of q and k and the KV-cache store
+// done inside the attention launch (launch_rope_store's results), so no
+// RoPE launch runs.  False (nothing launched) where it does not apply:
+// then launch_rope_store + launch_attention_prefill.
+constexpr int kPrefillRopeMaxTokens = 64;
+bool attention_prefill_rope(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                            uint16_t* key_cache, uint16_t* value_cache, const float2* rope,
+                            uint16_t* out, int count, int heads, int kv_heads, int head_dim,
+                            int max_seq, hipStream_t stream);
 void launch_silu_mul(const uint16_t* gate, const uint16_t* up, uint16_t* out, long long n,
                      hipStream_t stream);
 void launch_add(uint16_t* x, const uint16_t* y, long long n, hipStream_t stream);
