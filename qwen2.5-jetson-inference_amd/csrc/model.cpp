@@ -267,8 +267,13 @@ bool skinny_group(const infer_hip_model* m, const GemmItem* items, int count, in
   a.m = tokens;
   for (int i = 0; i < count; ++i) {
     const Linear& l = *items[i].l;
+    // An int8 gate|up pair takes the skinny pair launch up to
+    // kSkinnyMaxTokens (beyond gemm_skinny_preferred's 64): it saves the
+    // separate SiLU-mul launch (measured at Qwen2.5-0.5B shapes: TTFT 1.33-1.38
+    // -> 1.27-1.28 ms at 96 tokens, 1.38-1.42 -> 1.37-1.38 at 128).
+    const bool pair_w8 = pair_up && m->w8;
     if (!gemm_skinny_supported(l.w, items[i].x, tokens, l.n, l.k) ||
-        !gemm_skinny_preferred(m->w8, tokens, pair_up ? 2 * l.n : l.n, l.k)) {
+        !(pair_w8 || gemm_skinny_preferred(m->w8, tokens, pair_up ? 2 * l.n : l.n, l.k))) {
       return false;
     }
     a.d[i] = SkinnyDesc{l.w, m->w8 ? l.s : nullptr, l.b, nullptr, nullptr, nullptr,
